@@ -1,0 +1,684 @@
+/*
+ * oracle.c -- CPU restatement of decisive's quantized matrix-product path.
+ *
+ * TEST INFRASTRUCTURE ONLY: the checker for the HIP kernels, never the product.
+ * Each function cites the reference file:line it restates (relative to the
+ * hyperlogue/decisive tree). Built with -ffp-contract=off -fno-fast-math so the
+ * only fused multiply-adds are the explicit fmaf() calls that the reference's
+ * AVX2 kernel performs with _mm256_fmadd_ps.
+ */
+#define _GNU_SOURCE
+#include "oracle.h"
+
+#include <float.h>
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+#if defined(__x86_64__)
+#include <immintrin.h>
+#endif
+
+/* ------------------------------------------------------------------------ */
+/* IEEE conversions (half 2.7.1: bf16::from_f32 / f16::from_f32 round to    */
+/* nearest even; widening is exact).                                        */
+/* ------------------------------------------------------------------------ */
+
+static uint32_t bits_of(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static float float_of(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+float or_bf16_to_f32(uint16_t h) { return float_of((uint32_t)h << 16); }
+
+uint16_t or_f32_to_bf16(float f) {
+    uint32_t x = bits_of(f);
+    if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x0040u);
+    uint32_t lsb = (x >> 16) & 1u;
+    return (uint16_t)((x + 0x7fffu + lsb) >> 16);
+}
+
+float or_f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1fu;
+    uint32_t m = h & 0x3ffu;
+    if (e == 0x1f) return float_of(sign | 0x7f800000u | (m << 13));
+    if (e == 0) {
+        /* zero or subnormal: m * 2^-24, exact in binary32 */
+        float v = (float)m * 5.9604644775390625e-8f;
+        return sign ? -v : v;
+    }
+    return float_of(sign | ((e + 112u) << 23) | (m << 13));
+}
+
+uint16_t or_f32_to_f16(float f) {
+    uint32_t x = bits_of(f);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t exp = (x >> 23) & 0xffu;
+    uint32_t man = x & 0x7fffffu;
+    if (exp == 0xff) return (uint16_t)(sign | 0x7c00u | (man ? (0x200u | (man >> 13)) : 0u));
+    int e = (int)exp - 112; /* biased f16 exponent */
+    if (e >= 31) return (uint16_t)(sign | 0x7c00u);
+    if (e <= 0) {
+        if (e < -10) return (uint16_t)sign;
+        uint32_t full = man | 0x800000u;
+        int shift = 14 - e;
+        uint32_t q = full >> shift;
+        uint32_t rem = full & ((1u << shift) - 1u);
+        uint32_t half = 1u << (shift - 1);
+        if (rem > half || (rem == half && (q & 1u))) q++;
+        return (uint16_t)(sign | q);
+    }
+    uint32_t h = sign | ((uint32_t)e << 10) | (man >> 13);
+    uint32_t rem = man & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++;
+    return (uint16_t)h;
+}
+
+void or_f32_to_bf16_n(const float *x, size_t n, uint16_t *out) {
+    for (size_t i = 0; i < n; i++) out[i] = or_f32_to_bf16(x[i]);
+}
+void or_f32_to_f16_n(const float *x, size_t n, uint16_t *out) {
+    for (size_t i = 0; i < n; i++) out[i] = or_f32_to_f16(x[i]);
+}
+void or_f16_to_f32_n(const uint16_t *x, size_t n, float *out) {
+    for (size_t i = 0; i < n; i++) out[i] = or_f16_to_f32(x[i]);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Grouped quantizer: int8.rs:305-313 (group_scale_bits), :347-360          */
+/* (pack_bits); identical formula to packed.rs:43-45.                        */
+/* ------------------------------------------------------------------------ */
+
+static float limit_of(int bits) { return bits == 4 ? 7.0f : 127.0f; }
+
+float or_group_scale(const float *x, size_t n, int bits) {
+    float maximum = 0.0f;
+    for (size_t i = 0; i < n; i++) maximum = fmaxf(maximum, fabsf(x[i]));
+    float s = maximum / limit_of(bits);
+    return s > FLT_MIN ? s : FLT_MIN;
+}
+
+static int8_t quantize_one(float v, float inverse, float limit) {
+    float r = rintf(v * inverse); /* round_ties_even under the default mode */
+    if (r < -limit) r = -limit;
+    if (r > limit) r = limit;
+    return (int8_t)(int)r;
+}
+
+void or_group_codes(const float *x, size_t n, float scale, int bits, int8_t *out) {
+    float inverse = 1.0f / scale; /* f32::recip */
+    float limit = limit_of(bits);
+    for (size_t i = 0; i < n; i++) out[i] = quantize_one(x[i], inverse, limit);
+}
+
+/* ------------------------------------------------------------------------ */
+/* a1/a2: the g64 wire layout, packed.rs                                    */
+/* ------------------------------------------------------------------------ */
+
+static size_t group_bytes(int bits) { return 64u * (size_t)bits / 8u + 4u; }
+
+size_t or_packed_size(size_t rows, size_t cols, int bits) {
+    if (bits != 4 && bits != 8) return 0;
+    if (rows == 0 || cols == 0 || cols % 64 != 0) return 0;
+    return rows * (cols / 64) * group_bytes(bits);
+}
+
+int or_pack_g64(const uint16_t *bf16, size_t rows, size_t cols, int bits, uint8_t *out) {
+    if (!or_packed_size(rows, cols, bits)) return -1;
+    size_t groups = rows * cols / 64;
+    for (size_t g = 0; g < groups; g++) {
+        float values[64];
+        for (int i = 0; i < 64; i++) {
+            values[i] = or_bf16_to_f32(bf16[g * 64 + i]);
+            if (!isfinite(values[i])) return -2;
+        }
+        float scale = or_group_scale(values, 64, bits);
+        int8_t codes[64];
+        or_group_codes(values, 64, scale, bits, codes);
+        uint8_t *dst = out + g * group_bytes(bits);
+        if (bits == 4) {
+            for (int i = 0; i < 32; i++)
+                dst[i] = (uint8_t)((codes[2 * i] + 8) | ((codes[2 * i + 1] + 8) << 4));
+            dst += 32;
+        } else {
+            for (int i = 0; i < 64; i++) dst[i] = (uint8_t)codes[i];
+            dst += 64;
+        }
+        memcpy(dst, &scale, 4); /* little-endian host */
+    }
+    return 0;
+}
+
+static int code_at(const uint8_t *group, size_t k, int bits) {
+    if (bits == 4) return (int)((group[k / 2] >> (4 * (k % 2))) & 15u) - 8;
+    return (int)(int8_t)group[k];
+}
+
+int or_unpack_g64(const uint8_t *bytes, size_t nbytes, int bits, float *out) {
+    size_t stride = or_packed_size(1, 64, bits);
+    if (!stride || nbytes == 0 || nbytes % stride != 0) return -1;
+    for (size_t g = 0; g < nbytes / stride; g++) {
+        const uint8_t *group = bytes + g * stride;
+        float scale;
+        memcpy(&scale, group + stride - 4, 4);
+        if (!(isfinite(scale) && scale > 0.0f)) return -3;
+        for (size_t k = 0; k < 64; k++) out[g * 64 + k] = (float)code_at(group, k, bits) * scale;
+    }
+    return 0;
+}
+
+int or_project(const uint8_t *packed, int bits, size_t cols, const float *x, size_t outputs,
+               float *y) {
+    size_t stride = or_packed_size(1, cols, bits);
+    size_t gstride = or_packed_size(1, 64, bits);
+    if (!stride) return -1;
+    for (size_t i = 0; i < cols; i++)
+        if (!isfinite(x[i])) return -2;
+    size_t groups = cols / 64;
+    int32_t *codes = (int32_t *)malloc(cols * sizeof(int32_t));
+    float *scales = (float *)malloc(groups * sizeof(float));
+    for (size_t g = 0; g < groups; g++) {
+        float s = or_group_scale(x + g * 64, 64, 8);
+        float inverse = 1.0f / s;
+        for (size_t i = 0; i < 64; i++) codes[g * 64 + i] = quantize_one(x[g * 64 + i], inverse, 127.0f);
+        scales[g] = s;
+    }
+    for (size_t o = 0; o < outputs; o++) {
+        const uint8_t *row = packed + o * stride;
+        float sum = 0.0f;
+        for (size_t g = 0; g < groups; g++) {
+            const uint8_t *group = row + g * gstride;
+            float scale;
+            memcpy(&scale, group + gstride - 4, 4);
+            int32_t dot = 0;
+            for (size_t k = 0; k < 64; k++) dot += codes[g * 64 + k] * code_at(group, k, bits);
+            sum = sum + (float)dot * (scales[g] * scale);
+        }
+        y[o] = sum;
+    }
+    free(codes);
+    free(scales);
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* D1: g32/f16 layout                                                       */
+/* ------------------------------------------------------------------------ */
+
+size_t or_g32_size(size_t rows, size_t cols) {
+    if (rows == 0 || cols == 0 || cols % 32 != 0) return 0;
+    return rows * (cols / 32) * 18u;
+}
+
+int or_pack_g32_f16(const float *w, size_t rows, size_t cols, uint8_t *out) {
+    if (!or_g32_size(rows, cols)) return -1;
+    const float smallest = 5.9604644775390625e-8f; /* f16 bits 0x0001 */
+    size_t groups = rows * cols / 32;
+    for (size_t g = 0; g < groups; g++) {
+        const float *v = w + g * 32;
+        float maximum = 0.0f;
+        for (int i = 0; i < 32; i++) {
+            if (!isfinite(v[i])) return -2;
+            maximum = fmaxf(maximum, fabsf(v[i]));
+        }
+        float scale = maximum / 7.0f;
+        if (!(scale > smallest)) scale = smallest;
+        float inverse = 1.0f / scale;
+        uint8_t *dst = out + g * 18;
+        for (int i = 0; i < 16; i++) {
+            int c0 = quantize_one(v[2 * i], inverse, 7.0f);
+            int c1 = quantize_one(v[2 * i + 1], inverse, 7.0f);
+            dst[i] = (uint8_t)((c0 + 8) | ((c1 + 8) << 4));
+        }
+        uint16_t h = or_f32_to_f16(scale);
+        dst[16] = (uint8_t)(h & 0xff);
+        dst[17] = (uint8_t)(h >> 8);
+    }
+    return 0;
+}
+
+int or_unpack_g32_f16(const uint8_t *bytes, size_t nbytes, float *out) {
+    if (nbytes == 0 || nbytes % 18 != 0) return -1;
+    for (size_t g = 0; g < nbytes / 18; g++) {
+        const uint8_t *group = bytes + g * 18;
+        float scale = or_f16_to_f32((uint16_t)(group[16] | (group[17] << 8)));
+        if (!(isfinite(scale) && scale > 0.0f)) return -3;
+        for (size_t k = 0; k < 32; k++) out[g * 32 + k] = (float)code_at(group, k, 4) * scale;
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* a3/a4: grouped weight and activation quantization, int8.rs               */
+/* ------------------------------------------------------------------------ */
+
+int or_weight_quantize(const uint16_t *bf16, size_t n, size_t k, int bits, int8_t *codes,
+                       float *scales) {
+    if ((bits != 4 && bits != 8) || n == 0 || k == 0) return -1;
+    size_t groups = (k + 63) / 64;
+    for (size_t c = 0; c < n; c++) {
+        for (size_t g = 0; g < groups; g++) {
+            size_t count = k - g * 64 < 64 ? k - g * 64 : 64;
+            float values[64] = {0};
+            for (size_t i = 0; i < count; i++) {
+                values[i] = or_bf16_to_f32(bf16[c * k + g * 64 + i]);
+                if (!isfinite(values[i])) return -2;
+            }
+            float s = or_group_scale(values, 64, bits);
+            scales[c * groups + g] = s;
+            or_group_codes(values, 64, s, bits, codes + (c * groups + g) * 64);
+        }
+    }
+    return 0;
+}
+
+void or_act_quantize(const float *x, size_t m, size_t k, int bits, int8_t *q, float *s) {
+    size_t groups = (k + 63) / 64;
+    for (size_t r = 0; r < m; r++) {
+        for (size_t g = 0; g < groups; g++) {
+            size_t count = k - g * 64 < 64 ? k - g * 64 : 64;
+            const float *values = x + r * k + g * 64;
+            float scale = or_group_scale(values, count, bits);
+            s[r * groups + g] = scale;
+            int8_t *out = q + (r * groups + g) * 64;
+            memset(out, 0, 64);
+            or_group_codes(values, count, scale, bits, out);
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* a5: grouped W{4,8}A8 product                                              */
+/* ------------------------------------------------------------------------ */
+
+void or_grouped_gemm(const int8_t *qx, const float *sx, size_t m, const int8_t *qw,
+                     const float *sw, size_t n, size_t k, int fused, float *y) {
+    size_t groups = (k + 63) / 64;
+    for (size_t r = 0; r < m; r++) {
+        for (size_t c = 0; c < n; c++) {
+            float acc = 0.0f;
+            for (size_t g = 0; g < groups; g++) {
+                const int8_t *a = qx + (r * groups + g) * 64;
+                const int8_t *b = qw + (c * groups + g) * 64;
+                int32_t dot = 0;
+                for (int i = 0; i < 64; i++) dot += (int32_t)a[i] * (int32_t)b[i];
+                if (fused) {
+                    float s = sw[c * groups + g] * sx[r * groups + g];
+                    acc = fmaf((float)dot, s, acc);
+                } else {
+                    acc = acc + (float)dot * (sx[r * groups + g] * sw[c * groups + g]);
+                }
+            }
+            y[r * n + c] = acc;
+        }
+    }
+}
+
+void or_matrix_apply(const float *x, size_t m, const int8_t *qw, const float *sw, size_t n,
+                     size_t k, int act_bits, int fused, float *y) {
+    for (size_t i = 0; i < m * k; i++) {
+        if (!isfinite(x[i])) {
+            for (size_t j = 0; j < m * n; j++) y[j] = NAN;
+            return;
+        }
+    }
+    size_t groups = (k + 63) / 64;
+    int8_t *q = (int8_t *)malloc(m * groups * 64 + 1);
+    float *s = (float *)malloc(m * groups * sizeof(float) + 4);
+    or_act_quantize(x, m, k, act_bits, q, s);
+    or_grouped_gemm(q, s, m, qw, sw, n, k, fused, y);
+    free(q);
+    free(s);
+}
+
+/* ------------------------------------------------------------------------ */
+/* a3 panel layout and the AVX2 rows<R,Q4> kernel (CPU baseline)             */
+/* ------------------------------------------------------------------------ */
+
+size_t or_panel_bytes(size_t n, size_t k, int bits) {
+    size_t groups = (k + 63) / 64;
+    return (n + 7) / 8 * groups * 512 / (bits == 4 ? 2 : 1);
+}
+
+void or_panel_pack(const int8_t *codes, const float *scales, size_t n, size_t k, int bits,
+                   uint8_t *data, float *pscales) {
+    size_t groups = (k + 63) / 64;
+    size_t panels = (n + 7) / 8;
+    memset(data, 0, or_panel_bytes(n, k, bits));
+    memset(pscales, 0, panels * groups * 8 * sizeof(float));
+    for (size_t p = 0; p < panels; p++) {
+        uint8_t *pd = data + p * groups * 512 / (bits == 4 ? 2 : 1);
+        for (size_t c = 0; c < 8 && p * 8 + c < n; c++) {
+            size_t col = p * 8 + c;
+            for (size_t g = 0; g < groups; g++) {
+                pscales[(p * groups + g) * 8 + c] = scales[col * groups + g];
+                const int8_t *src = codes + (col * groups + g) * 64;
+                for (size_t kk = 0; kk < 64; kk++) {
+                    size_t at = g * 512 + kk / 4 * 32 + c * 4 + kk % 4;
+                    if (bits == 4) {
+                        uint8_t nib = (uint8_t)(src[kk] + 8) & 15u;
+                        pd[at / 2] |= (uint8_t)(nib << (4 * (at % 2)));
+                    } else {
+                        pd[at] = (uint8_t)src[kk];
+                    }
+                }
+            }
+        }
+    }
+}
+
+int or_has_avx2(void) {
+#if defined(__x86_64__)
+    __builtin_cpu_init();
+    return __builtin_cpu_supports("avx2") && __builtin_cpu_supports("fma");
+#else
+    return 0;
+#endif
+}
+
+#if defined(__x86_64__)
+struct panel_job {
+    const uint8_t *data;
+    const float *pscales;
+    size_t n, k, m;
+    int bits;
+    const int8_t *qx;
+    const float *sx;
+    float *y;
+    size_t tiles;
+    size_t next; /* atomic tile counter */
+};
+
+__attribute__((target("avx2"))) static __m256i unpack_q4(const uint8_t *p) {
+    __m256i packed = _mm256_cvtepu8_epi16(_mm_loadu_si128((const __m128i *)p));
+    __m256i low = _mm256_and_si256(packed, _mm256_set1_epi16(0x000f));
+    __m256i high = _mm256_and_si256(_mm256_slli_epi16(packed, 4), _mm256_set1_epi16(0x0f00));
+    return _mm256_sub_epi8(_mm256_or_si256(low, high), _mm256_set1_epi8(8));
+}
+
+/* int8.rs:524-585 rows<R,Q4>: R rows x one 8-column panel. `q4` selects the
+ * on-the-fly nibble unpack; otherwise `pd` holds one signed byte per code. */
+__attribute__((target("avx2,fma"))) static void panel_rows(const struct panel_job *j,
+                                                           const uint8_t *pd, const float *ps,
+                                                           int q4, size_t panel, size_t first,
+                                                           size_t rows) {
+    size_t groups = (j->k + 63) / 64;
+    __m256i one = _mm256_set1_epi16(1);
+    __m256 sums[8];
+    for (size_t r = 0; r < rows; r++) sums[r] = _mm256_setzero_ps();
+    for (size_t g = 0; g < groups; g++) {
+        __m256i acc[8];
+        for (size_t r = 0; r < rows; r++) acc[r] = _mm256_setzero_si256();
+        size_t base = g * 512;
+        for (size_t kk = 0; kk < 64; kk += 4) {
+            __m256i b = q4 ? unpack_q4(pd + (base + kk * 8) / 2)
+                           : _mm256_loadu_si256((const __m256i *)(pd + base + kk * 8));
+            __m256i magnitude = _mm256_abs_epi8(b);
+            for (size_t r = 0; r < rows; r++) {
+                int32_t word;
+                memcpy(&word, j->qx + ((first + r) * groups + g) * 64 + kk, 4);
+                __m256i a = _mm256_set1_epi32(word);
+                __m256i pair = _mm256_maddubs_epi16(magnitude, _mm256_sign_epi8(a, b));
+                acc[r] = _mm256_add_epi32(acc[r], _mm256_madd_epi16(pair, one));
+            }
+        }
+        __m256 sw = _mm256_loadu_ps(ps + g * 8);
+        for (size_t r = 0; r < rows; r++) {
+            __m256 s = _mm256_mul_ps(sw, _mm256_set1_ps(j->sx[(first + r) * groups + g]));
+            sums[r] = _mm256_fmadd_ps(_mm256_cvtepi32_ps(acc[r]), s, sums[r]);
+        }
+    }
+    for (size_t r = 0; r < rows; r++) {
+        float *dst = j->y + (first + r) * j->n + panel * 8;
+        float tail[8];
+        _mm256_storeu_ps(tail, sums[r]);
+        size_t count = j->n - panel * 8 < 8 ? j->n - panel * 8 : 8;
+        memcpy(dst, tail, count * sizeof(float));
+    }
+}
+
+__attribute__((target("avx2,fma"))) static void *panel_worker(void *arg) {
+    struct panel_job *j = (struct panel_job *)arg;
+    size_t groups = (j->k + 63) / 64;
+    size_t panels = (j->n + 7) / 8;
+    size_t panel_stride = groups * 512 / (j->bits == 4 ? 2 : 1);
+    int buffered = j->bits == 4 && j->m >= 16; /* int8.rs:241 */
+    uint8_t *expanded = buffered ? (uint8_t *)malloc(groups * 512) : NULL;
+    for (;;) {
+        size_t tile = __atomic_fetch_add(&j->next, 1, __ATOMIC_RELAXED);
+        if (tile >= j->tiles) break;
+        size_t end = tile * 4 + 4 < panels ? tile * 4 + 4 : panels;
+        for (size_t panel = tile * 4; panel < end; panel++) {
+            const uint8_t *pd = j->data + panel * panel_stride;
+            const float *ps = j->pscales + panel * groups * 8;
+            int q4 = j->bits == 4;
+            if (buffered) { /* int8.rs:446-480 project_buffered */
+                for (size_t at = 0; at < groups * 512; at += 32)
+                    _mm256_storeu_si256((__m256i *)(expanded + at), unpack_q4(pd + at / 2));
+                pd = expanded;
+                q4 = 0;
+            }
+            size_t full = j->m / 4 * 4; /* project_panel::<4>, int8.rs:496-522 */
+            for (size_t r = 0; r < full; r += 4) panel_rows(j, pd, ps, q4, panel, r, 4);
+            if (j->m > full) panel_rows(j, pd, ps, q4, panel, full, j->m - full);
+        }
+    }
+    free(expanded);
+    return NULL;
+}
+#endif
+
+int or_panel_apply_avx2(const uint8_t *data, const float *pscales, size_t n, size_t k, int bits,
+                        const int8_t *qx, const float *sx, size_t m, int threads, float *y) {
+#if defined(__x86_64__)
+    if (!or_has_avx2()) return -1;
+    struct panel_job job = {data, pscales, n, k, m, bits, qx, sx, y, (n + 31) / 32, 0};
+    if (threads <= 1) {
+        panel_worker(&job);
+        return 0;
+    }
+    pthread_t *ids = (pthread_t *)malloc(sizeof(pthread_t) * (size_t)threads);
+    for (int t = 0; t < threads; t++) pthread_create(&ids[t], NULL, panel_worker, &job);
+    for (int t = 0; t < threads; t++) pthread_join(ids[t], NULL);
+    free(ids);
+    return 0;
+#else
+    (void)data; (void)pscales; (void)n; (void)k; (void)bits; (void)qx; (void)sx; (void)m;
+    (void)threads; (void)y;
+    return -1;
+#endif
+}
+
+/* ------------------------------------------------------------------------ */
+/* a11/a12: per-row int8, webgpu/int8.rs                                     */
+/* ------------------------------------------------------------------------ */
+
+/* webgpu/int8.rs:115 even(): floor-based round half to even. */
+static int32_t even(float v) {
+    float lo = floorf(v);
+    float f = v - lo;
+    int32_t i = (int32_t)lo;
+    return i + ((f > 0.5f || (f == 0.5f && (i & 1) == 1)) ? 1 : 0);
+}
+
+void or_i8_quantize_rows(const float *x, size_t rows, size_t k, int8_t *q, float *scales,
+                         int32_t *sums) {
+    for (size_t r = 0; r < rows; r++) {
+        const float *row = x + r * k;
+        float maximum = 0.0f;
+        for (size_t j = 0; j < k; j++) maximum = fmaxf(maximum, fabsf(row[j]));
+        float scale = maximum / 127.0f;
+        int32_t total = 0;
+        for (size_t j = 0; j < k; j++) {
+            int32_t v = 0;
+            if (scale > 0.0f) {
+                v = even(row[j] / scale);
+                if (v < -127) v = -127;
+                if (v > 127) v = 127;
+            }
+            total += v;
+            q[r * k + j] = (int8_t)v;
+        }
+        scales[r] = scale;
+        if (sums) sums[r] = total;
+    }
+}
+
+struct i8_job {
+    const int8_t *qa, *qw;
+    const float *sa, *sw;
+    size_t m, n, k;
+    int32_t *raw;
+    float *y;
+    size_t next;
+};
+
+static void *i8_worker(void *arg) {
+    struct i8_job *j = (struct i8_job *)arg;
+    for (;;) {
+        size_t r = __atomic_fetch_add(&j->next, 1, __ATOMIC_RELAXED);
+        if (r >= j->m) break;
+        const int8_t *a = j->qa + r * j->k;
+        for (size_t c = 0; c < j->n; c++) {
+            const int8_t *b = j->qw + c * j->k;
+            int32_t dot = 0;
+            for (size_t i = 0; i < j->k; i++) dot += (int32_t)a[i] * (int32_t)b[i];
+            if (j->raw) j->raw[r * j->n + c] = dot;
+            if (j->y) j->y[r * j->n + c] = ((float)dot * j->sa[r]) * j->sw[c];
+        }
+    }
+    return NULL;
+}
+
+void or_i8_gemm(const int8_t *qa, const float *sa, size_t m, const int8_t *qw, const float *sw,
+                size_t n, size_t k, int threads, int32_t *raw, float *y) {
+    struct i8_job job = {qa, qw, sa, sw, m, n, k, raw, y, 0};
+    if (threads <= 1) {
+        i8_worker(&job);
+        return;
+    }
+    pthread_t *ids = (pthread_t *)malloc(sizeof(pthread_t) * (size_t)threads);
+    for (int t = 0; t < threads; t++) pthread_create(&ids[t], NULL, i8_worker, &job);
+    for (int t = 0; t < threads; t++) pthread_join(ids[t], NULL);
+    free(ids);
+}
+
+/* ------------------------------------------------------------------------ */
+/* W4A16 closed form                                                         */
+/* ------------------------------------------------------------------------ */
+
+void or_w4a16(const uint16_t *x_f16, size_t m, size_t k, const float *w, size_t n, double *y) {
+    double *xr = (double *)malloc(k * sizeof(double));
+    for (size_t r = 0; r < m; r++) {
+        for (size_t i = 0; i < k; i++) xr[i] = (double)or_f16_to_f32(x_f16[r * k + i]);
+        for (size_t c = 0; c < n; c++) {
+            const float *wr = w + c * k;
+            double acc = 0.0;
+            for (size_t i = 0; i < k; i++) acc += xr[i] * (double)wr[i];
+            y[r * n + c] = acc;
+        }
+    }
+    free(xr);
+}
+
+/* ------------------------------------------------------------------------ */
+/* a14: epilogues                                                            */
+/* ------------------------------------------------------------------------ */
+
+void or_layernorm(float *x, size_t rows, size_t d, const float *w, const float *b, float eps) {
+    for (size_t r = 0; r < rows; r++) {
+        float *row = x + r * d;
+        float sum = 0.0f;
+        for (size_t i = 0; i < d; i++) sum = sum + row[i];
+        float mean = sum / (float)d;
+        float var = 0.0f;
+        for (size_t i = 0; i < d; i++) var = var + (row[i] - mean) * (row[i] - mean);
+        var = var / (float)d;
+        float inv = 1.0f / sqrtf(var + eps);
+        for (size_t i = 0; i < d; i++) row[i] = (row[i] - mean) * inv * w[i] + b[i];
+    }
+}
+
+void or_gelu(float *x, size_t n) {
+    for (size_t i = 0; i < n; i++) x[i] = 0.5f * x[i] * (1.0f + erff(x[i] * 0.70710678118654752f));
+}
+
+void or_rmsnorm(const float *x, size_t rows, size_t d, const float *w, float eps, int zero_centered,
+                float *y) {
+    for (size_t r = 0; r < rows; r++) {
+        const float *src = x + r * d;
+        float ss = 0.0f;
+        for (size_t i = 0; i < d; i++) ss = ss + src[i] * src[i];
+        float scale = 1.0f / sqrtf(ss / (float)d + eps);
+        for (size_t i = 0; i < d; i++) y[r * d + i] = (src[i] * scale) * (zero_centered ? 1.0f + w[i] : w[i]);
+    }
+}
+
+static float silu(float v) { return v * (1.0f / (1.0f + expf(-v))); }
+
+void or_silu_mul(float *gate, const float *up, size_t n) {
+    for (size_t i = 0; i < n; i++) gate[i] = silu(gate[i]) * up[i];
+}
+
+void or_softmax(float *x, size_t n) {
+    float maximum = -INFINITY;
+    for (size_t i = 0; i < n; i++) maximum = fmaxf(maximum, x[i]);
+    float sum = 0.0f;
+    for (size_t i = 0; i < n; i++) {
+        x[i] = expf(x[i] - maximum);
+        sum = sum + x[i];
+    }
+    for (size_t i = 0; i < n; i++) x[i] = x[i] / sum;
+}
+
+void or_mean_rows(const float *x, size_t rows, size_t d, float *out) {
+    for (size_t i = 0; i < d; i++) out[i] = 0.0f;
+    for (size_t r = 0; r < rows; r++)
+        for (size_t i = 0; i < d; i++) out[i] = out[i] + x[r * d + i];
+    for (size_t i = 0; i < d; i++) out[i] = out[i] / (float)rows;
+}
+
+void or_attention(const float *q, const float *k, const float *v, size_t seq, size_t heads,
+                  size_t dh, float scale, float *out) {
+    size_t width = heads * dh;
+    double *p = (double *)malloc(seq * sizeof(double));
+    for (size_t h = 0; h < heads; h++) {
+        for (size_t i = 0; i < seq; i++) {
+            double maximum = -INFINITY;
+            for (size_t j = 0; j < seq; j++) {
+                double dot = 0.0;
+                for (size_t d = 0; d < dh; d++)
+                    dot += (double)q[i * width + h * dh + d] * (double)k[j * width + h * dh + d];
+                p[j] = dot * (double)scale;
+                if (p[j] > maximum) maximum = p[j];
+            }
+            double sum = 0.0;
+            for (size_t j = 0; j < seq; j++) {
+                p[j] = exp(p[j] - maximum);
+                sum += p[j];
+            }
+            for (size_t d = 0; d < dh; d++) {
+                double acc = 0.0;
+                for (size_t j = 0; j < seq; j++) acc += p[j] * (double)v[j * width + h * dh + d];
+                out[i * width + h * dh + d] = (float)(acc / sum);
+            }
+        }
+    }
+    free(p);
+}
+
+void or_silu_requant(const float *gate, const float *up, size_t m, size_t n, int8_t *q, float *s) {
+    size_t blocks = n / 64;
+    float values[64];
+    for (size_t r = 0; r < m; r++) {
+        for (size_t b = 0; b < blocks; b++) {
+            for (int i = 0; i < 64; i++) {
+                size_t at = r * n + b * 64 + (size_t)i;
+                values[i] = silu(gate[at]) * up[at];
+            }
+            float scale = or_group_scale(values, 64, 8);
+            s[r * blocks + b] = scale;
+            or_group_codes(values, 64, scale, 8, q + (r * blocks + b) * 64);
+        }
+    }
+}

@@ -1,0 +1,369 @@
+"""numpy front end for the C oracle (liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg use this module as the checker. The product package
+(decisive_amd) never imports it.
+
+Every wrapper names the function of oracle.c it calls; oracle.c cites the
+reference file:line each function restates.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "liboracle.so"
+
+_lib = None
+
+
+def build(force: bool = False) -> Path:
+    """Compile liboracle.so with the committed Makefile."""
+    if force or not LIB_PATH.exists():
+        subprocess.run(["make", "-s", "-C", str(HERE), "-B" if force else "all"], check=True)
+    return LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        _lib = ctypes.CDLL(str(LIB_PATH))
+        _declare(_lib)
+    return _lib
+
+
+P = ctypes.c_void_p
+SZ = ctypes.c_size_t
+I = ctypes.c_int
+F = ctypes.c_float
+
+
+def _declare(L):
+    sig = {
+        "or_packed_size": (SZ, [SZ, SZ, I]),
+        "or_pack_g64": (I, [P, SZ, SZ, I, P]),
+        "or_unpack_g64": (I, [P, SZ, I, P]),
+        "or_project": (I, [P, I, SZ, P, SZ, P]),
+        "or_g32_size": (SZ, [SZ, SZ]),
+        "or_pack_g32_f16": (I, [P, SZ, SZ, P]),
+        "or_unpack_g32_f16": (I, [P, SZ, P]),
+        "or_group_scale": (F, [P, SZ, I]),
+        "or_group_codes": (None, [P, SZ, F, I, P]),
+        "or_weight_quantize": (I, [P, SZ, SZ, I, P, P]),
+        "or_act_quantize": (None, [P, SZ, SZ, I, P, P]),
+        "or_grouped_gemm": (None, [P, P, SZ, P, P, SZ, SZ, I, P]),
+        "or_matrix_apply": (None, [P, SZ, P, P, SZ, SZ, I, I, P]),
+        "or_panel_bytes": (SZ, [SZ, SZ, I]),
+        "or_panel_pack": (None, [P, P, SZ, SZ, I, P, P]),
+        "or_panel_apply_avx2": (I, [P, P, SZ, SZ, I, P, P, SZ, I, P]),
+        "or_has_avx2": (I, []),
+        "or_i8_quantize_rows": (None, [P, SZ, SZ, P, P, P]),
+        "or_i8_gemm": (None, [P, P, SZ, P, P, SZ, SZ, I, P, P]),
+        "or_w4a16": (None, [P, SZ, SZ, P, SZ, P]),
+        "or_layernorm": (None, [P, SZ, SZ, P, P, F]),
+        "or_gelu": (None, [P, SZ]),
+        "or_rmsnorm": (None, [P, SZ, SZ, P, F, I, P]),
+        "or_silu_mul": (None, [P, P, SZ]),
+        "or_softmax": (None, [P, SZ]),
+        "or_mean_rows": (None, [P, SZ, SZ, P]),
+        "or_attention": (None, [P, P, P, SZ, SZ, SZ, F, P]),
+        "or_silu_requant": (None, [P, P, SZ, SZ, P, P]),
+        "or_f32_to_bf16_n": (None, [P, SZ, P]),
+        "or_f32_to_f16_n": (None, [P, SZ, P]),
+        "or_f16_to_f32_n": (None, [P, SZ, P]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+
+
+def _p(a: np.ndarray):
+    assert a.flags["C_CONTIGUOUS"], "oracle arrays must be C-contiguous"
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _c(a, dtype):
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+class OracleError(ValueError):
+    pass
+
+
+# ---- IEEE conversions ----------------------------------------------------
+
+def f32_to_bf16(x) -> np.ndarray:
+    x = _c(x, np.float32)
+    out = np.empty(x.shape, np.uint16)
+    lib().or_f32_to_bf16_n(_p(x), x.size, _p(out))
+    return out
+
+
+def bf16_to_f32(h) -> np.ndarray:
+    h = _c(h, np.uint16)
+    return (h.astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_f16_bits(x) -> np.ndarray:
+    x = _c(x, np.float32)
+    out = np.empty(x.shape, np.uint16)
+    lib().or_f32_to_f16_n(_p(x), x.size, _p(out))
+    return out
+
+
+def f16_bits_to_f32(h) -> np.ndarray:
+    h = _c(h, np.uint16)
+    out = np.empty(h.shape, np.float32)
+    lib().or_f16_to_f32_n(_p(h), h.size, _p(out))
+    return out
+
+
+# ---- wire layouts ----------------------------------------------------------
+
+def packed_size(rows, cols, bits) -> int:
+    return int(lib().or_packed_size(rows, cols, bits))
+
+
+def pack_g64(bf16, rows, cols, bits) -> np.ndarray:
+    """or_pack_g64: packed.rs:31-56."""
+    bf16 = _c(bf16, np.uint16).reshape(-1)
+    size = packed_size(rows, cols, bits)
+    if not size or bf16.size != rows * cols:
+        raise OracleError("invalid group-64 matrix shape")
+    out = np.empty(size, np.uint8)
+    rc = lib().or_pack_g64(_p(bf16), rows, cols, bits, _p(out))
+    if rc == -2:
+        raise OracleError("nonfinite packed weight")
+    if rc:
+        raise OracleError("invalid group-64 matrix shape")
+    return out
+
+
+def unpack_g64(packed, bits) -> np.ndarray:
+    """or_unpack_g64: packed.rs:59-73."""
+    packed = _c(packed, np.uint8).reshape(-1)
+    stride = packed_size(1, 64, bits)
+    if packed.size == 0 or not stride or packed.size % stride:
+        raise OracleError("invalid packed rows")
+    out = np.empty(packed.size // stride * 64, np.float32)
+    rc = lib().or_unpack_g64(_p(packed), packed.size, bits, _p(out))
+    if rc:
+        raise OracleError("invalid packed scale" if rc == -3 else "invalid packed rows")
+    return out
+
+
+def project(packed, bits, cols, x, outputs) -> np.ndarray:
+    """or_project: packed.rs:75-119."""
+    packed = _c(packed, np.uint8).reshape(-1)
+    x = _c(x, np.float32).reshape(-1)
+    y = np.empty(outputs, np.float32)
+    rc = lib().or_project(_p(packed), bits, cols, _p(x), outputs, _p(y))
+    if rc:
+        raise OracleError("invalid packed readout" if rc == -1 else "nonfinite readout activation")
+    return y
+
+
+def pack_g32_f16(w, rows, cols) -> np.ndarray:
+    w = _c(w, np.float32).reshape(-1)
+    size = int(lib().or_g32_size(rows, cols))
+    if not size or w.size != rows * cols:
+        raise OracleError("invalid group-32 matrix shape")
+    out = np.empty(size, np.uint8)
+    rc = lib().or_pack_g32_f16(_p(w), rows, cols, _p(out))
+    if rc:
+        raise OracleError("nonfinite weight" if rc == -2 else "invalid group-32 matrix shape")
+    return out
+
+
+def unpack_g32_f16(packed) -> np.ndarray:
+    packed = _c(packed, np.uint8).reshape(-1)
+    if packed.size == 0 or packed.size % 18:
+        raise OracleError("invalid packed rows")
+    out = np.empty(packed.size // 18 * 32, np.float32)
+    rc = lib().or_unpack_g32_f16(_p(packed), packed.size, _p(out))
+    if rc:
+        raise OracleError("invalid packed scale")
+    return out
+
+
+# ---- grouped quantizers ------------------------------------------------------
+
+def group_scale(x, bits) -> float:
+    x = _c(x, np.float32).reshape(-1)
+    return float(lib().or_group_scale(_p(x), x.size, bits))
+
+
+def group_codes(x, scale, bits) -> np.ndarray:
+    x = _c(x, np.float32).reshape(-1)
+    out = np.empty(x.size, np.int8)
+    lib().or_group_codes(_p(x), x.size, np.float32(scale), bits, _p(out))
+    return out
+
+
+def weight_quantize(bf16, n, k, bits):
+    """or_weight_quantize: int8.rs:51-152 -> (codes [n, G*64] i8, scales [n, G] f32)."""
+    bf16 = _c(bf16, np.uint16).reshape(-1)
+    g = (k + 63) // 64
+    codes = np.empty((n, g * 64), np.int8)
+    scales = np.empty((n, g), np.float32)
+    rc = lib().or_weight_quantize(_p(bf16), n, k, bits, _p(codes), _p(scales))
+    if rc:
+        raise OracleError("non-finite INT8 weight" if rc == -2 else "invalid INT8 matrix shape")
+    return codes, scales
+
+
+def act_quantize(x, m, k, bits=8):
+    """or_act_quantize: int8.rs:178-202 -> (q [m, G*64] i8, s [m, G] f32)."""
+    x = _c(x, np.float32).reshape(-1)
+    g = (k + 63) // 64
+    q = np.empty((m, g * 64), np.int8)
+    s = np.empty((m, g), np.float32)
+    if m:
+        lib().or_act_quantize(_p(x), m, k, bits, _p(q), _p(s))
+    return q, s
+
+
+def grouped_gemm(qx, sx, m, qw, sw, n, k, fused=True) -> np.ndarray:
+    """or_grouped_gemm: int8.rs:524-585 (fused) / :259-287 (unfused)."""
+    y = np.empty((m, n), np.float32)
+    if m and n:
+        lib().or_grouped_gemm(_p(_c(qx, np.int8)), _p(_c(sx, np.float32)), m,
+                              _p(_c(qw, np.int8)), _p(_c(sw, np.float32)), n, k,
+                              1 if fused else 0, _p(y))
+    return y
+
+
+def matrix_apply(x, m, qw, sw, n, k, act_bits=8, fused=True) -> np.ndarray:
+    """or_matrix_apply: int8.rs:166-176."""
+    x = _c(x, np.float32).reshape(-1)
+    y = np.empty((m, n), np.float32)
+    if m and n:
+        lib().or_matrix_apply(_p(x), m, _p(_c(qw, np.int8)), _p(_c(sw, np.float32)), n, k,
+                              act_bits, 1 if fused else 0, _p(y))
+    return y
+
+
+def panel_pack(codes, scales, n, k, bits):
+    codes = _c(codes, np.int8)
+    scales = _c(scales, np.float32)
+    g = (k + 63) // 64
+    data = np.empty(int(lib().or_panel_bytes(n, k, bits)), np.uint8)
+    ps = np.empty((n + 7) // 8 * g * 8, np.float32)
+    lib().or_panel_pack(_p(codes), _p(scales), n, k, bits, _p(data), _p(ps))
+    return data, ps
+
+
+def has_avx2() -> bool:
+    return bool(lib().or_has_avx2())
+
+
+def panel_apply_avx2(data, ps, n, k, bits, qx, sx, m, threads=1) -> np.ndarray:
+    """or_panel_apply_avx2: int8.rs:229-256 + :404-585."""
+    y = np.empty((m, n), np.float32)
+    rc = lib().or_panel_apply_avx2(_p(data), _p(ps), n, k, bits, _p(_c(qx, np.int8)),
+                                   _p(_c(sx, np.float32)), m, threads, _p(y))
+    if rc:
+        raise OracleError("AVX2/FMA unavailable")
+    return y
+
+
+# ---- per-row int8 ---------------------------------------------------------------
+
+def i8_quantize_rows(x, rows, k):
+    """or_i8_quantize_rows: webgpu/int8.rs:107-145 -> (q [rows,k], scale [rows], sum [rows])."""
+    x = _c(x, np.float32).reshape(-1)
+    q = np.empty((rows, k), np.int8)
+    s = np.empty(rows, np.float32)
+    sums = np.empty(rows, np.int32)
+    lib().or_i8_quantize_rows(_p(x), rows, k, _p(q), _p(s), _p(sums))
+    return q, s, sums
+
+
+def i8_gemm(qa, sa, m, qw, sw, n, k, threads=1, raw=True, scaled=True):
+    """or_i8_gemm: webgpu/int8.rs:147-242 -> (i32 [m,n] or None, f32 [m,n] or None)."""
+    r = np.empty((m, n), np.int32) if raw else None
+    y = np.empty((m, n), np.float32) if scaled else None
+    lib().or_i8_gemm(_p(_c(qa, np.int8)), _p(_c(sa, np.float32)), m, _p(_c(qw, np.int8)),
+                     _p(_c(sw, np.float32)), n, k, threads,
+                     _p(r) if raw else None, _p(y) if scaled else None)
+    return r, y
+
+
+# ---- W4A16 closed form and epilogues --------------------------------------------
+
+def w4a16(x_f16_bits, m, k, w_dequant, n) -> np.ndarray:
+    y = np.empty((m, n), np.float64)
+    lib().or_w4a16(_p(_c(x_f16_bits, np.uint16)), m, k, _p(_c(w_dequant, np.float32)), n, _p(y))
+    return y
+
+
+def layernorm(x, w, b, eps):
+    x = np.array(x, np.float32, copy=True, order="C")
+    rows, d = x.shape
+    lib().or_layernorm(_p(x), rows, d, _p(_c(w, np.float32)), _p(_c(b, np.float32)), np.float32(eps))
+    return x
+
+
+def gelu(x):
+    x = np.array(x, np.float32, copy=True, order="C")
+    lib().or_gelu(_p(x), x.size)
+    return x
+
+
+def rmsnorm(x, w, eps, zero_centered=True):
+    x = _c(x, np.float32)
+    rows, d = x.shape
+    y = np.empty_like(x)
+    lib().or_rmsnorm(_p(x), rows, d, _p(_c(w, np.float32)), np.float32(eps),
+                     1 if zero_centered else 0, _p(y))
+    return y
+
+
+def silu_mul(gate, up):
+    g = np.array(gate, np.float32, copy=True, order="C")
+    lib().or_silu_mul(_p(g), _p(_c(up, np.float32)), g.size)
+    return g
+
+
+def softmax(x):
+    x = np.array(x, np.float32, copy=True, order="C")
+    lib().or_softmax(_p(x), x.size)
+    return x
+
+
+def mean_rows(x):
+    x = _c(x, np.float32)
+    rows, d = x.shape
+    out = np.empty(d, np.float32)
+    lib().or_mean_rows(_p(x), rows, d, _p(out))
+    return out
+
+
+def attention(q, k, v, heads, scale):
+    q, k, v = (_c(a, np.float32) for a in (q, k, v))
+    seq, width = q.shape
+    out = np.empty_like(q)
+    lib().or_attention(_p(q), _p(k), _p(v), seq, heads, width // heads, np.float32(scale), _p(out))
+    return out
+
+
+def silu_requant(gate, up):
+    gate = _c(gate, np.float32)
+    up = _c(up, np.float32)
+    m, n = gate.shape
+    q = np.empty((m, n), np.int8)
+    s = np.empty((m, n // 64), np.float32)
+    lib().or_silu_requant(_p(gate), _p(up), m, n, _p(q), _p(s))
+    return q, s
+
+
+def nprocs_env_default() -> int:
+    return max(1, min(16, os.cpu_count() or 1))

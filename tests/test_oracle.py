@@ -1,0 +1,358 @@
+"""Pins the CPU oracle before it is trusted as the checker.
+
+Each test checks the oracle against something other than its own formula: the
+reference's committed known-answer vectors, numpy/torch IEEE conversions,
+integer brute force, float64 closed forms, or the reference tests' own
+invariants (src/models/pplx_flash/int8.rs:591-962, packed.rs:121-208).
+"""
+import json
+import math
+import struct
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+GOLDEN = json.loads((Path(__file__).parent / "golden" / "reference_vectors.json").read_text())
+
+
+def bf16_bytes(values):
+    """The reference tests build BF16 by truncating f32 bits (packed.rs:135-138)."""
+    v = np.asarray(values, np.float32)
+    return (v.view(np.uint32) >> 16).astype(np.uint16)
+
+
+def half_bf16(values, o):
+    """half::bf16::from_f32 (round to nearest even), as int8.rs:692 uses."""
+    return o.f32_to_bf16(np.asarray(values, np.float32))
+
+
+# ---- IEEE conversions against independent libraries -------------------------
+
+def test_f16_conversion_matches_numpy(oracle):
+    rng = np.random.default_rng(3)
+    x = np.concatenate([
+        rng.standard_normal(20000).astype(np.float32) * np.float32(100),
+        rng.standard_normal(20000).astype(np.float32) * np.float32(1e-5),
+        np.array([0.0, -0.0, 65504.0, 65520.0, 65519.99, 6.1035156e-05, 5.96e-08, 2.98e-08,
+                  2.9802322e-08, 8.9406967e-08, np.inf, -np.inf, 1e-30], np.float32),
+    ])
+    got = oracle.f32_to_f16_bits(x)
+    want = x.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, want)
+    back = oracle.f16_bits_to_f32(got)
+    assert np.array_equal(back.view(np.uint32), want.view(np.float16).astype(np.float32).view(np.uint32))
+
+
+def test_bf16_conversion_matches_torch(oracle):
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal(50000).astype(np.float32) * np.float32(3)
+    x[:4] = [0.0, -0.0, 3.4e38, 1e-40]
+    got = oracle.f32_to_bf16(x)
+    want = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, want)
+
+
+# ---- golden vectors held by the reference --------------------------------------
+
+def test_q4_golden_group(oracle):
+    g = GOLDEN["q4_group"]
+    raw = bf16_bytes(g["values"] * g["repeat"])
+    packed = oracle.pack_g64(raw, 1, 64, 4)
+    assert packed.tobytes() == bytes.fromhex(g["bytes_hex"]) * g["bytes_repeat"] + struct.pack("<f", g["scale"])
+    z = GOLDEN["q4_zero_group"]
+    packed = oracle.pack_g64(np.zeros(64, np.uint16), 1, 64, 4)
+    assert packed.tobytes() == bytes.fromhex(z["bytes_hex"]) * z["bytes_repeat"] + struct.pack("<f", 2.0 ** z["scale_exponent"])
+
+
+def test_q8_golden_group(oracle):
+    g = GOLDEN["q8_group"]
+    packed = oracle.pack_g64(bf16_bytes(g["values"] * g["repeat"]), 1, 64, 8)
+    assert packed.tobytes() == bytes(g["bytes"] * g["bytes_repeat"]) + struct.pack("<f", g["scale"])
+    packed = oracle.pack_g64(np.zeros(64, np.uint16), 1, 64, 8)
+    assert packed.tobytes() == bytes(64) + struct.pack("<f", 2.0 ** -126)
+
+
+def test_quantized_rows_ties_to_even_and_signed_zero(oracle):
+    for case in GOLDEN["quantized_rows"]["cases"]:
+        x = np.array(case["input"], np.float32)
+        for div in (1.0, 16.0):
+            v = x / np.float32(div)
+            s = oracle.group_scale(v, case["bits"])
+            codes = oracle.group_codes(v, s, case["bits"])
+            deq = codes.astype(np.float32) * np.float32(s)
+            assert np.array_equal(deq, np.array(case["expected"], np.float32) / np.float32(div))
+        zeros = np.array([0.0, -0.0, 0.0, -0.0], np.float32)
+        s = oracle.group_scale(zeros, case["bits"])
+        deq = oracle.group_codes(zeros, s, case["bits"]).astype(np.float32) * np.float32(s)
+        assert not np.signbit(deq).any() and (deq == 0).all()
+
+
+# ---- packed.rs tests restated ------------------------------------------------
+
+def test_grouped_codes_and_scale_match_native(oracle):
+    """packed.rs:124-161: wire codes/scales == Matrix codes/scales; sizes."""
+    values = np.array([(i - 32.0) / 16.0 if i < 64 else (i - 96.0) * 8.0 for i in range(128)], np.float32)
+    raw = bf16_bytes(values)
+    for bits, group in ((4, 36), (8, 68)):
+        packed = oracle.pack_g64(raw, 1, 128, bits)
+        assert packed.size == 2 * group
+        codes, scales = oracle.weight_quantize(raw, 1, 128, bits)
+        for g in range(2):
+            blk = packed[g * group:(g + 1) * group]
+            assert blk[-4:].tobytes() == struct.pack("<f", scales[0, g])
+            if bits == 4:
+                wire = np.stack([(blk[:32] & 15), (blk[:32] >> 4)], 1).reshape(-1).astype(np.int32) - 8
+            else:
+                wire = blk[:64].view(np.int8).astype(np.int32)
+            assert np.array_equal(wire, codes[0, g * 64:(g + 1) * 64].astype(np.int32))
+        assert oracle.unpack_g64(packed, bits).size == 128
+        assert np.isfinite(oracle.project(packed, bits, 128, values, 1)[0])
+    assert oracle.packed_size(1, 63, 4) == 0
+    assert oracle.packed_size(1, 64, 2) == 0
+
+
+def test_packed_projection_and_embeddings_match_native(oracle):
+    """packed.rs:162-208: project == scalar Matrix::apply exactly; unpack == append."""
+    n, k = 67, 128
+    i = np.arange(n * k)
+    values = np.where(i % 128 >= 64, 0.0, ((i * 23 % 127) - 63) / 32.0).astype(np.float32)
+    raw = bf16_bytes(values)
+    x = np.array([127.0 if j == 0 else ((j % 9) - 4.0) * 0.5 for j in range(k)], np.float32)
+    for bits in (4, 8):
+        packed = oracle.pack_g64(raw, n, k, bits)
+        codes, scales = oracle.weight_quantize(raw, n, k, bits)
+        reference = oracle.matrix_apply(x, 1, codes, scales, n, k, 8, fused=False)[0]
+        assert np.array_equal(oracle.project(packed, bits, k, x, 3), reference[:3])
+        assert np.array_equal(oracle.project(packed, bits, k, x, n), reference)
+        row = oracle.packed_size(1, k, bits)
+        decoded = oracle.unpack_g64(packed[5 * row:6 * row], bits)
+        append = codes[5, :k].astype(np.float32) * np.repeat(scales[5], 64)[:k]
+        assert np.array_equal(decoded, append)
+
+
+def test_unpack_rejects_bad_scales_and_lengths(oracle):
+    packed = oracle.pack_g64(bf16_bytes(np.ones(64)), 1, 64, 4)
+    bad = packed.copy()
+    bad[-4:] = np.frombuffer(struct.pack("<f", -1.0), np.uint8)
+    with pytest.raises(oracle.OracleError):
+        oracle.unpack_g64(bad, 4)
+    with pytest.raises(oracle.OracleError):
+        oracle.unpack_g64(packed[:-1], 4)
+    with pytest.raises(oracle.OracleError):
+        oracle.pack_g64(bf16_bytes([np.nan] + [0.0] * 63), 1, 64, 4)
+
+
+# ---- int8.rs tests restated ---------------------------------------------------
+
+def _independent_grouped(x, weights, m, k, n, ab, wb):
+    """int8.rs:701-733: per-group codes by numpy rint in f32, dot in float64."""
+    out = np.zeros((m, n))
+    for r in range(m):
+        for c in range(n):
+            total = 0.0
+            for g in range(0, k, 64):
+                xv = x[r * k + g:r * k + min(g + 64, k)]
+                wv = weights[c * k + g:c * k + min(g + 64, k)]
+
+                def quant(v, bits):
+                    lim = np.float32(7 if bits == 4 else 127)
+                    s = max(np.float32(np.abs(v).max() / lim), np.float32(np.finfo(np.float32).tiny))
+                    inv = np.float32(1) / np.float32(s)
+                    return np.clip(np.rint(v * inv), -lim, lim).astype(np.int64), s
+
+                a, sa = quant(xv, ab)
+                b, sb = quant(wv, wb)
+                total += float((a * b).sum()) * float(np.float32(sa * sb))
+            out[r, c] = total
+    return out
+
+
+@pytest.mark.parametrize("wb,ab", GOLDEN["grouped_dot_shapes"]["bits"])
+def test_q4_and_q8_match_independent_grouped_dots(oracle, wb, ab):
+    tol = GOLDEN["grouped_dot_shapes"]["tolerance"]
+    for m, k, n in GOLDEN["grouped_dot_shapes"]["mkn"]:
+        i = np.arange(k * n)
+        weights = half_bf16(((i * 37 % 257) - 128.0) / 31.0, oracle)
+        wf = oracle.bf16_to_f32(weights)
+        x = (((np.arange(m * k) * 13 % 255) - 127.0) / 17.0).astype(np.float32)
+        expected = _independent_grouped(x, wf, m, k, n, ab, wb)
+        codes, scales = oracle.weight_quantize(weights, n, k, wb)
+        a = oracle.matrix_apply(x, m, codes, scales, n, k, ab, fused=True)
+        b = oracle.matrix_apply(x, m, codes, scales, n, k, ab, fused=False)
+        assert np.all(np.abs(a - expected) <= tol["abs"] + np.abs(expected) * tol["rel"])
+        assert np.all(np.abs(b - expected) <= tol["abs"] + np.abs(expected) * tol["rel"])
+        if m and oracle.has_avx2() and ab == 8:
+            qx, sx = oracle.act_quantize(x, m, k, ab)
+            data, ps = oracle.panel_pack(codes, scales, n, k, wb)
+            for threads in (1, 3):
+                avx = oracle.panel_apply_avx2(data, ps, n, k, wb, qx, sx, m, threads)
+                assert np.array_equal(avx.view(np.uint32), a.view(np.uint32)), (m, k, n, threads)
+        z = oracle.matrix_apply(np.zeros(m * k, np.float32), m, codes, scales, n, k, ab)
+        assert (z == 0).all()
+
+
+def test_activation_rounding_at_boundaries(oracle):
+    """int8.rs:774-798 boundary set; codes checked against numpy's rint."""
+    values = [0.0, -0.0, np.finfo(np.float32).tiny, -np.finfo(np.float32).tiny]
+    for i in range(-127, 127):
+        h = np.float32(i + 0.5)
+        values += [np.nextafter(h, np.float32(-np.inf)), h, np.nextafter(h, np.float32(np.inf))]
+    values = np.array(values, np.float32)
+    for s in (1.0, 0.0037, float(np.finfo(np.float32).tiny), 1e30):
+        scaled = (values * np.float32(s)).astype(np.float32)
+        for n in (1, 7, 8, 9, 63, 64, 65, scaled.size):
+            v = scaled[:n]
+            got = oracle.group_codes(v, np.float32(s), 8)
+            inv = np.float32(1) / np.float32(s)
+            want = np.clip(np.rint(v * inv), -127, 127).astype(np.int8)
+            assert np.array_equal(got, want), (s, n)
+            assert (got != -128).all()
+            gs = oracle.group_scale(v, 8)
+            assert gs == max(np.float32(np.abs(v).max() / np.float32(127)), np.finfo(np.float32).tiny)
+
+
+def test_integer_extrema_tails(oracle):
+    """int8.rs:877-949: integer-valued extremes vs float64 closed form."""
+    tol = GOLDEN["extrema_shapes"]["tolerance"]
+    for m, k, n in GOLDEN["extrema_shapes"]["mkn"]:
+        i = np.arange(k * n)
+        w = np.select([i % 5 == 0, i % 5 == 1, i % 5 == 2], [-127.0, 127.0, 0.0], (i % 31) / 8.0).astype(np.float32)
+        j = np.arange(m * k)
+        x = np.select([j % 7 == 0, j % 7 == 1, j % 7 == 2], [127.0, -127.0, 0.0], (j % 13) - 6.0).astype(np.float32)
+        raw = half_bf16(w, oracle)
+        codes, scales = oracle.weight_quantize(raw, n, k, 8)
+        got = oracle.matrix_apply(x, m, codes, scales, n, k, 8, fused=False)
+        expected = _independent_grouped(x, oracle.bf16_to_f32(raw), m, k, n, 8, 8)
+        assert np.all(np.abs(got - expected) <= tol["abs"] + np.abs(expected) * tol["rel"])
+        fused = oracle.matrix_apply(x, m, codes, scales, n, k, 8, fused=True)
+        assert np.all(np.abs(fused - got) <= 0.02 + np.abs(got) * 1e-6)
+
+
+def test_invalid_weights_and_nonfinite_activations(oracle):
+    """int8.rs:952-962."""
+    with pytest.raises(oracle.OracleError):
+        oracle.weight_quantize(np.array([0x7fc0], np.uint16), 1, 1, 8)
+    codes, scales = oracle.weight_quantize(np.zeros(1, np.uint16), 1, 1, 8)
+    assert np.isnan(oracle.matrix_apply(np.array([np.nan], np.float32), 1, codes, scales, 1, 1)[0, 0])
+    assert oracle.matrix_apply(np.zeros(1, np.float32), 1, codes, scales, 1, 1)[0, 0] == 0.0
+
+
+# ---- per-row int8 (webgpu/int8.rs, webgpu/q4.rs known answers) -----------------
+
+@pytest.mark.parametrize("m,n,k", GOLDEN["q4_raw_check_shapes"]["mnk"])
+def test_i8_rows_exact_raw_dots(oracle, m, n, k):
+    """webgpu/q4.rs:476-501: integer-valued inputs quantize to themselves; raw
+    i32 equals the independent signed dot."""
+    a = np.array([127.0 if i % k == 0 else ((i * 17 % 255) - 127.0) for i in range(m * k)], np.float32)
+    b = np.array([127.0 if i % k == 0 else ((i * 11 % 15) - 7.0) for i in range(n * k)], np.float32)
+    qa, sa, suma = oracle.i8_quantize_rows(a, m, k)
+    qb, sb, sumb = oracle.i8_quantize_rows(b, n, k)
+    assert (sa == 1.0).all() and (sb == 1.0).all()
+    assert np.array_equal(qa.astype(np.float32).reshape(-1), a)
+    assert np.array_equal(suma, a.reshape(m, k).sum(1).astype(np.int32))
+    raw, y = oracle.i8_gemm(qa, sa, m, qb, sb, n, k)
+    want = a.reshape(m, k).astype(np.int64) @ b.reshape(n, k).astype(np.int64).T
+    assert np.array_equal(raw, want.astype(np.int32))
+    assert np.array_equal(y, raw.astype(np.float32))
+
+
+def test_i8_quantizer_division_and_zero_rows(oracle):
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((9, 130)).astype(np.float32)
+    x[3] = 0.0
+    q, s, sums = oracle.i8_quantize_rows(x, 9, 130)
+    assert s[3] == 0.0 and (q[3] == 0).all() and sums[3] == 0
+    scale = (np.abs(x).max(1) / np.float32(127)).astype(np.float32)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        want = np.clip(np.rint(x / scale[:, None]), -127, 127)
+    want[3] = 0
+    assert np.array_equal(q.astype(np.float32), want.astype(np.float32))
+    assert np.array_equal(s, scale)
+    r1, y1 = oracle.i8_gemm(q, s, 9, q, s, 9, 130, threads=1)
+    r3, y3 = oracle.i8_gemm(q, s, 9, q, s, 9, 130, threads=3)
+    assert np.array_equal(r1, r3) and np.array_equal(y1, y3)
+    assert np.array_equal(y1, (r1.astype(np.float32) * s[:, None]).astype(np.float32) * s[None, :])
+
+
+# ---- g32/f16 layout (D1) --------------------------------------------------------
+
+def test_g32_f16_layout_invariants(oracle):
+    rng = np.random.default_rng(1)
+    w = (rng.standard_normal((8, 256)) * 0.02).astype(np.float32)
+    w[2, :32] = 0.0
+    w[3, 32:64] = 0.35
+    packed = oracle.pack_g32_f16(w, 8, 256)
+    assert packed.size == 8 * 8 * 18
+    groups = packed.reshape(-1, 18)
+    codes = np.stack([groups[:, :16] & 15, groups[:, :16] >> 4], 2).reshape(-1, 32).astype(np.int32) - 8
+    assert (np.abs(codes) <= 7).all()
+    scales = groups[:, 16:18].copy().view(np.float16).astype(np.float32).reshape(-1)
+    deq = oracle.unpack_g32_f16(packed).reshape(-1, 32)
+    assert np.array_equal(deq, codes.astype(np.float32) * scales[:, None])
+    # an all-zero run keeps the smallest f16 subnormal and decodes to zeros
+    assert scales[2 * 8] == np.float32(2.0 ** -24) and (deq[2 * 8] == 0).all()
+    # a constant run is exact: code 7 with scale v/7 rounded to f16
+    assert (codes[3 * 8 + 1] == 7).all()
+    assert np.allclose(deq[3 * 8 + 1], 0.35, rtol=2 ** -10)
+    # per-group error bound: |w - deq| <= scale/2 (+ the f16 scale rounding)
+    err = np.abs(w.reshape(-1, 32) - deq)
+    assert (err <= scales[:, None] * 0.5 + np.abs(w.reshape(-1, 32)) * 2 ** -10 + 1e-12).all()
+
+
+# ---- closed forms and epilogues -------------------------------------------------
+
+def test_w4a16_closed_form_matches_numpy(oracle):
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((3, 96)).astype(np.float32)
+    xh = oracle.f32_to_f16_bits(x)
+    w = rng.standard_normal((5, 96)).astype(np.float32)
+    got = oracle.w4a16(xh, 3, 96, w, 5)
+    want = oracle.f16_bits_to_f32(xh).astype(np.float64) @ w.astype(np.float64).T
+    assert np.allclose(got, want, rtol=1e-13, atol=1e-13)
+
+
+def test_epilogues_match_float64(oracle):
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((5, 96)).astype(np.float32)
+    w = rng.standard_normal(96).astype(np.float32)
+    b = rng.standard_normal(96).astype(np.float32)
+    xd = x.astype(np.float64)
+    mu = xd.mean(1, keepdims=True)
+    ln = (xd - mu) / np.sqrt(((xd - mu) ** 2).mean(1, keepdims=True) + 1e-12) * w + b
+    assert np.allclose(oracle.layernorm(x, w, b, 1e-12), ln, atol=2e-5)
+    g = np.array([0.5 * v * (1 + math.erf(v / math.sqrt(2))) for v in xd.reshape(-1)]).reshape(x.shape)
+    assert np.allclose(oracle.gelu(x), g, atol=1e-6)
+    rms = xd / np.sqrt((xd ** 2).mean(1, keepdims=True) + 1e-6) * (1 + w)
+    assert np.allclose(oracle.rmsnorm(x, w, 1e-6), rms, atol=2e-5)
+    up = rng.standard_normal(x.shape).astype(np.float32)
+    assert np.allclose(oracle.silu_mul(x, up), xd / (1 + np.exp(-xd)) * up, atol=1e-5)
+    sm = np.exp(xd[0] - xd[0].max())
+    assert np.allclose(oracle.softmax(x[0]), sm / sm.sum(), atol=1e-7)
+    assert np.allclose(oracle.mean_rows(x), xd.mean(0), atol=1e-6)
+
+
+def test_attention_closed_form(oracle):
+    rng = np.random.default_rng(8)
+    seq, heads, dh = 7, 2, 8
+    q, k, v = (rng.standard_normal((seq, heads * dh)).astype(np.float32) for _ in range(3))
+    out = oracle.attention(q, k, v, heads, 1 / math.sqrt(dh))
+    for h in range(heads):
+        sl = slice(h * dh, (h + 1) * dh)
+        s = q[:, sl].astype(np.float64) @ k[:, sl].astype(np.float64).T / math.sqrt(dh)
+        p = np.exp(s - s.max(1, keepdims=True))
+        p /= p.sum(1, keepdims=True)
+        assert np.allclose(out[:, sl], p @ v[:, sl].astype(np.float64), atol=1e-6)
+
+
+def test_silu_requant_is_unfused_composition(oracle):
+    """grouped_q4.rs:27-41 + the a4 quantizer per 64-column block."""
+    rng = np.random.default_rng(9)
+    gate = rng.standard_normal((3, 128)).astype(np.float32)
+    up = rng.standard_normal((3, 128)).astype(np.float32)
+    q, s = oracle.silu_requant(gate, up)
+    v = oracle.silu_mul(gate, up)
+    q2, s2 = oracle.act_quantize(v, 3, 128, 8)
+    assert np.array_equal(q, q2) and np.array_equal(s, s2)
+    assert np.allclose(q.astype(np.float64) * np.repeat(s, 64, 1), v, atol=np.repeat(s, 64, 1) * 0.5 + 1e-12)
