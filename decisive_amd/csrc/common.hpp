@@ -1,0 +1,108 @@
+// common.hpp -- shared definitions of libdecisive_rocm (gfx950 / CDNA4).
+//
+// Native HBM layout of a quantized weight [rows x cols] (called N x K below):
+//
+//   Q4 ("tile16x128"): N is padded to Np = 16*ceil(N/16), K to Kp = 128*ceil(K/128).
+//     codes  : [Np/16][Kp/128][64 lanes][16 bytes]       (1 KiB per chunk)
+//     scales : [Np/16][Kp/128][16 rows][8 bytes]          (128 B per chunk)
+//   Lane l = q*16 + j of a chunk (t, kb) belongs to row n = 16*t + j. Its 16
+//   bytes are four 32-bit words; word s holds the 8 codes of
+//   k = 128*kb + 32*s + 8*q + e (e = 0..7) as (code + 8) nibbles, e = 2p at bits
+//   4p and e = 2p+1 at bits 16 + 4p. With that order
+//     ((word >> 4p) & 0x000F000F) | 0x64006400
+//   is the f16 pair (1024 + code_2p + 8, 1024 + code_2p+1 + 8), so one packed
+//   f16 subtract of 1032 yields the exact codes in k order -- the B fragment of
+//   one v_mfma_f32_16x16x32_f16 per word, loaded with a single 128-bit load.
+//   The 8-byte scale record of (t, kb, j) is four f16 scales (one per 32-run)
+//   for group-32 weights or two f32 scales (one per 64-run) for group-64.
+//
+//   Q8 ("tile16x64"): Kp = 64*ceil(K/64); codes [Np/16][Kp/64][64 lanes][16 B],
+//     lane (q, j) holds int8 codes of k = 64*kb + 16*q + 0..15 in order (the B
+//     fragment of v_mfma_i32_16x16x64_i8); scales [Np/16][Kp/64][16] f32.
+//
+// Padding codes are 0 and padding scales 0, so padded rows/columns contribute
+// nothing; kernels never read activations beyond K.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+namespace dz {
+
+typedef _Float16 half_t;
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef int int4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int uint4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int uint2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+
+enum class WeightKind : int { Q4G64 = 0, Q8G64 = 1, Q4G32 = 2 };
+
+struct Weight {
+    int rows = 0, cols = 0;       // N x K
+    int np = 0, kp = 0;           // padded
+    int bits = 4, group = 64;     // code bits and scale run length
+    int groups = 0;               // ceil(K/64) for the grouped int8 path
+    WeightKind kind = WeightKind::Q4G64;
+    uint8_t *codes = nullptr;     // device
+    uint8_t *scales = nullptr;    // device
+    size_t code_bytes = 0, scale_bytes = 0;
+    int tiles() const { return np / 16; }
+    int kblocks() const { return bits == 4 ? kp / 128 : kp / 64; }
+};
+
+// ---- device helpers ---------------------------------------------------------
+
+__device__ __forceinline__ half8_t as_half8(uint4_t v) { return __builtin_bit_cast(half8_t, v); }
+
+// 8 packed (code+8) nibbles in the tile16x128 order -> 8 exact f16 codes.
+__device__ __forceinline__ uint4_t nibbles_to_half8(uint32_t w) {
+    const half2_t bias = {(half_t)1032.0f, (half_t)1032.0f};
+    uint4_t out;
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+        uint32_t t = ((w >> (4 * p)) & 0x000F000Fu) | 0x64006400u;
+        half2_t h = __builtin_bit_cast(half2_t, t) - bias;
+        out[p] = __builtin_bit_cast(uint32_t, h);
+    }
+    return out;
+}
+
+// 8 packed nibbles -> two words of signed int8 codes in k order (e0..e3, e4..e7).
+__device__ __forceinline__ uint2_t nibbles_to_i8(uint32_t w) {
+    uint32_t lo = w & 0x0F0F0F0Fu;         // bytes: e0 e4 e1 e5
+    uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;  // bytes: e2 e6 e3 e7
+    // offset binary -> two's complement per byte without carries
+    lo = (lo + 0x78787878u) ^ 0x80808080u;
+    hi = (hi + 0x78787878u) ^ 0x80808080u;
+    uint2_t out;
+    out[0] = __builtin_amdgcn_perm(hi, lo, 0x06040200u);  // e0 e1 e2 e3
+    out[1] = __builtin_amdgcn_perm(hi, lo, 0x07050301u);  // e4 e5 e6 e7
+    return out;
+}
+
+__device__ __forceinline__ float4_t mfma_f16(half8_t a, half8_t b, float4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ int4_t mfma_i8(int4_t a, int4_t b, int4_t c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float f16_bits_to_float(uint32_t h) {
+    return (float)__builtin_bit_cast(half_t, (unsigned short)h);
+}
+
+// ---- host helpers ------------------------------------------------------------
+
+struct Status {
+    int32_t code = 0;
+    std::string message;
+};
+
+}  // namespace dz

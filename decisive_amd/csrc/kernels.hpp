@@ -1,0 +1,75 @@
+// kernels.hpp -- host-side launchers of the HIP kernels (internal to the library).
+#pragma once
+
+#include "common.hpp"
+
+namespace dz {
+
+// ---- quant.hip ----------------------------------------------------------------
+// Wire layout -> native layout; sets *bad (device int) when a scale is not
+// finite and positive.
+void launch_upload(const Weight &w, const uint8_t *wire, int *bad, hipStream_t s);
+// Device quantizer from f32/f16/bf16 values (dtype 0/1/2); sets *bad on a
+// non-finite weight.
+void launch_quantize_weight(const Weight &w, const void *values, int dtype, int *bad,
+                            hipStream_t s);
+// y [rows x cols] f32 (or f16 when dtype == 1) of rows ids (nullptr = all rows).
+void launch_dequant(const Weight &w, const int32_t *ids, int count, void *y, int dtype,
+                    hipStream_t s);
+// As launch_dequant; ids outside [0, rows) give zero rows and set *bad.
+void launch_dequant_checked(const Weight &w, const int32_t *ids, int count, void *y, int dtype,
+                            int *bad, hipStream_t s);
+// Native Q4 group-64 -> the packed.rs wire layout for every row (device buffer).
+void launch_export_q4g64(const Weight &w, uint8_t *wire, hipStream_t s);
+// int8.rs:178-202 prepare: q [m x G*64], s [m x G]; sets *bad on non-finite x.
+void launch_act_quantize(const float *x, int m, int k, int bits, int8_t *q, float *sc, int *bad,
+                         hipStream_t s);
+// webgpu/int8.rs:107-145.
+void launch_i8_quantize_rows(const float *x, int rows, int k, int8_t *q, float *scales,
+                             int32_t *sums, hipStream_t s);
+void launch_fill_i32(int *p, int value, int count, hipStream_t s);
+
+// ---- products.hip --------------------------------------------------------------
+// Grouped W{4,8}A{8,4}: bit-exact AVX2 order. bad (may be null): NaN outputs.
+void launch_grouped(const Weight &w, const int8_t *q, const float *sx, int m, float *y,
+                    const int *bad, int variant, hipStream_t s);
+// W4A16: y [m x N] f32 from x f16 [m x K].
+void launch_w4a16(const Weight &w, const half_t *x, int m, float *y, int gemv_variant,
+                  int gemm_variant, hipStream_t s);
+// W4A16 with f16 output and optional fused epilogue (0 none, 1 GELU, 2 +residual f16)
+void launch_w4a16_f16(const Weight &w, const half_t *x, int m, half_t *y, int epilogue,
+                      const half_t *residual, int variant, hipStream_t s);
+// Per-row int8 GEMM: raw int32 or f32 epilogue.
+void launch_i8_gemm(const int8_t *a, const float *sa, int m, const int8_t *b, const float *sb,
+                    int n, int k, void *y, int raw, int variant, hipStream_t s);
+// Fused gate/up W4A8 + SiLU + A8 requantization (grouped_q4_mlp.wgsl).
+void launch_mlp_requant(const Weight &gate, const Weight &up, const int8_t *q, const float *sx,
+                        int m, int8_t *qo, float *so, const int *bad, hipStream_t s);
+
+// ---- epilogue.hip ----------------------------------------------------------------
+void launch_layernorm(const void *x, void *y, int dtype, int rows, int d, const float *w,
+                      const float *b, float eps, hipStream_t s);
+void launch_rmsnorm(const float *x, float *y, int rows, int d, const float *w, float eps,
+                    int zero_centered, hipStream_t s);
+void launch_gelu(void *x, int dtype, size_t n, hipStream_t s);
+void launch_silu_mul(float *g, const float *u, size_t n, hipStream_t s);
+void launch_add(void *x, const void *y, int dtype, size_t n, hipStream_t s);
+void launch_softmax_rows(float *x, int rows, int n, hipStream_t s);
+void launch_mean_rows(const void *x, int dtype, int batch, int rows, int d, float *out,
+                      hipStream_t s);
+void launch_attention(const half_t *qkv, half_t *out, int batch, int seq, int heads, int dh,
+                      float scale, hipStream_t s);
+void launch_fill_normal_f32(float *p, size_t n, uint64_t seed, float stddev, hipStream_t s);
+void launch_fill_f32(float *p, size_t n, float v, hipStream_t s);
+
+// ---- variants (tuner) --------------------------------------------------------------
+struct VariantFamily {
+    const char *family;
+    const char *const *names;
+    int count;
+};
+int variant_count(const char *family);
+const char *variant_name(const char *family, int index);
+int variant_index(const char *family, const char *name);
+
+}  // namespace dz

@@ -1,0 +1,649 @@
+// products.hip -- quantized matrix products on CDNA4 matrix cores.
+//
+//  grouped   : W{4,8}A{8,4}, the reference's numeric mode. One
+//              v_mfma_i32_16x16x64_i8 per 64-run gives the exact int32 group
+//              dot; outputs fold groups in order with
+//              acc = fma(f32(dot), sw*sx, acc), the AVX2 rows<R,Q4> order of
+//              src/models/pplx_flash/int8.rs:524-585, so results are bit-exact.
+//  gemv      : W4A16 for M <= 16 rows, HBM bound. Each lane streams one 128-bit
+//              word of packed codes per 128-k block; codes become exact f16 and
+//              feed v_mfma_f32_16x16x32_f16; per-32-run scales are applied to the
+//              f32 partials. K is split into 8 fixed chunks reduced in order, so
+//              every variant is bitwise equal.
+//  gemm      : W4A16 for large M, MFMA bound. The activation tile is staged in
+//              LDS; each wave dequantizes its weight fragments (code * scale in
+//              f16) straight from HBM and accumulates in f32.
+//  i8_gemm   : per-row int8 (webgpu/int8.rs:147-242): exact int32 dots on
+//              v_mfma_i32_16x16x64_i8, epilogue (f32(dot)*sa)*sw.
+#include <float.h>
+
+#include "kernels.hpp"
+
+namespace dz {
+
+namespace {
+
+__device__ __forceinline__ size_t q4_lane(int t, int kb, int kbs, int q, int j) {
+    return ((((size_t)t * kbs + kb) * 64) + q * 16 + j) * 16;
+}
+
+// ============================================================================
+// grouped W{4,8}A{8,4}
+// ============================================================================
+
+// One wave per 16x16 output tile; a block of 4 waves covers 64 columns.
+template <int BITS>
+__global__ __launch_bounds__(256) void grouped_kernel(const uint8_t *__restrict__ codes,
+                                                      const uint8_t *__restrict__ scales,
+                                                      const int8_t *__restrict__ q,
+                                                      const float *__restrict__ sx, int m, int n,
+                                                      int groups, int kbs, float *__restrict__ y,
+                                                      const int *__restrict__ bad) {
+    const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const int t = blockIdx.x * 4 + wave;
+    const int mt = blockIdx.y;
+    if (t * 16 >= n) return;
+    const int qd = lane / 16, i = lane % 16, j = i;
+    const int arow = mt * 16 + i;
+    const bool arow_ok = arow < m;
+    const bool nan_out = bad != nullptr && *bad != 0;
+    float4_t acc = {0.f, 0.f, 0.f, 0.f};
+    const int4_t zero = {0, 0, 0, 0};
+    const int8_t *qrow = q + (size_t)arow * groups * 64;
+    if (!nan_out) {
+        for (int g = 0; g < groups; g++) {
+            int4_t a = zero, b;
+            float sw;
+            if (BITS == 4) {
+                const int kb = g >> 1, s0 = (g & 1) * 2;
+                uint2_t wds = *(const uint2_t *)(codes + q4_lane(t, kb, kbs, qd, j) + s0 * 4);
+                uint2_t lo = nibbles_to_i8(wds[0]), hi = nibbles_to_i8(wds[1]);
+                b = int4_t{(int)lo[0], (int)lo[1], (int)hi[0], (int)hi[1]};
+                if (arow_ok) {
+                    uint2_t a0 = *(const uint2_t *)(qrow + g * 64 + qd * 8);
+                    uint2_t a1 = *(const uint2_t *)(qrow + g * 64 + 32 + qd * 8);
+                    a = int4_t{(int)a0[0], (int)a0[1], (int)a1[0], (int)a1[1]};
+                }
+                sw = ((const float *)(scales + (((size_t)t * kbs + kb) * 16 + j) * 8))[g & 1];
+            } else {
+                b = *(const int4_t *)(codes + q4_lane(t, g, kbs, qd, j));
+                if (arow_ok) a = *(const int4_t *)(qrow + g * 64 + qd * 16);
+                sw = ((const float *)scales)[((size_t)t * kbs + g) * 16 + j];
+            }
+            int4_t d = mfma_i8(a, b, zero);
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                int r = mt * 16 + qd * 4 + v;
+                float sxv = r < m ? sx[(size_t)r * groups + g] : 0.0f;
+                acc[v] = __builtin_fmaf((float)d[v], __fmul_rn(sw, sxv), acc[v]);
+            }
+        }
+    }
+    const int col = t * 16 + j;
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+        int r = mt * 16 + qd * 4 + v;
+        if (r < m && col < n) y[(size_t)r * n + col] = nan_out ? __builtin_nanf("") : acc[v];
+    }
+}
+
+// Fused gate/up + SiLU + A8 requantization (grouped_q4_mlp.wgsl:78-105): a
+// block is 16 rows x one 64-column block; the four waves hold 16 columns each.
+__global__ __launch_bounds__(256) void mlp_requant_kernel(
+    const uint8_t *__restrict__ gcodes, const uint8_t *__restrict__ gscales,
+    const uint8_t *__restrict__ ucodes, const uint8_t *__restrict__ uscales,
+    const int8_t *__restrict__ q, const float *__restrict__ sx, int m, int n, int groups, int kbs,
+    int8_t *__restrict__ qo, float *__restrict__ so, const int *__restrict__ bad) {
+    __shared__ float rmax[4][16];
+    const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const int t = blockIdx.x * 4 + wave;
+    const int mt = blockIdx.y;
+    const int qd = lane / 16, i = lane % 16, j = i;
+    const int arow = mt * 16 + i;
+    const bool arow_ok = arow < m;
+    const bool nan_out = bad != nullptr && *bad != 0;
+    float4_t ga = {0.f, 0.f, 0.f, 0.f}, ua = {0.f, 0.f, 0.f, 0.f};
+    const int4_t zero = {0, 0, 0, 0};
+    const int8_t *qrow = q + (size_t)arow * groups * 64;
+    for (int g = 0; g < groups; g++) {
+        const int kb = g >> 1, s0 = (g & 1) * 2;
+        int4_t a = zero;
+        if (arow_ok) {
+            uint2_t a0 = *(const uint2_t *)(qrow + g * 64 + qd * 8);
+            uint2_t a1 = *(const uint2_t *)(qrow + g * 64 + 32 + qd * 8);
+            a = int4_t{(int)a0[0], (int)a0[1], (int)a1[0], (int)a1[1]};
+        }
+        uint2_t gw = *(const uint2_t *)(gcodes + q4_lane(t, kb, kbs, qd, j) + s0 * 4);
+        uint2_t uw = *(const uint2_t *)(ucodes + q4_lane(t, kb, kbs, qd, j) + s0 * 4);
+        uint2_t g0 = nibbles_to_i8(gw[0]), g1 = nibbles_to_i8(gw[1]);
+        uint2_t u0 = nibbles_to_i8(uw[0]), u1 = nibbles_to_i8(uw[1]);
+        int4_t gb = {(int)g0[0], (int)g0[1], (int)g1[0], (int)g1[1]};
+        int4_t ub = {(int)u0[0], (int)u0[1], (int)u1[0], (int)u1[1]};
+        int4_t gd = mfma_i8(a, gb, zero);
+        int4_t ud = mfma_i8(a, ub, zero);
+        size_t rec = (((size_t)t * kbs + kb) * 16 + j) * 8;
+        float gs = ((const float *)(gscales + rec))[g & 1];
+        float us = ((const float *)(uscales + rec))[g & 1];
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            int r = mt * 16 + qd * 4 + v;
+            float sxv = r < m ? sx[(size_t)r * groups + g] : 0.0f;
+            ga[v] = __builtin_fmaf((float)gd[v], __fmul_rn(gs, sxv), ga[v]);
+            ua[v] = __builtin_fmaf((float)ud[v], __fmul_rn(us, sxv), ua[v]);
+        }
+    }
+    float4_t val;
+    float local[4];
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+        float gv = ga[v];
+        float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-gv)));
+        val[v] = __fmul_rn(__fmul_rn(gv, sig), ua[v]);
+        local[v] = fabsf(val[v]);
+    }
+    // row maxima over the 16 columns of this wave (lanes with equal qd)
+#pragma unroll
+    for (int v = 0; v < 4; v++)
+        for (int off = 8; off > 0; off >>= 1) local[v] = fmaxf(local[v], __shfl_xor(local[v], off, 16));
+    if (j == 0)
+        for (int v = 0; v < 4; v++) rmax[wave][qd * 4 + v] = local[v];
+    __syncthreads();
+    const int col = t * 16 + j;
+    const int blocks = n / 64;
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+        int rr = qd * 4 + v;
+        int r = mt * 16 + rr;
+        float maximum = fmaxf(fmaxf(rmax[0][rr], rmax[1][rr]), fmaxf(rmax[2][rr], rmax[3][rr]));
+        float scale = fmaxf(__fdiv_rn(maximum, 127.0f), FLT_MIN);
+        float inverse = __frcp_rn(scale);
+        float c = fminf(fmaxf(__builtin_rintf(__fmul_rn(val[v], inverse)), -127.0f), 127.0f);
+        if (r < m) {
+            if (nan_out) {
+                qo[(size_t)r * n + col] = 0;
+                if (wave == 0 && j == 0) so[(size_t)r * blocks + blockIdx.x] = __builtin_nanf("");
+            } else {
+                qo[(size_t)r * n + col] = (int8_t)(int)c;
+                if (wave == 0 && j == 0) so[(size_t)r * blocks + blockIdx.x] = scale;
+            }
+        }
+    }
+}
+
+// ============================================================================
+// W4A16 skinny-M GEMV
+// ============================================================================
+
+constexpr int kChunks = 8;  // fixed K split: reduction order is variant independent
+
+template <int WAVES, int UNROLL, bool G32>
+__global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const uint8_t *__restrict__ codes,
+                                                          const uint8_t *__restrict__ scales,
+                                                          const half_t *__restrict__ x, int m,
+                                                          int k, int n, int kbs,
+                                                          float *__restrict__ y) {
+    constexpr int PER_WAVE = kChunks / WAVES;
+    __shared__ float4_t red[kChunks][64];
+    const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const int t = blockIdx.x, mt = blockIdx.y;
+    const int qd = lane / 16, i = lane % 16, j = i;
+    const int arow = mt * 16 + i;
+    const bool arow_ok = arow < m;
+    const half_t *xrow = x + (size_t)arow * k;
+    const uint8_t *cbase = codes + q4_lane(t, 0, kbs, qd, j);
+    const uint8_t *sbase = scales + ((size_t)t * kbs * 16 + j) * 8;
+    const int per = (kbs + kChunks - 1) / kChunks;
+    const half8_t hz = {};
+    const float4_t fz = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int cc = 0; cc < PER_WAVE; cc++) {
+        const int chunk = wave * PER_WAVE + cc;
+        const int kb0 = chunk * per;
+        const int kb1 = min(kbs, kb0 + per);
+        float4_t acc = fz;
+        for (int kb = kb0; kb < kb1; kb += UNROLL) {
+            uint4_t c[UNROLL];
+            uint2_t sc[UNROLL];
+#pragma unroll
+            for (int u = 0; u < UNROLL; u++) {
+                if (kb + u < kb1) {
+                    c[u] = __builtin_nontemporal_load((const uint4_t *)(cbase + (size_t)(kb + u) * 1024));
+                    sc[u] = *(const uint2_t *)(sbase + (size_t)(kb + u) * 128);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < UNROLL; u++) {
+                if (kb + u < kb1) {
+#pragma unroll
+                    for (int s = 0; s < 4; s++) {
+                        half8_t b = as_half8(nibbles_to_half8(c[u][s]));
+                        const int kk = (kb + u) * 128 + s * 32 + qd * 8;
+                        half8_t a = hz;
+                        if (arow_ok && kk < k) a = *(const half8_t *)(xrow + kk);
+                        float4_t p = mfma_f16(a, b, fz);
+                        float scale;
+                        if (G32)
+                            scale = f16_bits_to_float((sc[u][s >> 1] >> (16 * (s & 1))) & 0xffffu);
+                        else
+                            scale = __builtin_bit_cast(float, sc[u][s >> 1]);
+#pragma unroll
+                        for (int v = 0; v < 4; v++) acc[v] = __builtin_fmaf(p[v], scale, acc[v]);
+                    }
+                }
+            }
+        }
+        red[chunk][lane] = acc;
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    float4_t total = red[0][lane];
+#pragma unroll
+    for (int cidx = 1; cidx < kChunks; cidx++) {
+        float4_t r = red[cidx][lane];
+#pragma unroll
+        for (int v = 0; v < 4; v++) total[v] = __fadd_rn(total[v], r[v]);
+    }
+    const int col = t * 16 + j;
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+        int r = mt * 16 + qd * 4 + v;
+        if (r < m && col < n) y[(size_t)r * n + col] = total[v];
+    }
+}
+
+// ============================================================================
+// W4A16 large-M GEMM
+// ============================================================================
+
+// Block tile BM x BN, waves WM x WN, wave tile (BM/WM) x (BN/WN). One k-step
+// is a 128-k block. The activation tile lives in LDS as BM rows of sixteen
+// 16-byte chunks; chunk c of row r sits at slot c ^ (r & 15) so the 16 rows a
+// ds_read_b128 touches fall in distinct banks.
+// Epilogue: 0 -> f32 out; 1 -> f16 out; 2 -> f16 GELU; 3 -> f16 + residual.
+template <int BM, int BN, int WM, int WN, bool G32, int EPI>
+__global__ __launch_bounds__(WM *WN * 64) void gemm_w4a16_kernel(
+    const uint8_t *__restrict__ codes, const uint8_t *__restrict__ scales,
+    const half_t *__restrict__ x, int m, int k, int n, int kbs, void *__restrict__ out,
+    const half_t *__restrict__ residual) {
+    constexpr int THREADS = WM * WN * 64;
+    constexpr int TM = BM / WM, TN = BN / WN;
+    constexpr int MB = TM / 16, NT = TN / 16;
+    constexpr int CHUNKS = BM * 16;  // 16-byte chunks of the A tile
+    constexpr int PER_THREAD = CHUNKS / THREADS;
+    static_assert(CHUNKS % THREADS == 0, "tile/threads mismatch");
+    extern __shared__ __align__(16) uint8_t lds[];
+
+    const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const int wm = wave / WN, wn = wave % WN;
+    const int qd = lane / 16, i = lane % 16, j = i;
+    const int bn = blockIdx.x, bm = blockIdx.y;
+    const int row0 = bm * BM, col0 = bn * BN;
+    const int tile0 = (col0 + wn * TN) / 16;
+    const int tiles = (n + 15) / 16;
+
+    float4_t acc[MB][NT];
+#pragma unroll
+    for (int a = 0; a < MB; a++)
+#pragma unroll
+        for (int b = 0; b < NT; b++) acc[a][b] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+    uint4_t pa[PER_THREAD];
+    auto load_a = [&](int kb) {
+#pragma unroll
+        for (int p = 0; p < PER_THREAD; p++) {
+            int idx = threadIdx.x + p * THREADS;
+            int r = idx / 16, ch = idx % 16;
+            int gr = row0 + r, gk = kb * 128 + ch * 8;
+            uint4_t v = {0u, 0u, 0u, 0u};
+            if (gr < m && gk < k) v = *(const uint4_t *)(x + (size_t)gr * k + gk);
+            pa[p] = v;
+        }
+    };
+    auto store_a = [&]() {
+#pragma unroll
+        for (int p = 0; p < PER_THREAD; p++) {
+            int idx = threadIdx.x + p * THREADS;
+            int r = idx / 16, ch = idx % 16;
+            *(uint4_t *)(lds + r * 256 + ((ch ^ (r & 15)) * 16)) = pa[p];
+        }
+    };
+    uint4_t pc[NT];
+    uint2_t ps[NT];
+    auto load_b = [&](int kb) {
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            int t = tile0 + nt;
+            if (t < tiles) {
+                pc[nt] = *(const uint4_t *)(codes + q4_lane(t, kb, kbs, qd, j));
+                ps[nt] = *(const uint2_t *)(scales + (((size_t)t * kbs + kb) * 16 + j) * 8);
+            } else {
+                pc[nt] = uint4_t{0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u};
+                ps[nt] = uint2_t{0u, 0u};
+            }
+        }
+    };
+
+    load_a(0);
+    load_b(0);
+    for (int kb = 0; kb < kbs; kb++) {
+        __syncthreads();
+        store_a();
+        // dequantize this k-block's weight fragments: code * scale in f16
+        half8_t bf[NT][4];
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                half_t sh;
+                if (G32)
+                    sh = __builtin_bit_cast(half_t, (unsigned short)((ps[nt][s >> 1] >> (16 * (s & 1))) & 0xffffu));
+                else
+                    sh = (half_t)__builtin_bit_cast(float, ps[nt][s >> 1]);
+                half2_t s2 = {sh, sh};
+                uint4_t cw = nibbles_to_half8(pc[nt][s]);
+#pragma unroll
+                for (int p = 0; p < 4; p++) cw[p] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, cw[p]) * s2);
+                bf[nt][s] = as_half8(cw);
+            }
+        }
+        __syncthreads();
+        if (kb + 1 < kbs) {
+            load_a(kb + 1);
+            load_b(kb + 1);
+        }
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+#pragma unroll
+            for (int mb = 0; mb < MB; mb++) {
+                int r = wm * TM + mb * 16 + i;
+                int ch = s * 4 + qd;
+                half8_t a = *(const half8_t *)(lds + r * 256 + ((ch ^ (r & 15)) * 16));
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++) acc[mb][nt] = mfma_f16(a, bf[nt][s], acc[mb][nt]);
+            }
+        }
+    }
+    // epilogue
+#pragma unroll
+    for (int mb = 0; mb < MB; mb++) {
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            int col = col0 + wn * TN + nt * 16 + j;
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                int r = row0 + wm * TM + mb * 16 + qd * 4 + v;
+                if (r < m && col < n) {
+                    float val = acc[mb][nt][v];
+                    size_t at = (size_t)r * n + col;
+                    if (EPI == 0) {
+                        ((float *)out)[at] = val;
+                    } else if (EPI == 1) {
+                        ((half_t *)out)[at] = (half_t)val;
+                    } else if (EPI == 2) {
+                        float gl = 0.5f * val * (1.0f + erff(val * 0.70710678118654752f));
+                        ((half_t *)out)[at] = (half_t)gl;
+                    } else {
+                        ((half_t *)out)[at] = (half_t)(val + (float)residual[at]);
+                    }
+                }
+            }
+        }
+    }
+}
+
+// ============================================================================
+// per-row int8 GEMM
+// ============================================================================
+
+// K-step 64 bytes; both tiles staged in LDS as rows of four 16-byte chunks,
+// chunk c of row r at slot c ^ ((r >> 2) & 3).
+template <int BM, int BN, int WM, int WN>
+__global__ __launch_bounds__(WM *WN * 64) void i8_gemm_kernel(const int8_t *__restrict__ a,
+                                                              const float *__restrict__ sa, int m,
+                                                              const int8_t *__restrict__ b,
+                                                              const float *__restrict__ sb, int n,
+                                                              int k, void *__restrict__ y,
+                                                              int raw) {
+    constexpr int THREADS = WM * WN * 64;
+    constexpr int TM = BM / WM, TN = BN / WN;
+    constexpr int MB = TM / 16, NB = TN / 16;
+    constexpr int ACH = BM * 4, BCH = BN * 4;
+    constexpr int PA = (ACH + THREADS - 1) / THREADS, PB = (BCH + THREADS - 1) / THREADS;
+    __shared__ __align__(16) uint8_t la[2][BM * 64];
+    __shared__ __align__(16) uint8_t lb[2][BN * 64];
+
+    const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const int wm = wave / WN, wn = wave % WN;
+    const int qd = lane / 16, i = lane % 16;
+    const int row0 = blockIdx.y * BM, col0 = blockIdx.x * BN;
+    const int steps = (k + 63) / 64;
+
+    int4_t acc[MB][NB];
+#pragma unroll
+    for (int x = 0; x < MB; x++)
+#pragma unroll
+        for (int z = 0; z < NB; z++) acc[x][z] = int4_t{0, 0, 0, 0};
+
+    uint4_t ra[PA], rb[PB];
+    auto load_chunk = [&](const int8_t *src, int rows, int r, int kk) -> uint4_t {
+        uint4_t v = {0u, 0u, 0u, 0u};
+        if (r < rows) {
+            const int8_t *p = src + (size_t)r * k + kk;
+            if (kk + 16 <= k) {
+                v = *(const uint4_t *)p;
+            } else if (kk < k) {
+                uint8_t tmp[16] = {};
+                for (int e = 0; e < 16 && kk + e < k; e++) tmp[e] = (uint8_t)p[e];
+                v = *(uint4_t *)tmp;
+            }
+        }
+        return v;
+    };
+    auto load = [&](int step) {
+#pragma unroll
+        for (int p = 0; p < PA; p++) {
+            int idx = threadIdx.x + p * THREADS;
+            if (idx < ACH) ra[p] = load_chunk(a, m, row0 + idx / 4, step * 64 + (idx % 4) * 16);
+        }
+#pragma unroll
+        for (int p = 0; p < PB; p++) {
+            int idx = threadIdx.x + p * THREADS;
+            if (idx < BCH) rb[p] = load_chunk(b, n, col0 + idx / 4, step * 64 + (idx % 4) * 16);
+        }
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int p = 0; p < PA; p++) {
+            int idx = threadIdx.x + p * THREADS;
+            if (idx < ACH) {
+                int r = idx / 4, c = idx % 4;
+                *(uint4_t *)(la[buf] + r * 64 + ((c ^ ((r >> 2) & 3)) * 16)) = ra[p];
+            }
+        }
+#pragma unroll
+        for (int p = 0; p < PB; p++) {
+            int idx = threadIdx.x + p * THREADS;
+            if (idx < BCH) {
+                int r = idx / 4, c = idx % 4;
+                *(uint4_t *)(lb[buf] + r * 64 + ((c ^ ((r >> 2) & 3)) * 16)) = rb[p];
+            }
+        }
+    };
+
+    load(0);
+    store(0);
+    __syncthreads();
+    for (int st = 0; st < steps; st++) {
+        const int buf = st & 1;
+        if (st + 1 < steps) load(st + 1);
+        int4_t bfrag[NB];
+#pragma unroll
+        for (int z = 0; z < NB; z++) {
+            int r = wn * TN + z * 16 + i;
+            bfrag[z] = *(const int4_t *)(lb[buf] + r * 64 + ((qd ^ ((r >> 2) & 3)) * 16));
+        }
+#pragma unroll
+        for (int x = 0; x < MB; x++) {
+            int r = wm * TM + x * 16 + i;
+            int4_t af = *(const int4_t *)(la[buf] + r * 64 + ((qd ^ ((r >> 2) & 3)) * 16));
+#pragma unroll
+            for (int z = 0; z < NB; z++) acc[x][z] = mfma_i8(af, bfrag[z], acc[x][z]);
+        }
+        if (st + 1 < steps) store(buf ^ 1);
+        __syncthreads();
+    }
+#pragma unroll
+    for (int x = 0; x < MB; x++) {
+#pragma unroll
+        for (int z = 0; z < NB; z++) {
+            int col = col0 + wn * TN + z * 16 + i;
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                int r = row0 + wm * TM + x * 16 + qd * 4 + v;
+                if (r < m && col < n) {
+                    size_t at = (size_t)r * n + col;
+                    if (raw)
+                        ((int32_t *)y)[at] = acc[x][z][v];
+                    else
+                        ((float *)y)[at] = __fmul_rn(__fmul_rn((float)acc[x][z][v], sa[r]), sb[col]);
+                }
+            }
+        }
+    }
+}
+
+inline unsigned cdiv(size_t a, size_t b) { return (unsigned)((a + b - 1) / b); }
+
+// ---- variant tables -------------------------------------------------------------
+
+const char *const kGemvNames[] = {"w8u4", "w4u4", "w4u8", "w2u8"};
+const char *const kGemmNames[] = {"256x128w2x2", "128x128w2x2", "128x64w2x2"};
+const char *const kI8Names[] = {"128x128w2x2", "256x128w2x2", "64x64w2x2"};
+const char *const kGroupedNames[] = {"wave16x16"};
+
+template <int W, int U>
+void gemv_launch(const Weight &w, const half_t *x, int m, float *y, hipStream_t s) {
+    dim3 grid(w.tiles(), cdiv(m, 16));
+    if (w.kind == WeightKind::Q4G32)
+        hipLaunchKernelGGL((gemv_kernel<W, U, true>), grid, dim3(W * 64), 0, s, w.codes, w.scales, x, m,
+                           w.cols, w.rows, w.kblocks(), y);
+    else
+        hipLaunchKernelGGL((gemv_kernel<W, U, false>), grid, dim3(W * 64), 0, s, w.codes, w.scales, x, m,
+                           w.cols, w.rows, w.kblocks(), y);
+}
+
+template <int BM, int BN, int WM, int WN, int EPI>
+void gemm_launch(const Weight &w, const half_t *x, int m, void *y, const half_t *res, hipStream_t s) {
+    dim3 grid(cdiv(w.rows, BN), cdiv(m, BM));
+    size_t lds = BM * 256;
+    if (w.kind == WeightKind::Q4G32)
+        hipLaunchKernelGGL((gemm_w4a16_kernel<BM, BN, WM, WN, true, EPI>), grid, dim3(WM * WN * 64), lds, s,
+                           w.codes, w.scales, x, m, w.cols, w.rows, w.kblocks(), y, res);
+    else
+        hipLaunchKernelGGL((gemm_w4a16_kernel<BM, BN, WM, WN, false, EPI>), grid, dim3(WM * WN * 64), lds, s,
+                           w.codes, w.scales, x, m, w.cols, w.rows, w.kblocks(), y, res);
+}
+
+template <int EPI>
+void gemm_dispatch(const Weight &w, const half_t *x, int m, void *y, const half_t *res, int variant,
+                   hipStream_t s) {
+    switch (variant) {
+        case 1: gemm_launch<128, 128, 2, 2, EPI>(w, x, m, y, res, s); break;
+        case 2: gemm_launch<128, 64, 2, 2, EPI>(w, x, m, y, res, s); break;
+        default: gemm_launch<256, 128, 2, 2, EPI>(w, x, m, y, res, s); break;
+    }
+}
+
+}  // namespace
+
+int variant_count(const char *family) {
+    std::string f(family);
+    if (f == "gemv") return 4;
+    if (f == "gemm_w4a16") return 3;
+    if (f == "i8_gemm") return 3;
+    if (f == "grouped") return 1;
+    return 0;
+}
+
+const char *variant_name(const char *family, int index) {
+    std::string f(family);
+    if (index < 0 || index >= variant_count(family)) return nullptr;
+    if (f == "gemv") return kGemvNames[index];
+    if (f == "gemm_w4a16") return kGemmNames[index];
+    if (f == "i8_gemm") return kI8Names[index];
+    if (f == "grouped") return kGroupedNames[index];
+    return nullptr;
+}
+
+int variant_index(const char *family, const char *name) {
+    for (int i = 0; i < variant_count(family); i++)
+        if (std::string(variant_name(family, i)) == name) return i;
+    return -1;
+}
+
+void launch_grouped(const Weight &w, const int8_t *q, const float *sx, int m, float *y,
+                    const int *bad, int variant, hipStream_t s) {
+    (void)variant;
+    if (m == 0) return;
+    dim3 grid(cdiv(w.tiles(), 4), cdiv(m, 16));
+    if (w.bits == 4)
+        hipLaunchKernelGGL(grouped_kernel<4>, grid, dim3(256), 0, s, w.codes, w.scales, q, sx, m, w.rows,
+                           w.groups, w.kblocks(), y, bad);
+    else
+        hipLaunchKernelGGL(grouped_kernel<8>, grid, dim3(256), 0, s, w.codes, w.scales, q, sx, m, w.rows,
+                           w.groups, w.kblocks(), y, bad);
+}
+
+void launch_mlp_requant(const Weight &gate, const Weight &up, const int8_t *q, const float *sx,
+                        int m, int8_t *qo, float *so, const int *bad, hipStream_t s) {
+    if (m == 0) return;
+    dim3 grid(gate.rows / 64, cdiv(m, 16));
+    hipLaunchKernelGGL(mlp_requant_kernel, grid, dim3(256), 0, s, gate.codes, gate.scales, up.codes,
+                       up.scales, q, sx, m, gate.rows, gate.groups, gate.kblocks(), qo, so, bad);
+}
+
+void launch_w4a16(const Weight &w, const half_t *x, int m, float *y, int gemv_variant,
+                  int gemm_variant, hipStream_t s) {
+    if (m == 0) return;
+    if (m <= 16) {
+        switch (gemv_variant) {
+            case 1: gemv_launch<4, 4>(w, x, m, y, s); break;
+            case 2: gemv_launch<4, 8>(w, x, m, y, s); break;
+            case 3: gemv_launch<2, 8>(w, x, m, y, s); break;
+            default: gemv_launch<8, 4>(w, x, m, y, s); break;
+        }
+    } else {
+        gemm_dispatch<0>(w, x, m, y, nullptr, gemm_variant, s);
+    }
+}
+
+void launch_w4a16_f16(const Weight &w, const half_t *x, int m, half_t *y, int epilogue,
+                      const half_t *residual, int variant, hipStream_t s) {
+    if (m == 0) return;
+    switch (epilogue) {
+        case 1: gemm_dispatch<2>(w, x, m, y, residual, variant, s); break;
+        case 2: gemm_dispatch<3>(w, x, m, y, residual, variant, s); break;
+        default: gemm_dispatch<1>(w, x, m, y, residual, variant, s); break;
+    }
+}
+
+void launch_i8_gemm(const int8_t *a, const float *sa, int m, const int8_t *b, const float *sb,
+                    int n, int k, void *y, int raw, int variant, hipStream_t s) {
+    if (m == 0 || n == 0) return;
+    switch (variant) {
+        case 1:
+            hipLaunchKernelGGL((i8_gemm_kernel<256, 128, 2, 2>), dim3(cdiv(n, 128), cdiv(m, 256)), dim3(256), 0, s,
+                               a, sa, m, b, sb, n, k, y, raw);
+            break;
+        case 2:
+            hipLaunchKernelGGL((i8_gemm_kernel<64, 64, 2, 2>), dim3(cdiv(n, 64), cdiv(m, 64)), dim3(256), 0, s,
+                               a, sa, m, b, sb, n, k, y, raw);
+            break;
+        default:
+            hipLaunchKernelGGL((i8_gemm_kernel<128, 128, 2, 2>), dim3(cdiv(n, 128), cdiv(m, 128)), dim3(256), 0, s,
+                               a, sa, m, b, sb, n, k, y, raw);
+            break;
+    }
+}
+
+}  // namespace dz

@@ -1,0 +1,652 @@
+// runtime.hip -- the extern "C" boundary of libdecisive_rocm.so.
+//
+// Every entry point validates its arguments on the host, records a message in
+// the context on failure and returns a dz_status whose names follow the
+// reference's error codes (src/inference/mod.rs:44-85). Kernels run on the
+// context stream; device-side validation (scales, non-finite inputs, token
+// ids) reports through a device flag that the synchronous entry points read.
+#include <float.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <map>
+#include <string>
+
+#include "../../include/decisive_rocm.h"
+#include "kernels.hpp"
+
+struct dz_weight {
+    dz::Weight w;
+    int device = 0;
+};
+
+struct dz_ctx {
+    int device = 0;
+    hipStream_t own = nullptr;
+    hipStream_t stream = nullptr;
+    std::string error;
+    std::string arch;
+    int cus = 0;
+    int clock_khz = 0;
+    int *flag = nullptr;  // device int: validation / non-finite flag
+    void *work = nullptr; // activation quantization workspace
+    size_t work_bytes = 0;
+    std::map<std::string, int> variants;
+    std::string tuning;   // JSON of the last selection
+};
+
+namespace dz {
+int32_t encoder_create_random(dz_ctx *ctx, const dz_encoder_config *cfg, uint64_t seed,
+                              dz_encoder **out);
+void encoder_destroy(dz_ctx *ctx, dz_encoder *enc);
+int32_t encoder_row_bytes(const dz_encoder *enc, size_t *row_bytes);
+const dz_weight *encoder_weight(const dz_encoder *enc, int layer, int which);
+int32_t encoder_read_rows(dz_ctx *ctx, const dz_encoder *enc, const int32_t *ids, size_t count,
+                          void *out);
+int32_t encoder_forward(dz_ctx *ctx, dz_encoder *enc, const int32_t *ids_dev, const void *rows_host,
+                        size_t batch, size_t seq, float *out);
+int32_t tune(dz_ctx *ctx, uint32_t budget_ms, const char *cache_in, char *cache_out, size_t cap);
+}  // namespace dz
+
+namespace {
+
+int32_t fail(dz_ctx *ctx, int32_t code, const std::string &msg) {
+    if (ctx) ctx->error = msg;
+    return code;
+}
+
+int32_t hip_fail(dz_ctx *ctx, hipError_t e, const char *what) {
+    std::string msg = std::string(what) + ": " + hipGetErrorString(e);
+    int32_t code = (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) ? DZ_RESOURCE_LIMIT
+                                                                               : DZ_INFERENCE_FAILED;
+    if (code == DZ_RESOURCE_LIMIT) msg += " (exceeds device limits)";
+    return fail(ctx, code, msg);
+}
+
+#define DZ_HIP(ctx, expr, what)                  \
+    do {                                         \
+        hipError_t e_ = (expr);                  \
+        if (e_ != hipSuccess) return hip_fail(ctx, e_, what); \
+    } while (0)
+
+#define DZ_BEGIN(ctx)                                                              \
+    do {                                                                           \
+        if (!(ctx)) return DZ_INVALID_REQUEST;                                      \
+        (ctx)->error.clear();                                                       \
+        hipError_t e_ = hipSetDevice((ctx)->device);                                \
+        if (e_ != hipSuccess) return hip_fail(ctx, e_, "hipSetDevice");             \
+    } while (0)
+
+// Launch status of the kernels just enqueued.
+int32_t launched(dz_ctx *ctx, const char *what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(ctx, e, what);
+    return DZ_OK;
+}
+
+int variant(dz_ctx *ctx, const char *family) {
+    auto it = ctx->variants.find(family);
+    return it == ctx->variants.end() ? 0 : it->second;
+}
+
+// Resets the flag, then returns its value after running `enqueue` and syncing.
+template <class F>
+int32_t flagged_sync(dz_ctx *ctx, F enqueue, int *value) {
+    dz::launch_fill_i32(ctx->flag, 0, 1, ctx->stream);
+    enqueue();
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(ctx, e, "kernel launch");
+    DZ_HIP(ctx, hipMemcpyAsync(value, ctx->flag, sizeof(int), hipMemcpyDeviceToHost, ctx->stream),
+           "flag readback");
+    DZ_HIP(ctx, hipStreamSynchronize(ctx->stream), "stream synchronize");
+    return DZ_OK;
+}
+
+int32_t ensure_work(dz_ctx *ctx, size_t bytes) {
+    if (ctx->work_bytes >= bytes) return DZ_OK;
+    if (ctx->work) {
+        DZ_HIP(ctx, hipStreamSynchronize(ctx->stream), "stream synchronize");
+        hipFree(ctx->work);
+        ctx->work = nullptr;
+        ctx->work_bytes = 0;
+    }
+    size_t want = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
+    DZ_HIP(ctx, hipMalloc(&ctx->work, want), "workspace allocation");
+    ctx->work_bytes = want;
+    return DZ_OK;
+}
+
+bool valid_dtype(int32_t d) { return d == DZ_F32 || d == DZ_F16 || d == DZ_BF16; }
+
+int32_t alloc_weight(dz_ctx *ctx, dz::WeightKind kind, size_t rows, size_t cols, dz_weight **out) {
+    if (rows == 0 || cols == 0 || rows > (1u << 28) || cols > (1u << 28))
+        return fail(ctx, DZ_INVALID_PARAMETERS, "invalid weight shape");
+    dz_weight *h = new dz_weight();
+    dz::Weight &w = h->w;
+    w.kind = kind;
+    w.rows = (int)rows;
+    w.cols = (int)cols;
+    w.bits = kind == dz::WeightKind::Q8G64 ? 8 : 4;
+    w.group = kind == dz::WeightKind::Q4G32 ? 32 : 64;
+    w.groups = (int)((cols + 63) / 64);
+    w.np = (int)((rows + 15) / 16 * 16);
+    w.kp = w.bits == 4 ? (int)((cols + 127) / 128 * 128) : (int)((cols + 63) / 64 * 64);
+    w.code_bytes = (size_t)w.np * w.kp / (w.bits == 4 ? 2 : 1);
+    w.scale_bytes = w.bits == 4 ? (size_t)w.np * (w.kp / 128) * 8 : (size_t)w.np * (w.kp / 64) * 4;
+    h->device = ctx->device;
+    hipError_t e = hipMalloc(&w.codes, w.code_bytes);
+    if (e == hipSuccess) e = hipMalloc(&w.scales, w.scale_bytes);
+    if (e == hipSuccess) e = hipMemsetAsync(w.codes, w.bits == 4 ? 0x88 : 0, w.code_bytes, ctx->stream);
+    if (e == hipSuccess) e = hipMemsetAsync(w.scales, 0, w.scale_bytes, ctx->stream);
+    if (e != hipSuccess) {
+        if (w.codes) hipFree(w.codes);
+        if (w.scales) hipFree(w.scales);
+        delete h;
+        return hip_fail(ctx, e, "weight allocation");
+    }
+    *out = h;
+    return DZ_OK;
+}
+
+void free_weight(dz_weight *h) {
+    if (!h) return;
+    if (h->w.codes) hipFree(h->w.codes);
+    if (h->w.scales) hipFree(h->w.scales);
+    delete h;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *dz_status_name(int32_t status) {
+    switch (status) {
+        case DZ_OK: return "OK";
+        case DZ_INVALID_REQUEST: return "INVALID_REQUEST";
+        case DZ_INVALID_PARAMETERS: return "INVALID_PARAMETERS";
+        case DZ_CANCELLED: return "CANCELLED";
+        case DZ_CACHE_OWNER: return "CACHE_OWNER";
+        case DZ_INPUT_TOO_LONG: return "INPUT_TOO_LONG";
+        case DZ_GPU_UNAVAILABLE: return "GPU_UNAVAILABLE";
+        case DZ_RESOURCE_LIMIT: return "RESOURCE_LIMIT";
+        case DZ_MISSING_GPU_FEATURE: return "MISSING_GPU_FEATURE";
+        case DZ_INFERENCE_FAILED: return "INFERENCE_FAILED";
+        case DZ_INVALID_CHECKPOINT: return "INVALID_CHECKPOINT";
+        case DZ_UNSUPPORTED_CACHE: return "UNSUPPORTED_CACHE";
+        default: return "UNKNOWN";
+    }
+}
+
+int32_t dz_init(int32_t device, dz_ctx **out) {
+    if (!out) return DZ_INVALID_REQUEST;
+    *out = nullptr;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count == 0) return DZ_GPU_UNAVAILABLE;
+    if (device < 0 || device >= count) return DZ_GPU_UNAVAILABLE;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess) return DZ_GPU_UNAVAILABLE;
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) return DZ_MISSING_GPU_FEATURE;
+    dz_ctx *ctx = new dz_ctx();
+    ctx->device = device;
+    ctx->arch = prop.gcnArchName;
+    ctx->cus = prop.multiProcessorCount;
+    ctx->clock_khz = prop.clockRate;
+    if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&ctx->own, hipStreamNonBlocking) != hipSuccess ||
+        hipMalloc(&ctx->flag, 256) != hipSuccess) {
+        delete ctx;
+        return DZ_GPU_UNAVAILABLE;
+    }
+    ctx->stream = ctx->own;
+    *out = ctx;
+    return DZ_OK;
+}
+
+void dz_destroy(dz_ctx *ctx) {
+    if (!ctx) return;
+    hipSetDevice(ctx->device);
+    hipStreamSynchronize(ctx->stream);
+    if (ctx->work) hipFree(ctx->work);
+    if (ctx->flag) hipFree(ctx->flag);
+    if (ctx->own) hipStreamDestroy(ctx->own);
+    delete ctx;
+}
+
+const char *dz_last_error(const dz_ctx *ctx) { return ctx ? ctx->error.c_str() : "no context"; }
+
+int32_t dz_set_stream(dz_ctx *ctx, void *hip_stream) {
+    DZ_BEGIN(ctx);
+    ctx->stream = hip_stream ? (hipStream_t)hip_stream : ctx->own;
+    return DZ_OK;
+}
+
+int32_t dz_sync(dz_ctx *ctx) {
+    DZ_BEGIN(ctx);
+    DZ_HIP(ctx, hipStreamSynchronize(ctx->stream), "stream synchronize");
+    return DZ_OK;
+}
+
+int32_t dz_info(dz_ctx *ctx, char *buf, size_t cap) {
+    DZ_BEGIN(ctx);
+    std::string s = "{\"arch\":\"" + ctx->arch + "\",\"compute_units\":" + std::to_string(ctx->cus) +
+                    ",\"clock_khz\":" + std::to_string(ctx->clock_khz) + ",\"variants\":{";
+    bool first = true;
+    for (const char *f : {"gemv", "gemm_w4a16", "i8_gemm", "grouped"}) {
+        if (!first) s += ",";
+        first = false;
+        s += std::string("\"") + f + "\":\"" + dz::variant_name(f, variant(ctx, f)) + "\"";
+    }
+    s += "},\"tuning\":" + (ctx->tuning.empty() ? std::string("null") : ctx->tuning) + "}";
+    if (!buf || cap < s.size() + 1) return fail(ctx, DZ_RESOURCE_LIMIT, "info buffer too small");
+    memcpy(buf, s.c_str(), s.size() + 1);
+    return DZ_OK;
+}
+
+int32_t dz_alloc(dz_ctx *ctx, size_t bytes, void **dev) {
+    DZ_BEGIN(ctx);
+    if (!dev) return fail(ctx, DZ_INVALID_REQUEST, "null output");
+    DZ_HIP(ctx, hipMalloc(dev, bytes ? bytes : 1), "hipMalloc");
+    return DZ_OK;
+}
+
+int32_t dz_free(dz_ctx *ctx, void *dev) {
+    DZ_BEGIN(ctx);
+    DZ_HIP(ctx, hipStreamSynchronize(ctx->stream), "stream synchronize");
+    if (dev) DZ_HIP(ctx, hipFree(dev), "hipFree");
+    return DZ_OK;
+}
+
+int32_t dz_copy_h2d(dz_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    DZ_BEGIN(ctx);
+    if (bytes && (!dst || !src)) return fail(ctx, DZ_INVALID_REQUEST, "null pointer");
+    DZ_HIP(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream), "copy to device");
+    DZ_HIP(ctx, hipStreamSynchronize(ctx->stream), "stream synchronize");
+    return DZ_OK;
+}
+
+int32_t dz_copy_d2h(dz_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    DZ_BEGIN(ctx);
+    if (bytes && (!dst || !src)) return fail(ctx, DZ_INVALID_REQUEST, "null pointer");
+    DZ_HIP(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream), "copy to host");
+    DZ_HIP(ctx, hipStreamSynchronize(ctx->stream), "stream synchronize");
+    return DZ_OK;
+}
+
+// ---- weights ------------------------------------------------------------------------
+
+int32_t dz_weight_upload(dz_ctx *ctx, const void *packed, size_t bytes, int32_t layout,
+                         size_t rows, size_t cols, dz_weight **out) {
+    DZ_BEGIN(ctx);
+    if (!out || (!packed && bytes)) return fail(ctx, DZ_INVALID_REQUEST, "null pointer");
+    *out = nullptr;
+    dz::WeightKind kind;
+    size_t run, gbytes;
+    switch (layout) {
+        case DZ_Q4_G64_F32: kind = dz::WeightKind::Q4G64; run = 64; gbytes = 36; break;
+        case DZ_Q8_G64_F32: kind = dz::WeightKind::Q8G64; run = 64; gbytes = 68; break;
+        case DZ_Q4_G32_F16: kind = dz::WeightKind::Q4G32; run = 32; gbytes = 18; break;
+        default: return fail(ctx, DZ_INVALID_PARAMETERS, "unknown packed layout");
+    }
+    if (rows == 0 || cols == 0 || cols % run != 0)
+        return fail(ctx, DZ_INVALID_CHECKPOINT, "invalid packed matrix shape");
+    if (bytes != rows * (cols / run) * gbytes)
+        return fail(ctx, DZ_INVALID_CHECKPOINT, "packed byte count does not match the shape");
+    dz_weight *h = nullptr;
+    int32_t rc = alloc_weight(ctx, kind, rows, cols, &h);
+    if (rc) return rc;
+    uint8_t *staging = nullptr;
+    hipError_t e = hipMalloc(&staging, bytes);
+    if (e != hipSuccess) {
+        free_weight(h);
+        return hip_fail(ctx, e, "staging allocation");
+    }
+    e = hipMemcpyAsync(staging, packed, bytes, hipMemcpyHostToDevice, ctx->stream);
+    int bad = 0;
+    if (e == hipSuccess) {
+        rc = flagged_sync(ctx, [&] { dz::launch_upload(h->w, staging, ctx->flag, ctx->stream); }, &bad);
+    } else {
+        rc = hip_fail(ctx, e, "copy to device");
+    }
+    hipFree(staging);
+    if (rc) {
+        free_weight(h);
+        return rc;
+    }
+    if (bad) {
+        free_weight(h);
+        return fail(ctx, DZ_INVALID_CHECKPOINT, "invalid packed scale");
+    }
+    *out = h;
+    return DZ_OK;
+}
+
+int32_t dz_weight_quantize(dz_ctx *ctx, const void *values, int32_t dtype, size_t rows,
+                           size_t cols, int32_t bits, int32_t group, dz_weight **out) {
+    DZ_BEGIN(ctx);
+    if (!out || !values) return fail(ctx, DZ_INVALID_REQUEST, "null pointer");
+    *out = nullptr;
+    if (!valid_dtype(dtype)) return fail(ctx, DZ_INVALID_PARAMETERS, "unknown dtype");
+    dz::WeightKind kind;
+    if (bits == 4 && group == 64)
+        kind = dz::WeightKind::Q4G64;
+    else if (bits == 8 && group == 64)
+        kind = dz::WeightKind::Q8G64;
+    else if (bits == 4 && group == 32)
+        kind = dz::WeightKind::Q4G32;
+    else
+        return fail(ctx, DZ_INVALID_PARAMETERS, "unsupported quantization bits");
+    dz_weight *h = nullptr;
+    int32_t rc = alloc_weight(ctx, kind, rows, cols, &h);
+    if (rc) return rc;
+    int bad = 0;
+    rc = flagged_sync(ctx, [&] { dz::launch_quantize_weight(h->w, values, dtype, ctx->flag, ctx->stream); }, &bad);
+    if (rc || bad) {
+        free_weight(h);
+        return rc ? rc : fail(ctx, DZ_INVALID_CHECKPOINT, "non-finite INT8 weight");
+    }
+    *out = h;
+    return DZ_OK;
+}
+
+int32_t dz_weight_free(dz_ctx *ctx, dz_weight *w) {
+    DZ_BEGIN(ctx);
+    DZ_HIP(ctx, hipStreamSynchronize(ctx->stream), "stream synchronize");
+    free_weight(w);
+    return DZ_OK;
+}
+
+int32_t dz_weight_info(const dz_weight *h, size_t *rows, size_t *cols, int32_t *bits,
+                       int32_t *group, size_t *device_bytes) {
+    if (!h) return DZ_INVALID_REQUEST;
+    if (rows) *rows = (size_t)h->w.rows;
+    if (cols) *cols = (size_t)h->w.cols;
+    if (bits) *bits = h->w.bits;
+    if (group) *group = h->w.group;
+    if (device_bytes) *device_bytes = h->w.code_bytes + h->w.scale_bytes;
+    return DZ_OK;
+}
+
+int32_t dz_dequant(dz_ctx *ctx, const dz_weight *w, float *y) {
+    DZ_BEGIN(ctx);
+    if (!w || !y) return fail(ctx, DZ_INVALID_REQUEST, "null pointer");
+    dz::launch_dequant(w->w, nullptr, w->w.rows, y, 0, ctx->stream);
+    return launched(ctx, "dequant");
+}
+
+int32_t dz_dequant_rows(dz_ctx *ctx, const dz_weight *w, const int32_t *ids, size_t count, void *y,
+                        int32_t dtype) {
+    DZ_BEGIN(ctx);
+    if (!w || (count && (!ids || !y))) return fail(ctx, DZ_INVALID_REQUEST, "null pointer");
+    if (dtype != DZ_F32 && dtype != DZ_F16) return fail(ctx, DZ_INVALID_PARAMETERS, "dtype must be f32 or f16");
+    int bad = 0;
+    int32_t rc = flagged_sync(ctx, [&] {
+        dz::launch_dequant_checked(w->w, ids, (int)count, y, dtype == DZ_F16 ? 1 : 0, ctx->flag, ctx->stream);
+    }, &bad);
+    if (rc) return rc;
+    if (bad) return fail(ctx, DZ_INVALID_REQUEST, "token ID out of range");
+    return DZ_OK;
+}
+
+// ---- quantized products ------------------------------------------------------------
+
+int32_t dz_act_quantize(dz_ctx *ctx, const float *x, size_t m, size_t k, int32_t bits, int8_t *q,
+                        float *s) {
+    DZ_BEGIN(ctx);
+    if (bits != 4 && bits != 8) return fail(ctx, DZ_INVALID_PARAMETERS, "unsupported quantization bits");
+    if (k == 0) return fail(ctx, DZ_INVALID_PARAMETERS, "invalid activation shape");
+    if (m && (!x || !q || !s)) return fail(ctx, DZ_INVALID_REQUEST, "null pointer");
+    dz::launch_act_quantize(x, (int)m, (int)k, bits, q, s, nullptr, ctx->stream);
+    return launched(ctx, "act_quantize");
+}
+
+namespace {
+
+int32_t grouped_linear(dz_ctx *ctx, const dz_weight *a, const dz_weight *b, const float *x,
+                       size_t m, float *ya, float *yb, int32_t mode) {
+    const dz::Weight &w = a->w;
+    if (w.kind == dz::WeightKind::Q4G32)
+        return fail(ctx, DZ_INVALID_PARAMETERS, "grouped int8 mode needs a group-64 weight");
+    if (b && (b->w.cols != w.cols || b->w.kind == dz::WeightKind::Q4G32))
+        return fail(ctx, DZ_INVALID_PARAMETERS, "paired weights must share the input width");
+    if (m == 0) return DZ_OK;
+    size_t qbytes = m * (size_t)w.groups * 64, sbytes = m * (size_t)w.groups * sizeof(float);
+    int32_t rc = ensure_work(ctx, qbytes + sbytes + 256);
+    if (rc) return rc;
+    int8_t *q = (int8_t *)ctx->work;
+    float *s = (float *)((uint8_t *)ctx->work + (qbytes + 255) / 256 * 256);
+    dz::launch_fill_i32(ctx->flag, 0, 1, ctx->stream);
+    dz::launch_act_quantize(x, (int)m, w.cols, mode == DZ_W4A4 ? 4 : 8, q, s, ctx->flag, ctx->stream);
+    dz::launch_grouped(w, q, s, (int)m, ya, ctx->flag, variant(ctx, "grouped"), ctx->stream);
+    if (b) dz::launch_grouped(b->w, q, s, (int)m, yb, ctx->flag, variant(ctx, "grouped"), ctx->stream);
+    return launched(ctx, "grouped linear");
+}
+
+}  // namespace
+
+int32_t dz_linear(dz_ctx *ctx, const dz_weight *w, const void *x, int32_t x_dtype, size_t m,
+                  float *y, int32_t mode) {
+    DZ_BEGIN(ctx);
+    if (!w || (m && (!x || !y))) return fail(ctx, DZ_INVALID_REQUEST, "null pointer");
+    if (m > (1u << 24)) return fail(ctx, DZ_INPUT_TOO_LONG, "input budget exceeded");
+    if (mode == DZ_W4A8 || mode == DZ_W4A4) {
+        if (x_dtype != DZ_F32) return fail(ctx, DZ_INVALID_PARAMETERS, "grouped int8 mode takes f32 activations");
+        if (mode == DZ_W4A4 && w->w.bits != 4) return fail(ctx, DZ_INVALID_PARAMETERS, "W4A4 needs a Q4 weight");
+        return grouped_linear(ctx, w, nullptr, (const float *)x, m, y, nullptr, mode);
+    }
+    if (mode == DZ_W4A16) {
+        if (x_dtype != DZ_F16) return fail(ctx, DZ_INVALID_PARAMETERS, "W4A16 takes f16 activations");
+        if (w->w.bits != 4) return fail(ctx, DZ_INVALID_PARAMETERS, "W4A16 needs a Q4 weight");
+        if (w->w.cols % 8 != 0) return fail(ctx, DZ_INVALID_PARAMETERS, "W4A16 needs cols % 8 == 0");
+        if (m == 0) return DZ_OK;
+        dz::launch_w4a16(w->w, (const dz::half_t *)x, (int)m, y, variant(ctx, "gemv"),
+                         variant(ctx, "gemm_w4a16"), ctx->stream);
+        return launched(ctx, "w4a16 linear");
+    }
+    return fail(ctx, DZ_INVALID_PARAMETERS, "unknown mode");
+}
+
+int32_t dz_linear_pair(dz_ctx *ctx, const dz_weight *a, const dz_weight *b, const float *x, size_t m,
+                       float *ya, float *yb, int32_t mode) {
+    DZ_BEGIN(ctx);
+    if (!a || !b || (m && (!x || !ya || !yb))) return fail(ctx, DZ_INVALID_REQUEST, "null pointer");
+    if (mode != DZ_W4A8 && mode != DZ_W4A4) return fail(ctx, DZ_INVALID_PARAMETERS, "pair takes a grouped int8 mode");
+    return grouped_linear(ctx, a, b, x, m, ya, yb, mode);
+}
+
+int32_t dz_mlp_requant(dz_ctx *ctx, const dz_weight *gate, const dz_weight *up, const float *x,
+                       size_t m, int8_t *qo, float *so) {
+    DZ_BEGIN(ctx);
+    if (!gate || !up || (m && (!x || !qo || !so))) return fail(ctx, DZ_INVALID_REQUEST, "null pointer");
+    const dz::Weight &g = gate->w, &u = up->w;
+    if (g.kind != dz::WeightKind::Q4G64 || u.kind != dz::WeightKind::Q4G64)
+        return fail(ctx, DZ_INVALID_PARAMETERS, "fused MLP needs Q4 group-64 weights");
+    if (g.rows != u.rows || g.cols != u.cols || g.rows % 64 != 0)
+        return fail(ctx, DZ_INVALID_PARAMETERS, "fused MLP shapes must match with rows % 64 == 0");
+    if (m == 0) return DZ_OK;
+    size_t qbytes = m * (size_t)g.groups * 64, sbytes = m * (size_t)g.groups * sizeof(float);
+    int32_t rc = ensure_work(ctx, qbytes + sbytes + 256);
+    if (rc) return rc;
+    int8_t *q = (int8_t *)ctx->work;
+    float *s = (float *)((uint8_t *)ctx->work + (qbytes + 255) / 256 * 256);
+    dz::launch_fill_i32(ctx->flag, 0, 1, ctx->stream);
+    dz::launch_act_quantize(x, (int)m, g.cols, 8, q, s, ctx->flag, ctx->stream);
+    dz::launch_mlp_requant(g, u, q, s, (int)m, qo, so, ctx->flag, ctx->stream);
+    return launched(ctx, "fused MLP");
+}
+
+int32_t dz_linear_q8(dz_ctx *ctx, const dz_weight *w, const int8_t *q, const float *s, size_t m,
+                     float *y) {
+    DZ_BEGIN(ctx);
+    if (!w || (m && (!q || !s || !y))) return fail(ctx, DZ_INVALID_REQUEST, "null pointer");
+    if (w->w.kind == dz::WeightKind::Q4G32)
+        return fail(ctx, DZ_INVALID_PARAMETERS, "grouped int8 mode needs a group-64 weight");
+    dz::launch_grouped(w->w, q, s, (int)m, y, nullptr, variant(ctx, "grouped"), ctx->stream);
+    return launched(ctx, "grouped linear");
+}
+
+int32_t dz_i8_quantize_rows(dz_ctx *ctx, const float *x, size_t rows, size_t k, int8_t *q,
+                            float *scales, int32_t *sums) {
+    DZ_BEGIN(ctx);
+    if (rows && (!x || !q || !scales)) return fail(ctx, DZ_INVALID_REQUEST, "null pointer");
+    if (k == 0 || k > 32768) return fail(ctx, DZ_INVALID_PARAMETERS, "INT8 reduction must be 1..32768");
+    dz::launch_i8_quantize_rows(x, (int)rows, (int)k, q, scales, sums, ctx->stream);
+    return launched(ctx, "i8 quantize");
+}
+
+int32_t dz_i8_gemm(dz_ctx *ctx, const int8_t *a, const float *sa, size_t m, const int8_t *w,
+                   const float *sw, size_t n, size_t k, void *y, int32_t raw) {
+    DZ_BEGIN(ctx);
+    if ((m && n) && (!a || !w || !y || (!raw && (!sa || !sw))))
+        return fail(ctx, DZ_INVALID_REQUEST, "null pointer");
+    if (k == 0 || k > 32768) return fail(ctx, DZ_INVALID_PARAMETERS, "INT8 reduction must be 1..32768");
+    dz::launch_i8_gemm(a, sa, (int)m, w, sw, (int)n, (int)k, y, raw ? 1 : 0, variant(ctx, "i8_gemm"), ctx->stream);
+    return launched(ctx, "i8 gemm");
+}
+
+// ---- epilogues --------------------------------------------------------------------------
+
+int32_t dz_layernorm(dz_ctx *ctx, const void *x, void *y, int32_t dtype, size_t rows, size_t d,
+                     const float *w, const float *b, float eps) {
+    DZ_BEGIN(ctx);
+    if (dtype != DZ_F32 && dtype != DZ_F16) return fail(ctx, DZ_INVALID_PARAMETERS, "dtype must be f32 or f16");
+    if (rows && (!x || !y || !w || !b || d == 0)) return fail(ctx, DZ_INVALID_REQUEST, "invalid layernorm arguments");
+    dz::launch_layernorm(x, y, dtype == DZ_F16 ? 1 : 0, (int)rows, (int)d, w, b, eps, ctx->stream);
+    return launched(ctx, "layernorm");
+}
+
+int32_t dz_rmsnorm(dz_ctx *ctx, const float *x, float *y, size_t rows, size_t d, const float *w,
+                   float eps, int32_t zero_centered) {
+    DZ_BEGIN(ctx);
+    if (rows && (!x || !y || !w || d == 0)) return fail(ctx, DZ_INVALID_REQUEST, "invalid rmsnorm arguments");
+    dz::launch_rmsnorm(x, y, (int)rows, (int)d, w, eps, zero_centered, ctx->stream);
+    return launched(ctx, "rmsnorm");
+}
+
+int32_t dz_gelu(dz_ctx *ctx, void *x, int32_t dtype, size_t n) {
+    DZ_BEGIN(ctx);
+    if (dtype != DZ_F32 && dtype != DZ_F16) return fail(ctx, DZ_INVALID_PARAMETERS, "dtype must be f32 or f16");
+    if (n && !x) return fail(ctx, DZ_INVALID_REQUEST, "null pointer");
+    dz::launch_gelu(x, dtype == DZ_F16 ? 1 : 0, n, ctx->stream);
+    return launched(ctx, "gelu");
+}
+
+int32_t dz_silu_mul(dz_ctx *ctx, float *g, const float *u, size_t n) {
+    DZ_BEGIN(ctx);
+    if (n && (!g || !u)) return fail(ctx, DZ_INVALID_REQUEST, "null pointer");
+    dz::launch_silu_mul(g, u, n, ctx->stream);
+    return launched(ctx, "silu_mul");
+}
+
+int32_t dz_add(dz_ctx *ctx, void *x, const void *y, int32_t dtype, size_t n) {
+    DZ_BEGIN(ctx);
+    if (dtype != DZ_F32 && dtype != DZ_F16) return fail(ctx, DZ_INVALID_PARAMETERS, "dtype must be f32 or f16");
+    if (n && (!x || !y)) return fail(ctx, DZ_INVALID_REQUEST, "null pointer");
+    dz::launch_add(x, y, dtype == DZ_F16 ? 1 : 0, n, ctx->stream);
+    return launched(ctx, "add");
+}
+
+int32_t dz_softmax_rows(dz_ctx *ctx, float *x, size_t rows, size_t n) {
+    DZ_BEGIN(ctx);
+    if (rows && (!x || n == 0)) return fail(ctx, DZ_INVALID_REQUEST, "invalid softmax arguments");
+    dz::launch_softmax_rows(x, (int)rows, (int)n, ctx->stream);
+    return launched(ctx, "softmax");
+}
+
+int32_t dz_mean_rows(dz_ctx *ctx, const void *x, int32_t dtype, size_t batch, size_t rows, size_t d,
+                     float *out) {
+    DZ_BEGIN(ctx);
+    if (dtype != DZ_F32 && dtype != DZ_F16) return fail(ctx, DZ_INVALID_PARAMETERS, "dtype must be f32 or f16");
+    if (batch && (!x || !out || rows == 0 || d == 0)) return fail(ctx, DZ_INVALID_REQUEST, "invalid mean arguments");
+    dz::launch_mean_rows(x, dtype == DZ_F16 ? 1 : 0, (int)batch, (int)rows, (int)d, out, ctx->stream);
+    return launched(ctx, "mean");
+}
+
+int32_t dz_attention(dz_ctx *ctx, const void *qkv, void *out, size_t batch, size_t seq, size_t heads,
+                     size_t dh, float scale) {
+    DZ_BEGIN(ctx);
+    if (dh != 64) return fail(ctx, DZ_INVALID_PARAMETERS, "attention needs head_dim 64");
+    if (batch && seq && (!qkv || !out || heads == 0)) return fail(ctx, DZ_INVALID_REQUEST, "null pointer");
+    dz::launch_attention((const dz::half_t *)qkv, (dz::half_t *)out, (int)batch, (int)seq, (int)heads,
+                         (int)dh, scale, ctx->stream);
+    return launched(ctx, "attention");
+}
+
+// ---- encoder --------------------------------------------------------------------------
+
+int32_t dz_encoder_create_random(dz_ctx *ctx, const dz_encoder_config *cfg, uint64_t seed,
+                                 dz_encoder **out) {
+    DZ_BEGIN(ctx);
+    return dz::encoder_create_random(ctx, cfg, seed, out);
+}
+
+void dz_encoder_destroy(dz_ctx *ctx, dz_encoder *enc) {
+    if (!ctx) return;
+    hipSetDevice(ctx->device);
+    dz::encoder_destroy(ctx, enc);
+}
+
+int32_t dz_encoder_embedding_row_bytes(const dz_encoder *enc, size_t *row_bytes) {
+    return dz::encoder_row_bytes(enc, row_bytes);
+}
+
+const dz_weight *dz_encoder_weight(const dz_encoder *enc, int32_t layer, int32_t which) {
+    return dz::encoder_weight(enc, layer, which);
+}
+
+int32_t dz_encoder_read_rows(dz_ctx *ctx, const dz_encoder *enc, const int32_t *ids, size_t count,
+                             void *out) {
+    DZ_BEGIN(ctx);
+    return dz::encoder_read_rows(ctx, enc, ids, count, out);
+}
+
+int32_t dz_encoder_forward(dz_ctx *ctx, dz_encoder *enc, const int32_t *ids, size_t batch, size_t seq,
+                           float *out) {
+    DZ_BEGIN(ctx);
+    return dz::encoder_forward(ctx, enc, ids, nullptr, batch, seq, out);
+}
+
+int32_t dz_encoder_forward_rows(dz_ctx *ctx, dz_encoder *enc, const void *rows, size_t batch,
+                                size_t seq, float *out) {
+    DZ_BEGIN(ctx);
+    return dz::encoder_forward(ctx, enc, nullptr, rows, batch, seq, out);
+}
+
+// ---- tuner ---------------------------------------------------------------------------
+
+int32_t dz_tune(dz_ctx *ctx, uint32_t budget_ms, const char *cache_in, char *cache_out, size_t cap) {
+    DZ_BEGIN(ctx);
+    return dz::tune(ctx, budget_ms, cache_in, cache_out, cap);
+}
+
+int32_t dz_select_variant(dz_ctx *ctx, const char *family, const char *name) {
+    DZ_BEGIN(ctx);
+    if (!family || !name) return fail(ctx, DZ_INVALID_REQUEST, "null pointer");
+    int idx = dz::variant_index(family, name);
+    if (idx < 0) return fail(ctx, DZ_INVALID_PARAMETERS, std::string("unknown variant ") + family + "/" + name);
+    ctx->variants[family] = idx;
+    return DZ_OK;
+}
+
+}  // extern "C"
+
+// ---- helpers shared with encoder.hip and tuner.hip -----------------------------------
+
+namespace dz {
+
+int32_t ctx_fail(dz_ctx *ctx, int32_t code, const std::string &msg) { return fail(ctx, code, msg); }
+int32_t ctx_hip_fail(dz_ctx *ctx, hipError_t e, const char *what) { return hip_fail(ctx, e, what); }
+hipStream_t ctx_stream(dz_ctx *ctx) { return ctx->stream; }
+int *ctx_flag(dz_ctx *ctx) { return ctx->flag; }
+int ctx_variant(dz_ctx *ctx, const char *family) { return variant(ctx, family); }
+void ctx_set_variant(dz_ctx *ctx, const char *family, int index) { ctx->variants[family] = index; }
+void ctx_set_tuning(dz_ctx *ctx, const std::string &json) { ctx->tuning = json; }
+std::string ctx_device_key(dz_ctx *ctx) {
+    return ctx->arch + "/" + std::to_string(ctx->cus) + "cu/" + std::to_string(ctx->clock_khz) + "khz";
+}
+const Weight &weight_of(const dz_weight *h) { return h->w; }
+int32_t weight_quantize(dz_ctx *ctx, const void *values, int dtype, size_t rows, size_t cols, int bits,
+                        int group, dz_weight **out) {
+    return dz_weight_quantize(ctx, values, dtype, rows, cols, bits, group, out);
+}
+void weight_free(dz_weight *h) { free_weight(h); }
+
+}  // namespace dz

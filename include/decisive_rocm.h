@@ -1,0 +1,248 @@
+/*
+ * decisive_rocm.h -- C ABI of the MI355X (gfx950) quantized matrix-product
+ * library, libdecisive_rocm.so.
+ *
+ * The reference (hyperlogue/decisive, Rust) has no FFI on this path: its
+ * quantized products are Rust functions called in-process. Each entry point
+ * below names the reference function whose behaviour it takes over; a Rust
+ * `Rocm` backend binds these with `extern "C"`.
+ *
+ * Conventions
+ *  - Every call returns a dz_status; on failure dz_last_error(ctx) holds a
+ *    message that stays valid until the next call on the same context.
+ *  - Pointers named *_dev are device memory on the context's GPU (from
+ *    dz_alloc, hipMalloc or a framework allocator). *_host pointers are host
+ *    memory borrowed for the duration of the call.
+ *  - Work is enqueued on the context's stream (dz_set_stream may replace it)
+ *    and is asynchronous unless stated; dz_sync waits for it.
+ *  - A context is not thread-safe; the caller serialises calls, as the
+ *    reference's `Backend::predict(&mut self, ..)` does.
+ */
+#ifndef DECISIVE_ROCM_H
+#define DECISIVE_ROCM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct dz_ctx dz_ctx;
+typedef struct dz_weight dz_weight;
+typedef struct dz_encoder dz_encoder;
+
+/* Status codes map 1:1 onto the reference's error codes
+ * (src/inference/mod.rs:44-85, parameters.rs:368-376, browser/pplx.rs:105). */
+typedef enum dz_status {
+    DZ_OK = 0,
+    DZ_INVALID_REQUEST = 1,     /* "INVALID_REQUEST"     mod.rs:32-35   */
+    DZ_INVALID_PARAMETERS = 2,  /* "INVALID_PARAMETERS"  parameters.rs:370-373 */
+    DZ_CANCELLED = 3,           /* "CANCELLED"           mod.rs:95      */
+    DZ_CACHE_OWNER = 4,         /* "CACHE_OWNER"         mod.rs:199-202 */
+    DZ_INPUT_TOO_LONG = 5,      /* "INPUT_TOO_LONG"      mod.rs:58-62   */
+    DZ_GPU_UNAVAILABLE = 6,     /* "GPU_UNAVAILABLE"     mod.rs:65-66   */
+    DZ_RESOURCE_LIMIT = 7,      /* "RESOURCE_LIMIT"      mod.rs:67-68   */
+    DZ_MISSING_GPU_FEATURE = 8, /* "MISSING_GPU_FEATURE" mod.rs:63-64   */
+    DZ_INFERENCE_FAILED = 9,    /* "INFERENCE_FAILED"    mod.rs:73-74   */
+    DZ_INVALID_CHECKPOINT = 10, /* "INVALID_CHECKPOINT"  browser/pplx.rs:105,126 */
+    DZ_UNSUPPORTED_CACHE = 11   /* "UNSUPPORTED_CACHE"   mod.rs:181-186 */
+} dz_status;
+
+/* Packed weight layouts accepted by dz_weight_upload. */
+typedef enum dz_layout {
+    /* packed.rs:3-56: per row, per 64-run along K: 32 bytes of code+8 nibbles
+     * (low nibble = even k) then the f32 LE scale; 36 B per group. */
+    DZ_Q4_G64_F32 = 0,
+    /* packed.rs:3-56 with bits=8: 64 two's-complement code bytes + f32 scale. */
+    DZ_Q8_G64_F32 = 1,
+    /* Group-32 variant with f16 scales: 16 code bytes + f16 LE scale (18 B). */
+    DZ_Q4_G32_F16 = 2
+} dz_layout;
+
+typedef enum dz_dtype { DZ_F32 = 0, DZ_F16 = 1, DZ_BF16 = 2 } dz_dtype;
+
+/* Numeric mode of dz_linear. */
+typedef enum dz_mode {
+    /* Activations re-quantized per (row, 64-group) to int8 (int8.rs:178-202)
+     * and multiplied with exact int32 group dots folded in the AVX2 order
+     * acc = fma(f32(dot), sw*sx, acc) (int8.rs:524-585). Bit-exact with the
+     * reference CPU path. x is f32. W8A8 when the weight is Q8. */
+    DZ_W4A8 = 0,
+    /* As DZ_W4A8 with 4-bit activation codes (int8.rs:59-69 Precision bits). */
+    DZ_W4A4 = 1,
+    /* f16 activations times dequantized Q4 weights, f32 accumulation. */
+    DZ_W4A16 = 2
+} dz_mode;
+
+/* ---- context -------------------------------------------------------------- */
+
+/* Name of a status ("OK", "INVALID_REQUEST", ...). Never NULL. */
+const char *dz_status_name(int32_t status);
+/* Opens a context on HIP device `device` with its own stream. Fails with
+ * DZ_GPU_UNAVAILABLE when there is no device, DZ_MISSING_GPU_FEATURE when the
+ * device is not gfx950. */
+int32_t dz_init(int32_t device, dz_ctx **out);
+void dz_destroy(dz_ctx *ctx);
+const char *dz_last_error(const dz_ctx *ctx);
+/* Replaces the context stream (a hipStream_t); NULL restores its own. */
+int32_t dz_set_stream(dz_ctx *ctx, void *hip_stream);
+int32_t dz_sync(dz_ctx *ctx);
+/* JSON description of the device and the selected kernel variants. */
+int32_t dz_info(dz_ctx *ctx, char *buf, size_t cap);
+
+/* Device memory for callers without an allocator of their own. */
+int32_t dz_alloc(dz_ctx *ctx, size_t bytes, void **dev);
+int32_t dz_free(dz_ctx *ctx, void *dev);
+int32_t dz_copy_h2d(dz_ctx *ctx, void *dst_dev, const void *src_host, size_t bytes);
+int32_t dz_copy_d2h(dz_ctx *ctx, void *dst_host, const void *src_dev, size_t bytes);
+
+/* ---- weights ---------------------------------------------------------------- */
+
+/* Takes over packed.rs:59-73 (unpack validation) at load: copies `bytes` of a
+ * packed [rows x cols] matrix in `layout` to the device and re-tiles it into
+ * the library's HBM layout. Rejects a scale that is not finite and positive
+ * (DZ_INVALID_CHECKPOINT), a byte count that does not match packed.rs:10-19
+ * size() (DZ_INVALID_CHECKPOINT) and an unknown layout (DZ_INVALID_PARAMETERS).
+ * Synchronous. */
+int32_t dz_weight_upload(dz_ctx *ctx, const void *packed_host, size_t bytes, int32_t layout,
+                         size_t rows, size_t cols, dz_weight **out);
+/* Takes over int8.rs:51-152 Matrix::from_bf16_optimized (plain mode; bits 4
+ * or 8, group 64, f32 scales; any cols, zero padded) and, with group == 32
+ * and bits == 4, the group-32/f16 quantizer. `values_dev` is [rows x cols] of
+ * `dtype`. Non-finite weights give DZ_INVALID_CHECKPOINT. Synchronous. */
+int32_t dz_weight_quantize(dz_ctx *ctx, const void *values_dev, int32_t dtype, size_t rows,
+                           size_t cols, int32_t bits, int32_t group, dz_weight **out);
+int32_t dz_weight_free(dz_ctx *ctx, dz_weight *w);
+/* rows, cols, bits, group and device bytes of a weight; any pointer may be NULL. */
+int32_t dz_weight_info(const dz_weight *w, size_t *rows, size_t *cols, int32_t *bits,
+                       int32_t *group, size_t *device_bytes);
+
+/* packed.rs:59-73 unpack / quantized_rows.rs:89-110 append: y = f32(code)*scale,
+ * [rows x cols] f32, bit-exact. */
+int32_t dz_dequant(dz_ctx *ctx, const dz_weight *w, float *y_dev);
+/* Dequantizes the rows listed in ids_dev (int32, count entries) into
+ * y_dev [count x cols] of `dtype` (f32 exact; f16 rounds to nearest even):
+ * the embedding-row gather of browser_gpu.rs:177-209 done on device. */
+int32_t dz_dequant_rows(dz_ctx *ctx, const dz_weight *w, const int32_t *ids_dev, size_t count,
+                        void *y_dev, int32_t dtype);
+
+/* ---- quantized products ------------------------------------------------------ */
+
+/* int8.rs:178-202 Matrix::prepare: per (row, 64-group) activation codes.
+ * x_dev f32 [m x k]; q_dev int8 [m x G*64] (G = ceil(k/64), tail zero);
+ * s_dev f32 [m x G]. bits is 8 or 4. */
+int32_t dz_act_quantize(dz_ctx *ctx, const float *x_dev, size_t m, size_t k, int32_t bits,
+                        int8_t *q_dev, float *s_dev);
+/* int8.rs:166-176 Matrix::apply (DZ_W4A8/DZ_W4A4; x f32, a non-finite value
+ * anywhere in x makes every output NaN, int8.rs:170-173) or the W4A16 product
+ * (x f16). y_dev f32 [m x rows(w)]. m may be 0. */
+int32_t dz_linear(dz_ctx *ctx, const dz_weight *w, const void *x_dev, int32_t x_dtype, size_t m,
+                  float *y_dev, int32_t mode);
+/* int8.rs:204-227 Matrix::apply_pair: one activation quantization shared by
+ * two weights with the same cols. */
+int32_t dz_linear_pair(dz_ctx *ctx, const dz_weight *a, const dz_weight *b, const float *x_dev,
+                       size_t m, float *ya_dev, float *yb_dev, int32_t mode);
+/* grouped_q4_mlp.wgsl:1-105 (q4_mlp): gate/up W4A8 products of one input,
+ * v = silu(gate)*up, re-quantized per (row, 64-column block) to the A8 form of
+ * dz_act_quantize: q_dev int8 [m x n], s_dev f32 [m x n/64]. n % 64 == 0. */
+int32_t dz_mlp_requant(dz_ctx *ctx, const dz_weight *gate, const dz_weight *up,
+                       const float *x_dev, size_t m, int8_t *q_dev, float *s_dev);
+/* Product of already-quantized activations (the A8 form above) with a weight:
+ * the down_proj consumer of dz_mlp_requant. */
+int32_t dz_linear_q8(dz_ctx *ctx, const dz_weight *w, const int8_t *q_dev, const float *s_dev,
+                     size_t m, float *y_dev);
+
+/* webgpu/int8.rs:107-145 quantize: per row scale = absmax/127 (no floor),
+ * q = clamp(rne(x/scale), +-127), 0 when scale == 0; sums = sum of q.
+ * q_dev int8 [rows x k] (signed), scales_dev f32 [rows], sums_dev int32 [rows]
+ * (may be NULL). */
+int32_t dz_i8_quantize_rows(dz_ctx *ctx, const float *x_dev, size_t rows, size_t k,
+                            int8_t *q_dev, float *scales_dev, int32_t *sums_dev);
+/* webgpu/int8.rs:147-242 gemm(fused=false, raw): y [m x n] = exact int32
+ * sum_k a[i,k]*w[j,k] (raw != 0, y int32) or (f32(dot)*sa[i])*sw[j] (y f32). */
+int32_t dz_i8_gemm(dz_ctx *ctx, const int8_t *a_dev, const float *sa_dev, size_t m,
+                   const int8_t *w_dev, const float *sw_dev, size_t n, size_t k, void *y_dev,
+                   int32_t raw);
+
+/* ---- layer epilogues --------------------------------------------------------- */
+
+/* decima/cpu.rs:529-540 LayerNorm over rows of d: (x-mean)*rsqrt(var+eps)*w+b.
+ * x/y are f32 or f16 (dtype), w/b f32. y may alias x. */
+int32_t dz_layernorm(dz_ctx *ctx, const void *x_dev, void *y_dev, int32_t dtype, size_t rows,
+                     size_t d, const float *w_dev, const float *b_dev, float eps);
+/* pplx_flash/cpu.rs:310-333 rms_from (zero_centered != 0 uses 1 + w). f32. */
+int32_t dz_rmsnorm(dz_ctx *ctx, const float *x_dev, float *y_dev, size_t rows, size_t d,
+                   const float *w_dev, float eps, int32_t zero_centered);
+/* decima/cpu.rs:542-556 gelu (erf form), in place, f32 or f16. */
+int32_t dz_gelu(dz_ctx *ctx, void *x_dev, int32_t dtype, size_t n);
+/* pplx_flash/cpu.rs:348-371 silu_mul: gate = silu(gate)*up, f32. */
+int32_t dz_silu_mul(dz_ctx *ctx, float *gate_dev, const float *up_dev, size_t n);
+/* pplx_flash/cpu.rs:334-347 add: x += y, f32 or f16. */
+int32_t dz_add(dz_ctx *ctx, void *x_dev, const void *y_dev, int32_t dtype, size_t n);
+/* pplx_flash/cpu.rs:519-529 softmax over each row of n, f32. */
+int32_t dz_softmax_rows(dz_ctx *ctx, float *x_dev, size_t rows, size_t n);
+/* decima/cpu.rs:574-586 mean over rows: x [batch x rows x d] (f32/f16) ->
+ * out f32 [batch x d]. */
+int32_t dz_mean_rows(dz_ctx *ctx, const void *x_dev, int32_t dtype, size_t batch, size_t rows,
+                     size_t d, float *out_dev);
+/* Non-causal softmax attention (pplx_flash/backbone.rs:484-615 without the
+ * gate/RoPE): qkv f16 [batch*seq x 3*heads*dh] (q | k | v), out f16
+ * [batch*seq x heads*dh]; scores scaled by `scale`, f32 softmax. dh == 64. */
+int32_t dz_attention(dz_ctx *ctx, const void *qkv_dev, void *out_dev, size_t batch, size_t seq,
+                     size_t heads, size_t dh, float scale);
+
+/* ---- encoder forward -------------------------------- */
+
+typedef struct dz_encoder_config {
+    int32_t layers;     /* 24   */
+    int32_t hidden;     /* 1024 */
+    int32_t heads;      /* 16   */
+    int32_t head_dim;   /* 64   */
+    int32_t ffn;        /* 4096 */
+    int32_t vocab;      /* 32000 */
+    float ln_eps;       /* LayerNorm epsilon */
+} dz_encoder_config;
+
+/* Builds an encoder with random-init weights from `seed` (all linear weights
+ * N(0, 0.02) quantized to Q4 g32/f16 on device, embedding rows Q4 g64/f32,
+ * LayerNorm weight 1 / bias 0). Synchronous. */
+int32_t dz_encoder_create_random(dz_ctx *ctx, const dz_encoder_config *cfg, uint64_t seed,
+                                 dz_encoder **out);
+void dz_encoder_destroy(dz_ctx *ctx, dz_encoder *enc);
+/* The packed embedding rows (Q4 g64/f32 wire layout) of ids_host, copied to
+ * out_host (count * row_bytes); the EmbeddingCache source. Synchronous. */
+int32_t dz_encoder_embedding_row_bytes(const dz_encoder *enc, size_t *row_bytes);
+int32_t dz_encoder_read_rows(dz_ctx *ctx, const dz_encoder *enc, const int32_t *ids_host,
+                             size_t count, void *out_host);
+/* The encoder's weights for inspection: which = 0 qkv [3h x h], 1 output
+ * [h x h], 2 ffn up [f x h], 3 ffn down [h x f] of `layer`; 4 the embedding
+ * table [vocab x h]. Owned by the encoder; NULL when out of range. */
+const dz_weight *dz_encoder_weight(const dz_encoder *enc, int32_t layer, int32_t which);
+/* Forward over batch x seq token ids (ids_dev int32) -> mean-pooled
+ * embeddings out_dev f32 [batch x hidden]. */
+int32_t dz_encoder_forward(dz_ctx *ctx, dz_encoder *enc, const int32_t *ids_dev, size_t batch,
+                           size_t seq, float *out_dev);
+/* Same forward from packed embedding rows already gathered on the host
+ * (rows_host: batch*seq rows in the Q4 g64/f32 wire layout), as the
+ * EmbeddingCache hands them over (browser/pplx.rs:76-137). */
+int32_t dz_encoder_forward_rows(dz_ctx *ctx, dz_encoder *enc, const void *rows_host,
+                                size_t batch, size_t seq, float *out_dev);
+
+/* ---- kernel tuner (webgpu/checkpoint.rs:95-294, 428-652) ------------------------ */
+
+/* Times the tile variants of every tuned kernel family at the reference's
+ * tuning shapes within budget_ms, keeps the fastest variant whose output is
+ * bitwise equal to the family's reference variant and faster than 0.99x it.
+ * cache_in (JSON from an earlier cache_out, or NULL) is reused while its key
+ * still matches, re-checking equality only. The selection JSON is written to
+ * cache_out (cap bytes). budget_ms == 0 keeps the reference variants. */
+int32_t dz_tune(dz_ctx *ctx, uint32_t budget_ms, const char *cache_in, char *cache_out,
+                size_t cap);
+/* Forces a variant of a family by name (tests and benchmarks). */
+int32_t dz_select_variant(dz_ctx *ctx, const char *family, const char *variant);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -18,3 +18,11 @@ def oracle():
     from oracle import oracle as o
     o.lib()
     return o
+
+
+@pytest.fixture(scope="session")
+def ctx():
+    from decisive_amd import rocm
+    c = rocm.Context(0)
+    yield c
+    c.close()

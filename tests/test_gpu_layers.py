@@ -1,0 +1,187 @@
+"""GPU parity of the layer epilogues, attention, the encoder forward and the
+tuner. Float reductions here are trees, so the bar is a tolerance against the
+oracle's float64/f32 restatements (erff, expf: parity unpinned at the ulp)."""
+import math
+
+import numpy as np
+import pytest
+
+from decisive_amd import rocm
+from tests.gpu_util import bits_equal, cosine, dev, empty, host
+
+pytestmark = pytest.mark.gpu
+
+
+def test_layernorm_gelu_rms_softmax_mean(ctx, oracle):
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(1)
+    rows, d = 37, 1024
+    x = (rng.standard_normal((rows, d)) * 3 + 1).astype(np.float32)
+    w = rng.standard_normal(d).astype(np.float32)
+    b = rng.standard_normal(d).astype(np.float32)
+    y = empty((rows, d), torch.float32)
+    ctx.layernorm(dev(x), y, rocm.F32, rows, d, dev(w), dev(b), 1e-12)
+    assert np.allclose(host(ctx, y), oracle.layernorm(x, w, b, 1e-12), atol=2e-5, rtol=1e-5)
+    xh = dev(x.astype(np.float16))
+    yh = empty((rows, d), torch.float16)
+    ctx.layernorm(xh, yh, rocm.F16, rows, d, dev(w), dev(b), 1e-5)
+    ref = oracle.layernorm(x.astype(np.float16).astype(np.float32), w, b, 1e-5)
+    assert np.allclose(host(ctx, yh).astype(np.float32), ref, atol=1e-2, rtol=2e-3)
+    g = dev(x.copy())
+    ctx.gelu(g, rocm.F32, x.size)
+    assert np.allclose(host(ctx, g), oracle.gelu(x), atol=1e-5, rtol=1e-5)
+    r = empty((rows, d), torch.float32)
+    ctx.rmsnorm(dev(x), r, rows, d, dev(w), 1e-6)
+    assert np.allclose(host(ctx, r), oracle.rmsnorm(x, w, 1e-6), atol=1e-5, rtol=1e-5)
+    up = rng.standard_normal((rows, d)).astype(np.float32)
+    gs = dev(x.copy())
+    ctx.silu_mul(gs, dev(up), x.size)
+    assert np.allclose(host(ctx, gs), oracle.silu_mul(x, up), atol=1e-5, rtol=1e-5)
+    sm = dev(x.copy())
+    ctx.softmax_rows(sm, rows, d)
+    got = host(ctx, sm)
+    for i in range(rows):
+        assert np.allclose(got[i], oracle.softmax(x[i]), atol=1e-7, rtol=1e-5)
+    mean = empty((1, d), torch.float32)
+    ctx.mean_rows(dev(x), rocm.F32, 1, rows, d, mean)
+    assert np.allclose(host(ctx, mean)[0], oracle.mean_rows(x), atol=1e-5)
+    a = dev(x.copy())
+    ctx.add(a, dev(up), rocm.F32, x.size)
+    assert bits_equal(host(ctx, a), x + up)
+
+
+@pytest.mark.parametrize("batch,seq,heads", [(1, 64, 1), (2, 100, 3), (1, 1024, 2)])
+def test_attention_matches_closed_form(ctx, oracle, batch, seq, heads):
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(seq)
+    width = heads * 64
+    qkv = (rng.standard_normal((batch * seq, 3 * width)) * 0.8).astype(np.float16)
+    out = empty((batch * seq, width), torch.float16)
+    ctx.attention(dev(qkv), out, batch, seq, heads, 64, 1 / 8)
+    got = host(ctx, out).astype(np.float32)
+    for b in range(batch):
+        sl = slice(b * seq, (b + 1) * seq)
+        q, k, v = (qkv[sl, i * width:(i + 1) * width].astype(np.float32) for i in range(3))
+        ref = oracle.attention(q, k, v, heads, 1 / 8)
+        assert np.abs(got[sl] - ref).max() <= 5e-3
+        assert cosine(got[sl], ref) >= 0.9999
+
+
+def _encoder_reference(ctx, enc, cfg, ids, batch, seq):
+    """float32 composition of the dequantized encoder weights, rounding to f16
+    where the GPU stores activations."""
+    torch = pytest.importorskip("torch")
+
+    def deq(layer, which):
+        w = enc.weight(layer, which)
+        y = empty((w.rows, w.cols), torch.float32)
+        ctx.dequant(w, y)
+        return host(ctx, y)
+
+    f16 = lambda a: a.astype(np.float16).astype(np.float32)
+    d = cfg.hidden
+    ones, zeros = np.ones(d, np.float32), np.zeros(d, np.float32)
+    h = f16(deq(0, rocm.Encoder.EMBED)[ids])
+    h = f16(ctx_ln(h, ones, zeros, cfg.ln_eps))
+    for layer in range(cfg.layers):
+        wqkv, wo, w1, w2 = (deq(layer, i) for i in range(4))
+        qkv = f16(h @ wqkv.T)
+        att = np.empty((h.shape[0], d), np.float32)
+        for b in range(batch):
+            sl = slice(b * seq, (b + 1) * seq)
+            att[sl] = oracle_attention(qkv[sl, :d], qkv[sl, d:2 * d], qkv[sl, 2 * d:], cfg.heads)
+        att = f16(att)
+        h = f16(ctx_ln(f16(att @ wo.T + h), ones, zeros, cfg.ln_eps))
+        ff = h @ w1.T
+        ff = f16(0.5 * ff * (1 + np.vectorize(math.erf)(ff / math.sqrt(2))))
+        h = f16(ctx_ln(f16(ff @ w2.T + h), ones, zeros, cfg.ln_eps))
+    return h.reshape(batch, seq, d).mean(1)
+
+
+def ctx_ln(x, w, b, eps):
+    mu = x.mean(1, keepdims=True)
+    var = ((x - mu) ** 2).mean(1, keepdims=True)
+    return ((x - mu) / np.sqrt(var + eps) * w + b).astype(np.float32)
+
+
+def oracle_attention(q, k, v, heads):
+    out = np.empty_like(q)
+    for h in range(heads):
+        sl = slice(h * 64, (h + 1) * 64)
+        s = q[:, sl].astype(np.float64) @ k[:, sl].astype(np.float64).T / 8.0
+        p = np.exp(s - s.max(1, keepdims=True))
+        p /= p.sum(1, keepdims=True)
+        out[:, sl] = p @ v[:, sl]
+    return out
+
+
+def test_small_encoder_matches_composition(ctx, oracle):
+    torch = pytest.importorskip("torch")
+    cfg = rocm.EncoderConfig(layers=2, hidden=128, heads=2, head_dim=64, ffn=256, vocab=100, ln_eps=1e-5)
+    enc = ctx.encoder_random(cfg, 7)
+    batch, seq = 2, 64
+    ids = np.random.default_rng(3).integers(0, cfg.vocab, batch * seq).astype(np.int32)
+    out = empty((batch, cfg.hidden), torch.float32)
+    enc.forward(dev(ids), batch, seq, out)
+    got = host(ctx, out)
+    want = _encoder_reference(ctx, enc, cfg, ids, batch, seq)
+    assert cosine(got, want) >= 0.999
+    assert np.abs(got - want).max() <= 2e-2
+    # the embedding-cache path (packed host rows) gives the same bits
+    rows = enc.read_rows(ids)
+    out2 = empty((batch, cfg.hidden), torch.float32)
+    enc.forward_rows(rows, batch, seq, out2)
+    assert bits_equal(host(ctx, out2), got)
+    # wire rows equal the oracle's unpack of the same table
+    full = empty((cfg.vocab, cfg.hidden), torch.float32)
+    ctx.dequant(enc.weight(0, rocm.Encoder.EMBED), full)
+    assert bits_equal(oracle.unpack_g64(rows, 4).reshape(-1, cfg.hidden), host(ctx, full)[ids])
+    with pytest.raises(rocm.DzError) as e:
+        enc.forward(dev(np.array([0, cfg.vocab], np.int32)), 1, 2, out)
+    assert e.value.code == "INVALID_REQUEST"
+    enc.close()
+
+
+def test_config3_encoder_full_size_runs_finite_and_deterministic(ctx):
+    torch = pytest.importorskip("torch")
+    cfg = rocm.EncoderConfig(layers=24, hidden=1024, heads=16, head_dim=64, ffn=4096, vocab=32000, ln_eps=1e-5)
+    enc = ctx.encoder_random(cfg, 1)
+    ids = np.random.default_rng(1).integers(0, 32000, 8 * 1024).astype(np.int32)
+    out = empty((8, 1024), torch.float32)
+    enc.forward(dev(ids), 8, 1024, out)
+    a = host(ctx, out)
+    enc.forward(dev(ids), 8, 1024, out)
+    b = host(ctx, out)
+    assert np.isfinite(a).all() and bits_equal(a, b)
+    assert np.abs(a).max() > 0
+    enc.close()
+
+
+def test_tuner_selects_bitwise_equal_variants_and_caches(ctx):
+    sel = ctx.tune(400)
+    fams = sel["families"]
+    for fam in ("gemv", "gemm_w4a16", "i8_gemm"):
+        f = fams[fam]
+        assert f["selected"] == sel["selected"][fam]
+        if "agrees" in f:
+            idx = f["candidates"].index(f["selected"])
+            assert f["agrees"][idx] is True
+            if idx:
+                assert f["ms_per_run"][idx] < f["ms_per_run"][0] * 0.99
+    again = ctx.tune(400, cache=__import__("json").dumps(sel))
+    assert again["key"] == sel["key"]
+    for fam in ("gemv", "gemm_w4a16", "i8_gemm"):
+        assert again["families"][fam].get("cached") is True
+        assert again["selected"][fam] == sel["selected"][fam]
+    info = ctx.info()
+    assert info["variants"]["gemv"] == sel["selected"]["gemv"]
+    # a zero budget starts no selection stage (parameters.rs:305-322)
+    zero = ctx.tune(0)
+    for fam in ("gemv", "gemm_w4a16", "i8_gemm"):
+        assert zero["selected"][fam] == rocm_reference(fam)
+    for fam, name in sel["selected"].items():
+        ctx.select_variant(fam, rocm_reference(fam))
+
+
+def rocm_reference(fam):
+    return {"gemv": "w8u4", "gemm_w4a16": "256x128w2x2", "i8_gemm": "128x128w2x2"}[fam]

@@ -1,0 +1,312 @@
+"""GPU parity of the quantized products.
+
+W4A8/W8A8/W4A4 and the per-row int8 GEMM are integer work folded in a fixed
+float order: bit-exact against the oracle. W4A16 has no reference kernel: it is
+checked against the float64 closed form with the north-star tolerance
+(max-abs <= 1e-2, cosine >= 0.9999)."""
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from decisive_amd import rocm
+from tests.gpu_util import bits_equal, cosine, dev, empty, host
+
+pytestmark = pytest.mark.gpu
+GOLDEN = json.loads((Path(__file__).parent / "golden" / "reference_vectors.json").read_text())
+MAX_ABS = 1e-2  # north_star tolerance for f16/f32 GEMM outputs
+MIN_COS = 0.9999
+
+
+# ---- grouped W{4,8}A{8,4} ------------------------------------------------------------
+
+@pytest.mark.parametrize("wb,ab", GOLDEN["grouped_dot_shapes"]["bits"])
+def test_grouped_matches_avx2_order_bit_exact(ctx, oracle, wb, ab):
+    """int8.rs:678-772 shapes and generators: GPU == oracle fused (AVX2) order."""
+    torch = pytest.importorskip("torch")
+    for m, k, n in GOLDEN["grouped_dot_shapes"]["mkn"]:
+        i = np.arange(k * n)
+        raw = oracle.f32_to_bf16(((i * 37 % 257) - 128.0) / 31.0)
+        x = (((np.arange(m * k) * 13 % 255) - 127.0) / 17.0).astype(np.float32)
+        w = ctx.quantize(dev(raw), rocm.BF16, n, k, wb, 64)
+        y = empty((max(m, 1), n), torch.float32)
+        ctx.linear(w, dev(x) if m else 0, rocm.F32, m, y if m else 0, rocm.W4A4 if ab == 4 else rocm.W4A8)
+        if m == 0:
+            continue
+        codes, scales = oracle.weight_quantize(raw, n, k, wb)
+        want = oracle.matrix_apply(x, m, codes, scales, n, k, ab, fused=True)
+        got = host(ctx, y)[:m]
+        assert bits_equal(got, want), (m, k, n, float(np.abs(got - want).max()))
+
+
+@pytest.mark.parametrize("case", range(5))
+@pytest.mark.parametrize("bits", [4, 8])
+def test_kernel_check_cases_vs_project(ctx, oracle, case, bits):
+    """webgpu/grouped_q4.rs:215-311 cases through the wire layout: bit-exact with
+    the AVX2 order and within 1e-4 + 2e-6*|a||b| of packed::project."""
+    torch = pytest.importorskip("torch")
+    m, n, k = GOLDEN["kernel_check_shapes"]["mnk"][case]
+    i = np.arange(m * k)
+    if case == 4:
+        a = np.where((i // k) % 2 == 0, 127.0, -127.0)
+    elif case == 3:
+        a = ((i * 73 % 1021) - 510.0) / 113.0
+    else:
+        a = ((i * 17 % 255) - 127.0) * np.where(i % k < 64, 0.125, 4.0)
+    a = a.astype(np.float32)
+    j = np.arange(n * k)
+    if case == 4:
+        b = np.where(((j // k) + (j % k) // 64) % 3 == 0, -7.0, 7.0)
+    elif case == 3:
+        b = ((j * 47 % 257) - 128.0) / 193.0
+    else:
+        b = ((j * 11 % 15) - 7.0) * np.where(j % k < 64, 0.25, 8.0)
+    b = b.astype(np.float32)
+    raw = (b.view(np.uint32) >> 16).astype(np.uint16)  # truncating BF16, grouped_q4.rs:247-250
+    packed = oracle.pack_g64(raw, n, k, bits)
+    w = ctx.upload(packed, rocm.Q4_G64_F32 if bits == 4 else rocm.Q8_G64_F32, n, k)
+    y = empty((m, n), torch.float32)
+    ctx.linear(w, dev(a), rocm.F32, m, y, rocm.W4A8)
+    got = host(ctx, y)
+    codes, scales = oracle.weight_quantize(raw, n, k, bits)
+    assert bits_equal(got, oracle.matrix_apply(a, m, codes, scales, n, k, 8, fused=True))
+    packed_abs = oracle.pack_g64((np.abs(b).view(np.uint32) >> 16).astype(np.uint16), n, k, bits)
+    for r in range(m):
+        want = oracle.project(packed, bits, k, a[r * k:(r + 1) * k], n)
+        mag = oracle.project(packed_abs, bits, k, np.abs(a[r * k:(r + 1) * k]), n)
+        assert np.all(np.abs(got[r] - want) <= 1e-4 + mag * 2e-6)
+
+
+def test_config1_q4_linear_bit_exact(ctx, oracle):
+    """x N(0,1) [128 x 1024] seed 0, W N(0,0.02) [1024 x 1024]
+    seed 1, through the reference's g64 quantizer (BF16 input)."""
+    torch = pytest.importorskip("torch")
+    m = k = n = 1024
+    m = 128
+    x = np.random.default_rng(0).standard_normal((m, k)).astype(np.float32)
+    wf = (np.random.default_rng(1).standard_normal((n, k)) * 0.02).astype(np.float32)
+    raw = oracle.f32_to_bf16(wf)
+    packed = oracle.pack_g64(raw, n, k, 4)
+    w = ctx.upload(packed, rocm.Q4_G64_F32, n, k)
+    y = empty((m, n), torch.float32)
+    ctx.linear(w, dev(x), rocm.F32, m, y, rocm.W4A8)
+    codes, scales = oracle.weight_quantize(raw, n, k, 4)
+    want = oracle.matrix_apply(x, m, codes, scales, n, k, 8, fused=True)
+    assert bits_equal(host(ctx, y), want)
+    # the g32/f16 twin in W4A16 against the float64 closed form
+    packed32 = oracle.pack_g32_f16(wf, n, k)
+    w32 = ctx.upload(packed32, rocm.Q4_G32_F16, n, k)
+    xh = oracle.f32_to_f16_bits(x)
+    ctx.linear(w32, dev(xh.view(np.float16)), rocm.F16, m, y, rocm.W4A16)
+    closed = oracle.w4a16(xh, m, k, oracle.unpack_g32_f16(packed32).reshape(n, k), n)
+    got = host(ctx, y)
+    assert np.abs(got - closed).max() <= MAX_ABS and cosine(got, closed) >= MIN_COS
+
+
+def test_nonfinite_activation_makes_every_output_nan(ctx, oracle):
+    """int8.rs:170-173 and :952-962."""
+    torch = pytest.importorskip("torch")
+    raw = oracle.f32_to_bf16(np.ones((9, 70), np.float32))
+    w = ctx.quantize(dev(raw), rocm.BF16, 9, 70, 4, 64)
+    x = np.zeros((3, 70), np.float32)
+    x[2, 69] = np.inf
+    y = empty((3, 9), torch.float32)
+    ctx.linear(w, dev(x), rocm.F32, 3, y, rocm.W4A8)
+    assert np.isnan(host(ctx, y)).all()
+    x[2, 69] = 0.0
+    ctx.linear(w, dev(x), rocm.F32, 3, y, rocm.W4A8)
+    assert (host(ctx, y) == 0).all()
+
+
+def test_pair_shares_one_quantization(ctx, oracle):
+    """int8.rs:204-227 apply_pair == two applies (and thread-count invariance
+    becomes launch invariance: repeated calls are bitwise identical)."""
+    torch = pytest.importorskip("torch")
+    m, k, n = 33, 320, 96
+    rng = np.random.default_rng(11)
+    a = ctx.quantize(dev(rng.standard_normal((n, k)).astype(np.float32)), rocm.F32, n, k, 4, 64)
+    b = ctx.quantize(dev(rng.standard_normal((n, k)).astype(np.float32)), rocm.F32, n, k, 4, 64)
+    x = dev(rng.standard_normal((m, k)).astype(np.float32))
+    ya, yb, y1, y2 = (empty((m, n), torch.float32) for _ in range(4))
+    ctx.linear_pair(a, b, x, m, ya, yb)
+    ctx.linear(a, x, rocm.F32, m, y1, rocm.W4A8)
+    ctx.linear(b, x, rocm.F32, m, y2, rocm.W4A8)
+    assert bits_equal(host(ctx, ya), host(ctx, y1)) and bits_equal(host(ctx, yb), host(ctx, y2))
+
+
+def test_fused_mlp_requant_equals_unfused(ctx, oracle):
+    """grouped_q4.rs:313-354: fused gate/up/SiLU/requant == unfused, word-exact;
+    both against the oracle composition within one code."""
+    torch = pytest.importorskip("torch")
+    m, n, k = GOLDEN["fused_mlp_check"]["mnk"]
+
+    def weight(seed):
+        v = (((np.arange(n * k) * seed % 251) - 125.0) / 400.0).astype(np.float32)
+        return (v.view(np.uint32) >> 16).astype(np.uint16)
+
+    graw, uraw = weight(37), weight(53)
+    gate = ctx.upload(oracle.pack_g64(graw, n, k, 4), rocm.Q4_G64_F32, n, k)
+    up = ctx.upload(oracle.pack_g64(uraw, n, k, 4), rocm.Q4_G64_F32, n, k)
+    x = (((np.arange(m * k) * 29 % 509) - 254.0) / 97.0).astype(np.float32)
+    xd = dev(x)
+    q = empty((m, n), torch.int8)
+    s = empty((m, n // 64), torch.float32)
+    ctx.mlp_requant(gate, up, xd, m, q, s)
+    g = empty((m, n), torch.float32)
+    u = empty((m, n), torch.float32)
+    ctx.linear_pair(gate, up, xd, m, g, u)
+    ctx.silu_mul(g, u, m * n)
+    q2 = empty((m, n), torch.int8)
+    s2 = empty((m, n // 64), torch.float32)
+    ctx.act_quantize(g, m, n, 8, q2, s2)
+    assert np.array_equal(host(ctx, q), host(ctx, q2))
+    assert bits_equal(host(ctx, s), host(ctx, s2))
+    # oracle composition (its expf may differ from the GPU's by an ulp)
+    gc, gs = oracle.weight_quantize(graw, n, k, 4)
+    uc, us = oracle.weight_quantize(uraw, n, k, 4)
+    go = oracle.matrix_apply(x, m, gc, gs, n, k, 8, fused=True)
+    uo = oracle.matrix_apply(x, m, uc, us, n, k, 8, fused=True)
+    oq, os_ = oracle.silu_requant(go, uo)
+    assert np.abs(host(ctx, q).astype(np.int32) - oq.astype(np.int32)).max() <= 1
+    assert np.allclose(host(ctx, s), os_, rtol=1e-5)
+    # down_proj consumer of the A8 records equals the oracle's grouped product
+    draw = oracle.f32_to_bf16(np.random.default_rng(3).standard_normal((64, n)).astype(np.float32))
+    down = ctx.quantize(dev(draw), rocm.BF16, 64, n, 4, 64)
+    yd = empty((m, 64), torch.float32)
+    ctx.linear_q8(down, q, s, m, yd)
+    dq, dsc = oracle.weight_quantize(draw, 64, n, 4)
+    want = oracle.grouped_gemm(host(ctx, q), host(ctx, s), m, dq, dsc, 64, n, fused=True)
+    assert bits_equal(host(ctx, yd), want)
+
+
+# ---- W4A16 ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("m", [1, 4, 8])
+def test_config2_gemv_vs_closed_form(ctx, oracle, m):
+    """f16 x N(0,1) seed 0, K = N = 4096, W N(0,0.02) seed 1, g32/f16."""
+    torch = pytest.importorskip("torch")
+    k = n = 4096
+    x = np.random.default_rng(0).standard_normal((m, k)).astype(np.float32)
+    wf = (np.random.default_rng(1).standard_normal((n, k)) * 0.02).astype(np.float32)
+    packed = oracle.pack_g32_f16(wf, n, k)
+    w = ctx.upload(packed, rocm.Q4_G32_F16, n, k)
+    xh = oracle.f32_to_f16_bits(x)
+    y = empty((m, n), torch.float32)
+    ctx.linear(w, dev(xh.view(np.float16)), rocm.F16, m, y, rocm.W4A16)
+    got = host(ctx, y)
+    want = oracle.w4a16(xh, m, k, oracle.unpack_g32_f16(packed).reshape(n, k), n)
+    assert np.abs(got - want).max() <= MAX_ABS
+    assert cosine(got, want) >= MIN_COS
+    # every GEMV variant keeps the reduction order: bitwise equal outputs
+    for name in ("w8u4", "w4u4", "w4u8", "w2u8"):
+        ctx.select_variant("gemv", name)
+        y2 = empty((m, n), torch.float32)
+        ctx.linear(w, dev(xh.view(np.float16)), rocm.F16, m, y2, rocm.W4A16)
+        assert bits_equal(host(ctx, y2), got), name
+    ctx.select_variant("gemv", "w8u4")
+
+
+@pytest.mark.parametrize("layout", [rocm.Q4_G32_F16, rocm.Q4_G64_F32])
+@pytest.mark.parametrize("m,k,n", [(17, 256, 48), (256, 1024, 1024), (1000, 512, 1536), (33, 4096, 272)])
+def test_large_m_gemm_vs_closed_form(ctx, oracle, layout, m, k, n):
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(m + k + n)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    wf = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    if layout == rocm.Q4_G32_F16:
+        packed = oracle.pack_g32_f16(wf, n, k)
+        deq = oracle.unpack_g32_f16(packed).reshape(n, k)
+    else:
+        packed = oracle.pack_g64(oracle.f32_to_bf16(wf), n, k, 4)
+        deq = oracle.unpack_g64(packed, 4).reshape(n, k)
+    w = ctx.upload(packed, layout, n, k)
+    xh = oracle.f32_to_f16_bits(x)
+    want = oracle.w4a16(xh, m, k, deq, n)
+    outs = []
+    for name in ("256x128w2x2", "128x128w2x2", "128x64w2x2"):
+        ctx.select_variant("gemm_w4a16", name)
+        y = empty((m, n), torch.float32)
+        ctx.linear(w, dev(xh.view(np.float16)), rocm.F16, m, y, rocm.W4A16)
+        got = host(ctx, y)
+        assert np.abs(got - want).max() <= MAX_ABS, name
+        assert cosine(got, want) >= MIN_COS, name
+        outs.append(got)
+    ctx.select_variant("gemm_w4a16", "256x128w2x2")
+    for o in outs[1:]:
+        assert bits_equal(o, outs[0])
+
+
+def test_config5_prefill_rows_vs_fp32(ctx, oracle):
+    """BASELINE config 5 at full size (M=16384, K=4096, N=14336); a row sample is
+    checked against an fp32 product of the dequantized weights."""
+    torch = pytest.importorskip("torch")
+    m, k, n = 16384, 4096, 14336
+    g = torch.Generator(device="cuda").manual_seed(1)
+    wdev = torch.randn((n, k), generator=g, device="cuda", dtype=torch.float32) * 0.02
+    w = ctx.quantize(wdev, rocm.F32, n, k, 4, 32)
+    del wdev
+    x = torch.randn((m, k), generator=torch.Generator(device="cuda").manual_seed(0), device="cuda").half()
+    torch.cuda.synchronize()
+    y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    ctx.linear(w, x, rocm.F16, m, y, rocm.W4A16)
+    deq = torch.empty((n, k), dtype=torch.float32, device="cuda")
+    ctx.dequant(w, deq)
+    ctx.sync()
+    rows = torch.arange(0, m, 61, device="cuda")
+    ref = (x[rows].double() @ deq.double().T).float()
+    got = y[rows]
+    err = (got - ref).abs().max().item()
+    cos = torch.nn.functional.cosine_similarity(got.double().reshape(1, -1), ref.double().reshape(1, -1)).item()
+    assert err <= MAX_ABS and cos >= MIN_COS, (err, cos)
+    assert torch.isfinite(y).all().item()
+
+
+# ---- per-row int8 ----------------------------------------------------------------------
+
+@pytest.mark.parametrize("m,n,k", GOLDEN["q4_raw_check_shapes"]["mnk"] + [[77, 45, 100], [1, 1, 4], [130, 260, 4100]])
+def test_i8_gemm_exact(ctx, oracle, m, n, k):
+    """webgpu/q4.rs:476-501 known answers plus ragged shapes: raw int32 and the
+    f32 epilogue are bit-exact; every variant agrees."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(m * n + k)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal((n, k)).astype(np.float32)
+    qa, sa, _ = oracle.i8_quantize_rows(a, m, k)
+    qb, sb, _ = oracle.i8_quantize_rows(b, n, k)
+    raw, yf = oracle.i8_gemm(qa, sa, m, qb, sb, n, k, threads=8)
+    for name in ("128x128w2x2", "256x128w2x2", "64x64w2x2"):
+        ctx.select_variant("i8_gemm", name)
+        r = empty((m, n), torch.int32)
+        y = empty((m, n), torch.float32)
+        da, db, dsa, dsb = dev(qa), dev(qb), dev(sa), dev(sb)
+        ctx.i8_gemm(da, dsa, m, db, dsb, n, k, r, raw=True)
+        ctx.i8_gemm(da, dsa, m, db, dsb, n, k, y, raw=False)
+        assert np.array_equal(host(ctx, r), raw), name
+        assert bits_equal(host(ctx, y), yf), name
+    ctx.select_variant("i8_gemm", "128x128w2x2")
+
+
+def test_config4_int8_full_size(ctx, oracle):
+    """W f32 [4096 x 4096] N(0,0.02) per-channel, A f32
+    [8192 x 4096] N(0,1) per-token; quantized on the GPU (bit-exact with the
+    oracle) and the i32 accumulators bit-exact on a row sample."""
+    torch = pytest.importorskip("torch")
+    m, n, k = 8192, 4096, 4096
+    a = np.random.default_rng(0).standard_normal((m, k)).astype(np.float32)
+    b = (np.random.default_rng(1).standard_normal((n, k)) * 0.02).astype(np.float32)
+    qa = empty((m, k), torch.int8)
+    sa = empty(m, torch.float32)
+    qb = empty((n, k), torch.int8)
+    sb = empty(n, torch.float32)
+    ctx.i8_quantize_rows(dev(a), m, k, qa, sa)
+    ctx.i8_quantize_rows(dev(b), n, k, qb, sb)
+    oqa, osa, _ = oracle.i8_quantize_rows(a, m, k)
+    oqb, osb, _ = oracle.i8_quantize_rows(b, n, k)
+    assert np.array_equal(host(ctx, qa), oqa) and np.array_equal(host(ctx, qb), oqb)
+    assert bits_equal(host(ctx, sa), osa) and bits_equal(host(ctx, sb), osb)
+    r = empty((m, n), torch.int32)
+    ctx.i8_gemm(qa, sa, m, qb, sb, n, k, r, raw=True)
+    rows = np.arange(0, m, 97)
+    want, _ = oracle.i8_gemm(oqa[rows], osa[rows], rows.size, oqb, osb, n, k, threads=16, scaled=False)
+    assert np.array_equal(host(ctx, r)[rows], want)
