@@ -60,6 +60,12 @@ struct Weight {
 
 __device__ __forceinline__ half8_t as_half8(uint4_t v) { return __builtin_bit_cast(half8_t, v); }
 
+// Bit casts of one 32-bit word. Arguments are taken by value: applying
+// __builtin_bit_cast to an ext_vector element directly reads element 0.
+__device__ __forceinline__ float word_as_float(uint32_t w) { return __builtin_bit_cast(float, w); }
+__device__ __forceinline__ half2_t word_as_half2(uint32_t w) { return __builtin_bit_cast(half2_t, w); }
+__device__ __forceinline__ uint32_t half2_as_word(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
+
 // 8 packed (code+8) nibbles in the tile16x128 order -> 8 exact f16 codes.
 __device__ __forceinline__ uint4_t nibbles_to_half8(uint32_t w) {
     const half2_t bias = {(half_t)1032.0f, (half_t)1032.0f};

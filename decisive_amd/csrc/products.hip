@@ -225,7 +225,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const uint8_t *__restr
                         if (G32)
                             scale = f16_bits_to_float((sc[u][s >> 1] >> (16 * (s & 1))) & 0xffffu);
                         else
-                            scale = __builtin_bit_cast(float, sc[u][s >> 1]);
+                            scale = word_as_float(sc[u][s >> 1]);
 #pragma unroll
                         for (int v = 0; v < 4; v++) acc[v] = __builtin_fmaf(p[v], scale, acc[v]);
                     }
@@ -338,11 +338,11 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_w4a16_kernel(
                 if (G32)
                     sh = __builtin_bit_cast(half_t, (unsigned short)((ps[nt][s >> 1] >> (16 * (s & 1))) & 0xffffu));
                 else
-                    sh = (half_t)__builtin_bit_cast(float, ps[nt][s >> 1]);
+                    sh = (half_t)word_as_float(ps[nt][s >> 1]);
                 half2_t s2 = {sh, sh};
                 uint4_t cw = nibbles_to_half8(pc[nt][s]);
 #pragma unroll
-                for (int p = 0; p < 4; p++) cw[p] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, cw[p]) * s2);
+                for (int p = 0; p < 4; p++) cw[p] = half2_as_word(word_as_half2(cw[p]) * s2);
                 bf[nt][s] = as_half8(cw);
             }
         }

@@ -10,6 +10,7 @@
 // hashes the device, the tuning version and the kernel sources (:279-294); a
 // cached choice is only re-checked for equality (:498-513). Inputs are hashed
 // packed words with small positive scales (:847-852).
+#include <ctype.h>
 #include <string.h>
 
 #include <algorithm>
@@ -126,14 +127,21 @@ struct Family {
     int m, n, k;  // tuning shape
 };
 
-// Extracts "name":"value" from a flat JSON object (the tuner's own output).
+// The string value of the first `"name": "value"` member in s (the tuner's own
+// output, possibly re-serialized with whitespace around the colon).
 std::string json_field(const std::string &s, const std::string &name) {
-    std::string pat = "\"" + name + "\":\"";
-    size_t at = s.find(pat);
-    if (at == std::string::npos) return "";
-    at += pat.size();
-    size_t end = s.find('"', at);
-    return end == std::string::npos ? "" : s.substr(at, end - at);
+    const std::string pat = "\"" + name + "\"";
+    for (size_t at = s.find(pat); at != std::string::npos; at = s.find(pat, at + 1)) {
+        size_t p = at + pat.size();
+        while (p < s.size() && isspace((unsigned char)s[p])) p++;
+        if (p >= s.size() || s[p] != ':') continue;
+        p++;
+        while (p < s.size() && isspace((unsigned char)s[p])) p++;
+        if (p >= s.size() || s[p] != '"') continue;
+        size_t end = s.find('"', p + 1);
+        return end == std::string::npos ? "" : s.substr(p + 1, end - p - 1);
+    }
+    return "";
 }
 
 }  // namespace

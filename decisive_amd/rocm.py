@@ -105,6 +105,13 @@ def load():
     """Loads the in-tree library; raises when it has not been built."""
     global _lib
     if _lib is None:
+        try:
+            # torch wheels bundle their own libamdhip64.so.7; loading torch first
+            # makes this library bind to that same runtime (one HIP runtime per
+            # process). Without torch the library uses /opt/rocm's runtime.
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         if not LIB_PATH.exists():
             raise RuntimeError(f"{LIB_PATH} is missing: run decisive_amd/build.py (no CPU fallback exists)")
         lib = ctypes.CDLL(str(LIB_PATH))

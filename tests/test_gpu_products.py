@@ -208,7 +208,7 @@ def test_config2_gemv_vs_closed_form(ctx, oracle, m):
 
 
 @pytest.mark.parametrize("layout", [rocm.Q4_G32_F16, rocm.Q4_G64_F32])
-@pytest.mark.parametrize("m,k,n", [(17, 256, 48), (256, 1024, 1024), (1000, 512, 1536), (33, 4096, 272)])
+@pytest.mark.parametrize("m,k,n", [(3, 512, 80), (17, 256, 48), (256, 1024, 1024), (1000, 512, 1536), (33, 4096, 272)])
 def test_large_m_gemm_vs_closed_form(ctx, oracle, layout, m, k, n):
     torch = pytest.importorskip("torch")
     rng = np.random.default_rng(m + k + n)
