@@ -7,8 +7,9 @@ A step is one pass of the activations through WEIGHT_COPIES distinct Q4
 [4096 x 4096] weights (one GEMV launch each, replayed as one HIP graph), so
 the 256 MB Infinity Cache cannot serve repeated weights and the number is an
 HBM number. `value` is whole-job GB/s of algorithmic bytes over the timed
-region; `roofline` prices the GEMV kernel's own average duration (HIP events
-around each launch on the library stream) against 8 TB/s.
+region; `roofline` prices the GEMV kernel's average launch duration (the
+timed region, HIP events on the library stream, over the launch count)
+against 8 TB/s.
 
 Secondary configurations (int8 GEMM, Q4 prefill GEMM, encoder forward) are
 reported under "secondary" in the same JSON line.
@@ -205,13 +206,14 @@ def main():
         torch.cuda.synchronize()
         wall = time.perf_counter() - wall0
         total_ms = t0.elapsed_time(t1)
-        # the GEMV kernel's own duration: event pairs around single launches
-        kernel_ms = event_avg_ms(torch, side, lambda r: ctx.linear(weights[r % WEIGHT_COPIES], x, rocm.F16, M_ROWS,
-                                                                    y[r % WEIGHT_COPIES], rocm.W4A16), 512)
     ctx.set_stream(None)
 
     per_launch = gemv_bytes(M_ROWS, K_DIM, N_DIM)
     launches = args.steps * WEIGHT_COPIES
+    # The graph replays the GEMV launches back to back on one stream, so the
+    # timed region divided by the launch count is the kernel's average launch
+    # duration (what rocprofv3's kernel trace reports per dispatch).
+    kernel_ms = total_ms / launches
     value = launches * per_launch / (total_ms * 1e-3) / 1e9
     achieved = per_launch / (kernel_ms * 1e-3) / 1e9
     y_host = y[0].float().cpu().numpy()

@@ -8,7 +8,7 @@
 //  gemv      : W4A16 for M <= 16 rows, HBM bound. Each lane streams one 128-bit
 //              word of packed codes per 128-k block; codes become exact f16 and
 //              feed v_mfma_f32_16x16x32_f16; per-32-run scales are applied to the
-//              f32 partials. K is split into 8 fixed chunks reduced in order, so
+//              f32 partials. K is split into 16 fixed chunks reduced in order, so
 //              every variant is bitwise equal.
 //  gemm      : W4A16 for large M, MFMA bound. The activation tile is staged in
 //              LDS; each wave dequantizes its weight fragments (code * scale in
@@ -173,80 +173,158 @@ __global__ __launch_bounds__(256) void mlp_requant_kernel(
 // ============================================================================
 // W4A16 skinny-M GEMV
 // ============================================================================
+//
+// HBM bound: a launch is one pass over the packed weight, so its time is the
+// load latency plus whatever runs after the last bytes land. The kernel is
+// shaped so that every load of a wave is in flight at once and little work
+// follows them:
+//  - one block per 16-row tile, K split into kGemvChunks fixed chunks; a wave
+//    owns PW chunks and walks them two k-blocks at a time;
+//  - per sub-step a wave issues ONE full-width load for its activation rows
+//    and the two scale records (staged through the wave's own LDS slice), and
+//    one 16-byte code load per k-block, with no branch or select between them
+//    (out-of-range lanes read a zero page or a clamped valid block), so the
+//    three requests leave back to back;
+//  - codes become exact f16 with 9 VALU ops per 8 codes (v_and_or with the
+//    1024 exponent, one shift per word, packed add/fma to remove the bias);
+//  - only the MFMA output rows that hold live activation rows get the scale
+//    FMA; chunk partials are summed in chunk order by wave 0.
+// Every output is  sum_c ( sum_{kb in c} sum_s fma(p_s, scale_s, .) ), chunks
+// added in order, whatever WAVES or MPAD is, so all variants are bitwise equal.
 
-constexpr int kChunks = 8;  // fixed K split: reduction order is variant independent
+constexpr int kGemvChunks = 16;
 
-template <int WAVES, int UNROLL, bool G32>
+// Read by staged lanes whose unit lies outside the activations or scales.
+__device__ __align__(16) uint4_t g_zero_unit[1];
+
+__device__ __forceinline__ uint32_t and_or(uint32_t v, uint32_t mask, uint32_t bits) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(v), "s"(mask), "v"(bits));
+    return r;
+}
+
+// 8 (code + 8) nibbles in the tile16x128 order -> 8 exact f16 codes.
+// Pairs at bits (0,16) and (8,24) give 1024 + nib; pairs at (4,20), (12,28)
+// give 1024 + 16*nib, turned into nib - 8 by one exact fma (x/16 - 72).
+__device__ __forceinline__ uint4_t unpack_codes(uint32_t w, uint32_t magic) {
+    const half2_t bias = {(half_t)-1032.0f, (half_t)-1032.0f};
+    const half2_t sixteenth = {(half_t)0.0625f, (half_t)0.0625f};
+    const half2_t bias16 = {(half_t)-72.0f, (half_t)-72.0f};
+    const uint32_t w8 = w >> 8;
+    uint4_t out;
+    out[0] = half2_as_word(word_as_half2(and_or(w, 0x000F000Fu, magic)) + bias);
+    out[1] = half2_as_word(__builtin_elementwise_fma(word_as_half2(and_or(w, 0x00F000F0u, magic)), sixteenth, bias16));
+    out[2] = half2_as_word(word_as_half2(and_or(w8, 0x000F000Fu, magic)) + bias);
+    out[3] = half2_as_word(__builtin_elementwise_fma(word_as_half2(and_or(w8, 0x00F000F0u, magic)), sixteenth, bias16));
+    return out;
+}
+
+template <int MPAD>
+struct GemvShape {
+    static constexpr int LIVE = MPAD < 4 ? MPAD : 4;     // MFMA output rows per lane that are live
+    static constexpr int XROW = 512 + 16;                // staged activation row: 256 f16 + pad
+    static constexpr int SLICE = MPAD * XROW + 256;      // per wave: rows, then 2 scale records
+    static constexpr int UNITS = MPAD * 32 + 16;         // 16-byte units staged per sub-step
+    static constexpr int LOADS = (UNITS + 63) / 64;
+};
+
+template <int WAVES, int MPAD, bool G32>
 __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const uint8_t *__restrict__ codes,
                                                           const uint8_t *__restrict__ scales,
                                                           const half_t *__restrict__ x, int m,
                                                           int k, int n, int kbs,
                                                           float *__restrict__ y) {
-    constexpr int PER_WAVE = kChunks / WAVES;
-    __shared__ float4_t red[kChunks][64];
+    using S = GemvShape<MPAD>;
+    constexpr int PW = kGemvChunks / WAVES;
+    extern __shared__ __align__(16) uint8_t lds[];
     const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
-    const int t = blockIdx.x, mt = blockIdx.y;
+    const int t = blockIdx.x;
     const int qd = lane / 16, i = lane % 16, j = i;
-    const int arow = mt * 16 + i;
-    const bool arow_ok = arow < m;
-    const half_t *xrow = x + (size_t)arow * k;
+    uint8_t *slice = lds + wave * S::SLICE;
     const uint8_t *cbase = codes + q4_lane(t, 0, kbs, qd, j);
-    const uint8_t *sbase = scales + ((size_t)t * kbs * 16 + j) * 8;
-    const int per = (kbs + kChunks - 1) / kChunks;
-    const half8_t hz = {};
+    const int per = (kbs + kGemvChunks - 1) / kGemvChunks;
+    const uint32_t magic = 0x64006400u;
     const float4_t fz = {0.f, 0.f, 0.f, 0.f};
+    float part[PW][S::LIVE];
+
 #pragma unroll
-    for (int cc = 0; cc < PER_WAVE; cc++) {
-        const int chunk = wave * PER_WAVE + cc;
+    for (int cc = 0; cc < PW; cc++) {
+        const int chunk = wave * PW + cc;
         const int kb0 = chunk * per;
         const int kb1 = min(kbs, kb0 + per);
-        float4_t acc = fz;
-        for (int kb = kb0; kb < kb1; kb += UNROLL) {
-            uint4_t c[UNROLL];
-            uint2_t sc[UNROLL];
+        float acc[S::LIVE];
 #pragma unroll
-            for (int u = 0; u < UNROLL; u++) {
-                if (kb + u < kb1) {
-                    c[u] = __builtin_nontemporal_load((const uint4_t *)(cbase + (size_t)(kb + u) * 1024));
-                    sc[u] = *(const uint2_t *)(sbase + (size_t)(kb + u) * 128);
+        for (int v = 0; v < S::LIVE; v++) acc[v] = 0.0f;
+        uint4_t st[S::LOADS], c0, c1;
+        auto issue = [&](int kb) {
+#pragma unroll
+            for (int L = 0; L < S::LOADS; L++) {
+                const int u = L * 64 + lane;
+                const uint8_t *p = (const uint8_t *)g_zero_unit;
+                if (u < MPAD * 32) {
+                    const int r = u / 32, kk = kb * 128 + (u % 32) * 8;
+                    if (r < m && kk < k && kb + (u % 32) / 16 < kb1) p = (const uint8_t *)(x + (size_t)r * k + kk);
+                } else if (u < S::UNITS) {
+                    const int q = u - MPAD * 32, kbq = kb + q / 8;
+                    if (kbq < kb1) p = scales + ((size_t)t * kbs + kbq) * 128 + (q % 8) * 16;
                 }
+                st[L] = *(const uint4_t *)p;
             }
+            // a k-block past the chunk end reads a valid block: its activations
+            // and scales are zero, so it adds exactly 0
+            c0 = __builtin_nontemporal_load((const uint4_t *)(cbase + (size_t)(kb < kb1 ? kb : kb0) * 1024));
+            c1 = __builtin_nontemporal_load((const uint4_t *)(cbase + (size_t)(kb + 1 < kb1 ? kb + 1 : kb0) * 1024));
+        };
+        if (kb0 < kb1) issue(kb0);
+        for (int kb = kb0; kb < kb1; kb += 2) {
 #pragma unroll
-            for (int u = 0; u < UNROLL; u++) {
-                if (kb + u < kb1) {
+            for (int L = 0; L < S::LOADS; L++) {
+                const int u = L * 64 + lane;
+                if (u < MPAD * 32) *(uint4_t *)(slice + (u / 32) * S::XROW + (u % 32) * 16) = st[L];
+                else if (u < S::UNITS) *(uint4_t *)(slice + MPAD * S::XROW + (u - MPAD * 32) * 16) = st[L];
+            }
+            const uint4_t cw[2] = {c0, c1};
+            if (kb + 2 < kb1) issue(kb + 2);
 #pragma unroll
-                    for (int s = 0; s < 4; s++) {
-                        half8_t b = as_half8(nibbles_to_half8(c[u][s]));
-                        const int kk = (kb + u) * 128 + s * 32 + qd * 8;
-                        half8_t a = hz;
-                        if (arow_ok && kk < k) a = *(const half8_t *)(xrow + kk);
-                        float4_t p = mfma_f16(a, b, fz);
-                        float scale;
-                        if (G32)
-                            scale = f16_bits_to_float((sc[u][s >> 1] >> (16 * (s & 1))) & 0xffffu);
-                        else
-                            scale = word_as_float(sc[u][s >> 1]);
+            for (int uu = 0; uu < 2; uu++) {
+                const uint2_t sc = *(const uint2_t *)(slice + MPAD * S::XROW + uu * 128 + j * 8);
 #pragma unroll
-                        for (int v = 0; v < 4; v++) acc[v] = __builtin_fmaf(p[v], scale, acc[v]);
-                    }
+                for (int s = 0; s < 4; s++) {
+                    half8_t a = half8_t{};
+                    if (i < MPAD) a = *(const half8_t *)(slice + i * S::XROW + (uu * 128 + s * 32 + qd * 8) * 2);
+                    const float4_t p = mfma_f16(a, as_half8(unpack_codes(cw[uu][s], magic)), fz);
+                    float scale;
+                    if (G32)
+                        scale = f16_bits_to_float((sc[s >> 1] >> (16 * (s & 1))) & 0xffffu);
+                    else
+                        scale = word_as_float(sc[s >> 1]);
+#pragma unroll
+                    for (int v = 0; v < S::LIVE; v++) acc[v] = __builtin_fmaf(p[v], scale, acc[v]);
                 }
             }
         }
-        red[chunk][lane] = acc;
+#pragma unroll
+        for (int v = 0; v < S::LIVE; v++) part[cc][v] = acc[v];
     }
+    // chunk partials replace the wave's staged data (each wave only reuses its own slice)
+    float *mine = (float *)slice;
+#pragma unroll
+    for (int cc = 0; cc < PW; cc++)
+#pragma unroll
+        for (int v = 0; v < S::LIVE; v++) mine[(cc * S::LIVE + v) * 64 + lane] = part[cc][v];
     __syncthreads();
-    if (wave != 0) return;
-    float4_t total = red[0][lane];
+    if (wave != 0 || qd * 4 >= MPAD) return;
+    float total[S::LIVE];
 #pragma unroll
-    for (int cidx = 1; cidx < kChunks; cidx++) {
-        float4_t r = red[cidx][lane];
+    for (int c = 0; c < kGemvChunks; c++) {
+        const float *src = (const float *)(lds + (c / PW) * S::SLICE) + (c % PW) * S::LIVE * 64;
 #pragma unroll
-        for (int v = 0; v < 4; v++) total[v] = __fadd_rn(total[v], r[v]);
+        for (int v = 0; v < S::LIVE; v++) total[v] = c == 0 ? src[v * 64 + lane] : __fadd_rn(total[v], src[v * 64 + lane]);
     }
     const int col = t * 16 + j;
 #pragma unroll
-    for (int v = 0; v < 4; v++) {
-        int r = mt * 16 + qd * 4 + v;
+    for (int v = 0; v < S::LIVE; v++) {
+        const int r = qd * 4 + v;
         if (r < m && col < n) y[(size_t)r * n + col] = total[v];
     }
 }
@@ -516,20 +594,41 @@ inline unsigned cdiv(size_t a, size_t b) { return (unsigned)((a + b - 1) / b); }
 
 // ---- variant tables -------------------------------------------------------------
 
-const char *const kGemvNames[] = {"w8u4", "w4u4", "w4u8", "w2u8"};
+const char *const kGemvNames[] = {"w16", "w8"};
 const char *const kGemmNames[] = {"256x128w2x2", "128x128w2x2", "128x64w2x2"};
 const char *const kI8Names[] = {"128x128w2x2", "256x128w2x2", "64x64w2x2"};
 const char *const kGroupedNames[] = {"wave16x16"};
 
-template <int W, int U>
+template <int W, int MPAD, bool G32>
+void gemv_launch_one(const Weight &w, const half_t *x, int m, float *y, hipStream_t s) {
+    using S = GemvShape<MPAD>;
+    const size_t lds = (size_t)W * S::SLICE;
+    static bool configured[64] = {};  // the LDS limit is a per-device function attribute
+    int dev = 0;
+    hipGetDevice(&dev);
+    if (dev >= 0 && dev < 64 && !configured[dev]) {
+        hipFuncSetAttribute((const void *)gemv_kernel<W, MPAD, G32>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        configured[dev] = true;
+    }
+    hipLaunchKernelGGL((gemv_kernel<W, MPAD, G32>), dim3(w.tiles()), dim3(W * 64), lds, s, w.codes, w.scales, x,
+                       m, w.cols, w.rows, w.kblocks(), y);
+}
+
+template <int W, bool G32>
+void gemv_launch_m(const Weight &w, const half_t *x, int m, float *y, hipStream_t s) {
+    if (m <= 1) gemv_launch_one<W, 1, G32>(w, x, m, y, s);
+    else if (m <= 2) gemv_launch_one<W, 2, G32>(w, x, m, y, s);
+    else if (m <= 4) gemv_launch_one<W, 4, G32>(w, x, m, y, s);
+    else if (m <= 8) gemv_launch_one<W, 8, G32>(w, x, m, y, s);
+    else gemv_launch_one<W, 16, G32>(w, x, m, y, s);
+}
+
+template <int W>
 void gemv_launch(const Weight &w, const half_t *x, int m, float *y, hipStream_t s) {
-    dim3 grid(w.tiles(), cdiv(m, 16));
     if (w.kind == WeightKind::Q4G32)
-        hipLaunchKernelGGL((gemv_kernel<W, U, true>), grid, dim3(W * 64), 0, s, w.codes, w.scales, x, m,
-                           w.cols, w.rows, w.kblocks(), y);
+        gemv_launch_m<W, true>(w, x, m, y, s);
     else
-        hipLaunchKernelGGL((gemv_kernel<W, U, false>), grid, dim3(W * 64), 0, s, w.codes, w.scales, x, m,
-                           w.cols, w.rows, w.kblocks(), y);
+        gemv_launch_m<W, false>(w, x, m, y, s);
 }
 
 template <int BM, int BN, int WM, int WN, int EPI>
@@ -558,7 +657,7 @@ void gemm_dispatch(const Weight &w, const half_t *x, int m, void *y, const half_
 
 int variant_count(const char *family) {
     std::string f(family);
-    if (f == "gemv") return 4;
+    if (f == "gemv") return 2;
     if (f == "gemm_w4a16") return 3;
     if (f == "i8_gemm") return 3;
     if (f == "grouped") return 1;
@@ -606,12 +705,10 @@ void launch_w4a16(const Weight &w, const half_t *x, int m, float *y, int gemv_va
                   int gemm_variant, hipStream_t s) {
     if (m == 0) return;
     if (m <= 16) {
-        switch (gemv_variant) {
-            case 1: gemv_launch<4, 4>(w, x, m, y, s); break;
-            case 2: gemv_launch<4, 8>(w, x, m, y, s); break;
-            case 3: gemv_launch<2, 8>(w, x, m, y, s); break;
-            default: gemv_launch<8, 4>(w, x, m, y, s); break;
-        }
+        if (gemv_variant == 1)
+            gemv_launch<8>(w, x, m, y, s);
+        else
+            gemv_launch<16>(w, x, m, y, s);
     } else {
         gemm_dispatch<0>(w, x, m, y, nullptr, gemm_variant, s);
     }

@@ -436,6 +436,7 @@ int32_t dz_linear(dz_ctx *ctx, const dz_weight *w, const void *x, int32_t x_dtyp
         if (x_dtype != DZ_F16) return fail(ctx, DZ_INVALID_PARAMETERS, "W4A16 takes f16 activations");
         if (w->w.bits != 4) return fail(ctx, DZ_INVALID_PARAMETERS, "W4A16 needs a Q4 weight");
         if (w->w.cols % 8 != 0) return fail(ctx, DZ_INVALID_PARAMETERS, "W4A16 needs cols % 8 == 0");
+        if (((uintptr_t)x & 15) != 0) return fail(ctx, DZ_INVALID_PARAMETERS, "W4A16 activations must be 16-byte aligned");
         if (m == 0) return DZ_OK;
         dz::launch_w4a16(w->w, (const dz::half_t *)x, (int)m, y, variant(ctx, "gemv"),
                          variant(ctx, "gemm_w4a16"), ctx->stream);

@@ -199,12 +199,53 @@ def test_config2_gemv_vs_closed_form(ctx, oracle, m):
     assert np.abs(got - want).max() <= MAX_ABS
     assert cosine(got, want) >= MIN_COS
     # every GEMV variant keeps the reduction order: bitwise equal outputs
-    for name in ("w8u4", "w4u4", "w4u8", "w2u8"):
+    for name in ("w16", "w8"):
         ctx.select_variant("gemv", name)
         y2 = empty((m, n), torch.float32)
         ctx.linear(w, dev(xh.view(np.float16)), rocm.F16, m, y2, rocm.W4A16)
         assert bits_equal(host(ctx, y2), got), name
-    ctx.select_variant("gemv", "w8u4")
+    ctx.select_variant("gemv", "w16")
+
+
+@pytest.mark.parametrize("k,n", [(96, 17), (2560, 300), (4160, 33), (8, 1)])
+def test_gemv_ragged_rows_are_independent_of_m(ctx, oracle, k, n):
+    """Skinny path for every row count 1..16: closed form within tolerance, and
+    each output row bitwise equal to the same row computed alone (a row's
+    arithmetic does not depend on how many rows share the launch)."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(k * 31 + n)
+    x = rng.standard_normal((16, k)).astype(np.float32)
+    wf = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    w = ctx.quantize(dev(wf), rocm.F32, n, k, 4, 32)
+    deq = empty((n, k), torch.float32)
+    ctx.dequant(w, deq)
+    deq = host(ctx, deq)
+    xh = oracle.f32_to_f16_bits(x)
+    xd = dev(xh.view(np.float16))
+    want = oracle.w4a16(xh, 16, k, deq, n)
+    alone = []
+    for r in range(16):
+        y1 = empty((1, n), torch.float32)
+        ctx.linear(w, xd[r:r + 1], rocm.F16, 1, y1, rocm.W4A16)
+        alone.append(host(ctx, y1)[0])
+    alone = np.stack(alone)
+    assert np.abs(alone - want).max() <= MAX_ABS
+    for m in (2, 3, 5, 8, 9, 16):
+        y = empty((m, n), torch.float32)
+        ctx.linear(w, xd, rocm.F16, m, y, rocm.W4A16)
+        got = host(ctx, y)
+        assert bits_equal(got, alone[:m]), m
+
+
+def test_w4a16_rejects_misaligned_activations(ctx, oracle):
+    torch = pytest.importorskip("torch")
+    k = n = 64
+    w = ctx.quantize(dev(np.ones((n, k), np.float32) * 0.01), rocm.F32, n, k, 4, 32)
+    buf = empty((2 * k + 8,), torch.float16)
+    y = empty((1, n), torch.float32)
+    with pytest.raises(rocm.DzError) as e:
+        ctx.linear(w, buf.data_ptr() + 2, rocm.F16, 1, y, rocm.W4A16)
+    assert e.value.code == "INVALID_PARAMETERS"
 
 
 @pytest.mark.parametrize("layout", [rocm.Q4_G32_F16, rocm.Q4_G64_F32])
