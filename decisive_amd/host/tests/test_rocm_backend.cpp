@@ -1,0 +1,177 @@
+// test_rocm_backend.cpp -- Model<Rocm> on an MI355X (needs the GPU).
+//
+// The Rocm backend behind the reference's Model<B> contract: predictions
+// equal a direct dz_encoder_forward of the same token ids bit for bit, the
+// embedding-row cache serves repeats without changing results, long inputs
+// are split by maxSequenceTokens rather than truncated, and failures clear
+// the cache (src/inference/mod.rs:240-242).
+#include <cstring>
+#include <vector>
+
+#include "../rocm_backend.hpp"
+#include "harness.hpp"
+
+using namespace decisive;
+
+namespace {
+
+dz_encoder_config small_config() {
+    dz_encoder_config c{};
+    c.layers = 2;
+    c.hidden = 256;
+    c.heads = 4;
+    c.head_dim = 64;
+    c.ffn = 1024;
+    c.vocab = 1000;
+    c.ln_eps = 1e-5f;
+    return c;
+}
+
+TuningOptions no_tuning() {
+    TuningOptions t;
+    t.mode = TuningMode::Off;
+    return t;
+}
+
+std::vector<uint32_t> ids_of(size_t n, uint32_t seed) {
+    std::vector<uint32_t> ids(n);
+    uint32_t s = seed;
+    for (auto &id : ids) {
+        s = s * 1664525u + 1013904223u;
+        id = (s >> 8) % 1000;
+    }
+    return ids;
+}
+
+Request request_of(const std::vector<uint32_t> &ids) {
+    Request r;
+    r.state = Json::array();
+    for (uint32_t id : ids) r.state.push_back(Json((uint64_t)id));
+    r.questions["embedding"] = Json::object();
+    return r;
+}
+
+// Mean-pooled embedding of `ids` through dz_encoder_forward (ids on device).
+std::vector<float> direct(Rocm &rocm, const std::vector<uint32_t> &ids) {
+    dz_ctx *ctx = rocm.context();
+    std::vector<int32_t> as_i32(ids.begin(), ids.end());
+    void *ids_dev = nullptr, *out_dev = nullptr;
+    std::vector<float> out((size_t)rocm.config().hidden);
+    CHECK(dz_alloc(ctx, ids.size() * 4, &ids_dev) == DZ_OK);
+    CHECK(dz_alloc(ctx, out.size() * 4, &out_dev) == DZ_OK);
+    CHECK(dz_copy_h2d(ctx, ids_dev, as_i32.data(), ids.size() * 4) == DZ_OK);
+    CHECK(dz_encoder_forward(ctx, rocm.encoder(), (const int32_t *)ids_dev, 1, ids.size(), (float *)out_dev) == DZ_OK);
+    CHECK(dz_copy_d2h(ctx, out.data(), out_dev, out.size() * 4) == DZ_OK);
+    dz_free(ctx, ids_dev);
+    dz_free(ctx, out_dev);
+    return out;
+}
+
+bool same_bits(const Json &embedding, const std::vector<float> &want) {
+    if (!embedding.is_array() || embedding.size() != want.size()) return false;
+    for (size_t i = 0; i < want.size(); i++) {
+        float got = (float)embedding[i].as_number();
+        if (std::memcmp(&got, &want[i], 4) != 0) return false;
+    }
+    return true;
+}
+
+Model<Rocm> make_model() {
+    auto made = Rocm::create(0, small_config(), 7, no_tuning());
+    if (!made.ok()) {
+        fprintf(stderr, "Rocm::create failed: %s\n", made.error().to_string().c_str());
+        std::exit(2);
+    }
+    return Model<Rocm>(made.take());
+}
+
+}  // namespace
+
+TEST(rocm_capabilities_and_parameters) {
+    Model<Rocm> model = make_model();
+    Capabilities c = model.capabilities();
+    CHECK_EQ(c.model, std::string("pplx-flash"));
+    CHECK_EQ(c.backend, std::string("rocm"));
+    CHECK(c.has_cache("embedding") && !c.has_cache("prefix"));
+    CHECK_EQ(c.tuning, std::string("auto"));
+    PplxParameters zero;
+    zero.max_sequence_tokens = 0;
+    auto r = model.predict(request_of({1, 2}), &zero, nullptr, Cancellation{});
+    CHECK(!r.ok() && r.error().code == "INVALID_PARAMETERS");
+    CacheOptions prefix;
+    prefix.require_prefix = true;
+    CHECK_EQ(model.create_cache(prefix).error().code, std::string("UNSUPPORTED_CACHE"));
+}
+
+TEST(rocm_predict_equals_direct_forward_and_cache_reuse_is_exact) {
+    Model<Rocm> model = make_model();
+    auto cache = model.create_cache(CacheOptions{});
+    CHECK(cache.ok());
+    std::vector<uint32_t> ids = ids_of(77, 3);
+    ids[5] = ids[9];  // a repeated token
+    auto first = model.predict(request_of(ids), nullptr, &cache.value(), Cancellation{});
+    CHECK(first.ok());
+    if (!first.ok()) return;
+    CHECK_EQ(first.value().backend, std::string("rocm"));
+    CHECK_EQ(first.value().response["tokens"], Json(77));
+    CHECK_EQ(first.value().response["chunks"], Json(1));
+    std::vector<float> want = direct(model.backend(), ids);
+    CHECK(same_bits(first.value().response["embeddings"][0], want));
+    uint64_t misses = cache.value().state().misses();
+    auto second = model.predict(request_of(ids), nullptr, &cache.value(), Cancellation{});
+    CHECK(second.ok());
+    CHECK_EQ(cache.value().state().misses(), misses);  // every row served from the cache
+    CHECK(cache.value().state().hits() > 0);
+    CHECK(second.ok() && second.value().response == first.value().response);
+}
+
+TEST(rocm_splits_long_inputs_by_max_sequence_tokens) {
+    Model<Rocm> model = make_model();
+    PplxParameters p;
+    p.max_sequence_tokens = 128;
+    std::vector<uint32_t> ids = ids_of(300, 11);
+    auto r = model.predict(request_of(ids), &p, nullptr, Cancellation{});
+    CHECK(r.ok());
+    if (!r.ok()) return;
+    CHECK_EQ(r.value().response["chunks"], Json(3));
+    for (size_t c = 0; c < 3; c++) {
+        std::vector<uint32_t> chunk(ids.begin() + c * 128, ids.begin() + std::min<size_t>(300, (c + 1) * 128));
+        CHECK(same_bits(r.value().response["embeddings"][c], direct(model.backend(), chunk)));
+    }
+}
+
+TEST(rocm_failures_clear_the_cache_and_cancellation_is_checked) {
+    Model<Rocm> model = make_model();
+    auto cache = model.create_cache(CacheOptions{});
+    CHECK(model.predict(request_of(ids_of(20, 5)), nullptr, &cache.value(), Cancellation{}).ok());
+    CHECK(cache.value().state().rows() > 0);
+    Request bad = request_of({1, 2, 99999});
+    auto r = model.predict(bad, nullptr, &cache.value(), Cancellation{});
+    CHECK(!r.ok() && r.error().code == "INVALID_REQUEST");
+    CHECK_EQ(cache.value().state().rows(), (size_t)0);
+    Request text;
+    text.state = "not token ids";
+    text.questions["q"] = 1;
+    CHECK_EQ(model.predict(text, nullptr, nullptr, Cancellation{}).error().code, std::string("INVALID_REQUEST"));
+    Cancellation c;
+    c.cancel();
+    CHECK_EQ(model.predict(request_of({1}), nullptr, nullptr, c).error().code, std::string("CANCELLED"));
+    auto batch = model.predict_batch({request_of({1}), bad, request_of({2, 3})}, nullptr, &cache.value(),
+                                     Cancellation{});
+    CHECK(batch.ok());
+    CHECK(batch.value()[0].success() && !batch.value()[1].success() && batch.value()[2].success());
+}
+
+TEST(rocm_tuning_runs_within_budget_and_is_reported) {
+    TuningOptions t;
+    t.budget_ms = 300;
+    auto made = Rocm::create(0, small_config(), 7, t);
+    CHECK(made.ok());
+    if (!made.ok()) return;
+    const Json &tuning = made.value().tuning();
+    CHECK(tuning.is_object());
+    CHECK(tuning["selected"].is_object());
+    CHECK(tuning["selected"]["gemv"].is_string());
+}
+
+int main(int argc, char **argv) { return harness::run_all(argc, argv); }
