@@ -151,7 +151,7 @@ def w4a8_line(torch, ctx, rocm, stream) -> dict:
     for w in ws:
         w.free()
     return {"us_per_product": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
-            "note": "flag reset + activation quantizer + grouped int8 product per product (hip graph)"}
+            "note": "one launch per product: activation quantization inside the grouped kernel (hip graph)"}
 
 
 def secondary(torch, ctx, rocm, stream) -> dict:

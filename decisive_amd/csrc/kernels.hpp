@@ -24,6 +24,9 @@ void launch_export_q4g64(const Weight &w, uint8_t *wire, hipStream_t s);
 // int8.rs:178-202 prepare: q [m x G*64], s [m x G]; sets *bad on non-finite x.
 void launch_act_quantize(const float *x, int m, int k, int bits, int8_t *q, float *sc, int *bad,
                          hipStream_t s);
+// grouped_q4.rs:3-25: the same codes and scales as 17-word records per group.
+void launch_act_quantize_records(const float *x, int m, int k, uint32_t *records, int *bad,
+                                 hipStream_t s);
 // webgpu/int8.rs:107-145.
 void launch_i8_quantize_rows(const float *x, int rows, int k, int8_t *q, float *scales,
                              int32_t *sums, hipStream_t s);
@@ -33,6 +36,16 @@ void launch_fill_i32(int *p, int value, int count, hipStream_t s);
 // Grouped W{4,8}A{8,4}: bit-exact AVX2 order. bad (may be null): NaN outputs.
 void launch_grouped(const Weight &w, const int8_t *q, const float *sx, int m, float *y,
                     const int *bad, int variant, hipStream_t s);
+// Few-row grouped products (any m; one launch, 16 rows per block row):
+//  from f32 x quantized in the kernel (m <= 16 keeps the all-NaN semantics of
+//  a non-finite x; bad_out, may be null, is set when x holds one);
+void launch_grouped_small(const Weight &w, const float *x, int m, int abits, float *y, int *bad_out,
+                          bool project, hipStream_t s);
+//  from int8 codes + f32 scales (bad_in, may be null: NaN outputs when set);
+void launch_grouped_codes(const Weight &w, const int8_t *q, const float *sx, int m, float *y,
+                          const int *bad_in, bool project, hipStream_t s);
+//  from the 17-word A8 records of grouped_q4.rs:3-25.
+void launch_grouped_records(const Weight &w, const uint32_t *records, int m, float *y, hipStream_t s);
 // W4A16: y [m x N] f32 from x f16 [m x K].
 void launch_w4a16(const Weight &w, const half_t *x, int m, float *y, int gemv_variant,
                   int gemm_variant, hipStream_t s);

@@ -87,6 +87,210 @@ __global__ __launch_bounds__(256) void grouped_kernel(const uint8_t *__restrict_
     }
 }
 
+// ============================================================================
+// grouped W{4,8}A{8,4}, few rows (M <= 16 per block row)
+// ============================================================================
+//
+// One block per 16-column tile. The 64-groups are taken in windows of
+// kGvWindow; in a window each of the kGvWaves waves owns kGvSub consecutive
+// groups: it loads their weight codes, weight scales and activation codes
+// (or f32 activations, quantized here with the a4 formula), takes each
+// group's exact int32 dot with one v_mfma_i32_16x16x64_i8 and leaves it in
+// LDS. After a barrier, lane (r, c) folds the window's groups into its output
+// in group order, so the result is the reference's fold whatever the split:
+//   fused   acc = fma(f32(dot), sw*sx, acc)        int8.rs:524-585 (AVX2 rows)
+//   project acc = acc + f32(dot) * (sx*sw)          packed.rs:102-116
+// Activation sources (AMODE): 0 f32 x quantized in the kernel (every block
+// sees all of x, so a non-finite value anywhere makes every output NaN, as
+// int8.rs:170-173 requires); 1 int8 codes + f32 scales (the dz_act_quantize
+// layout); 2 the 17-word records of grouped_q4.rs:3-25.
+
+constexpr int kGvWaves = 16;
+constexpr int kGvSub = 4;
+constexpr int kGvWindow = kGvWaves * kGvSub;
+
+template <int MPAD>
+struct GvShape {
+    static constexpr int ASTRIDE = kGvSub * 64 + 16;           // staged codes per row (+ pad)
+    static constexpr int ACODE = MPAD * ASTRIDE;                // per wave
+    static constexpr int ACODE_ALL = kGvWaves * ACODE;
+    static constexpr int ASX = MPAD * kGvWindow * 4;            // activation scales of a window
+    static constexpr int SW = kGvWindow * 16 * 4;               // weight scales of a window
+    static constexpr int DOTS = kGvWindow * MPAD * 16 * 4;      // int32 group dots of a window
+    static constexpr int BYTES = ACODE_ALL + ASX + SW + DOTS + 16;
+};
+
+template <int BITS, int MPAD, int AMODE, bool PROJECT>
+__global__ __launch_bounds__(kGvWaves * 64) void grouped_gemv_kernel(
+    const uint8_t *__restrict__ codes, const uint8_t *__restrict__ scales, const void *__restrict__ a,
+    const float *__restrict__ sa, int m, int k, int n, int groups, int kbs, int abits,
+    float *__restrict__ y, const int *__restrict__ bad_in, int *__restrict__ bad_out) {
+    using S = GvShape<MPAD>;
+    extern __shared__ __align__(16) uint8_t lds[];
+    float *asx = (float *)(lds + S::ACODE_ALL);
+    float *sw = (float *)(lds + S::ACODE_ALL + S::ASX);
+    int32_t *dots = (int32_t *)(lds + S::ACODE_ALL + S::ASX + S::SW);
+    int *flag = (int *)(lds + S::ACODE_ALL + S::ASX + S::SW + S::DOTS);
+    const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const int t = blockIdx.x, row0 = blockIdx.y * 16;
+    const int qd = lane / 16, i = lane % 16, j = i;
+    uint8_t *acode = lds + wave * S::ACODE;
+    const int fr = threadIdx.x / 16, fc = threadIdx.x % 16;  // fold lane -> output (row, column)
+    const bool folds = threadIdx.x < MPAD * 16;
+    const float limit = abits == 4 ? 7.0f : 127.0f;
+    if (threadIdx.x == 0) *flag = (bad_in != nullptr && *bad_in != 0) ? 1 : 0;
+    float acc = 0.0f;
+    __syncthreads();
+
+    for (int w0 = 0; w0 < groups; w0 += kGvWindow) {
+        const int g0 = w0 + wave * kGvSub;
+        // ---- weight codes: Q4 one 16-byte lane word per k-block (two groups), Q8 one per group
+        constexpr int BLOADS = BITS == 4 ? kGvSub / 2 : kGvSub;
+        uint4_t bq[BLOADS];
+#pragma unroll
+        for (int u = 0; u < BLOADS; u++) {
+            int blk = BITS == 4 ? g0 / 2 + u : g0 + u;
+            blk = blk < kbs ? blk : 0;  // past the end: a valid block whose dots are never folded
+            bq[u] = *(const uint4_t *)(codes + q4_lane(t, blk, kbs, qd, j));
+        }
+        // ---- weight scales of the wave's groups: 256 contiguous bytes, 16 lanes x 16 B
+        uint4_t swv = {0u, 0u, 0u, 0u};
+        const int first_blk = BITS == 4 ? g0 / 2 : g0;
+        const int blk_of_lane = BITS == 4 ? first_blk + lane / 8 : first_blk + lane / 4;
+        if (lane < 16 && blk_of_lane < kbs) swv = *(const uint4_t *)(scales + ((size_t)t * kbs + first_blk) * (BITS == 4 ? 128 : 64) + lane * 16);
+        // ---- activation codes and scales
+        if (AMODE == 0) {
+            const float *x = (const float *)a;
+            float4_t xv[MPAD];
+#pragma unroll
+            for (int r = 0; r < MPAD; r++) {
+                const int row = row0 + r, g = g0 + lane / 16, kk = g * 64 + (lane % 16) * 4;
+                float4_t v = {0.f, 0.f, 0.f, 0.f};
+                if (row < m && g < groups) {
+                    const float *p = x + (size_t)row * k + kk;
+                    if ((k & 3) == 0 && kk + 4 <= k) {
+                        v = *(const float4_t *)p;
+                    } else {
+                        for (int e = 0; e < 4; e++) v[e] = kk + e < k ? p[e] : 0.0f;
+                    }
+                }
+                xv[r] = v;
+            }
+#pragma unroll
+            for (int r = 0; r < MPAD; r++) {
+                float maximum = 0.0f;
+                bool finite = true;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    finite = finite && __builtin_isfinite(xv[r][e]);
+                    maximum = fmaxf(maximum, fabsf(xv[r][e]));
+                }
+                for (int off = 8; off > 0; off >>= 1) maximum = fmaxf(maximum, __shfl_xor(maximum, off, 16));
+                if (!finite) atomicOr(flag, 1);
+                const float scale = fmaxf(__fdiv_rn(maximum, limit), FLT_MIN);
+                const float inverse = __frcp_rn(scale);
+                uint32_t word = 0;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    float q = fminf(fmaxf(__builtin_rintf(__fmul_rn(xv[r][e], inverse)), -limit), limit);
+                    word |= ((uint32_t)(uint8_t)(int8_t)(int)q) << (8 * e);
+                }
+                *(uint32_t *)(acode + r * S::ASTRIDE + (lane / 16) * 64 + (lane % 16) * 4) = word;
+                if (lane % 16 == 0) asx[r * kGvWindow + (g0 - w0) + lane / 16] = scale;
+            }
+        } else if (AMODE == 1) {
+            const int8_t *q = (const int8_t *)a;
+            constexpr int UNITS = MPAD * 16;  // 16-byte units: row, group, quarter
+#pragma unroll
+            for (int L = 0; L < (UNITS + 63) / 64; L++) {
+                const int u = L * 64 + lane;
+                const int r = u / 16, gg = (u % 16) / 4, part = u % 4, row = row0 + r, g = g0 + gg;
+                uint4_t v = {0u, 0u, 0u, 0u};
+                if (u < UNITS && row < m && g < groups) v = *(const uint4_t *)(q + ((size_t)row * groups + g) * 64 + part * 16);
+                if (u < UNITS) *(uint4_t *)(acode + r * S::ASTRIDE + gg * 64 + part * 16) = v;
+            }
+            if (lane < MPAD * kGvSub) {
+                const int r = lane / kGvSub, gg = lane % kGvSub, row = row0 + r, g = g0 + gg;
+                asx[r * kGvWindow + (g0 - w0) + gg] = (row < m && g < groups) ? sa[(size_t)row * groups + g] : 0.0f;
+            }
+        } else {
+            const uint32_t *rec = (const uint32_t *)a;
+            constexpr int WORDS = MPAD * kGvSub * 17;
+#pragma unroll
+            for (int L = 0; L < (WORDS + 63) / 64; L++) {
+                const int u = L * 64 + lane;
+                const int r = u / (kGvSub * 17), gg = (u / 17) % kGvSub, wd = u % 17, row = row0 + r, g = g0 + gg;
+                uint32_t v = 0u;
+                if (u < WORDS && row < m && g < groups) v = rec[((size_t)row * groups + g) * 17 + wd];
+                if (u < WORDS) {
+                    if (wd < 16) *(uint32_t *)(acode + r * S::ASTRIDE + gg * 64 + wd * 4) = v;
+                    else asx[r * kGvWindow + (g0 - w0) + gg] = __builtin_bit_cast(float, v);
+                }
+            }
+        }
+        // weight scales to LDS as sw[group in window][column]
+        if (lane < 16) {
+            if (BITS == 4) {
+                // record (kb, column) holds the f32 scales of groups 2kb and 2kb+1
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const int col = (lane % 8) * 2 + h;
+                    const int gl = g0 - w0 + (lane / 8) * 2;
+                    sw[gl * 16 + col] = word_as_float(swv[h * 2]);
+                    sw[(gl + 1) * 16 + col] = word_as_float(swv[h * 2 + 1]);
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; e++) sw[(g0 - w0 + lane / 4) * 16 + (lane % 4) * 4 + e] = word_as_float(swv[e]);
+            }
+        }
+        // ---- exact group dots
+#pragma unroll
+        for (int gg = 0; gg < kGvSub; gg++) {
+            if (g0 + gg >= groups) break;
+            int4_t av = {0, 0, 0, 0}, bv;
+            if (BITS == 4) {
+                const uint4_t w = bq[gg / 2];
+                const uint2_t lo = nibbles_to_i8(w[(gg % 2) * 2]), hi = nibbles_to_i8(w[(gg % 2) * 2 + 1]);
+                bv = int4_t{(int)lo[0], (int)lo[1], (int)hi[0], (int)hi[1]};
+                if (i < MPAD) {
+                    const uint2_t a0 = *(const uint2_t *)(acode + i * S::ASTRIDE + gg * 64 + qd * 8);
+                    const uint2_t a1 = *(const uint2_t *)(acode + i * S::ASTRIDE + gg * 64 + 32 + qd * 8);
+                    av = int4_t{(int)a0[0], (int)a0[1], (int)a1[0], (int)a1[1]};
+                }
+            } else {
+                bv = __builtin_bit_cast(int4_t, bq[gg]);
+                if (i < MPAD) av = *(const int4_t *)(acode + i * S::ASTRIDE + gg * 64 + qd * 16);
+            }
+            const int4_t d = mfma_i8(av, bv, int4_t{0, 0, 0, 0});
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int r = qd * 4 + v;
+                if (r < MPAD) dots[((g0 - w0 + gg) * MPAD + r) * 16 + j] = d[v];
+            }
+        }
+        __syncthreads();
+        if (folds) {
+            const int end = min(groups - w0, kGvWindow);
+            for (int gw = 0; gw < end; gw++) {
+                const float dot = (float)dots[(gw * MPAD + fr) * 16 + fc];
+                const float sxv = asx[fr * kGvWindow + gw], swv2 = sw[gw * 16 + fc];
+                if (PROJECT)
+                    acc = __fadd_rn(acc, __fmul_rn(dot, __fmul_rn(sxv, swv2)));
+                else
+                    acc = __builtin_fmaf(dot, __fmul_rn(swv2, sxv), acc);
+            }
+        }
+        __syncthreads();
+    }
+    const bool nan_out = *flag != 0;
+    if (nan_out && bad_out != nullptr && threadIdx.x == 0) atomicOr(bad_out, 1);
+    if (folds) {
+        const int row = row0 + fr, col = t * 16 + fc;
+        if (row < m && col < n) y[(size_t)row * n + col] = nan_out ? __builtin_nanf("") : acc;
+    }
+}
+
 // Fused gate/up + SiLU + A8 requantization (grouped_q4_mlp.wgsl:78-105): a
 // block is 16 rows x one 64-column block; the four waves hold 16 columns each.
 __global__ __launch_bounds__(256) void mlp_requant_kernel(
@@ -653,6 +857,43 @@ void gemm_dispatch(const Weight &w, const half_t *x, int m, void *y, const half_
     }
 }
 
+
+template <int BITS, int MPAD, int AMODE, bool PROJECT>
+void gv_launch_one(const Weight &w, const void *a, const float *sa, int m, int abits, float *y,
+                   const int *bad_in, int *bad_out, hipStream_t s) {
+    using S = GvShape<MPAD>;
+    static bool configured[64] = {};  // the LDS limit is a per-device function attribute
+    int dev = 0;
+    hipGetDevice(&dev);
+    if (dev >= 0 && dev < 64 && !configured[dev]) {
+        hipFuncSetAttribute((const void *)grouped_gemv_kernel<BITS, MPAD, AMODE, PROJECT>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, S::BYTES);
+        configured[dev] = true;
+    }
+    dim3 grid(w.tiles(), cdiv(m, 16));
+    hipLaunchKernelGGL((grouped_gemv_kernel<BITS, MPAD, AMODE, PROJECT>), grid, dim3(kGvWaves * 64), S::BYTES, s,
+                       w.codes, w.scales, a, sa, m, w.cols, w.rows, w.groups, w.kblocks(), abits, y, bad_in, bad_out);
+}
+
+template <int BITS, int AMODE, bool PROJECT>
+void gv_launch_m(const Weight &w, const void *a, const float *sa, int m, int abits, float *y,
+                 const int *bad_in, int *bad_out, hipStream_t s) {
+    if (m <= 1) gv_launch_one<BITS, 1, AMODE, PROJECT>(w, a, sa, m, abits, y, bad_in, bad_out, s);
+    else if (m <= 2) gv_launch_one<BITS, 2, AMODE, PROJECT>(w, a, sa, m, abits, y, bad_in, bad_out, s);
+    else if (m <= 4) gv_launch_one<BITS, 4, AMODE, PROJECT>(w, a, sa, m, abits, y, bad_in, bad_out, s);
+    else if (m <= 8) gv_launch_one<BITS, 8, AMODE, PROJECT>(w, a, sa, m, abits, y, bad_in, bad_out, s);
+    else gv_launch_one<BITS, 16, AMODE, PROJECT>(w, a, sa, m, abits, y, bad_in, bad_out, s);
+}
+
+template <int AMODE, bool PROJECT>
+void gv_launch(const Weight &w, const void *a, const float *sa, int m, int abits, float *y,
+               const int *bad_in, int *bad_out, hipStream_t s) {
+    if (w.bits == 4)
+        gv_launch_m<4, AMODE, PROJECT>(w, a, sa, m, abits, y, bad_in, bad_out, s);
+    else
+        gv_launch_m<8, AMODE, PROJECT>(w, a, sa, m, abits, y, bad_in, bad_out, s);
+}
+
 }  // namespace
 
 int variant_count(const char *family) {
@@ -678,6 +919,29 @@ int variant_index(const char *family, const char *name) {
     for (int i = 0; i < variant_count(family); i++)
         if (std::string(variant_name(family, i)) == name) return i;
     return -1;
+}
+
+void launch_grouped_small(const Weight &w, const float *x, int m, int abits, float *y, int *bad_out,
+                          bool project, hipStream_t s) {
+    if (m == 0) return;
+    if (project)
+        gv_launch<0, true>(w, x, nullptr, m, abits, y, nullptr, bad_out, s);
+    else
+        gv_launch<0, false>(w, x, nullptr, m, abits, y, nullptr, bad_out, s);
+}
+
+void launch_grouped_codes(const Weight &w, const int8_t *q, const float *sx, int m, float *y,
+                          const int *bad_in, bool project, hipStream_t s) {
+    if (m == 0) return;
+    if (project)
+        gv_launch<1, true>(w, q, sx, m, 8, y, bad_in, nullptr, s);
+    else
+        gv_launch<1, false>(w, q, sx, m, 8, y, bad_in, nullptr, s);
+}
+
+void launch_grouped_records(const Weight &w, const uint32_t *records, int m, float *y, hipStream_t s) {
+    if (m == 0) return;
+    gv_launch<2, false>(w, records, nullptr, m, 8, y, nullptr, nullptr, s);
 }
 
 void launch_grouped(const Weight &w, const int8_t *q, const float *sx, int m, float *y,

@@ -245,8 +245,11 @@ __global__ void dequant_kernel(const uint8_t *__restrict__ codes, const uint8_t 
 // ---- activation quantizer (a4) --------------------------------------------------------
 
 // 16 lanes per (row, 64-group); each lane owns 4 consecutive values.
+// records != nullptr writes the 17-word records of grouped_q4.rs:3-25 instead:
+// words 0..15 the codes (4 per word, element 4l+e in byte e), word 16 the scale.
 __global__ void act_quantize_kernel(const float *__restrict__ x, int m, int k, int bits,
-                                    int8_t *__restrict__ q, float *__restrict__ sc, int *bad) {
+                                    int8_t *__restrict__ q, float *__restrict__ sc, int *bad,
+                                    uint32_t *__restrict__ records) {
     int groups = (k + 63) / 64;
     size_t gid = (blockIdx.x * (size_t)blockDim.x + threadIdx.x) / 16;
     int l = threadIdx.x % 16;
@@ -274,6 +277,12 @@ __global__ void act_quantize_kernel(const float *__restrict__ x, int m, int k, i
         int kk = g * 64 + l * 4 + e;
         int c = kk < k ? quantize_code(v[e], inverse, limit) : 0;
         word |= ((uint32_t)(uint8_t)(int8_t)c) << (8 * e);
+    }
+    if (records != nullptr) {
+        uint32_t *rec = records + ((size_t)r * groups + g) * 17;
+        rec[l] = word;
+        if (l == 0) rec[16] = __builtin_bit_cast(uint32_t, scale);
+        return;
     }
     *(uint32_t *)(q + ((size_t)r * groups + g) * 64 + l * 4) = word;
     if (l == 0) sc[(size_t)r * groups + g] = scale;
@@ -388,7 +397,15 @@ void launch_act_quantize(const float *x, int m, int k, int bits, int8_t *q, floa
     size_t lanes = (size_t)m * ((k + 63) / 64) * 16;
     if (!lanes) return;
     hipLaunchKernelGGL(act_quantize_kernel, dim3(blocks_for(lanes, 256)), dim3(256), 0, s, x, m, k,
-                       bits, q, sc, bad);
+                       bits, q, sc, bad, (uint32_t *)nullptr);
+}
+
+void launch_act_quantize_records(const float *x, int m, int k, uint32_t *records, int *bad,
+                                 hipStream_t s) {
+    size_t lanes = (size_t)m * ((k + 63) / 64) * 16;
+    if (!lanes) return;
+    hipLaunchKernelGGL(act_quantize_kernel, dim3(blocks_for(lanes, 256)), dim3(256), 0, s, x, m, k,
+                       8, (int8_t *)nullptr, (float *)nullptr, bad, records);
 }
 
 void launch_i8_quantize_rows(const float *x, int rows, int k, int8_t *q, float *scales,

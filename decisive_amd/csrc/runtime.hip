@@ -408,13 +408,20 @@ int32_t grouped_linear(dz_ctx *ctx, const dz_weight *a, const dz_weight *b, cons
     if (b && (b->w.cols != w.cols || b->w.kind == dz::WeightKind::Q4G32))
         return fail(ctx, DZ_INVALID_PARAMETERS, "paired weights must share the input width");
     if (m == 0) return DZ_OK;
+    const int abits = mode == DZ_W4A4 ? 4 : 8;
+    if (m <= 16) {
+        // one launch per weight: the kernel quantizes x itself (same codes as act_quantize)
+        dz::launch_grouped_small(w, x, (int)m, abits, ya, nullptr, false, ctx->stream);
+        if (b) dz::launch_grouped_small(b->w, x, (int)m, abits, yb, nullptr, false, ctx->stream);
+        return launched(ctx, "grouped linear");
+    }
     size_t qbytes = m * (size_t)w.groups * 64, sbytes = m * (size_t)w.groups * sizeof(float);
     int32_t rc = ensure_work(ctx, qbytes + sbytes + 256);
     if (rc) return rc;
     int8_t *q = (int8_t *)ctx->work;
     float *s = (float *)((uint8_t *)ctx->work + (qbytes + 255) / 256 * 256);
     dz::launch_fill_i32(ctx->flag, 0, 1, ctx->stream);
-    dz::launch_act_quantize(x, (int)m, w.cols, mode == DZ_W4A4 ? 4 : 8, q, s, ctx->flag, ctx->stream);
+    dz::launch_act_quantize(x, (int)m, w.cols, abits, q, s, ctx->flag, ctx->stream);
     dz::launch_grouped(w, q, s, (int)m, ya, ctx->flag, variant(ctx, "grouped"), ctx->stream);
     if (b) dz::launch_grouped(b->w, q, s, (int)m, yb, ctx->flag, variant(ctx, "grouped"), ctx->stream);
     return launched(ctx, "grouped linear");
@@ -480,8 +487,58 @@ int32_t dz_linear_q8(dz_ctx *ctx, const dz_weight *w, const int8_t *q, const flo
     if (!w || (m && (!q || !s || !y))) return fail(ctx, DZ_INVALID_REQUEST, "null pointer");
     if (w->w.kind == dz::WeightKind::Q4G32)
         return fail(ctx, DZ_INVALID_PARAMETERS, "grouped int8 mode needs a group-64 weight");
-    dz::launch_grouped(w->w, q, s, (int)m, y, nullptr, variant(ctx, "grouped"), ctx->stream);
+    if (m <= 16)
+        dz::launch_grouped_codes(w->w, q, s, (int)m, y, nullptr, false, ctx->stream);
+    else
+        dz::launch_grouped(w->w, q, s, (int)m, y, nullptr, variant(ctx, "grouped"), ctx->stream);
     return launched(ctx, "grouped linear");
+}
+
+int32_t dz_project(dz_ctx *ctx, const dz_weight *w, const float *x, size_t m, float *y) {
+    DZ_BEGIN(ctx);
+    if (!w || (m && (!x || !y))) return fail(ctx, DZ_INVALID_REQUEST, "null pointer");
+    if (w->w.kind == dz::WeightKind::Q4G32 || w->w.cols % 64 != 0)
+        return fail(ctx, DZ_INVALID_PARAMETERS, "invalid packed readout shape");
+    if (m == 0) return DZ_OK;
+    if (m > (1u << 24)) return fail(ctx, DZ_INPUT_TOO_LONG, "input budget exceeded");
+    int bad = 0;
+    int32_t rc;
+    if (m <= 16) {
+        rc = flagged_sync(ctx, [&] {
+            dz::launch_grouped_small(w->w, x, (int)m, 8, y, ctx->flag, true, ctx->stream);
+        }, &bad);
+    } else {
+        size_t qbytes = m * (size_t)w->w.groups * 64, sbytes = m * (size_t)w->w.groups * sizeof(float);
+        rc = ensure_work(ctx, qbytes + sbytes + 256);
+        if (rc) return rc;
+        int8_t *q = (int8_t *)ctx->work;
+        float *s = (float *)((uint8_t *)ctx->work + (qbytes + 255) / 256 * 256);
+        rc = flagged_sync(ctx, [&] {
+            dz::launch_act_quantize(x, (int)m, w->w.cols, 8, q, s, ctx->flag, ctx->stream);
+            dz::launch_grouped_codes(w->w, q, s, (int)m, y, ctx->flag, true, ctx->stream);
+        }, &bad);
+    }
+    if (rc) return rc;
+    if (bad) return fail(ctx, DZ_INFERENCE_FAILED, "nonfinite readout activation");
+    return DZ_OK;
+}
+
+int32_t dz_act_quantize_records(dz_ctx *ctx, const float *x, size_t m, size_t k, uint32_t *records) {
+    DZ_BEGIN(ctx);
+    if (k == 0 || k % 64 != 0) return fail(ctx, DZ_INVALID_PARAMETERS, "records need k % 64 == 0");
+    if (m && (!x || !records)) return fail(ctx, DZ_INVALID_REQUEST, "null pointer");
+    dz::launch_act_quantize_records(x, (int)m, (int)k, records, nullptr, ctx->stream);
+    return launched(ctx, "act_quantize_records");
+}
+
+int32_t dz_linear_records(dz_ctx *ctx, const dz_weight *w, const uint32_t *records, size_t m, float *y) {
+    DZ_BEGIN(ctx);
+    if (!w || (m && (!records || !y))) return fail(ctx, DZ_INVALID_REQUEST, "null pointer");
+    if (w->w.kind == dz::WeightKind::Q4G32 || w->w.cols % 64 != 0)
+        return fail(ctx, DZ_INVALID_PARAMETERS, "records products need a group-64 weight with cols % 64 == 0");
+    if (m > (1u << 24)) return fail(ctx, DZ_INPUT_TOO_LONG, "input budget exceeded");
+    dz::launch_grouped_records(w->w, records, (int)m, y, ctx->stream);
+    return launched(ctx, "grouped records linear");
 }
 
 int32_t dz_i8_quantize_rows(dz_ctx *ctx, const float *x, size_t rows, size_t k, int8_t *q,

@@ -73,6 +73,9 @@ _SIGNATURES = {
     "dz_linear_pair": (I32, [P, P, P, P, SZ, P, P, I32]),
     "dz_mlp_requant": (I32, [P, P, P, P, SZ, P, P]),
     "dz_linear_q8": (I32, [P, P, P, P, SZ, P]),
+    "dz_project": (I32, [P, P, P, SZ, P]),
+    "dz_act_quantize_records": (I32, [P, P, SZ, SZ, P]),
+    "dz_linear_records": (I32, [P, P, P, SZ, P]),
     "dz_i8_quantize_rows": (I32, [P, P, SZ, SZ, P, P, P]),
     "dz_i8_gemm": (I32, [P, P, P, SZ, P, P, SZ, SZ, P, I32]),
     "dz_layernorm": (I32, [P, P, P, I32, SZ, SZ, P, P, F]),
@@ -239,6 +242,15 @@ class Context:
 
     def linear_q8(self, w: Weight, q, s, m: int, y):
         self._check(load().dz_linear_q8(self.handle, w.handle, _addr(q), _addr(s), m, _addr(y)))
+
+    def project(self, w: Weight, x, m: int, y):
+        self._check(load().dz_project(self.handle, w.handle, _addr(x), m, _addr(y)))
+
+    def act_quantize_records(self, x, m: int, k: int, records):
+        self._check(load().dz_act_quantize_records(self.handle, _addr(x), m, k, _addr(records)))
+
+    def linear_records(self, w: Weight, records, m: int, y):
+        self._check(load().dz_linear_records(self.handle, w.handle, _addr(records), m, _addr(y)))
 
     def i8_quantize_rows(self, x, rows: int, k: int, q, scales, sums=None):
         self._check(load().dz_i8_quantize_rows(self.handle, _addr(x), rows, k, _addr(q), _addr(scales),

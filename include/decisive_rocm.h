@@ -153,6 +153,23 @@ int32_t dz_mlp_requant(dz_ctx *ctx, const dz_weight *gate, const dz_weight *up,
 int32_t dz_linear_q8(dz_ctx *ctx, const dz_weight *w, const int8_t *q_dev, const float *s_dev,
                      size_t m, float *y_dev);
 
+/* packed.rs:75-119 project: the portable W{4,8}A8 product of the readout,
+ * folding groups as sum += f32(dot) * (sx*sw) (separate multiply and add,
+ * unlike dz_linear's fused fold). x_dev f32 [m x cols], y_dev f32
+ * [m x rows(w)]; the weight is group-64 with cols % 64 == 0. Synchronous: a
+ * non-finite activation gives DZ_INFERENCE_FAILED ("nonfinite readout
+ * activation"), as the reference's ensure! does. */
+int32_t dz_project(dz_ctx *ctx, const dz_weight *w, const float *x_dev, size_t m, float *y_dev);
+/* webgpu/grouped_q4.rs:3-25 quantize: the activation codes and scales of
+ * dz_act_quantize written as 17-word records per (row, 64-group): words 0..15
+ * the int8 codes (element 4l+e in byte e of word l), word 16 the f32 scale.
+ * records_dev uint32 [m x k/64 x 17]; k % 64 == 0. */
+int32_t dz_act_quantize_records(dz_ctx *ctx, const float *x_dev, size_t m, size_t k,
+                                uint32_t *records_dev);
+/* grouped_q4_tuned.wgsl:1-84 (int8_gemm on records): the W4A8/W8A8 product of
+ * dz_linear consuming 17-word records, y_dev f32 [m x rows(w)]. */
+int32_t dz_linear_records(dz_ctx *ctx, const dz_weight *w, const uint32_t *records_dev, size_t m,
+                          float *y_dev);
 /* webgpu/int8.rs:107-145 quantize: per row scale = absmax/127 (no floor),
  * q = clamp(rne(x/scale), +-127), 0 when scale == 0; sums = sum of q.
  * q_dev int8 [rows x k] (signed), scales_dev f32 [rows], sums_dev int32 [rows]
