@@ -30,6 +30,9 @@ void launch_act_quantize_records(const float *x, int m, int k, uint32_t *records
 // webgpu/int8.rs:107-145.
 void launch_i8_quantize_rows(const float *x, int rows, int k, int8_t *q, float *scales,
                              int32_t *sums, hipStream_t s);
+// webgpu/q4.rs:48-73: per-row Q4 into the word buffer [rows*(k/8) | scales | sums].
+void launch_q4_quantize_rows(const void *values, int dtype, int rows, int k, uint32_t *out, int *bad,
+                             hipStream_t s);
 void launch_fill_i32(int *p, int value, int count, hipStream_t s);
 
 // ---- products.hip --------------------------------------------------------------
@@ -52,9 +55,10 @@ void launch_w4a16(const Weight &w, const half_t *x, int m, float *y, int gemv_va
 // W4A16 with f16 output and optional fused epilogue (0 none, 1 GELU, 2 +residual f16)
 void launch_w4a16_f16(const Weight &w, const half_t *x, int m, half_t *y, int epilogue,
                       const half_t *residual, int variant, hipStream_t s);
-// Per-row int8 GEMM: raw int32 or f32 epilogue.
+// Per-row int8 GEMM: raw int32 or f32 epilogue. With b_q4, b is the per-row Q4
+// word buffer of launch_q4_quantize_rows (codes expanded to int8 in registers).
 void launch_i8_gemm(const int8_t *a, const float *sa, int m, const int8_t *b, const float *sb,
-                    int n, int k, void *y, int raw, int variant, hipStream_t s);
+                    int n, int k, void *y, int raw, int variant, hipStream_t s, bool b_q4 = false);
 // Fused gate/up W4A8 + SiLU + A8 requantization (grouped_q4_mlp.wgsl).
 void launch_mlp_requant(const Weight &gate, const Weight &up, const int8_t *q, const float *sx,
                         int m, int8_t *qo, float *so, const int *bad, hipStream_t s);

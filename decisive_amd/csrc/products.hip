@@ -679,7 +679,18 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_w4a16_kernel(
 
 // K-step 64 bytes; both tiles staged in LDS as rows of four 16-byte chunks,
 // chunk c of row r at slot c ^ ((r >> 2) & 3).
-template <int BM, int BN, int WM, int WN>
+// 8 (code + 8) nibbles of a per-row Q4 word (element t at bits 4t) -> two
+// words of signed int8 codes in element order.
+__device__ __forceinline__ uint2_t row_nibbles_to_i8(uint32_t w) {
+    const uint32_t lo = w & 0x0F0F0F0Fu;         // elements 0 2 4 6
+    const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;  // elements 1 3 5 7
+    uint2_t out;
+    out[0] = (__builtin_amdgcn_perm(hi, lo, 0x05010400u) + 0x78787878u) ^ 0x80808080u;  // 0 1 2 3
+    out[1] = (__builtin_amdgcn_perm(hi, lo, 0x07030602u) + 0x78787878u) ^ 0x80808080u;  // 4 5 6 7
+    return out;
+}
+
+template <int BM, int BN, int WM, int WN, bool Q4B>
 __global__ __launch_bounds__(WM *WN * 64) void i8_gemm_kernel(const int8_t *__restrict__ a,
                                                               const float *__restrict__ sa, int m,
                                                               const int8_t *__restrict__ b,
@@ -721,6 +732,17 @@ __global__ __launch_bounds__(WM *WN * 64) void i8_gemm_kernel(const int8_t *__re
         }
         return v;
     };
+    // per-row Q4 B: 16 codes = two words of row r (k % 8 == 0), expanded to int8
+    auto load_q4_chunk = [&](int r, int kk) -> uint4_t {
+        uint4_t v = {0u, 0u, 0u, 0u};
+        if (r < n && kk < k) {
+            const uint32_t *row = (const uint32_t *)b + (size_t)r * (k / 8);
+            const uint2_t c0 = row_nibbles_to_i8(row[kk / 8]);
+            const uint2_t c1 = kk + 8 < k ? row_nibbles_to_i8(row[kk / 8 + 1]) : uint2_t{0u, 0u};
+            v = uint4_t{c0[0], c0[1], c1[0], c1[1]};
+        }
+        return v;
+    };
     auto load = [&](int step) {
 #pragma unroll
         for (int p = 0; p < PA; p++) {
@@ -730,7 +752,9 @@ __global__ __launch_bounds__(WM *WN * 64) void i8_gemm_kernel(const int8_t *__re
 #pragma unroll
         for (int p = 0; p < PB; p++) {
             int idx = threadIdx.x + p * THREADS;
-            if (idx < BCH) rb[p] = load_chunk(b, n, col0 + idx / 4, step * 64 + (idx % 4) * 16);
+            if (idx < BCH)
+                rb[p] = Q4B ? load_q4_chunk(col0 + idx / 4, step * 64 + (idx % 4) * 16)
+                            : load_chunk(b, n, col0 + idx / 4, step * 64 + (idx % 4) * 16);
         }
     };
     auto store = [&](int buf) {
@@ -988,23 +1012,32 @@ void launch_w4a16_f16(const Weight &w, const half_t *x, int m, half_t *y, int ep
     }
 }
 
-void launch_i8_gemm(const int8_t *a, const float *sa, int m, const int8_t *b, const float *sb,
-                    int n, int k, void *y, int raw, int variant, hipStream_t s) {
-    if (m == 0 || n == 0) return;
+template <bool Q4B>
+void i8_gemm_dispatch(const int8_t *a, const float *sa, int m, const int8_t *b, const float *sb, int n,
+                      int k, void *y, int raw, int variant, hipStream_t s) {
     switch (variant) {
         case 1:
-            hipLaunchKernelGGL((i8_gemm_kernel<256, 128, 2, 2>), dim3(cdiv(n, 128), cdiv(m, 256)), dim3(256), 0, s,
-                               a, sa, m, b, sb, n, k, y, raw);
+            hipLaunchKernelGGL((i8_gemm_kernel<256, 128, 2, 2, Q4B>), dim3(cdiv(n, 128), cdiv(m, 256)), dim3(256), 0,
+                               s, a, sa, m, b, sb, n, k, y, raw);
             break;
         case 2:
-            hipLaunchKernelGGL((i8_gemm_kernel<64, 64, 2, 2>), dim3(cdiv(n, 64), cdiv(m, 64)), dim3(256), 0, s,
+            hipLaunchKernelGGL((i8_gemm_kernel<64, 64, 2, 2, Q4B>), dim3(cdiv(n, 64), cdiv(m, 64)), dim3(256), 0, s,
                                a, sa, m, b, sb, n, k, y, raw);
             break;
         default:
-            hipLaunchKernelGGL((i8_gemm_kernel<128, 128, 2, 2>), dim3(cdiv(n, 128), cdiv(m, 128)), dim3(256), 0, s,
-                               a, sa, m, b, sb, n, k, y, raw);
+            hipLaunchKernelGGL((i8_gemm_kernel<128, 128, 2, 2, Q4B>), dim3(cdiv(n, 128), cdiv(m, 128)), dim3(256), 0,
+                               s, a, sa, m, b, sb, n, k, y, raw);
             break;
     }
+}
+
+void launch_i8_gemm(const int8_t *a, const float *sa, int m, const int8_t *b, const float *sb,
+                    int n, int k, void *y, int raw, int variant, hipStream_t s, bool b_q4) {
+    if (m == 0 || n == 0) return;
+    if (b_q4)
+        i8_gemm_dispatch<true>(a, sa, m, b, sb, n, k, y, raw, variant, s);
+    else
+        i8_gemm_dispatch<false>(a, sa, m, b, sb, n, k, y, raw, variant, s);
 }
 
 }  // namespace dz

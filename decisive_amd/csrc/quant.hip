@@ -324,6 +324,57 @@ __global__ __launch_bounds__(256) void i8_quantize_rows_kernel(const float *__re
     }
 }
 
+// ---- per-row Q4 (a13) -----------------------------------------------------------------
+
+// webgpu/q4.rs:48-73: one block per row. scale = absmax/7 (f32 division, no
+// floor); code = clamp(rne(x/scale), +-7), 0 when scale == 0; word j of the row
+// holds element 8j+t as (code + 8) at bits 4t. After the rows*(k/8) code words
+// come the rows f32 scales and the rows i32 code sums. Sets *bad on a
+// non-finite value.
+__global__ __launch_bounds__(256) void q4_quantize_rows_kernel(const void *__restrict__ values, int dtype,
+                                                                int rows, int k, uint32_t *__restrict__ out,
+                                                                int *bad) {
+    __shared__ float smax[4];
+    __shared__ int ssum[4];
+    const int r = blockIdx.x;
+    const size_t base = (size_t)r * k;
+    float maximum = 0.0f;
+    bool finite = true;
+    for (int i = threadIdx.x; i < k; i += 256) {
+        float v = load_value(values, dtype, base + i);
+        finite = finite && __builtin_isfinite(v);
+        maximum = fmaxf(maximum, fabsf(v));
+    }
+    if (!finite) atomicOr(bad, 1);
+    for (int off = 32; off > 0; off >>= 1) maximum = fmaxf(maximum, __shfl_xor(maximum, off));
+    if (threadIdx.x % 64 == 0) smax[threadIdx.x / 64] = maximum;
+    __syncthreads();
+    maximum = fmaxf(fmaxf(smax[0], smax[1]), fmaxf(smax[2], smax[3]));
+    const float scale = __fdiv_rn(maximum, 7.0f);
+    const int words = k / 8;
+    int total = 0;
+    for (int w = threadIdx.x; w < words; w += 256) {
+        uint32_t packed = 0;
+        for (int t = 0; t < 8; t++) {
+            int q = 0;
+            if (scale > 0.0f) {
+                q = (int)__builtin_rintf(__fdiv_rn(load_value(values, dtype, base + (size_t)w * 8 + t), scale));
+                q = q < -7 ? -7 : (q > 7 ? 7 : q);
+            }
+            total += q;
+            packed |= (uint32_t)(q + 8) << (4 * t);
+        }
+        out[(size_t)r * words + w] = packed;
+    }
+    for (int off = 32; off > 0; off >>= 1) total += __shfl_xor(total, off);
+    if (threadIdx.x % 64 == 0) ssum[threadIdx.x / 64] = total;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        out[(size_t)rows * words + r] = __builtin_bit_cast(uint32_t, scale);
+        out[(size_t)rows * words + rows + r] = (uint32_t)(ssum[0] + ssum[1] + ssum[2] + ssum[3]);
+    }
+}
+
 // Native Q4 group-64 -> packed.rs wire layout: one thread per (row, 64-run).
 __global__ void export_q4g64_kernel(const uint8_t *__restrict__ codes,
                                     const uint8_t *__restrict__ scales, int rows, int cols, int kbs,
@@ -412,6 +463,12 @@ void launch_i8_quantize_rows(const float *x, int rows, int k, int8_t *q, float *
                              int32_t *sums, hipStream_t s) {
     if (!rows) return;
     hipLaunchKernelGGL(i8_quantize_rows_kernel, dim3(rows), dim3(256), 0, s, x, k, q, scales, sums);
+}
+
+void launch_q4_quantize_rows(const void *values, int dtype, int rows, int k, uint32_t *out, int *bad,
+                             hipStream_t s) {
+    if (!rows) return;
+    hipLaunchKernelGGL(q4_quantize_rows_kernel, dim3(rows), dim3(256), 0, s, values, dtype, rows, k, out, bad);
 }
 
 void launch_export_q4g64(const Weight &w, uint8_t *wire, hipStream_t s) {

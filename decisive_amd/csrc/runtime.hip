@@ -560,6 +560,35 @@ int32_t dz_i8_gemm(dz_ctx *ctx, const int8_t *a, const float *sa, size_t m, cons
     return launched(ctx, "i8 gemm");
 }
 
+int32_t dz_q4_quantize_rows(dz_ctx *ctx, const void *values, int32_t dtype, size_t rows, size_t k,
+                            uint32_t *out) {
+    DZ_BEGIN(ctx);
+    if (dtype != DZ_F32 && dtype != DZ_F16) return fail(ctx, DZ_INVALID_PARAMETERS, "dtype must be f32 or f16");
+    if (k == 0 || k % 8 != 0 || k > 32768)
+        return fail(ctx, DZ_INVALID_PARAMETERS, "Q4 reduction must be a multiple of eight, at most 32768");
+    if (rows && (!values || !out)) return fail(ctx, DZ_INVALID_REQUEST, "null pointer");
+    if (rows == 0) return DZ_OK;
+    int bad = 0;
+    int32_t rc = flagged_sync(ctx, [&] {
+        dz::launch_q4_quantize_rows(values, dtype == DZ_F16 ? 1 : 0, (int)rows, (int)k, out, ctx->flag, ctx->stream);
+    }, &bad);
+    if (rc) return rc;
+    if (bad) return fail(ctx, DZ_INVALID_CHECKPOINT, "non-finite Q4 weight");
+    return DZ_OK;
+}
+
+int32_t dz_q4_rows_gemm(dz_ctx *ctx, const int8_t *a, const float *sa, size_t m, const uint32_t *w, size_t n,
+                        size_t k, void *y, int32_t raw) {
+    DZ_BEGIN(ctx);
+    if ((m && n) && (!a || !w || !y || (!raw && !sa))) return fail(ctx, DZ_INVALID_REQUEST, "null pointer");
+    if (k == 0 || k % 8 != 0 || k > 32768)
+        return fail(ctx, DZ_INVALID_PARAMETERS, "Q4 reduction must be a multiple of eight, at most 32768");
+    const float *sw = (const float *)(w + n * (k / 8));  // the row scales follow the code words
+    dz::launch_i8_gemm(a, sa, (int)m, (const int8_t *)w, sw, (int)n, (int)k, y, raw ? 1 : 0, variant(ctx, "i8_gemm"),
+                       ctx->stream, true);
+    return launched(ctx, "q4 rows gemm");
+}
+
 // ---- epilogues --------------------------------------------------------------------------
 
 int32_t dz_layernorm(dz_ctx *ctx, const void *x, void *y, int32_t dtype, size_t rows, size_t d,

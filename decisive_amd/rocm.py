@@ -78,6 +78,8 @@ _SIGNATURES = {
     "dz_linear_records": (I32, [P, P, P, SZ, P]),
     "dz_i8_quantize_rows": (I32, [P, P, SZ, SZ, P, P, P]),
     "dz_i8_gemm": (I32, [P, P, P, SZ, P, P, SZ, SZ, P, I32]),
+    "dz_q4_quantize_rows": (I32, [P, P, I32, SZ, SZ, P]),
+    "dz_q4_rows_gemm": (I32, [P, P, P, SZ, P, SZ, SZ, P, I32]),
     "dz_layernorm": (I32, [P, P, P, I32, SZ, SZ, P, P, F]),
     "dz_rmsnorm": (I32, [P, P, P, SZ, SZ, P, F, I32]),
     "dz_gelu": (I32, [P, P, I32, SZ]),
@@ -261,6 +263,13 @@ class Context:
                                       1 if raw else 0))
 
     # ---- epilogues ----
+    def q4_quantize_rows(self, values, dtype: int, rows: int, k: int, out):
+        self._check(load().dz_q4_quantize_rows(self.handle, _addr(values), dtype, rows, k, _addr(out)))
+
+    def q4_rows_gemm(self, a, sa, m: int, w, n: int, k: int, y, raw: bool):
+        self._check(load().dz_q4_rows_gemm(self.handle, _addr(a), _addr(sa), m, _addr(w), n, k, _addr(y),
+                                           1 if raw else 0))
+
     def layernorm(self, x, y, dtype: int, rows: int, d: int, w, b, eps: float):
         self._check(load().dz_layernorm(self.handle, _addr(x), _addr(y), dtype, rows, d, _addr(w), _addr(b), eps))
 

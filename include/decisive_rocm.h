@@ -182,6 +182,21 @@ int32_t dz_i8_gemm(dz_ctx *ctx, const int8_t *a_dev, const float *sa_dev, size_t
                    const int8_t *w_dev, const float *sw_dev, size_t n, size_t k, void *y_dev,
                    int32_t raw);
 
+/* webgpu/q4.rs:48-73 quantize_q4 (the per-output-channel Q4 mode): per row
+ * scale = absmax/7 (f32 division, no floor), code = clamp(rne(x/scale), +-7)
+ * (0 when scale == 0). out_dev is the reference's word buffer, uint32
+ * [rows*(k/8) + 2*rows]: rows*(k/8) code words (element 8j+t of a row as
+ * code+8 at bits 4t of its word j), then the rows f32 scales, then the rows
+ * i32 code sums. values_dev is f16 (as the reference) or f32. k % 8 == 0,
+ * k <= 32768. Synchronous; a non-finite weight gives DZ_INVALID_CHECKPOINT. */
+int32_t dz_q4_quantize_rows(dz_ctx *ctx, const void *values_dev, int32_t dtype, size_t rows, size_t k,
+                            uint32_t *out_dev);
+/* webgpu/q4.rs:99-105 gemm (int8::gemm with Q4 weights expanded): a_dev int8
+ * [m x k] per-row codes (dz_i8_quantize_rows), w_dev the buffer above for n
+ * rows; y_dev [m x n] = exact int32 dots (raw != 0) or (f32(dot)*sa)*sw. */
+int32_t dz_q4_rows_gemm(dz_ctx *ctx, const int8_t *a_dev, const float *sa_dev, size_t m,
+                        const uint32_t *w_dev, size_t n, size_t k, void *y_dev, int32_t raw);
+
 /* ---- layer epilogues --------------------------------------------------------- */
 
 /* decima/cpu.rs:529-540 LayerNorm over rows of d: (x-mean)*rsqrt(var+eps)*w+b.

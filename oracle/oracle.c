@@ -524,6 +524,51 @@ void or_i8_quantize_rows(const float *x, size_t rows, size_t k, int8_t *q, float
     }
 }
 
+/* ------------------------------------------------------------------------ */
+/* a13: per-row Q4 from f16 weights, webgpu/q4.rs:48-73 (the legacy         */
+/* symmetric per-output-channel mode). Output words, as the reference's     */
+/* buffer: rows*(k/8) code words (element 8j+t of a row at bits 4t of word  */
+/* j, code+8), then rows f32 scales, then rows i32 code sums.               */
+/* ------------------------------------------------------------------------ */
+
+int or_q4_quantize_rows(const uint16_t *x_f16, size_t rows, size_t k, uint32_t *out) {
+    if (k == 0 || k % 8 != 0 || k > 32768) return -1;
+    const size_t words = k / 8;
+    for (size_t r = 0; r < rows; r++) {
+        const uint16_t *row = x_f16 + r * k;
+        float maximum = 0.0f;
+        for (size_t j = 0; j < k; j++) maximum = fmaxf(maximum, fabsf(or_f16_to_f32(row[j])));
+        float scale = maximum / 7.0f;
+        int32_t total = 0;
+        for (size_t j = 0; j < words; j++) {
+            uint32_t packed = 0;
+            for (size_t t = 0; t < 8; t++) {
+                int32_t q = 0;
+                if (scale > 0.0f) {
+                    q = even(or_f16_to_f32(row[j * 8 + t]) / scale);
+                    if (q < -7) q = -7;
+                    if (q > 7) q = 7;
+                }
+                total += q;
+                packed |= (uint32_t)(q + 8) << (4 * t);
+            }
+            out[r * words + j] = packed;
+        }
+        uint32_t bits;
+        memcpy(&bits, &scale, 4);
+        out[rows * words + r] = bits;
+        out[rows * words + rows + r] = (uint32_t)total;
+    }
+    return 0;
+}
+
+/* The signed codes of that buffer, [rows x k] int8 (q4.rs:81-97 expand). */
+void or_q4_rows_codes(const uint32_t *words, size_t rows, size_t k, int8_t *codes) {
+    for (size_t r = 0; r < rows; r++)
+        for (size_t j = 0; j < k; j++)
+            codes[r * k + j] = (int8_t)((int)((words[r * (k / 8) + j / 8] >> (4 * (j % 8))) & 15u) - 8);
+}
+
 struct i8_job {
     const int8_t *qa, *qw;
     const float *sa, *sw;

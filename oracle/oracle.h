@@ -98,6 +98,10 @@ void or_i8_quantize_rows(const float *x, size_t rows, size_t k, int8_t *q,
                          float *scales, int32_t *sums);
 /* int8.rs:147-242 gemm(): exact int32 dot; raw -> i32, else (f32(dot)*sx)*sw.
  * Either output pointer may be NULL. threads >= 1 splits rows. */
+/* webgpu/q4.rs:48-73 quantize (a13): per-row Q4 of f16 weights into the
+ * reference's word buffer [rows*(k/8) codes | rows scales | rows sums]. */
+int or_q4_quantize_rows(const uint16_t *x_f16, size_t rows, size_t k, uint32_t *out);
+void or_q4_rows_codes(const uint32_t *words, size_t rows, size_t k, int8_t *codes);
 void or_i8_gemm(const int8_t *qa, const float *sa, size_t m, const int8_t *qw,
                 const float *sw, size_t n, size_t k, int threads, int32_t *raw,
                 float *y);

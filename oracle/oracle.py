@@ -66,6 +66,8 @@ def _declare(L):
         "or_has_avx2": (I, []),
         "or_i8_quantize_rows": (None, [P, SZ, SZ, P, P, P]),
         "or_i8_gemm": (None, [P, P, SZ, P, P, SZ, SZ, I, P, P]),
+        "or_q4_quantize_rows": (I, [P, SZ, SZ, P]),
+        "or_q4_rows_codes": (None, [P, SZ, SZ, P]),
         "or_w4a16": (None, [P, SZ, SZ, P, SZ, P]),
         "or_layernorm": (None, [P, SZ, SZ, P, P, F]),
         "or_gelu": (None, [P, SZ]),
@@ -295,6 +297,24 @@ def i8_gemm(qa, sa, m, qw, sw, n, k, threads=1, raw=True, scaled=True):
                      _p(_c(sw, np.float32)), n, k, threads,
                      _p(r) if raw else None, _p(y) if scaled else None)
     return r, y
+
+
+def q4_quantize_rows(x_f16_bits, rows, k) -> np.ndarray:
+    """or_q4_quantize_rows: webgpu/q4.rs:48-73 -> uint32 [rows*(k/8) + 2*rows]."""
+    out = np.empty(rows * (k // 8) + 2 * rows, np.uint32)
+    rc = lib().or_q4_quantize_rows(_p(_c(x_f16_bits, np.uint16)), rows, k, _p(out))
+    if rc:
+        raise OracleError("Q4 reduction must be a multiple of eight, at most 32768")
+    return out
+
+
+def q4_rows_split(words, rows, k):
+    """(codes int8 [rows, k], scales f32 [rows], sums i32 [rows]) of a q4 buffer."""
+    words = _c(words, np.uint32)
+    codes = np.empty((rows, k), np.int8)
+    lib().or_q4_rows_codes(_p(words), rows, k, _p(codes))
+    base = rows * (k // 8)
+    return codes, words[base:base + rows].view(np.float32).copy(), words[base + rows:base + 2 * rows].view(np.int32).copy()
 
 
 # ---- W4A16 closed form and epilogues --------------------------------------------

@@ -351,3 +351,35 @@ def test_config4_int8_full_size(ctx, oracle):
     rows = np.arange(0, m, 97)
     want, _ = oracle.i8_gemm(oqa[rows], osa[rows], rows.size, oqb, osb, n, k, threads=16, scaled=False)
     assert np.array_equal(host(ctx, r)[rows], want)
+
+
+# ---- per-row Q4 product (webgpu/q4.rs:99-105) ----------------------------------------
+
+@pytest.mark.parametrize("m,n,k", GOLDEN["q4_raw_check_shapes"]["mnk"] + [[77, 45, 104], [130, 260, 4104], [256, 512, 4096]])
+def test_q4_rows_gemm_exact(ctx, oracle, m, n, k):
+    """Exact int32 dots of int8 activations with per-row Q4 codes (brute
+    force), and the (f32(dot)*sa)*sw epilogue bit for bit; the first two
+    shapes use the known-answer inputs of q4.rs:107-142."""
+    torch = pytest.importorskip("torch")
+    if [m, n, k] in GOLDEN["q4_raw_check_shapes"]["mnk"]:
+        i = np.arange(m * k)
+        a = np.where(i % k == 0, 127.0, ((i * 17 % 255) - 127.0)).astype(np.float32)
+        j = np.arange(n * k)
+        b = np.where(j % k == 0, 7.0, ((j * 11 % 15) - 7.0)).astype(np.float32)
+    else:
+        rng = np.random.default_rng(m + n + k)
+        a = rng.standard_normal(m * k).astype(np.float32)
+        b = (rng.standard_normal(n * k) * 0.02).astype(np.float32)
+    bits16 = oracle.f32_to_f16_bits(b)
+    words = empty((n * (k // 8) + 2 * n,), torch.int32)
+    ctx.q4_quantize_rows(dev(bits16.view(np.float16)), rocm.F16, n, k, words)
+    qa, sa, _ = oracle.i8_quantize_rows(a, m, k)
+    raw = empty((m, n), torch.int32)
+    y = empty((m, n), torch.float32)
+    ctx.q4_rows_gemm(dev(qa), dev(sa), m, words, n, k, raw, raw=True)
+    ctx.q4_rows_gemm(dev(qa), dev(sa), m, words, n, k, y, raw=False)
+    codes, scales, _ = oracle.q4_rows_split(oracle.q4_quantize_rows(bits16, n, k), n, k)
+    expected = qa.astype(np.int64) @ codes.astype(np.int64).T
+    assert np.array_equal(host(ctx, raw).astype(np.int64), expected)
+    _, want = oracle.i8_gemm(qa, sa, m, codes, scales, n, k, raw=False)
+    assert bits_equal(host(ctx, y), want)

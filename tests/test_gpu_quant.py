@@ -173,3 +173,37 @@ def test_dequant_rows_gathers_and_rejects_bad_ids(ctx, oracle):
     with pytest.raises(rocm.DzError) as e:
         ctx.dequant_rows(w, dev(np.array([1, 40], np.int32)), 2, y, rocm.F32)
     assert e.value.code == "INVALID_REQUEST"
+
+
+# ---- per-row Q4 (webgpu/q4.rs) --------------------------------------------------------
+
+@pytest.mark.parametrize("rows,k", [(7, 72), (4, 64), (33, 1000), (128, 4096), (1, 8)])
+def test_q4_rows_quantizer_bit_exact(ctx, oracle, rows, k):
+    """webgpu/q4.rs:48-73 from f16 weights: every code word, scale and sum."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(rows * k)
+    w = (rng.standard_normal((rows, k)) * 0.02).astype(np.float32)
+    w[0, :] = 0.0  # a zero row: scale 0, codes 0
+    bits16 = oracle.f32_to_f16_bits(w)
+    out = empty((rows * (k // 8) + 2 * rows,), torch.int32)
+    ctx.q4_quantize_rows(dev(bits16.view(np.float16)), rocm.F16, rows, k, out)
+    got = host(ctx, out).view(np.uint32)
+    want = oracle.q4_quantize_rows(bits16, rows, k)
+    assert bits_equal(got, want)
+    # f32 input holding f16-representable values gives the same buffer
+    out32 = empty((rows * (k // 8) + 2 * rows,), torch.int32)
+    ctx.q4_quantize_rows(dev(oracle.f16_bits_to_f32(bits16)), rocm.F32, rows, k, out32)
+    assert bits_equal(host(ctx, out32).view(np.uint32), want)
+
+
+def test_q4_rows_quantizer_rejects_bad_input(ctx, oracle):
+    torch = pytest.importorskip("torch")
+    out = empty((64,), torch.int32)
+    with pytest.raises(rocm.DzError) as e:
+        ctx.q4_quantize_rows(dev(np.ones(12, np.float32)), rocm.F32, 1, 12, out)
+    assert e.value.code == "INVALID_PARAMETERS"
+    x = np.ones((2, 16), np.float32)
+    x[1, 3] = np.nan
+    with pytest.raises(rocm.DzError) as e:
+        ctx.q4_quantize_rows(dev(x), rocm.F32, 2, 16, out)
+    assert e.value.code == "INVALID_CHECKPOINT"

@@ -356,3 +356,40 @@ def test_silu_requant_is_unfused_composition(oracle):
     q2, s2 = oracle.act_quantize(v, 3, 128, 8)
     assert np.array_equal(q, q2) and np.array_equal(s, s2)
     assert np.allclose(q.astype(np.float64) * np.repeat(s, 64, 1), v, atol=np.repeat(s, 64, 1) * 0.5 + 1e-12)
+
+
+# ---- per-row Q4 (webgpu/q4.rs) ----------------------------------------------------------
+
+@pytest.mark.parametrize("m,n,k", GOLDEN["q4_raw_check_shapes"]["mnk"])
+def test_q4_rows_known_answer(oracle, m, n, k):
+    """webgpu/q4.rs:107-142: integer weights in [-7, 7] with a 7 in every row
+    quantize to themselves (scale exactly 1.0, sums = row sums) and the raw
+    int32 dots against int8-quantized integer activations are exact."""
+    i = np.arange(m * k)
+    a = np.where(i % k == 0, 127.0, ((i * 17 % 255) - 127.0)).astype(np.float32)
+    j = np.arange(n * k)
+    b = np.where(j % k == 0, 7.0, ((j * 11 % 15) - 7.0)).astype(np.float32)
+    words = oracle.q4_quantize_rows(oracle.f32_to_f16_bits(b), n, k)
+    codes, scales, sums = oracle.q4_rows_split(words, n, k)
+    assert np.array_equal(codes.astype(np.float32), b.reshape(n, k))
+    assert np.array_equal(scales.view(np.uint32), np.full(n, np.float32(1.0)).view(np.uint32))
+    assert np.array_equal(sums, b.reshape(n, k).sum(1).astype(np.int32))
+    qa, sa, _ = oracle.i8_quantize_rows(a, m, k)
+    raw, _ = oracle.i8_gemm(qa, sa, m, codes, scales, n, k, scaled=False)
+    expected = a.reshape(m, k).astype(np.int64) @ b.reshape(n, k).astype(np.int64).T
+    assert np.array_equal(raw.astype(np.int64), expected)
+
+
+def test_q4_rows_rounding_and_zero_rows(oracle):
+    """x/scale rounded half to even (q4.rs:60 even), clamped to +-7; an all-zero
+    row has scale 0 and codes 0 (stored as 8)."""
+    k = 16
+    row0 = np.array([7, 3.5, 2.5, -2.5, 0.5, -0.5, 1.5, -1.5, 6.5, -6.5, 0, 1, 2, 3, 4, 5], np.float32)
+    row1 = np.zeros(k, np.float32)
+    words = oracle.q4_quantize_rows(oracle.f32_to_f16_bits(np.concatenate([row0, row1])), 2, k)
+    codes, scales, sums = oracle.q4_rows_split(words, 2, k)
+    assert codes[0].tolist() == [7, 4, 2, -2, 0, 0, 2, -2, 6, -6, 0, 1, 2, 3, 4, 5]
+    assert scales[1] == 0.0 and not codes[1].any() and sums[1] == 0
+    assert words[2] == 0x88888888 and words[3] == 0x88888888
+    with pytest.raises(oracle.OracleError):
+        oracle.q4_quantize_rows(np.zeros(12, np.uint16), 1, 12)
