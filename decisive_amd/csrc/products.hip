@@ -818,13 +818,217 @@ __global__ __launch_bounds__(WM *WN * 64) void i8_gemm_kernel(const int8_t *__re
     }
 }
 
+
+// Tiles are assigned XCD-aware: consecutive block ids go to different XCDs,
+// so tile ids are taken in XCD-major order and grouped GROUP_M tile-rows at a
+// time, keeping the blocks that share an XCD's L2 on neighbouring tiles.
+
+__device__ __forceinline__ void xcd_tile(int bid, int nblocks, int tiles_m, int tiles_n, int &tm, int &tn) {
+    constexpr int XCDS = 8, GROUP_M = 4;
+    int linear = bid;
+    if (nblocks % XCDS == 0) linear = (bid % XCDS) * (nblocks / XCDS) + bid / XCDS;
+    const int per_group = GROUP_M * tiles_n;
+    const int group = linear / per_group;
+    const int first_m = group * GROUP_M;
+    const int gsize = min(tiles_m - first_m, GROUP_M);
+    const int in_group = linear % per_group;
+    tm = first_m + in_group % gsize;
+    tn = in_group / gsize;
+}
+
+
+typedef int int16_t_v __attribute__((ext_vector_type(16)));
+
+// Deep-pipelined per-row int8 GEMM. Block tile BM x BN over 4 waves (2 x 2),
+// 32x32x32 i8 MFMAs, k-steps of BK bytes (64 or 128) in NS LDS stages filled
+// by buffer_load ... lds (no VGPR staging). NS - 1 k-steps are in flight: a
+// step waits only for its own stage (s_waitcnt vmcnt of the younger stages'
+// loads) before the workgroup barrier, so HBM/L2 latency overlaps NS - 2
+// steps of MFMA work. Stage rows are BK bytes of 16-byte chunks, XOR-swizzled
+// so fragment reads and DMA writes are bank-conflict free:
+//   BK = 128: slot = chunk ^ (row & 7); BK = 64: slot = chunk ^ ((row >> 1) & 3).
+// Rows past m (n) and chunks past k read as zero (buffer range checks), so
+// any m, n and k % 16 == 0 work. The f32 epilogue reads its row and column
+// scales from LDS.
+template <int BK>
+__device__ __forceinline__ int pipe_slot(int c, int r) {
+    return BK == 128 ? (c ^ (r & 7)) : (c ^ ((r >> 1) & 3));
+}
+
+template <int BM, int BN, int BK, int NS, int WGM, int WGN>
+__global__ __launch_bounds__(WGM *WGN * 64) void i8_gemm_pipe_kernel(const int8_t *__restrict__ a, const float *__restrict__ sa,
+                                                           int m, const int8_t *__restrict__ b,
+                                                           const float *__restrict__ sb, int n, int k,
+                                                           void *__restrict__ y, int raw) {
+    static_assert(NS >= 2 && NS <= 4, "2 to 4 stages");
+    constexpr int WAVES = WGM * WGN, THREADS = WAVES * 64;
+    constexpr int TM = BM / WGM, TN = BN / WGN, MB = TM / 32, NB = TN / 32;
+    constexpr int CPR = BK / 16;                 // 16-byte chunks per stage row
+    constexpr int RPI = 64 / CPR;                // stage rows filled by one DMA instruction
+    constexpr int STAGE = (BM + BN) * BK;
+    constexpr int DPW = (BM + BN) / RPI / WAVES; // DMA instructions per wave per stage
+    static_assert(DPW * WAVES * RPI == BM + BN, "DMA blocks split evenly over the waves");
+    constexpr int SUBS = BK / 32;                // k-substeps of one 32x32x32 MFMA
+    static_assert((NS - 2) * DPW <= 63, "vmcnt range");
+    __shared__ __align__(16) uint8_t st0[STAGE];
+    __shared__ __align__(16) uint8_t st1[STAGE];
+    __shared__ __align__(16) uint8_t st2[NS > 2 ? STAGE : 16];
+    __shared__ __align__(16) uint8_t st3[NS > 3 ? STAGE : 16];
+    __shared__ float scale_rows[BM], scale_cols[BN];
+    uint8_t *const stages[4] = {st0, st1, st2, st3};
+
+    // the wave index is uniform; saying so keeps the DMA's buffer resource in SGPRs
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), lane = threadIdx.x % 64;
+    const int wm = wave / WGN, wn = wave % WGN;
+    const int h = lane / 32, i = lane % 32;
+    const int tiles_m = (m + BM - 1) / BM, tiles_n = (n + BN - 1) / BN;
+    int tm, tn;
+    xcd_tile(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+    const int row0 = tm * BM, col0 = tn * BN;
+    const int steps = (k + BK - 1) / BK;
+    const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(a + (size_t)row0 * k), (short)0, min(BM, m - row0) * k, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsb = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(b + (size_t)col0 * k), (short)0, min(BN, n - col0) * k, 0x00020000);
+    // Lane l fills slot l % CPR of stage row RPI*blk + l / CPR. That row's
+    // source chunk depends on the lane only, so one VGPR offset serves every
+    // DMA instruction; the instruction's first row comes in as soffset.
+    const int lrow = lane / CPR;
+    const int c16 = pipe_slot<BK>(lane % CPR, lrow) * 16;  // slot^swizzle is an involution
+    const uint32_t lane_off = (uint32_t)(lrow * k + c16);
+    // DMA instructions p0 <= p < p1 of a stage (issued in slices between MFMA groups)
+    auto dma = [&](uint8_t *stage, int st, int p0, int p1) {
+        const int kk = st * BK;
+        const uint32_t voff = kk + c16 < k ? lane_off + (uint32_t)kk : 0x80000000u;
+#pragma unroll
+        for (int p = p0; p < p1; p++) {
+            const int blk = wave * DPW + p;
+            auto *dst = (__attribute__((address_space(3))) void *)(stage + __builtin_amdgcn_readfirstlane(blk * 1024));
+            if (blk * RPI < BM)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, dst, 16, voff, blk * RPI * k, 0, 0);
+            else
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb, dst, 16, voff, (blk * RPI - BM) * k, 0, 0);
+        }
+    };
+    auto read_frags = [&](const uint8_t *stage, int sub, int4_t *af, int4_t *bf) {
+        const uint8_t *la = stage, *lb = stage + BM * BK;
+        const int c = sub * 2 + h;
+#pragma unroll
+        for (int x = 0; x < MB; x++) {
+            const int r = wm * TM + x * 32 + i;
+            af[x] = *(const int4_t *)(la + r * BK + pipe_slot<BK>(c, r) * 16);
+        }
+#pragma unroll
+        for (int z = 0; z < NB; z++) {
+            const int r = wn * TN + z * 32 + i;
+            bf[z] = *(const int4_t *)(lb + r * BK + pipe_slot<BK>(c, r) * 16);
+        }
+    };
+    int16_t_v acc[MB][NB];
+#pragma unroll
+    for (int x = 0; x < MB; x++)
+#pragma unroll
+        for (int z = 0; z < NB; z++) acc[x][z] = int16_t_v{};
+    // compute on `stage`; when `next` is set, the loads of step `next_step`
+    // into it are issued in SUBS slices, one before each substep's MFMAs
+    auto compute = [&](const uint8_t *stage, uint8_t *next, int next_step) {
+        int4_t af[2][MB], bf[2][NB];
+        read_frags(stage, 0, af[0], bf[0]);
+#pragma unroll
+        for (int sub = 0; sub < SUBS; sub++) {
+            const int cur = sub & 1;
+            if (next) dma(next, next_step, sub * DPW / SUBS, (sub + 1) * DPW / SUBS);
+            if (sub + 1 < SUBS) read_frags(stage, sub + 1, af[cur ^ 1], bf[cur ^ 1]);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int x = 0; x < MB; x++)
+#pragma unroll
+                for (int z = 0; z < NB; z++)
+                    acc[x][z] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[cur][x], bf[cur][z], acc[x][z], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    if (!raw) {
+        for (int r = threadIdx.x; r < BM; r += THREADS) scale_rows[r] = row0 + r < m ? sa[row0 + r] : 0.0f;
+        for (int c = threadIdx.x; c < BN; c += THREADS) scale_cols[c] = col0 + c < n ? sb[col0 + c] : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < NS - 1; j++)
+        if (j < steps) dma(stages[j], j, 0, DPW);
+    for (int base = 0; base < steps; base += NS) {
+#pragma unroll
+        for (int j = 0; j < NS; j++) {
+            const int s2 = base + j;
+            if (s2 >= steps) break;
+            // this wave's loads of step s2 are done once at most the younger
+            // steps' loads are outstanding; then the barrier covers every wave
+            if (s2 + NS - 2 < steps)
+                asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((NS - 2) * DPW) : "memory");
+            else
+                asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+            compute(stages[j], s2 + NS - 1 < steps ? stages[(j + NS - 1) % NS] : nullptr, s2 + NS - 1);
+        }
+    }
+    __syncthreads();
+    // Epilogue: each wave turns a 32-row slice of its tile into row-major
+    // order in its own LDS region (the stage arrays are free now) and writes
+    // it with 16-byte stores, four consecutive columns per lane.
+    // wave w's slab: stage array w % NS, after the slabs of the waves before it there
+    const int home = wave % NS;  // chosen without indexing `stages` at run time
+    uint8_t *slab_stage = home == 0 ? st0 : home == 1 ? st1 : home == 2 ? st2 : st3;
+    uint32_t *slab = (uint32_t *)(slab_stage + (wave / NS) * 32 * TN * 4);
+    static_assert(((WAVES + NS - 1) / NS) * 32 * TN * 4 <= STAGE, "epilogue slabs fit the stage arrays");
+    float cs[NB];
+    if (!raw) {
+#pragma unroll
+        for (int z = 0; z < NB; z++) cs[z] = scale_cols[wn * TN + z * 32 + i];
+    }
+#pragma unroll
+    for (int x = 0; x < MB; x++) {
+        float rs[16];
+        if (!raw) {
+#pragma unroll
+            for (int e = 0; e < 16; e++) rs[e] = scale_rows[wm * TM + x * 32 + 8 * (e / 4) + 4 * h + (e % 4)];
+        }
+#pragma unroll
+        for (int z = 0; z < NB; z++) {
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const int rl = 8 * (e / 4) + 4 * h + (e % 4), cl = z * 32 + i;
+                uint32_t v = (uint32_t)acc[x][z][e];
+                if (!raw) v = __builtin_bit_cast(uint32_t, __fmul_rn(__fmul_rn((float)acc[x][z][e], rs[e]), cs[z]));
+                slab[rl * TN + cl] = v;
+            }
+        }
+        // the slab is this wave's alone: LDS accesses of one wave complete in order
+        constexpr int QUADS = TN / 4;                   // 16-byte pieces per row
+        constexpr int ROWS_PER_PASS = 64 / QUADS;
+#pragma unroll
+        for (int pass = 0; pass < 32 / ROWS_PER_PASS; pass++) {
+            const int rl = pass * ROWS_PER_PASS + lane / QUADS, q = lane % QUADS;
+            const uint4_t v = *(const uint4_t *)(slab + rl * TN + q * 4);
+            const int r = row0 + wm * TM + x * 32 + rl, c = col0 + wn * TN + q * 4;
+            if (r < m) {
+                uint32_t *dst = (uint32_t *)y + (size_t)r * n + c;
+                if (c + 4 <= n && (n & 3) == 0 && ((uintptr_t)y & 15) == 0) {
+                    *(uint4_t *)dst = v;
+                } else {
+                    for (int e = 0; e < 4; e++)
+                        if (c + e < n) dst[e] = v[e];
+                }
+            }
+        }
+    }
+}
 inline unsigned cdiv(size_t a, size_t b) { return (unsigned)((a + b - 1) / b); }
 
 // ---- variant tables -------------------------------------------------------------
 
 const char *const kGemvNames[] = {"w16", "w8"};
 const char *const kGemmNames[] = {"256x128w2x2", "128x128w2x2", "128x64w2x2"};
-const char *const kI8Names[] = {"128x128w2x2", "256x128w2x2", "64x64w2x2"};
+const char *const kI8Names[] = {"256x256p2w8", "256x256p4k64w8", "256x128p3w8", "256x128p3",
+                                 "128x128w2x2", "256x128w2x2", "64x64w2x2"};
 const char *const kGroupedNames[] = {"wave16x16"};
 
 template <int W, int MPAD, bool G32>
@@ -924,7 +1128,7 @@ int variant_count(const char *family) {
     std::string f(family);
     if (f == "gemv") return 2;
     if (f == "gemm_w4a16") return 3;
-    if (f == "i8_gemm") return 3;
+    if (f == "i8_gemm") return 7;
     if (f == "grouped") return 1;
     return 0;
 }
@@ -1012,15 +1216,38 @@ void launch_w4a16_f16(const Weight &w, const half_t *x, int m, half_t *y, int ep
     }
 }
 
+template <int BM, int BN, int BK, int NS, int WGM = 2, int WGN = 2>
+bool i8_pipe_launch(const int8_t *a, const float *sa, int m, const int8_t *b, const float *sb, int n, int k,
+                    void *y, int raw, hipStream_t s) {
+    if (k % 16 != 0 || (size_t)BM * k >= ((size_t)1 << 31) || (size_t)BN * k >= ((size_t)1 << 31)) return false;
+    const unsigned blocks = cdiv(m, BM) * cdiv(n, BN);
+    hipLaunchKernelGGL((i8_gemm_pipe_kernel<BM, BN, BK, NS, WGM, WGN>), dim3(blocks), dim3(WGM * WGN * 64), 0, s, a,
+                       sa, m, b, sb, n, k, y, raw);
+    return true;
+}
+
+// Variants 0-3 are the pipelined buffer-to-LDS kernels (int8 B, k % 16 == 0);
+// 4-6 stage through registers and take any k and the per-row Q4 B operand.
+// Every variant computes exact int32 dots, so all are bitwise equal; when a
+// pipelined variant cannot take a shape, the register-staged 128x128 runs.
 template <bool Q4B>
 void i8_gemm_dispatch(const int8_t *a, const float *sa, int m, const int8_t *b, const float *sb, int n,
                       int k, void *y, int raw, int variant, hipStream_t s) {
+    if (!Q4B) {
+        switch (variant) {
+            case 0: if (i8_pipe_launch<256, 256, 128, 2, 2, 4>(a, sa, m, b, sb, n, k, y, raw, s)) return; break;
+            case 1: if (i8_pipe_launch<256, 256, 64, 4, 2, 4>(a, sa, m, b, sb, n, k, y, raw, s)) return; break;
+            case 2: if (i8_pipe_launch<256, 128, 128, 3, 2, 4>(a, sa, m, b, sb, n, k, y, raw, s)) return; break;
+            case 3: if (i8_pipe_launch<256, 128, 128, 3, 2, 2>(a, sa, m, b, sb, n, k, y, raw, s)) return; break;
+            default: break;
+        }
+    }
     switch (variant) {
-        case 1:
+        case 5:
             hipLaunchKernelGGL((i8_gemm_kernel<256, 128, 2, 2, Q4B>), dim3(cdiv(n, 128), cdiv(m, 256)), dim3(256), 0,
                                s, a, sa, m, b, sb, n, k, y, raw);
             break;
-        case 2:
+        case 6:
             hipLaunchKernelGGL((i8_gemm_kernel<64, 64, 2, 2, Q4B>), dim3(cdiv(n, 64), cdiv(m, 64)), dim3(256), 0, s,
                                a, sa, m, b, sb, n, k, y, raw);
             break;

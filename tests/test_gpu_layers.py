@@ -184,4 +184,4 @@ def test_tuner_selects_bitwise_equal_variants_and_caches(ctx):
 
 
 def rocm_reference(fam):
-    return {"gemv": "w16", "gemm_w4a16": "256x128w2x2", "i8_gemm": "128x128w2x2"}[fam]
+    return {"gemv": "w16", "gemm_w4a16": "256x128w2x2", "i8_gemm": "256x256p2w8"}[fam]

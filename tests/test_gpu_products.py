@@ -305,7 +305,12 @@ def test_config5_prefill_rows_vs_fp32(ctx, oracle):
 
 # ---- per-row int8 ----------------------------------------------------------------------
 
-@pytest.mark.parametrize("m,n,k", GOLDEN["q4_raw_check_shapes"]["mnk"] + [[77, 45, 100], [1, 1, 4], [130, 260, 4100]])
+I8_VARIANTS = ("256x256p2w8", "256x256p4k64w8", "256x128p3w8", "256x128p3", "128x128w2x2", "256x128w2x2",
+               "64x64w2x2")
+
+
+@pytest.mark.parametrize("m,n,k", GOLDEN["q4_raw_check_shapes"]["mnk"] + [[77, 45, 100], [1, 1, 4], [130, 260, 4100],
+                                                                          [300, 520, 4112], [256, 256, 256], [513, 257, 80]])
 def test_i8_gemm_exact(ctx, oracle, m, n, k):
     """webgpu/q4.rs:476-501 known answers plus ragged shapes: raw int32 and the
     f32 epilogue are bit-exact; every variant agrees."""
@@ -316,7 +321,7 @@ def test_i8_gemm_exact(ctx, oracle, m, n, k):
     qa, sa, _ = oracle.i8_quantize_rows(a, m, k)
     qb, sb, _ = oracle.i8_quantize_rows(b, n, k)
     raw, yf = oracle.i8_gemm(qa, sa, m, qb, sb, n, k, threads=8)
-    for name in ("128x128w2x2", "256x128w2x2", "64x64w2x2"):
+    for name in I8_VARIANTS:
         ctx.select_variant("i8_gemm", name)
         r = empty((m, n), torch.int32)
         y = empty((m, n), torch.float32)
@@ -325,7 +330,7 @@ def test_i8_gemm_exact(ctx, oracle, m, n, k):
         ctx.i8_gemm(da, dsa, m, db, dsb, n, k, y, raw=False)
         assert np.array_equal(host(ctx, r), raw), name
         assert bits_equal(host(ctx, y), yf), name
-    ctx.select_variant("i8_gemm", "128x128w2x2")
+    ctx.select_variant("i8_gemm", I8_VARIANTS[0])
 
 
 def test_config4_int8_full_size(ctx, oracle):
@@ -348,9 +353,13 @@ def test_config4_int8_full_size(ctx, oracle):
     assert bits_equal(host(ctx, sa), osa) and bits_equal(host(ctx, sb), osb)
     r = empty((m, n), torch.int32)
     ctx.i8_gemm(qa, sa, m, qb, sb, n, k, r, raw=True)
+    got = host(ctx, r)
     rows = np.arange(0, m, 97)
     want, _ = oracle.i8_gemm(oqa[rows], osa[rows], rows.size, oqb, osb, n, k, threads=16, scaled=False)
-    assert np.array_equal(host(ctx, r)[rows], want)
+    assert np.array_equal(got[rows], want)
+    # every row: sum_j C[i, j] == A[i] . (sum_j B[j]) exactly (integer checksum)
+    colsum = oqb.astype(np.int64).sum(axis=0)
+    assert np.array_equal(got.astype(np.int64).sum(axis=1), oqa.astype(np.int64) @ colsum)
 
 
 # ---- per-row Q4 product (webgpu/q4.rs:99-105) ----------------------------------------
