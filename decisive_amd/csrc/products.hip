@@ -891,23 +891,26 @@ __global__ __launch_bounds__(WGM *WGN * 64) void i8_gemm_pipe_kernel(const int8_
     const __amdgpu_buffer_rsrc_t rsb = __builtin_amdgcn_make_buffer_rsrc(
         (void *)(b + (size_t)col0 * k), (short)0, min(BN, n - col0) * k, 0x00020000);
     // Lane l fills slot l % CPR of stage row RPI*blk + l / CPR. That row's
-    // source chunk depends on the lane only, so one VGPR offset serves every
-    // DMA instruction; the instruction's first row comes in as soffset.
+    // source chunk depends on the lane only. The whole byte offset (row and
+    // chunk) goes in the VGPR offset, the part the buffer range check covers,
+    // so rows past m (n) and chunks past k read as zero and nothing past the
+    // operands is touched; soffset stays 0.
     const int lrow = lane / CPR;
     const int c16 = pipe_slot<BK>(lane % CPR, lrow) * 16;  // slot^swizzle is an involution
     const uint32_t lane_off = (uint32_t)(lrow * k + c16);
     // DMA instructions p0 <= p < p1 of a stage (issued in slices between MFMA groups)
     auto dma = [&](uint8_t *stage, int st, int p0, int p1) {
         const int kk = st * BK;
+        // >= 2^31 stays out of range after adding a row offset (BM, BN rows * k < 2^31)
         const uint32_t voff = kk + c16 < k ? lane_off + (uint32_t)kk : 0x80000000u;
 #pragma unroll
         for (int p = p0; p < p1; p++) {
             const int blk = wave * DPW + p;
             auto *dst = (__attribute__((address_space(3))) void *)(stage + __builtin_amdgcn_readfirstlane(blk * 1024));
             if (blk * RPI < BM)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, dst, 16, voff, blk * RPI * k, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, dst, 16, voff + (uint32_t)(blk * RPI * k), 0, 0, 0);
             else
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb, dst, 16, voff, (blk * RPI - BM) * k, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb, dst, 16, voff + (uint32_t)((blk * RPI - BM) * k), 0, 0, 0);
         }
     };
     auto read_frags = [&](const uint8_t *stage, int sub, int4_t *af, int4_t *bf) {
@@ -1021,12 +1024,241 @@ __global__ __launch_bounds__(WGM *WGN * 64) void i8_gemm_pipe_kernel(const int8_
         }
     }
 }
+
+// ============================================================================
+// pipelined W4A16 GEMM (large M)
+// ============================================================================
+
+typedef int int32x4_t __attribute__((ext_vector_type(4)));
+
+// Raw buffer resource (stride 0, range-checked offsets) over [p, p + bytes).
+__device__ __forceinline__ int32x4_t buffer_rsrc(const void *p, uint32_t bytes) {
+    const uint64_t a = (uint64_t)(uintptr_t)p;
+    return int32x4_t{(int)(uint32_t)a, (int)((uint32_t)(a >> 32) & 0xffffu), (int)bytes, 0x00020000};
+}
+
+// 32-bit LDS address of a __shared__ object
+__device__ __forceinline__ uint32_t lds_address(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+// buffer_load_dwordx4 ... lds: lane l's 16 bytes at rsrc + voff land at
+// LDS lds + 16 * l. Issued as asm so that the compiler does not add waits
+// for it before LDS reads of other buffers; the caller waits (s_waitcnt
+// vmcnt + s_barrier) before reading what it wrote.
+__device__ __forceinline__ void dma16(uint32_t lds, uint32_t voff, int32x4_t rsrc) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(lds), "v"(voff), "s"(rsrc)
+                 : "memory", "m0");
+}
+
+// Block tile BM x BN over WGM x WGN waves; one k-step is one 128-k block, in
+// two LDS stages filled by buffer_load ... lds while the other is computed:
+//  - activations: BM rows of 256 bytes; chunk c (8 halves) of row r sits at
+//    slot c ^ (r & 15), so the 16 rows of a fragment read fall in distinct
+//    banks. The byte offset of every load is in the VGPR offset, which the
+//    buffer range check covers: rows past m and chunks past k read as zero;
+//  - weight codes: the 1 KiB tile16x128 chunk of each 16-column tile, copied
+//    as is (its lane order is the MFMA operand order);
+//  - scale records go straight to registers, one step ahead.
+// The stage loads are issued as asm (dma16) and waited for at the step's
+// barrier; the one compute body reads whichever stage is current.
+// Codes become f16 exactly as in gemm_w4a16_kernel (exact code times the f16
+// scale, rounded once), and each output accumulates one
+// v_mfma_f32_16x16x32_f16 per 32-k run in k order, so both kernels give the
+// same bits. The MFMA is issued as D[n][m] = W . X^T: lane (q, j) ends with
+// four consecutive output columns of one row and stores them as one vector.
+template <int BM, int BN, int WGM, int WGN, bool G32, int EPI>
+__global__ __launch_bounds__(WGM *WGN * 64) void w4a16_pipe_kernel(
+    const uint8_t *__restrict__ codes, const uint8_t *__restrict__ scales, const half_t *__restrict__ x, int m,
+    int k, int n, int kbs, void *__restrict__ out, const half_t *__restrict__ residual) {
+    constexpr int WAVES = WGM * WGN;
+    constexpr int TM = BM / WGM, TN = BN / WGN, MB = TM / 16, NT = TN / 16;
+    constexpr int XSTAGE = BM * 256, WSTAGE = BN / 16 * 1024;
+    constexpr int XPW = BM / 4 / WAVES;   // 4-row activation DMA instructions per wave per step
+    constexpr int WPW = BN / 16 / WAVES;  // code-chunk DMA instructions per wave per step
+    static_assert(XPW * 4 * WAVES == BM && XPW % 4 == 0, "a wave's first DMA row is a multiple of 16");
+    static_assert(WPW * 16 * WAVES == BN && WPW >= 1, "code chunks split evenly over the waves");
+    static_assert(MB % 2 == 0, "activation fragments are read in two halves");
+    __shared__ __align__(16) uint8_t xs[2 * XSTAGE];
+    __shared__ __align__(16) uint8_t ws[2 * WSTAGE];
+
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), lane = threadIdx.x % 64;
+    const int wm = wave / WGN, wn = wave % WGN;
+    const int q = lane / 16, j = lane % 16;
+    const int tiles_m = (m + BM - 1) / BM, tiles_n = (n + BN - 1) / BN;
+    int tm, tn;
+    xcd_tile(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+    const int row0 = tm * BM, col0 = tn * BN;
+    const int tiles = (n + 15) / 16, tile0 = col0 / 16;
+    const int32x4_t rsx = buffer_rsrc(x + (size_t)row0 * k, (uint32_t)(min(BM, m - row0) * k * 2));
+    const int32x4_t rsw = buffer_rsrc(codes + (size_t)tile0 * kbs * 1024,
+                                      (uint32_t)(min(BN / 16, tiles - tile0) * kbs * 1024));
+    const uint32_t xs_lds = lds_address(xs), ws_lds = lds_address(ws);
+
+    // Activation DMA: lane (q, j) of instruction blk fills slot j of row
+    // 4*blk + q, whose source chunk is j ^ (row & 15) = j ^ q ^ 4*(blk & 3).
+    const uint32_t xlane = (uint32_t)(q * k * 2);
+    const int cx = j ^ q;
+    auto dma = [&](int stage, int kb) {
+        const int kk = kb * 128;
+        const bool whole = kk + 128 <= k;
+#pragma unroll
+        for (int p = 0; p < XPW; p++) {
+            const int c = cx ^ (4 * (p & 3));
+            const int blk = wave * XPW + p;
+            uint32_t voff = xlane + (uint32_t)(blk * 4 * k * 2 + kk * 2) + (uint32_t)(c * 16);
+            if (!whole && kk + 8 * c >= k) voff = 0x80000000u;
+            dma16(__builtin_amdgcn_readfirstlane(xs_lds + stage * XSTAGE + blk * 1024), voff, rsx);
+        }
+#pragma unroll
+        for (int p = 0; p < WPW; p++) {
+            const int t = wave * WPW + p;
+            dma16(__builtin_amdgcn_readfirstlane(ws_lds + stage * WSTAGE + t * 1024),
+                  (uint32_t)((t * kbs + kb) * 1024 + lane * 16), rsw);
+        }
+    };
+    // scale records of this wave's tiles (clamped to a real tile past n): a
+    // uniform tile offset plus the lane's row
+    size_t srec[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) srec[nt] = (size_t)min(tile0 + wn * NT + nt, tiles - 1) * kbs * 128;
+    const uint8_t *const srow = scales + j * 8;
+    auto load_scales = [&](uint2_t *sc, int kb) {
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) sc[nt] = *(const uint2_t *)(srow + srec[nt] + (size_t)kb * 128);
+    };
+
+    float4_t acc[MB][NT];
+#pragma unroll
+    for (int a = 0; a < MB; a++)
+#pragma unroll
+        for (int b = 0; b < NT; b++) acc[a][b] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+    const uint32_t magic = 0x64006400u;
+    constexpr int HM = MB / 2;  // activation fragments per group
+    // word s of this wave's code chunks -> the f16 weight fragments of run s
+    auto dequant = [&](const uint8_t *wst, const uint2_t *sc, int s, half8_t *wf) {
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            const uint32_t word = *(const uint32_t *)(wst + ((wn * NT + nt) * 64 + lane) * 16 + 4 * s);
+            half_t sh;
+            if (G32)
+                sh = __builtin_bit_cast(half_t, (unsigned short)((sc[nt][s >> 1] >> (16 * (s & 1))) & 0xffffu));
+            else
+                sh = (half_t)word_as_float(sc[nt][s >> 1]);
+            const half2_t s2 = {sh, sh};
+            uint4_t c8 = unpack_codes(word, magic);
+#pragma unroll
+            for (int e = 0; e < 4; e++) c8[e] = half2_as_word(word_as_half2(c8[e]) * s2);
+            wf[nt] = as_half8(c8);
+        }
+    };
+    // Activation rows of this wave are r = wm*TM + 16*mb + j, so r & 15 = j.
+    // Group g = 2s + h covers run s and fragment rows h*HM .. h*HM + HM - 1.
+    auto read_x = [&](const uint8_t *xst, int g, half8_t *xf) {
+        const int s = g / 2, h = g % 2;
+        const uint8_t *base = xst + (wm * TM + h * HM * 16 + j) * 256 + (((4 * s + q) ^ j) * 16);
+#pragma unroll
+        for (int x2 = 0; x2 < HM; x2++) xf[x2] = *(const half8_t *)(base + x2 * 16 * 256);
+    };
+    auto compute = [&](const uint8_t *xst, const uint8_t *wst, const uint2_t *sc) {
+        half8_t xf[2][HM], wf[2][NT];
+        read_x(xst, 0, xf[0]);
+        dequant(wst, sc, 0, wf[0]);
+#pragma unroll
+        for (int g = 0; g < 8; g++) {
+            const int s = g / 2, h = g % 2;
+            // the next group's operands are fetched while this group's MFMAs run
+            if (g + 1 < 8) read_x(xst, g + 1, xf[(g + 1) & 1]);
+            if (h == 1 && s + 1 < 4) dequant(wst, sc, s + 1, wf[(s + 1) & 1]);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int x2 = 0; x2 < HM; x2++)
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++)
+                    acc[h * HM + x2][nt] = mfma_f16(wf[s & 1][nt], xf[g & 1][x2], acc[h * HM + x2][nt]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    uint2_t sc[NT], nsc[NT];
+    dma(0, 0);
+    load_scales(sc, 0);
+    for (int kb = 0; kb < kbs; kb++) {
+        const int cur = kb & 1;
+        // this wave's loads of step kb are done; the barrier covers every wave
+        // (and every wave has finished reading the stage the next loads overwrite)
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0); the compiler sees it too
+        __builtin_amdgcn_s_barrier();
+        if (kb + 1 < kbs) {
+            dma(cur ^ 1, kb + 1);
+            load_scales(nsc, kb + 1);
+        }
+        compute(xs + cur * XSTAGE, ws + cur * WSTAGE, sc);
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) sc[nt] = nsc[nt];
+    }
+
+    // epilogue: acc[mb][nt][v] = Y[row][col + v]
+    const bool vec = (n & 3) == 0 && ((uintptr_t)out & 15) == 0 && (EPI != 3 || ((uintptr_t)residual & 7) == 0);
+#pragma unroll
+    for (int mb = 0; mb < MB; mb++) {
+        const int r = row0 + wm * TM + mb * 16 + j;
+        if (r >= m) continue;
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            const int c = col0 + wn * TN + nt * 16 + 4 * q;
+            if (c >= n) continue;
+            const size_t at = (size_t)r * n + c;
+            float v[4] = {acc[mb][nt][0], acc[mb][nt][1], acc[mb][nt][2], acc[mb][nt][3]};
+            if (EPI == 0) {
+                if (vec) {
+                    *(float4_t *)((float *)out + at) = float4_t{v[0], v[1], v[2], v[3]};
+                } else {
+                    for (int e = 0; e < 4; e++)
+                        if (c + e < n) ((float *)out)[at + e] = v[e];
+                }
+            } else {
+                half_t o[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    if (EPI == 1) o[e] = (half_t)v[e];
+                    else if (EPI == 2) o[e] = (half_t)(0.5f * v[e] * (1.0f + erff(v[e] * 0.70710678118654752f)));
+                    else o[e] = (half_t)0.0f;
+                }
+                if (EPI == 3) {
+                    if (vec) {
+                        const uint2_t rw = *(const uint2_t *)(residual + at);
+                        const half2_t r01 = word_as_half2(rw[0]), r23 = word_as_half2(rw[1]);
+                        o[0] = (half_t)(v[0] + (float)r01[0]);
+                        o[1] = (half_t)(v[1] + (float)r01[1]);
+                        o[2] = (half_t)(v[2] + (float)r23[0]);
+                        o[3] = (half_t)(v[3] + (float)r23[1]);
+                    } else {
+                        for (int e = 0; e < 4; e++)
+                            if (c + e < n) o[e] = (half_t)(v[e] + (float)residual[at + e]);
+                    }
+                }
+                if (vec) {
+                    const half2_t o01 = {o[0], o[1]}, o23 = {o[2], o[3]};
+                    *(uint2_t *)((half_t *)out + at) = uint2_t{half2_as_word(o01), half2_as_word(o23)};
+                } else {
+                    for (int e = 0; e < 4; e++)
+                        if (c + e < n) ((half_t *)out)[at + e] = o[e];
+                }
+            }
+        }
+    }
+}
+
 inline unsigned cdiv(size_t a, size_t b) { return (unsigned)((a + b - 1) / b); }
 
 // ---- variant tables -------------------------------------------------------------
 
 const char *const kGemvNames[] = {"w16", "w8"};
-const char *const kGemmNames[] = {"256x128w2x2", "128x128w2x2", "128x64w2x2"};
+const char *const kGemmNames[] = {"256x256p2w8", "256x128w2x2", "128x128w2x2", "128x64w2x2"};
 const char *const kI8Names[] = {"256x256p2w8", "256x256p4k64w8", "256x128p3w8", "256x128p3",
                                  "128x128w2x2", "256x128w2x2", "64x64w2x2"};
 const char *const kGroupedNames[] = {"wave16x16"};
@@ -1075,14 +1307,33 @@ void gemm_launch(const Weight &w, const half_t *x, int m, void *y, const half_t 
                            w.codes, w.scales, x, m, w.cols, w.rows, w.kblocks(), y, res);
 }
 
+template <int BM, int BN, int WGM, int WGN, int EPI>
+bool w4a16_pipe_launch(const Weight &w, const half_t *x, int m, void *y, const half_t *res, hipStream_t s) {
+    // byte offsets are 32-bit and relative to the block's first row / tile
+    if ((size_t)BM * w.cols * 2 >= ((size_t)1 << 31) || (size_t)(BN / 16) * w.kblocks() * 1024 >= ((size_t)1 << 31))
+        return false;
+    const unsigned blocks = cdiv(m, BM) * cdiv(w.rows, BN);
+    if (w.kind == WeightKind::Q4G32)
+        hipLaunchKernelGGL((w4a16_pipe_kernel<BM, BN, WGM, WGN, true, EPI>), dim3(blocks), dim3(WGM * WGN * 64), 0, s,
+                           w.codes, w.scales, x, m, w.cols, w.rows, w.kblocks(), y, res);
+    else
+        hipLaunchKernelGGL((w4a16_pipe_kernel<BM, BN, WGM, WGN, false, EPI>), dim3(blocks), dim3(WGM * WGN * 64), 0, s,
+                           w.codes, w.scales, x, m, w.cols, w.rows, w.kblocks(), y, res);
+    return true;
+}
+
+// Variant 0 is the pipelined kernel; 1-3 stage through registers. All give
+// the same bits (same f16 dequantization, one MFMA per 32-k run in k order).
 template <int EPI>
 void gemm_dispatch(const Weight &w, const half_t *x, int m, void *y, const half_t *res, int variant,
                    hipStream_t s) {
     switch (variant) {
-        case 1: gemm_launch<128, 128, 2, 2, EPI>(w, x, m, y, res, s); break;
-        case 2: gemm_launch<128, 64, 2, 2, EPI>(w, x, m, y, res, s); break;
-        default: gemm_launch<256, 128, 2, 2, EPI>(w, x, m, y, res, s); break;
+        case 0: if (w4a16_pipe_launch<256, 256, 2, 4, EPI>(w, x, m, y, res, s)) return; break;
+        case 2: gemm_launch<128, 128, 2, 2, EPI>(w, x, m, y, res, s); return;
+        case 3: gemm_launch<128, 64, 2, 2, EPI>(w, x, m, y, res, s); return;
+        default: break;
     }
+    gemm_launch<256, 128, 2, 2, EPI>(w, x, m, y, res, s);
 }
 
 
@@ -1127,7 +1378,7 @@ void gv_launch(const Weight &w, const void *a, const float *sa, int m, int abits
 int variant_count(const char *family) {
     std::string f(family);
     if (f == "gemv") return 2;
-    if (f == "gemm_w4a16") return 3;
+    if (f == "gemm_w4a16") return 4;
     if (f == "i8_gemm") return 7;
     if (f == "grouped") return 1;
     return 0;

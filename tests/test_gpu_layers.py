@@ -142,6 +142,27 @@ def test_small_encoder_matches_composition(ctx, oracle):
     enc.close()
 
 
+def test_encoder_bits_do_not_depend_on_the_gemm_variant(ctx):
+    """The encoder's projections use the f16, GELU and residual epilogues of
+    the W4A16 GEMM; every GEMM variant must give the same forward bits."""
+    torch = pytest.importorskip("torch")
+    cfg = rocm.EncoderConfig(layers=2, hidden=256, heads=4, head_dim=64, ffn=1024, vocab=300, ln_eps=1e-5)
+    enc = ctx.encoder_random(cfg, 11)
+    batch, seq = 3, 200
+    ids = np.random.default_rng(5).integers(0, cfg.vocab, batch * seq).astype(np.int32)
+    outs = []
+    for name in ("256x256p2w8", "256x128w2x2", "128x128w2x2", "128x64w2x2"):
+        ctx.select_variant("gemm_w4a16", name)
+        out = empty((batch, cfg.hidden), torch.float32)
+        enc.forward(dev(ids), batch, seq, out)
+        outs.append((name, host(ctx, out)))
+    ctx.select_variant("gemm_w4a16", rocm_reference("gemm_w4a16"))
+    assert np.isfinite(outs[0][1]).all()
+    for name, o in outs[1:]:
+        assert bits_equal(o, outs[0][1]), name
+    enc.close()
+
+
 def test_config3_encoder_full_size_runs_finite_and_deterministic(ctx):
     torch = pytest.importorskip("torch")
     cfg = rocm.EncoderConfig(layers=24, hidden=1024, heads=16, head_dim=64, ffn=4096, vocab=32000, ln_eps=1e-5)
@@ -184,4 +205,4 @@ def test_tuner_selects_bitwise_equal_variants_and_caches(ctx):
 
 
 def rocm_reference(fam):
-    return {"gemv": "w16", "gemm_w4a16": "256x128w2x2", "i8_gemm": "256x256p2w8"}[fam]
+    return {"gemv": "w16", "gemm_w4a16": "256x256p2w8", "i8_gemm": "256x256p2w8"}[fam]

@@ -248,9 +248,15 @@ def test_w4a16_rejects_misaligned_activations(ctx, oracle):
     assert e.value.code == "INVALID_PARAMETERS"
 
 
+W4A16_VARIANTS = ("256x256p2w8", "256x128w2x2", "128x128w2x2", "128x64w2x2")
+
+
 @pytest.mark.parametrize("layout", [rocm.Q4_G32_F16, rocm.Q4_G64_F32])
-@pytest.mark.parametrize("m,k,n", [(3, 512, 80), (17, 256, 48), (256, 1024, 1024), (1000, 512, 1536), (33, 4096, 272)])
+@pytest.mark.parametrize("m,k,n", [(3, 512, 80), (17, 256, 48), (256, 1024, 1024), (1000, 512, 1536), (33, 4096, 272),
+                                   (300, 576, 200), (513, 192, 1040), (257, 4096, 257)])
 def test_large_m_gemm_vs_closed_form(ctx, oracle, layout, m, k, n):
+    """Every W4A16 GEMM variant against the float64 closed form, and all of
+    them bitwise equal (ragged m and n, k tails inside a 128-k block)."""
     torch = pytest.importorskip("torch")
     rng = np.random.default_rng(m + k + n)
     x = rng.standard_normal((m, k)).astype(np.float32)
@@ -265,7 +271,7 @@ def test_large_m_gemm_vs_closed_form(ctx, oracle, layout, m, k, n):
     xh = oracle.f32_to_f16_bits(x)
     want = oracle.w4a16(xh, m, k, deq, n)
     outs = []
-    for name in ("256x128w2x2", "128x128w2x2", "128x64w2x2"):
+    for name in W4A16_VARIANTS:
         ctx.select_variant("gemm_w4a16", name)
         y = empty((m, n), torch.float32)
         ctx.linear(w, dev(xh.view(np.float16)), rocm.F16, m, y, rocm.W4A16)
@@ -273,9 +279,9 @@ def test_large_m_gemm_vs_closed_form(ctx, oracle, layout, m, k, n):
         assert np.abs(got - want).max() <= MAX_ABS, name
         assert cosine(got, want) >= MIN_COS, name
         outs.append(got)
-    ctx.select_variant("gemm_w4a16", "256x128w2x2")
-    for o in outs[1:]:
-        assert bits_equal(o, outs[0])
+    ctx.select_variant("gemm_w4a16", W4A16_VARIANTS[0])
+    for name, o in zip(W4A16_VARIANTS[1:], outs[1:]):
+        assert bits_equal(o, outs[0]), name
 
 
 def test_config5_prefill_rows_vs_fp32(ctx, oracle):
