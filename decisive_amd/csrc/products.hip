@@ -1029,6 +1029,21 @@ __global__ __launch_bounds__(WGM *WGN * 64) void i8_gemm_pipe_kernel(const int8_
 // pipelined W4A16 GEMM (large M)
 // ============================================================================
 
+// unpack_codes without asm: lo/hi masks come in SGPRs and the exponent in a
+// VGPR, so each (w & mask) | magic is one v_and_or_b32
+__device__ __forceinline__ uint4_t unpack_codes_c(uint32_t w, uint32_t mlo, uint32_t mhi, uint32_t magic) {
+    const half2_t bias = {(half_t)-1032.0f, (half_t)-1032.0f};
+    const half2_t sixteenth = {(half_t)0.0625f, (half_t)0.0625f};
+    const half2_t bias16 = {(half_t)-72.0f, (half_t)-72.0f};
+    const uint32_t w8 = w >> 8;
+    uint4_t out;
+    out[0] = half2_as_word(word_as_half2((w & mlo) | magic) + bias);
+    out[1] = half2_as_word(__builtin_elementwise_fma(word_as_half2((w & mhi) | magic), sixteenth, bias16));
+    out[2] = half2_as_word(word_as_half2((w8 & mlo) | magic) + bias);
+    out[3] = half2_as_word(__builtin_elementwise_fma(word_as_half2((w8 & mhi) | magic), sixteenth, bias16));
+    return out;
+}
+
 typedef int int32x4_t __attribute__((ext_vector_type(4)));
 
 // Raw buffer resource (stride 0, range-checked offsets) over [p, p + bytes).
@@ -1058,18 +1073,19 @@ __device__ __forceinline__ void dma16(uint32_t lds, uint32_t voff, int32x4_t rsr
 //  - activations: BM rows of 256 bytes; chunk c (8 halves) of row r sits at
 //    slot c ^ (r & 15), so the 16 rows of a fragment read fall in distinct
 //    banks. The byte offset of every load is in the VGPR offset, which the
-//    buffer range check covers: rows past m and chunks past k read as zero;
+//    buffer range check covers: rows past m read as zero;
 //  - weight codes: the 1 KiB tile16x128 chunk of each 16-column tile, copied
 //    as is (its lane order is the MFMA operand order);
 //  - scale records go straight to registers, one step ahead.
 // The stage loads are issued as asm (dma16) and waited for at the step's
-// barrier; the one compute body reads whichever stage is current.
+// barrier; the one compute body reads whichever stage is current. Needs
+// k % 128 == 0 (the launcher falls back otherwise).
 // Codes become f16 exactly as in gemm_w4a16_kernel (exact code times the f16
 // scale, rounded once), and each output accumulates one
 // v_mfma_f32_16x16x32_f16 per 32-k run in k order, so both kernels give the
 // same bits. The MFMA is issued as D[n][m] = W . X^T: lane (q, j) ends with
 // four consecutive output columns of one row and stores them as one vector.
-template <int BM, int BN, int WGM, int WGN, bool G32, int EPI>
+template <int BM, int BN, int WGM, int WGN, bool G32, int EPI, int VALU_PER_MFMA = 2>
 __global__ __launch_bounds__(WGM *WGN * 64) void w4a16_pipe_kernel(
     const uint8_t *__restrict__ codes, const uint8_t *__restrict__ scales, const half_t *__restrict__ x, int m,
     int k, int n, int kbs, void *__restrict__ out, const half_t *__restrict__ residual) {
@@ -1101,22 +1117,25 @@ __global__ __launch_bounds__(WGM *WGN * 64) void w4a16_pipe_kernel(
     // 4*blk + q, whose source chunk is j ^ (row & 15) = j ^ q ^ 4*(blk & 3).
     const uint32_t xlane = (uint32_t)(q * k * 2);
     const int cx = j ^ q;
-    auto dma = [&](int stage, int kb) {
+    constexpr int DMA_GROUPS = 4;  // the next step's loads are spread over the first groups
+    constexpr int DMA_N = XPW + WPW;
+    // loads [DMA_N*part/DMA_GROUPS, DMA_N*(part+1)/DMA_GROUPS) of one stage
+    // (k % 128 == 0: every chunk of a step is inside the row)
+    auto dma_part = [&](int stage, int kb, int part, int32x4_t rx, int32x4_t rw) {
         const int kk = kb * 128;
-        const bool whole = kk + 128 <= k;
 #pragma unroll
-        for (int p = 0; p < XPW; p++) {
-            const int c = cx ^ (4 * (p & 3));
-            const int blk = wave * XPW + p;
-            uint32_t voff = xlane + (uint32_t)(blk * 4 * k * 2 + kk * 2) + (uint32_t)(c * 16);
-            if (!whole && kk + 8 * c >= k) voff = 0x80000000u;
-            dma16(__builtin_amdgcn_readfirstlane(xs_lds + stage * XSTAGE + blk * 1024), voff, rsx);
-        }
-#pragma unroll
-        for (int p = 0; p < WPW; p++) {
-            const int t = wave * WPW + p;
-            dma16(__builtin_amdgcn_readfirstlane(ws_lds + stage * WSTAGE + t * 1024),
-                  (uint32_t)((t * kbs + kb) * 1024 + lane * 16), rsw);
+        for (int p = 0; p < DMA_N; p++) {
+            if (p < DMA_N * part / DMA_GROUPS || p >= DMA_N * (part + 1) / DMA_GROUPS) continue;
+            if (p < XPW) {
+                const int c = cx ^ (4 * (p & 3));
+                const int blk = wave * XPW + p;
+                const uint32_t voff = xlane + (uint32_t)(blk * 4 * k * 2 + kk * 2) + (uint32_t)(c * 16);
+                dma16(__builtin_amdgcn_readfirstlane(xs_lds + stage * XSTAGE + blk * 1024), voff, rx);
+            } else {
+                const int t = wave * WPW + (p - XPW);
+                dma16(__builtin_amdgcn_readfirstlane(ws_lds + stage * WSTAGE + t * 1024),
+                      (uint32_t)((t * kbs + kb) * 1024 + lane * 16), rw);
+            }
         }
     };
     // scale records of this wave's tiles (clamped to a real tile past n): a
@@ -1136,25 +1155,11 @@ __global__ __launch_bounds__(WGM *WGN * 64) void w4a16_pipe_kernel(
 #pragma unroll
         for (int b = 0; b < NT; b++) acc[a][b] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-    const uint32_t magic = 0x64006400u;
+    // nibble masks in SGPRs and the f16 exponent in a VGPR (held opaque so
+    // they are not folded back into literals, which v_and_or_b32 cannot take)
+    uint32_t mlo = 0x000F000Fu, mhi = 0x00F000F0u, magic_v = 0x64006400u;
+    asm volatile("" : "+s"(mlo), "+s"(mhi), "+v"(magic_v));
     constexpr int HM = MB / 2;  // activation fragments per group
-    // word s of this wave's code chunks -> the f16 weight fragments of run s
-    auto dequant = [&](const uint8_t *wst, const uint2_t *sc, int s, half8_t *wf) {
-#pragma unroll
-        for (int nt = 0; nt < NT; nt++) {
-            const uint32_t word = *(const uint32_t *)(wst + ((wn * NT + nt) * 64 + lane) * 16 + 4 * s);
-            half_t sh;
-            if (G32)
-                sh = __builtin_bit_cast(half_t, (unsigned short)((sc[nt][s >> 1] >> (16 * (s & 1))) & 0xffffu));
-            else
-                sh = (half_t)word_as_float(sc[nt][s >> 1]);
-            const half2_t s2 = {sh, sh};
-            uint4_t c8 = unpack_codes(word, magic);
-#pragma unroll
-            for (int e = 0; e < 4; e++) c8[e] = half2_as_word(word_as_half2(c8[e]) * s2);
-            wf[nt] = as_half8(c8);
-        }
-    };
     // Activation rows of this wave are r = wm*TM + 16*mb + j, so r & 15 = j.
     // Group g = 2s + h covers run s and fragment rows h*HM .. h*HM + HM - 1.
     auto read_x = [&](const uint8_t *xst, int g, half8_t *xf) {
@@ -1163,28 +1168,63 @@ __global__ __launch_bounds__(WGM *WGN * 64) void w4a16_pipe_kernel(
 #pragma unroll
         for (int x2 = 0; x2 < HM; x2++) xf[x2] = *(const half8_t *)(base + x2 * 16 * 256);
     };
-    auto compute = [&](const uint8_t *xst, const uint8_t *wst, const uint2_t *sc) {
+    // word s of the code chunks of tiles [t0, t1) -> f16 weight fragments of
+    // run s. A lane's 16-byte chunk is read whole at run 0 (lanes 16 bytes
+    // apart: no bank conflicts, unlike one 4-byte word per lane).
+    uint4_t cw[NT];
+    auto dequant_part = [&](const uint8_t *wst, const uint2_t *sc, int s, half8_t *wf, int t0, int t1) {
+#pragma unroll
+        for (int nt = t0; nt < t1; nt++) {
+            if (s == 0) cw[nt] = *(const uint4_t *)(wst + ((wn * NT + nt) * 64 + lane) * 16);
+            const uint32_t word = cw[nt][s];
+            half_t sh;
+            if (G32)
+                sh = __builtin_bit_cast(half_t, (unsigned short)((sc[nt][s >> 1] >> (16 * (s & 1))) & 0xffffu));
+            else
+                sh = (half_t)word_as_float(sc[nt][s >> 1]);
+            const half2_t s2 = {sh, sh};
+            uint4_t c8 = unpack_codes_c(word, mlo, mhi, magic_v);
+#pragma unroll
+            for (int e = 0; e < 4; e++) c8[e] = half2_as_word(word_as_half2(c8[e]) * s2);
+            wf[nt] = as_half8(c8);
+        }
+    };
+    // Group g = 2s + h: 16 MFMAs of run s on fragment rows h*HM.., interleaved
+    // (sched_group_barrier) with the next group's activation reads, half of
+    // run s+1's dequantization and, in the first DMA_GROUPS groups, a slice
+    // of the next step's stage loads.
+    auto compute = [&](const uint8_t *xst, const uint8_t *wst, const uint2_t *sc, int next_stage, int next_kb,
+                       int32x4_t rx, int32x4_t rw) {
         half8_t xf[2][HM], wf[2][NT];
         read_x(xst, 0, xf[0]);
-        dequant(wst, sc, 0, wf[0]);
+        dequant_part(wst, sc, 0, wf[0], 0, NT);
 #pragma unroll
         for (int g = 0; g < 8; g++) {
             const int s = g / 2, h = g % 2;
-            // the next group's operands are fetched while this group's MFMAs run
+            if (g < DMA_GROUPS) dma_part(next_stage, next_kb, g, rx, rw);
             if (g + 1 < 8) read_x(xst, g + 1, xf[(g + 1) & 1]);
-            if (h == 1 && s + 1 < 4) dequant(wst, sc, s + 1, wf[(s + 1) & 1]);
-            __builtin_amdgcn_sched_barrier(0);
+            if (s + 1 < 4) dequant_part(wst, sc, s + 1, wf[(s + 1) & 1], h * NT / 2, (h + 1) * NT / 2);
 #pragma unroll
             for (int x2 = 0; x2 < HM; x2++)
 #pragma unroll
                 for (int nt = 0; nt < NT; nt++)
                     acc[h * HM + x2][nt] = mfma_f16(wf[s & 1][nt], xf[g & 1][x2], acc[h * HM + x2][nt]);
+            // one MFMA, then a share of the reads and VALU work, repeated
+#pragma unroll
+            for (int i = 0; i < HM * NT; i++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                if (i < HM + 1) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, VALU_PER_MFMA, 0);
+            }
             __builtin_amdgcn_sched_barrier(0);
         }
     };
 
     uint2_t sc[NT], nsc[NT];
-    dma(0, 0);
+#pragma unroll
+    for (int part = 0; part < DMA_GROUPS; part++) dma_part(0, 0, part, rsx, rsw);
+    // the last step's "next" loads go to a zero-length buffer: no traffic, no branch
+    const int32x4_t none = {rsx[0], rsx[1], 0, rsx[3]};
     load_scales(sc, 0);
     for (int kb = 0; kb < kbs; kb++) {
         const int cur = kb & 1;
@@ -1192,14 +1232,13 @@ __global__ __launch_bounds__(WGM *WGN * 64) void w4a16_pipe_kernel(
         // (and every wave has finished reading the stage the next loads overwrite)
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0); the compiler sees it too
         __builtin_amdgcn_s_barrier();
-        if (kb + 1 < kbs) {
-            dma(cur ^ 1, kb + 1);
-            load_scales(nsc, kb + 1);
-        }
-        compute(xs + cur * XSTAGE, ws + cur * WSTAGE, sc);
+        const bool more = kb + 1 < kbs;
+        if (more) load_scales(nsc, kb + 1);
+        compute(xs + cur * XSTAGE, ws + cur * WSTAGE, sc, cur ^ 1, kb + 1, more ? rsx : none, more ? rsw : none);
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) sc[nt] = nsc[nt];
     }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // no LDS write in flight once the block ends
 
     // epilogue: acc[mb][nt][v] = Y[row][col + v]
     const bool vec = (n & 3) == 0 && ((uintptr_t)out & 15) == 0 && (EPI != 3 || ((uintptr_t)residual & 7) == 0);
@@ -1309,8 +1348,9 @@ void gemm_launch(const Weight &w, const half_t *x, int m, void *y, const half_t 
 
 template <int BM, int BN, int WGM, int WGN, int EPI>
 bool w4a16_pipe_launch(const Weight &w, const half_t *x, int m, void *y, const half_t *res, hipStream_t s) {
-    // byte offsets are 32-bit and relative to the block's first row / tile
-    if ((size_t)BM * w.cols * 2 >= ((size_t)1 << 31) || (size_t)(BN / 16) * w.kblocks() * 1024 >= ((size_t)1 << 31))
+    // whole 128-k steps; byte offsets are 32-bit and relative to the block's first row / tile
+    if (w.cols % 128 != 0 || (size_t)BM * w.cols * 2 >= ((size_t)1 << 31) ||
+        (size_t)(BN / 16) * w.kblocks() * 1024 >= ((size_t)1 << 31))
         return false;
     const unsigned blocks = cdiv(m, BM) * cdiv(w.rows, BN);
     if (w.kind == WeightKind::Q4G32)
