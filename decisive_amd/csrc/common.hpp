@@ -104,6 +104,30 @@ __device__ __forceinline__ float f16_bits_to_float(uint32_t h) {
     return (float)__builtin_bit_cast(half_t, (unsigned short)h);
 }
 
+typedef int int32x4_t __attribute__((ext_vector_type(4)));
+
+// Raw buffer resource (stride 0, range-checked offsets) over [p, p + bytes).
+__device__ __forceinline__ int32x4_t buffer_rsrc(const void *p, uint32_t bytes) {
+    const uint64_t a = (uint64_t)(uintptr_t)p;
+    return int32x4_t{(int)(uint32_t)a, (int)((uint32_t)(a >> 32) & 0xffffu), (int)bytes, 0x00020000};
+}
+
+// 32-bit LDS address of a __shared__ object
+__device__ __forceinline__ uint32_t lds_address(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+// buffer_load_dwordx4 ... lds: lane l's 16 bytes at rsrc + voff land at
+// LDS lds + 16 * l. Issued as asm so that the compiler does not add waits
+// for it before LDS reads of other buffers; the caller waits (s_waitcnt
+// vmcnt + s_barrier) before reading what it wrote.
+__device__ __forceinline__ void dma16(uint32_t lds, uint32_t voff, int32x4_t rsrc) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(lds), "v"(voff), "s"(rsrc)
+                 : "memory", "m0");
+}
+
 // ---- host helpers ------------------------------------------------------------
 
 struct Status {

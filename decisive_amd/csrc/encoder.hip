@@ -230,6 +230,7 @@ int32_t encoder_forward(dz_ctx *ctx, dz_encoder *e, const int32_t *ids_dev, cons
     if (batch == 0 || seq == 0) return ctx_fail(ctx, DZ_INVALID_REQUEST, "empty batch");
     size_t tokens = batch * seq;
     if (tokens > (1u << 20)) return ctx_fail(ctx, DZ_INPUT_TOO_LONG, "input budget exceeded");
+    if (!attention_fits(seq, (size_t)e->cfg.heads)) return ctx_fail(ctx, DZ_INPUT_TOO_LONG, "sequence too long");
     int32_t rc = ensure_capacity(ctx, e, tokens);
     if (rc) return rc;
     const dz_encoder_config &c = e->cfg;

@@ -184,115 +184,185 @@ __global__ void mean_rows_kernel(const void *__restrict__ x, int dtype, int batc
 
 // ---- flash attention, head_dim 64 ----------------------------------------------------
 //
-// Block = 4 waves = 64 queries of one (batch, head). Scores are computed
-// transposed, S^T = K Q^T, so a lane's accumulator column is one query: the
-// online-softmax rescale is a per-lane scalar and the P^T values a lane holds
-// (keys 16*kb + 4*qd + v) are exactly the keys it feeds to O^T = V^T P^T when
-// the MFMA k-slots are labelled (kb pair, v). V is staged transposed in LDS.
-constexpr int kAttnKeys = 64;
-constexpr int kVStride = 72;  // halfs per V^T row (padding against bank conflicts)
+// Block = 8 waves x 32 queries of one (batch, head); keys in steps of 64,
+// K and V tiles (64 rows x 128 bytes each) double-buffered in LDS by
+// buffer_load ... lds, so each K/V row is read from L2 once per 256 queries.
+// Scores are computed transposed, S^T = K Q^T (v_mfma_f32_16x16x32_f16, A =
+// K rows from LDS, B = Q rows held in registers), so a lane's accumulator
+// column is one query: the online-softmax max, sum and rescale are per-lane
+// scalars. O^T = V^T P^T: the P^T values a lane holds (keys 16kb + 4q + v of
+// query j) are the B operand when the MFMA k-slots of a 32-key block c are
+// labelled 8q + e -> key 32c + 16(e / 4) + 4q + e % 4, and the matching V^T
+// operand (8 keys of one dh per lane) is read with ds_read_b64_tr_b16, whose
+// 16-lane groups give lane 4a + b element b of the 8-byte chunks addressed by
+// lanes a, a + 4, a + 8, a + 12.
+// LDS swizzles (bank-conflict free for both reads and the loads):
+//   K: 16-byte chunk c of row r at slot c ^ ((r >> 1) & 7)
+//   V: 8-byte unit u of row r at unit u ^ (4 * ((r >> 1) & 3))
+constexpr int kAttnWaves = 8;
+constexpr int kAttnQB = 2;                                // 16-query blocks per wave
+constexpr int kAttnQueries = kAttnWaves * kAttnQB * 16;  // per block
+constexpr int kAttnKeys = 64;                             // per step
 
-__global__ __launch_bounds__(256) void attention_kernel(const half_t *__restrict__ qkv,
-                                                        half_t *__restrict__ out, int seq,
-                                                        int heads, float scale_log2) {
-    __shared__ __align__(16) half_t ks[kAttnKeys * 64];
-    __shared__ __align__(16) half_t vt[64 * kVStride];
-    const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
-    const int qd = lane / 16, j = lane % 16;
-    const int qblock = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+typedef short short4_t __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(const half_t *__restrict__ qkv,
+                                                                    half_t *__restrict__ out, int seq,
+                                                                    int heads, float scale_log2) {
+    __shared__ __align__(16) uint8_t ks[2 * kAttnKeys * 128];
+    __shared__ __align__(16) uint8_t vs[2 * kAttnKeys * 128];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), lane = threadIdx.x % 64;
+    const int q4 = lane / 16, j = lane % 16;
+    const int h = blockIdx.y, b = blockIdx.z;
     const int width = heads * 64;
-    const size_t ld3 = (size_t)3 * width;
+    const size_t ld3 = (size_t)3 * width;  // halves per token row of qkv
     const half_t *base = qkv + (size_t)b * seq * ld3;
-    const int query = qblock * 64 + wave * 16 + j;
-    const bool qok = query < seq;
+    const int32x4_t rs = buffer_rsrc(base, (uint32_t)((size_t)seq * ld3 * 2));
+    const uint32_t ks_lds = lds_address(ks), vs_lds = lds_address(vs);
 
-    // Q^T fragments: lane (qd, j) holds Q[query j][dh 8qd + e] for dh halves 0/1.
-    half8_t qf[2];
-    for (int ds = 0; ds < 2; ds++) {
-        half8_t v = {};
-        if (qok) v = *(const half8_t *)(base + (size_t)query * ld3 + h * 64 + ds * 32 + qd * 8);
-        qf[ds] = v;
+    // Q^T fragments: lane (q4, j) holds Q[query j][dh 32ds + 8q4 + e]
+    const int q0 = blockIdx.x * kAttnQueries + wave * (kAttnQB * 16);
+    half8_t qf[kAttnQB][2];
+#pragma unroll
+    for (int qb = 0; qb < kAttnQB; qb++) {
+        const int query = q0 + qb * 16 + j;
+#pragma unroll
+        for (int ds = 0; ds < 2; ds++) {
+            half8_t v = {};
+            if (query < seq) v = *(const half8_t *)(base + (size_t)query * ld3 + h * 64 + ds * 32 + q4 * 8);
+            qf[qb][ds] = v;
+        }
     }
+
+    // Stage loads: wave w copies K rows 8w..8w+7 and V rows 8w..8w+7 of a
+    // step (one instruction each; lane l -> row 8w + l/8, 16-byte slot l%8).
+    const int lrow = wave * 8 + lane / 8, lslot = lane % 8;
+    const uint32_t koff = (uint32_t)(lrow * ld3 * 2 + width * 2 + h * 128 + ((lslot ^ ((lrow >> 1) & 7)) * 16));
+    const uint32_t voff = (uint32_t)(lrow * ld3 * 2 + 2 * width * 2 + h * 128 + ((lslot ^ (2 * ((lrow >> 1) & 3))) * 16));
+    const uint32_t step_bytes = (uint32_t)(kAttnKeys * ld3 * 2);
+    auto load_step = [&](int stage, int step) {
+        dma16(__builtin_amdgcn_readfirstlane(ks_lds + stage * kAttnKeys * 128 + wave * 1024), koff + step * step_bytes, rs);
+        dma16(__builtin_amdgcn_readfirstlane(vs_lds + stage * kAttnKeys * 128 + wave * 1024), voff + step * step_bytes, rs);
+    };
+
     const float4_t fz = {0.f, 0.f, 0.f, 0.f};
-    float4_t o[4] = {fz, fz, fz, fz};  // O^T[dh 16*db + 4qd + v][query j]
-    float mrow = -INFINITY, lsum = 0.0f;
+    float4_t o[kAttnQB][4];  // O^T[dh 16db + 4q4 + v][query j]
+    float mrow[kAttnQB], lsum[kAttnQB];
+#pragma unroll
+    for (int qb = 0; qb < kAttnQB; qb++) {
+        mrow[qb] = -INFINITY;
+        lsum[qb] = 0.0f;
+#pragma unroll
+        for (int db = 0; db < 4; db++) o[qb][db] = fz;
+    }
 
-    for (int k0 = 0; k0 < seq; k0 += kAttnKeys) {
-        __syncthreads();
-        // stage K (row-major, 16-byte chunks swizzled) and V^T
-        for (int c = threadIdx.x; c < kAttnKeys * 8; c += 256) {
-            int kr = c / 8, ch = c % 8;
-            int key = k0 + kr;
-            uint4_t kv = {0u, 0u, 0u, 0u}, vv = {0u, 0u, 0u, 0u};
-            if (key < seq) {
-                const half_t *row = base + (size_t)key * ld3 + h * 64 + ch * 8;
-                kv = *(const uint4_t *)(row + width);
-                vv = *(const uint4_t *)(row + 2 * width);
-            }
-            *(uint4_t *)(ks + kr * 64 + ((ch ^ (kr & 7)) * 8)) = kv;
-            half8_t vh = as_half8(vv);
-            for (int e = 0; e < 8; e++) vt[(ch * 8 + e) * kVStride + kr] = vh[e];
-        }
-        __syncthreads();
-        // S^T for 64 keys: 4 key blocks x 2 dh halves
-        float4_t sc[4];
+    const int steps = (seq + kAttnKeys - 1) / kAttnKeys;
+    load_step(0, 0);
+    for (int st = 0; st < steps; st++) {
+        const int cur = st & 1;
+        // this wave's loads of step st are done; the barrier covers every wave
+        // (and every wave has finished reading the stage the next loads overwrite)
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+        __builtin_amdgcn_s_barrier();
+        if (st + 1 < steps) load_step(cur ^ 1, st + 1);
+        const uint8_t *kst = ks + cur * kAttnKeys * 128;
+        const uint8_t *vst = vs + cur * kAttnKeys * 128;
+
+        // S^T for 64 keys: sc[qb][kb][v] = S^T[key 16kb + 4q4 + v][query j]
+        float4_t sc[kAttnQB][4];
+#pragma unroll
         for (int kb = 0; kb < 4; kb++) {
-            float4_t acc = fz;
-            int kr = kb * 16 + j;  // A row = key (lane%16)
-            for (int ds = 0; ds < 2; ds++) {
-                int ch = ds * 4 + qd;
-                half8_t a = *(const half8_t *)(ks + kr * 64 + ((ch ^ (kr & 7)) * 8));
-                acc = mfma_f16(a, qf[ds], acc);
+            const int r = kb * 16 + j;
+            half8_t kf[2];
+#pragma unroll
+            for (int ds = 0; ds < 2; ds++) kf[ds] = *(const half8_t *)(kst + r * 128 + (((ds * 4 + q4) ^ ((r >> 1) & 7)) * 16));
+#pragma unroll
+            for (int qb = 0; qb < kAttnQB; qb++) {
+                float4_t acc = mfma_f16(kf[0], qf[qb][0], fz);
+                sc[qb][kb] = mfma_f16(kf[1], qf[qb][1], acc);
             }
-            sc[kb] = acc;  // lane holds S^T[key 16kb + 4qd + v][query j]
         }
-        // online softmax over keys for query j (lanes j, j+16, j+32, j+48)
-        float bmax = -INFINITY;
-        for (int kb = 0; kb < 4; kb++)
-            for (int v = 0; v < 4; v++) {
-                int key = k0 + kb * 16 + qd * 4 + v;
-                float s = key < seq ? sc[kb][v] * scale_log2 : -INFINITY;
-                sc[kb][v] = s;
-                bmax = fmaxf(bmax, s);
-            }
-        bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
-        bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
-        float mnew = fmaxf(mrow, bmax);
-        float alpha = __builtin_amdgcn_exp2f(mrow - mnew);
-        mrow = mnew;
-        lsum *= alpha;
-        for (int db = 0; db < 4; db++)
-            for (int v = 0; v < 4; v++) o[db][v] *= alpha;
-        half_t p[4][4];
-        for (int kb = 0; kb < 4; kb++)
-            for (int v = 0; v < 4; v++) {
-                float e = __builtin_amdgcn_exp2f(sc[kb][v] - mnew);
-                lsum += e;
-                p[kb][v] = (half_t)e;
-            }
-        // O^T += V^T P^T: two 32-slot steps, slots = (kb pair, v)
-        for (int c = 0; c < 2; c++) {
-            half8_t bfr = {p[2 * c][0], p[2 * c][1], p[2 * c][2], p[2 * c][3],
-                           p[2 * c + 1][0], p[2 * c + 1][1], p[2 * c + 1][2], p[2 * c + 1][3]};
+        // V^T fragments of the two 32-key blocks: vf[c][db] (8 keys of dh 16db + j)
+        half8_t vf[2][4];
+#pragma unroll
+        for (int c = 0; c < 2; c++)
+#pragma unroll
             for (int db = 0; db < 4; db++) {
-                int dh = db * 16 + j;  // A row = dh (lane%16)
-                const half_t *vr = vt + dh * kVStride;
-                uint2_t lo = *(const uint2_t *)(vr + (2 * c) * 16 + qd * 4);
-                uint2_t hi = *(const uint2_t *)(vr + (2 * c + 1) * 16 + qd * 4);
-                uint4_t av = {lo[0], lo[1], hi[0], hi[1]};
-                o[db] = mfma_f16(as_half8(av), bfr, o[db]);
+                short4_t part[2];
+#pragma unroll
+                for (int r2 = 0; r2 < 2; r2++) {
+                    // lane 16g + 4v + a addresses row 32c + 16r2 + 4g + v, unit 4db + a
+                    const int row = 32 * c + 16 * r2 + 4 * q4 + (j >> 2);
+                    const int unit = (4 * db + (j & 3)) ^ (4 * ((row >> 1) & 3));
+                    part[r2] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (__attribute__((address_space(3))) short4_t *)(vst + row * 128 + unit * 8));
+                }
+                const uint2_t lo = __builtin_bit_cast(uint2_t, part[0]), hi = __builtin_bit_cast(uint2_t, part[1]);
+                vf[c][db] = as_half8(uint4_t{lo[0], lo[1], hi[0], hi[1]});
+            }
+
+        const bool ragged = (st + 1) * kAttnKeys > seq;
+#pragma unroll
+        for (int qb = 0; qb < kAttnQB; qb++) {
+            // online softmax over this step's keys for query j (lanes j, j+16, j+32, j+48)
+            if (ragged) {
+#pragma unroll
+                for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+                    for (int v = 0; v < 4; v++)
+                        if (st * kAttnKeys + kb * 16 + q4 * 4 + v >= seq) sc[qb][kb][v] = -INFINITY;
+            }
+            float bmax = -INFINITY;
+#pragma unroll
+            for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+                for (int v = 0; v < 4; v++) bmax = fmaxf(bmax, sc[qb][kb][v]);
+            bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
+            bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+            const float mnew = fmaxf(mrow[qb], bmax);
+            const float alpha = __builtin_amdgcn_exp2f((mrow[qb] - mnew) * scale_log2);
+            mrow[qb] = mnew;
+            const float moff = -mnew * scale_log2;
+            lsum[qb] *= alpha;
+#pragma unroll
+            for (int db = 0; db < 4; db++)
+#pragma unroll
+                for (int v = 0; v < 4; v++) o[qb][db][v] *= alpha;
+            half_t p[4][4];
+#pragma unroll
+            for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[qb][kb][v], scale_log2, moff));
+                    lsum[qb] += e;
+                    p[kb][v] = (half_t)e;
+                }
+            // O^T += V^T P^T over the two 32-key blocks
+#pragma unroll
+            for (int c = 0; c < 2; c++) {
+                const half8_t pf = {p[2 * c][0], p[2 * c][1], p[2 * c][2], p[2 * c][3],
+                                    p[2 * c + 1][0], p[2 * c + 1][1], p[2 * c + 1][2], p[2 * c + 1][3]};
+#pragma unroll
+                for (int db = 0; db < 4; db++) o[qb][db] = mfma_f16(vf[c][db], pf, o[qb][db]);
             }
         }
     }
-    lsum += __shfl_xor(lsum, 16);
-    lsum += __shfl_xor(lsum, 32);
-    if (!qok) return;
-    float inv = 1.0f / lsum;
-    half_t *dst = out + ((size_t)b * seq + query) * width + h * 64;
-    for (int db = 0; db < 4; db++) {
-        half_t r[4];
-        for (int v = 0; v < 4; v++) r[v] = (half_t)(o[db][v] * inv);
-        *(uint2_t *)(dst + db * 16 + qd * 4) = *(uint2_t *)r;
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // no LDS write in flight once the block ends
+#pragma unroll
+    for (int qb = 0; qb < kAttnQB; qb++) {
+        float l = lsum[qb];
+        l += __shfl_xor(l, 16);
+        l += __shfl_xor(l, 32);
+        const int query = q0 + qb * 16 + j;
+        if (query >= seq) continue;
+        const float inv = 1.0f / l;
+        half_t *dst = out + ((size_t)b * seq + query) * width + h * 64;
+#pragma unroll
+        for (int db = 0; db < 4; db++) {
+            const half2_t r01 = {(half_t)(o[qb][db][0] * inv), (half_t)(o[qb][db][1] * inv)};
+            const half2_t r23 = {(half_t)(o[qb][db][2] * inv), (half_t)(o[qb][db][3] * inv)};
+            *(uint2_t *)(dst + db * 16 + q4 * 4) = uint2_t{half2_as_word(r01), half2_as_word(r23)};
+        }
     }
 }
 
@@ -367,8 +437,8 @@ void launch_attention(const half_t *qkv, half_t *out, int batch, int seq, int he
                       float scale, hipStream_t s) {
     (void)dh;
     if (!batch || !seq) return;
-    dim3 grid(cdiv(seq, 64), heads, batch);
-    hipLaunchKernelGGL(attention_kernel, grid, dim3(256), 0, s, qkv, out, seq, heads,
+    dim3 grid(cdiv(seq, kAttnQueries), heads, batch);
+    hipLaunchKernelGGL(attention_kernel, grid, dim3(kAttnWaves * 64), 0, s, qkv, out, seq, heads,
                        scale * 1.4426950408889634f);
 }
 void launch_fill_normal_f32(float *p, size_t n, uint64_t seed, float stddev, hipStream_t s) {

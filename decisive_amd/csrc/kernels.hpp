@@ -74,6 +74,11 @@ void launch_add(void *x, const void *y, int dtype, size_t n, hipStream_t s);
 void launch_softmax_rows(float *x, int rows, int n, hipStream_t s);
 void launch_mean_rows(const void *x, int dtype, int batch, int rows, int d, float *out,
                       hipStream_t s);
+// The attention kernel addresses one sequence of qkv rows with 32-bit byte
+// offsets: (seq + 64) * 3 * heads * 64 halves must stay below 2^31 bytes.
+inline bool attention_fits(size_t seq, size_t heads) {
+    return (seq + 64) * 3 * heads * 64 * 2 < ((size_t)1 << 31);
+}
 void launch_attention(const half_t *qkv, half_t *out, int batch, int seq, int heads, int dh,
                       float scale, hipStream_t s);
 void launch_fill_normal_f32(float *p, size_t n, uint64_t seed, float stddev, hipStream_t s);

@@ -652,6 +652,7 @@ int32_t dz_attention(dz_ctx *ctx, const void *qkv, void *out, size_t batch, size
     DZ_BEGIN(ctx);
     if (dh != 64) return fail(ctx, DZ_INVALID_PARAMETERS, "attention needs head_dim 64");
     if (batch && seq && (!qkv || !out || heads == 0)) return fail(ctx, DZ_INVALID_REQUEST, "null pointer");
+    if (!dz::attention_fits(seq, heads)) return fail(ctx, DZ_INPUT_TOO_LONG, "attention sequence too long");
     dz::launch_attention((const dz::half_t *)qkv, (dz::half_t *)out, (int)batch, (int)seq, (int)heads,
                          (int)dh, scale, ctx->stream);
     return launched(ctx, "attention");

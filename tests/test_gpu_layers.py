@@ -68,7 +68,7 @@ def test_layernorm_f16_rows(ctx, oracle, d):
     assert np.allclose(got, ref, atol=1e-2, rtol=2e-3)
 
 
-@pytest.mark.parametrize("batch,seq,heads", [(1, 64, 1), (2, 100, 3), (1, 1024, 2)])
+@pytest.mark.parametrize("batch,seq,heads", [(1, 64, 1), (2, 100, 3), (1, 1024, 2), (3, 300, 2), (1, 513, 1), (2, 1, 2)])
 def test_attention_matches_closed_form(ctx, oracle, batch, seq, heads):
     torch = pytest.importorskip("torch")
     rng = np.random.default_rng(seq)
@@ -83,6 +83,16 @@ def test_attention_matches_closed_form(ctx, oracle, batch, seq, heads):
         ref = oracle.attention(q, k, v, heads, 1 / 8)
         assert np.abs(got[sl] - ref).max() <= 5e-3
         assert cosine(got[sl], ref) >= 0.9999
+
+
+def test_attention_rejects_sequences_past_32bit_offsets(ctx):
+    """Rejected on the host before any launch (the kernel's byte offsets are 32-bit)."""
+    torch = pytest.importorskip("torch")
+    small = empty((64, 3 * 1024), torch.float16)
+    out = empty((64, 1024), torch.float16)
+    with pytest.raises(rocm.DzError) as e:
+        ctx.attention(small, out, 1, 400000, 16, 64, 1 / 8)
+    assert e.value.code == "INPUT_TOO_LONG"
 
 
 def _encoder_reference(ctx, enc, cfg, ids, batch, seq):
