@@ -104,6 +104,28 @@ __device__ __forceinline__ float f16_bits_to_float(uint32_t h) {
     return (float)__builtin_bit_cast(half_t, (unsigned short)h);
 }
 
+// erf(x) by Abramowitz & Stegun, Handbook of Mathematical Functions (1964),
+// formula 7.1.26: erf(x) = 1 - (a1 t + a2 t^2 + a3 t^3 + a4 t^4 + a5 t^5) e^(-x^2)
+// with t = 1 / (1 + p x) for x >= 0, |error| <= 1.5e-7, odd extension for x < 0.
+// Branch-free (one reciprocal, one exp2); used by the erf-GELU epilogues.
+__device__ __forceinline__ float erf_as7126(float x) {
+    const float ax = fabsf(x);
+    const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.3275911f, ax, 1.0f));
+    float p = 1.061405429f;
+    p = __builtin_fmaf(p, t, -1.453152027f);
+    p = __builtin_fmaf(p, t, 1.421413741f);
+    p = __builtin_fmaf(p, t, -0.284496736f);
+    p = __builtin_fmaf(p, t, 0.254829592f);
+    p *= t;
+    const float e = __builtin_amdgcn_exp2f(-(ax * ax) * 1.4426950408889634f);
+    return __builtin_copysignf(__builtin_fmaf(-p, e, 1.0f), x);
+}
+
+// erf-GELU: 0.5 x (1 + erf(x / sqrt(2)))
+__device__ __forceinline__ float gelu_erf(float x) {
+    return 0.5f * x * (1.0f + erf_as7126(x * 0.70710678118654752f));
+}
+
 typedef int int32x4_t __attribute__((ext_vector_type(4)));
 
 // Raw buffer resource (stride 0, range-checked offsets) over [p, p + bytes).

@@ -2,7 +2,8 @@
 //
 // Reference behaviour:
 //  - LayerNorm with bias:  src/models/decima/cpu.rs:529-540
-//  - erf GELU:             src/models/decima/cpu.rs:542-556
+//  - erf GELU:             src/models/decima/cpu.rs:542-556 (erf by Abramowitz &
+//                          Stegun 7.1.26, |error| <= 1.5e-7; the reference calls libm erff)
 //  - zero-centred RMSNorm: src/models/pplx_flash/cpu.rs:310-333
 //  - SiLU * up:            src/models/pplx_flash/cpu.rs:348-371, 513-518
 //  - residual add:         src/models/pplx_flash/cpu.rs:334-347
@@ -134,7 +135,7 @@ __global__ void gelu_kernel(void *x, int dtype, size_t n) {
     size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
     if (i >= n) return;
     float v = ld(x, dtype, i);
-    st(x, dtype, i, 0.5f * v * (1.0f + erff(v * 0.70710678118654752f)));
+    st(x, dtype, i, gelu_erf(v));
 }
 
 __global__ void silu_mul_kernel(float *g, const float *u, size_t n) {
@@ -172,14 +173,24 @@ __global__ __launch_bounds__(256) void softmax_rows_kernel(float *x, int n) {
 }
 
 // out[b][c] = mean over rows of x[b][r][c]; one thread per (b, c).
-__global__ void mean_rows_kernel(const void *__restrict__ x, int dtype, int batch, int rows, int d,
-                                 float *__restrict__ out) {
-    size_t id = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
-    if (id >= (size_t)batch * d) return;
-    int c = (int)(id % d), b = (int)(id / d);
+// Block (b, column group of 64): thread (g, c) sums rows g, g + 16, ... of
+// column 64*blockIdx.x + c, then the 16 partial sums of a column are added
+// in g order: a fixed order, so the result does not depend on timing.
+__global__ __launch_bounds__(1024) void mean_rows_kernel(const void *__restrict__ x, int dtype, int batch,
+                                                         int rows, int d, float *__restrict__ out) {
+    __shared__ float part[16][65];
+    const int c = threadIdx.x % 64, g = threadIdx.x / 64;
+    const int col = blockIdx.x * 64 + c, b = blockIdx.y;
     float s = 0.0f;
-    for (int r = 0; r < rows; r++) s += ld(x, dtype, ((size_t)b * rows + r) * d + c);
-    out[id] = s / (float)rows;
+    if (col < d)
+        for (int r = g; r < rows; r += 16) s += ld(x, dtype, ((size_t)b * rows + r) * d + col);
+    part[g][c] = s;
+    __syncthreads();
+    if (g == 0 && col < d) {
+        float t = 0.0f;
+        for (int i = 0; i < 16; i++) t += part[i][c];
+        out[(size_t)b * d + col] = t / (float)rows;
+    }
 }
 
 // ---- flash attention, head_dim 64 ----------------------------------------------------
@@ -430,8 +441,7 @@ void launch_softmax_rows(float *x, int rows, int n, hipStream_t s) {
 }
 void launch_mean_rows(const void *x, int dtype, int batch, int rows, int d, float *out,
                       hipStream_t s) {
-    size_t n = (size_t)batch * d;
-    if (n) hipLaunchKernelGGL(mean_rows_kernel, dim3(cdiv(n, 256)), dim3(256), 0, s, x, dtype, batch, rows, d, out);
+    if (batch && d) hipLaunchKernelGGL(mean_rows_kernel, dim3(cdiv(d, 64), batch), dim3(1024), 0, s, x, dtype, batch, rows, d, out);
 }
 void launch_attention(const half_t *qkv, half_t *out, int batch, int seq, int heads, int dh,
                       float scale, hipStream_t s) {

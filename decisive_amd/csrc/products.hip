@@ -662,7 +662,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_w4a16_kernel(
                     } else if (EPI == 1) {
                         ((half_t *)out)[at] = (half_t)val;
                     } else if (EPI == 2) {
-                        float gl = 0.5f * val * (1.0f + erff(val * 0.70710678118654752f));
+                        float gl = gelu_erf(val);
                         ((half_t *)out)[at] = (half_t)gl;
                     } else {
                         ((half_t *)out)[at] = (half_t)(val + (float)residual[at]);
@@ -1240,7 +1240,7 @@ __global__ __launch_bounds__(WGM *WGN * 64) void w4a16_pipe_kernel(
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     if (EPI == 1) o[e] = (half_t)v[e];
-                    else if (EPI == 2) o[e] = (half_t)(0.5f * v[e] * (1.0f + erff(v[e] * 0.70710678118654752f)));
+                    else if (EPI == 2) o[e] = (half_t)gelu_erf(v[e]);
                     else o[e] = (half_t)0.0f;
                 }
                 if (EPI == 3) {

@@ -45,9 +45,36 @@ def test_layernorm_gelu_rms_softmax_mean(ctx, oracle):
     mean = empty((1, d), torch.float32)
     ctx.mean_rows(dev(x), rocm.F32, 1, rows, d, mean)
     assert np.allclose(host(ctx, mean)[0], oracle.mean_rows(x), atol=1e-5)
+    # several sequences, f16 rows, a column count that is not a multiple of 64
+    xs = rng.standard_normal((3, 50, 100)).astype(np.float16)
+    means = empty((3, 100), torch.float32)
+    ctx.mean_rows(dev(xs.reshape(150, 100)), rocm.F16, 3, 50, 100, means)
+    for bi in range(3):
+        assert np.allclose(host(ctx, means)[bi], oracle.mean_rows(xs[bi].astype(np.float32)), atol=1e-5)
     a = dev(x.copy())
     ctx.add(a, dev(up), rocm.F32, x.size)
     assert bits_equal(host(ctx, a), x + up)
+
+
+def test_gelu_erf_against_float64(ctx):
+    """GELU's erf (Abramowitz & Stegun 7.1.26, |error| <= 1.5e-7) on a dense
+    grid and at the limits, against float64 math.erf."""
+    import math
+    x = np.concatenate([np.linspace(-8, 8, 200001, dtype=np.float32),
+                        np.array([0.0, -0.0, 20.0, -20.0, 1e-30, -1e-30, 3.0e38, np.inf], np.float32)])
+    g = dev(x.copy())
+    ctx.gelu(g, rocm.F32, x.size)
+    got = host(ctx, g).astype(np.float64)
+    xd = x.astype(np.float64)
+    erf = np.array([math.erf(v / math.sqrt(2.0)) if np.isfinite(v) else 1.0 for v in xd])
+    want = 0.5 * xd * (1.0 + erf)
+    fin = np.abs(xd) <= 8
+    # 0.5|x| * 1.5e-7 from the approximation plus a few f32 roundings of the result
+    assert np.all(np.abs(got[fin] - want[fin]) <= 0.5 * np.abs(xd[fin]) * 2e-7 + np.abs(want[fin]) * 4e-7 + 1e-30)
+    # 0, -0, 20, -20, +-1e-30, 3e38, inf
+    assert got[-8] == 0.0 and got[-7] == 0.0 and got[-6] == 20.0 and got[-5] == 0.0
+    assert abs(got[-4]) <= 1e-30 and abs(got[-3]) <= 1e-30
+    assert got[-2] == np.float32(3.0e38) and got[-1] == np.inf
 
 
 @pytest.mark.parametrize("d", [512, 1024, 2048, 768])
