@@ -845,14 +845,15 @@ typedef int int16_t_v __attribute__((ext_vector_type(16)));
 // step waits only for its own stage (s_waitcnt vmcnt of the younger stages'
 // loads) before the workgroup barrier, so HBM/L2 latency overlaps NS - 2
 // steps of MFMA work. Stage rows are BK bytes of 16-byte chunks, XOR-swizzled
-// so fragment reads and DMA writes are bank-conflict free:
-//   BK = 128: slot = chunk ^ (row & 7); BK = 64: slot = chunk ^ ((row >> 1) & 3).
+// so that the 16 rows of a fragment read (16 lanes per 256-byte LDS cycle)
+// fall in distinct banks, with 256 / BK rows sharing a bank line:
+//   BK = 128: slot = chunk ^ ((row >> 1) & 7); BK = 64: slot = chunk ^ ((row >> 2) & 3).
 // Rows past m (n) and chunks past k read as zero (buffer range checks), so
 // any m, n and k % 16 == 0 work. The f32 epilogue reads its row and column
 // scales from LDS.
 template <int BK>
 __device__ __forceinline__ int pipe_slot(int c, int r) {
-    return BK == 128 ? (c ^ (r & 7)) : (c ^ ((r >> 1) & 3));
+    return BK == 128 ? (c ^ ((r >> 1) & 7)) : (c ^ ((r >> 2) & 3));
 }
 
 template <int BM, int BN, int BK, int NS, int WGM, int WGN>
@@ -895,17 +896,23 @@ __global__ __launch_bounds__(WGM *WGN * 64) void i8_gemm_pipe_kernel(const int8_
     // chunk) goes in the VGPR offset, the part the buffer range check covers,
     // so rows past m (n) and chunks past k read as zero and nothing past the
     // operands is touched; soffset stays 0.
+    // The swizzle of row RPI*blk + lrow depends on blk only through its
+    // parity (BK = 128) or not at all (BK = 64); DPW is even, so the parity
+    // of blk is that of p.
+    static_assert(DPW % 2 == 0, "instruction parity known at compile time");
     const int lrow = lane / CPR;
-    const int c16 = pipe_slot<BK>(lane % CPR, lrow) * 16;  // slot^swizzle is an involution
-    const uint32_t lane_off = (uint32_t)(lrow * k + c16);
+    const int c16[2] = {pipe_slot<BK>(lane % CPR, lrow) * 16, pipe_slot<BK>(lane % CPR, lrow + RPI) * 16};
+    const uint32_t lane_off[2] = {(uint32_t)(lrow * k + c16[0]), (uint32_t)(lrow * k + c16[1])};
     // DMA instructions p0 <= p < p1 of a stage (issued in slices between MFMA groups)
     auto dma = [&](uint8_t *stage, int st, int p0, int p1) {
         const int kk = st * BK;
         // >= 2^31 stays out of range after adding a row offset (BM, BN rows * k < 2^31)
-        const uint32_t voff = kk + c16 < k ? lane_off + (uint32_t)kk : 0x80000000u;
+        const uint32_t voff0 = kk + c16[0] < k ? lane_off[0] + (uint32_t)kk : 0x80000000u;
+        const uint32_t voff1 = kk + c16[1] < k ? lane_off[1] + (uint32_t)kk : 0x80000000u;
 #pragma unroll
         for (int p = p0; p < p1; p++) {
             const int blk = wave * DPW + p;
+            const uint32_t voff = (p & 1) ? voff1 : voff0;
             auto *dst = (__attribute__((address_space(3))) void *)(stage + __builtin_amdgcn_readfirstlane(blk * 1024));
             if (blk * RPI < BM)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, dst, 16, voff + (uint32_t)(blk * RPI * k), 0, 0, 0);
