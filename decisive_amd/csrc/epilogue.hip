@@ -217,7 +217,7 @@ constexpr int kAttnKeys = 64;                             // per step
 
 typedef short short4_t __attribute__((ext_vector_type(4)));
 
-__global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(const half_t *__restrict__ qkv,
+__global__ __launch_bounds__(kAttnWaves * 64, 4) void attention_kernel(const half_t *__restrict__ qkv,
                                                                     half_t *__restrict__ out, int seq,
                                                                     int heads, float scale_log2) {
     __shared__ __align__(16) uint8_t ks[2 * kAttnKeys * 128];
@@ -293,26 +293,8 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(const half_t
                 sc[qb][kb] = mfma_f16(kf[1], qf[qb][1], acc);
             }
         }
-        // V^T fragments of the two 32-key blocks: vf[c][db] (8 keys of dh 16db + j)
-        half8_t vf[2][4];
-#pragma unroll
-        for (int c = 0; c < 2; c++)
-#pragma unroll
-            for (int db = 0; db < 4; db++) {
-                short4_t part[2];
-#pragma unroll
-                for (int r2 = 0; r2 < 2; r2++) {
-                    // lane 16g + 4v + a addresses row 32c + 16r2 + 4g + v, unit 4db + a
-                    const int row = 32 * c + 16 * r2 + 4 * q4 + (j >> 2);
-                    const int unit = (4 * db + (j & 3)) ^ (4 * ((row >> 1) & 3));
-                    part[r2] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        (__attribute__((address_space(3))) short4_t *)(vst + row * 128 + unit * 8));
-                }
-                const uint2_t lo = __builtin_bit_cast(uint2_t, part[0]), hi = __builtin_bit_cast(uint2_t, part[1]);
-                vf[c][db] = as_half8(uint4_t{lo[0], lo[1], hi[0], hi[1]});
-            }
-
         const bool ragged = (st + 1) * kAttnKeys > seq;
+        half8_t pf[kAttnQB][2];  // P^T operands of the two 32-key blocks
 #pragma unroll
         for (int qb = 0; qb < kAttnQB; qb++) {
             // online softmax over this step's keys for query j (lanes j, j+16, j+32, j+48)
@@ -331,32 +313,47 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(const half_t
             bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
             bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
             const float mnew = fmaxf(mrow[qb], bmax);
-            const float alpha = __builtin_amdgcn_exp2f((mrow[qb] - mnew) * scale_log2);
-            mrow[qb] = mnew;
             const float moff = -mnew * scale_log2;
-            lsum[qb] *= alpha;
+            // rescale only when some query of the wave has a new maximum
+            // (skipping a multiply by exactly 1 changes nothing)
+            if (__builtin_amdgcn_ballot_w64(mnew != mrow[qb])) {
+                const float alpha = __builtin_amdgcn_exp2f((mrow[qb] - mnew) * scale_log2);
+                lsum[qb] *= alpha;
 #pragma unroll
-            for (int db = 0; db < 4; db++)
+                for (int db = 0; db < 4; db++)
 #pragma unroll
-                for (int v = 0; v < 4; v++) o[qb][db][v] *= alpha;
-            half_t p[4][4];
+                    for (int v = 0; v < 4; v++) o[qb][db][v] *= alpha;
+            }
+            mrow[qb] = mnew;
 #pragma unroll
             for (int kb = 0; kb < 4; kb++)
 #pragma unroll
                 for (int v = 0; v < 4; v++) {
                     const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[qb][kb][v], scale_log2, moff));
                     lsum[qb] += e;
-                    p[kb][v] = (half_t)e;
+                    pf[qb][kb / 2][(kb % 2) * 4 + v] = (half_t)e;
                 }
-            // O^T += V^T P^T over the two 32-key blocks
-#pragma unroll
-            for (int c = 0; c < 2; c++) {
-                const half8_t pf = {p[2 * c][0], p[2 * c][1], p[2 * c][2], p[2 * c][3],
-                                    p[2 * c + 1][0], p[2 * c + 1][1], p[2 * c + 1][2], p[2 * c + 1][3]};
-#pragma unroll
-                for (int db = 0; db < 4; db++) o[qb][db] = mfma_f16(vf[c][db], pf, o[qb][db]);
-            }
         }
+        // O^T += V^T P^T over the two 32-key blocks; the V^T operand (8 keys
+        // of dh 16db + j) is read just before the MFMAs that use it
+#pragma unroll
+        for (int c = 0; c < 2; c++)
+#pragma unroll
+            for (int db = 0; db < 4; db++) {
+                short4_t part[2];
+#pragma unroll
+                for (int r2 = 0; r2 < 2; r2++) {
+                    // lane 16g + 4v + a addresses row 32c + 16r2 + 4g + v, unit 4db + a
+                    const int row = 32 * c + 16 * r2 + 4 * q4 + (j >> 2);
+                    const int unit = (4 * db + (j & 3)) ^ (4 * ((row >> 1) & 3));
+                    part[r2] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (__attribute__((address_space(3))) short4_t *)(vst + row * 128 + unit * 8));
+                }
+                const uint2_t lo = __builtin_bit_cast(uint2_t, part[0]), hi = __builtin_bit_cast(uint2_t, part[1]);
+                const half8_t vf = as_half8(uint4_t{lo[0], lo[1], hi[0], hi[1]});
+#pragma unroll
+                for (int qb = 0; qb < kAttnQB; qb++) o[qb][db] = mfma_f16(vf, pf[qb][c], o[qb][db]);
+            }
     }
     __builtin_amdgcn_s_waitcnt(0x0F70);  // no LDS write in flight once the block ends
 #pragma unroll

@@ -1280,8 +1280,8 @@ inline unsigned cdiv(size_t a, size_t b) { return (unsigned)((a + b - 1) / b); }
 // ---- variant tables -------------------------------------------------------------
 
 const char *const kGemvNames[] = {"w16", "w8"};
-const char *const kGemmNames[] = {"pipe-auto", "256x256p2w8", "128x128p2w4", "256x128w2x2", "128x128w2x2",
-                                   "128x64w2x2"};
+const char *const kGemmNames[] = {"pipe-auto",   "256x256p2w8", "128x128p2w4", "128x256p2w8",
+                                   "256x128w2x2", "128x128w2x2", "128x64w2x2"};
 const char *const kI8Names[] = {"256x256p2w8", "256x256p4k64w8", "256x128p3w8", "256x128p3",
                                  "128x128w2x2", "256x128w2x2", "64x64w2x2"};
 const char *const kGroupedNames[] = {"wave16x16"};
@@ -1360,27 +1360,33 @@ int device_cus() {
     return cus[dev];
 }
 
-// Variants 0-2 are the pipelined kernel: 256x256 tiles on 8 waves (one block
-// per CU), 128x128 tiles on 4 waves (two blocks per CU), and "auto", which
-// takes 256x256 when that gives at least one tile per compute unit and
-// 128x128 otherwise. 3-5 stage through registers. All give the same bits
-// (same f16 dequantization, one MFMA per 32-k run in k order); the pipelined
-// ones need k % 128 == 0 and fall back to 256x128w2x2 otherwise.
+// Variants 0-3 are the pipelined kernel: "auto", 256x256 tiles on 8 waves
+// (one block per CU), 128x128 tiles on 4 waves (two blocks per CU) and
+// 128x256 tiles on 8 waves. "auto" takes the largest of 256x256, 128x256 and
+// 128x128 that gives at least one tile per compute unit. 4-6 stage through
+// registers. All give the same bits (same f16 dequantization, one MFMA per
+// 32-k run in k order); the pipelined ones need k % 128 == 0 and fall back to
+// 256x128w2x2 otherwise.
 template <int EPI>
 void gemm_dispatch(const Weight &w, const half_t *x, int m, void *y, const half_t *res, int variant,
                    hipStream_t s) {
     switch (variant) {
-        case 0:
-            if (cdiv(m, 256) * cdiv(w.rows, 256) >= (unsigned)device_cus()) {
+        case 0: {
+            const unsigned cus = (unsigned)device_cus();
+            if (cdiv(m, 256) * cdiv(w.rows, 256) >= cus) {
                 if (w4a16_pipe_launch<256, 256, 2, 4, EPI>(w, x, m, y, res, s)) return;
+            } else if (cdiv(m, 128) * cdiv(w.rows, 256) >= cus) {
+                if (w4a16_pipe_launch<128, 256, 2, 4, EPI>(w, x, m, y, res, s)) return;
             } else {
                 if (w4a16_pipe_launch<128, 128, 2, 2, EPI>(w, x, m, y, res, s)) return;
             }
             break;
+        }
         case 1: if (w4a16_pipe_launch<256, 256, 2, 4, EPI>(w, x, m, y, res, s)) return; break;
         case 2: if (w4a16_pipe_launch<128, 128, 2, 2, EPI>(w, x, m, y, res, s)) return; break;
-        case 4: gemm_launch<128, 128, 2, 2, EPI>(w, x, m, y, res, s); return;
-        case 5: gemm_launch<128, 64, 2, 2, EPI>(w, x, m, y, res, s); return;
+        case 3: if (w4a16_pipe_launch<128, 256, 2, 4, EPI>(w, x, m, y, res, s)) return; break;
+        case 5: gemm_launch<128, 128, 2, 2, EPI>(w, x, m, y, res, s); return;
+        case 6: gemm_launch<128, 64, 2, 2, EPI>(w, x, m, y, res, s); return;
         default: break;
     }
     gemm_launch<256, 128, 2, 2, EPI>(w, x, m, y, res, s);
@@ -1428,7 +1434,7 @@ void gv_launch(const Weight &w, const void *a, const float *sa, int m, int abits
 int variant_count(const char *family) {
     std::string f(family);
     if (f == "gemv") return 2;
-    if (f == "gemm_w4a16") return 6;
+    if (f == "gemm_w4a16") return 7;
     if (f == "i8_gemm") return 7;
     if (f == "grouped") return 1;
     return 0;

@@ -248,7 +248,8 @@ def test_w4a16_rejects_misaligned_activations(ctx, oracle):
     assert e.value.code == "INVALID_PARAMETERS"
 
 
-W4A16_VARIANTS = ("pipe-auto", "256x256p2w8", "128x128p2w4", "256x128w2x2", "128x128w2x2", "128x64w2x2")
+W4A16_VARIANTS = ("pipe-auto", "256x256p2w8", "128x128p2w4", "128x256p2w8", "256x128w2x2", "128x128w2x2",
+                  "128x64w2x2")
 
 
 @pytest.mark.parametrize("layout", [rocm.Q4_G32_F16, rocm.Q4_G64_F32])
