@@ -17,6 +17,8 @@
 //              v_mfma_i32_16x16x64_i8, epilogue (f32(dot)*sa)*sw.
 #include <float.h>
 
+#include <algorithm>
+
 #include "kernels.hpp"
 
 namespace dz {
@@ -1068,10 +1070,13 @@ __device__ __forceinline__ uint4_t unpack_codes_c(uint32_t w, uint32_t mlo, uint
 // v_mfma_f32_16x16x32_f16 per 32-k run in k order, so both kernels give the
 // same bits. The MFMA is issued as D[n][m] = W . X^T: lane (q, j) ends with
 // four consecutive output columns of one row and stores them as one vector.
+// A launch covers the n output columns that codes / scales / out / residual
+// point at (a multiple-of-16 slice of the weight); ldo is the row stride of
+// out and residual.
 template <int BM, int BN, int WGM, int WGN, bool G32, int EPI, int VALU_PER_MFMA = 2>
 __global__ __launch_bounds__(WGM *WGN * 64) void w4a16_pipe_kernel(
     const uint8_t *__restrict__ codes, const uint8_t *__restrict__ scales, const half_t *__restrict__ x, int m,
-    int k, int n, int kbs, void *__restrict__ out, const half_t *__restrict__ residual) {
+    int k, int n, int kbs, void *__restrict__ out, const half_t *__restrict__ residual, int ldo) {
     constexpr int WAVES = WGM * WGN;
     constexpr int TM = BM / WGM, TN = BN / WGN, MB = TM / 16, NT = TN / 16;
     constexpr int XSTAGE = BM * 256, WSTAGE = BN / 16 * 1024;
@@ -1224,7 +1229,8 @@ __global__ __launch_bounds__(WGM *WGN * 64) void w4a16_pipe_kernel(
     __builtin_amdgcn_s_waitcnt(0x0F70);  // no LDS write in flight once the block ends
 
     // epilogue: acc[mb][nt][v] = Y[row][col + v]
-    const bool vec = (n & 3) == 0 && ((uintptr_t)out & 15) == 0 && (EPI != 3 || ((uintptr_t)residual & 7) == 0);
+    const bool vec = (n & 3) == 0 && (ldo & 3) == 0 && ((uintptr_t)out & 15) == 0 &&
+                     (EPI != 3 || ((uintptr_t)residual & 7) == 0);
 #pragma unroll
     for (int mb = 0; mb < MB; mb++) {
         const int r = row0 + wm * TM + mb * 16 + j;
@@ -1233,7 +1239,7 @@ __global__ __launch_bounds__(WGM *WGN * 64) void w4a16_pipe_kernel(
         for (int nt = 0; nt < NT; nt++) {
             const int c = col0 + wn * TN + nt * 16 + 4 * q;
             if (c >= n) continue;
-            const size_t at = (size_t)r * n + c;
+            const size_t at = (size_t)r * ldo + c;
             float v[4] = {acc[mb][nt][0], acc[mb][nt][1], acc[mb][nt][2], acc[mb][nt][3]};
             if (EPI == 0) {
                 if (vec) {
@@ -1330,19 +1336,28 @@ void gemm_launch(const Weight &w, const half_t *x, int m, void *y, const half_t 
                            w.codes, w.scales, x, m, w.cols, w.rows, w.kblocks(), y, res);
 }
 
+// Columns [c0, c0 + nc) of the product (c0 a multiple of 16) with BM x BN tiles.
 template <int BM, int BN, int WGM, int WGN, int EPI>
-bool w4a16_pipe_launch(const Weight &w, const half_t *x, int m, void *y, const half_t *res, hipStream_t s) {
+bool w4a16_pipe_launch(const Weight &w, const half_t *x, int m, void *y, const half_t *res, hipStream_t s,
+                       int c0 = 0, int nc = -1) {
+    if (nc < 0) nc = w.rows - c0;
     // whole 128-k steps; byte offsets are 32-bit and relative to the block's first row / tile
-    if (w.cols % 128 != 0 || (size_t)BM * w.cols * 2 >= ((size_t)1 << 31) ||
+    if (w.cols % 128 != 0 || c0 % 16 != 0 || (size_t)BM * w.cols * 2 >= ((size_t)1 << 31) ||
         (size_t)(BN / 16) * w.kblocks() * 1024 >= ((size_t)1 << 31))
         return false;
-    const unsigned blocks = cdiv(m, BM) * cdiv(w.rows, BN);
+    if (nc <= 0) return true;
+    const size_t t0 = (size_t)(c0 / 16) * w.kblocks();  // first (tile, k-block) of the slice
+    const uint8_t *codes = w.codes + t0 * 1024, *scales = w.scales + t0 * 128;
+    const size_t esz = EPI == 0 ? 4 : 2;
+    void *yo = (uint8_t *)y + (size_t)c0 * esz;
+    const half_t *ro = res ? res + c0 : nullptr;
+    const unsigned blocks = cdiv(m, BM) * cdiv(nc, BN);
     if (w.kind == WeightKind::Q4G32)
         hipLaunchKernelGGL((w4a16_pipe_kernel<BM, BN, WGM, WGN, true, EPI>), dim3(blocks), dim3(WGM * WGN * 64), 0, s,
-                           w.codes, w.scales, x, m, w.cols, w.rows, w.kblocks(), y, res);
+                           codes, scales, x, m, w.cols, nc, w.kblocks(), yo, ro, w.rows);
     else
         hipLaunchKernelGGL((w4a16_pipe_kernel<BM, BN, WGM, WGN, false, EPI>), dim3(blocks), dim3(WGM * WGN * 64), 0, s,
-                           w.codes, w.scales, x, m, w.cols, w.rows, w.kblocks(), y, res);
+                           codes, scales, x, m, w.cols, nc, w.kblocks(), yo, ro, w.rows);
     return true;
 }
 
@@ -1362,9 +1377,11 @@ int device_cus() {
 
 // Variants 0-3 are the pipelined kernel: "auto", 256x256 tiles on 8 waves
 // (one block per CU), 128x128 tiles on 4 waves (two blocks per CU) and
-// 128x256 tiles on 8 waves. "auto" takes the largest of 256x256, 128x256 and
-// 128x128 that gives at least one tile per compute unit. 4-6 stage through
-// registers. All give the same bits (same f16 dequantization, one MFMA per
+// 128x256 tiles on 8 waves. "auto" runs 256x256 tiles over the leading
+// columns that fill whole waves of compute units and 128x256 tiles over the
+// rest (one launch each), or, below one wave of 256x256 tiles, the largest of
+// 128x256 and 128x128 that gives at least one tile per unit. 4-6 stage
+// through registers. All give the same bits (same f16 dequantization, one MFMA per
 // 32-k run in k order); the pipelined ones need k % 128 == 0 and fall back to
 // 256x128w2x2 otherwise.
 template <int EPI>
@@ -1373,8 +1390,15 @@ void gemm_dispatch(const Weight &w, const half_t *x, int m, void *y, const half_
     switch (variant) {
         case 0: {
             const unsigned cus = (unsigned)device_cus();
-            if (cdiv(m, 256) * cdiv(w.rows, 256) >= cus) {
-                if (w4a16_pipe_launch<256, 256, 2, 4, EPI>(w, x, m, y, res, s)) return;
+            const unsigned tm = cdiv(m, 256), tn = cdiv(w.rows, 256);
+            if (tm * tn >= cus) {
+                // 256-column blocks that fill whole waves; the rest on 128x256 tiles
+                unsigned lead = tn;
+                if ((tm * tn) % cus != 0 && tm <= cus && cus % tm == 0) lead = (tm * tn) / cus * (cus / tm);
+                const int c1 = (int)std::min<size_t>((size_t)lead * 256, (size_t)w.rows);
+                if (w4a16_pipe_launch<256, 256, 2, 4, EPI>(w, x, m, y, res, s, 0, c1) &&
+                    w4a16_pipe_launch<128, 256, 2, 4, EPI>(w, x, m, y, res, s, c1, w.rows - c1))
+                    return;
             } else if (cdiv(m, 128) * cdiv(w.rows, 256) >= cus) {
                 if (w4a16_pipe_launch<128, 256, 2, 4, EPI>(w, x, m, y, res, s)) return;
             } else {

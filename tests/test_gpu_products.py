@@ -285,6 +285,37 @@ def test_large_m_gemm_vs_closed_form(ctx, oracle, layout, m, k, n):
         assert bits_equal(o, outs[0]), name
 
 
+@pytest.mark.parametrize("n", [3072, 3120])
+def test_w4a16_column_split_matches_register_kernel(ctx, oracle, n):
+    """M=8192, K=1024: 256x256 tiles fill whole waves of compute units over
+    the leading columns and 128x256 tiles take the rest (two launches); the
+    bits equal the register-staged kernel's, and sampled rows the float64
+    product of the dequantized weights."""
+    torch = pytest.importorskip("torch")
+    m, k = 8192, 1024
+    g = torch.Generator(device="cuda").manual_seed(n)
+    wdev = torch.randn((n, k), generator=g, device="cuda", dtype=torch.float32) * 0.02
+    w = ctx.quantize(wdev, rocm.F32, n, k, 4, 32)
+    del wdev
+    x = torch.randn((m, k), generator=torch.Generator(device="cuda").manual_seed(3), device="cuda").half()
+    ys = []
+    for name in ("pipe-auto", "256x128w2x2"):
+        ctx.select_variant("gemm_w4a16", name)
+        y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+        ctx.linear(w, x, rocm.F16, m, y, rocm.W4A16)
+        ctx.sync()
+        ys.append(y)
+    ctx.select_variant("gemm_w4a16", W4A16_VARIANTS[0])
+    assert torch.equal(ys[0], ys[1])
+    deq = torch.empty((n, k), dtype=torch.float32, device="cuda")
+    ctx.dequant(w, deq)
+    ctx.sync()
+    rows = torch.arange(0, m, 509, device="cuda")
+    ref = (x[rows].double() @ deq.double().T).float()
+    assert (ys[0][rows] - ref).abs().max().item() <= MAX_ABS
+    w.free()
+
+
 def test_config5_prefill_rows_vs_fp32(ctx, oracle):
     """BASELINE config 5 at full size (M=16384, K=4096, N=14336); a row sample is
     checked against an fp32 product of the dequantized weights."""
