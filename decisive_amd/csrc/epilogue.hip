@@ -15,6 +15,8 @@
 // tolerance rather than bit for bit.
 #include <float.h>
 
+#include <algorithm>
+
 #include "kernels.hpp"
 
 namespace dz {
@@ -67,54 +69,77 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const void *__restrict__
     }
 }
 
-// f16 rows of d = 512 * C columns: one wave per row, the row in registers
-// (C 16-byte chunks per lane: columns 512c + 8*lane + 0..7), shuffle-tree
-// sums, the same two-pass mean / variance as layernorm_kernel.
+// f16 rows of d = 512 * C columns. Each wave walks rows wave_id, wave_id +
+// total waves, ...: the row sits in registers (C 16-byte chunks per lane:
+// columns 512c + 8*lane + 0..7), the gains and biases of the lane's columns
+// are loaded once, and the next row's load is issued before the current row
+// is normalized. Shuffle-tree sums, the same two-pass mean / variance as
+// layernorm_kernel.
 template <int C>
 __global__ __launch_bounds__(256) void layernorm_f16_rows_kernel(const half_t *__restrict__ x,
                                                                  half_t *__restrict__ y, int rows,
                                                                  const float *__restrict__ w,
                                                                  const float *__restrict__ b, float eps) {
     constexpr int D = 512 * C;
-    const int row = blockIdx.x * 4 + threadIdx.x / 64, lane = threadIdx.x % 64;
+    const int lane = threadIdx.x % 64;
+    const int stride = gridDim.x * 4;
+    int row = blockIdx.x * 4 + threadIdx.x / 64;
     if (row >= rows) return;  // whole wave
-    const half_t *src = x + (size_t)row * D;
-    float v[C][8];
-#pragma unroll
-    for (int c = 0; c < C; c++) {
-        const half8_t h = *(const half8_t *)(src + c * 512 + lane * 8);
-#pragma unroll
-        for (int e = 0; e < 8; e++) v[c][e] = (float)h[e];
-    }
-    float s = 0.0f;
-#pragma unroll
-    for (int c = 0; c < C; c++)
-#pragma unroll
-        for (int e = 0; e < 8; e++) s += v[c][e];
-    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
-    const float mean = s / (float)D;
-    float q = 0.0f;
-#pragma unroll
-    for (int c = 0; c < C; c++)
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const float d0 = v[c][e] - mean;
-            q += d0 * d0;
-        }
-    for (int off = 32; off > 0; off >>= 1) q += __shfl_xor(q, off);
-    const float inv = 1.0f / sqrtf(q / (float)D + eps);
-    half_t *dst = y + (size_t)row * D;
+    float ww[C][8], bb[C][8];
 #pragma unroll
     for (int c = 0; c < C; c++) {
         const int col = c * 512 + lane * 8;
         const float4_t w0 = *(const float4_t *)(w + col), w1 = *(const float4_t *)(w + col + 4);
         const float4_t b0 = *(const float4_t *)(b + col), b1 = *(const float4_t *)(b + col + 4);
-        const float ww[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
-        const float bb[8] = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
-        half8_t o;
 #pragma unroll
-        for (int e = 0; e < 8; e++) o[e] = (half_t)((v[c][e] - mean) * inv * ww[e] + bb[e]);
-        *(half8_t *)(dst + col) = o;
+        for (int e = 0; e < 4; e++) {
+            ww[c][e] = w0[e];
+            ww[c][e + 4] = w1[e];
+            bb[c][e] = b0[e];
+            bb[c][e + 4] = b1[e];
+        }
+    }
+    half8_t h[C];
+#pragma unroll
+    for (int c = 0; c < C; c++) h[c] = *(const half8_t *)(x + (size_t)row * D + c * 512 + lane * 8);
+    for (;;) {
+        float v[C][8];
+#pragma unroll
+        for (int c = 0; c < C; c++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[c][e] = (float)h[c][e];
+        const int next = row + stride;
+        if (next < rows) {
+#pragma unroll
+            for (int c = 0; c < C; c++) h[c] = *(const half8_t *)(x + (size_t)next * D + c * 512 + lane * 8);
+        }
+        float s = 0.0f;
+#pragma unroll
+        for (int c = 0; c < C; c++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) s += v[c][e];
+        for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
+        const float mean = s / (float)D;
+        float q = 0.0f;
+#pragma unroll
+        for (int c = 0; c < C; c++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float d0 = v[c][e] - mean;
+                q += d0 * d0;
+            }
+        for (int off = 32; off > 0; off >>= 1) q += __shfl_xor(q, off);
+        const float inv = 1.0f / sqrtf(q / (float)D + eps);
+        half_t *dst = y + (size_t)row * D;
+#pragma unroll
+        for (int c = 0; c < C; c++) {
+            half8_t o;
+#pragma unroll
+            for (int e = 0; e < 8; e++) o[e] = (half_t)((v[c][e] - mean) * inv * ww[c][e] + bb[c][e]);
+            *(half8_t *)(dst + c * 512 + lane * 8) = o;
+        }
+        if (next >= rows) break;
+        row = next;
     }
 }
 
@@ -409,7 +434,8 @@ void launch_layernorm(const void *x, void *y, int dtype, int rows, int d, const 
     const bool fast = dtype == 1 && (d == 512 || d == 1024 || d == 2048) &&
                       (((uintptr_t)x | (uintptr_t)y | (uintptr_t)w | (uintptr_t)b) & 15) == 0;
     if (fast) {
-        const dim3 grid(cdiv(rows, 4));
+        // two rows per wave (4-wave blocks): the second row's load overlaps the first row's work
+        const dim3 grid(cdiv(rows, 8));
         const half_t *xh = (const half_t *)x;
         half_t *yh = (half_t *)y;
         if (d == 512) hipLaunchKernelGGL(layernorm_f16_rows_kernel<1>, grid, dim3(256), 0, s, xh, yh, rows, w, b, eps);
