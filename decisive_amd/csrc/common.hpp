@@ -150,6 +150,15 @@ __device__ __forceinline__ void dma16(uint32_t lds, uint32_t voff, int32x4_t rsr
                  : "memory", "m0");
 }
 
+// buffer_load_dword ... lds: lane l's 4 bytes at rsrc + voff land at LDS
+// lds + 4 * l (same contract as dma16).
+__device__ __forceinline__ void dma4(uint32_t lds, uint32_t voff, int32x4_t rsrc) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+                 :
+                 : "s"(lds), "v"(voff), "s"(rsrc)
+                 : "memory", "m0");
+}
+
 // ---- host helpers ------------------------------------------------------------
 
 struct Status {

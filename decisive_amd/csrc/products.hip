@@ -1281,6 +1281,199 @@ __global__ __launch_bounds__(WGM *WGN * 64) void w4a16_pipe_kernel(
     }
 }
 
+// ============================================================================
+// pipelined grouped W{4,8}A{8,4} (bit-exact, large M)
+// ============================================================================
+//
+// The reference's fused fold (int8.rs:524-585) with each group's exact int32
+// dot taken by v_mfma_i32_16x16x64_i8:
+//     acc = fma(f32(dot_g), sw[g][c] * sx[r][g], acc)   for g = 0, 1, ... in order,
+// so the outputs equal grouped_kernel's (and the oracle's) bit for bit.
+// Block tile BM x BN on WGM x WGN waves; one k-step covers two 64-groups, in
+// two LDS stages filled by buffer_load ... lds while the other is computed:
+//  - activation codes: BM rows x 128 bytes (chunk c of row r at slot
+//    c ^ ((r >> 1) & 7), conflict-free for the 16 rows of a fragment read);
+//  - weight codes: Q4 one 1 KiB tile16x128 chunk per 16-column tile, Q8 two
+//    1 KiB tile16x64 chunks;
+//  - weight scales: 128 bytes per tile (Q4: [row][group] f32 pairs, Q8:
+//    [group][row]); activation scales: BM rows x 2 f32.
+// The MFMA takes the weight operand first, so lane (q, j) holds the dots of
+// four consecutive output columns of one row: its weight scales are one
+// 16-byte LDS read and its activation scale one 4-byte read. The fold (a
+// convert, the scale product and the fma per output and group) is VALU work
+// and bounds the kernel; the MFMAs take about a third of its time.
+// Groups past `groups` (the odd tail of a k-step) are not folded.
+template <int BITS, int BM, int BN, int WGM, int WGN>
+__global__ __launch_bounds__(WGM *WGN * 64) void grouped_pipe_kernel(
+    const uint8_t *__restrict__ codes, const uint8_t *__restrict__ scales, const int8_t *__restrict__ q,
+    const float *__restrict__ sx, int m, int n, int groups, int kbs, float *__restrict__ y,
+    const int *__restrict__ bad) {
+    constexpr int WAVES = WGM * WGN;
+    constexpr int TM = BM / WGM, TN = BN / WGN, MB = TM / 16, NT = TN / 16;
+    constexpr int TILES = BN / 16;
+    constexpr int XSTAGE = BM * 128;
+    constexpr int CSTAGE = TILES * (BITS == 4 ? 1024 : 2048);
+    constexpr int SWSTAGE = TILES * 128;
+    constexpr int SXSTAGE = BM * 8;
+    constexpr int XPW = BM / 8 / WAVES;          // 8-row activation loads per wave
+    constexpr int CPW = CSTAGE / 1024 / WAVES;   // code-chunk loads per wave
+    static_assert(XPW * 8 * WAVES == BM && XPW % 2 == 0, "activation rows split evenly, even count per wave");
+    static_assert(CPW * 1024 * WAVES == CSTAGE && CPW >= 1, "code chunks split evenly");
+    static_assert(TILES == 8, "one 1 KiB weight-scale load per stage");
+    static_assert(BM * 2 == WAVES * 64, "one 4-byte activation-scale load per wave");
+    __shared__ __align__(16) uint8_t xs[2 * XSTAGE];
+    __shared__ __align__(16) uint8_t cs[2 * CSTAGE];
+    __shared__ __align__(16) uint8_t sws[2 * SWSTAGE];
+    __shared__ __align__(16) uint8_t sxs[2 * SXSTAGE];
+
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), lane = threadIdx.x % 64;
+    const int wm = wave / WGN, wn = wave % WGN;
+    const int qd = lane / 16, j = lane % 16;
+    const int tiles_m = (m + BM - 1) / BM, tiles_n = (n + BN - 1) / BN;
+    int tm, tn;
+    xcd_tile(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+    const int row0 = tm * BM, col0 = tn * BN;
+    const int tiles = (n + 15) / 16, tile0 = col0 / 16, tvalid = min(TILES, tiles - tile0);
+    const int rvalid = min(BM, m - row0);
+    const uint32_t rowbytes = (uint32_t)groups * 64;
+    const int32x4_t rq = buffer_rsrc(q + (size_t)row0 * rowbytes, (uint32_t)rvalid * rowbytes);
+    const int32x4_t rc = buffer_rsrc(codes + (size_t)tile0 * kbs * 1024, (uint32_t)(tvalid * kbs * 1024));
+    const uint32_t swtile = BITS == 4 ? (uint32_t)kbs * 128 : (uint32_t)groups * 64;  // scale bytes per tile
+    const int32x4_t rw = buffer_rsrc(scales + (size_t)tile0 * swtile, (uint32_t)tvalid * swtile);
+    const int32x4_t rs = buffer_rsrc(sx + (size_t)row0 * groups, (uint32_t)(rvalid * groups * 4));
+    const uint32_t xs_lds = lds_address(xs), cs_lds = lds_address(cs);
+    const uint32_t sws_lds = lds_address(sws), sxs_lds = lds_address(sxs);
+
+    // activation loads: lane l of instruction blk fills slot l % 8 of row
+    // 8*blk + l/8; the swizzle depends on blk only through its parity
+    const int lrow = lane / 8;
+    const uint32_t xoff[2] = {
+        (uint32_t)(lrow * rowbytes + (((lane % 8) ^ ((lrow >> 1) & 7)) * 16)),
+        (uint32_t)(lrow * rowbytes + (((lane % 8) ^ (((lrow + 8) >> 1) & 7)) * 16))};
+    auto load_stage = [&](int stage, int st, bool live) {
+        const int32x4_t nq = live ? rq : int32x4_t{rq[0], rq[1], 0, rq[3]};
+        const int32x4_t nc = live ? rc : int32x4_t{rc[0], rc[1], 0, rc[3]};
+        const int32x4_t nw = live ? rw : int32x4_t{rw[0], rw[1], 0, rw[3]};
+        const int32x4_t ns = live ? rs : int32x4_t{rs[0], rs[1], 0, rs[3]};
+#pragma unroll
+        for (int p = 0; p < XPW; p++) {
+            const int blk = wave * XPW + p;
+            dma16(__builtin_amdgcn_readfirstlane(xs_lds + stage * XSTAGE + blk * 1024),
+                  xoff[p & 1] + (uint32_t)(blk * 8) * rowbytes + (uint32_t)st * 128, nq);
+        }
+#pragma unroll
+        for (int p = 0; p < CPW; p++) {
+            const int ci = wave * CPW + p;  // Q4: tile; Q8: tile * 2 + group of the step
+            const int t = BITS == 4 ? ci : ci / 2;
+            const int kc = BITS == 4 ? st : 2 * st + ci % 2;
+            dma16(__builtin_amdgcn_readfirstlane(cs_lds + stage * CSTAGE + ci * 1024),
+                  (uint32_t)((t * kbs + kc) * 1024 + lane * 16), nc);
+        }
+        if (wave == 0) {
+            const int t = lane / 8;
+            const uint32_t off = BITS == 4 ? (uint32_t)(t * kbs + st) * 128 : (uint32_t)(t * groups + 2 * st) * 64;
+            dma16(__builtin_amdgcn_readfirstlane(sws_lds + stage * SWSTAGE), off + (uint32_t)(lane % 8) * 16, nw);
+        }
+        {
+            const int r = wave * 32 + lane / 2;
+            dma4(__builtin_amdgcn_readfirstlane(sxs_lds + stage * SXSTAGE + wave * 256),
+                 (uint32_t)((r * groups + 2 * st + (lane & 1)) * 4), ns);
+        }
+    };
+
+    float4_t acc[MB][NT];
+#pragma unroll
+    for (int a = 0; a < MB; a++)
+#pragma unroll
+        for (int b = 0; b < NT; b++) acc[a][b] = float4_t{0.f, 0.f, 0.f, 0.f};
+    const int4_t zero = {0, 0, 0, 0};
+    const bool nan_out = bad != nullptr && *bad != 0;
+    const int steps = (groups + 1) / 2;
+
+    // one group of a stage: weight fragments and scales once, then per row
+    // block the activation fragment, its scale, NT MFMAs and the fold
+    auto fold_group = [&](const uint8_t *xst, const uint8_t *cst, const uint8_t *swst, const uint8_t *sxst, int gp) {
+        int4_t bfr[NT];
+        float4_t swv[NT];
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            const int t = wn * NT + nt;
+            if (BITS == 4) {
+                const uint2_t wds = *(const uint2_t *)(cst + t * 1024 + lane * 16 + gp * 8);
+                const uint2_t lo = nibbles_to_i8(wds[0]), hi = nibbles_to_i8(wds[1]);
+                bfr[nt] = int4_t{(int)lo[0], (int)lo[1], (int)hi[0], (int)hi[1]};
+                const float4_t s01 = *(const float4_t *)(swst + t * 128 + qd * 32);       // rows 4qd, 4qd+1
+                const float4_t s23 = *(const float4_t *)(swst + t * 128 + qd * 32 + 16);  // rows 4qd+2, 4qd+3
+                swv[nt] = gp ? float4_t{s01[1], s01[3], s23[1], s23[3]} : float4_t{s01[0], s01[2], s23[0], s23[2]};
+            } else {
+                bfr[nt] = *(const int4_t *)(cst + (t * 2 + gp) * 1024 + lane * 16);
+                swv[nt] = *(const float4_t *)(swst + t * 128 + gp * 64 + qd * 16);
+            }
+        }
+#pragma unroll
+        for (int mb = 0; mb < MB; mb++) {
+            const int r = wm * TM + mb * 16 + j;
+            int4_t afr;
+            if (BITS == 4) {
+                const int c1 = 4 * gp + qd / 2, c2 = c1 + 2;
+                const uint2_t a0 = *(const uint2_t *)(xst + r * 128 + ((c1 ^ ((r >> 1) & 7)) * 16) + 8 * (qd & 1));
+                const uint2_t a1 = *(const uint2_t *)(xst + r * 128 + ((c2 ^ ((r >> 1) & 7)) * 16) + 8 * (qd & 1));
+                afr = int4_t{(int)a0[0], (int)a0[1], (int)a1[0], (int)a1[1]};
+            } else {
+                const int c = 4 * gp + qd;
+                afr = *(const int4_t *)(xst + r * 128 + ((c ^ ((r >> 1) & 7)) * 16));
+            }
+            const float sxv = *(const float *)(sxst + r * 8 + gp * 4);
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                const int4_t d = mfma_i8(bfr[nt], afr, zero);
+#pragma unroll
+                for (int v = 0; v < 4; v++)
+                    acc[mb][nt][v] = __builtin_fmaf((float)d[v], __fmul_rn(swv[nt][v], sxv), acc[mb][nt][v]);
+            }
+        }
+    };
+
+    if (!nan_out) {
+        load_stage(0, 0, true);
+        for (int st = 0; st < steps; st++) {
+            const int cur = st & 1;
+            // this wave's loads of step st are done; the barrier covers every wave
+            // (and every wave has finished reading the stage the next loads overwrite)
+            __builtin_amdgcn_s_waitcnt(0x0F70);
+            __builtin_amdgcn_s_barrier();
+            load_stage(cur ^ 1, st + 1, st + 1 < steps);
+            const uint8_t *xst = xs + cur * XSTAGE, *cst = cs + cur * CSTAGE;
+            const uint8_t *swst = sws + cur * SWSTAGE, *sxst = sxs + cur * SXSTAGE;
+            fold_group(xst, cst, swst, sxst, 0);
+            if (2 * st + 1 < groups) fold_group(xst, cst, swst, sxst, 1);
+        }
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // no LDS write in flight once the block ends
+    }
+
+    // acc[mb][nt][v] = Y[row][col + v]
+    const bool vec = (n & 3) == 0 && ((uintptr_t)y & 15) == 0;
+#pragma unroll
+    for (int mb = 0; mb < MB; mb++) {
+        const int r = row0 + wm * TM + mb * 16 + j;
+        if (r >= m) continue;
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            const int c = col0 + wn * TN + nt * 16 + 4 * qd;
+            if (c >= n) continue;
+            float4_t v = acc[mb][nt];
+            if (nan_out) v = float4_t{__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf("")};
+            float *dst = y + (size_t)r * n + c;
+            if (vec) {
+                *(float4_t *)dst = v;
+            } else {
+                for (int e = 0; e < 4; e++)
+                    if (c + e < n) dst[e] = v[e];
+            }
+        }
+    }
+}
+
 inline unsigned cdiv(size_t a, size_t b) { return (unsigned)((a + b - 1) / b); }
 
 // ---- variant tables -------------------------------------------------------------
@@ -1290,7 +1483,7 @@ const char *const kGemmNames[] = {"pipe-auto",   "256x256p2w8", "128x128p2w4", "
                                    "256x128w2x2", "128x128w2x2", "128x64w2x2"};
 const char *const kI8Names[] = {"256x256p2w8", "256x256p4k64w8", "256x128p3w8", "256x128p3",
                                  "128x128w2x2", "256x128w2x2", "64x64w2x2"};
-const char *const kGroupedNames[] = {"wave16x16"};
+const char *const kGroupedNames[] = {"pipe-auto", "pipe256x128w8", "wave16x16"};
 
 template <int W, int MPAD, bool G32>
 void gemv_launch_one(const Weight &w, const half_t *x, int m, float *y, hipStream_t s) {
@@ -1460,7 +1653,7 @@ int variant_count(const char *family) {
     if (f == "gemv") return 2;
     if (f == "gemm_w4a16") return 7;
     if (f == "i8_gemm") return 7;
-    if (f == "grouped") return 1;
+    if (f == "grouped") return 3;
     return 0;
 }
 
@@ -1503,10 +1696,24 @@ void launch_grouped_records(const Weight &w, const uint32_t *records, int m, flo
     gv_launch<2, false>(w, records, nullptr, m, 8, y, nullptr, nullptr, s);
 }
 
+// Variant 1 is grouped_pipe_kernel (256x128 tiles, 8 waves), variant 2 the
+// one-wave-per-16x16-tile grouped_kernel, variant 0 ("auto") the first when
+// its grid covers at least half the compute units and the second otherwise.
+// All fold in the reference order, so all give the same bits.
 void launch_grouped(const Weight &w, const int8_t *q, const float *sx, int m, float *y,
                     const int *bad, int variant, hipStream_t s) {
-    (void)variant;
     if (m == 0) return;
+    const bool pipe = variant == 1 || (variant == 0 && 2 * cdiv(m, 256) * cdiv(w.rows, 128) >= (unsigned)device_cus());
+    if (pipe && (size_t)256 * w.groups * 64 < ((size_t)1 << 31) && (size_t)8 * w.kblocks() * 1024 < ((size_t)1 << 31)) {
+        const dim3 blocks(cdiv(m, 256) * cdiv(w.rows, 128));
+        if (w.bits == 4)
+            hipLaunchKernelGGL((grouped_pipe_kernel<4, 256, 128, 2, 4>), blocks, dim3(512), 0, s, w.codes, w.scales, q,
+                               sx, m, w.rows, w.groups, w.kblocks(), y, bad);
+        else
+            hipLaunchKernelGGL((grouped_pipe_kernel<8, 256, 128, 2, 4>), blocks, dim3(512), 0, s, w.codes, w.scales, q,
+                               sx, m, w.rows, w.groups, w.kblocks(), y, bad);
+        return;
+    }
     dim3 grid(cdiv(w.tiles(), 4), cdiv(m, 16));
     if (w.bits == 4)
         hipLaunchKernelGGL(grouped_kernel<4>, grid, dim3(256), 0, s, w.codes, w.scales, q, sx, m, w.rows,

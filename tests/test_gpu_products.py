@@ -40,6 +40,43 @@ def test_grouped_matches_avx2_order_bit_exact(ctx, oracle, wb, ab):
         assert bits_equal(got, want), (m, k, n, float(np.abs(got - want).max()))
 
 
+@pytest.mark.parametrize("wb,ab", [(4, 8), (8, 8), (4, 4)])
+@pytest.mark.parametrize("m,k,n", [(300, 4096, 520), (257, 1088, 200), (513, 64, 129), (40, 640, 1040)])
+def test_grouped_large_m_pipeline_bit_exact(ctx, oracle, wb, ab, m, k, n):
+    """M > 16 runs the pipelined grouped kernel: bit for bit the AVX2 fold
+    order of int8.rs:524-585 and the one-wave-per-tile kernel (ragged rows and
+    columns, an odd group count, a single group)."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(m + k + n + wb + ab)
+    raw = oracle.f32_to_bf16((rng.standard_normal((n, k)) * 0.05).astype(np.float32))
+    x = (rng.standard_normal((m, k)) * 1.5).astype(np.float32)
+    w = ctx.quantize(dev(raw), rocm.BF16, n, k, wb, 64)
+    mode = rocm.W4A4 if ab == 4 else rocm.W4A8
+    outs = []
+    for name in ("pipe256x128w8", "wave16x16"):
+        ctx.select_variant("grouped", name)
+        y = empty((m, n), torch.float32)
+        ctx.linear(w, dev(x), rocm.F32, m, y, mode)
+        outs.append(host(ctx, y))
+    ctx.select_variant("grouped", "pipe-auto")
+    codes, scales = oracle.weight_quantize(raw, n, k, wb)
+    want = oracle.matrix_apply(x, m, codes, scales, n, k, ab, fused=True)
+    assert bits_equal(outs[0], want), float(np.abs(outs[0] - want).max())
+    assert bits_equal(outs[1], outs[0])
+
+
+def test_grouped_large_m_nonfinite_activation_makes_every_output_nan(ctx, oracle):
+    """int8.rs:170-173 at M > 16: one non-finite activation -> every output NaN."""
+    torch = pytest.importorskip("torch")
+    raw = oracle.f32_to_bf16(np.full((48, 256), 0.01, np.float32))
+    w = ctx.quantize(dev(raw), rocm.BF16, 48, 256, 4, 64)
+    x = np.ones((40, 256), np.float32)
+    x[33, 5] = np.inf
+    y = empty((40, 48), torch.float32)
+    ctx.linear(w, dev(x), rocm.F32, 40, y, rocm.W4A8)
+    assert np.isnan(host(ctx, y)).all()
+
+
 @pytest.mark.parametrize("case", range(5))
 @pytest.mark.parametrize("bits", [4, 8])
 def test_kernel_check_cases_vs_project(ctx, oracle, case, bits):
