@@ -1474,6 +1474,182 @@ __global__ __launch_bounds__(WGM *WGN * 64) void grouped_pipe_kernel(
     }
 }
 
+// Fused MLP on the same pipeline (grouped_q4_mlp.wgsl:1-105, int8.rs fold):
+// gate and up products of one 256-row x 64-column block (one requant block),
+// silu(g) * u, then the A8 requantization of each row's 64 columns, exactly
+// as mlp_requant_kernel computes them. 8 waves stacked along M (wave tile
+// 32 x 64): a row's 64 columns are held by the four lanes j, j+16, j+32,
+// j+48 of one wave, so the row maximum is two shuffles. Q4 weights.
+__global__ __launch_bounds__(512) void mlp_pipe_kernel(
+    const uint8_t *__restrict__ gcodes, const uint8_t *__restrict__ gscales, const uint8_t *__restrict__ ucodes,
+    const uint8_t *__restrict__ uscales, const int8_t *__restrict__ q, const float *__restrict__ sx, int m, int n,
+    int groups, int kbs, int8_t *__restrict__ qo, float *__restrict__ so, const int *__restrict__ bad) {
+    constexpr int BM = 256, WAVES = 8, MB = 2, NT = 4;
+    constexpr int XSTAGE = BM * 128;   // activation codes, 2 groups per step
+    constexpr int CSTAGE = 8 * 1024;   // gate tiles 0-3, up tiles 0-3: one tile16x128 chunk each
+    constexpr int SWSTAGE = 2 * 1024;  // scale records: [weight][8 tiles x 128 B], tiles 0-3 used
+    constexpr int SXSTAGE = BM * 8;
+    constexpr int XPW = BM / 8 / WAVES;
+    __shared__ __align__(16) uint8_t xs[2 * XSTAGE];
+    __shared__ __align__(16) uint8_t cs[2 * CSTAGE];
+    __shared__ __align__(16) uint8_t sws[2 * SWSTAGE];
+    __shared__ __align__(16) uint8_t sxs[2 * SXSTAGE];
+
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), lane = threadIdx.x % 64;
+    const int qd = lane / 16, j = lane % 16;
+    const int tiles_m = (m + BM - 1) / BM, tiles_n = n / 64;
+    int tm, tn;
+    xcd_tile(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+    const int row0 = tm * BM, col0 = tn * 64, tile0 = col0 / 16;
+    const int rvalid = min(BM, m - row0);
+    const uint32_t rowbytes = (uint32_t)groups * 64;
+    const int32x4_t rq = buffer_rsrc(q + (size_t)row0 * rowbytes, (uint32_t)rvalid * rowbytes);
+    const int32x4_t rcg = buffer_rsrc(gcodes + (size_t)tile0 * kbs * 1024, (uint32_t)(4 * kbs * 1024));
+    const int32x4_t rcu = buffer_rsrc(ucodes + (size_t)tile0 * kbs * 1024, (uint32_t)(4 * kbs * 1024));
+    const int32x4_t rwg = buffer_rsrc(gscales + (size_t)tile0 * kbs * 128, (uint32_t)(4 * kbs * 128));
+    const int32x4_t rwu = buffer_rsrc(uscales + (size_t)tile0 * kbs * 128, (uint32_t)(4 * kbs * 128));
+    // (records of tiles 4-7 fall past these four tiles' range and read as zero)
+    const int32x4_t rs = buffer_rsrc(sx + (size_t)row0 * groups, (uint32_t)(rvalid * groups * 4));
+    const uint32_t xs_lds = lds_address(xs), cs_lds = lds_address(cs);
+    const uint32_t sws_lds = lds_address(sws), sxs_lds = lds_address(sxs);
+
+    const int lrow = lane / 8;
+    const uint32_t xoff[2] = {
+        (uint32_t)(lrow * rowbytes + (((lane % 8) ^ ((lrow >> 1) & 7)) * 16)),
+        (uint32_t)(lrow * rowbytes + (((lane % 8) ^ (((lrow + 8) >> 1) & 7)) * 16))};
+    auto zero_len = [](int32x4_t r) { return int32x4_t{r[0], r[1], 0, r[3]}; };
+    auto load_stage = [&](int stage, int st, bool live) {
+        const int32x4_t nq = live ? rq : zero_len(rq);
+#pragma unroll
+        for (int p = 0; p < XPW; p++) {
+            const int blk = wave * XPW + p;
+            dma16(__builtin_amdgcn_readfirstlane(xs_lds + stage * XSTAGE + blk * 1024),
+                  xoff[p & 1] + (uint32_t)(blk * 8) * rowbytes + (uint32_t)st * 128, nq);
+        }
+        {   // wave w copies chunk w: gate tiles for w < 4, up tiles for w >= 4
+            const uint32_t lds = __builtin_amdgcn_readfirstlane(cs_lds + stage * CSTAGE + wave * 1024);
+            const uint32_t off = (uint32_t)(((wave % 4) * kbs + st) * 1024 + lane * 16);
+            if (wave < 4) dma16(lds, off, live ? rcg : zero_len(rcg));
+            else dma16(lds, off, live ? rcu : zero_len(rcu));
+        }
+        if (wave < 2) {  // wave 0 the gate records, wave 1 the up records: lane l -> tile l / 8, piece l % 8
+            // (lanes of tiles 4-7 load records the block does not use, or zeros past the end)
+            const uint32_t lds = __builtin_amdgcn_readfirstlane(sws_lds + stage * SWSTAGE + wave * 1024);
+            const uint32_t off = (uint32_t)(((lane / 8) * kbs + st) * 128 + (lane % 8) * 16);
+            if (wave == 0) dma16(lds, off, live ? rwg : zero_len(rwg));
+            else dma16(lds, off, live ? rwu : zero_len(rwu));
+        }
+        {
+            const int r = wave * 32 + lane / 2;
+            dma4(__builtin_amdgcn_readfirstlane(sxs_lds + stage * SXSTAGE + wave * 256),
+                 (uint32_t)((r * groups + 2 * st + (lane & 1)) * 4), live ? rs : zero_len(rs));
+        }
+    };
+
+    float4_t ga[MB][NT], ua[MB][NT];
+#pragma unroll
+    for (int a = 0; a < MB; a++)
+#pragma unroll
+        for (int b = 0; b < NT; b++) ga[a][b] = ua[a][b] = float4_t{0.f, 0.f, 0.f, 0.f};
+    const int4_t zero = {0, 0, 0, 0};
+    const bool nan_out = bad != nullptr && *bad != 0;
+    const int steps = (groups + 1) / 2;
+
+    auto fold_group = [&](const uint8_t *xst, const uint8_t *cst, const uint8_t *swst, const uint8_t *sxst, int gp) {
+        int4_t gb[NT], ub[NT];
+        float4_t gs[NT], us[NT];
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+#pragma unroll
+            for (int wgt = 0; wgt < 2; wgt++) {
+                const uint2_t wds = *(const uint2_t *)(cst + (wgt * 4 + nt) * 1024 + lane * 16 + gp * 8);
+                const uint2_t lo = nibbles_to_i8(wds[0]), hi = nibbles_to_i8(wds[1]);
+                const int4_t b = int4_t{(int)lo[0], (int)lo[1], (int)hi[0], (int)hi[1]};
+                const float4_t s01 = *(const float4_t *)(swst + wgt * 1024 + nt * 128 + qd * 32);
+                const float4_t s23 = *(const float4_t *)(swst + wgt * 1024 + nt * 128 + qd * 32 + 16);
+                const float4_t sv = gp ? float4_t{s01[1], s01[3], s23[1], s23[3]} : float4_t{s01[0], s01[2], s23[0], s23[2]};
+                if (wgt == 0) {
+                    gb[nt] = b;
+                    gs[nt] = sv;
+                } else {
+                    ub[nt] = b;
+                    us[nt] = sv;
+                }
+            }
+        }
+#pragma unroll
+        for (int mb = 0; mb < MB; mb++) {
+            const int r = wave * 32 + mb * 16 + j;
+            const int c1 = 4 * gp + qd / 2, c2 = c1 + 2;
+            const uint2_t a0 = *(const uint2_t *)(xst + r * 128 + ((c1 ^ ((r >> 1) & 7)) * 16) + 8 * (qd & 1));
+            const uint2_t a1 = *(const uint2_t *)(xst + r * 128 + ((c2 ^ ((r >> 1) & 7)) * 16) + 8 * (qd & 1));
+            const int4_t afr = int4_t{(int)a0[0], (int)a0[1], (int)a1[0], (int)a1[1]};
+            const float sxv = *(const float *)(sxst + r * 8 + gp * 4);
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                const int4_t gd = mfma_i8(gb[nt], afr, zero);
+                const int4_t ud = mfma_i8(ub[nt], afr, zero);
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    ga[mb][nt][v] = __builtin_fmaf((float)gd[v], __fmul_rn(gs[nt][v], sxv), ga[mb][nt][v]);
+                    ua[mb][nt][v] = __builtin_fmaf((float)ud[v], __fmul_rn(us[nt][v], sxv), ua[mb][nt][v]);
+                }
+            }
+        }
+    };
+
+    if (!nan_out) {
+        load_stage(0, 0, true);
+        for (int st = 0; st < steps; st++) {
+            const int cur = st & 1;
+            __builtin_amdgcn_s_waitcnt(0x0F70);
+            __builtin_amdgcn_s_barrier();
+            load_stage(cur ^ 1, st + 1, st + 1 < steps);
+            const uint8_t *xst = xs + cur * XSTAGE, *cst = cs + cur * CSTAGE;
+            const uint8_t *swst = sws + cur * SWSTAGE, *sxst = sxs + cur * SXSTAGE;
+            fold_group(xst, cst, swst, sxst, 0);
+            if (2 * st + 1 < groups) fold_group(xst, cst, swst, sxst, 1);
+        }
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // no LDS write in flight once the block ends
+    }
+
+    // silu(g) * u and the A8 requantization of the row's 64 columns
+    const int blocks = n / 64;
+#pragma unroll
+    for (int mb = 0; mb < MB; mb++) {
+        const int r = row0 + wave * 32 + mb * 16 + j;
+        float val[NT][4];
+        float local = 0.0f;
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const float gv = ga[mb][nt][v];
+                const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-gv)));
+                val[nt][v] = __fmul_rn(__fmul_rn(gv, sig), ua[mb][nt][v]);
+                local = fmaxf(local, fabsf(val[nt][v]));
+            }
+        local = fmaxf(local, __shfl_xor(local, 16));
+        local = fmaxf(local, __shfl_xor(local, 32));
+        const float scale = fmaxf(__fdiv_rn(local, 127.0f), FLT_MIN);
+        const float inverse = __frcp_rn(scale);
+        if (r >= m) continue;
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            uint32_t packed = 0;
+            if (!nan_out) {
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const float c = fminf(fmaxf(__builtin_rintf(__fmul_rn(val[nt][v], inverse)), -127.0f), 127.0f);
+                    packed |= ((uint32_t)(uint8_t)(int8_t)(int)c) << (8 * v);
+                }
+            }
+            *(uint32_t *)(qo + (size_t)r * n + col0 + nt * 16 + 4 * qd) = packed;
+        }
+        if (qd == 0) so[(size_t)r * blocks + tn] = nan_out ? __builtin_nanf("") : scale;
+    }
+}
+
 inline unsigned cdiv(size_t a, size_t b) { return (unsigned)((a + b - 1) / b); }
 
 // ---- variant tables -------------------------------------------------------------
@@ -1726,6 +1902,14 @@ void launch_grouped(const Weight &w, const int8_t *q, const float *sx, int m, fl
 void launch_mlp_requant(const Weight &gate, const Weight &up, const int8_t *q, const float *sx,
                         int m, int8_t *qo, float *so, const int *bad, hipStream_t s) {
     if (m == 0) return;
+    // the pipelined kernel when its grid covers half the compute units (same bits either way)
+    const unsigned pblocks = cdiv(m, 256) * (unsigned)(gate.rows / 64);
+    if (2 * pblocks >= (unsigned)device_cus() && (size_t)256 * gate.groups * 64 < ((size_t)1 << 31) &&
+        (size_t)4 * gate.kblocks() * 1024 < ((size_t)1 << 31) && ((uintptr_t)qo & 3) == 0 && gate.rows % 4 == 0) {
+        hipLaunchKernelGGL(mlp_pipe_kernel, dim3(pblocks), dim3(512), 0, s, gate.codes, gate.scales, up.codes,
+                           up.scales, q, sx, m, gate.rows, gate.groups, gate.kblocks(), qo, so, bad);
+        return;
+    }
     dim3 grid(gate.rows / 64, cdiv(m, 16));
     hipLaunchKernelGGL(mlp_requant_kernel, grid, dim3(256), 0, s, gate.codes, gate.scales, up.codes,
                        up.scales, q, sx, m, gate.rows, gate.groups, gate.kblocks(), qo, so, bad);

@@ -172,6 +172,36 @@ def test_pair_shares_one_quantization(ctx, oracle):
     assert bits_equal(host(ctx, ya), host(ctx, y1)) and bits_equal(host(ctx, yb), host(ctx, y2))
 
 
+def test_fused_mlp_large_m_pipeline_equals_unfused(ctx, oracle):
+    """The pipelined fused MLP (grid of 256-row x 64-column blocks, ragged m,
+    an odd group count) is word-exact with the unfused composition."""
+    torch = pytest.importorskip("torch")
+    m, n, k = 600, 2752, 1088
+    rng = np.random.default_rng(11)
+    graw = oracle.f32_to_bf16((rng.standard_normal((n, k)) * 0.03).astype(np.float32))
+    uraw = oracle.f32_to_bf16((rng.standard_normal((n, k)) * 0.03).astype(np.float32))
+    gate = ctx.quantize(dev(graw), rocm.BF16, n, k, 4, 64)
+    up = ctx.quantize(dev(uraw), rocm.BF16, n, k, 4, 64)
+    x = (rng.standard_normal((m, k)) * 1.3).astype(np.float32)
+    xd = dev(x)
+    q = empty((m, n), torch.int8)
+    s = empty((m, n // 64), torch.float32)
+    ctx.mlp_requant(gate, up, xd, m, q, s)
+    g = empty((m, n), torch.float32)
+    u = empty((m, n), torch.float32)
+    ctx.linear_pair(gate, up, xd, m, g, u)
+    ctx.silu_mul(g, u, m * n)
+    q2 = empty((m, n), torch.int8)
+    s2 = empty((m, n // 64), torch.float32)
+    ctx.act_quantize(g, m, n, 8, q2, s2)
+    assert np.array_equal(host(ctx, q), host(ctx, q2))
+    assert bits_equal(host(ctx, s), host(ctx, s2))
+    # a non-finite activation: every scale NaN, every code 0 (int8.rs:170-173)
+    x[599, 7] = np.nan
+    ctx.mlp_requant(gate, up, dev(x), m, q, s)
+    assert np.isnan(host(ctx, s)).all() and not host(ctx, q).any()
+
+
 def test_fused_mlp_requant_equals_unfused(ctx, oracle):
     """grouped_q4.rs:313-354: fused gate/up/SiLU/requant == unfused, word-exact;
     both against the oracle composition within one code."""
