@@ -197,6 +197,25 @@ def secondary(torch, ctx, rocm, stream) -> dict:
                                                    "variant": ctx.info()["variants"]["gemm_w4a16"]}
     w.free()
     del x, y
+    # the reference's own numerics (bit-exact W4A8, int8.rs fold order) at the config 5 shape:
+    # f32 activations quantized to A8 on device, then the grouped product
+    wf = torch.randn((n, k), generator=torch.Generator(device="cuda").manual_seed(1), device="cuda") * 0.02
+    torch.cuda.synchronize()
+    w = ctx.quantize(wf, rocm.F32, n, k, 4, 64)
+    del wf
+    x = torch.randn((m, k), generator=torch.Generator(device="cuda").manual_seed(0), device="cuda")
+    y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    fn = lambda r: ctx.linear(w, x, rocm.F32, m, y, rocm.W4A8)  # noqa: E731
+    fn(0)
+    ms = timed_ms(torch, stream, fn, 5)
+    tops = 2 * m * n * k / (ms * 1e-3) / 1e12
+    out["q4_prefill_w4a8_bitexact_m16384_k4096_n14336"] = {
+        "ms": round(ms, 4), "TOP/s": round(tops, 1), "frac_of_i8_peak": round(tops / I8_PEAK_TOPS, 4),
+        "variant": ctx.info()["variants"].get("grouped"),
+        "note": "includes the A8 quantization of the f32 activations; VALU-bound fold (3 ops per output per group)"}
+    w.free()
+    del x, y
     # config 3: encoder forward, 24 x (1024, 16x64, 4096), batch 8 x 1024 tokens
     cfg = rocm.EncoderConfig(layers=24, hidden=1024, heads=16, head_dim=64, ffn=4096, vocab=32000, ln_eps=1e-5)
     enc = ctx.encoder_random(cfg, 1)
