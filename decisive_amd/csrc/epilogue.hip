@@ -16,6 +16,7 @@
 #include <float.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "kernels.hpp"
 
@@ -293,8 +294,10 @@ __global__ __launch_bounds__(kAttnWaves * 64, 4) void attention_kernel(const hal
     }
 
     const int steps = (seq + kAttnKeys - 1) / kAttnKeys;
-    load_step(0, 0);
-    for (int st = 0; st < steps; st++) {
+    // one step of 64 keys; MASK (the ragged last step only) sets scores of
+    // keys past seq to -inf
+    auto step = [&](int st, auto mask_c) {
+        constexpr bool MASK = decltype(mask_c)::value;
         const int cur = st & 1;
         // this wave's loads of step st are done; the barrier covers every wave
         // (and every wave has finished reading the stage the next loads overwrite)
@@ -318,12 +321,11 @@ __global__ __launch_bounds__(kAttnWaves * 64, 4) void attention_kernel(const hal
                 sc[qb][kb] = mfma_f16(kf[1], qf[qb][1], acc);
             }
         }
-        const bool ragged = (st + 1) * kAttnKeys > seq;
         half8_t pf[kAttnQB][2];  // P^T operands of the two 32-key blocks
 #pragma unroll
         for (int qb = 0; qb < kAttnQB; qb++) {
             // online softmax over this step's keys for query j (lanes j, j+16, j+32, j+48)
-            if (ragged) {
+            if (MASK) {
 #pragma unroll
                 for (int kb = 0; kb < 4; kb++)
 #pragma unroll
@@ -379,7 +381,12 @@ __global__ __launch_bounds__(kAttnWaves * 64, 4) void attention_kernel(const hal
 #pragma unroll
                 for (int qb = 0; qb < kAttnQB; qb++) o[qb][db] = mfma_f16(vf, pf[qb][c], o[qb][db]);
             }
-    }
+    };
+    load_step(0, 0);
+    const int full = seq / kAttnKeys;  // steps with 64 live keys
+    for (int st = 0; st < full; st++) step(st, std::false_type{});
+    if (full < steps) step(full, std::true_type{});
+
     __builtin_amdgcn_s_waitcnt(0x0F70);  // no LDS write in flight once the block ends
 #pragma unroll
     for (int qb = 0; qb < kAttnQB; qb++) {
