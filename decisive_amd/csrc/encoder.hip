@@ -27,7 +27,15 @@ const Weight &weight_of(const dz_weight *h);
 int32_t weight_quantize(dz_ctx *ctx, const void *values, int dtype, size_t rows, size_t cols, int bits,
                         int group, dz_weight **out);
 void weight_free(dz_weight *h);
+int32_t ctx_readout_rows(dz_ctx *ctx, const Weight &w, const float *norm, const void *hidden, int dtype,
+                         const int32_t *select, size_t rows, float eps, float *logits);
 
+}  // namespace dz
+
+namespace dz {
+constexpr int kReadoutCodes = DZ_READOUT_CODES;
+constexpr int kReadoutMarkers = DZ_READOUT_MAX_MARKERS;
+constexpr float kReadoutEps = DZ_READOUT_EPS;
 }  // namespace dz
 
 struct dz_encoder {
@@ -38,6 +46,12 @@ struct dz_encoder {
     };
     std::vector<Layer> layers;
     dz_weight *embed = nullptr;          // [vocab x hidden] Q4 group-64
+    // the decision readout (pplx_flash/mod.rs:149-185): 255 rows x hidden, Q4
+    // group-64 as the packed readout, after a zero-centred RMSNorm
+    dz_weight *readout = nullptr;
+    float *readout_norm = nullptr;
+    int32_t *markers = nullptr;          // device copy of the readout rows of one request
+    float *logits = nullptr;             // [kReadoutMarkers x 255]
     std::vector<uint8_t> embed_wire;     // the same table in the packed.rs layout (host)
     float *ln0w = nullptr, *ln0b = nullptr;
     // activations (f16) sized for `capacity` tokens
@@ -131,7 +145,9 @@ void encoder_destroy(dz_ctx *ctx, dz_encoder *e) {
             if (p) hipFree(p);
     }
     weight_free(e->embed);
-    for (float *p : {e->ln0w, e->ln0b})
+    weight_free(e->readout);
+    for (void *p : {(void *)e->ln0w, (void *)e->ln0b, (void *)e->readout_norm, (void *)e->markers,
+                    (void *)e->logits})
         if (p) hipFree(p);
     free_buffers(e);
     delete e;
@@ -173,6 +189,15 @@ int32_t encoder_create_random(dz_ctx *ctx, const dz_encoder_config *cfg, uint64_
         if (!rc) rc = const_vec(ctx, &L.ln2w, d, 1.0f);
         if (!rc) rc = const_vec(ctx, &L.ln2b, d, 0.0f);
     }
+    if (!rc) rc = random_weight(ctx, scratch, kReadoutCodes, d, s++, 4, 64, &e->readout);
+    if (!rc) {
+        // zero-centred norm weights near zero, as a trained model's are
+        hipError_t err2 = hipMalloc(&e->readout_norm, d * sizeof(float));
+        if (err2 == hipSuccess) err2 = hipMalloc(&e->markers, kReadoutMarkers * sizeof(int32_t));
+        if (err2 == hipSuccess) err2 = hipMalloc(&e->logits, (size_t)kReadoutMarkers * kReadoutCodes * sizeof(float));
+        if (err2 != hipSuccess) rc = ctx_hip_fail(ctx, err2, "encoder readout");
+        else launch_fill_normal_f32(e->readout_norm, d, s++, 0.02f, ctx_stream(ctx));
+    }
     if (!rc) {
         // host copy of the embedding table in the wire layout (the cache's source)
         size_t wire_bytes = (size_t)c.vocab * (d / 64) * 36;
@@ -196,6 +221,7 @@ int32_t encoder_create_random(dz_ctx *ctx, const dz_encoder_config *cfg, uint64_
 const dz_weight *encoder_weight(const dz_encoder *e, int layer, int which) {
     if (!e) return nullptr;
     if (which == 4) return e->embed;
+    if (which == 5) return e->readout;
     if (layer < 0 || layer >= (int)e->layers.size()) return nullptr;
     const auto &L = e->layers[layer];
     switch (which) {
@@ -224,9 +250,12 @@ int32_t encoder_read_rows(dz_ctx *ctx, const dz_encoder *e, const int32_t *ids, 
     return DZ_OK;
 }
 
-int32_t encoder_forward(dz_ctx *ctx, dz_encoder *e, const int32_t *ids_dev, const void *rows_host,
-                        size_t batch, size_t seq, float *out) {
-    if (!e || !out || (!ids_dev && !rows_host)) return ctx_fail(ctx, DZ_INVALID_REQUEST, "null pointer");
+namespace {
+
+// The encoder layers over batch x seq tokens, leaving the last hidden states
+// (f16 [batch*seq x hidden]) in e->h.
+int32_t encoder_hidden(dz_ctx *ctx, dz_encoder *e, const int32_t *ids_dev, const void *rows_host,
+                       size_t batch, size_t seq) {
     if (batch == 0 || seq == 0) return ctx_fail(ctx, DZ_INVALID_REQUEST, "empty batch");
     size_t tokens = batch * seq;
     if (tokens > (1u << 20)) return ctx_fail(ctx, DZ_INPUT_TOO_LONG, "input budget exceeded");
@@ -272,9 +301,62 @@ int32_t encoder_forward(dz_ctx *ctx, dz_encoder *e, const int32_t *ids_dev, cons
         launch_w4a16_f16(weight_of(L.down), e->ff, m, e->t, 2, e->h, gv, s);
         launch_layernorm(e->t, e->h, 1, m, d, L.ln2w, L.ln2b, c.ln_eps, s);
     }
-    launch_mean_rows(e->h, 1, (int)batch, (int)seq, d, out, s);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return ctx_hip_fail(ctx, err, "encoder forward");
+    return DZ_OK;
+}
+
+}  // namespace
+
+int32_t encoder_forward(dz_ctx *ctx, dz_encoder *e, const int32_t *ids_dev, const void *rows_host,
+                        size_t batch, size_t seq, float *out) {
+    if (!e || !out || (!ids_dev && !rows_host)) return ctx_fail(ctx, DZ_INVALID_REQUEST, "null pointer");
+    int32_t rc = encoder_hidden(ctx, e, ids_dev, rows_host, batch, seq);
+    if (rc) return rc;
+    launch_mean_rows(e->h, 1, (int)batch, (int)seq, e->cfg.hidden, out, ctx_stream(ctx));
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return ctx_hip_fail(ctx, err, "encoder forward");
+    return DZ_OK;
+}
+
+int32_t encoder_hidden_rows(dz_ctx *ctx, dz_encoder *e, const void *rows_host, size_t seq, float *hidden) {
+    if (!e || !rows_host || !hidden) return ctx_fail(ctx, DZ_INVALID_REQUEST, "null pointer");
+    int32_t rc = encoder_hidden(ctx, e, nullptr, rows_host, 1, seq);
+    if (rc) return rc;
+    launch_to_f32(e->h, 1, seq * (size_t)e->cfg.hidden, hidden, ctx_stream(ctx));
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return ctx_hip_fail(ctx, err, "encoder hidden rows");
+    return DZ_OK;
+}
+
+int32_t encoder_readout_params(const dz_encoder *e, const dz_weight **w, const float **norm) {
+    if (!e) return DZ_INVALID_REQUEST;
+    if (w) *w = e->readout;
+    if (norm) *norm = e->readout_norm;
+    return DZ_OK;
+}
+
+int32_t encoder_readout(dz_ctx *ctx, dz_encoder *e, const void *rows_host, size_t seq, const int32_t *markers,
+                        size_t count, float *logits_host) {
+    if (!e || !rows_host || (count && (!markers || !logits_host)))
+        return ctx_fail(ctx, DZ_INVALID_REQUEST, "null pointer");
+    if (count == 0) return ctx_fail(ctx, DZ_INVALID_REQUEST, "no readout markers");
+    if (count > (size_t)kReadoutMarkers) return ctx_fail(ctx, DZ_INPUT_TOO_LONG, "too many readout markers");
+    for (size_t i = 0; i < count; i++)
+        if (markers[i] < 0 || (size_t)markers[i] >= seq)
+            return ctx_fail(ctx, DZ_INVALID_REQUEST, "readout marker outside the sequence");
+    int32_t rc = encoder_hidden(ctx, e, nullptr, rows_host, 1, seq);
+    if (rc) return rc;
+    hipStream_t s = ctx_stream(ctx);
+    hipError_t err = hipMemcpyAsync(e->markers, markers, count * sizeof(int32_t), hipMemcpyHostToDevice, s);
+    if (err != hipSuccess) return ctx_hip_fail(ctx, err, "marker upload");
+    rc = ctx_readout_rows(ctx, weight_of(e->readout), e->readout_norm, e->h, 1, e->markers, count,
+                          kReadoutEps, e->logits);
+    if (rc) return rc;
+    err = hipMemcpyAsync(logits_host, e->logits, count * (size_t)kReadoutCodes * sizeof(float),
+                         hipMemcpyDeviceToHost, s);
+    if (err == hipSuccess) err = hipStreamSynchronize(s);
+    if (err != hipSuccess) return ctx_hip_fail(ctx, err, "logits readback");
     return DZ_OK;
 }
 

@@ -157,6 +157,52 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__restrict__ 
         y[base + i] = (x[base + i] * scale) * (zero_centered ? 1.0f + w[i] : w[i]);
 }
 
+// The readout's RMSNorm (pplx_flash/cpu.rs:310-333 rms_from, as applied by
+// pplx_flash/mod.rs:149-155): the sum of squares runs in row order, as the
+// reference's iterator sum does, so the result is bit-exact with it. One block
+// per selected row (`rows` picks hidden rows; null takes row r); the squares
+// are formed in parallel and lane 0 adds them in order from LDS.
+__global__ __launch_bounds__(64) void readout_rms_kernel(const void *__restrict__ h, int dtype,
+                                                         const int32_t *__restrict__ rows, int d,
+                                                         const float *__restrict__ w, float eps,
+                                                         int zero_centered, float *__restrict__ y) {
+    extern __shared__ float squares[];
+    __shared__ float scale_sh;
+    const size_t base = (size_t)(rows ? rows[blockIdx.x] : (int)blockIdx.x) * d;
+    for (int i = threadIdx.x; i < d; i += 64) {
+        const float v = ld(h, dtype, base + i);
+        squares[i] = __fmul_rn(v, v);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float ss = 0.0f;
+        for (int i = 0; i < d; i++) ss = __fadd_rn(ss, squares[i]);
+        // v_sqrt_f32 is not correctly rounded; a float's square root taken in
+        // f64 and rounded to f32 is (the exact root is never near enough to a
+        // float midpoint for the f64 error to matter)
+        const float t = __fadd_rn(__fdiv_rn(ss, (float)d), eps);
+        scale_sh = __fdiv_rn(1.0f, __double2float_rn(__dsqrt_rn((double)t)));
+    }
+    __syncthreads();
+    const float scale = scale_sh;
+    float *dst = y + (size_t)blockIdx.x * d;
+    for (int i = threadIdx.x; i < d; i += 64) {
+        const float g = zero_centered ? __fadd_rn(1.0f, w[i]) : w[i];
+        dst[i] = __fmul_rn(__fmul_rn(ld(h, dtype, base + i), scale), g);
+    }
+}
+
+// Sets bit `bit` of *flag when any of the n values is not finite.
+__global__ void flag_nonfinite_kernel(const float *__restrict__ y, size_t n, int *flag, int bit) {
+    size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+    if (i < n && !isfinite(y[i])) atomicOr(flag, bit);
+}
+
+__global__ void to_f32_kernel(const void *__restrict__ x, int dtype, size_t n, float *__restrict__ y) {
+    size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+    if (i < n) y[i] = ld(x, dtype, i);
+}
+
 __global__ void gelu_kernel(void *x, int dtype, size_t n) {
     size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
     if (i >= n) return;
@@ -456,6 +502,18 @@ void launch_rmsnorm(const float *x, float *y, int rows, int d, const float *w, f
                     int zero_centered, hipStream_t s) {
     if (rows)
         hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, s, x, y, d, w, eps, zero_centered);
+}
+void launch_readout_rms(const void *h, int dtype, const int32_t *rows, int n, int d, const float *w,
+                        float eps, int zero_centered, float *y, hipStream_t s) {
+    if (n && d)
+        hipLaunchKernelGGL(readout_rms_kernel, dim3(n), dim3(64), (size_t)d * sizeof(float), s, h, dtype,
+                           rows, d, w, eps, zero_centered, y);
+}
+void launch_flag_nonfinite(const float *y, size_t n, int *flag, int bit, hipStream_t s) {
+    if (n) hipLaunchKernelGGL(flag_nonfinite_kernel, dim3(cdiv(n, 256)), dim3(256), 0, s, y, n, flag, bit);
+}
+void launch_to_f32(const void *x, int dtype, size_t n, float *y, hipStream_t s) {
+    if (n) hipLaunchKernelGGL(to_f32_kernel, dim3(cdiv(n, 256)), dim3(256), 0, s, x, dtype, n, y);
 }
 void launch_gelu(void *x, int dtype, size_t n, hipStream_t s) {
     if (n) hipLaunchKernelGGL(gelu_kernel, dim3(cdiv(n, 256)), dim3(256), 0, s, x, dtype, n);

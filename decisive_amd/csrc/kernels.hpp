@@ -68,6 +68,14 @@ void launch_layernorm(const void *x, void *y, int dtype, int rows, int d, const 
                       const float *b, float eps, hipStream_t s);
 void launch_rmsnorm(const float *x, float *y, int rows, int d, const float *w, float eps,
                     int zero_centered, hipStream_t s);
+// Readout RMSNorm over n selected rows of h (f32 dtype 0 / f16 dtype 1; rows
+// null = the first n rows) into y f32 [n x d]; d <= kReadoutMaxCols.
+constexpr int kReadoutMaxCols = 16384;
+void launch_readout_rms(const void *h, int dtype, const int32_t *rows, int n, int d, const float *w,
+                        float eps, int zero_centered, float *y, hipStream_t s);
+void launch_flag_nonfinite(const float *y, size_t n, int *flag, int bit, hipStream_t s);
+// y f32 [n] = x (f32 dtype 0 / f16 dtype 1), exact
+void launch_to_f32(const void *x, int dtype, size_t n, float *y, hipStream_t s);
 void launch_gelu(void *x, int dtype, size_t n, hipStream_t s);
 void launch_silu_mul(float *g, const float *u, size_t n, hipStream_t s);
 void launch_add(void *x, const void *y, int dtype, size_t n, hipStream_t s);

@@ -43,6 +43,10 @@ int32_t encoder_row_bytes(const dz_encoder *enc, size_t *row_bytes);
 const dz_weight *encoder_weight(const dz_encoder *enc, int layer, int which);
 int32_t encoder_read_rows(dz_ctx *ctx, const dz_encoder *enc, const int32_t *ids, size_t count,
                           void *out);
+int32_t encoder_hidden_rows(dz_ctx *ctx, dz_encoder *e, const void *rows_host, size_t seq, float *hidden);
+int32_t encoder_readout_params(const dz_encoder *e, const dz_weight **w, const float **norm);
+int32_t encoder_readout(dz_ctx *ctx, dz_encoder *e, const void *rows_host, size_t seq, const int32_t *markers,
+                        size_t count, float *logits_host);
 int32_t encoder_forward(dz_ctx *ctx, dz_encoder *enc, const int32_t *ids_dev, const void *rows_host,
                         size_t batch, size_t seq, float *out);
 int32_t tune(dz_ctx *ctx, uint32_t budget_ms, const char *cache_in, char *cache_out, size_t cap);
@@ -113,6 +117,47 @@ int32_t ensure_work(dz_ctx *ctx, size_t bytes) {
     size_t want = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
     DZ_HIP(ctx, hipMalloc(&ctx->work, want), "workspace allocation");
     ctx->work_bytes = want;
+    return DZ_OK;
+}
+
+// Workspace bytes that enqueue_project needs for m rows.
+size_t project_work_bytes(const dz::Weight &w, size_t m) {
+    if (m <= 16) return 0;
+    return m * (size_t)w.groups * 64 + 256 + m * (size_t)w.groups * sizeof(float);
+}
+
+// packed.rs:75-119 project of x [m x cols] into y [m x rows(w)]; `work` holds
+// project_work_bytes(w, m). A non-finite activation sets bit 0 of the flag.
+void enqueue_project(dz_ctx *ctx, const dz::Weight &w, const float *x, size_t m, float *y, uint8_t *work) {
+    if (m <= 16) {
+        dz::launch_grouped_small(w, x, (int)m, 8, y, ctx->flag, true, ctx->stream);
+        return;
+    }
+    size_t qbytes = m * (size_t)w.groups * 64;
+    int8_t *q = (int8_t *)work;
+    float *sx = (float *)(work + (qbytes + 255) / 256 * 256);
+    dz::launch_act_quantize(x, (int)m, w.cols, 8, q, sx, ctx->flag, ctx->stream);
+    dz::launch_grouped_codes(w, q, sx, (int)m, y, ctx->flag, true, ctx->stream);
+}
+
+// pplx_flash/mod.rs:149-185 logits: the zero-centred RMSNorm of the selected
+// hidden rows (f32 dtype 0 or f16 dtype 1; `select` a device index array or
+// null), then project. Synchronous; logits on the device.
+int32_t readout_rows(dz_ctx *ctx, const dz::Weight &w, const float *norm, const void *hidden, int dtype,
+                     const int32_t *select, size_t rows, float eps, float *logits) {
+    const size_t xbytes = (rows * (size_t)w.cols * sizeof(float) + 255) / 256 * 256;
+    int32_t rc = ensure_work(ctx, xbytes + project_work_bytes(w, rows));
+    if (rc) return rc;
+    float *xn = (float *)ctx->work;
+    int bad = 0;
+    rc = flagged_sync(ctx, [&] {
+        dz::launch_readout_rms(hidden, dtype, select, (int)rows, w.cols, norm, eps, 1, xn, ctx->stream);
+        enqueue_project(ctx, w, xn, rows, logits, (uint8_t *)ctx->work + xbytes);
+        dz::launch_flag_nonfinite(logits, rows * (size_t)w.rows, ctx->flag, 2, ctx->stream);
+    }, &bad);
+    if (rc) return rc;
+    if (bad & 1) return fail(ctx, DZ_INFERENCE_FAILED, "nonfinite readout activation");
+    if (bad & 2) return fail(ctx, DZ_INFERENCE_FAILED, "non-finite packed logits");
     return DZ_OK;
 }
 
@@ -501,26 +546,24 @@ int32_t dz_project(dz_ctx *ctx, const dz_weight *w, const float *x, size_t m, fl
         return fail(ctx, DZ_INVALID_PARAMETERS, "invalid packed readout shape");
     if (m == 0) return DZ_OK;
     if (m > (1u << 24)) return fail(ctx, DZ_INPUT_TOO_LONG, "input budget exceeded");
+    int32_t rc = ensure_work(ctx, project_work_bytes(w->w, m));
+    if (rc) return rc;
     int bad = 0;
-    int32_t rc;
-    if (m <= 16) {
-        rc = flagged_sync(ctx, [&] {
-            dz::launch_grouped_small(w->w, x, (int)m, 8, y, ctx->flag, true, ctx->stream);
-        }, &bad);
-    } else {
-        size_t qbytes = m * (size_t)w->w.groups * 64, sbytes = m * (size_t)w->w.groups * sizeof(float);
-        rc = ensure_work(ctx, qbytes + sbytes + 256);
-        if (rc) return rc;
-        int8_t *q = (int8_t *)ctx->work;
-        float *s = (float *)((uint8_t *)ctx->work + (qbytes + 255) / 256 * 256);
-        rc = flagged_sync(ctx, [&] {
-            dz::launch_act_quantize(x, (int)m, w->w.cols, 8, q, s, ctx->flag, ctx->stream);
-            dz::launch_grouped_codes(w->w, q, s, (int)m, y, ctx->flag, true, ctx->stream);
-        }, &bad);
-    }
+    rc = flagged_sync(ctx, [&] { enqueue_project(ctx, w->w, x, m, y, (uint8_t *)ctx->work); }, &bad);
     if (rc) return rc;
     if (bad) return fail(ctx, DZ_INFERENCE_FAILED, "nonfinite readout activation");
     return DZ_OK;
+}
+
+int32_t dz_readout(dz_ctx *ctx, const dz_weight *w, const float *norm, const float *hidden, size_t rows,
+                   float eps, float *logits) {
+    DZ_BEGIN(ctx);
+    if (!w || !norm || (rows && (!hidden || !logits))) return fail(ctx, DZ_INVALID_REQUEST, "null pointer");
+    if (w->w.kind == dz::WeightKind::Q4G32 || w->w.cols % 64 != 0 || w->w.cols > dz::kReadoutMaxCols)
+        return fail(ctx, DZ_INVALID_PARAMETERS, "invalid packed readout shape");
+    if (rows == 0) return DZ_OK;
+    if (rows > (1u << 20)) return fail(ctx, DZ_INPUT_TOO_LONG, "input budget exceeded");
+    return readout_rows(ctx, w->w, norm, hidden, 0, nullptr, rows, eps, logits);
 }
 
 int32_t dz_act_quantize_records(dz_ctx *ctx, const float *x, size_t m, size_t k, uint32_t *records) {
@@ -698,6 +741,21 @@ int32_t dz_encoder_forward_rows(dz_ctx *ctx, dz_encoder *enc, const void *rows, 
     return dz::encoder_forward(ctx, enc, nullptr, rows, batch, seq, out);
 }
 
+int32_t dz_encoder_hidden_rows(dz_ctx *ctx, dz_encoder *enc, const void *rows, size_t seq, float *hidden) {
+    DZ_BEGIN(ctx);
+    return dz::encoder_hidden_rows(ctx, enc, rows, seq, hidden);
+}
+
+int32_t dz_encoder_readout_params(const dz_encoder *enc, const dz_weight **w, const float **norm) {
+    return dz::encoder_readout_params(enc, w, norm);
+}
+
+int32_t dz_encoder_readout_rows(dz_ctx *ctx, dz_encoder *enc, const void *rows, size_t seq,
+                                const int32_t *markers, size_t count, float *logits) {
+    DZ_BEGIN(ctx);
+    return dz::encoder_readout(ctx, enc, rows, seq, markers, count, logits);
+}
+
 // ---- tuner ---------------------------------------------------------------------------
 
 int32_t dz_tune(dz_ctx *ctx, uint32_t budget_ms, const char *cache_in, char *cache_out, size_t cap) {
@@ -736,5 +794,14 @@ int32_t weight_quantize(dz_ctx *ctx, const void *values, int dtype, size_t rows,
     return dz_weight_quantize(ctx, values, dtype, rows, cols, bits, group, out);
 }
 void weight_free(dz_weight *h) { free_weight(h); }
+int32_t ctx_readout_rows(dz_ctx *ctx, const Weight &w, const float *norm, const void *hidden, int dtype,
+                         const int32_t *select, size_t rows, float eps, float *logits) {
+    return readout_rows(ctx, w, norm, hidden, dtype, select, rows, eps, logits);
+}
+int32_t ctx_workspace(dz_ctx *ctx, size_t bytes, void **out) {
+    int32_t rc = ensure_work(ctx, bytes);
+    *out = rc ? nullptr : ctx->work;
+    return rc;
+}
 
 }  // namespace dz

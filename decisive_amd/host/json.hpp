@@ -1,34 +1,87 @@
 // json.hpp -- a small JSON value for the host layer (requests, parameters,
 // responses). The reference passes serde_json::Value through its inference
 // API (src/inference/mod.rs:18-42); this is the C++ stand-in: null, bool,
-// number (double), string, array and object (keys kept sorted, as
-// serde_json's default Map is), with a strict parser and a compact writer.
+// number (double, remembering whether it was written as an integer, as
+// serde_json's Number does), string, array and object (members kept in
+// insertion order: the reference builds serde_json with `preserve_order`,
+// Cargo.toml:50), with a strict parser and a compact writer whose number
+// text is serde_json's (shortest round-trip digits, `1.0` for integral
+// floats).
 #pragma once
 
 #include <cctype>
+#include <charconv>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
-#include <map>
 #include <memory>
 #include <stdexcept>
 #include <string>
+#include <utility>
 #include <vector>
 
 namespace decisive {
+
+// Object members in insertion order (serde_json's Map under preserve_order).
+// Lookup is a linear scan: requests and responses hold a handful of keys.
+// Assigning to an existing key keeps its position; two maps are equal when
+// they hold the same keys with equal values, in any order.
+template <class V>
+class OrderedMap {
+public:
+    using value_type = std::pair<std::string, V>;
+    using iterator = typename std::vector<value_type>::iterator;
+    using const_iterator = typename std::vector<value_type>::const_iterator;
+
+    iterator begin() { return items_.begin(); }
+    iterator end() { return items_.end(); }
+    const_iterator begin() const { return items_.begin(); }
+    const_iterator end() const { return items_.end(); }
+    size_t size() const { return items_.size(); }
+    bool empty() const { return items_.empty(); }
+
+    iterator find(const std::string &key) {
+        for (auto it = items_.begin(); it != items_.end(); ++it)
+            if (it->first == key) return it;
+        return items_.end();
+    }
+    const_iterator find(const std::string &key) const {
+        for (auto it = items_.begin(); it != items_.end(); ++it)
+            if (it->first == key) return it;
+        return items_.end();
+    }
+    size_t count(const std::string &key) const { return find(key) == end() ? 0 : 1; }
+    V &operator[](const std::string &key) {
+        auto it = find(key);
+        if (it != end()) return it->second;
+        items_.emplace_back(key, V());
+        return items_.back().second;
+    }
+    bool operator==(const OrderedMap &o) const {
+        if (size() != o.size()) return false;
+        for (const auto &kv : items_) {
+            auto it = o.find(kv.first);
+            if (it == o.end() || !(it->second == kv.second)) return false;
+        }
+        return true;
+    }
+
+private:
+    std::vector<value_type> items_;
+};
 
 class Json {
 public:
     enum class Kind { Null, Bool, Number, String, Array, Object };
     using Array = std::vector<Json>;
-    using Object = std::map<std::string, Json>;
+    using Object = OrderedMap<Json>;
 
     Json() = default;
     Json(std::nullptr_t) {}
     Json(bool b) : kind_(Kind::Bool), b_(b) {}
-    Json(int v) : kind_(Kind::Number), n_(v) {}
-    Json(int64_t v) : kind_(Kind::Number), n_((double)v) {}
-    Json(uint64_t v) : kind_(Kind::Number), n_((double)v) {}
+    Json(int v) : kind_(Kind::Number), integer_(true), n_(v) {}
+    Json(int64_t v) : kind_(Kind::Number), integer_(true), n_((double)v) {}
+    Json(uint64_t v) : kind_(Kind::Number), integer_(true), n_((double)v) {}
     Json(double v) : kind_(Kind::Number), n_(v) {}
     Json(const char *s) : kind_(Kind::String), s_(s) {}
     Json(std::string s) : kind_(Kind::String), s_(std::move(s)) {}
@@ -42,6 +95,8 @@ public:
     bool is_null() const { return kind_ == Kind::Null; }
     bool is_bool() const { return kind_ == Kind::Bool; }
     bool is_number() const { return kind_ == Kind::Number; }
+    // a number written or built as an integer (serde_json's is_u64/is_i64)
+    bool is_integer() const { return kind_ == Kind::Number && integer_; }
     bool is_string() const { return kind_ == Kind::String; }
     bool is_array() const { return kind_ == Kind::Array; }
     bool is_object() const { return kind_ == Kind::Object; }
@@ -97,6 +152,48 @@ public:
     }
     bool operator!=(const Json &o) const { return !(*this == o); }
 
+    // The shortest decimal digits that read back as x, and the exponent e
+    // of the first digit (x = d1.d2d3... * 10^e). x finite.
+    static void shortest_digits(double x, std::string &digits, int &exponent, bool &negative) {
+        char buf[64];
+        auto r = std::to_chars(buf, buf + sizeof buf, x, std::chars_format::scientific);
+        std::string t(buf, r.ptr);
+        negative = t[0] == '-';
+        if (negative) t.erase(0, 1);
+        size_t e = t.find('e');
+        exponent = std::stoi(t.substr(e + 1));
+        digits.clear();
+        for (size_t i = 0; i < e; i++)
+            if (t[i] != '.') digits += t[i];
+    }
+
+    // serde_json's float text (ryu's format: plain decimal with a ".0" for
+    // integral values while the decimal point stays within 21 digits, down
+    // to 1e-6, and d.ddde[-]x otherwise).
+    static std::string float_text(double x) {
+        std::string digits;
+        int e;
+        bool neg;
+        shortest_digits(x, digits, e, neg);
+        std::string out = neg ? "-" : "";
+        const int n = (int)digits.size();
+        const int kk = e + 1;  // digits before the decimal point
+        if (x == 0) {
+            out += "0.0";
+        } else if (n <= kk && kk <= 21) {
+            out += digits + std::string((size_t)(kk - n), '0') + ".0";
+        } else if (0 < kk && kk <= 21) {
+            out += digits.substr(0, (size_t)kk) + "." + digits.substr((size_t)kk);
+        } else if (-6 < kk && kk <= 0) {
+            out += "0." + std::string((size_t)(-kk), '0') + digits;
+        } else {
+            out += digits.substr(0, 1);
+            if (n > 1) out += "." + digits.substr(1);
+            out += "e" + std::to_string(e);
+        }
+        return out;
+    }
+
     std::string dump() const {
         std::string out;
         write(out);
@@ -115,6 +212,7 @@ public:
 private:
     Kind kind_ = Kind::Null;
     bool b_ = false;
+    bool integer_ = false;
     double n_ = 0.0;
     std::string s_;
     std::shared_ptr<Array> a_;
@@ -166,14 +264,13 @@ private:
             case Kind::Number: {
                 if (!std::isfinite(n_)) {
                     out += "null";  // serde_json writes non-finite floats as null
-                } else if (n_ == std::floor(n_) && std::fabs(n_) < 9.007199254740992e15) {
+                } else if (integer_) {
                     char buf[32];
-                    snprintf(buf, sizeof buf, "%lld", (long long)n_);
+                    if (n_ < 0) snprintf(buf, sizeof buf, "%lld", (long long)n_);
+                    else snprintf(buf, sizeof buf, "%llu", (unsigned long long)n_);
                     out += buf;
                 } else {
-                    char buf[40];
-                    snprintf(buf, sizeof buf, "%.17g", n_);
-                    out += buf;
+                    out += float_text(n_);
                 }
                 break;
             }
@@ -311,7 +408,12 @@ private:
             if (at >= t.size() || !isdigit((unsigned char)t[at])) throw std::runtime_error("invalid JSON number");
             while (at < t.size() && isdigit((unsigned char)t[at])) at++;
         }
-        return Json(std::stod(t.substr(start, at - start)));
+        std::string text = t.substr(start, at - start);
+        Json v(std::stod(text));
+        // serde_json keeps integer literals within u64/i64 as integers
+        bool plain = text.find_first_of(".eE") == std::string::npos;
+        if (plain && v.n_ >= -9.223372036854775808e18 && v.n_ < 1.8446744073709551616e19) v.integer_ = true;
+        return v;
     }
 
     static Json parse_value(const std::string &t, size_t &at, int depth) {

@@ -7,19 +7,27 @@
 //   Parameters = PplxParameters (maxSequenceTokens, default 1024, 0 rejected)
 //   CacheState = EmbeddingCache (packed Q4 g64/f32 embedding rows by token id)
 //   capabilities = {model "pplx-flash", backend "rocm", caches ["embedding"], tuning "auto"}
-// A request's `state` carries the token ids of the text (tokenization, the
-// reference's input.rs, is outside this path). Like the reference, input is
-// never truncated: a sequence longer than maxSequenceTokens is split into
-// chunks, each run as its own sequence (input.rs:227-282 splits requests
-// rather than truncating). The response holds one mean-pooled embedding per
-// chunk.
+// A request's `state` carries tokens, already encoded (tokenization, the
+// reference's input.rs plan, is outside this path), in one of two forms:
+//  - an array of token ids: the embedding response. Like the reference, input
+//    is never truncated: a sequence longer than maxSequenceTokens is split
+//    into chunks, each run as its own sequence (input.rs:227-282 splits
+//    requests rather than truncating); one mean-pooled embedding per chunk.
+//  - {"chunks": [{"ids", "markers", "keys", "counts"}, ...]}: the encoded
+//    chunks as the reference's inspect() lists them (mod.rs:186-191,
+//    input.rs:7-13 Encoded). Each chunk runs the encoder, the readout of the
+//    hidden rows at its markers (mod.rs:149-185) and the answer step
+//    (input.rs:284-326) for each key's question, as native.rs:193-274 does;
+//    the response is {"answers", "usage"} as there.
 #pragma once
 
+#include <cmath>
 #include <cstring>
 #include <string>
 #include <utility>
 #include <vector>
 
+#include "answer.hpp"
 #include "decisive_rocm.h"
 #include "embedding_cache.hpp"
 #include "inference.hpp"
@@ -69,6 +77,7 @@ public:
             out_dev_ = std::exchange(o.out_dev_, nullptr);
             row_bytes_ = o.row_bytes_;
             config_ = o.config_;
+            temperature_ = o.temperature_;
             tuning_ = std::move(o.tuning_);
         }
         return *this;
@@ -83,6 +92,15 @@ public:
     const dz_encoder_config &config() const { return config_; }
     const Json &tuning() const { return tuning_; }
 
+    // The decision temperature of the answer softmax (decision_config.json's
+    // "temperature" in the reference, input.rs:127-131: finite and positive).
+    Status set_temperature(float t) {
+        if (!(std::isfinite(t) && t > 0.0f)) return Error::engine("invalid temperature");
+        temperature_ = t;
+        return {};
+    }
+    float temperature() const { return temperature_; }
+
     Capabilities capabilities() const { return Capabilities{"pplx-flash", "rocm", {"embedding"}, "auto"}; }
     Result<EmbeddingCache> create_cache(const CacheOptions &options) const {
         return EmbeddingCache(options.max_bytes);
@@ -93,6 +111,7 @@ public:
                          const Cancellation &cancellation) {
         Status s = parameters.validate();
         if (!s) return s.error();
+        if (request.state.is_object()) return predict_answers(request, parameters, cache, cancellation);
         auto ids = token_ids(request);
         if (!ids) return ids.error();
         const std::vector<uint32_t> &all = ids.value();
@@ -118,6 +137,16 @@ public:
         return out;
     }
 
+    // Logits [markers x DZ_READOUT_CODES] of one sequence given as packed rows.
+    Result<std::vector<float>> readout(const std::vector<uint8_t> &rows, size_t tokens,
+                                       const std::vector<int32_t> &markers) {
+        std::vector<float> logits(markers.size() * DZ_READOUT_CODES);
+        int32_t rc = dz_encoder_readout_rows(ctx_, encoder_, rows.data(), tokens, markers.data(), markers.size(),
+                                             logits.data());
+        if (rc != DZ_OK) return status_error(ctx_, rc);
+        return logits;
+    }
+
     // The packed rows of `ids` from the encoder's embedding table.
     Result<std::vector<uint8_t>> read_rows(const std::vector<uint32_t> &ids) const {
         std::vector<int32_t> as_i32(ids.begin(), ids.end());
@@ -139,6 +168,89 @@ public:
 
 private:
     Rocm() = default;
+
+    struct Encoded {
+        std::vector<uint32_t> ids;
+        std::vector<int32_t> markers;
+        std::vector<std::string> keys;
+        std::vector<size_t> counts;
+    };
+
+    static bool whole(const Json &v, double limit) {
+        return v.is_number() && v.as_number() >= 0 && v.as_number() < limit && v.as_number() == (double)(uint64_t)v.as_number();
+    }
+
+    Result<Encoded> encoded_chunk(const Json &c, const Json &questions, size_t max_tokens) const {
+        if (!c.is_object() || !c["ids"].is_array() || !c["markers"].is_array() || !c["keys"].is_array() ||
+            !c["counts"].is_array())
+            return Error("INVALID_REQUEST", "each chunk needs ids, markers, keys and counts arrays");
+        Encoded e;
+        for (const Json &v : c["ids"].as_array()) {
+            if (!whole(v, (double)config_.vocab)) return Error("INVALID_REQUEST", "token id outside the vocabulary");
+            e.ids.push_back((uint32_t)v.as_number());
+        }
+        if (e.ids.empty()) return Error("INVALID_REQUEST", "a chunk needs at least one token");
+        if (e.ids.size() > max_tokens) return Error::engine("chunk exceeds token limit");
+        for (const Json &v : c["markers"].as_array()) {
+            if (!whole(v, (double)e.ids.size())) return Error("INVALID_REQUEST", "readout marker outside the chunk");
+            e.markers.push_back((int32_t)v.as_number());
+        }
+        for (const Json &v : c["keys"].as_array()) {
+            if (!v.is_string() || !questions[v.as_string()].is_object())
+                return Error("INVALID_REQUEST", "chunk key without a question");
+            e.keys.push_back(v.as_string());
+        }
+        for (const Json &v : c["counts"].as_array()) {
+            if (!whole(v, (double)DZ_READOUT_CODES + 1) || v.as_number() < 1)
+                return Error("INVALID_REQUEST", "answer count outside 1..255");
+            e.counts.push_back((size_t)v.as_number());
+        }
+        if (e.markers.size() != e.keys.size() || e.keys.size() != e.counts.size() || e.markers.empty() ||
+            e.markers.size() > DZ_READOUT_MAX_MARKERS)
+            return Error("INVALID_REQUEST", "markers, keys and counts must pair up (1..256 per chunk)");
+        return e;
+    }
+
+    // native.rs:193-274 over encoded chunks.
+    Result<Json> predict_answers(const Request &request, const PplxParameters &parameters, EmbeddingCache &cache,
+                                 const Cancellation &cancellation) {
+        const Json &chunks = request.state["chunks"];
+        if (!chunks.is_array() || chunks.size() == 0 || request.state.size() != 1)
+            return Error("INVALID_REQUEST", "state must hold a nonempty chunks array");
+        std::vector<Encoded> plan;
+        for (const Json &c : chunks.as_array()) {
+            auto e = encoded_chunk(c, request.questions, parameters.max_sequence_tokens);
+            if (!e) return e.error();
+            plan.push_back(e.take());
+        }
+        Json answers = Json::object();
+        uint64_t tokens = 0;
+        for (const Encoded &e : plan) {
+            Status s = cancellation.check();
+            if (!s) return s.error();
+            auto rows = cache.load(e.ids, [this](const std::vector<uint32_t> &miss) { return read_rows(miss); },
+                                   row_bytes_, cancellation);
+            if (!rows) return rows.error();
+            auto logits = readout(rows.value(), e.ids.size(), e.markers);
+            if (!logits) return logits.error();
+            for (size_t i = 0; i < e.keys.size(); i++) {
+                const float *row = logits.value().data() + i * DZ_READOUT_CODES;
+                std::vector<float> values(row, row + e.counts[i]);
+                auto a = answer(request.questions[e.keys[i]], values, temperature_);
+                if (!a) return a.error();
+                answers[e.keys[i]] = a.take();
+            }
+            tokens += e.ids.size();
+        }
+        Json usage = Json::object();
+        usage["input_tokens"] = Json(tokens);
+        usage["output_tokens"] = Json(0);
+        usage["sequences"] = Json((uint64_t)plan.size());
+        Json out = Json::object();
+        out["answers"] = std::move(answers);
+        out["usage"] = std::move(usage);
+        return out;
+    }
 
     Result<std::vector<uint32_t>> token_ids(const Request &request) const {
         if (!request.state.is_array() || request.state.size() == 0)
@@ -171,6 +283,7 @@ private:
     size_t row_bytes_ = 0;
     dz_encoder_config config_{};
     Json tuning_;
+    float temperature_ = 1.0f;
 };
 
 }  // namespace decisive

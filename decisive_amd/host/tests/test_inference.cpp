@@ -7,6 +7,11 @@
 #include <string>
 #include <vector>
 
+#include <fstream>
+#include <sstream>
+#include <unistd.h>
+
+#include "../answer.hpp"
 #include "../embedding_cache.hpp"
 #include "../inference.hpp"
 #include "harness.hpp"
@@ -254,7 +259,17 @@ TEST(embedding_cache_checks_cancellation_before_each_read) {
 
 TEST(json_round_trips_and_rejects_malformed_text) {
     Json j = Json::parse(R"({"b":[1,2.5,-3e2,true,null,"x\n\u00e9"],"a":{}})");
-    CHECK_EQ(j.dump(), std::string("{\"a\":{},\"b\":[1,2.5,-300,true,null,\"x\\n\xc3\xa9\"]}"));
+    // members keep their order; -3e2 is a float, written as serde_json does
+    CHECK_EQ(j.dump(), std::string("{\"b\":[1,2.5,-300.0,true,null,\"x\\n\xc3\xa9\"],\"a\":{}}"));
+    CHECK(j["b"][0].is_integer() && !j["b"][2].is_integer());
+    CHECK_EQ(Json(0.1).dump(), std::string("0.1"));
+    CHECK_EQ(Json(1e16).dump(), std::string("10000000000000000.0"));
+    CHECK_EQ(Json(1e22).dump(), std::string("1e22"));
+    CHECK_EQ(Json(1e-7).dump(), std::string("1e-7"));
+    CHECK_EQ(Json(0.000123).dump(), std::string("0.000123"));
+    CHECK_EQ(Json(-0.0).dump(), std::string("-0.0"));
+    // objects compare as maps: order does not matter
+    CHECK(Json::parse(R"({"x":1,"y":2})") == Json::parse(R"({"y":2,"x":1})"));
     CHECK(Json::parse(j.dump()) == j);
     for (const char *bad : {"{", "[1,]", "01", "\"\\x\"", "{\"a\" 1}", "tru", "1 2", "\"\\ud800\""}) {
         bool threw = false;
@@ -268,6 +283,106 @@ TEST(json_round_trips_and_rejects_malformed_text) {
     Json copy = j;
     copy["c"] = 1;  // copy on write leaves the original alone
     CHECK(j["c"].is_null());
+}
+
+// ---- answer step (input.rs:21-112, :284-326) ------------------------------------
+
+// tests/golden/<name>, found from this program's path (decisive_amd/host/build/).
+static Json golden(const char *name) {
+    char exe[4096];
+    ssize_t n = readlink("/proc/self/exe", exe, sizeof exe - 1);
+    std::string path = n > 0 ? std::string(exe, (size_t)n) : std::string();
+    path = path.substr(0, path.rfind('/')) + "/../../../tests/golden/" + name;
+    std::ifstream f(path);
+    std::stringstream text;
+    text << f.rdbuf();
+    return Json::parse(text.str());
+}
+
+// pplx_flash/mod.rs compare(): numbers within tol, objects by key with equal
+// sizes, everything else exactly.
+static bool close(const Json &a, const Json &b, double tol) {
+    if (a.is_number() && b.is_number()) return std::fabs(a.as_number() - b.as_number()) <= tol;
+    if (a.is_object() && b.is_object()) {
+        if (a.size() != b.size()) return false;
+        for (const auto &kv : a.as_object())
+            if (!close(kv.second, b[kv.first], tol)) return false;
+        return true;
+    }
+    return a == b;
+}
+
+static std::vector<float> floats(const Json &a) {
+    std::vector<float> v;
+    for (const Json &x : a.as_array()) v.push_back((float)x.as_number());
+    return v;
+}
+
+TEST(answers_match_the_reference_fixture_responses) {
+    Json g = golden("pplx_answers.json");
+    const float temperature = (float)g["temperature_fit"].as_number();
+    const double tol = g["tolerance"].as_number();
+    int checked = 0;
+    for (const Json &c : g["cases"].as_array()) {
+        for (const auto &kv : c["logits"].as_object()) {
+            const Json &q = c["questions"][kv.first];
+            auto a = answer(q, floats(kv.second), temperature);
+            CHECK(a.ok());
+            if (!a) continue;
+            const Json &want = c["answers"][kv.first];
+            CHECK(close(a.value(), want, tol));
+            // the probabilities keep the question's order (preserve_order)
+            if (want["probabilities"].is_object()) {
+                std::vector<std::string> got_keys, want_keys;
+                for (const auto &p : a.value()["probabilities"].as_object()) got_keys.push_back(p.first);
+                for (const auto &p : want["probabilities"].as_object()) want_keys.push_back(p.first);
+                CHECK(got_keys == want_keys);
+            }
+            // a wrong temperature is caught by the same comparison
+            auto off = answer(q, floats(kv.second), 1.0f);
+            CHECK(off.ok() && !close(off.value(), want, tol));
+            checked++;
+        }
+    }
+    CHECK_EQ(checked, 4);
+}
+
+TEST(answer_rejects_bad_questions_and_logit_counts) {
+    Json choice = Json::parse(R"({"type":"choice","criteria":{"a":null,"b":null}})");
+    CHECK(answer(choice, {1.f}, 1.f).error() == Error("INFERENCE_FAILED", "logit count mismatch"));
+    CHECK(answer(Json::parse(R"({"type":"rank"})"), {1.f}, 1.f).error().message ==
+          "question type must be choice, noul or score");
+    CHECK(answer(Json::parse(R"({"type":"choice","criteria":[1]})"), {1.f}, 1.f).error().message ==
+          "choice criteria must be an object");
+    CHECK(answer(Json::parse(R"({"type":"noul","criteria":[]})"), {1.f, 2.f}, 1.f).error().message ==
+          "noul criteria must be an object");
+    // one option: confidence 1; ties pick the first maximum
+    auto one = answer(Json::parse(R"({"type":"choice","criteria":{"only":null}})"), {3.f}, 1.f);
+    CHECK(one.ok() && one.value()["confidence"].as_number() == 1.0 && one.value()["choice"].as_string() == "only");
+    auto tie = answer(choice, {2.f, 2.f}, 1.f);
+    CHECK(tie.ok() && tie.value()["choice"].as_string() == "a" && tie.value()["confidence"].as_number() == 0.0);
+    // score: closed form on a two-level scale
+    auto score = answer(Json::parse(R"({"type":"score","criteria":["low","high"]})"), {0.f, 0.f}, 1.f);
+    CHECK(score.ok() && score.value()["score"].as_number() == 0.5 && score.value()["confidence"].as_number() == 0.0);
+}
+
+TEST(json_text_and_options_match_the_reference_known_answers) {
+    Json g = golden("pplx_answers.json");
+    for (const Json &c : g["json_text"].as_array()) CHECK_EQ(json_text(c["value"]), c["text"].as_string());
+    for (const Json &c : g["options"].as_array()) {
+        auto o = options(c["question"]);
+        if (!c["error"].is_null()) {
+            CHECK(!o.ok() && o.error().message == c["error"].as_string());
+            continue;
+        }
+        CHECK(o.ok());
+        if (!o) continue;
+        std::vector<std::string> keys;
+        for (const Json &k : c["keys"].as_array()) keys.push_back(k.as_string());
+        CHECK(o.value().keys == keys);
+        CHECK(Json(Json::Array(o.value().legend)) == c["legend"]);
+    }
+    CHECK_EQ(json_text(Json::parse("[1, 2.0, 0.5, 123456.75, 1e-5]")), std::string("[1, 2.0, 0.5, 123456.75, 1e-05]"));
 }
 
 int main(int argc, char **argv) { return harness::run_all(argc, argv); }

@@ -85,7 +85,94 @@ Model<Rocm> make_model() {
     return Model<Rocm>(made.take());
 }
 
+Json ids_json(const std::vector<uint32_t> &ids) {
+    Json a = Json::array();
+    for (uint32_t id : ids) a.push_back(Json((uint64_t)id));
+    return a;
+}
+
+// {"chunks": [...]} state over encoded chunks with the three question kinds.
+Request answer_request(const std::vector<uint32_t> &ids, std::vector<int> markers) {
+    Request r;
+    Json chunk = Json::object();
+    chunk["ids"] = ids_json(ids);
+    Json m = Json::array();
+    for (int v : markers) m.push_back(Json(v));
+    chunk["markers"] = m;
+    chunk["keys"] = Json::parse(R"(["team","refund","tone"])");
+    chunk["counts"] = Json::parse("[3,2,3]");
+    r.state = Json::object();
+    r.state["chunks"] = Json(Json::Array{chunk});
+    r.questions = Json::parse(R"({
+        "team": {"type": "choice", "criteria": {"billing": "Charges", "support": null, "sales": "Buying"}},
+        "refund": {"type": "noul"},
+        "tone": {"type": "score", "criteria": ["calm", "concerned", "angry"]}})");
+    return r;
+}
+
 }  // namespace
+
+TEST(rocm_answers_are_the_answer_step_over_the_readout_logits) {
+    Model<Rocm> model = make_model();
+    CHECK(model.backend().set_temperature(1.5539092f).ok());
+    CHECK(!model.backend().set_temperature(0.0f).ok());
+    auto cache = model.create_cache(CacheOptions{});
+    CHECK(cache.ok());
+    std::vector<uint32_t> ids = ids_of(120, 5);
+    Request req = answer_request(ids, {40, 80, 119});
+    auto got = model.predict(req, nullptr, &cache.value(), Cancellation{});
+    CHECK(got.ok());
+    if (!got.ok()) {
+        fprintf(stderr, "%s\n", got.error().to_string().c_str());
+        return;
+    }
+    const Json &resp = got.value().response;
+    CHECK_EQ(resp["usage"]["input_tokens"], Json(120));
+    CHECK_EQ(resp["usage"]["sequences"], Json(1));
+    // the same logits through the C ABI, then the answer step on the host
+    Rocm &rocm = model.backend();
+    auto rows = rocm.read_rows(ids);
+    CHECK(rows.ok());
+    auto logits = rocm.readout(rows.value(), ids.size(), {40, 80, 119});
+    CHECK(logits.ok());
+    const char *keys[3] = {"team", "refund", "tone"};
+    const size_t counts[3] = {3, 2, 3};
+    for (int i = 0; i < 3; i++) {
+        const float *row = logits.value().data() + i * DZ_READOUT_CODES;
+        auto want = answer(req.questions[keys[i]], std::vector<float>(row, row + counts[i]), rocm.temperature());
+        CHECK(want.ok() && resp["answers"][keys[i]] == want.value());
+    }
+    CHECK_EQ(resp["answers"]["team"]["type"], Json("choice"));
+    CHECK(resp["answers"]["refund"]["noul"].is_number());
+    CHECK(resp["answers"]["tone"]["legend"]["2"] == Json("angry"));
+    // repeats come from the embedding cache and give the same answers
+    uint64_t misses = cache.value().state().misses();
+    auto again = model.predict(req, nullptr, &cache.value(), Cancellation{});
+    CHECK(again.ok() && again.value().response == resp);
+    CHECK_EQ(cache.value().state().misses(), misses);
+}
+
+TEST(rocm_answer_requests_are_validated) {
+    Model<Rocm> model = make_model();
+    std::vector<uint32_t> ids = ids_of(30, 9);
+    auto code_of = [&](const Request &r, const PplxParameters *p = nullptr) {
+        auto out = model.predict(r, p, nullptr, Cancellation{});
+        return out.ok() ? std::string("OK") : out.error().code;
+    };
+    CHECK_EQ(code_of(answer_request(ids, {1, 2, 29})), std::string("OK"));
+    CHECK_EQ(code_of(answer_request(ids, {1, 2, 30})), std::string("INVALID_REQUEST"));  // marker past the chunk
+    Request unpaired = answer_request(ids, {1, 2});
+    CHECK_EQ(code_of(unpaired), std::string("INVALID_REQUEST"));
+    Request unknown = answer_request(ids, {1, 2, 3});
+    unknown.questions = Json::parse(R"({"team": {"type": "choice", "criteria": {"a": null}}})");
+    CHECK_EQ(code_of(unknown), std::string("INVALID_REQUEST"));  // keys without questions
+    PplxParameters short_limit;
+    short_limit.max_sequence_tokens = 16;
+    CHECK_EQ(code_of(answer_request(ids, {1, 2, 3}), &short_limit), std::string("INPUT_TOO_LONG"));
+    Request bad_count = answer_request(ids, {1, 2, 3});
+    bad_count.questions["team"]["criteria"] = Json::parse(R"({"a": null, "b": null})");  // 2 options, 3 logits
+    CHECK_EQ(code_of(bad_count), std::string("INFERENCE_FAILED"));
+}
 
 TEST(rocm_capabilities_and_parameters) {
     Model<Rocm> model = make_model();

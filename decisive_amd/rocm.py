@@ -95,6 +95,10 @@ _SIGNATURES = {
     "dz_encoder_weight": (P, [P, I32, I32]),
     "dz_encoder_forward": (I32, [P, P, P, SZ, SZ, P]),
     "dz_encoder_forward_rows": (I32, [P, P, P, SZ, SZ, P]),
+    "dz_encoder_hidden_rows": (I32, [P, P, P, SZ, P]),
+    "dz_readout": (I32, [P, P, P, P, SZ, F, P]),
+    "dz_encoder_readout_params": (I32, [P, PP, PP]),
+    "dz_encoder_readout_rows": (I32, [P, P, P, SZ, P, SZ, P]),
     "dz_tune": (I32, [P, U32, ctypes.c_char_p, ctypes.c_char_p, SZ]),
     "dz_select_variant": (I32, [P, ctypes.c_char_p, ctypes.c_char_p]),
 }
@@ -248,6 +252,10 @@ class Context:
     def project(self, w: Weight, x, m: int, y):
         self._check(load().dz_project(self.handle, w.handle, _addr(x), m, _addr(y)))
 
+    def readout(self, w: Weight, norm, hidden, rows: int, eps: float, logits):
+        self._check(load().dz_readout(self.handle, w.handle, _addr(norm), _addr(hidden), rows, eps,
+                                      _addr(logits)))
+
     def act_quantize_records(self, x, m: int, k: int, records):
         self._check(load().dz_act_quantize_records(self.handle, _addr(x), m, k, _addr(records)))
 
@@ -314,7 +322,8 @@ class Context:
 class Encoder:
     """dz_encoder: the configuration-3 encoder with device-resident weights."""
 
-    QKV, O, UP, DOWN, EMBED = 0, 1, 2, 3, 4
+    QKV, O, UP, DOWN, EMBED, READOUT = 0, 1, 2, 3, 4, 5
+    READOUT_CODES = 255
 
     def __init__(self, ctx: Context, handle: int, cfg: EncoderConfig):
         self.ctx, self.handle, self.cfg = ctx, handle, cfg
@@ -344,6 +353,28 @@ class Encoder:
         rows_host = np.ascontiguousarray(rows_host, dtype=np.uint8)
         self.ctx._check(load().dz_encoder_forward_rows(self.ctx.handle, self.handle, rows_host.ctypes.data, batch,
                                                        seq, _addr(out)))
+
+    def hidden_rows(self, rows_host, seq: int, hidden):
+        import numpy as np
+        rows_host = np.ascontiguousarray(rows_host, dtype=np.uint8)
+        self.ctx._check(load().dz_encoder_hidden_rows(self.ctx.handle, self.handle, rows_host.ctypes.data, seq,
+                                                      _addr(hidden)))
+
+    def readout_params(self):
+        """(readout Weight, device address of its norm weights)."""
+        w, norm = ctypes.c_void_p(), ctypes.c_void_p()
+        self.ctx._check(load().dz_encoder_readout_params(self.handle, ctypes.byref(w), ctypes.byref(norm)))
+        return Weight(self.ctx, w.value, owned=False), norm.value
+
+    def readout_rows(self, rows_host, seq: int, markers):
+        """Logits f32 [len(markers) x 255] of the hidden rows at markers."""
+        import numpy as np
+        rows_host = np.ascontiguousarray(rows_host, dtype=np.uint8)
+        markers = np.ascontiguousarray(markers, dtype=np.int32)
+        out = np.empty((markers.size, self.READOUT_CODES), np.float32)
+        self.ctx._check(load().dz_encoder_readout_rows(self.ctx.handle, self.handle, rows_host.ctypes.data, seq,
+                                                       markers.ctypes.data, markers.size, out.ctypes.data))
+        return out
 
     def close(self):
         if self.handle:

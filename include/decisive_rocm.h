@@ -249,7 +249,8 @@ int32_t dz_encoder_read_rows(dz_ctx *ctx, const dz_encoder *enc, const int32_t *
                              size_t count, void *out_host);
 /* The encoder's weights for inspection: which = 0 qkv [3h x h], 1 output
  * [h x h], 2 ffn up [f x h], 3 ffn down [h x f] of `layer`; 4 the embedding
- * table [vocab x h]. Owned by the encoder; NULL when out of range. */
+ * table [vocab x h]; 5 the readout [255 x h]. Owned by the encoder; NULL when
+ * out of range. */
 const dz_weight *dz_encoder_weight(const dz_encoder *enc, int32_t layer, int32_t which);
 /* Forward over batch x seq token ids (ids_dev int32) -> mean-pooled
  * embeddings out_dev f32 [batch x hidden]. */
@@ -260,6 +261,39 @@ int32_t dz_encoder_forward(dz_ctx *ctx, dz_encoder *enc, const int32_t *ids_dev,
  * EmbeddingCache hands them over (browser/pplx.rs:76-137). */
 int32_t dz_encoder_forward_rows(dz_ctx *ctx, dz_encoder *enc, const void *rows_host,
                                 size_t batch, size_t seq, float *out_dev);
+
+/* The per-token output of the encoder: the last layer's hidden states of one
+ * sequence of packed rows (as dz_encoder_forward_rows takes them), f32
+ * [seq x hidden] in hidden_dev (exact f16 -> f32). */
+int32_t dz_encoder_hidden_rows(dz_ctx *ctx, dz_encoder *enc, const void *rows_host, size_t seq,
+                               float *hidden_dev);
+
+/* ---- decision readout (pplx_flash/mod.rs:149-185 logits) ------------------------ */
+
+#define DZ_READOUT_CODES 255       /* answer codes per readout row (input.rs:137-140) */
+#define DZ_READOUT_MAX_MARKERS 256 /* readout rows per dz_encoder_readout_rows call */
+#define DZ_READOUT_EPS 1e-6f       /* RMSNorm epsilon of the readout (mod.rs:155) */
+
+/* pplx_flash/mod.rs:149-185 logits with a packed readout: for each of `rows`
+ * hidden rows (hidden_dev f32 [rows x cols(w)]) the zero-centred RMSNorm of
+ * pplx_flash/cpu.rs:310-333, y = (x * s) * (1 + norm), s = 1/sqrt(sum x^2 /
+ * cols + eps), with the squares summed in row order as the reference's sum
+ * is (bit-exact), then dz_project (packed.rs:75-119) into logits_dev f32
+ * [rows x rows(w)]. w is group-64 (Q4 or Q8 wire layout), cols(w) <= 16384.
+ * Synchronous. A non-finite normalised activation gives DZ_INFERENCE_FAILED
+ * "nonfinite readout activation", a non-finite logit "non-finite packed
+ * logits", as the reference's ensure!s. */
+int32_t dz_readout(dz_ctx *ctx, const dz_weight *w, const float *norm_dev, const float *hidden_dev,
+                   size_t rows, float eps, float *logits_dev);
+/* The encoder's readout: weight [DZ_READOUT_CODES x hidden] (Q4 g64) and its
+ * zero-centred norm weights (device f32 [hidden]); owned by the encoder. */
+int32_t dz_encoder_readout_params(const dz_encoder *enc, const dz_weight **w, const float **norm_dev);
+/* pplx_flash/native.rs:193-274 for one chunk: the encoder over one sequence
+ * of packed rows, then dz_readout of the hidden rows at markers_host (count
+ * positions < seq, count <= DZ_READOUT_MAX_MARKERS) with the encoder's
+ * readout. logits_host f32 [count x DZ_READOUT_CODES]. Synchronous. */
+int32_t dz_encoder_readout_rows(dz_ctx *ctx, dz_encoder *enc, const void *rows_host, size_t seq,
+                                const int32_t *markers_host, size_t count, float *logits_host);
 
 /* ---- kernel tuner (webgpu/checkpoint.rs:95-294, 428-652) ------------------------ */
 

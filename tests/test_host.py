@@ -11,9 +11,9 @@ BUILD = HOST / "build"
 
 
 def _program(name: str) -> Path:
+    """The test program, rebuilt by make when a source or header changed."""
     exe = BUILD / name
-    if not exe.exists():
-        subprocess.run(["make", "-s", "-C", str(HOST), f"build/{name}"], check=True)
+    subprocess.run(["make", "-s", "-C", str(HOST), str(exe)], check=True)
     return exe
 
 

@@ -393,3 +393,19 @@ def test_q4_rows_rounding_and_zero_rows(oracle):
     assert words[2] == 0x88888888 and words[3] == 0x88888888
     with pytest.raises(oracle.OracleError):
         oracle.q4_quantize_rows(np.zeros(12, np.uint16), 1, 12)
+
+
+def test_readout_rms_is_the_sequential_sum(oracle):
+    """The oracle's RMSNorm adds the squares in row order (the reference's
+    iterator sum): on a row where order matters, a pairwise sum differs."""
+    x = np.zeros((1, 4096), np.float32)
+    x[0, 0] = 4096.0
+    x[0, 1:] = 0.5
+    got = oracle.rmsnorm(x, np.zeros(4096, np.float32), 1e-6)
+    seq = np.float32(0)
+    for v in x[0]:
+        seq = np.float32(seq + np.float32(v * v))
+    scale = np.float32(1) / np.sqrt(np.float32(seq / np.float32(4096) + np.float32(1e-6)), dtype=np.float32)
+    assert np.array_equal(got[0].view(np.uint32), (x[0] * scale).astype(np.float32).view(np.uint32))
+    pair = np.float32(np.sum(x[0].astype(np.float32) ** 2, dtype=np.float32))
+    assert pair != seq
