@@ -27,6 +27,8 @@ const Weight &weight_of(const dz_weight *h);
 int32_t weight_quantize(dz_ctx *ctx, const void *values, int dtype, size_t rows, size_t cols, int bits,
                         int group, dz_weight **out);
 void weight_free(dz_weight *h);
+int32_t weight_upload(dz_ctx *ctx, const void *packed, size_t bytes, int32_t layout, size_t rows, size_t cols,
+                      dz_weight **out);
 int32_t ctx_readout_rows(dz_ctx *ctx, const Weight &w, const float *norm, const void *hidden, int dtype,
                          const int32_t *select, size_t rows, float eps, float *logits);
 
@@ -333,6 +335,27 @@ int32_t encoder_readout_params(const dz_encoder *e, const dz_weight **w, const f
     if (!e) return DZ_INVALID_REQUEST;
     if (w) *w = e->readout;
     if (norm) *norm = e->readout_norm;
+    return DZ_OK;
+}
+
+int32_t encoder_set_readout(dz_ctx *ctx, dz_encoder *e, const void *packed, size_t bytes, int32_t layout,
+                            const float *norm_host) {
+    if (!e || !packed || !norm_host) return ctx_fail(ctx, DZ_INVALID_REQUEST, "null pointer");
+    if (layout != DZ_Q4_G64_F32 && layout != DZ_Q8_G64_F32)
+        return ctx_fail(ctx, DZ_INVALID_PARAMETERS, "the readout is a group-64 packed matrix");
+    dz_weight *w = nullptr;
+    int32_t rc = weight_upload(ctx, packed, bytes, layout, kReadoutCodes, (size_t)e->cfg.hidden, &w);
+    if (rc) return rc;
+    hipStream_t s = ctx_stream(ctx);
+    hipError_t err = hipMemcpyAsync(e->readout_norm, norm_host, (size_t)e->cfg.hidden * sizeof(float),
+                                    hipMemcpyHostToDevice, s);
+    if (err == hipSuccess) err = hipStreamSynchronize(s);
+    if (err != hipSuccess) {
+        weight_free(w);
+        return ctx_hip_fail(ctx, err, "readout norm upload");
+    }
+    weight_free(e->readout);
+    e->readout = w;
     return DZ_OK;
 }
 

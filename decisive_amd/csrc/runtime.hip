@@ -45,6 +45,8 @@ int32_t encoder_read_rows(dz_ctx *ctx, const dz_encoder *enc, const int32_t *ids
                           void *out);
 int32_t encoder_hidden_rows(dz_ctx *ctx, dz_encoder *e, const void *rows_host, size_t seq, float *hidden);
 int32_t encoder_readout_params(const dz_encoder *e, const dz_weight **w, const float **norm);
+int32_t encoder_set_readout(dz_ctx *ctx, dz_encoder *e, const void *packed, size_t bytes, int32_t layout,
+                            const float *norm_host);
 int32_t encoder_readout(dz_ctx *ctx, dz_encoder *e, const void *rows_host, size_t seq, const int32_t *markers,
                         size_t count, float *logits_host);
 int32_t encoder_forward(dz_ctx *ctx, dz_encoder *enc, const int32_t *ids_dev, const void *rows_host,
@@ -750,6 +752,12 @@ int32_t dz_encoder_readout_params(const dz_encoder *enc, const dz_weight **w, co
     return dz::encoder_readout_params(enc, w, norm);
 }
 
+int32_t dz_encoder_set_readout(dz_ctx *ctx, dz_encoder *enc, const void *packed, size_t bytes, int32_t layout,
+                               const float *norm_host) {
+    DZ_BEGIN(ctx);
+    return dz::encoder_set_readout(ctx, enc, packed, bytes, layout, norm_host);
+}
+
 int32_t dz_encoder_readout_rows(dz_ctx *ctx, dz_encoder *enc, const void *rows, size_t seq,
                                 const int32_t *markers, size_t count, float *logits) {
     DZ_BEGIN(ctx);
@@ -794,6 +802,10 @@ int32_t weight_quantize(dz_ctx *ctx, const void *values, int dtype, size_t rows,
     return dz_weight_quantize(ctx, values, dtype, rows, cols, bits, group, out);
 }
 void weight_free(dz_weight *h) { free_weight(h); }
+int32_t weight_upload(dz_ctx *ctx, const void *packed, size_t bytes, int32_t layout, size_t rows, size_t cols,
+                      dz_weight **out) {
+    return dz_weight_upload(ctx, packed, bytes, layout, rows, cols, out);
+}
 int32_t ctx_readout_rows(dz_ctx *ctx, const Weight &w, const float *norm, const void *hidden, int dtype,
                          const int32_t *select, size_t rows, float eps, float *logits) {
     return readout_rows(ctx, w, norm, hidden, dtype, select, rows, eps, logits);

@@ -23,6 +23,7 @@
 
 #include <cmath>
 #include <cstring>
+#include <memory>
 #include <string>
 #include <utility>
 #include <vector>
@@ -31,6 +32,7 @@
 #include "decisive_rocm.h"
 #include "embedding_cache.hpp"
 #include "inference.hpp"
+#include "packed_checkpoint.hpp"
 
 namespace decisive {
 
@@ -68,6 +70,44 @@ public:
         return r;
     }
 
+    // A backend whose embedding rows, decision readout, final norm and answer
+    // temperature come from a packed checkpoint directory (validated with
+    // every file digest, as prepare_hf_q4.py:71-114 does; browser/pplx.rs:
+    // 140-330 loads the same parts). The embedding cache reads its misses from
+    // the checkpoint's embedding file (browser/pplx.rs:76-137). The encoder
+    // layers stay random-init from `seed`: the checkpoint's decoder layers
+    // belong to a different architecture. config.hidden must be the
+    // checkpoint's; config.vocab is taken from it. Embedding rows are read in
+    // the Q4 format (q4-e4).
+    static Result<Rocm> create_from_checkpoint(int device, const std::string &dir, dz_encoder_config config,
+                                               uint64_t seed, const TuningOptions &tuning = TuningOptions{},
+                                               const PackedModel &model = PackedModel{}) {
+        auto ck = PackedCheckpoint::open(dir, model);
+        if (!ck) return ck.error();
+        if (ck.value().format().bits != 4)
+            return Error("UNSUPPORTED_FORMAT", "the Rocm encoder reads q4-e4 embedding rows");
+        if ((size_t)config.hidden != model.hidden)
+            return Error("INVALID_PARAMETERS", "encoder hidden size differs from the checkpoint's");
+        config.vocab = (int32_t)ck.value().vocab();
+        auto made = create(device, config, seed, tuning);
+        if (!made) return made.error();
+        Rocm r = made.take();
+        auto readout = ck.value().readout_bytes();
+        if (!readout) return readout.error();
+        auto norm = ck.value().norm();
+        if (!norm) return norm.error();
+        int32_t rc = dz_encoder_set_readout(r.ctx_, r.encoder_, readout.value().data(), readout.value().size(),
+                                            ck.value().layout(), norm.value().data());
+        if (rc != DZ_OK) return status_error(r.ctx_, rc);
+        auto t = ck.value().temperature();
+        if (t) {
+            Status s = r.set_temperature(t.value());
+            if (!s) return s.error();
+        }
+        r.checkpoint_ = std::make_shared<PackedCheckpoint>(ck.take());
+        return r;
+    }
+
     Rocm(Rocm &&o) noexcept { *this = std::move(o); }
     Rocm &operator=(Rocm &&o) noexcept {
         if (this != &o) {
@@ -78,6 +118,7 @@ public:
             row_bytes_ = o.row_bytes_;
             config_ = o.config_;
             temperature_ = o.temperature_;
+            checkpoint_ = std::move(o.checkpoint_);
             tuning_ = std::move(o.tuning_);
         }
         return *this;
@@ -147,8 +188,10 @@ public:
         return logits;
     }
 
-    // The packed rows of `ids` from the encoder's embedding table.
+    // The packed rows of `ids`: from the checkpoint's embedding file when the
+    // backend was opened on one, else from the encoder's own table.
     Result<std::vector<uint8_t>> read_rows(const std::vector<uint32_t> &ids) const {
+        if (checkpoint_) return checkpoint_->embedding_rows(ids);
         std::vector<int32_t> as_i32(ids.begin(), ids.end());
         std::vector<uint8_t> out(ids.size() * row_bytes_);
         int32_t rc = dz_encoder_read_rows(ctx_, encoder_, as_i32.data(), ids.size(), out.data());
@@ -284,6 +327,7 @@ private:
     dz_encoder_config config_{};
     Json tuning_;
     float temperature_ = 1.0f;
+    std::shared_ptr<PackedCheckpoint> checkpoint_;
 };
 
 }  // namespace decisive

@@ -11,9 +11,14 @@
 #include <sstream>
 #include <unistd.h>
 
+#include <cstdlib>
+#include <filesystem>
+
 #include "../answer.hpp"
 #include "../embedding_cache.hpp"
 #include "../inference.hpp"
+#include "../packed_checkpoint.hpp"
+#include "../sha256.hpp"
 #include "harness.hpp"
 
 using namespace decisive;
@@ -383,6 +388,150 @@ TEST(json_text_and_options_match_the_reference_known_answers) {
         CHECK(Json(Json::Array(o.value().legend)) == c["legend"]);
     }
     CHECK_EQ(json_text(Json::parse("[1, 2.0, 0.5, 123456.75, 1e-5]")), std::string("[1, 2.0, 0.5, 123456.75, 1e-05]"));
+}
+
+// ---- SHA-256 and the packed checkpoint (prepare_hf_q4.py:31-114) ---------------------
+
+TEST(sha256_matches_the_fips_180_known_answers) {
+    CHECK_EQ(Sha256::of("", 0), std::string("e3b0c44298fc1c149afbf4c8996fb92427ae41e4649b934ca495991b7852b855"));
+    CHECK_EQ(Sha256::of("abc", 3), std::string("ba7816bf8f01cfea414140de5dae2223b00361a396177a9cb410ff61f20015ad"));
+    const char *two = "abcdbcdecdefdefgefghfghighijhijkijkljklmklmnlmnomnopnopq";
+    CHECK_EQ(Sha256::of(two, strlen(two)),
+             std::string("248d6a61d20638b8e5c026930c3e6039a33ce45964ff2167f6ecedd419db06c1"));
+    Sha256 million;
+    std::string a(1000, 'a');
+    for (int i = 0; i < 1000; i++) million.update(a.data(), a.size());
+    CHECK_EQ(million.hex(), std::string("cdc76e5c9914fb9281a1c7e284d73e67f1809a48a497200e046d39ccc7112cd0"));
+}
+
+namespace fs = std::filesystem;
+
+// The checkpoint that the test driver wrote (tests/test_host.py), copied to a
+// fresh directory so a case may damage it.
+static std::string checkpoint_copy(const char *tag) {
+    const char *src = getenv("DZ_CHECKPOINT_DIR");
+    if (!src) return std::string();
+    fs::path dst = fs::temp_directory_path() / (std::string("dz_ck_") + tag + "_" + std::to_string(getpid()));
+    fs::remove_all(dst);
+    fs::copy(src, dst, fs::copy_options::recursive);
+    return dst.string();
+}
+
+static Json read_json(const std::string &path) {
+    std::ifstream f(path);
+    std::stringstream t;
+    t << f.rdbuf();
+    return Json::parse(t.str());
+}
+
+static void write_json(const std::string &path, const Json &j) {
+    std::ofstream f(path, std::ios::trunc);
+    f << j.dump();
+}
+
+static std::string open_error(const std::string &dir) {
+    auto c = PackedCheckpoint::open(dir);
+    return c.ok() ? std::string("OK") : c.error().message;
+}
+
+TEST(checkpoint_accepts_the_complete_layout_and_reads_its_parts) {
+    std::string dir = checkpoint_copy("ok");
+    CHECK(!dir.empty());
+    if (dir.empty()) return;
+    auto c = PackedCheckpoint::open(dir);
+    CHECK(c.ok());
+    if (!c.ok()) {
+        fprintf(stderr, "%s\n", c.error().message.c_str());
+        return;
+    }
+    const PackedCheckpoint &ck = c.value();
+    CHECK_EQ(ck.format().name, std::string("q4-e4"));
+    CHECK_EQ(ck.row_bytes(), (size_t)1440);
+    CHECK_EQ(ck.vocab(), (uint64_t)50);
+    CHECK_EQ(ck.layers().size(), (size_t)32);
+    // a tensor is its byte range of the layer file
+    auto t = ck.tensor(7, "language_model.layers.7.norm.weight");
+    CHECK(t.ok() && t.value().size() == 256);
+    std::ifstream f(dir + "/q4-e4-layer-07.bin", std::ios::binary);
+    std::vector<char> all((std::istreambuf_iterator<char>(f)), std::istreambuf_iterator<char>());
+    CHECK(t.ok() && std::memcmp(t.value().data(), all.data() + 288, 256) == 0);
+    CHECK(!ck.tensor(7, "language_model.layers.8.norm.weight").ok());
+    // embedding rows at id * row_bytes, in request order
+    auto rows = ck.embedding_rows({3, 0, 3});
+    std::ifstream e(dir + "/q4-e4-embedding.bin", std::ios::binary);
+    std::vector<char> table((std::istreambuf_iterator<char>(e)), std::istreambuf_iterator<char>());
+    CHECK(rows.ok() && std::memcmp(rows.value().data(), table.data() + 3 * 1440, 1440) == 0 &&
+          std::memcmp(rows.value().data() + 1440, table.data(), 1440) == 0 &&
+          std::memcmp(rows.value().data() + 2880, table.data() + 3 * 1440, 1440) == 0);
+    CHECK(ck.embedding_rows({50}).error().code == "INVALID_REQUEST");
+    auto norm = ck.norm();
+    CHECK(norm.ok() && norm.value().size() == 2560 && std::isfinite(norm.value()[0]));
+    auto temperature = ck.temperature();
+    CHECK(temperature.ok() && temperature.value() == 1.5539091673122623f);
+    CHECK(ck.readout_bytes().ok() && ck.readout_bytes().value().size() == 255 * 1440);
+    fs::remove_all(dir);
+}
+
+// test_prepare_hf_q4.py:47-95: corrupt bytes, missing / duplicate /
+// overlapping tensors, wrong source, extra payload, traversal and symlinks.
+TEST(checkpoint_rejects_what_the_reference_validator_rejects) {
+    std::string dir = checkpoint_copy("bad");
+    if (dir.empty()) {
+        CHECK(!dir.empty());
+        return;
+    }
+    const std::string manifest_path = dir + "/packed-q4-e4.json";
+    const Json original = read_json(manifest_path);
+    auto with = [&](auto edit) {
+        Json m = original;
+        edit(m);
+        write_json(manifest_path, m);
+        std::string err = open_error(dir);
+        write_json(manifest_path, original);
+        return err;
+    };
+    CHECK_EQ(open_error(dir), std::string("OK"));
+    // corrupt bytes
+    {
+        std::string layer = dir + "/q4-e4-layer-07.bin";
+        std::ifstream in(layer, std::ios::binary);
+        std::vector<char> keep((std::istreambuf_iterator<char>(in)), std::istreambuf_iterator<char>());
+        std::vector<char> bad(keep.size(), 'x');
+        std::ofstream(layer, std::ios::binary | std::ios::trunc).write(bad.data(), (std::streamsize)bad.size());
+        CHECK(open_error(dir).find("Checksum") == 0);
+        std::ofstream(layer, std::ios::binary | std::ios::trunc).write(keep.data(), (std::streamsize)keep.size());
+    }
+    auto tensors0 = [](Json &m) -> Json & { return m["layers"][0]["tensors"]; };
+    CHECK_EQ(with([&](Json &m) { tensors0(m) = Json::array(); }), std::string("Missing layer tensors"));
+    CHECK_EQ(with([&](Json &m) { tensors0(m).push_back(Json(tensors0(m)[0])); }),
+             std::string("Unknown or repeated tensor"));
+    CHECK_EQ(with([&](Json &m) { tensors0(m)[0]["start"] = Json(1); }), std::string("Invalid tensor range"));
+    CHECK_EQ(with([&](Json &m) { m["revision"] = Json(std::string(40, '0')); }), std::string("Wrong source revision"));
+    CHECK_EQ(with([&](Json &m) { m["scheme"] = Json("other"); }), std::string("Unsupported packed format"));
+    CHECK_EQ(with([&](Json &m) {
+                 Json extra = Json::object();
+                 extra["bytes"] = Json(1);
+                 extra["sha256"] = Json(std::string(64, '0'));
+                 m["files"]["unexpected.bin"] = extra;
+             }),
+             std::string("Unexpected packed files"));
+    CHECK_EQ(with([&](Json &m) { m["layers"][3]["file"] = Json("q4-e4-layer-04.bin"); }),
+             std::string("Wrong layer filename/order"));
+    CHECK_EQ(with([&](Json &m) { m["decoder_bytes"] = Json(1); }), std::string("Decoder total mismatch"));
+    CHECK_EQ(with([&](Json &m) { m["group_bytes"] = Json(68); }), std::string("Wrong group layout"));
+    CHECK_EQ(with([&](Json &m) { m["readout"] = Json("q4-e4-norm.bin"); }), std::string("Invalid readout payload"));
+    // traversal and symlinks
+    Json files = Json::object();
+    files["../outside"] = Json::object();
+    CHECK_EQ(PackedCheckpoint::verify_files(dir, files).error().message, std::string("Unsafe filename"));
+    fs::create_symlink(dir + "/q4-e4-layer-00.bin", dir + "/link.bin");
+    Json linked = Json::object();
+    linked["link.bin"] = original["files"]["q4-e4-layer-00.bin"];
+    CHECK(PackedCheckpoint::verify_files(dir, linked).error().message.find("symlink") != std::string::npos);
+    // exactly one manifest
+    fs::copy_file(manifest_path, dir + "/packed-q8-e8.json");
+    CHECK_EQ(open_error(dir), std::string("Expected exactly one packed manifest"));
+    fs::remove_all(dir);
 }
 
 int main(int argc, char **argv) { return harness::run_all(argc, argv); }

@@ -5,6 +5,7 @@
 // embedding-row cache serves repeats without changing results, long inputs
 // are split by maxSequenceTokens rather than truncated, and failures clear
 // the cache (src/inference/mod.rs:240-242).
+#include <cstdlib>
 #include <cstring>
 #include <vector>
 
@@ -150,6 +151,87 @@ TEST(rocm_answers_are_the_answer_step_over_the_readout_logits) {
     auto again = model.predict(req, nullptr, &cache.value(), Cancellation{});
     CHECK(again.ok() && again.value().response == resp);
     CHECK_EQ(cache.value().state().misses(), misses);
+}
+
+TEST(rocm_backend_opened_on_a_packed_checkpoint) {
+    const char *dir = getenv("DZ_CHECKPOINT_DIR");
+    CHECK(dir != nullptr);
+    if (!dir) return;
+    dz_encoder_config cfg = small_config();
+    cfg.layers = 1;
+    cfg.hidden = 2560;
+    cfg.heads = 40;
+    cfg.ffn = 256;
+    auto made = Rocm::create_from_checkpoint(0, dir, cfg, 7, no_tuning());
+    CHECK(made.ok());
+    if (!made.ok()) {
+        fprintf(stderr, "%s\n", made.error().to_string().c_str());
+        return;
+    }
+    Model<Rocm> model(made.take());
+    Rocm &rocm = model.backend();
+    auto ck = PackedCheckpoint::open(dir);
+    CHECK(ck.ok());
+    if (!ck.ok()) return;
+    CHECK(rocm.temperature() == ck.value().temperature().value());
+    CHECK_EQ(rocm.config().vocab, 50);
+    std::vector<uint32_t> ids = {4, 49, 0, 4, 17, 23, 8, 31, 2, 11, 40, 6};
+    // rows come from the checkpoint's embedding file
+    auto rows = rocm.read_rows(ids);
+    CHECK(rows.ok() && rows.value() == ck.value().embedding_rows(ids).value());
+    // answers: the readout is the checkpoint's readout with its final norm
+    Request req = answer_request(ids, {0, 5, 11});
+    auto got = model.predict(req, nullptr, nullptr, Cancellation{});
+    CHECK(got.ok());
+    if (!got.ok()) {
+        fprintf(stderr, "%s\n", got.error().to_string().c_str());
+        return;
+    }
+    dz_ctx *ctx = rocm.context();
+    void *hidden = nullptr, *sel = nullptr, *norm_dev = nullptr, *logits_dev = nullptr;
+    const size_t d = 2560;
+    CHECK(dz_alloc(ctx, ids.size() * d * 4, &hidden) == DZ_OK);
+    CHECK(dz_alloc(ctx, 3 * d * 4, &sel) == DZ_OK);
+    CHECK(dz_alloc(ctx, d * 4, &norm_dev) == DZ_OK);
+    CHECK(dz_alloc(ctx, 3 * DZ_READOUT_CODES * 4, &logits_dev) == DZ_OK);
+    CHECK(dz_encoder_hidden_rows(ctx, rocm.encoder(), rows.value().data(), ids.size(), (float *)hidden) == DZ_OK);
+    std::vector<float> h(ids.size() * d), picked(3 * d);
+    CHECK(dz_copy_d2h(ctx, h.data(), hidden, h.size() * 4) == DZ_OK);
+    const int markers[3] = {0, 5, 11};
+    for (int i = 0; i < 3; i++) std::memcpy(&picked[i * d], &h[markers[i] * d], d * 4);
+    CHECK(dz_copy_h2d(ctx, sel, picked.data(), picked.size() * 4) == DZ_OK);
+    auto norm = ck.value().norm();
+    CHECK(dz_copy_h2d(ctx, norm_dev, norm.value().data(), d * 4) == DZ_OK);
+    auto readout = ck.value().readout_bytes();
+    dz_weight *w = nullptr;
+    CHECK(dz_weight_upload(ctx, readout.value().data(), readout.value().size(), DZ_Q4_G64_F32, DZ_READOUT_CODES,
+                           d, &w) == DZ_OK);
+    CHECK(dz_readout(ctx, w, (const float *)norm_dev, (const float *)sel, 3, DZ_READOUT_EPS, (float *)logits_dev) ==
+          DZ_OK);
+    std::vector<float> logits(3 * DZ_READOUT_CODES);
+    CHECK(dz_copy_d2h(ctx, logits.data(), logits_dev, logits.size() * 4) == DZ_OK);
+    const char *keys[3] = {"team", "refund", "tone"};
+    const size_t counts[3] = {3, 2, 3};
+    for (int i = 0; i < 3; i++) {
+        const float *row = logits.data() + i * DZ_READOUT_CODES;
+        auto want = answer(req.questions[keys[i]], std::vector<float>(row, row + counts[i]), rocm.temperature());
+        CHECK(want.ok() && got.value().response["answers"][keys[i]] == want.value());
+    }
+    dz_weight_free(ctx, w);
+    for (void *p : {hidden, sel, norm_dev, logits_dev}) dz_free(ctx, p);
+    // the embedding response of the same tokens is the forward of the file's rows
+    auto emb = model.predict(request_of(ids), nullptr, nullptr, Cancellation{});
+    CHECK(emb.ok());
+    void *out_dev = nullptr;
+    std::vector<float> want(d);
+    CHECK(dz_alloc(ctx, d * 4, &out_dev) == DZ_OK);
+    CHECK(dz_encoder_forward_rows(ctx, rocm.encoder(), rows.value().data(), 1, ids.size(), (float *)out_dev) == DZ_OK);
+    CHECK(dz_copy_d2h(ctx, want.data(), out_dev, d * 4) == DZ_OK);
+    dz_free(ctx, out_dev);
+    CHECK(emb.ok() && same_bits(emb.value().response["embeddings"][0], want));
+    // a checkpoint of another width is refused
+    dz_encoder_config narrow = small_config();
+    CHECK(Rocm::create_from_checkpoint(0, dir, narrow, 7, no_tuning()).error().code == "INVALID_PARAMETERS");
 }
 
 TEST(rocm_answer_requests_are_validated) {

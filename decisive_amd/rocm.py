@@ -99,6 +99,7 @@ _SIGNATURES = {
     "dz_readout": (I32, [P, P, P, P, SZ, F, P]),
     "dz_encoder_readout_params": (I32, [P, PP, PP]),
     "dz_encoder_readout_rows": (I32, [P, P, P, SZ, P, SZ, P]),
+    "dz_encoder_set_readout": (I32, [P, P, P, SZ, I32, P]),
     "dz_tune": (I32, [P, U32, ctypes.c_char_p, ctypes.c_char_p, SZ]),
     "dz_select_variant": (I32, [P, ctypes.c_char_p, ctypes.c_char_p]),
 }
@@ -365,6 +366,13 @@ class Encoder:
         w, norm = ctypes.c_void_p(), ctypes.c_void_p()
         self.ctx._check(load().dz_encoder_readout_params(self.handle, ctypes.byref(w), ctypes.byref(norm)))
         return Weight(self.ctx, w.value, owned=False), norm.value
+
+    def set_readout(self, packed_host, layout: int, norm_host):
+        import numpy as np
+        packed_host = np.ascontiguousarray(packed_host, dtype=np.uint8)
+        norm_host = np.ascontiguousarray(norm_host, dtype=np.float32)
+        self.ctx._check(load().dz_encoder_set_readout(self.ctx.handle, self.handle, packed_host.ctypes.data,
+                                                      packed_host.size, layout, norm_host.ctypes.data))
 
     def readout_rows(self, rows_host, seq: int, markers):
         """Logits f32 [len(markers) x 255] of the hidden rows at markers."""

@@ -288,6 +288,14 @@ int32_t dz_readout(dz_ctx *ctx, const dz_weight *w, const float *norm_dev, const
 /* The encoder's readout: weight [DZ_READOUT_CODES x hidden] (Q4 g64) and its
  * zero-centred norm weights (device f32 [hidden]); owned by the encoder. */
 int32_t dz_encoder_readout_params(const dz_encoder *enc, const dz_weight **w, const float **norm_dev);
+/* Replaces the encoder's readout with a loaded one (browser/pplx.rs:212-218
+ * and mod.rs:126-135: the packed readout file, Q4 or Q8 by its size, and the
+ * final norm of a packed checkpoint): packed_host holds DZ_READOUT_CODES x hidden in a group-64
+ * wire layout (DZ_Q4_G64_F32 or DZ_Q8_G64_F32, validated as
+ * dz_weight_upload does), norm_host f32 [hidden] the zero-centred norm
+ * weights. The encoder owns the uploaded copy. Synchronous. */
+int32_t dz_encoder_set_readout(dz_ctx *ctx, dz_encoder *enc, const void *packed_host, size_t bytes,
+                               int32_t layout, const float *norm_host);
 /* pplx_flash/native.rs:193-274 for one chunk: the encoder over one sequence
  * of packed rows, then dz_readout of the hidden rows at markers_host (count
  * positions < seq, count <= DZ_READOUT_MAX_MARKERS) with the encoder's
