@@ -194,7 +194,20 @@ def secondary(torch, ctx, rocm, stream) -> dict:
     tf = 2 * m * n * k / (ms * 1e-3) / 1e12
     out["q4_prefill_w4a16_m16384_k4096_n14336"] = {"ms": round(ms, 4), "TFLOP/s": round(tf, 1),
                                                    "frac_of_f16_peak": round(tf / F16_PEAK_TFLOPS, 4),
-                                                   "variant": ctx.info()["variants"]["gemm_w4a16"]}
+                                                   "variant": ctx.info()["variants"]["gemm_w4a16"],
+                                                   "out": "f32"}
+    del y
+    # the same product in prefill form: f16 out (what the next layer reads), one rounding
+    y = torch.empty((m, n), dtype=torch.float16, device="cuda")
+    fn = lambda r: ctx.linear_f16(w, x, m, y)  # noqa: E731
+    for r in range(2):
+        fn(r)
+    ms = timed_ms(torch, stream, fn, 10)
+    tf = 2 * m * n * k / (ms * 1e-3) / 1e12
+    out["q4_prefill_w4a16_f16out_m16384_k4096_n14336"] = {
+        "ms": round(ms, 4), "TFLOP/s": round(tf, 1), "frac_of_f16_peak": round(tf / F16_PEAK_TFLOPS, 4),
+        "variant": ctx.info()["variants"]["gemm_w4a16"], "out": "f16",
+        "note": "dz_linear_f16: f32 accumulation, each output rounded once to f16"}
     w.free()
     del x, y
     # the reference's own numerics (bit-exact W4A8, int8.rs fold order) at the config 5 shape:

@@ -121,6 +121,15 @@ __device__ __forceinline__ float erf_as7126(float x) {
     return __builtin_copysignf(__builtin_fmaf(-p, e, 1.0f), x);
 }
 
+// v as an f32 value: the compiler cannot fuse the operation that produced it
+// into a following f16 conversion (v_fma_mixlo_f16 rounds the exact result
+// once, to f16, where f32 code rounds twice), so an f16 epilogue rounds the
+// same f32 value that an f32 output holds.
+__device__ __forceinline__ float f32_rounded(float v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
 // erf-GELU: 0.5 x (1 + erf(x / sqrt(2)))
 __device__ __forceinline__ float gelu_erf(float x) {
     return 0.5f * x * (1.0f + erf_as7126(x * 0.70710678118654752f));

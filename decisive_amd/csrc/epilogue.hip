@@ -203,6 +203,18 @@ __global__ void to_f32_kernel(const void *__restrict__ x, int dtype, size_t n, f
     if (i < n) y[i] = ld(x, dtype, i);
 }
 
+// The f16 epilogue of the W4A16 GEMM applied to f32 products (the GEMV
+// path): 0 none, 1 erf-GELU, 2 + residual; one rounding to f16 at the end.
+__global__ void f16_epilogue_kernel(const float *__restrict__ v, int epi, const half_t *__restrict__ res,
+                                    half_t *__restrict__ y, size_t n) {
+    size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    float t = v[i];
+    if (epi == 1) t = gelu_erf(t);
+    else if (epi == 2) t = t + (float)res[i];
+    y[i] = (half_t)f32_rounded(t);
+}
+
 __global__ void gelu_kernel(void *x, int dtype, size_t n) {
     size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
     if (i >= n) return;
@@ -514,6 +526,9 @@ void launch_flag_nonfinite(const float *y, size_t n, int *flag, int bit, hipStre
 }
 void launch_to_f32(const void *x, int dtype, size_t n, float *y, hipStream_t s) {
     if (n) hipLaunchKernelGGL(to_f32_kernel, dim3(cdiv(n, 256)), dim3(256), 0, s, x, dtype, n, y);
+}
+void launch_f16_epilogue(const float *v, int epi, const half_t *res, half_t *y, size_t n, hipStream_t s) {
+    if (n) hipLaunchKernelGGL(f16_epilogue_kernel, dim3(cdiv(n, 256)), dim3(256), 0, s, v, epi, res, y, n);
 }
 void launch_gelu(void *x, int dtype, size_t n, hipStream_t s) {
     if (n) hipLaunchKernelGGL(gelu_kernel, dim3(cdiv(n, 256)), dim3(256), 0, s, x, dtype, n);

@@ -74,6 +74,8 @@ constexpr int kReadoutMaxCols = 16384;
 void launch_readout_rms(const void *h, int dtype, const int32_t *rows, int n, int d, const float *w,
                         float eps, int zero_centered, float *y, hipStream_t s);
 void launch_flag_nonfinite(const float *y, size_t n, int *flag, int bit, hipStream_t s);
+// y f16 [n] = epilogue(v) (0 none, 1 GELU, 2 + res), rounded once
+void launch_f16_epilogue(const float *v, int epi, const half_t *res, half_t *y, size_t n, hipStream_t s);
 // y f32 [n] = x (f32 dtype 0 / f16 dtype 1), exact
 void launch_to_f32(const void *x, int dtype, size_t n, float *y, hipStream_t s);
 void launch_gelu(void *x, int dtype, size_t n, hipStream_t s);

@@ -664,10 +664,9 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_w4a16_kernel(
                     } else if (EPI == 1) {
                         ((half_t *)out)[at] = (half_t)val;
                     } else if (EPI == 2) {
-                        float gl = gelu_erf(val);
-                        ((half_t *)out)[at] = (half_t)gl;
+                        ((half_t *)out)[at] = (half_t)f32_rounded(gelu_erf(val));
                     } else {
-                        ((half_t *)out)[at] = (half_t)(val + (float)residual[at]);
+                        ((half_t *)out)[at] = (half_t)f32_rounded(val + (float)residual[at]);
                     }
                 }
             }
@@ -1253,20 +1252,20 @@ __global__ __launch_bounds__(WGM *WGN * 64) void w4a16_pipe_kernel(
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     if (EPI == 1) o[e] = (half_t)v[e];
-                    else if (EPI == 2) o[e] = (half_t)gelu_erf(v[e]);
+                    else if (EPI == 2) o[e] = (half_t)f32_rounded(gelu_erf(v[e]));
                     else o[e] = (half_t)0.0f;
                 }
                 if (EPI == 3) {
                     if (vec) {
                         const uint2_t rw = *(const uint2_t *)(residual + at);
                         const half2_t r01 = word_as_half2(rw[0]), r23 = word_as_half2(rw[1]);
-                        o[0] = (half_t)(v[0] + (float)r01[0]);
-                        o[1] = (half_t)(v[1] + (float)r01[1]);
-                        o[2] = (half_t)(v[2] + (float)r23[0]);
-                        o[3] = (half_t)(v[3] + (float)r23[1]);
+                        o[0] = (half_t)f32_rounded(v[0] + (float)r01[0]);
+                        o[1] = (half_t)f32_rounded(v[1] + (float)r01[1]);
+                        o[2] = (half_t)f32_rounded(v[2] + (float)r23[0]);
+                        o[3] = (half_t)f32_rounded(v[3] + (float)r23[1]);
                     } else {
                         for (int e = 0; e < 4; e++)
-                            if (c + e < n) o[e] = (half_t)(v[e] + (float)residual[at + e]);
+                            if (c + e < n) o[e] = (half_t)f32_rounded(v[e] + (float)residual[at + e]);
                     }
                 }
                 if (vec) {

@@ -499,6 +499,34 @@ int32_t dz_linear(dz_ctx *ctx, const dz_weight *w, const void *x, int32_t x_dtyp
     return fail(ctx, DZ_INVALID_PARAMETERS, "unknown mode");
 }
 
+int32_t dz_linear_f16(dz_ctx *ctx, const dz_weight *w, const void *x, size_t m, void *y, int32_t epilogue,
+                      const void *residual) {
+    DZ_BEGIN(ctx);
+    if (!w || (m && (!x || !y))) return fail(ctx, DZ_INVALID_REQUEST, "null pointer");
+    if (epilogue < DZ_EPI_NONE || epilogue > DZ_EPI_RESIDUAL)
+        return fail(ctx, DZ_INVALID_PARAMETERS, "unknown epilogue");
+    if (epilogue == DZ_EPI_RESIDUAL && m && !residual) return fail(ctx, DZ_INVALID_REQUEST, "null residual");
+    if (w->w.bits != 4) return fail(ctx, DZ_INVALID_PARAMETERS, "W4A16 needs a Q4 weight");
+    if (w->w.cols % 8 != 0) return fail(ctx, DZ_INVALID_PARAMETERS, "W4A16 needs cols % 8 == 0");
+    if (((uintptr_t)x & 15) != 0) return fail(ctx, DZ_INVALID_PARAMETERS, "W4A16 activations must be 16-byte aligned");
+    if (m == 0) return DZ_OK;
+    if (m > (1u << 24)) return fail(ctx, DZ_INPUT_TOO_LONG, "input budget exceeded");
+    if (m <= 16) {
+        // the GEMV's f32 products (dz_linear's few-row arithmetic), then the epilogue
+        const size_t count = m * (size_t)w->w.rows;
+        int32_t rc = ensure_work(ctx, count * sizeof(float));
+        if (rc) return rc;
+        dz::launch_w4a16(w->w, (const dz::half_t *)x, (int)m, (float *)ctx->work, variant(ctx, "gemv"),
+                         variant(ctx, "gemm_w4a16"), ctx->stream);
+        dz::launch_f16_epilogue((const float *)ctx->work, epilogue, (const dz::half_t *)residual,
+                                (dz::half_t *)y, count, ctx->stream);
+    } else {
+        dz::launch_w4a16_f16(w->w, (const dz::half_t *)x, (int)m, (dz::half_t *)y, epilogue,
+                             (const dz::half_t *)residual, variant(ctx, "gemm_w4a16"), ctx->stream);
+    }
+    return launched(ctx, "w4a16 f16 linear");
+}
+
 int32_t dz_linear_pair(dz_ctx *ctx, const dz_weight *a, const dz_weight *b, const float *x, size_t m,
                        float *ya, float *yb, int32_t mode) {
     DZ_BEGIN(ctx);

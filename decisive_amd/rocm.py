@@ -25,6 +25,7 @@ STATUS_NAMES = {
 }
 Q4_G64_F32, Q8_G64_F32, Q4_G32_F16 = 0, 1, 2
 F32, F16, BF16 = 0, 1, 2
+EPI_NONE, EPI_GELU, EPI_RESIDUAL = 0, 1, 2
 W4A8, W4A4, W4A16 = 0, 1, 2
 
 
@@ -71,6 +72,7 @@ _SIGNATURES = {
     "dz_act_quantize": (I32, [P, P, SZ, SZ, I32, P, P]),
     "dz_linear": (I32, [P, P, P, I32, SZ, P, I32]),
     "dz_linear_pair": (I32, [P, P, P, P, SZ, P, P, I32]),
+    "dz_linear_f16": (I32, [P, P, P, SZ, P, I32, P]),
     "dz_mlp_requant": (I32, [P, P, P, P, SZ, P, P]),
     "dz_linear_q8": (I32, [P, P, P, P, SZ, P]),
     "dz_project": (I32, [P, P, P, SZ, P]),
@@ -240,6 +242,9 @@ class Context:
 
     def linear(self, w: Weight, x, x_dtype: int, m: int, y, mode: int):
         self._check(load().dz_linear(self.handle, w.handle, _addr(x), x_dtype, m, _addr(y), mode))
+
+    def linear_f16(self, w: Weight, x, m: int, y, epilogue: int = 0, residual=None):
+        self._check(load().dz_linear_f16(self.handle, w.handle, _addr(x), m, _addr(y), epilogue, _addr(residual)))
 
     def linear_pair(self, a: Weight, b: Weight, x, m: int, ya, yb, mode: int = W4A8):
         self._check(load().dz_linear_pair(self.handle, a.handle, b.handle, _addr(x), m, _addr(ya), _addr(yb), mode))

@@ -143,6 +143,20 @@ int32_t dz_linear(dz_ctx *ctx, const dz_weight *w, const void *x_dev, int32_t x_
  * two weights with the same cols. */
 int32_t dz_linear_pair(dz_ctx *ctx, const dz_weight *a, const dz_weight *b, const float *x_dev,
                        size_t m, float *ya_dev, float *yb_dev, int32_t mode);
+/* The prefill form of DZ_W4A16 (the encoder's
+ * projections): f16 activations x_dev [m x cols(w)] (16-byte aligned) ->
+ * f16 y_dev [m x rows(w)]: the products accumulate in f32 as dz_linear's
+ * DZ_W4A16 does, and each output is rounded to f16 once, after the epilogue:
+ *   DZ_EPI_NONE      y = x W^T
+ *   DZ_EPI_GELU      y = gelu(x W^T), erf form (decima/cpu.rs:542-556)
+ *   DZ_EPI_RESIDUAL  y = x W^T + residual, residual_dev f16 [m x rows(w)]
+ * Bits equal f16(dz_linear(..., DZ_W4A16)) after the same epilogue in f32.
+ * Q4 weight (either group), cols % 8 == 0. */
+#define DZ_EPI_NONE 0
+#define DZ_EPI_GELU 1
+#define DZ_EPI_RESIDUAL 2
+int32_t dz_linear_f16(dz_ctx *ctx, const dz_weight *w, const void *x_dev, size_t m, void *y_dev,
+                      int32_t epilogue, const void *residual_dev);
 /* grouped_q4_mlp.wgsl:1-105 (q4_mlp): gate/up W4A8 products of one input,
  * v = silu(gate)*up, re-quantized per (row, 64-column block) to the A8 form of
  * dz_act_quantize: q_dev int8 [m x n], s_dev f32 [m x n/64]. n % 64 == 0. */

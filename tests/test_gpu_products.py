@@ -352,6 +352,53 @@ def test_large_m_gemm_vs_closed_form(ctx, oracle, layout, m, k, n):
         assert bits_equal(o, outs[0]), name
 
 
+@pytest.mark.parametrize("epilogue", [rocm.EPI_NONE, rocm.EPI_GELU, rocm.EPI_RESIDUAL])
+@pytest.mark.parametrize("m,k,n", [(3, 512, 80), (300, 576, 200), (1000, 1024, 1536), (257, 4096, 257)])
+def test_w4a16_f16_output_is_the_f32_product_rounded_once(ctx, oracle, epilogue, m, k, n):
+    """dz_linear_f16: the f32 product of dz_linear, then the epilogue in f32
+    (GELU by dz_gelu, residual added in f32), rounded once to f16 -- bit for
+    bit, on every GEMM variant."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(m + 3 * k + n + epilogue)
+    xh = oracle.f32_to_f16_bits(rng.standard_normal((m, k)).astype(np.float32))
+    wf = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    w = ctx.upload(oracle.pack_g32_f16(wf, n, k), rocm.Q4_G32_F16, n, k)
+    res = rng.standard_normal((m, n)).astype(np.float16)
+    x = dev(xh.view(np.float16))
+    ctx.select_variant("gemm_w4a16", W4A16_VARIANTS[0])
+    y32 = empty((m, n), torch.float32)
+    ctx.linear(w, x, rocm.F16, m, y32, rocm.W4A16)
+    if epilogue == rocm.EPI_GELU:
+        ctx.gelu(y32, rocm.F32, m * n)
+    want = host(ctx, y32)
+    if epilogue == rocm.EPI_RESIDUAL:
+        want = (want + res.astype(np.float32)).astype(np.float32)
+    want = want.astype(np.float16)
+    rd = dev(res)
+    for name in W4A16_VARIANTS:
+        ctx.select_variant("gemm_w4a16", name)
+        y = empty((m, n), torch.float16)
+        ctx.linear_f16(w, x, m, y, epilogue, rd if epilogue == rocm.EPI_RESIDUAL else None)
+        got = host(ctx, y)
+        assert np.array_equal(got.view(np.uint16), want.view(np.uint16)), name
+    ctx.select_variant("gemm_w4a16", W4A16_VARIANTS[0])
+
+
+def test_w4a16_f16_output_rejects_bad_arguments(ctx, oracle):
+    torch = pytest.importorskip("torch")
+    w = ctx.quantize(dev(np.ones((64, 64), np.float32) * 0.01), rocm.F32, 64, 64, 4, 32)
+    x = empty((2, 64), torch.float16)
+    y = empty((2, 64), torch.float16)
+    for epilogue, res, code in [(3, None, "INVALID_PARAMETERS"), (rocm.EPI_RESIDUAL, None, "INVALID_REQUEST")]:
+        with pytest.raises(rocm.DzError) as e:
+            ctx.linear_f16(w, x, 2, y, epilogue, res)
+        assert e.value.code == code
+    w8 = ctx.quantize(dev(np.ones((64, 64), np.float32) * 0.01), rocm.F32, 64, 64, 8, 64)
+    with pytest.raises(rocm.DzError) as e:
+        ctx.linear_f16(w8, x, 2, y)
+    assert e.value.code == "INVALID_PARAMETERS"
+
+
 @pytest.mark.parametrize("n", [3072, 3120])
 def test_w4a16_column_split_matches_register_kernel(ctx, oracle, n):
     """M=8192, K=1024: 256x256 tiles fill whole waves of compute units over
