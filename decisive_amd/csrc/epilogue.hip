@@ -499,8 +499,8 @@ void launch_layernorm(const void *x, void *y, int dtype, int rows, int d, const 
     const bool fast = dtype == 1 && (d == 512 || d == 1024 || d == 2048) &&
                       (((uintptr_t)x | (uintptr_t)y | (uintptr_t)w | (uintptr_t)b) & 15) == 0;
     if (fast) {
-        // two rows per wave (4-wave blocks): the second row's load overlaps the first row's work
-        const dim3 grid(cdiv(rows, 8));
+        // one row per wave (4-wave blocks): every row's load is in flight at once
+        const dim3 grid(cdiv(rows, 4));
         const half_t *xh = (const half_t *)x;
         half_t *yh = (half_t *)y;
         if (d == 512) hipLaunchKernelGGL(layernorm_f16_rows_kernel<1>, grid, dim3(256), 0, s, xh, yh, rows, w, b, eps);

@@ -1,0 +1,778 @@
+// pplx.hip -- the Pplx decider forward on the quantized products: the hybrid
+// decoder of hyperlogue/decisive src/models/pplx_flash/backbone.rs (three
+// gated-delta layers, then one gated full-attention layer, repeated), the
+// final zero-centred RMSNorm and the packed readout (mod.rs:149-185), over
+// one sequence of packed embedding rows (native.rs:193-274).
+//
+// The layer RMSNorms are the readout's bit-exact cpu::rms_from (squares added
+// in row order). Every projection is the reference's W4A8 product (dz_linear_pair,
+// dz_linear, dz_mlp_requant + dz_linear_q8: the int8.rs group fold, bit-exact
+// with the CPU path); the layer ops between them are the kernels below:
+//   conv_silu      cpu.rs:372-391 (causal depthwise conv of width 4 + SiLU)
+//   delta_prep     backbone.rs:366-379 (q/k unit norms, decay g, beta)
+//   delta_scan     backbone.rs:380-407 (the gated delta rule, one state
+//                  column per lane group; f32 with fused multiply-adds)
+//   delta_gate     backbone.rs:310-326, cpu.rs:392-414
+//   head_norm_rope cpu.rs:310-333 per head (zero-centred) + backbone.rs:415-428
+//   attention      backbone.rs:509-579 (non-causal softmax attention, GQA)
+//   attention_gate cpu.rs:415-429
+// Those are tolerance-checked against the oracle's restatement; the
+// reference's own orders (sequential sums, unfused products) are kept where
+// they cost nothing.
+#include <string.h>
+
+#include <algorithm>
+#include <string>
+#include <type_traits>
+#include <vector>
+
+#include "../../include/decisive_rocm.h"
+#include "kernels.hpp"
+
+namespace dz {
+
+int32_t ctx_fail(dz_ctx *ctx, int32_t code, const std::string &msg);
+int32_t ctx_hip_fail(dz_ctx *ctx, hipError_t e, const char *what);
+hipStream_t ctx_stream(dz_ctx *ctx);
+int *ctx_flag(dz_ctx *ctx);
+const Weight &weight_of(const dz_weight *h);
+int32_t weight_upload(dz_ctx *ctx, const void *packed, size_t bytes, int32_t layout, size_t rows, size_t cols,
+                      dz_weight **out);
+void weight_free(dz_weight *h);
+int32_t ctx_readout_rows(dz_ctx *ctx, const Weight &w, const float *norm, const void *hidden, int dtype,
+                         const int32_t *select, size_t rows, float eps, float *logits);
+
+namespace {
+
+constexpr int kLd = 128;   // delta head width (backbone.rs LD)
+constexpr int kAd = 256;   // attention head width (backbone.rs AD)
+constexpr int kMaxKeys = 8192;
+
+inline unsigned blocks_of(size_t n, unsigned threads) { return (unsigned)((n + threads - 1) / threads); }
+
+__device__ __forceinline__ float sigmoid_ref(float v) { return __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-v))); }
+__device__ __forceinline__ float silu_ref(float v) { return __fmul_rn(v, sigmoid_ref(v)); }
+__device__ __forceinline__ float wave_sum(float v) {
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+    return v;
+}
+// 1/sqrt(t) with the square root correctly rounded (taken in f64)
+__device__ __forceinline__ float rsqrt_rn(float t) { return __fdiv_rn(1.0f, __double2float_rn(__dsqrt_rn((double)t))); }
+
+// out[t][c] = silu(sum_tap x[t-3+tap][c] * w[tap][c]); rows before 0 are zero
+__global__ void conv_silu_kernel(const float *__restrict__ x, int n, int width, const float *__restrict__ w,
+                                 float *__restrict__ out) {
+    const size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+    if (i >= (size_t)n * width) return;
+    const int t = (int)(i / width), c = (int)(i % width);
+    float sum = 0.0f;
+#pragma unroll
+    for (int tap = 0; tap < 4; tap++) {
+        const int row = t - 3 + tap;
+        const float v = row < 0 ? 0.0f : x[(size_t)row * width + c];
+        sum = __fadd_rn(sum, __fmul_rn(v, w[(size_t)tap * width + c]));
+    }
+    out[i] = silu_ref(sum);
+}
+
+// One block per token, one wave per key head: unit q and k (q also scaled by
+// 1/sqrt(ld)); threads below lh compute the decay g and beta of head h.
+__global__ void delta_prep_kernel(const float *__restrict__ conv, int lh, int lk, const float *__restrict__ a,
+                                  const float *__restrict__ b, const float *__restrict__ decay,
+                                  const float *__restrict__ dt, float *__restrict__ qhat,
+                                  float *__restrict__ khat, float *__restrict__ gb) {
+    const int t = blockIdx.x, wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const size_t lkv = (size_t)lk * kLd, width = 2 * lkv + (size_t)lh * kLd;
+    if (wave < lk) {
+        const float *qs = conv + (size_t)t * width + (size_t)wave * kLd;
+        const float *ks = qs + lkv;
+        const float q0 = qs[lane], q1 = qs[lane + 64], k0 = ks[lane], k1 = ks[lane + 64];
+        const float qi = rsqrt_rn(__fadd_rn(wave_sum(q0 * q0 + q1 * q1), 1e-6f));
+        const float ki = rsqrt_rn(__fadd_rn(wave_sum(k0 * k0 + k1 * k1), 1e-6f));
+        const float root = rsqrt_rn((float)kLd);
+        float *qd = qhat + ((size_t)t * lk + wave) * kLd, *kd = khat + ((size_t)t * lk + wave) * kLd;
+        qd[lane] = __fmul_rn(__fmul_rn(q0, qi), root);
+        qd[lane + 64] = __fmul_rn(__fmul_rn(q1, qi), root);
+        kd[lane] = __fmul_rn(k0, ki);
+        kd[lane + 64] = __fmul_rn(k1, ki);
+    }
+    for (int h = threadIdx.x; h < lh; h += blockDim.x) {
+        const float x = __fadd_rn(a[(size_t)t * lh + h], dt[h]);
+        const float softplus = x > 20.0f ? x : log1pf(expf(x));
+        gb[((size_t)t * lh + h) * 2] = expf(__fmul_rn(-decay[h], softplus));
+        gb[((size_t)t * lh + h) * 2 + 1] = sigmoid_ref(b[(size_t)t * lh + h]);
+    }
+}
+
+// The gated delta rule. A wave owns 16 state columns j of head h; lane
+// (r, c) holds rows [32r, 32r + 32) of column 16*blockIdx.y + c in registers.
+// Per token: S *= g; mem = S^T k; delta = (v - mem) beta; S += k delta^T;
+// out = S^T q. The row sums close over the four row groups with two
+// cross-lane adds. The next token's inputs load while this one computes.
+__global__ __launch_bounds__(64) void delta_scan_kernel(const float *__restrict__ qhat,
+                                                        const float *__restrict__ khat,
+                                                        const float *__restrict__ conv,
+                                                        const float *__restrict__ gb, int n, int lh, int lk,
+                                                        float *__restrict__ out) {
+    constexpr int R = kLd / 4;
+    const int h = blockIdx.x, lane = threadIdx.x, r = lane / 16, c = lane % 16;
+    const int j = blockIdx.y * 16 + c;
+    const int kh = h / (lh / lk);
+    const size_t lkv = (size_t)lk * kLd, width = 2 * lkv + (size_t)lh * kLd;
+    float S[R];
+#pragma unroll
+    for (int i = 0; i < R; i++) S[i] = 0.0f;
+    float4_t kn[R / 4], qn[R / 4];
+    float vn = 0.0f, gn = 0.0f, bn = 0.0f;
+    auto fetch = [&](int t) {
+        const float4_t *kp = (const float4_t *)(khat + ((size_t)t * lk + kh) * kLd + r * R);
+        const float4_t *qp = (const float4_t *)(qhat + ((size_t)t * lk + kh) * kLd + r * R);
+#pragma unroll
+        for (int u = 0; u < R / 4; u++) {
+            kn[u] = kp[u];
+            qn[u] = qp[u];
+        }
+        vn = conv[(size_t)t * width + 2 * lkv + (size_t)h * kLd + j];
+        gn = gb[((size_t)t * lh + h) * 2];
+        bn = gb[((size_t)t * lh + h) * 2 + 1];
+    };
+    if (n > 0) fetch(0);
+    for (int t = 0; t < n; t++) {
+        float k[R], q[R];
+#pragma unroll
+        for (int u = 0; u < R / 4; u++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                k[4 * u + e] = kn[u][e];
+                q[4 * u + e] = qn[u][e];
+            }
+        const float v = vn, g = gn, beta = bn;
+        if (t + 1 < n) fetch(t + 1);
+        float m0 = 0.0f, m1 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < R; i += 2) {
+            S[i] *= g;
+            S[i + 1] *= g;
+            m0 = __builtin_fmaf(S[i], k[i], m0);
+            m1 = __builtin_fmaf(S[i + 1], k[i + 1], m1);
+        }
+        float mem = m0 + m1;
+        mem += __shfl_xor(mem, 16);
+        mem += __shfl_xor(mem, 32);
+        const float delta = (v - mem) * beta;
+        float o0 = 0.0f, o1 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < R; i += 2) {
+            S[i] = __builtin_fmaf(k[i], delta, S[i]);
+            S[i + 1] = __builtin_fmaf(k[i + 1], delta, S[i + 1]);
+            o0 = __builtin_fmaf(S[i], q[i], o0);
+            o1 = __builtin_fmaf(S[i + 1], q[i + 1], o1);
+        }
+        float o = o0 + o1;
+        o += __shfl_xor(o, 16);
+        o += __shfl_xor(o, 32);
+        if (r == 0) out[((size_t)h * n + t) * kLd + j] = o;
+    }
+}
+
+// ctx[t][h*ld + i] = ((src*s)*norm[i])*silu(z), s = 1/sqrt(mean(src^2) + 1e-6)
+__global__ __launch_bounds__(64) void delta_gate_kernel(const float *__restrict__ heads, int n, int lh,
+                                                        const float *__restrict__ norm,
+                                                        const float *__restrict__ z, float *__restrict__ ctx) {
+    const int t = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+    const float *src = heads + ((size_t)h * n + t) * kLd;
+    const float s0 = src[lane], s1 = src[lane + 64];
+    const float scale = rsqrt_rn(__fadd_rn(wave_sum(s0 * s0 + s1 * s1) / (float)kLd, 1e-6f));
+    const size_t at = (size_t)t * lh * kLd + (size_t)h * kLd;
+    ctx[at + lane] = __fmul_rn(__fmul_rn(__fmul_rn(s0, scale), norm[lane]), silu_ref(z[at + lane]));
+    ctx[at + lane + 64] =
+        __fmul_rn(__fmul_rn(__fmul_rn(s1, scale), norm[lane + 64]), silu_ref(z[at + lane + 64]));
+}
+
+// Per (row, head): zero-centred RMSNorm of the 256 values at src + row*src_row
+// + head*src_head, then the rotary embedding of dims [0, 64) at position
+// pos[row] (row when pos is null): dims i and i + 32 turn by pos * freq[i].
+// src and dst may be the same buffer (each wave reads its values first).
+__global__ __launch_bounds__(64) void head_norm_rope_kernel(const float *src, size_t src_row, int src_head,
+                                                            int heads, const float *__restrict__ w,
+                                                            const int32_t *__restrict__ pos,
+                                                            const float *__restrict__ freq, float *dst) {
+    const int row = blockIdx.x, head = blockIdx.y, lane = threadIdx.x;
+    const float4_t x = *(const float4_t *)(src + (size_t)row * src_row + (size_t)head * src_head + lane * 4);
+    const float ss = wave_sum(x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3]);
+    const float scale = rsqrt_rn(__fadd_rn(ss / (float)kAd, 1e-6f));
+    float y[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) y[e] = __fmul_rn(__fmul_rn(x[e], scale), __fadd_rn(1.0f, w[lane * 4 + e]));
+    // lanes 0-7 hold dims 0-31, lanes 8-15 dims 32-63
+    const float p = (float)(pos ? pos[row] : row);
+    float partner[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) partner[e] = __shfl(y[e], lane < 8 ? lane + 8 : lane - 8);
+    if (lane < 16) {
+        const int base = (lane % 8) * 4;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            float sn, cs;
+            sincosf(__fmul_rn(p, freq[base + e]), &sn, &cs);
+            if (lane < 8) y[e] = __fsub_rn(__fmul_rn(y[e], cs), __fmul_rn(partner[e], sn));
+            else y[e] = __fadd_rn(__fmul_rn(y[e], cs), __fmul_rn(partner[e], sn));
+        }
+    }
+    *(float4_t *)(dst + ((size_t)row * heads + head) * kAd + lane * 4) = float4_t{y[0], y[1], y[2], y[3]};
+}
+
+// One wave per (head, query): scores over every key (lanes split the keys),
+// max-subtracted softmax, then P V with lanes splitting the 256 dims.
+// q [nq x ah x 256], k [nk x akv x 256] (normed, rotated), v rows of v_row
+// floats with head kh at kh*256; out [ah x nq x 256].
+__global__ __launch_bounds__(64) void attention_kernel(const float *__restrict__ q, const float *__restrict__ k,
+                                                       const float *__restrict__ v, size_t v_row, int nq, int nk,
+                                                       int ah, int akv, float scale, float *__restrict__ out) {
+    extern __shared__ float sh[];  // q row (256), then the nk scores
+    const int h = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+    const int kh = h / (ah / akv);
+    float *qs = sh, *ps = sh + kAd;
+    *(float4_t *)(qs + lane * 4) = *(const float4_t *)(q + ((size_t)t * ah + h) * kAd + lane * 4);
+    __syncthreads();
+    float mx = -INFINITY;
+    for (int jj = lane; jj < nk; jj += 64) {
+        const float4_t *kr = (const float4_t *)(k + ((size_t)jj * akv + kh) * kAd);
+        float d0 = 0.0f, d1 = 0.0f;
+#pragma unroll 8
+        for (int u = 0; u < kAd / 4; u += 2) {
+            const float4_t a0 = kr[u], a1 = kr[u + 1];
+            const float4_t b0 = *(const float4_t *)(qs + 4 * u), b1 = *(const float4_t *)(qs + 4 * u + 4);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                d0 = __builtin_fmaf(a0[e], b0[e], d0);
+                d1 = __builtin_fmaf(a1[e], b1[e], d1);
+            }
+        }
+        const float s = (d0 + d1) * scale;
+        ps[jj] = s;
+        mx = fmaxf(mx, s);
+    }
+    mx = wave_max(mx);
+    float sum = 0.0f;
+    for (int jj = lane; jj < nk; jj += 64) {
+        const float p = expf(ps[jj] - mx);
+        ps[jj] = p;
+        sum += p;
+    }
+    sum = wave_sum(sum);
+    __syncthreads();
+    float4_t acc = {0.f, 0.f, 0.f, 0.f};
+    for (int jj = 0; jj < nk; jj++) {
+        const float p = ps[jj];
+        const float4_t vv = *(const float4_t *)(v + (size_t)jj * v_row + (size_t)kh * kAd + lane * 4);
+#pragma unroll
+        for (int e = 0; e < 4; e++) acc[e] = __builtin_fmaf(p, vv[e], acc[e]);
+    }
+    const float inv = 1.0f / sum;
+    *(float4_t *)(out + ((size_t)h * nq + t) * kAd + lane * 4) =
+        float4_t{acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
+}
+
+// out[t][h*256 + i] = heads[h][t][i] * sigmoid(z), z at zsrc + t*z_row + h*z_head + i
+__global__ void attention_gate_kernel(const float *__restrict__ heads, int n, int ah,
+                                      const float *__restrict__ zsrc, size_t z_row, int z_head,
+                                      float *__restrict__ out) {
+    const size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+    if (i >= (size_t)n * ah * kAd) return;
+    const int t = (int)(i / ((size_t)ah * kAd)), h = (int)((i / kAd) % ah), d = (int)(i % kAd);
+    const float z = zsrc[(size_t)t * z_row + (size_t)h * z_head + d];
+    out[i] = __fmul_rn(heads[((size_t)h * n + t) * kAd + d], sigmoid_ref(z));
+}
+
+// dst[r] = src[idx[r]], rows of `width` floats
+__global__ void gather_rows_kernel(const float *__restrict__ src, const int32_t *__restrict__ idx, int rows,
+                                   int width, float *__restrict__ dst) {
+    const size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+    if (i >= (size_t)rows * width) return;
+    const int r = (int)(i / width), c = (int)(i % width);
+    dst[i] = src[(size_t)idx[r] * width + c];
+}
+
+}  // namespace
+}  // namespace dz
+
+struct dz_pplx {
+    dz_pplx_config cfg{};
+    struct Layer {
+        bool attention = false;
+        float *input_norm = nullptr, *post_norm = nullptr;
+        dz_weight *qkv = nullptr, *z = nullptr, *a = nullptr, *b = nullptr, *out = nullptr;
+        float *conv = nullptr, *decay = nullptr, *dt = nullptr, *norm = nullptr;
+        dz_weight *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr;
+        float *qnorm = nullptr, *knorm = nullptr;
+        dz_weight *gate = nullptr, *up = nullptr, *down = nullptr;
+    };
+    std::vector<Layer> layers;
+    dz_weight *readout = nullptr;
+    float *final_norm = nullptr;
+    float *freq = nullptr;  // rotary frequencies [32]
+    // activations for `capacity` tokens
+    size_t capacity = 0;
+    std::vector<void *> buffers;
+    float *hidden = nullptr, *normed = nullptr, *wide = nullptr, *z = nullptr, *ab = nullptr, *conv_out = nullptr,
+          *qhat = nullptr, *khat = nullptr, *gb = nullptr, *heads = nullptr, *ctx = nullptr, *projected = nullptr,
+          *key = nullptr, *value = nullptr, *query = nullptr, *picked = nullptr, *gate = nullptr, *up = nullptr,
+          *logits = nullptr;
+    int8_t *codes = nullptr;
+    float *code_scales = nullptr;
+    int32_t *markers = nullptr;
+    uint8_t *rows_dev = nullptr;
+    dz::Weight rows_weight;
+};
+
+namespace dz {
+
+namespace {
+
+size_t conv_width(const dz_pplx_config &c) { return 2 * (size_t)c.delta_key_heads * kLd + (size_t)c.delta_heads * kLd; }
+
+void free_activations(dz_pplx *p) {
+    for (void *b : p->buffers) hipFree(b);
+    p->buffers.clear();
+    p->capacity = 0;
+}
+
+int32_t ensure_capacity(dz_ctx *ctx, dz_pplx *p, size_t n) {
+    if (p->capacity >= n) return DZ_OK;
+    hipStreamSynchronize(ctx_stream(ctx));
+    free_activations(p);
+    const dz_pplx_config &c = p->cfg;
+    const size_t d = c.hidden, cw = conv_width(c), lv = (size_t)c.delta_heads * kLd;
+    const size_t qw = 2 * (size_t)c.attn_heads * kAd, kvw = (size_t)c.attn_kv_heads * kAd;
+    const size_t wide = std::max(cw, qw), ctxw = std::max(lv, (size_t)c.attn_heads * kAd);
+    hipError_t err = hipSuccess;
+    auto get = [&](auto **ptr, size_t bytes) {
+        void *q = nullptr;
+        if (err == hipSuccess) err = hipMalloc(&q, bytes < 256 ? 256 : bytes);
+        if (err == hipSuccess) p->buffers.push_back(q);
+        *ptr = (std::remove_reference_t<decltype(**ptr)> *)q;
+    };
+    get(&p->hidden, n * d * 4);
+    get(&p->normed, n * d * 4);
+    get(&p->wide, n * wide * 4);
+    get(&p->z, n * lv * 4);
+    get(&p->ab, n * c.delta_heads * 2 * 4);
+    get(&p->conv_out, n * cw * 4);
+    get(&p->qhat, n * c.delta_key_heads * kLd * 4);
+    get(&p->khat, n * c.delta_key_heads * kLd * 4);
+    get(&p->gb, n * c.delta_heads * 2 * 4);
+    get(&p->heads, n * std::max(lv, (size_t)c.attn_heads * kAd) * 4);
+    get(&p->ctx, n * ctxw * 4);
+    get(&p->projected, n * d * 4);
+    get(&p->key, n * kvw * 4);
+    get(&p->value, n * kvw * 4);
+    get(&p->query, n * (size_t)c.attn_heads * kAd * 4);
+    get(&p->picked, n * d * 4);
+    get(&p->gate, n * (size_t)c.ff * 4);
+    get(&p->up, n * (size_t)c.ff * 4);
+    get(&p->codes, n * (size_t)c.ff);
+    get(&p->code_scales, n * (size_t)(c.ff / 64) * 4);
+    get(&p->markers, (size_t)DZ_READOUT_MAX_MARKERS * 4);
+    get(&p->logits, (size_t)DZ_READOUT_MAX_MARKERS * DZ_READOUT_CODES * 4);
+    get(&p->rows_dev, n * (d / 64) * 36);
+    Weight &w = p->rows_weight;
+    w.kind = WeightKind::Q4G64;
+    w.bits = 4;
+    w.group = 64;
+    w.rows = (int)n;
+    w.cols = (int)d;
+    w.groups = (int)(d / 64);
+    w.np = (int)((n + 15) / 16 * 16);
+    w.kp = (int)((d + 127) / 128 * 128);
+    w.code_bytes = (size_t)w.np * w.kp / 2;
+    w.scale_bytes = (size_t)w.np * (w.kp / 128) * 8;
+    get(&w.codes, w.code_bytes);
+    get(&w.scales, w.scale_bytes);
+    if (err != hipSuccess) {
+        free_activations(p);
+        return ctx_hip_fail(ctx, err, "pplx activations");
+    }
+    p->capacity = n;
+    return DZ_OK;
+}
+
+int32_t vec_upload(dz_ctx *ctx, float **dst, const float *src, size_t count) {
+    if (!*dst) {
+        hipError_t e = hipMalloc(dst, count * sizeof(float));
+        if (e != hipSuccess) return ctx_hip_fail(ctx, e, "pplx vector");
+    }
+    hipError_t e = hipMemcpyAsync(*dst, src, count * sizeof(float), hipMemcpyHostToDevice, ctx_stream(ctx));
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx_stream(ctx));
+    if (e != hipSuccess) return ctx_hip_fail(ctx, e, "pplx vector");
+    return DZ_OK;
+}
+
+bool starts(const std::string &s, const char *p, std::string *rest) {
+    size_t n = strlen(p);
+    if (s.compare(0, n, p) != 0) return false;
+    *rest = s.substr(n);
+    return true;
+}
+
+}  // namespace
+
+void pplx_destroy(dz_ctx *ctx, dz_pplx *p) {
+    if (!p) return;
+    hipStreamSynchronize(ctx_stream(ctx));
+    for (auto &l : p->layers) {
+        for (dz_weight *w : {l.qkv, l.z, l.a, l.b, l.out, l.q, l.k, l.v, l.o, l.gate, l.up, l.down}) weight_free(w);
+        for (float *f : {l.input_norm, l.post_norm, l.conv, l.decay, l.dt, l.norm, l.qnorm, l.knorm})
+            if (f) hipFree(f);
+    }
+    weight_free(p->readout);
+    for (float *f : {p->final_norm, p->freq})
+        if (f) hipFree(f);
+    free_activations(p);
+    delete p;
+}
+
+int32_t pplx_create(dz_ctx *ctx, const dz_pplx_config *cfg, dz_pplx **out) {
+    if (!cfg || !out) return ctx_fail(ctx, DZ_INVALID_REQUEST, "null pointer");
+    *out = nullptr;
+    const dz_pplx_config c = *cfg;
+    if (c.layers < 1 || c.hidden < 64 || c.hidden % 64 != 0 || c.ff < 64 || c.ff % 64 != 0 ||
+        c.delta_head_dim != kLd || c.attn_head_dim != kAd || c.delta_heads < 1 || c.delta_key_heads < 1 ||
+        c.delta_heads % c.delta_key_heads != 0 || c.attn_heads < 1 || c.attn_kv_heads < 1 ||
+        c.attn_heads % c.attn_kv_heads != 0 || c.delta_key_heads > 16)
+        return ctx_fail(ctx, DZ_INVALID_PARAMETERS,
+                        "pplx config: hidden and ff multiples of 64, delta head dim 128, attention head dim 256, "
+                        "heads divisible by their key heads, at most 16 delta key heads");
+    dz_pplx *p = new dz_pplx();
+    p->cfg = c;
+    p->layers.resize(c.layers);
+    for (int i = 0; i < c.layers; i++) p->layers[i].attention = i % 4 == 3;  // backbone.rs:132-136
+    // backbone.rs:227-229 inv_freq[i] = 1 / 1e7^(2i/64), in f32
+    float freq[32];
+    for (int i = 0; i < 32; i++) freq[i] = 1.0f / powf(10000000.0f, (float)(2 * i) / 64.0f);
+    int32_t rc = vec_upload(ctx, &p->freq, freq, 32);
+    if (rc) {
+        pplx_destroy(ctx, p);
+        return rc;
+    }
+    *out = p;
+    return DZ_OK;
+}
+
+int32_t pplx_set_weight(dz_ctx *ctx, dz_pplx *p, const char *name, const void *packed, size_t bytes, int32_t layout,
+                        size_t rows, size_t cols) {
+    if (!p || !name || !packed) return ctx_fail(ctx, DZ_INVALID_REQUEST, "null pointer");
+    if (layout != DZ_Q4_G64_F32 && layout != DZ_Q8_G64_F32)
+        return ctx_fail(ctx, DZ_INVALID_PARAMETERS, "pplx projections are group-64 packed matrices");
+    const dz_pplx_config &c = p->cfg;
+    const size_t d = c.hidden, cw = conv_width(c), lv = (size_t)c.delta_heads * kLd;
+    std::string s(name), rest;
+    dz_weight **slot = nullptr;
+    size_t want_r = 0, want_c = 0;
+    if (s == "readout") {
+        slot = &p->readout;
+        want_r = DZ_READOUT_CODES;
+        want_c = d;
+    } else if (starts(s, "language_model.layers.", &rest)) {
+        const size_t dot = rest.find('.');
+        const int i = dot == std::string::npos ? -1 : atoi(rest.substr(0, dot).c_str());
+        if (i < 0 || i >= c.layers || rest.substr(0, dot) != std::to_string(i))
+            return ctx_fail(ctx, DZ_INVALID_CHECKPOINT, "layer index out of range: " + s);
+        auto &L = p->layers[i];
+        const std::string t = rest.substr(dot + 1);
+        struct Slot {
+            const char *name;
+            bool attention;
+            dz_weight **w;
+            size_t r, c;
+        } slots[] = {
+            {"linear_attn.in_proj_qkv.weight", false, &L.qkv, cw, d},
+            {"linear_attn.in_proj_z.weight", false, &L.z, lv, d},
+            {"linear_attn.in_proj_a.weight", false, &L.a, (size_t)c.delta_heads, d},
+            {"linear_attn.in_proj_b.weight", false, &L.b, (size_t)c.delta_heads, d},
+            {"linear_attn.out_proj.weight", false, &L.out, d, lv},
+            {"self_attn.q_proj.weight", true, &L.q, 2 * (size_t)c.attn_heads * kAd, d},
+            {"self_attn.k_proj.weight", true, &L.k, (size_t)c.attn_kv_heads * kAd, d},
+            {"self_attn.v_proj.weight", true, &L.v, (size_t)c.attn_kv_heads * kAd, d},
+            {"self_attn.o_proj.weight", true, &L.o, d, (size_t)c.attn_heads * kAd},
+            {"mlp.gate_proj.weight", L.attention, &L.gate, (size_t)c.ff, d},
+            {"mlp.up_proj.weight", L.attention, &L.up, (size_t)c.ff, d},
+            {"mlp.down_proj.weight", L.attention, &L.down, d, (size_t)c.ff},
+        };
+        for (const Slot &sl : slots)
+            if (t == sl.name) {
+                if (sl.attention != L.attention) return ctx_fail(ctx, DZ_INVALID_CHECKPOINT, "unsupported layer layout: " + s);
+                slot = sl.w;
+                want_r = sl.r;
+                want_c = sl.c;
+            }
+    }
+    if (!slot) return ctx_fail(ctx, DZ_INVALID_CHECKPOINT, "unknown pplx tensor: " + s);
+    if (rows != want_r || cols != want_c) return ctx_fail(ctx, DZ_INVALID_CHECKPOINT, "tensor shape mismatch: " + s);
+    dz_weight *w = nullptr;
+    int32_t rc = weight_upload(ctx, packed, bytes, layout, rows, cols, &w);
+    if (rc) return rc;
+    weight_free(*slot);
+    *slot = w;
+    return DZ_OK;
+}
+
+int32_t pplx_set_vector(dz_ctx *ctx, dz_pplx *p, const char *name, const float *values, size_t count) {
+    if (!p || !name || !values) return ctx_fail(ctx, DZ_INVALID_REQUEST, "null pointer");
+    const dz_pplx_config &c = p->cfg;
+    const size_t d = c.hidden, cw = conv_width(c);
+    std::string s(name), rest;
+    if (s == "language_model.norm.weight") {
+        if (count != d) return ctx_fail(ctx, DZ_INVALID_CHECKPOINT, "tensor shape mismatch: " + s);
+        return vec_upload(ctx, &p->final_norm, values, count);
+    }
+    if (!starts(s, "language_model.layers.", &rest)) return ctx_fail(ctx, DZ_INVALID_CHECKPOINT, "unknown pplx tensor: " + s);
+    const size_t dot = rest.find('.');
+    const int i = dot == std::string::npos ? -1 : atoi(rest.substr(0, dot).c_str());
+    if (i < 0 || i >= c.layers || rest.substr(0, dot) != std::to_string(i))
+        return ctx_fail(ctx, DZ_INVALID_CHECKPOINT, "layer index out of range: " + s);
+    auto &L = p->layers[i];
+    const std::string t = rest.substr(dot + 1);
+    auto need = [&](bool attention, size_t n) { return L.attention == attention && count == n; };
+    if (t == "input_layernorm.weight" && count == d) return vec_upload(ctx, &L.input_norm, values, count);
+    if (t == "post_attention_layernorm.weight" && count == d) return vec_upload(ctx, &L.post_norm, values, count);
+    if (t == "linear_attn.conv1d.weight" && need(false, cw * 4)) {
+        // conv1d.weight [width, 1, 4] -> tap-major [4 x width] (backbone.rs:170-178)
+        std::vector<float> packed(4 * cw);
+        for (size_t tap = 0; tap < 4; tap++)
+            for (size_t ch = 0; ch < cw; ch++) packed[tap * cw + ch] = values[ch * 4 + tap];
+        return vec_upload(ctx, &L.conv, packed.data(), packed.size());
+    }
+    if (t == "linear_attn.A_log" && need(false, (size_t)c.delta_heads)) {
+        std::vector<float> decay(values, values + count);
+        for (float &v : decay) v = expf(v);  // backbone.rs:179-183
+        return vec_upload(ctx, &L.decay, decay.data(), count);
+    }
+    if (t == "linear_attn.dt_bias" && need(false, (size_t)c.delta_heads)) return vec_upload(ctx, &L.dt, values, count);
+    if (t == "linear_attn.norm.weight" && need(false, kLd)) return vec_upload(ctx, &L.norm, values, count);
+    if (t == "self_attn.q_norm.weight" && need(true, kAd)) return vec_upload(ctx, &L.qnorm, values, count);
+    if (t == "self_attn.k_norm.weight" && need(true, kAd)) return vec_upload(ctx, &L.knorm, values, count);
+    return ctx_fail(ctx, DZ_INVALID_CHECKPOINT, "unknown pplx tensor or shape: " + s);
+}
+
+namespace {
+
+bool complete(const dz_pplx *p, std::string *missing) {
+    for (size_t i = 0; i < p->layers.size(); i++) {
+        const auto &L = p->layers[i];
+        bool ok = L.input_norm && L.post_norm && L.gate && L.up && L.down;
+        ok = ok && (L.attention ? (L.q && L.k && L.v && L.o && L.qnorm && L.knorm)
+                                : (L.qkv && L.z && L.a && L.b && L.out && L.conv && L.decay && L.dt && L.norm));
+        if (!ok) {
+            *missing = "layer " + std::to_string(i);
+            return false;
+        }
+    }
+    if (!p->readout || !p->final_norm) {
+        *missing = "readout or final norm";
+        return false;
+    }
+    return true;
+}
+
+// dz_linear_pair / dz_linear / the MLP, on the context's stream
+int32_t linear(dz_ctx *ctx, const dz_weight *w, const float *x, size_t m, float *y) {
+    return dz_linear(ctx, w, x, DZ_F32, m, y, DZ_W4A8);
+}
+
+// backbone.rs:232-250: post-norm MLP with residual, in place on hidden
+int32_t mlp(dz_ctx *ctx, dz_pplx *p, const dz_pplx::Layer &L, size_t n) {
+    const dz_pplx_config &c = p->cfg;
+    hipStream_t s = ctx_stream(ctx);
+    launch_readout_rms(p->hidden, 0, nullptr, (int)n, c.hidden, L.post_norm, 1e-6f, 1, p->normed, s);
+    int32_t rc;
+    if (weight_of(L.gate).kind == WeightKind::Q4G64 && weight_of(L.up).kind == WeightKind::Q4G64) {
+        // gate/up, silu(gate)*up and the A8 codes of the down projection in one pass
+        rc = dz_mlp_requant(ctx, L.gate, L.up, p->normed, n, p->codes, p->code_scales);
+        if (!rc) rc = dz_linear_q8(ctx, L.down, p->codes, p->code_scales, n, p->projected);
+    } else {
+        rc = dz_linear_pair(ctx, L.gate, L.up, p->normed, n, p->gate, p->up, DZ_W4A8);
+        if (!rc) launch_silu_mul(p->gate, p->up, n * (size_t)c.ff, s);
+        if (!rc) rc = linear(ctx, L.down, p->gate, n, p->projected);
+    }
+    if (rc) return rc;
+    launch_add(p->hidden, p->projected, 0, n * (size_t)c.hidden, s);
+    return DZ_OK;
+}
+
+int32_t delta_layer(dz_ctx *ctx, dz_pplx *p, const dz_pplx::Layer &L, size_t n) {
+    const dz_pplx_config &c = p->cfg;
+    hipStream_t s = ctx_stream(ctx);
+    const size_t cw = conv_width(c), lh = c.delta_heads;
+    launch_readout_rms(p->hidden, 0, nullptr, (int)n, c.hidden, L.input_norm, 1e-6f, 1, p->normed, s);
+    int32_t rc = dz_linear_pair(ctx, L.qkv, L.z, p->normed, n, p->wide, p->z, DZ_W4A8);
+    if (!rc) rc = dz_linear_pair(ctx, L.a, L.b, p->normed, n, p->ab, p->ab + n * lh, DZ_W4A8);
+    if (rc) return rc;
+    hipLaunchKernelGGL(conv_silu_kernel, dim3(blocks_of(n * cw, 256)), dim3(256), 0, s, p->wide, (int)n, (int)cw,
+                       L.conv, p->conv_out);
+    hipLaunchKernelGGL(delta_prep_kernel, dim3((unsigned)n), dim3(64 * c.delta_key_heads), 0, s, p->conv_out,
+                       c.delta_heads, c.delta_key_heads, p->ab, p->ab + n * lh, L.decay, L.dt, p->qhat, p->khat,
+                       p->gb);
+    hipLaunchKernelGGL(delta_scan_kernel, dim3(c.delta_heads, kLd / 16), dim3(64), 0, s, p->qhat, p->khat,
+                       p->conv_out, p->gb, (int)n, c.delta_heads, c.delta_key_heads, p->heads);
+    hipLaunchKernelGGL(delta_gate_kernel, dim3((unsigned)n, c.delta_heads), dim3(64), 0, s, p->heads, (int)n,
+                       c.delta_heads, L.norm, p->z, p->ctx);
+    rc = linear(ctx, L.out, p->ctx, n, p->projected);
+    if (rc) return rc;
+    launch_add(p->hidden, p->projected, 0, n * (size_t)c.hidden, s);
+    return DZ_OK;
+}
+
+// backbone.rs:471-615; with `markers` (count rows) the queries and the
+// hidden rows are cut to the markers (the reference's prune_last).
+int32_t attention_layer(dz_ctx *ctx, dz_pplx *p, const dz_pplx::Layer &L, size_t n, const int32_t *markers,
+                        size_t count, size_t *rows_out) {
+    const dz_pplx_config &c = p->cfg;
+    hipStream_t s = ctx_stream(ctx);
+    const size_t d = c.hidden, kvw = (size_t)c.attn_kv_heads * kAd, qw = 2 * (size_t)c.attn_heads * kAd;
+    launch_readout_rms(p->hidden, 0, nullptr, (int)n, c.hidden, L.input_norm, 1e-6f, 1, p->normed, s);
+    int32_t rc = dz_linear_pair(ctx, L.k, L.v, p->normed, n, p->key, p->value, DZ_W4A8);
+    if (rc) return rc;
+    const size_t nq = markers ? count : n;
+    const float *qin = p->normed;
+    if (markers) {
+        hipLaunchKernelGGL(gather_rows_kernel, dim3(blocks_of(count * d, 256)), dim3(256), 0, s, p->normed, markers,
+                           (int)count, (int)d, p->picked);
+        qin = p->picked;
+    }
+    rc = linear(ctx, L.q, qin, nq, p->wide);
+    if (rc) return rc;
+    // queries: [q | z] per head; keys in place
+    hipLaunchKernelGGL(head_norm_rope_kernel, dim3((unsigned)nq, c.attn_heads), dim3(64), 0, s, p->wide, qw, 2 * kAd,
+                       c.attn_heads, L.qnorm, markers, p->freq, p->query);
+    hipLaunchKernelGGL(head_norm_rope_kernel, dim3((unsigned)n, c.attn_kv_heads), dim3(64), 0, s, p->key, kvw, kAd,
+                       c.attn_kv_heads, L.knorm, nullptr, p->freq, p->key);
+    const size_t lds = (kAd + n) * sizeof(float);
+    hipLaunchKernelGGL(attention_kernel, dim3(c.attn_heads, (unsigned)nq), dim3(64), lds, s, p->query, p->key,
+                       p->value, kvw, (int)nq, (int)n, c.attn_heads, c.attn_kv_heads, 1.0f / 16.0f, p->heads);
+    hipLaunchKernelGGL(attention_gate_kernel, dim3(blocks_of(nq * c.attn_heads * kAd, 256)), dim3(256), 0, s,
+                       p->heads, (int)nq, c.attn_heads, p->wide + kAd, qw, 2 * kAd, p->ctx);
+    rc = linear(ctx, L.o, p->ctx, nq, p->projected);
+    if (rc) return rc;
+    if (markers) {
+        hipLaunchKernelGGL(gather_rows_kernel, dim3(blocks_of(count * d, 256)), dim3(256), 0, s, p->hidden, markers,
+                           (int)count, (int)d, p->picked);
+        hipError_t e = hipMemcpyAsync(p->hidden, p->picked, count * d * sizeof(float), hipMemcpyDeviceToDevice, s);
+        if (e != hipSuccess) return ctx_hip_fail(ctx, e, "pplx prune");
+    }
+    launch_add(p->hidden, p->projected, 0, nq * d, s);
+    *rows_out = nq;
+    return DZ_OK;
+}
+
+}  // namespace
+
+// Layer `index` on hidden rows already in p->hidden (tests and the forward).
+int32_t pplx_run_layer(dz_ctx *ctx, dz_pplx *p, int index, size_t n, const int32_t *markers, size_t count,
+                       size_t *rows_out) {
+    const auto &L = p->layers[index];
+    int32_t rc;
+    size_t rows = n;
+    if (L.attention) {
+        rc = attention_layer(ctx, p, L, n, markers, count, &rows);
+    } else {
+        rc = delta_layer(ctx, p, L, n);
+    }
+    if (rc) return rc;
+    rc = mlp(ctx, p, L, rows);
+    if (rc) return rc;
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return ctx_hip_fail(ctx, e, "pplx layer");
+    *rows_out = rows;
+    return DZ_OK;
+}
+
+int32_t pplx_layer(dz_ctx *ctx, dz_pplx *p, int index, float *hidden, size_t n, const int32_t *markers_host,
+                   size_t count) {
+    if (!p || !hidden) return ctx_fail(ctx, DZ_INVALID_REQUEST, "null pointer");
+    if (index < 0 || index >= p->cfg.layers) return ctx_fail(ctx, DZ_INVALID_REQUEST, "layer index out of range");
+    if (n == 0 || n > (size_t)kMaxKeys) return ctx_fail(ctx, DZ_INPUT_TOO_LONG, "sequence length outside 1..8192");
+    std::string missing;
+    if (!complete(p, &missing)) return ctx_fail(ctx, DZ_INVALID_CHECKPOINT, "missing pplx weights: " + missing);
+    const auto &L = p->layers[index];
+    if (markers_host && !L.attention) return ctx_fail(ctx, DZ_INVALID_REQUEST, "cannot prune a recurrent layer");
+    if (markers_host && (count == 0 || count > (size_t)DZ_READOUT_MAX_MARKERS))
+        return ctx_fail(ctx, DZ_INVALID_REQUEST, "marker count outside 1..256");
+    for (size_t i = 0; markers_host && i < count; i++)
+        if (markers_host[i] < 0 || (size_t)markers_host[i] >= n)
+            return ctx_fail(ctx, DZ_INVALID_REQUEST, "readout marker outside the sequence");
+    int32_t rc = ensure_capacity(ctx, p, n);
+    if (rc) return rc;
+    hipStream_t s = ctx_stream(ctx);
+    const size_t d = p->cfg.hidden;
+    hipError_t e = hipMemcpyAsync(p->hidden, hidden, n * d * 4, hipMemcpyDeviceToDevice, s);
+    if (e == hipSuccess && markers_host)
+        e = hipMemcpyAsync(p->markers, markers_host, count * 4, hipMemcpyHostToDevice, s);
+    if (e != hipSuccess) return ctx_hip_fail(ctx, e, "pplx layer input");
+    size_t rows = n;
+    rc = pplx_run_layer(ctx, p, index, n, markers_host ? p->markers : nullptr, count, &rows);
+    if (rc) return rc;
+    e = hipMemcpyAsync(hidden, p->hidden, rows * d * 4, hipMemcpyDeviceToDevice, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return ctx_hip_fail(ctx, e, "pplx layer output");
+    return DZ_OK;
+}
+
+int32_t pplx_forward_rows(dz_ctx *ctx, dz_pplx *p, const void *rows_host, size_t n, const int32_t *markers,
+                          size_t count, float *logits_host) {
+    if (!p || !rows_host || !markers || !logits_host) return ctx_fail(ctx, DZ_INVALID_REQUEST, "null pointer");
+    if (n == 0 || n > (size_t)kMaxKeys) return ctx_fail(ctx, DZ_INPUT_TOO_LONG, "sequence length outside 1..8192");
+    if (count == 0 || count > (size_t)DZ_READOUT_MAX_MARKERS)
+        return ctx_fail(ctx, DZ_INVALID_REQUEST, "marker count outside 1..256");
+    for (size_t i = 0; i < count; i++)
+        if (markers[i] < 0 || (size_t)markers[i] >= n)
+            return ctx_fail(ctx, DZ_INVALID_REQUEST, "readout marker outside the sequence");
+    std::string missing;
+    if (!complete(p, &missing)) return ctx_fail(ctx, DZ_INVALID_CHECKPOINT, "missing pplx weights: " + missing);
+    int32_t rc = ensure_capacity(ctx, p, n);
+    if (rc) return rc;
+    hipStream_t s = ctx_stream(ctx);
+    const size_t d = p->cfg.hidden;
+    // embedding rows: the packed wire rows, unpacked exactly (packed.rs:59-73)
+    hipError_t e = hipMemcpyAsync(p->rows_dev, rows_host, n * (d / 64) * 36, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = hipMemcpyAsync(p->markers, markers, count * 4, hipMemcpyHostToDevice, s);
+    if (e != hipSuccess) return ctx_hip_fail(ctx, e, "pplx input upload");
+    p->rows_weight.rows = (int)n;
+    int bad = 0;
+    launch_fill_i32(ctx_flag(ctx), 0, 1, s);
+    launch_upload(p->rows_weight, p->rows_dev, ctx_flag(ctx), s);
+    launch_dequant(p->rows_weight, nullptr, (int)n, p->hidden, 0, s);
+    e = hipMemcpyAsync(&bad, ctx_flag(ctx), sizeof(int), hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return ctx_hip_fail(ctx, e, "pplx input upload");
+    if (bad) return ctx_fail(ctx, DZ_INVALID_CHECKPOINT, "invalid packed scale");
+    size_t rows = n;
+    const int last = p->cfg.layers - 1;
+    const bool prune = p->layers[last].attention;  // mod.rs prune_last (a recurrent last layer is not cut)
+    for (int i = 0; i < p->cfg.layers; i++) {
+        rc = pplx_run_layer(ctx, p, i, rows, prune && i == last ? p->markers : nullptr, count, &rows);
+        if (rc) return rc;
+    }
+    // backbone.rs:247-249: the hidden state stays finite
+    launch_fill_i32(ctx_flag(ctx), 0, 1, s);
+    launch_flag_nonfinite(p->hidden, rows * d, ctx_flag(ctx), 1, s);
+    e = hipMemcpyAsync(&bad, ctx_flag(ctx), sizeof(int), hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return ctx_hip_fail(ctx, e, "pplx forward");
+    if (bad) return ctx_fail(ctx, DZ_INFERENCE_FAILED, "non-finite hidden state");
+    // mod.rs:149-185: rows are the markers' (pruned) or selected here
+    const int32_t *select = prune ? nullptr : p->markers;
+    rc = ctx_readout_rows(ctx, weight_of(p->readout), p->final_norm, p->hidden, 0, select, count, DZ_READOUT_EPS,
+                          p->logits);
+    if (rc) return rc;
+    e = hipMemcpyAsync(logits_host, p->logits, count * (size_t)DZ_READOUT_CODES * 4, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return ctx_hip_fail(ctx, e, "logits readback");
+    return DZ_OK;
+}
+
+}  // namespace dz

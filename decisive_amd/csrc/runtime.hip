@@ -49,6 +49,15 @@ int32_t encoder_set_readout(dz_ctx *ctx, dz_encoder *e, const void *packed, size
                             const float *norm_host);
 int32_t encoder_readout(dz_ctx *ctx, dz_encoder *e, const void *rows_host, size_t seq, const int32_t *markers,
                         size_t count, float *logits_host);
+int32_t pplx_create(dz_ctx *ctx, const dz_pplx_config *cfg, dz_pplx **out);
+void pplx_destroy(dz_ctx *ctx, dz_pplx *p);
+int32_t pplx_set_weight(dz_ctx *ctx, dz_pplx *p, const char *name, const void *packed, size_t bytes, int32_t layout,
+                        size_t rows, size_t cols);
+int32_t pplx_set_vector(dz_ctx *ctx, dz_pplx *p, const char *name, const float *values, size_t count);
+int32_t pplx_layer(dz_ctx *ctx, dz_pplx *p, int index, float *hidden, size_t n, const int32_t *markers_host,
+                   size_t count);
+int32_t pplx_forward_rows(dz_ctx *ctx, dz_pplx *p, const void *rows_host, size_t n, const int32_t *markers,
+                          size_t count, float *logits_host);
 int32_t encoder_forward(dz_ctx *ctx, dz_encoder *enc, const int32_t *ids_dev, const void *rows_host,
                         size_t batch, size_t seq, float *out);
 int32_t tune(dz_ctx *ctx, uint32_t budget_ms, const char *cache_in, char *cache_out, size_t cap);
@@ -790,6 +799,40 @@ int32_t dz_encoder_readout_rows(dz_ctx *ctx, dz_encoder *enc, const void *rows, 
                                 const int32_t *markers, size_t count, float *logits) {
     DZ_BEGIN(ctx);
     return dz::encoder_readout(ctx, enc, rows, seq, markers, count, logits);
+}
+
+// ---- the Pplx decider ---------------------------------------------------------------
+
+int32_t dz_pplx_create(dz_ctx *ctx, const dz_pplx_config *cfg, dz_pplx **out) {
+    DZ_BEGIN(ctx);
+    return dz::pplx_create(ctx, cfg, out);
+}
+
+void dz_pplx_destroy(dz_ctx *ctx, dz_pplx *model) {
+    if (ctx && model) dz::pplx_destroy(ctx, model);
+}
+
+int32_t dz_pplx_set_weight(dz_ctx *ctx, dz_pplx *model, const char *name, const void *packed, size_t bytes,
+                           int32_t layout, size_t rows, size_t cols) {
+    DZ_BEGIN(ctx);
+    return dz::pplx_set_weight(ctx, model, name, packed, bytes, layout, rows, cols);
+}
+
+int32_t dz_pplx_set_vector(dz_ctx *ctx, dz_pplx *model, const char *name, const float *values, size_t count) {
+    DZ_BEGIN(ctx);
+    return dz::pplx_set_vector(ctx, model, name, values, count);
+}
+
+int32_t dz_pplx_layer(dz_ctx *ctx, dz_pplx *model, int32_t layer, float *hidden, size_t n, const int32_t *markers,
+                      size_t count) {
+    DZ_BEGIN(ctx);
+    return dz::pplx_layer(ctx, model, layer, hidden, n, markers, count);
+}
+
+int32_t dz_pplx_forward_rows(dz_ctx *ctx, dz_pplx *model, const void *rows, size_t n, const int32_t *markers,
+                             size_t count, float *logits) {
+    DZ_BEGIN(ctx);
+    return dz::pplx_forward_rows(ctx, model, rows, n, markers, count, logits);
 }
 
 // ---- tuner ---------------------------------------------------------------------------

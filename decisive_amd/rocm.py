@@ -44,6 +44,13 @@ class EncoderConfig(ctypes.Structure):
                 ("ln_eps", ctypes.c_float)]
 
 
+class PplxConfig(ctypes.Structure):
+    _fields_ = [("layers", ctypes.c_int32), ("hidden", ctypes.c_int32), ("ff", ctypes.c_int32),
+                ("delta_heads", ctypes.c_int32), ("delta_key_heads", ctypes.c_int32),
+                ("delta_head_dim", ctypes.c_int32), ("attn_heads", ctypes.c_int32),
+                ("attn_kv_heads", ctypes.c_int32), ("attn_head_dim", ctypes.c_int32)]
+
+
 _lib = None
 
 P, SZ, I32, U32, U64, F = (ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int32, ctypes.c_uint32,
@@ -102,6 +109,12 @@ _SIGNATURES = {
     "dz_encoder_readout_params": (I32, [P, PP, PP]),
     "dz_encoder_readout_rows": (I32, [P, P, P, SZ, P, SZ, P]),
     "dz_encoder_set_readout": (I32, [P, P, P, SZ, I32, P]),
+    "dz_pplx_create": (I32, [P, ctypes.POINTER(PplxConfig), PP]),
+    "dz_pplx_destroy": (None, [P, P]),
+    "dz_pplx_set_weight": (I32, [P, P, ctypes.c_char_p, P, SZ, I32, SZ, SZ]),
+    "dz_pplx_set_vector": (I32, [P, P, ctypes.c_char_p, P, SZ]),
+    "dz_pplx_layer": (I32, [P, P, I32, P, SZ, P, SZ]),
+    "dz_pplx_forward_rows": (I32, [P, P, P, SZ, P, SZ, P]),
     "dz_tune": (I32, [P, U32, ctypes.c_char_p, ctypes.c_char_p, SZ]),
     "dz_select_variant": (I32, [P, ctypes.c_char_p, ctypes.c_char_p]),
 }
@@ -315,6 +328,12 @@ class Context:
         self._check(load().dz_encoder_create_random(self.handle, ctypes.byref(cfg), seed, ctypes.byref(h)))
         return Encoder(self, h.value, cfg)
 
+    # ---- the Pplx decider ----
+    def pplx_create(self, cfg: PplxConfig) -> "Pplx":
+        h = ctypes.c_void_p()
+        self._check(load().dz_pplx_create(self.handle, ctypes.byref(cfg), ctypes.byref(h)))
+        return Pplx(self, h.value, cfg)
+
     # ---- tuner ----
     def tune(self, budget_ms: int, cache: str | None = None) -> dict:
         out = ctypes.create_string_buffer(1 << 16)
@@ -392,4 +411,44 @@ class Encoder:
     def close(self):
         if self.handle:
             load().dz_encoder_destroy(self.ctx.handle, self.handle)
+            self.handle = 0
+
+
+class Pplx:
+    """dz_pplx: the Pplx decider (hybrid gated-delta / attention decoder)."""
+
+    def __init__(self, ctx: Context, handle: int, cfg: PplxConfig):
+        self.ctx, self.handle, self.cfg = ctx, handle, cfg
+
+    def set_weight(self, name: str, packed, layout: int, rows: int, cols: int):
+        import numpy as np
+        packed = np.ascontiguousarray(packed, dtype=np.uint8)
+        self.ctx._check(load().dz_pplx_set_weight(self.ctx.handle, self.handle, name.encode(), packed.ctypes.data,
+                                                  packed.size, layout, rows, cols))
+
+    def set_vector(self, name: str, values):
+        import numpy as np
+        values = np.ascontiguousarray(values, dtype=np.float32).ravel()
+        self.ctx._check(load().dz_pplx_set_vector(self.ctx.handle, self.handle, name.encode(), values.ctypes.data,
+                                                  values.size))
+
+    def layer(self, index: int, hidden_dev, n: int, markers=None):
+        import numpy as np
+        m = None if markers is None else np.ascontiguousarray(markers, dtype=np.int32)
+        self.ctx._check(load().dz_pplx_layer(self.ctx.handle, self.handle, index, _addr(hidden_dev), n,
+                                             None if m is None else m.ctypes.data, 0 if m is None else m.size))
+
+    def forward_rows(self, rows_host, n: int, markers):
+        """Logits f32 [len(markers) x 255]."""
+        import numpy as np
+        rows_host = np.ascontiguousarray(rows_host, dtype=np.uint8)
+        m = np.ascontiguousarray(markers, dtype=np.int32)
+        out = np.empty((m.size, 255), np.float32)
+        self.ctx._check(load().dz_pplx_forward_rows(self.ctx.handle, self.handle, rows_host.ctypes.data, n,
+                                                    m.ctypes.data, m.size, out.ctypes.data))
+        return out
+
+    def close(self):
+        if self.handle:
+            load().dz_pplx_destroy(self.ctx.handle, self.handle)
             self.handle = 0

@@ -317,6 +317,50 @@ int32_t dz_encoder_set_readout(dz_ctx *ctx, dz_encoder *enc, const void *packed_
 int32_t dz_encoder_readout_rows(dz_ctx *ctx, dz_encoder *enc, const void *rows_host, size_t seq,
                                 const int32_t *markers_host, size_t count, float *logits_host);
 
+/* ---- the Pplx decider (src/models/pplx_flash: backbone.rs, mod.rs, native.rs) ---- */
+
+typedef struct dz_pplx dz_pplx;
+typedef struct dz_pplx_config {
+    int32_t layers;          /* 32 (backbone.rs: layer i is full attention when i % 4 == 3) */
+    int32_t hidden;          /* 2560 (D) */
+    int32_t ff;              /* 9216 (FF) */
+    int32_t delta_heads;     /* 32 (LH) */
+    int32_t delta_key_heads; /* 16 (LK), at most 16 */
+    int32_t delta_head_dim;  /* 128 (LD), fixed */
+    int32_t attn_heads;      /* 16 (AH) */
+    int32_t attn_kv_heads;   /* 4 (KV / AD) */
+    int32_t attn_head_dim;   /* 256 (AD), fixed */
+} dz_pplx_config;
+
+/* An empty model of the given shape; weights arrive by name. */
+int32_t dz_pplx_create(dz_ctx *ctx, const dz_pplx_config *cfg, dz_pplx **out);
+void dz_pplx_destroy(dz_ctx *ctx, dz_pplx *model);
+/* A packed projection by its checkpoint name (export_packed.rs:44-64 stores
+ * every 2-D tensor this way): "language_model.layers.<i>.<linear_attn|
+ * self_attn|mlp>.<proj>.weight" or "readout" (DZ_READOUT_CODES x hidden);
+ * rows x cols as the checkpoint lists them. Synchronous upload, validated as
+ * dz_weight_upload. An unknown name or shape is DZ_INVALID_CHECKPOINT. */
+int32_t dz_pplx_set_weight(dz_ctx *ctx, dz_pplx *model, const char *name, const void *packed_host,
+                           size_t bytes, int32_t layout, size_t rows, size_t cols);
+/* A vector by its checkpoint name, as f32 values in the checkpoint's order:
+ * the layer norms, linear_attn.conv1d.weight ([width, 1, 4]), A_log, dt_bias,
+ * linear_attn.norm.weight, self_attn.q_norm / k_norm, language_model.norm.weight. */
+int32_t dz_pplx_set_vector(dz_ctx *ctx, dz_pplx *model, const char *name, const float *values_host,
+                           size_t count);
+/* One decoder layer (backbone.rs:207-250) in place on hidden_dev f32
+ * [n x hidden]. With markers_host (an attention layer only) the layer keeps
+ * the marker rows, in marker order (prune_last). */
+int32_t dz_pplx_layer(dz_ctx *ctx, dz_pplx *model, int32_t layer, float *hidden_dev, size_t n,
+                      const int32_t *markers_host, size_t count);
+/* native.rs:193-274 for one chunk: packed embedding rows (rows_host, n rows
+ * of the group-64 wire layout), every layer (the last one cut to the
+ * markers when it is an attention layer), the final zero-centred RMSNorm
+ * and the packed readout of the marker rows: logits_host f32
+ * [count x DZ_READOUT_CODES]. n <= 8192. Synchronous; a non-finite hidden
+ * state is DZ_INFERENCE_FAILED "non-finite hidden state" (backbone.rs:247). */
+int32_t dz_pplx_forward_rows(dz_ctx *ctx, dz_pplx *model, const void *rows_host, size_t n,
+                             const int32_t *markers_host, size_t count, float *logits_host);
+
 /* ---- kernel tuner (webgpu/checkpoint.rs:95-294, 428-652) ------------------------ */
 
 /* Times the tile variants of every tuned kernel family at the reference's

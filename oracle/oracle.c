@@ -727,3 +727,141 @@ void or_silu_requant(const float *gate, const float *up, size_t m, size_t n, int
         }
     }
 }
+
+/* ---- Pplx decoder layer ops ---- */
+
+static float sigmoidf_ref(float v) { return 1.0f / (1.0f + expf(-v)); }
+
+void or_conv_silu(const float *x, size_t n, size_t width, const float *w, float *out) {
+    for (size_t t = 0; t < n; t++)
+        for (size_t c = 0; c < width; c++) {
+            float sum = 0.0f;
+            for (size_t tap = 0; tap < 4; tap++) {
+                const long row = (long)t - 3 + (long)tap;
+                const float v = row < 0 ? 0.0f : x[(size_t)row * width + c];
+                sum = sum + v * w[tap * width + c];
+            }
+            out[t * width + c] = silu(sum);
+        }
+}
+
+void or_delta_scan(const float *conv, size_t n, int lh, int lk, int ld, const float *a, const float *b,
+                   const float *decay, const float *dt, float *out) {
+    const size_t lkv = (size_t)lk * ld, width = 2 * lkv + (size_t)lh * ld;
+    const int group = lh / lk;
+    float *state = (float *)calloc((size_t)ld * ld, sizeof(float));
+    float *q = (float *)malloc(ld * sizeof(float)), *k = (float *)malloc(ld * sizeof(float));
+    float *memory = (float *)malloc(ld * sizeof(float)), *delta = (float *)malloc(ld * sizeof(float));
+    for (int h = 0; h < lh; h++) {
+        memset(state, 0, (size_t)ld * ld * sizeof(float));
+        const int kh = h / group;
+        for (size_t t = 0; t < n; t++) {
+            const float *row = conv + t * width;
+            memcpy(q, row + (size_t)kh * ld, ld * sizeof(float));
+            memcpy(k, row + lkv + (size_t)kh * ld, ld * sizeof(float));
+            float qs = 0.0f, ks = 0.0f;
+            for (int i = 0; i < ld; i++) qs = qs + q[i] * q[i];
+            for (int i = 0; i < ld; i++) ks = ks + k[i] * k[i];
+            const float qi = 1.0f / sqrtf(qs + 1e-6f), ki = 1.0f / sqrtf(ks + 1e-6f);
+            const float root = 1.0f / sqrtf((float)ld);
+            for (int i = 0; i < ld; i++) {
+                q[i] = (q[i] * qi) * root;
+                k[i] = k[i] * ki;
+            }
+            const float x = a[t * lh + h] + dt[h];
+            const float softplus = x > 20.0f ? x : log1pf(expf(x));
+            const float g = expf(-decay[h] * softplus);
+            const float beta = sigmoidf_ref(b[t * lh + h]);
+            for (int j = 0; j < ld; j++) memory[j] = 0.0f;
+            for (int i = 0; i < ld; i++)
+                for (int j = 0; j < ld; j++) {
+                    state[i * ld + j] = state[i * ld + j] * g;
+                    memory[j] = memory[j] + state[i * ld + j] * k[i];
+                }
+            const float *v = row + 2 * lkv + (size_t)h * ld;
+            for (int j = 0; j < ld; j++) delta[j] = (v[j] - memory[j]) * beta;
+            float *dst = out + ((size_t)h * n + t) * ld;
+            for (int j = 0; j < ld; j++) dst[j] = 0.0f;
+            for (int i = 0; i < ld; i++)
+                for (int j = 0; j < ld; j++) {
+                    state[i * ld + j] = state[i * ld + j] + k[i] * delta[j];
+                    dst[j] = dst[j] + state[i * ld + j] * q[i];
+                }
+        }
+    }
+    free(state);
+    free(q);
+    free(k);
+    free(memory);
+    free(delta);
+}
+
+void or_delta_gate(const float *heads, size_t n, int lh, int ld, const float *norm, const float *z,
+                   float *ctx) {
+    for (size_t t = 0; t < n; t++)
+        for (int h = 0; h < lh; h++) {
+            const float *src = heads + ((size_t)h * n + t) * ld;
+            float ss = 0.0f;
+            for (int i = 0; i < ld; i++) ss = ss + src[i] * src[i];
+            const float scale = 1.0f / sqrtf(ss / (float)ld + 1e-6f);
+            for (int i = 0; i < ld; i++) {
+                const size_t at = t * (size_t)lh * ld + (size_t)h * ld + i;
+                ctx[at] = ((src[i] * scale) * norm[i]) * silu(z[at]);
+            }
+        }
+}
+
+void or_rope(float *x, size_t rows, int heads, int ad, const size_t *pos, const float *freq) {
+    for (size_t r = 0; r < rows; r++)
+        for (int h = 0; h < heads; h++) {
+            float *head = x + (r * heads + h) * (size_t)ad;
+            for (int i = 0; i < 32; i++) {
+                const float angle = (float)pos[r] * freq[i];
+                const float c = cosf(angle), sn = sinf(angle);
+                const float a = head[i], b = head[i + 32];
+                head[i] = a * c - b * sn;
+                head[i + 32] = b * c + a * sn;
+            }
+        }
+}
+
+void or_attention_gqa(const float *q, const float *k, const float *v, size_t nq, size_t nk, int ah, int akv,
+                      int ad, float scale, float *out) {
+    const int group = ah / akv;
+    double *p = (double *)malloc(nk * sizeof(double));
+    for (int h = 0; h < ah; h++) {
+        const int kh = h / group;
+        for (size_t t = 0; t < nq; t++) {
+            const float *qr = q + (t * ah + h) * (size_t)ad;
+            double mx = -INFINITY;
+            for (size_t j = 0; j < nk; j++) {
+                const float *kr = k + (j * akv + kh) * (size_t)ad;
+                double d = 0.0;
+                for (int i = 0; i < ad; i++) d += (double)qr[i] * kr[i];
+                p[j] = d * scale;
+                if (p[j] > mx) mx = p[j];
+            }
+            double sum = 0.0;
+            for (size_t j = 0; j < nk; j++) {
+                p[j] = exp(p[j] - mx);
+                sum += p[j];
+            }
+            float *o = out + ((size_t)h * nq + t) * ad;
+            for (int i = 0; i < ad; i++) {
+                double acc = 0.0;
+                for (size_t j = 0; j < nk; j++) acc += p[j] * v[(j * akv + kh) * (size_t)ad + i];
+                o[i] = (float)(acc / sum);
+            }
+        }
+    }
+    free(p);
+}
+
+void or_attention_gate(const float *heads, size_t n, int ah, int ad, const float *z, float *out) {
+    for (size_t t = 0; t < n; t++)
+        for (int h = 0; h < ah; h++)
+            for (int i = 0; i < ad; i++) {
+                const size_t at = t * (size_t)ah * ad + (size_t)h * ad + i;
+                out[at] = heads[((size_t)h * n + t) * ad + i] * sigmoidf_ref(z[at]);
+            }
+}

@@ -136,6 +136,39 @@ void or_attention(const float *q, const float *k, const float *v, size_t seq,
 void or_silu_requant(const float *gate, const float *up, size_t m, size_t n,
                      int8_t *q, float *s);
 
+/* ---- Pplx decoder layer ops (src/models/pplx_flash/backbone.rs, cpu.rs) ----
+ * Dimensions are parameters; the reference fixes hidden 2560, FF 9216, 32
+ * delta heads (lh) of ld = 128 over 16 key heads (lk), 16 attention heads
+ * (ah) of ad = 256 over 4 key/value heads (akv). */
+/* cpu.rs:372-391 conv_silu over a fresh sequence (backbone.rs:271-283):
+ * out[t][c] = silu(sum over tap 0..3 of x[t-3+tap][c] * w[tap][c]), rows
+ * before t = 0 zero (the zero history); the sum starts at 0 in tap order with
+ * unfused products. x, out [n x width]; w [4 x width] (tap-major, as
+ * backbone.rs:170-178 repacks conv1d.weight [width, 1, 4]). */
+void or_conv_silu(const float *x, size_t n, size_t width, const float *w, float *out);
+/* backbone.rs:349-408 delta_scan for every head over a fresh state: conv
+ * [n x (2*lk*ld + lh*ld)] holds the q heads, k heads and v heads of each
+ * token; head h reads q/k head h / (lh/lk). a, b [n x lh]; decay = exp(A_log)
+ * and dt [lh]. out [lh x n x ld]. */
+void or_delta_scan(const float *conv, size_t n, int lh, int lk, int ld, const float *a, const float *b,
+                   const float *decay, const float *dt, float *out);
+/* backbone.rs:310-326 and cpu.rs:392-414: per (t, h), s = 1/sqrt(sum(src^2)/ld
+ * + 1e-6), ctx[t][h*ld + i] = ((src[i]*s)*norm[i])*silu(z[t][h*ld + i]).
+ * heads [lh x n x ld], z and ctx [n x lh*ld]. */
+void or_delta_gate(const float *heads, size_t n, int lh, int ld, const float *norm, const float *z,
+                   float *ctx);
+/* backbone.rs:415-428 rope: per row (position pos[r]) and head of width ad,
+ * dims i and i+32 (i < 32) rotate by angle = f32(pos) * freq[i]. */
+void or_rope(float *x, size_t rows, int heads, int ad, const size_t *pos, const float *freq);
+/* backbone.rs:509-579 attention core, in f64 (closed form; the reference uses
+ * matrixmultiply's sgemm): q [nq x ah x ad], k and v [nk x akv x ad]; head h
+ * reads key/value head h / (ah/akv); out [ah x nq x ad] = softmax(q.k * scale) v. */
+void or_attention_gqa(const float *q, const float *k, const float *v, size_t nq, size_t nk, int ah, int akv,
+                      int ad, float scale, float *out);
+/* cpu.rs:415-429 attention_gate: out[t][h*ad + i] = heads[h][t][i] *
+ * sigmoid(z[t][h*ad + i]); heads [ah x n x ad], z and out [n x ah*ad]. */
+void or_attention_gate(const float *heads, size_t n, int ah, int ad, const float *z, float *out);
+
 #ifdef __cplusplus
 }
 #endif

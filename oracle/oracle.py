@@ -77,6 +77,12 @@ def _declare(L):
         "or_mean_rows": (None, [P, SZ, SZ, P]),
         "or_attention": (None, [P, P, P, SZ, SZ, SZ, F, P]),
         "or_silu_requant": (None, [P, P, SZ, SZ, P, P]),
+        "or_conv_silu": (None, [P, SZ, SZ, P, P]),
+        "or_delta_scan": (None, [P, SZ, I, I, I, P, P, P, P, P]),
+        "or_delta_gate": (None, [P, SZ, I, I, P, P, P]),
+        "or_rope": (None, [P, SZ, I, I, P, P]),
+        "or_attention_gqa": (None, [P, P, P, SZ, SZ, I, I, I, F, P]),
+        "or_attention_gate": (None, [P, SZ, I, I, P, P]),
         "or_f32_to_bf16_n": (None, [P, SZ, P]),
         "or_f32_to_f16_n": (None, [P, SZ, P]),
         "or_f16_to_f32_n": (None, [P, SZ, P]),
@@ -387,3 +393,65 @@ def silu_requant(gate, up):
 
 def nprocs_env_default() -> int:
     return max(1, min(16, os.cpu_count() or 1))
+
+
+# ---- Pplx decoder layer ops (backbone.rs, cpu.rs) ----
+
+def conv_silu(x, w):
+    """cpu.rs:372-391 over a fresh sequence: x [n x width], w [4 x width]."""
+    x = _c(x, np.float32)
+    n, width = x.shape
+    out = np.empty_like(x)
+    lib().or_conv_silu(_p(x), n, width, _p(_c(w, np.float32)), _p(out))
+    return out
+
+
+def delta_scan(conv, lh, lk, ld, a, b, decay, dt):
+    """backbone.rs:349-408 for every head: returns heads [lh x n x ld]."""
+    conv = _c(conv, np.float32)
+    n = conv.shape[0]
+    out = np.empty((lh, n, ld), np.float32)
+    lib().or_delta_scan(_p(conv), n, lh, lk, ld, _p(_c(a, np.float32)), _p(_c(b, np.float32)),
+                        _p(_c(decay, np.float32)), _p(_c(dt, np.float32)), _p(out))
+    return out
+
+
+def delta_gate(heads, norm, z):
+    """backbone.rs:310-326 + cpu.rs:392-414: heads [lh x n x ld], z [n x lh*ld]."""
+    heads = _c(heads, np.float32)
+    lh, n, ld = heads.shape
+    out = np.empty((n, lh * ld), np.float32)
+    lib().or_delta_gate(_p(heads), n, lh, ld, _p(_c(norm, np.float32)), _p(_c(z, np.float32)), _p(out))
+    return out
+
+
+def rope(x, heads, ad, positions, freq):
+    """backbone.rs:415-428 on a copy of x [rows x heads*ad]."""
+    x = np.array(x, np.float32, copy=True, order="C")
+    pos = np.ascontiguousarray(positions, dtype=np.uint64)
+    lib().or_rope(_p(x), x.shape[0], heads, ad, _p(pos), _p(_c(freq, np.float32)))
+    return x
+
+
+def attention_gqa(q, k, v, ah, akv, ad, scale):
+    """backbone.rs:509-579 in f64: q [nq x ah*ad], k/v [nk x akv*ad] -> [ah x nq x ad]."""
+    q, k, v = _c(q, np.float32), _c(k, np.float32), _c(v, np.float32)
+    nq, nk = q.shape[0], k.shape[0]
+    out = np.empty((ah, nq, ad), np.float32)
+    lib().or_attention_gqa(_p(q), _p(k), _p(v), nq, nk, ah, akv, ad, np.float32(scale), _p(out))
+    return out
+
+
+def attention_gate(heads, z):
+    """cpu.rs:415-429: heads [ah x n x ad], z [n x ah*ad]."""
+    heads = _c(heads, np.float32)
+    ah, n, ad = heads.shape
+    out = np.empty((n, ah * ad), np.float32)
+    lib().or_attention_gate(_p(heads), n, ah, ad, _p(_c(z, np.float32)), _p(out))
+    return out
+
+
+def rope_freq():
+    """backbone.rs:227-229: inv_freq[i] = 1 / 1e7^((2i)/64) in f32."""
+    return np.array([np.float32(1.0) / np.power(np.float32(10_000_000.0), np.float32(2 * i) / np.float32(64.0),
+                                                dtype=np.float32) for i in range(32)], np.float32)

@@ -1,0 +1,111 @@
+"""The Pplx decider on the GPU (dz_pplx_*): each decoder layer and the whole
+chunk forward against the oracle's composition of the reference's layer
+(backbone.rs:207-250) on a random model at test sizes. The projections are
+the bit-exact W4A8 products; the layer ops between them (SiLU conv, delta
+rule, RMSNorms, rotary embedding, softmax attention, gates) use device exp/sin
+and fused multiply-adds, so the comparison is to a tolerance: cosine >=
+0.9999 and max-abs <= 2e-3 relative to the output's largest value."""
+import numpy as np
+import pytest
+
+from decisive_amd import rocm
+from tests import pplx_model
+from tests.gpu_util import cosine, dev, empty, host
+
+pytestmark = pytest.mark.gpu
+
+# two query heads per key/value head on both mixers, so a wrong head mapping shows
+SMALL = dict(layers=4, hidden=256, ff=512, delta_heads=4, delta_key_heads=2, delta_head_dim=128,
+             attn_heads=4, attn_kv_heads=2, attn_head_dim=256)
+
+
+def close(got, want, rel=2e-3):
+    scale = max(float(np.abs(want).max()), 1e-6)
+    return cosine(got, want) >= 0.9999 and float(np.abs(got - want).max()) <= rel * scale
+
+
+@pytest.fixture(scope="module")
+def small(ctx, oracle):
+    model = pplx_model.random_model(oracle, SMALL, seed=3)
+    p = pplx_model.load(ctx, rocm, model)
+    yield model, p
+    p.close()
+
+
+@pytest.mark.parametrize("layer", [0, 1, 3])
+@pytest.mark.parametrize("n", [1, 5, 37])
+def test_layer_matches_the_reference_layer(ctx, oracle, small, layer, n):
+    torch = pytest.importorskip("torch")
+    model, p = small
+    h = np.random.default_rng(n + layer).standard_normal((n, SMALL["hidden"])).astype(np.float32)
+    hd = dev(h)
+    p.layer(layer, hd, n)
+    got = host(ctx, hd)
+    want = pplx_model.ref_layer(oracle, model, layer, h)
+    assert close(got, want), (float(cosine(got, want)), float(np.abs(got - want).max()))
+
+
+def test_attention_layer_prunes_to_the_markers_in_order(ctx, oracle, small):
+    torch = pytest.importorskip("torch")
+    model, p = small
+    n, markers = 23, [17, 2, 22, 9]
+    h = np.random.default_rng(8).standard_normal((n, SMALL["hidden"])).astype(np.float32)
+    hd = dev(h)
+    p.layer(3, hd, n, markers)
+    got = host(ctx, hd)[:len(markers)]
+    want = pplx_model.ref_layer(oracle, model, 3, h, markers)
+    assert close(got, want)
+    # a recurrent layer cannot be cut
+    with pytest.raises(rocm.DzError) as e:
+        p.layer(0, dev(h), n, markers)
+    assert e.value.code == "INVALID_REQUEST"
+
+
+@pytest.mark.parametrize("n", [6, 64])
+def test_forward_logits_match_the_reference_chunk(ctx, oracle, small, n):
+    model, p = small
+    ids = np.random.default_rng(n).integers(0, 64, n)
+    markers = [n - 1, 0, n // 2]
+    got = p.forward_rows(model.embedding[ids], n, markers)
+    want = pplx_model.ref_forward(oracle, model, ids, markers)
+    assert got.shape == (3, 255) and np.isfinite(got).all()
+    assert close(got, want, rel=5e-3), (float(cosine(got, want)), float(np.abs(got - want).max()))
+
+
+def test_delta_scan_state_carries_across_tokens(ctx, oracle, small):
+    """The last token's output depends on the first token (the recurrent
+    state): changing only token 0 changes the output at token n-1."""
+    torch = pytest.importorskip("torch")
+    model, p = small
+    n = 12
+    h = np.random.default_rng(2).standard_normal((n, SMALL["hidden"])).astype(np.float32)
+    h2 = h.copy()
+    h2[0] *= -1
+    a, b = dev(h), dev(h2)
+    p.layer(0, a, n)
+    p.layer(0, b, n)
+    assert not np.allclose(host(ctx, a)[n - 1], host(ctx, b)[n - 1])
+
+
+def test_missing_weights_and_bad_names_are_rejected(ctx, oracle):
+    torch = pytest.importorskip("torch")
+    cfg = dict(SMALL, layers=1)
+    p = ctx.pplx_create(rocm.PplxConfig(**cfg))
+    with pytest.raises(rocm.DzError) as e:
+        p.layer(0, dev(np.zeros((2, 256), np.float32)), 2)
+    assert e.value.code == "INVALID_CHECKPOINT" and "missing" in str(e.value)
+    with pytest.raises(rocm.DzError) as e:
+        p.set_vector("language_model.layers.0.nope", np.zeros(4, np.float32))
+    assert e.value.code == "INVALID_CHECKPOINT"
+    with pytest.raises(rocm.DzError) as e:
+        p.set_vector("language_model.layers.7.input_layernorm.weight", np.zeros(256, np.float32))
+    assert e.value.code == "INVALID_CHECKPOINT"
+    # layer 0 is a delta layer: attention weights do not belong there
+    wire = oracle.pack_g64(oracle.f32_to_bf16(np.zeros((256, 256), np.float32) + 0.01), 256, 256, 4)
+    with pytest.raises(rocm.DzError) as e:
+        p.set_weight("language_model.layers.0.self_attn.o_proj.weight", wire, rocm.Q4_G64_F32, 256, 256)
+    assert e.value.code == "INVALID_CHECKPOINT"
+    with pytest.raises(rocm.DzError) as e:
+        ctx.pplx_create(rocm.PplxConfig(**dict(SMALL, delta_head_dim=64)))
+    assert e.value.code == "INVALID_PARAMETERS"
+    p.close()

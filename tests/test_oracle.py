@@ -409,3 +409,151 @@ def test_readout_rms_is_the_sequential_sum(oracle):
     assert np.array_equal(got[0].view(np.uint32), (x[0] * scale).astype(np.float32).view(np.uint32))
     pair = np.float32(np.sum(x[0].astype(np.float32) ** 2, dtype=np.float32))
     assert pair != seq
+
+
+# ---- Pplx decoder layer ops (backbone.rs, cpu.rs), pinned by properties ----
+
+def _silu64(x):
+    x = np.asarray(x, np.float64)
+    return x / (1.0 + np.exp(-x))
+
+
+def test_conv_silu_taps_are_causal_and_in_order(oracle):
+    """A one-hot tap shifts the sequence: tap 3 is the current token, tap 0
+    the token three back, and rows before the start are zero (backbone.rs:271-283)."""
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((9, 24)).astype(np.float32)
+    for tap in range(4):
+        w = np.zeros((4, 24), np.float32)
+        w[tap] = 1.0
+        got = oracle.conv_silu(x, w)
+        shifted = np.zeros_like(x)
+        lag = 3 - tap
+        shifted[lag:] = x[:9 - lag]
+        assert np.allclose(got, _silu64(shifted), rtol=1e-6, atol=1e-7), tap
+    # linear in the taps before the activation
+    w = rng.standard_normal((4, 24)).astype(np.float32)
+    pre = sum(np.pad(x, ((3 - t, 0), (0, 0)))[:9] * w[t] for t in range(4))
+    assert np.allclose(oracle.conv_silu(x, w), _silu64(pre), rtol=1e-5, atol=1e-6)
+
+
+def _delta_inputs(n, lh, lk, ld, keys, values, queries=None, a=None, b=None, decay=None, dt=None):
+    """conv rows holding q heads, k heads, v heads; keys/queries per (t, kh)."""
+    lkv = lk * ld
+    conv = np.zeros((n, 2 * lkv + lh * ld), np.float32)
+    for t in range(n):
+        for kh in range(lk):
+            conv[t, lkv + kh * ld:lkv + (kh + 1) * ld] = keys[t][kh]
+            conv[t, kh * ld:(kh + 1) * ld] = (queries if queries is not None else keys)[t][kh]
+        for h in range(lh):
+            conv[t, 2 * lkv + h * ld:2 * lkv + (h + 1) * ld] = values[t][h]
+    a = np.zeros((n, lh), np.float32) if a is None else a
+    b = np.full((n, lh), 40.0, np.float32) if b is None else b     # beta = sigmoid(40) = 1 in f32
+    decay = np.zeros(lh, np.float32) if decay is None else decay    # g = exp(-0 * softplus) = 1
+    dt = np.zeros(lh, np.float32) if dt is None else dt
+    return conv, a, b, decay, dt
+
+
+def test_delta_scan_reads_back_what_it_wrote(oracle):
+    """beta = 1, g = 1, orthonormal keys: the state stores k v^T, so a query
+    equal to a key written earlier (or now) returns that value / sqrt(ld),
+    and an unwritten key returns 0 (the delta rule with the readout after
+    the update, backbone.rs:382-407). Heads 2h and 2h+1 share key head h."""
+    lh, lk, ld, n = 4, 2, 16, 6
+    rng = np.random.default_rng(1)
+    e = np.eye(ld, dtype=np.float32)
+    keys = [[e[(3 * t + kh) % ld] * (1.0 + t) for kh in range(lk)] for t in range(n)]  # scale is normalized away
+    values = [[rng.standard_normal(ld).astype(np.float32) for _ in range(lh)] for _ in range(n)]
+    queries = [[e[(3 * max(t - 2, 0) + kh) % ld] for kh in range(lk)] for t in range(n)]
+    conv, a, b, decay, dt = _delta_inputs(n, lh, lk, ld, keys, values, queries)
+    out = oracle.delta_scan(conv, lh, lk, ld, a, b, decay, dt)
+    for h in range(lh):
+        for t in range(n):
+            want = values[max(t - 2, 0)][h] / np.sqrt(ld)
+            assert np.allclose(out[h, t], want, rtol=1e-5, atol=1e-6), (h, t)
+    # a query no key has touched reads zero
+    queries = [[e[2 + 3 * kh] for kh in range(lk)] for _ in range(n)]  # keys 3t + kh never hit 2 or 5
+    conv, a, b, decay, dt = _delta_inputs(n, lh, lk, ld, keys, values, queries)
+    assert np.abs(oracle.delta_scan(conv, lh, lk, ld, a, b, decay, dt)).max() == 0.0
+
+
+def test_delta_scan_decays_and_overwrites(oracle):
+    """g = exp(-decay * softplus(a + dt)) scales the old state before each
+    step; beta < 1 writes beta * (v - old read): writing v1 then v2 to one key
+    leaves beta*v2 + beta*(1 - beta)*g*v1 (the erase-then-write of the delta rule)."""
+    lh, lk, ld = 2, 1, 8
+    e = np.eye(ld, dtype=np.float32)
+    v1, v2 = np.arange(1, ld + 1, dtype=np.float32), np.linspace(-1, 1, ld).astype(np.float32)
+    keys = [[e[0]], [e[0]]]
+    values = [[v1, v1], [v2, v2]]
+    a = np.full((2, lh), 0.3, np.float32)
+    dt = np.array([0.2, -0.4], np.float32)
+    decay = np.array([0.5, 1.5], np.float32)
+    b = np.full((2, lh), 0.25, np.float32)
+    conv, a, b, decay, dt = _delta_inputs(2, lh, lk, ld, keys, values, None, a, b, decay, dt)
+    out = oracle.delta_scan(conv, lh, lk, ld, a, b, decay, dt)
+    beta = 1.0 / (1.0 + np.exp(-0.25))
+    for h in range(lh):
+        g = np.exp(-decay[h] * np.log1p(np.exp(0.3 + dt[h])))
+        first = beta * v1                      # written at t = 0 (state starts at zero)
+        second = g * first + beta * (v2 - g * first)
+        assert np.allclose(out[h, 0], first / np.sqrt(ld), rtol=1e-5, atol=1e-6)
+        assert np.allclose(out[h, 1], second / np.sqrt(ld), rtol=1e-5, atol=1e-6), h
+
+
+def test_delta_gate_and_attention_gate_closed_forms(oracle):
+    rng = np.random.default_rng(2)
+    lh, ld, n = 3, 16, 5
+    heads = rng.standard_normal((lh, n, ld)).astype(np.float32) * 3
+    norm = rng.standard_normal(ld).astype(np.float32)
+    z = rng.standard_normal((n, lh * ld)).astype(np.float32)
+    got = oracle.delta_gate(heads, norm, z)
+    h64 = heads.astype(np.float64)
+    scale = 1.0 / np.sqrt((h64 ** 2).mean(axis=2, keepdims=True) + 1e-6)
+    want = (h64 * scale * norm).transpose(1, 0, 2).reshape(n, lh * ld) * _silu64(z)
+    assert np.allclose(got, want, rtol=1e-5, atol=1e-6)
+    got = oracle.attention_gate(heads, z)
+    want = h64.transpose(1, 0, 2).reshape(n, lh * ld) / (1.0 + np.exp(-z.astype(np.float64)))
+    assert np.allclose(got, want, rtol=1e-6, atol=1e-7)
+
+
+def test_rope_rotates_the_first_64_dims_by_position(oracle):
+    """Pairs (i, i + 32) rotate by pos * freq[i]; dims from 64 on and position
+    0 are unchanged; the dot of two rotated vectors depends only on the
+    position difference (backbone.rs:415-428, :227-229)."""
+    rng = np.random.default_rng(3)
+    freq = oracle.rope_freq()
+    assert freq[0] == 1.0 and abs(freq[31] - 1e7 ** (-62 / 64)) < 1e-9
+    q = rng.standard_normal((1, 256)).astype(np.float32)
+    k = rng.standard_normal((1, 256)).astype(np.float32)
+    assert np.array_equal(oracle.rope(q, 1, 256, [0], freq), q)
+    r = oracle.rope(q, 1, 256, [7], freq)
+    assert np.array_equal(r[:, 64:], q[:, 64:])
+    pairs = lambda x: x[0, :32].astype(np.float64) ** 2 + x[0, 32:64].astype(np.float64) ** 2
+    assert np.allclose(pairs(r), pairs(q), rtol=1e-5)
+    d1 = float(oracle.rope(q, 1, 256, [9], freq) @ oracle.rope(k, 1, 256, [4], freq).T)
+    d2 = float(oracle.rope(q, 1, 256, [5], freq) @ k.T)
+    assert abs(d1 - d2) < 1e-3 * (1 + abs(d2))
+
+
+def test_attention_gqa_maps_heads_to_kv_heads(oracle):
+    """Head h attends with key/value head h / (ah/akv); zero queries give the
+    mean of the values; permuting the keys with their values changes nothing."""
+    rng = np.random.default_rng(4)
+    ah, akv, ad, nq, nk = 4, 2, 8, 3, 5
+    q = rng.standard_normal((nq, ah * ad)).astype(np.float32)
+    k = rng.standard_normal((nk, akv * ad)).astype(np.float32)
+    v = rng.standard_normal((nk, akv * ad)).astype(np.float32)
+    out = oracle.attention_gqa(q, k, v, ah, akv, ad, 0.5)
+    for h in range(ah):
+        kh = h // (ah // akv)
+        qh, kk, vv = (q[:, h * ad:(h + 1) * ad].astype(np.float64), k[:, kh * ad:(kh + 1) * ad].astype(np.float64),
+                      v[:, kh * ad:(kh + 1) * ad].astype(np.float64))
+        s = qh @ kk.T * 0.5
+        p = np.exp(s - s.max(axis=1, keepdims=True))
+        want = (p / p.sum(axis=1, keepdims=True)) @ vv
+        assert np.allclose(out[h], want, rtol=1e-5, atol=1e-6), h
+    zero = oracle.attention_gqa(np.zeros_like(q), k, v, ah, akv, ad, 0.5)
+    assert np.allclose(zero[0, 0], v[:, :ad].mean(axis=0), rtol=1e-5, atol=1e-6)
+    perm = rng.permutation(nk)
+    assert np.allclose(oracle.attention_gqa(q, k[perm], v[perm], ah, akv, ad, 0.5), out, rtol=1e-5, atol=1e-6)
