@@ -29,6 +29,7 @@
 #include <vector>
 
 #include "answer.hpp"
+#include "chunks.hpp"
 #include "decisive_rocm.h"
 #include "embedding_cache.hpp"
 #include "inference.hpp"
@@ -212,87 +213,15 @@ public:
 private:
     Rocm() = default;
 
-    struct Encoded {
-        std::vector<uint32_t> ids;
-        std::vector<int32_t> markers;
-        std::vector<std::string> keys;
-        std::vector<size_t> counts;
-    };
-
-    static bool whole(const Json &v, double limit) {
-        return v.is_number() && v.as_number() >= 0 && v.as_number() < limit && v.as_number() == (double)(uint64_t)v.as_number();
-    }
-
-    Result<Encoded> encoded_chunk(const Json &c, const Json &questions, size_t max_tokens) const {
-        if (!c.is_object() || !c["ids"].is_array() || !c["markers"].is_array() || !c["keys"].is_array() ||
-            !c["counts"].is_array())
-            return Error("INVALID_REQUEST", "each chunk needs ids, markers, keys and counts arrays");
-        Encoded e;
-        for (const Json &v : c["ids"].as_array()) {
-            if (!whole(v, (double)config_.vocab)) return Error("INVALID_REQUEST", "token id outside the vocabulary");
-            e.ids.push_back((uint32_t)v.as_number());
-        }
-        if (e.ids.empty()) return Error("INVALID_REQUEST", "a chunk needs at least one token");
-        if (e.ids.size() > max_tokens) return Error::engine("chunk exceeds token limit");
-        for (const Json &v : c["markers"].as_array()) {
-            if (!whole(v, (double)e.ids.size())) return Error("INVALID_REQUEST", "readout marker outside the chunk");
-            e.markers.push_back((int32_t)v.as_number());
-        }
-        for (const Json &v : c["keys"].as_array()) {
-            if (!v.is_string() || !questions[v.as_string()].is_object())
-                return Error("INVALID_REQUEST", "chunk key without a question");
-            e.keys.push_back(v.as_string());
-        }
-        for (const Json &v : c["counts"].as_array()) {
-            if (!whole(v, (double)DZ_READOUT_CODES + 1) || v.as_number() < 1)
-                return Error("INVALID_REQUEST", "answer count outside 1..255");
-            e.counts.push_back((size_t)v.as_number());
-        }
-        if (e.markers.size() != e.keys.size() || e.keys.size() != e.counts.size() || e.markers.empty() ||
-            e.markers.size() > DZ_READOUT_MAX_MARKERS)
-            return Error("INVALID_REQUEST", "markers, keys and counts must pair up (1..256 per chunk)");
-        return e;
-    }
-
-    // native.rs:193-274 over encoded chunks.
+    // native.rs:193-274 over encoded chunks, reading out with the encoder.
     Result<Json> predict_answers(const Request &request, const PplxParameters &parameters, EmbeddingCache &cache,
                                  const Cancellation &cancellation) {
-        const Json &chunks = request.state["chunks"];
-        if (!chunks.is_array() || chunks.size() == 0 || request.state.size() != 1)
-            return Error("INVALID_REQUEST", "state must hold a nonempty chunks array");
-        std::vector<Encoded> plan;
-        for (const Json &c : chunks.as_array()) {
-            auto e = encoded_chunk(c, request.questions, parameters.max_sequence_tokens);
-            if (!e) return e.error();
-            plan.push_back(e.take());
-        }
-        Json answers = Json::object();
-        uint64_t tokens = 0;
-        for (const Encoded &e : plan) {
-            Status s = cancellation.check();
-            if (!s) return s.error();
-            auto rows = cache.load(e.ids, [this](const std::vector<uint32_t> &miss) { return read_rows(miss); },
-                                   row_bytes_, cancellation);
-            if (!rows) return rows.error();
-            auto logits = readout(rows.value(), e.ids.size(), e.markers);
-            if (!logits) return logits.error();
-            for (size_t i = 0; i < e.keys.size(); i++) {
-                const float *row = logits.value().data() + i * DZ_READOUT_CODES;
-                std::vector<float> values(row, row + e.counts[i]);
-                auto a = answer(request.questions[e.keys[i]], values, temperature_);
-                if (!a) return a.error();
-                answers[e.keys[i]] = a.take();
-            }
-            tokens += e.ids.size();
-        }
-        Json usage = Json::object();
-        usage["input_tokens"] = Json(tokens);
-        usage["output_tokens"] = Json(0);
-        usage["sequences"] = Json((uint64_t)plan.size());
-        Json out = Json::object();
-        out["answers"] = std::move(answers);
-        out["usage"] = std::move(usage);
-        return out;
+        return answer_chunks(
+            request, parameters, cache, cancellation, (uint32_t)config_.vocab, row_bytes_, temperature_,
+            [this](const std::vector<uint32_t> &miss) { return read_rows(miss); },
+            [this](const std::vector<uint8_t> &rows, size_t tokens, const std::vector<int32_t> &markers) {
+                return readout(rows, tokens, markers);
+            });
     }
 
     Result<std::vector<uint32_t>> token_ids(const Request &request) const {

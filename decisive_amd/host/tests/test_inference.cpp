@@ -534,4 +534,23 @@ TEST(checkpoint_rejects_what_the_reference_validator_rejects) {
     fs::remove_all(dir);
 }
 
+TEST(checkpoint_reader_accepts_a_pplx_decoder_checkpoint) {
+    const char *dir = getenv("DZ_PPLX_CHECKPOINT_DIR");
+    CHECK(dir != nullptr);
+    if (!dir) return;
+    PackedModel pm;
+    pm.layers = 4;
+    pm.hidden = 256;
+    auto c = PackedCheckpoint::open(dir, pm);
+    CHECK(c.ok());
+    if (!c.ok()) {
+        fprintf(stderr, "%s\n", c.error().message.c_str());
+        return;
+    }
+    // a delta layer holds 14 tensors, an attention layer 11 (backbone.rs:101-199)
+    CHECK_EQ(c.value().layers()[0].tensors.size(), (size_t)14);
+    CHECK_EQ(c.value().layers()[3].tensors.size(), (size_t)11);
+    CHECK(!PackedCheckpoint::open(dir).ok());  // the reference's 32 x 2560 shape does not fit
+}
+
 int main(int argc, char **argv) { return harness::run_all(argc, argv); }

@@ -9,6 +9,10 @@
 #include <cstring>
 #include <vector>
 
+#include <fstream>
+#include <sstream>
+
+#include "../pplx_backend.hpp"
 #include "../rocm_backend.hpp"
 #include "harness.hpp"
 
@@ -232,6 +236,95 @@ TEST(rocm_backend_opened_on_a_packed_checkpoint) {
     // a checkpoint of another width is refused
     dz_encoder_config narrow = small_config();
     CHECK(Rocm::create_from_checkpoint(0, dir, narrow, 7, no_tuning()).error().code == "INVALID_PARAMETERS");
+}
+
+TEST(rocm_pplx_answers_from_a_packed_checkpoint) {
+    const char *dir = getenv("DZ_PPLX_CHECKPOINT_DIR");
+    CHECK(dir != nullptr);
+    if (!dir) return;
+    dz_pplx_config cfg{4, 256, 512, 4, 2, 128, 4, 2, 256};
+    PackedModel pm;
+    pm.layers = 4;
+    pm.hidden = 256;
+    auto made = RocmPplx::open(0, dir, cfg, pm);
+    CHECK(made.ok());
+    if (!made.ok()) {
+        fprintf(stderr, "%s\n", made.error().to_string().c_str());
+        return;
+    }
+    Model<RocmPplx> model(made.take());
+    RocmPplx &pplx = model.backend();
+    CHECK(pplx.temperature() == 1.5539091673122623f);
+    std::ifstream f(std::string(dir) + "/expected_logits.json");
+    std::stringstream text;
+    text << f.rdbuf();
+    Json expected = Json::parse(text.str());
+    std::vector<uint32_t> ids;
+    for (const Json &v : expected["ids"].as_array()) ids.push_back((uint32_t)v.as_number());
+    std::vector<int32_t> markers;
+    for (const Json &v : expected["markers"].as_array()) markers.push_back((int32_t)v.as_number());
+    // the oracle's logits (tests/test_host.py) within the layer-op tolerance
+    auto rows = pplx.checkpoint().embedding_rows(ids);
+    CHECK(rows.ok());
+    auto lg = pplx.logits(rows.value(), ids.size(), markers);
+    CHECK(lg.ok());
+    if (!lg.ok()) {
+        fprintf(stderr, "%s\n", lg.error().to_string().c_str());
+        return;
+    }
+    double dot = 0, gg = 0, ww = 0, maxerr = 0, scale = 0;
+    for (size_t r = 0; r < markers.size(); r++)
+        for (size_t c = 0; c < DZ_READOUT_CODES; c++) {
+            const double g = lg.value()[r * DZ_READOUT_CODES + c], w = expected["logits"][r][c].as_number();
+            dot += g * w;
+            gg += g * g;
+            ww += w * w;
+            maxerr = std::max(maxerr, std::fabs(g - w));
+            scale = std::max(scale, std::fabs(w));
+        }
+    // the decoder is a chain of A8 quantizations: an ulp of difference in a
+    // layer op flips an activation code now and then, so the logits are
+    // compared to 1% of their largest value (the layers alone match far closer)
+    CHECK(dot / std::sqrt(gg * ww) >= 0.9999);
+    CHECK(maxerr <= 1e-2 * scale);
+    printf("pplx logits vs oracle: cos %.9f, max |d| %.5f of %.3f\n", dot / std::sqrt(gg * ww), maxerr, scale);
+    // answers through Model<RocmPplx>: the answer step over those logits
+    Request req;
+    Json chunk = Json::object();
+    chunk["ids"] = ids_json(ids);
+    Json m = Json::array();
+    for (int32_t v : markers) m.push_back(Json(v));
+    chunk["markers"] = m;
+    chunk["keys"] = Json::parse(R"(["team","refund","tone"])");
+    chunk["counts"] = Json::parse("[3,2,3]");
+    req.state = Json::object();
+    req.state["chunks"] = Json(Json::Array{chunk});
+    req.questions = answer_request(ids, {0, 1, 2}).questions;
+    auto cache = model.create_cache(CacheOptions{});
+    auto got = model.predict(req, nullptr, &cache.value(), Cancellation{});
+    CHECK(got.ok());
+    if (!got.ok()) {
+        fprintf(stderr, "%s\n", got.error().to_string().c_str());
+        return;
+    }
+    const char *keys[3] = {"team", "refund", "tone"};
+    const size_t counts[3] = {3, 2, 3};
+    for (int i = 0; i < 3; i++) {
+        const float *row = lg.value().data() + i * DZ_READOUT_CODES;
+        auto want = answer(req.questions[keys[i]], std::vector<float>(row, row + counts[i]), pplx.temperature());
+        CHECK(want.ok() && got.value().response["answers"][keys[i]] == want.value());
+    }
+    CHECK_EQ(got.value().response["usage"]["input_tokens"], Json((uint64_t)ids.size()));
+    uint64_t misses = cache.value().state().misses();
+    auto again = model.predict(req, nullptr, &cache.value(), Cancellation{});
+    CHECK(again.ok() && again.value().response == got.value().response);
+    CHECK_EQ(cache.value().state().misses(), misses);
+    // token-id states are not this backend's; shapes must match the checkpoint
+    CHECK_EQ(model.predict(request_of(ids), nullptr, nullptr, Cancellation{}).error().code,
+             std::string("INVALID_REQUEST"));
+    dz_pplx_config wide = cfg;
+    wide.hidden = 512;
+    CHECK(RocmPplx::open(0, dir, wide, pm).error().code == "INVALID_PARAMETERS");
 }
 
 TEST(rocm_answer_requests_are_validated) {

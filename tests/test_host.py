@@ -82,12 +82,76 @@ def write_checkpoint(root: Path, oracle) -> Path:
     return root
 
 
+PPLX_SMALL = dict(layers=4, hidden=256, ff=512, delta_heads=4, delta_key_heads=2, delta_head_dim=128,
+                  attn_heads=4, attn_kv_heads=2, attn_head_dim=256)
+
+
+def write_pplx_checkpoint(root: Path, oracle) -> Path:
+    """The random Pplx decider of tests/pplx_model.py (PPLX_SMALL, 64-token
+    vocabulary) as a q4-e4 packed checkpoint (export_packed.rs:13-103 layout),
+    plus expected_logits.json: the oracle's logits for one chunk."""
+    from tests import pplx_model
+    model = pplx_model.random_model(oracle, PPLX_SMALL, seed=5)
+    root.mkdir(parents=True, exist_ok=True)
+    files, layers, shard0, shard1 = {}, [], {}, {}
+
+    def write(name, data: bytes):
+        (root / name).write_bytes(data)
+        files[name] = {"bytes": len(data), "sha256": hashlib.sha256(data).hexdigest()}
+
+    def bf16_bytes(values):
+        return oracle.f32_to_bf16(np.asarray(values, np.float32)).tobytes()
+
+    cw = pplx_model.conv_width(PPLX_SMALL)
+    offset = 0
+    for i in range(PPLX_SMALL["layers"]):
+        prefix = f"language_model.layers.{i}."
+        blob, tensors = b"", []
+        for name in sorted(n for n in list(model.packed) + list(model.vectors) if n.startswith(prefix)):
+            if name in model.packed:
+                wire, rows, cols = model.packed[name]
+                data, shape = wire.tobytes(), [rows, cols]
+            else:
+                values = model.vectors[name]
+                data = bf16_bytes(values)
+                shape = [cw, 1, 4] if name.endswith("conv1d.weight") else [values.size]
+            n_el = int(np.prod(shape))
+            shard0[name] = {"dtype": "BF16", "shape": shape, "data_offsets": [offset, offset + 2 * n_el]}
+            offset += 2 * n_el
+            tensors.append({"name": name, "shape": shape, "start": len(blob), "end": len(blob) + len(data)})
+            blob += data
+        fname = f"q4-e4-layer-{i:02}.bin"
+        write(fname, blob)
+        layers.append({"file": fname, "bytes": len(blob), "tensors": tensors})
+    vocab = model.embedding.shape[0]
+    shard0["language_model.embed_tokens.weight"] = {"dtype": "BF16", "shape": [vocab, 256],
+                                                    "data_offsets": [offset, offset + vocab * 512]}
+    shard1["language_model.norm.weight"] = {"dtype": "BF16", "shape": [256], "data_offsets": [0, 512]}
+    write("q4-e4-embedding.bin", model.embedding.tobytes())
+    write("q4-e4-readout.bin", model.packed["readout"][0].tobytes())
+    write("q4-e4-norm.bin", bf16_bytes(model.vectors["language_model.norm.weight"]))
+    manifest = {"schema_version": 1, "revision": REVISION, "scheme": "q4-w4a8-e4-r4-g64", "group_size": 64,
+                "group_bytes": 36, "embedding_row_bytes": 256 // 64 * 36, "layers": layers,
+                "headers": [json.dumps(shard0), json.dumps(shard1)], "embedding": "q4-e4-embedding.bin",
+                "readout": "q4-e4-readout.bin", "norm": "q4-e4-norm.bin",
+                "decoder_bytes": sum(l["bytes"] for l in layers), "files": dict(sorted(files.items()))}
+    (root / "packed-q4-e4.json").write_text(json.dumps(manifest, indent=2))
+    (root / "decision_config.json").write_text(json.dumps({"temperature": 1.5539091673122623}))
+    ids = [int(v) for v in np.random.default_rng(9).integers(0, vocab, 40)]
+    markers = [39, 7, 20]
+    logits = pplx_model.ref_forward(oracle, model, np.array(ids), markers)
+    (root / "expected_logits.json").write_text(json.dumps({"ids": ids, "markers": markers,
+                                                           "logits": logits.tolist()}))
+    return root
+
+
 def test_model_cache_parameters_and_embedding_cache_on_cpu(tmp_path, oracle):
     """Ports of src/inference/tests.rs:57-141 plus EmbeddingCache
     (browser/pplx.rs:45-138), error-code mapping (mod.rs:56-78), the answer
     step (input.rs) and the packed checkpoint reader (prepare_hf_q4.py)."""
     ck = write_checkpoint(tmp_path / "ck", oracle)
-    r = _run(_program("test_inference"), 120, {"DZ_CHECKPOINT_DIR": str(ck)})
+    pk = write_pplx_checkpoint(tmp_path / "pplx", oracle)
+    r = _run(_program("test_inference"), 120, {"DZ_CHECKPOINT_DIR": str(ck), "DZ_PPLX_CHECKPOINT_DIR": str(pk)})
     assert r.returncode == 0, r.stderr
     assert "0 failed check(s)" in r.stdout
 
@@ -98,6 +162,7 @@ def test_rocm_backend_behind_model(tmp_path, oracle):
     for bit, cache reuse, splitting by maxSequenceTokens, failure clearing,
     answers, and a backend opened on a packed checkpoint."""
     ck = write_checkpoint(tmp_path / "ck", oracle)
-    r = _run(_program("test_rocm_backend"), 240, {"DZ_CHECKPOINT_DIR": str(ck)})
+    pk = write_pplx_checkpoint(tmp_path / "pplx", oracle)
+    r = _run(_program("test_rocm_backend"), 240, {"DZ_CHECKPOINT_DIR": str(ck), "DZ_PPLX_CHECKPOINT_DIR": str(pk)})
     assert r.returncode == 0, r.stdout + r.stderr
     assert "0 failed check(s)" in r.stdout

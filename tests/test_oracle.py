@@ -531,8 +531,8 @@ def test_rope_rotates_the_first_64_dims_by_position(oracle):
     assert np.array_equal(r[:, 64:], q[:, 64:])
     pairs = lambda x: x[0, :32].astype(np.float64) ** 2 + x[0, 32:64].astype(np.float64) ** 2
     assert np.allclose(pairs(r), pairs(q), rtol=1e-5)
-    d1 = float(oracle.rope(q, 1, 256, [9], freq) @ oracle.rope(k, 1, 256, [4], freq).T)
-    d2 = float(oracle.rope(q, 1, 256, [5], freq) @ k.T)
+    d1 = float((oracle.rope(q, 1, 256, [9], freq) @ oracle.rope(k, 1, 256, [4], freq).T)[0, 0])
+    d2 = float((oracle.rope(q, 1, 256, [5], freq) @ k.T)[0, 0])
     assert abs(d1 - d2) < 1e-3 * (1 + abs(d2))
 
 
