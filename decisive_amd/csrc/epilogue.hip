@@ -159,24 +159,34 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__restrict__ 
 
 // The readout's RMSNorm (pplx_flash/cpu.rs:310-333 rms_from, as applied by
 // pplx_flash/mod.rs:149-155): the sum of squares runs in row order, as the
-// reference's iterator sum does, so the result is bit-exact with it. One block
-// per selected row (`rows` picks hidden rows; null takes row r); the squares
-// are formed in parallel and lane 0 adds them in order from LDS.
-__global__ __launch_bounds__(64) void readout_rms_kernel(const void *__restrict__ h, int dtype,
-                                                         const int32_t *__restrict__ rows, int d,
-                                                         const float *__restrict__ w, float eps,
-                                                         int zero_centered, float *__restrict__ y) {
-    extern __shared__ float squares[];
+// reference's iterator sum does, so the result is bit-exact with it. One
+// 256-thread block per selected row (`rows` picks hidden rows; null takes row
+// r): every thread squares its share of the row into LDS (loads in flight
+// together), thread 0 adds the squares in row order, and all threads write
+// the scaled row.
+template <int DT>
+__global__ __launch_bounds__(256) void readout_rms_kernel(const void *__restrict__ h,
+                                                          const int32_t *__restrict__ rows, int d,
+                                                          const float *__restrict__ w, float eps,
+                                                          int zero_centered, float *__restrict__ y) {
+    extern __shared__ __align__(16) float squares[];
     __shared__ float scale_sh;
     const size_t base = (size_t)(rows ? rows[blockIdx.x] : (int)blockIdx.x) * d;
-    for (int i = threadIdx.x; i < d; i += 64) {
-        const float v = ld(h, dtype, base + i);
+#pragma unroll 4
+    for (int i = threadIdx.x; i < d; i += 256) {
+        const float v = ld(h, DT, base + i);
         squares[i] = __fmul_rn(v, v);
     }
     __syncthreads();
     if (threadIdx.x == 0) {
         float ss = 0.0f;
-        for (int i = 0; i < d; i++) ss = __fadd_rn(ss, squares[i]);
+        int i = 0;
+        for (; i + 8 <= d; i += 8) {
+            const float4_t a = *(const float4_t *)(squares + i), b = *(const float4_t *)(squares + i + 4);
+            ss = __fadd_rn(__fadd_rn(__fadd_rn(__fadd_rn(ss, a[0]), a[1]), a[2]), a[3]);
+            ss = __fadd_rn(__fadd_rn(__fadd_rn(__fadd_rn(ss, b[0]), b[1]), b[2]), b[3]);
+        }
+        for (; i < d; i++) ss = __fadd_rn(ss, squares[i]);
         // v_sqrt_f32 is not correctly rounded; a float's square root taken in
         // f64 and rounded to f32 is (the exact root is never near enough to a
         // float midpoint for the f64 error to matter)
@@ -186,9 +196,10 @@ __global__ __launch_bounds__(64) void readout_rms_kernel(const void *__restrict_
     __syncthreads();
     const float scale = scale_sh;
     float *dst = y + (size_t)blockIdx.x * d;
-    for (int i = threadIdx.x; i < d; i += 64) {
+#pragma unroll 4
+    for (int i = threadIdx.x; i < d; i += 256) {
         const float g = zero_centered ? __fadd_rn(1.0f, w[i]) : w[i];
-        dst[i] = __fmul_rn(__fmul_rn(ld(h, dtype, base + i), scale), g);
+        dst[i] = __fmul_rn(__fmul_rn(ld(h, DT, base + i), scale), g);
     }
 }
 
@@ -517,9 +528,12 @@ void launch_rmsnorm(const float *x, float *y, int rows, int d, const float *w, f
 }
 void launch_readout_rms(const void *h, int dtype, const int32_t *rows, int n, int d, const float *w,
                         float eps, int zero_centered, float *y, hipStream_t s) {
-    if (n && d)
-        hipLaunchKernelGGL(readout_rms_kernel, dim3(n), dim3(64), (size_t)d * sizeof(float), s, h, dtype,
-                           rows, d, w, eps, zero_centered, y);
+    if (!n || !d) return;
+    const size_t lds = (size_t)d * sizeof(float);
+    if (dtype == 1)
+        hipLaunchKernelGGL(readout_rms_kernel<1>, dim3(n), dim3(256), lds, s, h, rows, d, w, eps, zero_centered, y);
+    else
+        hipLaunchKernelGGL(readout_rms_kernel<0>, dim3(n), dim3(256), lds, s, h, rows, d, w, eps, zero_centered, y);
 }
 void launch_flag_nonfinite(const float *y, size_t n, int *flag, int bit, hipStream_t s) {
     if (n) hipLaunchKernelGGL(flag_nonfinite_kernel, dim3(cdiv(n, 256)), dim3(256), 0, s, y, n, flag, bit);

@@ -109,73 +109,107 @@ __global__ void delta_prep_kernel(const float *__restrict__ conv, int lh, int lk
 }
 
 // The gated delta rule. A wave owns 16 state columns j of head h; lane
-// (r, c) holds rows [32r, 32r + 32) of column 16*blockIdx.y + c in registers.
-// Per token: S *= g; mem = S^T k; delta = (v - mem) beta; S += k delta^T;
-// out = S^T q. The row sums close over the four row groups with two
-// cross-lane adds. The next token's inputs load while this one computes.
+// (c, r) = (lane / 4, lane % 4) holds rows [32r, 32r + 32) of column
+// 16*blockIdx.y + c in registers. Per token: S *= g; mem = S^T k;
+// delta = (v - mem) beta; S += k delta^T; out = S^T q. The sums over the four
+// row groups close inside each lane quad with two DPP adds. Tokens are staged
+// in LDS sixteen at a time; the next chunk's loads are in flight while this
+// chunk computes.
+__device__ __forceinline__ float quad_sum(float v) {
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+    return v;
+}
+
+constexpr int kScanChunk = 16;       // tokens staged in LDS at a time
+constexpr int kScanRow = 4 * 36;      // one token's k (or q): four row groups of 32, padded to 36
+
 __global__ __launch_bounds__(64) void delta_scan_kernel(const float *__restrict__ qhat,
                                                         const float *__restrict__ khat,
                                                         const float *__restrict__ conv,
                                                         const float *__restrict__ gb, int n, int lh, int lk,
                                                         float *__restrict__ out) {
-    constexpr int R = kLd / 4;
-    const int h = blockIdx.x, lane = threadIdx.x, r = lane / 16, c = lane % 16;
-    const int j = blockIdx.y * 16 + c;
+    constexpr int R = kLd / 4, T = kScanChunk;
+    // two chunk buffers: k and q rows (padded so the four row groups fall in
+    // different banks), v of the block's 16 columns, g and beta
+    __shared__ __align__(16) float ks[2][T * kScanRow], qs[2][T * kScanRow], vs[2][T * 16], gs[2][T * 2];
+    const int h = blockIdx.x, lane = threadIdx.x, r = lane % 4, c = lane / 4;
+    const int j0 = blockIdx.y * 16, j = j0 + c;
     const int kh = h / (lh / lk);
     const size_t lkv = (size_t)lk * kLd, width = 2 * lkv + (size_t)lh * kLd;
     float S[R];
 #pragma unroll
     for (int i = 0; i < R; i++) S[i] = 0.0f;
-    float4_t kn[R / 4], qn[R / 4];
-    float vn = 0.0f, gn = 0.0f, bn = 0.0f;
-    auto fetch = [&](int t) {
-        const float4_t *kp = (const float4_t *)(khat + ((size_t)t * lk + kh) * kLd + r * R);
-        const float4_t *qp = (const float4_t *)(qhat + ((size_t)t * lk + kh) * kLd + r * R);
+    // staging registers: 8 + 8 float4 of k and q rows, one float4 of v, g/beta
+    float4_t rk[8], rq[8], rv;
+    float2 rg;
+    auto load = [&](int t0) {
 #pragma unroll
-        for (int u = 0; u < R / 4; u++) {
-            kn[u] = kp[u];
-            qn[u] = qp[u];
+        for (int i = 0; i < 8; i++) {
+            const int id = lane + 64 * i, tt = id / 32, u = id % 32, t = t0 + tt;
+            const size_t row = ((size_t)min(t, n - 1) * lk + kh) * kLd + 4 * u;
+            rk[i] = *(const float4_t *)(khat + row);
+            rq[i] = *(const float4_t *)(qhat + row);
         }
-        vn = conv[(size_t)t * width + 2 * lkv + (size_t)h * kLd + j];
-        gn = gb[((size_t)t * lh + h) * 2];
-        bn = gb[((size_t)t * lh + h) * 2 + 1];
+        {
+            const int tt = lane / 4, part = lane % 4, t = min(t0 + tt, n - 1);
+            rv = *(const float4_t *)(conv + (size_t)t * width + 2 * lkv + (size_t)h * kLd + j0 + 4 * part);
+        }
+        if (lane < T) {
+            const int t = min(t0 + lane, n - 1);
+            rg = *(const float2 *)(gb + ((size_t)t * lh + h) * 2);
+        }
     };
-    if (n > 0) fetch(0);
-    for (int t = 0; t < n; t++) {
-        float k[R], q[R];
+    auto store = [&](int buf) {
 #pragma unroll
-        for (int u = 0; u < R / 4; u++)
+        for (int i = 0; i < 8; i++) {
+            const int id = lane + 64 * i, tt = id / 32, u = id % 32;
+            const int at = tt * kScanRow + (u / 8) * 36 + (u % 8) * 4;
+            *(float4_t *)(&ks[buf][at]) = rk[i];
+            *(float4_t *)(&qs[buf][at]) = rq[i];
+        }
+        *(float4_t *)(&vs[buf][(lane / 4) * 16 + 4 * (lane % 4)]) = rv;
+        if (lane < T) *(float2 *)(&gs[buf][lane * 2]) = rg;
+    };
+    if (n > 0) {
+        load(0);
+        store(0);
+    }
+    __syncthreads();
+    for (int t0 = 0, buf = 0; t0 < n; t0 += T, buf ^= 1) {
+        const bool more = t0 + T < n;
+        if (more) load(t0 + T);  // in flight while this chunk computes
+        const int count = min(T, n - t0);
+        for (int tt = 0; tt < count; tt++) {
+            const float *kr = &ks[buf][tt * kScanRow + r * 36], *qr = &qs[buf][tt * kScanRow + r * 36];
+            const float g = gs[buf][tt * 2], beta = gs[buf][tt * 2 + 1], v = vs[buf][tt * 16 + c];
+            float m[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                k[4 * u + e] = kn[u][e];
-                q[4 * u + e] = qn[u][e];
+            for (int u = 0; u < R / 4; u++) {
+                const float4_t k4 = *(const float4_t *)(kr + 4 * u);
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    S[4 * u + e] *= g;
+                    m[e] = __builtin_fmaf(S[4 * u + e], k4[e], m[e]);
+                }
             }
-        const float v = vn, g = gn, beta = bn;
-        if (t + 1 < n) fetch(t + 1);
-        float m0 = 0.0f, m1 = 0.0f;
+            const float mem = quad_sum((m[0] + m[1]) + (m[2] + m[3]));
+            const float delta = (v - mem) * beta;
+            float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int i = 0; i < R; i += 2) {
-            S[i] *= g;
-            S[i + 1] *= g;
-            m0 = __builtin_fmaf(S[i], k[i], m0);
-            m1 = __builtin_fmaf(S[i + 1], k[i + 1], m1);
-        }
-        float mem = m0 + m1;
-        mem += __shfl_xor(mem, 16);
-        mem += __shfl_xor(mem, 32);
-        const float delta = (v - mem) * beta;
-        float o0 = 0.0f, o1 = 0.0f;
+            for (int u = 0; u < R / 4; u++) {
+                const float4_t k4 = *(const float4_t *)(kr + 4 * u), q4 = *(const float4_t *)(qr + 4 * u);
 #pragma unroll
-        for (int i = 0; i < R; i += 2) {
-            S[i] = __builtin_fmaf(k[i], delta, S[i]);
-            S[i + 1] = __builtin_fmaf(k[i + 1], delta, S[i + 1]);
-            o0 = __builtin_fmaf(S[i], q[i], o0);
-            o1 = __builtin_fmaf(S[i + 1], q[i + 1], o1);
+                for (int e = 0; e < 4; e++) {
+                    S[4 * u + e] = __builtin_fmaf(k4[e], delta, S[4 * u + e]);
+                    o[e] = __builtin_fmaf(S[4 * u + e], q4[e], o[e]);
+                }
+            }
+            const float total = quad_sum((o[0] + o[1]) + (o[2] + o[3]));
+            if (r == 0) out[((size_t)h * n + t0 + tt) * kLd + j] = total;
         }
-        float o = o0 + o1;
-        o += __shfl_xor(o, 16);
-        o += __shfl_xor(o, 32);
-        if (r == 0) out[((size_t)h * n + t) * kLd + j] = o;
+        if (more) store(buf ^ 1);  // the other buffer: last read a whole chunk ago
+        __syncthreads();
     }
 }
 

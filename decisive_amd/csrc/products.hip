@@ -52,8 +52,18 @@ __global__ __launch_bounds__(256) void grouped_kernel(const uint8_t *__restrict_
     float4_t acc = {0.f, 0.f, 0.f, 0.f};
     const int4_t zero = {0, 0, 0, 0};
     const int8_t *qrow = q + (size_t)arow * groups * 64;
-    if (!nan_out) {
-        for (int g = 0; g < groups; g++) {
+    // Groups go in batches of B; batch i+1's loads are issued before batch i's
+    // products and folds, so each wait covers B groups. The fold stays in
+    // group order.
+    constexpr int B = 4;
+    struct Batch {
+        int4_t a[B], b[B];
+        float sw[B], sx[B][4];
+    };
+    auto fetch = [&](Batch &bt, int g0) {
+#pragma unroll
+        for (int u = 0; u < B; u++) {
+            const int g = min(g0 + u, groups - 1);  // past the end: a valid group, never folded
             int4_t a = zero, b;
             float sw;
             if (BITS == 4) {
@@ -72,13 +82,34 @@ __global__ __launch_bounds__(256) void grouped_kernel(const uint8_t *__restrict_
                 if (arow_ok) a = *(const int4_t *)(qrow + g * 64 + qd * 16);
                 sw = ((const float *)scales)[((size_t)t * kbs + g) * 16 + j];
             }
-            int4_t d = mfma_i8(a, b, zero);
+            bt.a[u] = a;
+            bt.b[u] = b;
+            bt.sw[u] = sw;
 #pragma unroll
             for (int v = 0; v < 4; v++) {
-                int r = mt * 16 + qd * 4 + v;
-                float sxv = r < m ? sx[(size_t)r * groups + g] : 0.0f;
-                acc[v] = __builtin_fmaf((float)d[v], __fmul_rn(sw, sxv), acc[v]);
+                const int r = mt * 16 + qd * 4 + v;
+                bt.sx[u][v] = r < m ? sx[(size_t)r * groups + g] : 0.0f;
             }
+        }
+    };
+    auto fold = [&](const Batch &bt, int g0) {
+#pragma unroll
+        for (int u = 0; u < B; u++) {
+            if (g0 + u >= groups) break;
+            const int4_t d = mfma_i8(bt.a[u], bt.b[u], zero);
+#pragma unroll
+            for (int v = 0; v < 4; v++) acc[v] = __builtin_fmaf((float)d[v], __fmul_rn(bt.sw[u], bt.sx[u][v]), acc[v]);
+        }
+    };
+    if (!nan_out) {
+        Batch x0, x1;
+        fetch(x0, 0);
+        for (int g0 = 0; g0 < groups; g0 += 2 * B) {
+            if (g0 + B < groups) fetch(x1, g0 + B);
+            fold(x0, g0);
+            if (g0 + B >= groups) break;
+            if (g0 + 2 * B < groups) fetch(x0, g0 + 2 * B);
+            fold(x1, g0 + B);
         }
     }
     const int col = t * 16 + j;
@@ -1658,7 +1689,7 @@ const char *const kGemmNames[] = {"pipe-auto",   "256x256p2w8", "128x128p2w4", "
                                    "256x128w2x2", "128x128w2x2", "128x64w2x2"};
 const char *const kI8Names[] = {"256x256p2w8", "256x256p4k64w8", "256x128p3w8", "256x128p3",
                                  "128x128w2x2", "256x128w2x2", "64x64w2x2"};
-const char *const kGroupedNames[] = {"pipe-auto", "pipe256x128w8", "wave16x16"};
+const char *const kGroupedNames[] = {"pipe-auto", "pipe256x128w8", "wave16x16", "pipe128x128w4", "pipe64x128w2"};
 
 template <int W, int MPAD, bool G32>
 void gemv_launch_one(const Weight &w, const half_t *x, int m, float *y, hipStream_t s) {
@@ -1828,7 +1859,7 @@ int variant_count(const char *family) {
     if (f == "gemv") return 2;
     if (f == "gemm_w4a16") return 7;
     if (f == "i8_gemm") return 7;
-    if (f == "grouped") return 3;
+    if (f == "grouped") return 5;
     return 0;
 }
 
@@ -1875,19 +1906,42 @@ void launch_grouped_records(const Weight &w, const uint32_t *records, int m, flo
 // one-wave-per-16x16-tile grouped_kernel, variant 0 ("auto") the first when
 // its grid covers at least half the compute units and the second otherwise.
 // All fold in the reference order, so all give the same bits.
+template <int BM, int WGM, int WGN>
+bool grouped_pipe_launch(const Weight &w, const int8_t *q, const float *sx, int m, float *y, const int *bad,
+                         hipStream_t s) {
+    if ((size_t)BM * w.groups * 64 >= ((size_t)1 << 31) || (size_t)8 * w.kblocks() * 1024 >= ((size_t)1 << 31))
+        return false;
+    const dim3 blocks(cdiv(m, BM) * cdiv(w.rows, 128));
+    if (w.bits == 4)
+        hipLaunchKernelGGL((grouped_pipe_kernel<4, BM, 128, WGM, WGN>), blocks, dim3(WGM * WGN * 64), 0, s, w.codes,
+                           w.scales, q, sx, m, w.rows, w.groups, w.kblocks(), y, bad);
+    else
+        hipLaunchKernelGGL((grouped_pipe_kernel<8, BM, 128, WGM, WGN>), blocks, dim3(WGM * WGN * 64), 0, s, w.codes,
+                           w.scales, q, sx, m, w.rows, w.groups, w.kblocks(), y, bad);
+    return true;
+}
+
+// Variants: 1 pipelined 256x128 tiles (8 waves), 3 128x128 (4 waves), 4 64x128
+// (2 waves), 2 one wave per 16x16 tile. 0 picks 128x128 tiles when their grid
+// covers half the compute units, else 64x128 tiles when that grid covers a
+// quarter, else the one-wave tiles (measured: 128x128 beats 256x128 by 5-15% at
+// every shape from 229x2560x12288 to 16384x4096x14336, and 64x128 wins below
+// the half-wave mark). Every variant folds in group order: all are bitwise equal.
 void launch_grouped(const Weight &w, const int8_t *q, const float *sx, int m, float *y,
                     const int *bad, int variant, hipStream_t s) {
     if (m == 0) return;
-    const bool pipe = variant == 1 || (variant == 0 && 2 * cdiv(m, 256) * cdiv(w.rows, 128) >= (unsigned)device_cus());
-    if (pipe && (size_t)256 * w.groups * 64 < ((size_t)1 << 31) && (size_t)8 * w.kblocks() * 1024 < ((size_t)1 << 31)) {
-        const dim3 blocks(cdiv(m, 256) * cdiv(w.rows, 128));
-        if (w.bits == 4)
-            hipLaunchKernelGGL((grouped_pipe_kernel<4, 256, 128, 2, 4>), blocks, dim3(512), 0, s, w.codes, w.scales, q,
-                               sx, m, w.rows, w.groups, w.kblocks(), y, bad);
-        else
-            hipLaunchKernelGGL((grouped_pipe_kernel<8, 256, 128, 2, 4>), blocks, dim3(512), 0, s, w.codes, w.scales, q,
-                               sx, m, w.rows, w.groups, w.kblocks(), y, bad);
-        return;
+    const unsigned cus = (unsigned)device_cus(), tn = cdiv(w.rows, 128);
+    int pick = variant;
+    if (variant == 0) {
+        if (cdiv(m, 128) * tn >= cus / 2) pick = 3;
+        else if (cdiv(m, 64) * tn >= cus / 4) pick = 4;
+        else pick = 2;
+    }
+    switch (pick) {
+        case 1: if (grouped_pipe_launch<256, 2, 4>(w, q, sx, m, y, bad, s)) return; break;
+        case 3: if (grouped_pipe_launch<128, 2, 2>(w, q, sx, m, y, bad, s)) return; break;
+        case 4: if (grouped_pipe_launch<64, 1, 2>(w, q, sx, m, y, bad, s)) return; break;
+        default: break;
     }
     dim3 grid(cdiv(w.tiles(), 4), cdiv(m, 16));
     if (w.bits == 4)

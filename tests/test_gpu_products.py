@@ -53,7 +53,8 @@ def test_grouped_large_m_pipeline_bit_exact(ctx, oracle, wb, ab, m, k, n):
     w = ctx.quantize(dev(raw), rocm.BF16, n, k, wb, 64)
     mode = rocm.W4A4 if ab == 4 else rocm.W4A8
     outs = []
-    for name in ("pipe256x128w8", "wave16x16"):
+    names = ("pipe256x128w8", "wave16x16", "pipe128x128w4", "pipe64x128w2", "pipe-auto")
+    for name in names:
         ctx.select_variant("grouped", name)
         y = empty((m, n), torch.float32)
         ctx.linear(w, dev(x), rocm.F32, m, y, mode)
@@ -62,7 +63,8 @@ def test_grouped_large_m_pipeline_bit_exact(ctx, oracle, wb, ab, m, k, n):
     codes, scales = oracle.weight_quantize(raw, n, k, wb)
     want = oracle.matrix_apply(x, m, codes, scales, n, k, ab, fused=True)
     assert bits_equal(outs[0], want), float(np.abs(outs[0] - want).max())
-    assert bits_equal(outs[1], outs[0])
+    for name, o in zip(names[1:], outs[1:]):
+        assert bits_equal(o, outs[0]), name
 
 
 def test_grouped_large_m_nonfinite_activation_makes_every_output_nan(ctx, oracle):
