@@ -112,6 +112,64 @@ def cpu_baseline(seconds: float = 10.0) -> dict:
                       f"Rust toolchain unavailable"}
 
 
+def encoder_cpu_baseline(seconds: float = 10.0) -> dict:
+    """Config 3's encoder layer on the host cores, for one 1024-token sequence:
+    the four projections by the reference's CPU W4A8 algorithm (C restatement
+    of int8.rs:229-585, AVX2 rows<4,Q4>, threaded), attention by numpy float32
+    matrix products (the reference's CPU attention is an sgemm), LayerNorm and
+    GELU vectorized in numpy. Layers run until `seconds` have passed; the
+    per-layer time is scaled to the 24-layer forward."""
+    from oracle import oracle as o
+    from scipy.special import erf
+    if not o.has_avx2():
+        return {"value": None, "unit": "embeddings/s", "cores": 0, "kind": "port", "sample": "AVX2 unavailable"}
+    threads = max(1, min(16, os.cpu_count() or 1))
+    d, heads, hd, ff, seq, layers = 1024, 16, 64, 4096, 1024, 24
+    rng = np.random.default_rng(1)
+    panels = []
+    for rows, cols in ((3 * d, d), (d, d), (ff, d), (d, ff)):
+        w = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
+        codes, scales = o.weight_quantize(o.f32_to_bf16(w), rows, cols, 4)
+        panels.append((o.panel_pack(codes, scales, rows, cols, 4), rows, cols))
+    del w
+
+    def apply(i, x):
+        (data, ps), rows, cols = panels[i]
+        qx, sx = o.act_quantize(x, x.shape[0], cols, 8)
+        return o.panel_apply_avx2(data, ps, rows, cols, 4, qx, sx, x.shape[0], threads)
+
+    def layernorm(x):
+        mu = x.mean(1, keepdims=True)
+        c = x - mu
+        return (c / np.sqrt((c * c).mean(1, keepdims=True) + 1e-5)).astype(np.float32)
+
+    def layer(h):
+        qkv = apply(0, h)
+        att = np.empty((seq, d), np.float32)
+        for a in range(heads):
+            q, k, v = (qkv[:, j * d + a * hd:j * d + (a + 1) * hd] for j in range(3))
+            sc = (q @ k.T) * np.float32(1 / 8)
+            p = np.exp(sc - sc.max(1, keepdims=True))
+            att[:, a * hd:(a + 1) * hd] = (p @ v) / p.sum(1, keepdims=True)
+        h = layernorm(apply(1, att) + h)
+        f = apply(2, h)
+        f = (0.5 * f * (1.0 + erf(f * np.float32(0.70710678)))).astype(np.float32)
+        return layernorm(apply(3, f) + h)
+
+    h = layernorm(rng.standard_normal((seq, d)).astype(np.float32))
+    done, start = 0, time.perf_counter()
+    while done < 2 or time.perf_counter() - start < seconds:
+        h = layer(h)
+        done += 1
+    elapsed = time.perf_counter() - start
+    assert np.isfinite(h).all()
+    per_sequence = elapsed / done * layers
+    return {"value": float(f"{1.0 / per_sequence:.4g}"), "unit": "embeddings/s", "cores": threads, "kind": "port",
+            "sample": f"{done} encoder layers of one 1024-token sequence in {elapsed:.1f} s, scaled to 24 layers "
+                      f"(W4A8 AVX2 products on {threads} threads, numpy f32 attention/LayerNorm/GELU; one "
+                      f"layer's weights reused); Rust toolchain unavailable"}
+
+
 def gemv_lines(torch, ctx, rocm, weights, stream) -> dict:
     """Config 2 at M = 4 and 8 (W4A16) and the bit-exact W4A8 GEMV at M = 1."""
     out = {}
@@ -154,7 +212,7 @@ def w4a8_line(torch, ctx, rocm, stream) -> dict:
             "note": "one launch per product: activation quantization inside the grouped kernel (hip graph)"}
 
 
-def secondary(torch, ctx, rocm, stream) -> dict:
+def secondary(torch, ctx, rocm, stream, cpu=True) -> dict:
     out = {}
     # config 4: int8 GEMM M=8192 K=N=4096
     m, n, k = 8192, 4096, 4096
@@ -243,7 +301,82 @@ def secondary(torch, ctx, rocm, stream) -> dict:
                                        "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1),
                                        "frac_of_f16_peak": round(flops / (ms * 1e-3) / 1e12 / F16_PEAK_TFLOPS, 4)}
     enc.close()
+    if cpu:
+        out["encoder_forward_b8_s1024"]["cpu_baseline"] = encoder_cpu_baseline()
+    # the Pplx decider at real size, one 1024-token chunk
+    out["pplx_decider_forward_s1024"] = pplx_line(torch, ctx, rocm, stream)
     return out
+
+
+def random_wire(rng, rows: int, cols: int, std: float = 0.02) -> np.ndarray:
+    """A random Q4 g64/f32 wire matrix (packed.rs:3-56): codes uniform in
+    [-7, 7] (nibbles code + 8), each group's f32 scale near std / 4.3 so the
+    weights have about the standard deviation `std`."""
+    groups = cols // 64
+    wire = np.empty((rows, groups, 36), np.uint8)
+    nib = rng.integers(1, 16, (rows, groups, 32, 2), dtype=np.uint8)
+    wire[..., :32] = nib[..., 0] | (nib[..., 1] << 4)
+    scale = (std / 4.3) * rng.uniform(0.8, 1.2, (rows, groups)).astype(np.float32)
+    wire[..., 32:] = scale.astype(np.float32)[..., None].view(np.uint8)
+    return wire.reshape(-1)
+
+
+def pplx_line(torch, ctx, rocm, stream, n: int = 1024, layers: int = 32) -> dict:
+    """The Pplx decider (backbone.rs:11-22 shape: 32 layers, hidden 2560, three
+    gated-delta layers then one gated-attention layer, FFN 9216) on one chunk
+    of `n` tokens with 4 answer markers, through dz_pplx_forward_rows: packed
+    embedding rows in, logits out (both host buffers, so the 3.7 MB row copy is
+    inside the timed region). Random wire weights: one delta layer's and one
+    attention layer's tensors, uploaded to every layer of that kind (each
+    layer holds its own device copy)."""
+    cfg = rocm.PplxConfig(layers=layers, hidden=2560, ff=9216, delta_heads=32, delta_key_heads=16,
+                          delta_head_dim=128, attn_heads=16, attn_kv_heads=4, attn_head_dim=256)
+    d, ff, ld, ad = 2560, 9216, 128, 256
+    cw = 2 * 16 * ld + 32 * ld
+    rng = np.random.default_rng(5)
+    delta = {"linear_attn.in_proj_qkv.weight": (cw, d), "linear_attn.in_proj_z.weight": (32 * ld, d),
+             "linear_attn.in_proj_a.weight": (32, d), "linear_attn.in_proj_b.weight": (32, d),
+             "linear_attn.out_proj.weight": (d, 32 * ld)}
+    attn = {"self_attn.q_proj.weight": (2 * 16 * ad, d), "self_attn.k_proj.weight": (4 * ad, d),
+            "self_attn.v_proj.weight": (4 * ad, d), "self_attn.o_proj.weight": (d, 16 * ad)}
+    mlp = {"mlp.gate_proj.weight": (ff, d), "mlp.up_proj.weight": (ff, d), "mlp.down_proj.weight": (d, ff)}
+    wires = {name: (random_wire(rng, r, c), r, c) for name, (r, c) in {**delta, **attn, **mlp}.items()}
+    vec = lambda size, scale, base=0.0: (base + rng.standard_normal(size) * scale).astype(np.float32)
+    vectors = {"linear_attn.conv1d.weight": vec(cw * 4, 0.4), "linear_attn.A_log": np.log(
+        rng.uniform(1.0, 16.0, 32)).astype(np.float32), "linear_attn.dt_bias": vec(32, 0.5),
+        "linear_attn.norm.weight": vec(ld, 0.1, 1.0), "self_attn.q_norm.weight": vec(ad, 0.1),
+        "self_attn.k_norm.weight": vec(ad, 0.1)}
+    norms = {"input_layernorm.weight": vec(d, 0.1), "post_attention_layernorm.weight": vec(d, 0.1)}
+    p = ctx.pplx_create(cfg)
+    for i in range(layers):
+        names = attn if i % 4 == 3 else delta
+        for name in list(names) + list(mlp):
+            wire, r, c = wires[name]
+            p.set_weight(f"language_model.layers.{i}.{name}", wire, rocm.Q4_G64_F32, r, c)
+        mixer = "self_attn." if i % 4 == 3 else "linear_attn."
+        for name, values in {**vectors, **norms}.items():
+            if name in norms or name.startswith(mixer):
+                p.set_vector(f"language_model.layers.{i}.{name}", values)
+    p.set_vector("language_model.norm.weight", vec(d, 0.1))
+    p.set_weight("readout", random_wire(rng, 255, d, 0.05), rocm.Q4_G64_F32, 255, d)
+    del wires
+    rows = random_wire(rng, n, d, 1.0).reshape(n, -1)
+    markers = [n - 1, n // 2, n // 3, 0]
+    logits = p.forward_rows(rows, n, markers)
+    assert np.isfinite(logits).all()
+    torch.cuda.synchronize()
+    reps = 5
+    wall = time.perf_counter()
+    ms = timed_ms(torch, stream, lambda r: p.forward_rows(rows, n, markers), reps)
+    wall = (time.perf_counter() - wall) * 1e3 / reps
+    p.close()
+    prods = 24 * 2 * n * (d * (cw + 32 * ld + 64) + 32 * ld * d) + 8 * 2 * n * (d * (2 * 16 * ad + 8 * ad) + 16 * ad * d)
+    prods += layers * 2 * n * 3 * d * ff
+    return {"ms": round(ms, 3), "wall_ms": round(wall, 3), "sequences/s": round(1e3 / ms, 2),
+            "tokens/s": round(n * 1e3 / ms, 1), "product_TOP/s": round(prods / (ms * 1e-3) / 1e12, 1),
+            "note": f"{layers} layers (24 gated-delta, 8 gated-attention), hidden 2560, one chunk of {n} tokens, "
+                    "4 markers; W4A8 products bit-exact with the CPU path; random Q4 g64 wire weights; "
+                    "host rows in and logits out inside the timed region"}
 
 
 def traffic_per_launch():
@@ -266,6 +399,7 @@ def main():
     ap.add_argument("--calibrate-copy", action="store_true",
                     help=f"also run a {COPY_BYTES >> 20} MiB device copy (counter calibration)")
     ap.add_argument("--tune", type=int, default=0, help="tuner budget in ms (0 keeps reference variants)")
+    ap.add_argument("--only", choices=["pplx"], help="run one secondary line alone and print it (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -279,6 +413,14 @@ def main():
     if args.tune:
         ctx.tune(args.tune)
     log(f"[bench] device {ctx.info()}")
+    if args.only == "pplx":
+        stream = torch.cuda.Stream()
+        ctx.set_stream(stream.cuda_stream)
+        with torch.cuda.stream(stream):
+            line = pplx_line(torch, ctx, rocm, stream)
+        ctx.set_stream(None)
+        print(json.dumps({"pplx_decider_forward_s1024": line}), flush=True)
+        return
 
     if args.calibrate_copy:
         src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device="cuda")
@@ -379,7 +521,7 @@ def main():
                 wgt.free()
             weights.clear()
             sec["q4_gemv_w4a8_m1_k4096_n4096_g64f32"] = w4a8_line(torch, ctx, rocm, stream)
-            sec.update(secondary(torch, ctx, rocm, stream))
+            sec.update(secondary(torch, ctx, rocm, stream, cpu=not args.no_cpu))
         result["secondary"] = sec
     ctx.set_stream(None)
     print(json.dumps(result), flush=True)

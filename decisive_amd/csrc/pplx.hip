@@ -312,6 +312,133 @@ __global__ __launch_bounds__(64) void attention_kernel(const float *__restrict__
         float4_t{acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
 }
 
+// Flash attention on f32 MFMA (v_mfma_f32_16x16x4_f32): one workgroup per
+// (16 queries, key/value head), one wave per query head of that group (GQA),
+// so the K/V blocks staged in LDS serve every head that reads them.
+// Per block of 32 keys a wave forms S^T = K Q^T (keys as MFMA rows, queries as
+// columns: each lane then holds 8 scores of one query), updates that query's
+// running maximum and sum, and adds V^T P^T into its 16 x 256 output tile.
+// The contraction index of S^T runs over dims as 64 * (lane / 16) + step, so a
+// lane's K operands are 16 consecutive float4s of one key row; K rows are
+// padded by 16 bytes so those reads from 16 keys hit distinct banks. Output
+// tile (s, u) row r is dim 64s + 4r + u, so one float4 of a V row feeds four
+// MFMAs. K/V blocks are double-buffered and loaded straight into LDS; keys
+// past the end load the last key's row and score -inf.
+constexpr int kAttnKeys = 32;
+constexpr int kAttnKRow = kAd * 4 + 16;
+constexpr int kAttnVRow = kAd * 4;
+constexpr int kAttnBuf = kAttnKeys * (kAttnKRow + kAttnVRow);
+constexpr int kAttnLds = 2 * kAttnBuf;
+constexpr int kAttnMaxGroup = 8;
+
+__global__ __launch_bounds__(kAttnMaxGroup * 64) void attention_mfma_kernel(
+    const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v, size_t v_row, int nq,
+    int nk, int ah, int akv, float scale, float *__restrict__ out) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int group = blockDim.x / 64;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), lane = threadIdx.x % 64;
+    const int kh = blockIdx.y, h = kh * group + wave;
+    const int col = lane % 16, g = lane / 16;
+    const int t = blockIdx.x * 16 + col;
+    float qv[64];
+    {
+        const float *src = q + ((size_t)(t < nq ? t : 0) * ah + h) * kAd + 64 * g;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const float4_t x = t < nq ? *(const float4_t *)(src + 4 * i) : float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int e = 0; e < 4; e++) qv[4 * i + e] = __fmul_rn(x[e], scale);
+        }
+    }
+    const int32x4_t krs = buffer_rsrc(k, (uint32_t)((size_t)nk * akv * kAd * 4));
+    const int32x4_t vrs = buffer_rsrc(v, (uint32_t)((size_t)nk * v_row * 4));
+    const uint32_t base = lds_address(lds);
+    auto issue = [&](int blk, int buf) {
+        const uint32_t kb = base + (uint32_t)(buf * kAttnBuf), vb = kb + kAttnKeys * kAttnKRow;
+        for (int r = wave; r < 2 * kAttnKeys; r += group) {
+            const int key = min(blk * kAttnKeys + r % kAttnKeys, nk - 1);
+            if (r < kAttnKeys)
+                dma16(kb + r * kAttnKRow, (uint32_t)(((size_t)key * akv + kh) * kAd * 4) + lane * 16, krs);
+            else
+                dma16(vb + (r - kAttnKeys) * kAttnVRow,
+                      (uint32_t)(((size_t)key * v_row + (size_t)kh * kAd) * 4) + lane * 16, vrs);
+        }
+    };
+    float4_t o[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) o[i] = float4_t{0.f, 0.f, 0.f, 0.f};
+    float m = -INFINITY, lsum = 0.0f;
+    const int nb = (nk + kAttnKeys - 1) / kAttnKeys;
+    issue(0, 0);
+    for (int b = 0; b < nb; b++) {
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // this wave's block-b loads have landed
+        __syncthreads();                     // every wave's have; block b-1's buffer is free
+        if (b + 1 < nb) issue(b + 1, (b + 1) & 1);
+        const uint8_t *kt = lds + (b & 1) * kAttnBuf, *vt = kt + kAttnKeys * kAttnKRow;
+        float4_t st[2];
+#pragma unroll
+        for (int T = 0; T < 2; T++) {
+            st[T] = float4_t{0.f, 0.f, 0.f, 0.f};
+            const uint8_t *kr = kt + (16 * T + col) * kAttnKRow + 256 * g;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const float4_t kk = *(const float4_t *)(kr + 16 * i);
+#pragma unroll
+                for (int e = 0; e < 4; e++) st[T] = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[e], qv[4 * i + e], st[T], 0, 0, 0);
+            }
+        }
+        float bm = -INFINITY;
+#pragma unroll
+        for (int T = 0; T < 2; T++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                if (b * kAttnKeys + 16 * T + 4 * g + i >= nk) st[T][i] = -INFINITY;
+                bm = fmaxf(bm, st[T][i]);
+            }
+        bm = fmaxf(bm, __shfl_xor(bm, 16));
+        bm = fmaxf(bm, __shfl_xor(bm, 32));
+        const float mn = fmaxf(m, bm);
+        const float alpha = expf(m - mn);
+        m = mn;
+        lsum = __fmul_rn(lsum, alpha);
+#pragma unroll
+        for (int i = 0; i < 16; i++) o[i] = o[i] * alpha;
+        float pv[2][4];
+#pragma unroll
+        for (int T = 0; T < 2; T++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                pv[T][i] = expf(st[T][i] - m);
+                lsum = __fadd_rn(lsum, pv[T][i]);
+            }
+#pragma unroll
+        for (int T = 0; T < 2; T++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint8_t *vr = vt + (16 * T + 4 * g + i) * kAttnVRow + 16 * col;
+#pragma unroll
+                for (int S = 0; S < 4; S++) {
+                    const float4_t vv = *(const float4_t *)(vr + 256 * S);
+#pragma unroll
+                    for (int u = 0; u < 4; u++)
+                        o[4 * S + u] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[u], pv[T][i], o[4 * S + u], 0, 0, 0);
+                }
+            }
+    }
+    lsum = __fadd_rn(lsum, __shfl_xor(lsum, 16));
+    lsum = __fadd_rn(lsum, __shfl_xor(lsum, 32));
+    if (t < nq) {
+        const float inv = 1.0f / lsum;
+        float *dst = out + ((size_t)h * nq + t) * kAd + 16 * g;
+#pragma unroll
+        for (int S = 0; S < 4; S++)
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                *(float4_t *)(dst + 64 * S + 4 * i) =
+                    float4_t{o[4 * S][i] * inv, o[4 * S + 1][i] * inv, o[4 * S + 2][i] * inv, o[4 * S + 3][i] * inv};
+    }
+}
+
 // out[t][h*256 + i] = heads[h][t][i] * sigmoid(z), z at zsrc + t*z_row + h*z_head + i
 __global__ void attention_gate_kernel(const float *__restrict__ heads, int n, int ah,
                                       const float *__restrict__ zsrc, size_t z_row, int z_head,
@@ -661,6 +788,32 @@ int32_t delta_layer(dz_ctx *ctx, dz_pplx *p, const dz_pplx::Layer &L, size_t n) 
     return DZ_OK;
 }
 
+// The MFMA kernel for query-head groups of up to 8 (the reference's 4) and
+// K/V byte offsets within 32 bits; the one-wave-per-query kernel otherwise.
+void launch_attention(dz_ctx *ctx, dz_pplx *p, size_t nq, size_t n, hipStream_t s) {
+    const dz_pplx_config &c = p->cfg;
+    const size_t kvw = (size_t)c.attn_kv_heads * kAd;
+    const int group = c.attn_heads / c.attn_kv_heads;
+    if (group <= kAttnMaxGroup && n * kvw * sizeof(float) < ((size_t)1 << 31)) {
+        static bool configured[64] = {};  // the LDS limit is a per-device function attribute
+        int dev = 0;
+        hipGetDevice(&dev);
+        if (dev >= 0 && dev < 64 && !configured[dev]) {
+            hipFuncSetAttribute((const void *)attention_mfma_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                kAttnLds);
+            configured[dev] = true;
+        }
+        hipLaunchKernelGGL(attention_mfma_kernel, dim3((unsigned)((nq + 15) / 16), c.attn_kv_heads),
+                           dim3(64 * group), kAttnLds, s, p->query, p->key, p->value, kvw, (int)nq, (int)n,
+                           c.attn_heads, c.attn_kv_heads, 1.0f / 16.0f, p->heads);
+        return;
+    }
+    (void)ctx;
+    const size_t lds = (kAd + n) * sizeof(float);
+    hipLaunchKernelGGL(attention_kernel, dim3(c.attn_heads, (unsigned)nq), dim3(64), lds, s, p->query, p->key,
+                       p->value, kvw, (int)nq, (int)n, c.attn_heads, c.attn_kv_heads, 1.0f / 16.0f, p->heads);
+}
+
 // backbone.rs:471-615; with `markers` (count rows) the queries and the
 // hidden rows are cut to the markers (the reference's prune_last).
 int32_t attention_layer(dz_ctx *ctx, dz_pplx *p, const dz_pplx::Layer &L, size_t n, const int32_t *markers,
@@ -685,9 +838,7 @@ int32_t attention_layer(dz_ctx *ctx, dz_pplx *p, const dz_pplx::Layer &L, size_t
                        c.attn_heads, L.qnorm, markers, p->freq, p->query);
     hipLaunchKernelGGL(head_norm_rope_kernel, dim3((unsigned)n, c.attn_kv_heads), dim3(64), 0, s, p->key, kvw, kAd,
                        c.attn_kv_heads, L.knorm, nullptr, p->freq, p->key);
-    const size_t lds = (kAd + n) * sizeof(float);
-    hipLaunchKernelGGL(attention_kernel, dim3(c.attn_heads, (unsigned)nq), dim3(64), lds, s, p->query, p->key,
-                       p->value, kvw, (int)nq, (int)n, c.attn_heads, c.attn_kv_heads, 1.0f / 16.0f, p->heads);
+    launch_attention(ctx, p, nq, n, s);
     hipLaunchKernelGGL(attention_gate_kernel, dim3(blocks_of(nq * c.attn_heads * kAd, 256)), dim3(256), 0, s,
                        p->heads, (int)nq, c.attn_heads, p->wide + kAd, qw, 2 * kAd, p->ctx);
     rc = linear(ctx, L.o, p->ctx, nq, p->projected);

@@ -75,6 +75,26 @@ def test_forward_logits_match_the_reference_chunk(ctx, oracle, small, n):
     assert close(got, want, rel=1e-2), (float(cosine(got, want)), float(np.abs(got - want).max()))
 
 
+# four query heads per key/value head, as the reference model has
+GQA4 = dict(SMALL, attn_heads=8, attn_kv_heads=2)
+
+
+@pytest.mark.parametrize("n,markers", [(300, None), (77, [76, 3, 40])])
+def test_attention_layer_with_head_groups_of_four(ctx, oracle, n, markers):
+    """Several 32-key blocks with a ragged tail, every query block, and the
+    marker-pruned form, with the reference's group of four query heads."""
+    torch = pytest.importorskip("torch")
+    model = pplx_model.random_model(oracle, dict(GQA4, layers=4), seed=9)
+    p = pplx_model.load(ctx, rocm, model)
+    h = np.random.default_rng(n).standard_normal((n, GQA4["hidden"])).astype(np.float32)
+    hd = dev(h)
+    p.layer(3, hd, n, markers)
+    got = host(ctx, hd)[:n if markers is None else len(markers)]
+    want = pplx_model.ref_layer(oracle, model, 3, h, markers)
+    p.close()
+    assert close(got, want), (float(cosine(got, want)), float(np.abs(got - want).max()))
+
+
 def test_delta_scan_state_carries_across_tokens(ctx, oracle, small):
     """The last token's output depends on the first token (the recurrent
     state): changing only token 0 changes the output at token n-1."""
