@@ -80,7 +80,8 @@ __global__ void conv_silu_kernel(const float *__restrict__ x, int n, int width, 
 }
 
 // One block per token, one wave per key head: unit q and k (q also scaled by
-// 1/sqrt(ld)); threads below lh compute the decay g and beta of head h.
+// 1/sqrt(ld)) and their dot product; threads below lh compute the decay g and
+// beta of head h. Record (t, h) of gb holds {g, beta, k.q of h's key head, 0}.
 __global__ void delta_prep_kernel(const float *__restrict__ conv, int lh, int lk, const float *__restrict__ a,
                                   const float *__restrict__ b, const float *__restrict__ decay,
                                   const float *__restrict__ dt, float *__restrict__ qhat,
@@ -95,81 +96,104 @@ __global__ void delta_prep_kernel(const float *__restrict__ conv, int lh, int lk
         const float ki = rsqrt_rn(__fadd_rn(wave_sum(k0 * k0 + k1 * k1), 1e-6f));
         const float root = rsqrt_rn((float)kLd);
         float *qd = qhat + ((size_t)t * lk + wave) * kLd, *kd = khat + ((size_t)t * lk + wave) * kLd;
-        qd[lane] = __fmul_rn(__fmul_rn(q0, qi), root);
-        qd[lane + 64] = __fmul_rn(__fmul_rn(q1, qi), root);
-        kd[lane] = __fmul_rn(k0, ki);
-        kd[lane + 64] = __fmul_rn(k1, ki);
+        const float qa = __fmul_rn(__fmul_rn(q0, qi), root), qb = __fmul_rn(__fmul_rn(q1, qi), root);
+        const float ka = __fmul_rn(k0, ki), kb = __fmul_rn(k1, ki);
+        qd[lane] = qa;
+        qd[lane + 64] = qb;
+        kd[lane] = ka;
+        kd[lane + 64] = kb;
+        const float kq = wave_sum(__builtin_fmaf(ka, qa, kb * qb));
+        const int per = lh / lk;
+        if (lane < per) gb[((size_t)t * lh + wave * per + lane) * 4 + 2] = kq;
     }
     for (int h = threadIdx.x; h < lh; h += blockDim.x) {
         const float x = __fadd_rn(a[(size_t)t * lh + h], dt[h]);
         const float softplus = x > 20.0f ? x : log1pf(expf(x));
-        gb[((size_t)t * lh + h) * 2] = expf(__fmul_rn(-decay[h], softplus));
-        gb[((size_t)t * lh + h) * 2 + 1] = sigmoid_ref(b[(size_t)t * lh + h]);
+        gb[((size_t)t * lh + h) * 4] = expf(__fmul_rn(-decay[h], softplus));
+        gb[((size_t)t * lh + h) * 4 + 1] = sigmoid_ref(b[(size_t)t * lh + h]);
     }
 }
 
-// The gated delta rule. A wave owns 16 state columns j of head h; lane
-// (c, r) = (lane / 4, lane % 4) holds rows [32r, 32r + 32) of column
-// 16*blockIdx.y + c in registers. Per token: S *= g; mem = S^T k;
-// delta = (v - mem) beta; S += k delta^T; out = S^T q. The sums over the four
-// row groups close inside each lane quad with two DPP adds. Tokens are staged
-// in LDS sixteen at a time; the next chunk's loads are in flight while this
-// chunk computes.
-__device__ __forceinline__ float quad_sum(float v) {
-    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
-    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
-    return v;
+// The gated delta rule. A block of 4 waves owns 8 state columns of head h
+// (blockIdx.y selects which 8); in each wave, lanes 32c..32c+31 hold column
+// 8*blockIdx.y + 2*wave + c, lane r of the half holding state rows 4r..4r+3
+// in registers. Per token the reference's steps (S *= g; mem = S^T k;
+// delta = (v - mem) beta; S += k delta^T; out = S^T q) are regrouped so that
+// both sums read the previous state: mem = g (S^T k), out = g (S^T q) +
+// delta (k.q) (k.q from delta_prep), S = g S + k delta^T; the two sums then
+// close together and the chain from one token to the next is short. A sum
+// over a half closes with four DPP adds inside each 16-lane row (xor 1, xor 2,
+// rotate 4, rotate 8) and one row swap (v_permlane16_swap), which leave the
+// total in every lane; lane r keeps token t0 + r's output and the wave stores
+// a whole chunk at once. Tokens are staged in LDS sixteen at a time, shared
+// by the four waves; the next chunk's loads are in flight while this chunk
+// computes. 512 blocks cover the 32 heads of the reference model, two waves
+// per SIMD.
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float half_sum(float v) {
+    v += dpp_move<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_move<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_move<0x124>(v);  // row_ror:4
+    v += dpp_move<0x128>(v);  // row_ror:8
+    // rows (0, 1) and (2, 3) exchange (v_permlane16_swap: odd rows of the
+    // first operand trade places with even rows of the second), so a + b holds
+    // both rows' sums in every lane. Issued as asm: this compiler's builtin
+    // for it returns the first result twice. The nops cover the VALU-write /
+    // permlane-read wait states on either side.
+    float a = v, b = v;
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+    return a + b;
 }
 
-constexpr int kScanChunk = 16;       // tokens staged in LDS at a time
-constexpr int kScanRow = 4 * 36;      // one token's k (or q): four row groups of 32, padded to 36
+constexpr int kScanChunk = 16;  // tokens staged in LDS at a time
+constexpr int kScanWaves = 4;
+constexpr int kScanCols = 2 * kScanWaves;  // state columns per block
 
-__global__ __launch_bounds__(64) void delta_scan_kernel(const float *__restrict__ qhat,
-                                                        const float *__restrict__ khat,
-                                                        const float *__restrict__ conv,
-                                                        const float *__restrict__ gb, int n, int lh, int lk,
-                                                        float *__restrict__ out) {
-    constexpr int R = kLd / 4, T = kScanChunk;
-    // two chunk buffers: k and q rows (padded so the four row groups fall in
-    // different banks), v of the block's 16 columns, g and beta
-    __shared__ __align__(16) float ks[2][T * kScanRow], qs[2][T * kScanRow], vs[2][T * 16], gs[2][T * 2];
-    const int h = blockIdx.x, lane = threadIdx.x, r = lane % 4, c = lane / 4;
-    const int j0 = blockIdx.y * 16, j = j0 + c;
+__global__ __launch_bounds__(kScanWaves * 64) void delta_scan_kernel(const float *__restrict__ qhat,
+                                                                     const float *__restrict__ khat,
+                                                                     const float *__restrict__ conv,
+                                                                     const float *__restrict__ gb, int n, int lh,
+                                                                     int lk, float *__restrict__ out) {
+    constexpr int T = kScanChunk;
+    __shared__ __align__(16) float ks[2][T * kLd], qs[2][T * kLd], vs[2][T * kScanCols], gs[2][T * 4];
+    const int h = blockIdx.x, tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
+    const int r = lane % 32, c = lane / 32;
+    const int j0 = blockIdx.y * kScanCols, j = j0 + 2 * wave + c;
     const int kh = h / (lh / lk);
     const size_t lkv = (size_t)lk * kLd, width = 2 * lkv + (size_t)lh * kLd;
-    float S[R];
-#pragma unroll
-    for (int i = 0; i < R; i++) S[i] = 0.0f;
-    // staging registers: 8 + 8 float4 of k and q rows, one float4 of v, g/beta
-    float4_t rk[8], rq[8], rv;
-    float2 rg;
+    constexpr int KQ = T * kLd / 4 / (kScanWaves * 64);  // float4s of k (and of q) per thread
+    float S[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    // staging registers: KQ float4s of k and of q per thread, v for the first
+    // threads, the {g, beta, k.q} records for the first 16
+    float4_t rk[KQ], rq[KQ], rv, rg;
     auto load = [&](int t0) {
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int id = lane + 64 * i, tt = id / 32, u = id % 32, t = t0 + tt;
-            const size_t row = ((size_t)min(t, n - 1) * lk + kh) * kLd + 4 * u;
+        for (int i = 0; i < KQ; i++) {
+            const int id = tid + kScanWaves * 64 * i;
+            const int t = min(t0 + id / 32, n - 1);
+            const size_t row = ((size_t)t * lk + kh) * kLd + 4 * (id % 32);
             rk[i] = *(const float4_t *)(khat + row);
             rq[i] = *(const float4_t *)(qhat + row);
         }
-        {
-            const int tt = lane / 4, part = lane % 4, t = min(t0 + tt, n - 1);
-            rv = *(const float4_t *)(conv + (size_t)t * width + 2 * lkv + (size_t)h * kLd + j0 + 4 * part);
+        if (tid < T * kScanCols / 4) {
+            const int tv = min(t0 + tid / (kScanCols / 4), n - 1);
+            rv = *(const float4_t *)(conv + (size_t)tv * width + 2 * lkv + (size_t)h * kLd + j0 +
+                                     4 * (tid % (kScanCols / 4)));
         }
-        if (lane < T) {
-            const int t = min(t0 + lane, n - 1);
-            rg = *(const float2 *)(gb + ((size_t)t * lh + h) * 2);
-        }
+        if (tid < T) rg = *(const float4_t *)(gb + ((size_t)min(t0 + tid, n - 1) * lh + h) * 4);
     };
     auto store = [&](int buf) {
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int id = lane + 64 * i, tt = id / 32, u = id % 32;
-            const int at = tt * kScanRow + (u / 8) * 36 + (u % 8) * 4;
-            *(float4_t *)(&ks[buf][at]) = rk[i];
-            *(float4_t *)(&qs[buf][at]) = rq[i];
+        for (int i = 0; i < KQ; i++) {
+            const int id = tid + kScanWaves * 64 * i;
+            *(float4_t *)(&ks[buf][4 * id]) = rk[i];
+            *(float4_t *)(&qs[buf][4 * id]) = rq[i];
         }
-        *(float4_t *)(&vs[buf][(lane / 4) * 16 + 4 * (lane % 4)]) = rv;
-        if (lane < T) *(float2 *)(&gs[buf][lane * 2]) = rg;
+        if (tid < T * kScanCols / 4) *(float4_t *)(&vs[buf][4 * tid]) = rv;
+        if (tid < T) *(float4_t *)(&gs[buf][4 * tid]) = rg;
     };
     if (n > 0) {
         load(0);
@@ -180,34 +204,29 @@ __global__ __launch_bounds__(64) void delta_scan_kernel(const float *__restrict_
         const bool more = t0 + T < n;
         if (more) load(t0 + T);  // in flight while this chunk computes
         const int count = min(T, n - t0);
+        float keep = 0.0f;
         for (int tt = 0; tt < count; tt++) {
-            const float *kr = &ks[buf][tt * kScanRow + r * 36], *qr = &qs[buf][tt * kScanRow + r * 36];
-            const float g = gs[buf][tt * 2], beta = gs[buf][tt * 2 + 1], v = vs[buf][tt * 16 + c];
-            float m[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            const float g = gs[buf][tt * 4], beta = gs[buf][tt * 4 + 1], kq = gs[buf][tt * 4 + 2];
+            const float v = vs[buf][tt * kScanCols + 2 * wave + c];
+            const float4_t k4 = *(const float4_t *)(&ks[buf][tt * kLd + 4 * r]);
+            const float4_t q4 = *(const float4_t *)(&qs[buf][tt * kLd + 4 * r]);
+            // S^T k and S^T q over the previous state, reduced together
+            float m0 = S[0] * k4[0], m1 = S[1] * k4[1], p0 = S[0] * q4[0], p1 = S[1] * q4[1];
+            m0 = __builtin_fmaf(S[2], k4[2], m0);
+            m1 = __builtin_fmaf(S[3], k4[3], m1);
+            p0 = __builtin_fmaf(S[2], q4[2], p0);
+            p1 = __builtin_fmaf(S[3], q4[3], p1);
 #pragma unroll
-            for (int u = 0; u < R / 4; u++) {
-                const float4_t k4 = *(const float4_t *)(kr + 4 * u);
+            for (int e = 0; e < 4; e++) S[e] *= g;
+            const float sk = half_sum(m0 + m1), sq = half_sum(p0 + p1);
+            // S = g S + k delta^T with delta = (v - g S^T k) beta; out = g S^T q + delta (k.q)
+            const float delta = (v - g * sk) * beta;
 #pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    S[4 * u + e] *= g;
-                    m[e] = __builtin_fmaf(S[4 * u + e], k4[e], m[e]);
-                }
-            }
-            const float mem = quad_sum((m[0] + m[1]) + (m[2] + m[3]));
-            const float delta = (v - mem) * beta;
-            float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int u = 0; u < R / 4; u++) {
-                const float4_t k4 = *(const float4_t *)(kr + 4 * u), q4 = *(const float4_t *)(qr + 4 * u);
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    S[4 * u + e] = __builtin_fmaf(k4[e], delta, S[4 * u + e]);
-                    o[e] = __builtin_fmaf(S[4 * u + e], q4[e], o[e]);
-                }
-            }
-            const float total = quad_sum((o[0] + o[1]) + (o[2] + o[3]));
-            if (r == 0) out[((size_t)h * n + t0 + tt) * kLd + j] = total;
+            for (int e = 0; e < 4; e++) S[e] = __builtin_fmaf(k4[e], delta, S[e]);
+            const float total = __builtin_fmaf(g, sq, delta * kq);
+            keep = r == tt ? total : keep;
         }
+        if (r < count) out[((size_t)h * n + t0 + r) * kLd + j] = keep;
         if (more) store(buf ^ 1);  // the other buffer: last read a whole chunk ago
         __syncthreads();
     }
@@ -526,7 +545,7 @@ int32_t ensure_capacity(dz_ctx *ctx, dz_pplx *p, size_t n) {
     get(&p->conv_out, n * cw * 4);
     get(&p->qhat, n * c.delta_key_heads * kLd * 4);
     get(&p->khat, n * c.delta_key_heads * kLd * 4);
-    get(&p->gb, n * c.delta_heads * 2 * 4);
+    get(&p->gb, n * c.delta_heads * 4 * 4);
     get(&p->heads, n * std::max(lv, (size_t)c.attn_heads * kAd) * 4);
     get(&p->ctx, n * ctxw * 4);
     get(&p->projected, n * d * 4);
@@ -778,7 +797,8 @@ int32_t delta_layer(dz_ctx *ctx, dz_pplx *p, const dz_pplx::Layer &L, size_t n) 
     hipLaunchKernelGGL(delta_prep_kernel, dim3((unsigned)n), dim3(64 * c.delta_key_heads), 0, s, p->conv_out,
                        c.delta_heads, c.delta_key_heads, p->ab, p->ab + n * lh, L.decay, L.dt, p->qhat, p->khat,
                        p->gb);
-    hipLaunchKernelGGL(delta_scan_kernel, dim3(c.delta_heads, kLd / 16), dim3(64), 0, s, p->qhat, p->khat,
+    hipLaunchKernelGGL(delta_scan_kernel, dim3(c.delta_heads, kLd / kScanCols), dim3(64 * kScanWaves), 0, s,
+                       p->qhat, p->khat,
                        p->conv_out, p->gb, (int)n, c.delta_heads, c.delta_key_heads, p->heads);
     hipLaunchKernelGGL(delta_gate_kernel, dim3((unsigned)n, c.delta_heads), dim3(64), 0, s, p->heads, (int)n,
                        c.delta_heads, L.norm, p->z, p->ctx);
