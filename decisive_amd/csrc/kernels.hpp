@@ -61,7 +61,7 @@ void launch_i8_gemm(const int8_t *a, const float *sa, int m, const int8_t *b, co
                     int n, int k, void *y, int raw, int variant, hipStream_t s, bool b_q4 = false);
 // Fused gate/up W4A8 + SiLU + A8 requantization (grouped_q4_mlp.wgsl).
 void launch_mlp_requant(const Weight &gate, const Weight &up, const int8_t *q, const float *sx,
-                        int m, int8_t *qo, float *so, const int *bad, hipStream_t s);
+                        int m, int8_t *qo, float *so, const int *bad, int variant, hipStream_t s);
 
 // ---- epilogue.hip ----------------------------------------------------------------
 void launch_layernorm(const void *x, void *y, int dtype, int rows, int d, const float *w,

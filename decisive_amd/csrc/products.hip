@@ -1505,16 +1505,19 @@ __global__ __launch_bounds__(WGM *WGN * 64) void grouped_pipe_kernel(
 }
 
 // Fused MLP on the same pipeline (grouped_q4_mlp.wgsl:1-105, int8.rs fold):
-// gate and up products of one 256-row x 64-column block (one requant block),
+// gate and up products of one BM-row x 64-column block (one requant block),
 // silu(g) * u, then the A8 requantization of each row's 64 columns, exactly
-// as mlp_requant_kernel computes them. 8 waves stacked along M (wave tile
+// as mlp_requant_kernel computes them. BM/32 waves stacked along M (wave tile
 // 32 x 64): a row's 64 columns are held by the four lanes j, j+16, j+32,
-// j+48 of one wave, so the row maximum is two shuffles. Q4 weights.
-__global__ __launch_bounds__(512) void mlp_pipe_kernel(
+// j+48 of one wave, so the row maximum is two shuffles. Q4 weights. BM is
+// 256 (8 waves) or 128 (4 waves, half the LDS: two blocks fit a CU).
+template <int BM>
+__global__ __launch_bounds__(BM / 32 * 64) void mlp_pipe_kernel(
     const uint8_t *__restrict__ gcodes, const uint8_t *__restrict__ gscales, const uint8_t *__restrict__ ucodes,
     const uint8_t *__restrict__ uscales, const int8_t *__restrict__ q, const float *__restrict__ sx, int m, int n,
     int groups, int kbs, int8_t *__restrict__ qo, float *__restrict__ so, const int *__restrict__ bad) {
-    constexpr int BM = 256, WAVES = 8, MB = 2, NT = 4;
+    static_assert(BM == 256 || BM == 128, "8 or 4 waves");
+    constexpr int WAVES = BM / 32, MB = 2, NT = 4;
     constexpr int XSTAGE = BM * 128;   // activation codes, 2 groups per step
     constexpr int CSTAGE = 8 * 1024;   // gate tiles 0-3, up tiles 0-3: one tile16x128 chunk each
     constexpr int SWSTAGE = 2 * 1024;  // scale records: [weight][8 tiles x 128 B], tiles 0-3 used
@@ -1556,10 +1559,11 @@ __global__ __launch_bounds__(512) void mlp_pipe_kernel(
             dma16(__builtin_amdgcn_readfirstlane(xs_lds + stage * XSTAGE + blk * 1024),
                   xoff[p & 1] + (uint32_t)(blk * 8) * rowbytes + (uint32_t)st * 128, nq);
         }
-        {   // wave w copies chunk w: gate tiles for w < 4, up tiles for w >= 4
-            const uint32_t lds = __builtin_amdgcn_readfirstlane(cs_lds + stage * CSTAGE + wave * 1024);
-            const uint32_t off = (uint32_t)(((wave % 4) * kbs + st) * 1024 + lane * 16);
-            if (wave < 4) dma16(lds, off, live ? rcg : zero_len(rcg));
+#pragma unroll
+        for (int ch = wave; ch < 8; ch += WAVES) {  // chunk ch: gate tiles for ch < 4, up tiles for ch >= 4
+            const uint32_t lds = __builtin_amdgcn_readfirstlane(cs_lds + stage * CSTAGE + ch * 1024);
+            const uint32_t off = (uint32_t)(((ch % 4) * kbs + st) * 1024 + lane * 16);
+            if (ch < 4) dma16(lds, off, live ? rcg : zero_len(rcg));
             else dma16(lds, off, live ? rcu : zero_len(rcu));
         }
         if (wave < 2) {  // wave 0 the gate records, wave 1 the up records: lane l -> tile l / 8, piece l % 8
@@ -1690,6 +1694,7 @@ const char *const kGemmNames[] = {"pipe-auto",   "256x256p2w8", "128x128p2w4", "
 const char *const kI8Names[] = {"256x256p2w8", "256x256p4k64w8", "256x128p3w8", "256x128p3",
                                  "128x128w2x2", "256x128w2x2", "64x64w2x2"};
 const char *const kGroupedNames[] = {"pipe-auto", "pipe256x128w8", "wave16x16", "pipe128x128w4", "pipe64x128w2"};
+const char *const kMlpNames[] = {"pipe-auto", "pipe256x64w8", "pipe128x64w4", "wave16x64"};
 
 template <int W, int MPAD, bool G32>
 void gemv_launch_one(const Weight &w, const half_t *x, int m, float *y, hipStream_t s) {
@@ -1860,6 +1865,7 @@ int variant_count(const char *family) {
     if (f == "gemm_w4a16") return 7;
     if (f == "i8_gemm") return 7;
     if (f == "grouped") return 5;
+    if (f == "mlp") return 4;
     return 0;
 }
 
@@ -1870,6 +1876,7 @@ const char *variant_name(const char *family, int index) {
     if (f == "gemm_w4a16") return kGemmNames[index];
     if (f == "i8_gemm") return kI8Names[index];
     if (f == "grouped") return kGroupedNames[index];
+    if (f == "mlp") return kMlpNames[index];
     return nullptr;
 }
 
@@ -1952,15 +1959,34 @@ void launch_grouped(const Weight &w, const int8_t *q, const float *sx, int m, fl
                            w.groups, w.kblocks(), y, bad);
 }
 
+// Variants: 1 pipelined 256x64 blocks (8 waves), 2 128x64 blocks (4 waves),
+// 3 one wave per 16x64 block. 0 picks the 256-row blocks when their grid
+// covers half the compute units but not all of them, else the 128-row blocks
+// when theirs covers half, else the one-wave blocks (measured at K=2560,
+// N=9216: 128-row blocks are 3-14% faster from M=1024 to 4096, 256-row blocks
+// 4% faster at M=229). All variants are word-exact with the unfused composition.
 void launch_mlp_requant(const Weight &gate, const Weight &up, const int8_t *q, const float *sx,
-                        int m, int8_t *qo, float *so, const int *bad, hipStream_t s) {
+                        int m, int8_t *qo, float *so, const int *bad, int variant, hipStream_t s) {
     if (m == 0) return;
-    // the pipelined kernel when its grid covers half the compute units (same bits either way)
-    const unsigned pblocks = cdiv(m, 256) * (unsigned)(gate.rows / 64);
-    if (2 * pblocks >= (unsigned)device_cus() && (size_t)256 * gate.groups * 64 < ((size_t)1 << 31) &&
-        (size_t)4 * gate.kblocks() * 1024 < ((size_t)1 << 31) && ((uintptr_t)qo & 3) == 0 && gate.rows % 4 == 0) {
-        hipLaunchKernelGGL(mlp_pipe_kernel, dim3(pblocks), dim3(512), 0, s, gate.codes, gate.scales, up.codes,
-                           up.scales, q, sx, m, gate.rows, gate.groups, gate.kblocks(), qo, so, bad);
+    const unsigned cus = (unsigned)device_cus(), tn = (unsigned)(gate.rows / 64);
+    const bool fits = (size_t)256 * gate.groups * 64 < ((size_t)1 << 31) &&
+                      (size_t)4 * gate.kblocks() * 1024 < ((size_t)1 << 31) && ((uintptr_t)qo & 3) == 0 &&
+                      gate.rows % 4 == 0;
+    int pick = variant;
+    if (variant == 0) {
+        const unsigned b256 = cdiv(m, 256) * tn, b128 = cdiv(m, 128) * tn;
+        if (2 * b256 >= cus && b256 < cus) pick = 1;
+        else if (2 * b128 >= cus) pick = 2;
+        else pick = 3;
+    }
+    if (fits && pick == 1) {
+        hipLaunchKernelGGL(mlp_pipe_kernel<256>, dim3(cdiv(m, 256) * tn), dim3(512), 0, s, gate.codes, gate.scales,
+                           up.codes, up.scales, q, sx, m, gate.rows, gate.groups, gate.kblocks(), qo, so, bad);
+        return;
+    }
+    if (fits && pick == 2) {
+        hipLaunchKernelGGL(mlp_pipe_kernel<128>, dim3(cdiv(m, 128) * tn), dim3(256), 0, s, gate.codes, gate.scales,
+                           up.codes, up.scales, q, sx, m, gate.rows, gate.groups, gate.kblocks(), qo, so, bad);
         return;
     }
     dim3 grid(gate.rows / 64, cdiv(m, 16));

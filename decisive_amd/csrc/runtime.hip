@@ -286,7 +286,7 @@ int32_t dz_info(dz_ctx *ctx, char *buf, size_t cap) {
     std::string s = "{\"arch\":\"" + ctx->arch + "\",\"compute_units\":" + std::to_string(ctx->cus) +
                     ",\"clock_khz\":" + std::to_string(ctx->clock_khz) + ",\"variants\":{";
     bool first = true;
-    for (const char *f : {"gemv", "gemm_w4a16", "i8_gemm", "grouped"}) {
+    for (const char *f : {"gemv", "gemm_w4a16", "i8_gemm", "grouped", "mlp"}) {
         if (!first) s += ",";
         first = false;
         s += std::string("\"") + f + "\":\"" + dz::variant_name(f, variant(ctx, f)) + "\"";
@@ -561,7 +561,7 @@ int32_t dz_mlp_requant(dz_ctx *ctx, const dz_weight *gate, const dz_weight *up, 
     float *s = (float *)((uint8_t *)ctx->work + (qbytes + 255) / 256 * 256);
     dz::launch_fill_i32(ctx->flag, 0, 1, ctx->stream);
     dz::launch_act_quantize(x, (int)m, g.cols, 8, q, s, ctx->flag, ctx->stream);
-    dz::launch_mlp_requant(g, u, q, s, (int)m, qo, so, ctx->flag, ctx->stream);
+    dz::launch_mlp_requant(g, u, q, s, (int)m, qo, so, ctx->flag, variant(ctx, "mlp"), ctx->stream);
     return launched(ctx, "fused MLP");
 }
 

@@ -175,8 +175,9 @@ def test_pair_shares_one_quantization(ctx, oracle):
 
 
 def test_fused_mlp_large_m_pipeline_equals_unfused(ctx, oracle):
-    """The pipelined fused MLP (grid of 256-row x 64-column blocks, ragged m,
-    an odd group count) is word-exact with the unfused composition."""
+    """Every fused MLP variant (256- and 128-row pipelined blocks, one-wave
+    blocks; ragged m, an odd group count) is word-exact with the unfused
+    composition."""
     torch = pytest.importorskip("torch")
     m, n, k = 600, 2752, 1088
     rng = np.random.default_rng(11)
@@ -186,9 +187,6 @@ def test_fused_mlp_large_m_pipeline_equals_unfused(ctx, oracle):
     up = ctx.quantize(dev(uraw), rocm.BF16, n, k, 4, 64)
     x = (rng.standard_normal((m, k)) * 1.3).astype(np.float32)
     xd = dev(x)
-    q = empty((m, n), torch.int8)
-    s = empty((m, n // 64), torch.float32)
-    ctx.mlp_requant(gate, up, xd, m, q, s)
     g = empty((m, n), torch.float32)
     u = empty((m, n), torch.float32)
     ctx.linear_pair(gate, up, xd, m, g, u)
@@ -196,8 +194,14 @@ def test_fused_mlp_large_m_pipeline_equals_unfused(ctx, oracle):
     q2 = empty((m, n), torch.int8)
     s2 = empty((m, n // 64), torch.float32)
     ctx.act_quantize(g, m, n, 8, q2, s2)
-    assert np.array_equal(host(ctx, q), host(ctx, q2))
-    assert bits_equal(host(ctx, s), host(ctx, s2))
+    q = empty((m, n), torch.int8)
+    s = empty((m, n // 64), torch.float32)
+    for name in ("pipe256x64w8", "pipe128x64w4", "wave16x64", "pipe-auto"):
+        ctx.select_variant("mlp", name)
+        q.zero_()
+        ctx.mlp_requant(gate, up, xd, m, q, s)
+        assert np.array_equal(host(ctx, q), host(ctx, q2)), name
+        assert bits_equal(host(ctx, s), host(ctx, s2)), name
     # a non-finite activation: every scale NaN, every code 0 (int8.rs:170-173)
     x[599, 7] = np.nan
     ctx.mlp_requant(gate, up, dev(x), m, q, s)
@@ -219,9 +223,6 @@ def test_fused_mlp_requant_equals_unfused(ctx, oracle):
     up = ctx.upload(oracle.pack_g64(uraw, n, k, 4), rocm.Q4_G64_F32, n, k)
     x = (((np.arange(m * k) * 29 % 509) - 254.0) / 97.0).astype(np.float32)
     xd = dev(x)
-    q = empty((m, n), torch.int8)
-    s = empty((m, n // 64), torch.float32)
-    ctx.mlp_requant(gate, up, xd, m, q, s)
     g = empty((m, n), torch.float32)
     u = empty((m, n), torch.float32)
     ctx.linear_pair(gate, up, xd, m, g, u)
@@ -229,8 +230,14 @@ def test_fused_mlp_requant_equals_unfused(ctx, oracle):
     q2 = empty((m, n), torch.int8)
     s2 = empty((m, n // 64), torch.float32)
     ctx.act_quantize(g, m, n, 8, q2, s2)
-    assert np.array_equal(host(ctx, q), host(ctx, q2))
-    assert bits_equal(host(ctx, s), host(ctx, s2))
+    q = empty((m, n), torch.int8)
+    s = empty((m, n // 64), torch.float32)
+    for name in ("pipe256x64w8", "pipe128x64w4", "wave16x64", "pipe-auto"):
+        ctx.select_variant("mlp", name)
+        q.zero_()
+        ctx.mlp_requant(gate, up, xd, m, q, s)
+        assert np.array_equal(host(ctx, q), host(ctx, q2)), name
+        assert bits_equal(host(ctx, s), host(ctx, s2)), name
     # oracle composition (its expf may differ from the GPU's by an ulp)
     gc, gs = oracle.weight_quantize(graw, n, k, 4)
     uc, us = oracle.weight_quantize(uraw, n, k, 4)
