@@ -41,6 +41,7 @@ int32_t weight_upload(dz_ctx *ctx, const void *packed, size_t bytes, int32_t lay
 void weight_free(dz_weight *h);
 int32_t ctx_readout_rows(dz_ctx *ctx, const Weight &w, const float *norm, const void *hidden, int dtype,
                          const int32_t *select, size_t rows, float eps, float *logits);
+int ctx_variant(dz_ctx *ctx, const char *family);
 
 namespace {
 
@@ -81,7 +82,7 @@ __global__ void conv_silu_kernel(const float *__restrict__ x, int n, int width, 
 
 // One block per token, one wave per key head: unit q and k (q also scaled by
 // 1/sqrt(ld)) and their dot product; threads below lh compute the decay g and
-// beta of head h. Record (t, h) of gb holds {g, beta, k.q of h's key head, 0}.
+// beta of head h. Record (t, h) of gb holds {g, beta, k.q of h's key head, log g}.
 __global__ void delta_prep_kernel(const float *__restrict__ conv, int lh, int lk, const float *__restrict__ a,
                                   const float *__restrict__ b, const float *__restrict__ decay,
                                   const float *__restrict__ dt, float *__restrict__ qhat,
@@ -109,8 +110,10 @@ __global__ void delta_prep_kernel(const float *__restrict__ conv, int lh, int lk
     for (int h = threadIdx.x; h < lh; h += blockDim.x) {
         const float x = __fadd_rn(a[(size_t)t * lh + h], dt[h]);
         const float softplus = x > 20.0f ? x : log1pf(expf(x));
-        gb[((size_t)t * lh + h) * 4] = expf(__fmul_rn(-decay[h], softplus));
+        const float logg = __fmul_rn(-decay[h], softplus);
+        gb[((size_t)t * lh + h) * 4] = expf(logg);
         gb[((size_t)t * lh + h) * 4 + 1] = sigmoid_ref(b[(size_t)t * lh + h]);
+        gb[((size_t)t * lh + h) * 4 + 3] = logg;
     }
 }
 
@@ -229,6 +232,252 @@ __global__ __launch_bounds__(kScanWaves * 64) void delta_scan_kernel(const float
         if (r < count) out[((size_t)h * n + t0 + r) * kLd + j] = keep;
         if (more) store(buf ^ 1);  // the other buffer: last read a whole chunk ago
         __syncthreads();
+    }
+}
+
+// ---- the gated delta rule by chunks of 64 tokens (f32 MFMA) ----------------
+// Over one chunk, with S0 the state before it, gamma_t the decay from the
+// chunk start through token t (exp of the running sum of log g) and
+// D[t][i] = gamma_t / gamma_i:
+//   A = strictly-lower(diag(beta) (K K^T * D)),  (I + A) [Uv | Wk] = [diag(beta) V | diag(beta gamma) K]
+//   U = Uv - Wk S0          (the values the chunk's tokens write, u_t = beta_t (v_t - mem_t))
+//   O = diag(gamma) Q S0 + lower(Q K^T * D) U
+//   S = gamma_last S0 + (diag(gamma_last / gamma) K)^T U
+// which is the token-by-token rule regrouped (each u_t is the reference's
+// delta). delta_chunk_prep_kernel does everything that does not involve S0,
+// for every (head, chunk) at once; delta_chunk_scan_kernel walks the chunks in
+// order for 16 state columns per block.
+constexpr int kChunk = 64;
+constexpr int kChunkWs = 2 * kChunk * kLd + kChunk * kChunk + kLd * kChunk + kChunk;  // floats per (head, chunk)
+constexpr int kChunkRow = kLd + 4;    // padded LDS row of K / Q (conflict-free float4 reads across rows)
+
+// One block (4 waves) per (head, chunk). Workspace record (floats):
+// Uv [64][128] | Wk [64][128] | P [64][64] | rKT [128][64] (gamma_last/gamma_t K[t][dk]) | gamma [64].
+__global__ __launch_bounds__(256) void delta_chunk_prep_kernel(const float *__restrict__ qhat,
+                                                               const float *__restrict__ khat,
+                                                               const float *__restrict__ conv,
+                                                               const float *__restrict__ gb, int n, int lh, int lk,
+                                                               float *__restrict__ ws) {
+    extern __shared__ __align__(16) float sm[];
+    float *ks = sm, *as = ks + kChunk * kChunkRow, *cum = as + kChunk * kChunk, *bet = cum + kChunk,
+          *bk = bet + kChunk;
+    const int h = blockIdx.x, c = blockIdx.y, tid = threadIdx.x;
+    const int wave = tid / 64, lane = tid % 64, col = lane % 16, g = lane / 16;
+    const int kh = h / (lh / lk), t0 = c * kChunk;
+    const size_t lkv = (size_t)lk * kLd, width = 2 * lkv + (size_t)lh * kLd;
+    float *rec = ws + ((size_t)h * gridDim.y + c) * kChunkWs;
+    float *uv = rec, *wk = uv + kChunk * kLd, *pm = wk + kChunk * kLd, *rkt = pm + kChunk * kChunk,
+          *gam = rkt + kLd * kChunk;
+    // stage K rows (zero past n), beta and log g (zero past n)
+    for (int e = tid; e < kChunk * kLd / 4; e += 256) {
+        const int t = e / (kLd / 4), u = e % (kLd / 4), tok = t0 + t;
+        float4_t kv = {0.f, 0.f, 0.f, 0.f};
+        if (tok < n) kv = *(const float4_t *)(khat + ((size_t)tok * lk + kh) * kLd + 4 * u);
+        *(float4_t *)(ks + t * kChunkRow + 4 * u) = kv;
+    }
+    if (tid < kChunk) {
+        const int tok = t0 + tid;
+        bet[tid] = tok < n ? gb[((size_t)tok * lh + h) * 4 + 1] : 0.0f;
+        cum[tid] = tok < n ? gb[((size_t)tok * lh + h) * 4 + 3] : 0.0f;
+    }
+    // this lane's Q fragment (row 16*wave + col, dims 32g..32g+31) for Q K^T
+    float4_t qf[8];
+    {
+        const int tok = t0 + 16 * wave + col;
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            qf[i] = tok < n ? *(const float4_t *)(qhat + ((size_t)tok * lk + kh) * kLd + 32 * g + 4 * i)
+                            : float4_t{0.f, 0.f, 0.f, 0.f};
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float run = 0.0f;
+        for (int t = 0; t < kChunk; t++) {
+            run += cum[t];
+            cum[t] = run;
+        }
+    }
+    __syncthreads();
+    if (tid < kChunk) bk[tid] = bet[tid] * expf(cum[tid]);
+    // K K^T and Q K^T, row block `wave`: lane (col, g) holds rows 16*wave + 4g + i of column block cb
+#pragma unroll 1
+    for (int cb = 0; cb < 4; cb++) {
+        float4_t kk = {0.f, 0.f, 0.f, 0.f}, qk = kk;
+        const float *ka = ks + (16 * wave + col) * kChunkRow + 32 * g;
+        const float *kb = ks + (16 * cb + col) * kChunkRow + 32 * g;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float4_t a4 = *(const float4_t *)(ka + 4 * i), b4 = *(const float4_t *)(kb + 4 * i);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                kk = __builtin_amdgcn_mfma_f32_16x16x4f32(a4[e], b4[e], kk, 0, 0, 0);
+                qk = __builtin_amdgcn_mfma_f32_16x16x4f32(qf[i][e], b4[e], qk, 0, 0, 0);
+            }
+        }
+        const int j = 16 * cb + col;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int r = 16 * wave + 4 * g + i;
+            const float d = j <= r ? expf(cum[r] - cum[j]) : 0.0f;
+            as[r * kChunk + j] = j < r ? bet[r] * d * kk[i] : 0.0f;
+            pm[r * kChunk + j] = d * qk[i];
+        }
+    }
+    __syncthreads();
+    // (I + A) x = b, one right-hand side per thread: columns of diag(beta) V
+    // (waves 0-1), then of diag(beta gamma) K (waves 2-3)
+    auto solve = [&](auto vcol_c) {
+        constexpr bool VCOL = decltype(vcol_c)::value;
+        const int cc = VCOL ? tid : tid - kLd;
+        const float *vsrc = conv + 2 * lkv + (size_t)h * kLd + cc;
+        float x[kChunk];  // the right-hand side, then the solution in place
+#pragma unroll
+        for (int i = 0; i < kChunk; i++) {
+            if (VCOL) x[i] = t0 + i < n ? bet[i] * vsrc[(size_t)(t0 + i) * width] : 0.0f;
+            else x[i] = bk[i] * ks[i * kChunkRow + cc];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 1; i < kChunk; i++) {
+            float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+#pragma unroll
+            for (int l = 0; l + 3 < i; l += 4) {
+                const float4_t a4 = *(const float4_t *)(as + i * kChunk + l);
+                s0 = __builtin_fmaf(a4[0], x[l], s0);
+                s1 = __builtin_fmaf(a4[1], x[l + 1], s1);
+                s2 = __builtin_fmaf(a4[2], x[l + 2], s2);
+                s3 = __builtin_fmaf(a4[3], x[l + 3], s3);
+            }
+#pragma unroll
+            for (int l = i & ~3; l < i; l++) s0 = __builtin_fmaf(as[i * kChunk + l], x[l], s0);
+            x[i] -= (s0 + s1) + (s2 + s3);
+        }
+        float *dst = VCOL ? uv : wk;
+#pragma unroll
+        for (int i = 0; i < kChunk; i++) dst[i * kLd + cc] = x[i];
+    };
+    if (__builtin_amdgcn_readfirstlane(wave) < 2) solve(std::true_type{});
+    else solve(std::false_type{});
+    // (gamma_last / gamma_t) K[t][dk], transposed; gamma_t
+    {
+        const int dk = tid / 2, th = (tid % 2) * 32;
+        const float last = cum[kChunk - 1];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            float4_t v4;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int t = th + 4 * u + e;
+                v4[e] = expf(last - cum[t]) * ks[t * kChunkRow + dk];
+            }
+            *(float4_t *)(rkt + dk * kChunk + th + 4 * u) = v4;
+        }
+        if (tid < kChunk) gam[tid] = expf(cum[tid]);
+    }
+}
+
+// One block (4 waves) per (head, 16 state columns); the chunks in order. The
+// state S (128 x 16) lives in LDS transposed (S_T[col][dk]); wave w computes
+// rows 16w..16w+15 of the chunk's U and O and the state rows 32w..32w+31.
+__global__ __launch_bounds__(256) void delta_chunk_scan_kernel(const float *__restrict__ qhat,
+                                                               const float *__restrict__ ws, int n, int lh, int lk,
+                                                               float *__restrict__ out) {
+    __shared__ __align__(16) float st[16 * kChunkRow];       // S_T [16][128 + 4]
+    __shared__ __align__(16) float ut[16 * (kChunk + 4)];    // U_T [16][64 + 4]
+    constexpr int UROW = kChunk + 4;
+    const int h = blockIdx.x, cb = blockIdx.y, tid = threadIdx.x;
+    const int wave = tid / 64, lane = tid % 64, col = lane % 16, g = lane / 16;
+    const int kh = h / (lh / lk);
+    const int chunks = (n + kChunk - 1) / kChunk;
+    for (int e = tid; e < 16 * kChunkRow; e += 256) st[e] = 0.0f;
+    __syncthreads();
+    // the global operands of one chunk for this lane; the next chunk's are in
+    // flight while the current one computes
+    struct Ops {
+        float4_t w[8], q[8], p[4], r[2][4];
+        float u[4], gm[4], last;
+    };
+    auto fetch = [&](int c) {
+        Ops o;
+        const float *rec = ws + ((size_t)h * chunks + c) * kChunkWs;
+        const float *uv = rec, *wk = uv + kChunk * kLd, *pm = wk + kChunk * kLd, *rkt = pm + kChunk * kChunk,
+                    *gam = rkt + kLd * kChunk;
+        const int row = 16 * wave + col, tq = min(c * kChunk + row, n - 1);
+        const float *qa = qhat + ((size_t)tq * lk + kh) * kLd + 32 * g;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            o.w[i] = *(const float4_t *)(wk + row * kLd + 32 * g + 4 * i);
+            o.q[i] = *(const float4_t *)(qa + 4 * i);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            o.p[i] = *(const float4_t *)(pm + row * kChunk + 16 * g + 4 * i);
+#pragma unroll
+            for (int d = 0; d < 2; d++) o.r[d][i] = *(const float4_t *)(rkt + (32 * wave + 16 * d + col) * kChunk + 16 * g + 4 * i);
+            const int t = 16 * wave + 4 * g + i;
+            o.u[i] = uv[t * kLd + 16 * cb + col];
+            o.gm[i] = gam[t];
+        }
+        o.last = gam[kChunk - 1];
+        return o;
+    };
+    Ops cur = fetch(0);
+    for (int c = 0; c < chunks; c++) {
+        Ops nxt = cur;
+        if (c + 1 < chunks) nxt = fetch(c + 1);
+        const int t0 = c * kChunk;
+        // X = Wk S and Q S over the 128 state rows
+        float4_t xw = {0.f, 0.f, 0.f, 0.f}, qsv = xw;
+        const float *sb = st + col * kChunkRow + 32 * g;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float4_t b4 = *(const float4_t *)(sb + 4 * i);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                xw = __builtin_amdgcn_mfma_f32_16x16x4f32(cur.w[i][e], b4[e], xw, 0, 0, 0);
+                qsv = __builtin_amdgcn_mfma_f32_16x16x4f32(cur.q[i][e], b4[e], qsv, 0, 0, 0);
+            }
+        }
+        // U = Uv - X (rows 16w + 4g + i), into U_T; O starts as gamma Q S
+        float4_t u4, o4;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            u4[i] = cur.u[i] - xw[i];
+            o4[i] = cur.gm[i] * qsv[i];
+        }
+        *(float4_t *)(ut + col * UROW + 16 * wave + 4 * g) = u4;
+        // U complete, every read of the old S done; an LDS-only wait keeps the
+        // next chunk's global loads in flight (__syncthreads would drain them)
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_s_barrier();
+        // O += P U and the state update share the U operands
+        const float *ub = ut + col * UROW + 16 * g;
+        float4_t sn[2];
+#pragma unroll
+        for (int d = 0; d < 2; d++) {
+            const float4_t old = *(const float4_t *)(st + col * kChunkRow + 32 * wave + 16 * d + 4 * g);
+            sn[d] = old * cur.last;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float4_t b4 = *(const float4_t *)(ub + 4 * i);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                o4 = __builtin_amdgcn_mfma_f32_16x16x4f32(cur.p[i][e], b4[e], o4, 0, 0, 0);
+#pragma unroll
+                for (int d = 0; d < 2; d++) sn[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(cur.r[d][i][e], b4[e], sn[d], 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int t = t0 + 16 * wave + 4 * g + i;
+            if (t < n) out[((size_t)h * n + t) * kLd + 16 * cb + col] = o4[i];
+        }
+#pragma unroll
+        for (int d = 0; d < 2; d++) *(float4_t *)(st + col * kChunkRow + 32 * wave + 16 * d + 4 * g) = sn[d];
+        cur = nxt;
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // the new S is complete; U_T is free
+        __builtin_amdgcn_s_barrier();
     }
 }
 
@@ -502,7 +751,7 @@ struct dz_pplx {
     float *hidden = nullptr, *normed = nullptr, *wide = nullptr, *z = nullptr, *ab = nullptr, *conv_out = nullptr,
           *qhat = nullptr, *khat = nullptr, *gb = nullptr, *heads = nullptr, *ctx = nullptr, *projected = nullptr,
           *key = nullptr, *value = nullptr, *query = nullptr, *picked = nullptr, *gate = nullptr, *up = nullptr,
-          *logits = nullptr;
+          *logits = nullptr, *chunk_ws = nullptr;
     int8_t *codes = nullptr;
     float *code_scales = nullptr;
     int32_t *markers = nullptr;
@@ -546,6 +795,7 @@ int32_t ensure_capacity(dz_ctx *ctx, dz_pplx *p, size_t n) {
     get(&p->qhat, n * c.delta_key_heads * kLd * 4);
     get(&p->khat, n * c.delta_key_heads * kLd * 4);
     get(&p->gb, n * c.delta_heads * 4 * 4);
+    get(&p->chunk_ws, (size_t)c.delta_heads * ((n + kChunk - 1) / kChunk) * kChunkWs * 4);
     get(&p->heads, n * std::max(lv, (size_t)c.attn_heads * kAd) * 4);
     get(&p->ctx, n * ctxw * 4);
     get(&p->projected, n * d * 4);
@@ -784,6 +1034,35 @@ int32_t mlp(dz_ctx *ctx, dz_pplx *p, const dz_pplx::Layer &L, size_t n) {
     return DZ_OK;
 }
 
+// Variant 1 runs the token-by-token scan, 2 the chunked one; 0 picks the
+// chunked scan from six chunks of tokens on (measured at the reference's
+// sizes: the chunked scan is 2% slower at 229 tokens, 2% faster at 512, 9%
+// faster at 1024 and 2048, over three delta layers and one attention layer).
+void launch_delta_scan(dz_ctx *ctx, dz_pplx *p, size_t n, hipStream_t s) {
+    const dz_pplx_config &c = p->cfg;
+    const int v = ctx_variant(ctx, "delta_scan");
+    const bool chunked = v == 2 || (v == 0 && n >= (size_t)6 * kChunk);
+    if (!chunked) {
+        hipLaunchKernelGGL(delta_scan_kernel, dim3(c.delta_heads, kLd / kScanCols), dim3(64 * kScanWaves), 0, s,
+                           p->qhat, p->khat, p->conv_out, p->gb, (int)n, c.delta_heads, c.delta_key_heads, p->heads);
+        return;
+    }
+    constexpr size_t lds = (size_t)(kChunk * kChunkRow + kChunk * kChunk + 3 * kChunk) * 4;
+    static bool configured[64] = {};  // the LDS limit is a per-device function attribute
+    int dev = 0;
+    hipGetDevice(&dev);
+    if (dev >= 0 && dev < 64 && !configured[dev]) {
+        hipFuncSetAttribute((const void *)delta_chunk_prep_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)lds);
+        configured[dev] = true;
+    }
+    const unsigned chunks = (unsigned)((n + kChunk - 1) / kChunk);
+    hipLaunchKernelGGL(delta_chunk_prep_kernel, dim3(c.delta_heads, chunks), dim3(256), lds, s, p->qhat, p->khat,
+                       p->conv_out, p->gb, (int)n, c.delta_heads, c.delta_key_heads, p->chunk_ws);
+    hipLaunchKernelGGL(delta_chunk_scan_kernel, dim3(c.delta_heads, kLd / 16), dim3(256), 0, s, p->qhat,
+                       p->chunk_ws, (int)n, c.delta_heads, c.delta_key_heads, p->heads);
+}
+
 int32_t delta_layer(dz_ctx *ctx, dz_pplx *p, const dz_pplx::Layer &L, size_t n) {
     const dz_pplx_config &c = p->cfg;
     hipStream_t s = ctx_stream(ctx);
@@ -797,9 +1076,7 @@ int32_t delta_layer(dz_ctx *ctx, dz_pplx *p, const dz_pplx::Layer &L, size_t n) 
     hipLaunchKernelGGL(delta_prep_kernel, dim3((unsigned)n), dim3(64 * c.delta_key_heads), 0, s, p->conv_out,
                        c.delta_heads, c.delta_key_heads, p->ab, p->ab + n * lh, L.decay, L.dt, p->qhat, p->khat,
                        p->gb);
-    hipLaunchKernelGGL(delta_scan_kernel, dim3(c.delta_heads, kLd / kScanCols), dim3(64 * kScanWaves), 0, s,
-                       p->qhat, p->khat,
-                       p->conv_out, p->gb, (int)n, c.delta_heads, c.delta_key_heads, p->heads);
+    launch_delta_scan(ctx, p, n, s);
     hipLaunchKernelGGL(delta_gate_kernel, dim3((unsigned)n, c.delta_heads), dim3(64), 0, s, p->heads, (int)n,
                        c.delta_heads, L.norm, p->z, p->ctx);
     rc = linear(ctx, L.out, p->ctx, n, p->projected);

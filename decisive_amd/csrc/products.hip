@@ -1695,6 +1695,7 @@ const char *const kI8Names[] = {"256x256p2w8", "256x256p4k64w8", "256x128p3w8", 
                                  "128x128w2x2", "256x128w2x2", "64x64w2x2"};
 const char *const kGroupedNames[] = {"pipe-auto", "pipe256x128w8", "wave16x16", "pipe128x128w4", "pipe64x128w2"};
 const char *const kMlpNames[] = {"pipe-auto", "pipe256x64w8", "pipe128x64w4", "wave16x64"};
+const char *const kDeltaNames[] = {"auto", "recurrent", "chunked64"};
 
 template <int W, int MPAD, bool G32>
 void gemv_launch_one(const Weight &w, const half_t *x, int m, float *y, hipStream_t s) {
@@ -1866,6 +1867,7 @@ int variant_count(const char *family) {
     if (f == "i8_gemm") return 7;
     if (f == "grouped") return 5;
     if (f == "mlp") return 4;
+    if (f == "delta_scan") return 3;
     return 0;
 }
 
@@ -1877,6 +1879,7 @@ const char *variant_name(const char *family, int index) {
     if (f == "i8_gemm") return kI8Names[index];
     if (f == "grouped") return kGroupedNames[index];
     if (f == "mlp") return kMlpNames[index];
+    if (f == "delta_scan") return kDeltaNames[index];
     return nullptr;
 }
 

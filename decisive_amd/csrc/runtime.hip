@@ -286,7 +286,7 @@ int32_t dz_info(dz_ctx *ctx, char *buf, size_t cap) {
     std::string s = "{\"arch\":\"" + ctx->arch + "\",\"compute_units\":" + std::to_string(ctx->cus) +
                     ",\"clock_khz\":" + std::to_string(ctx->clock_khz) + ",\"variants\":{";
     bool first = true;
-    for (const char *f : {"gemv", "gemm_w4a16", "i8_gemm", "grouped", "mlp"}) {
+    for (const char *f : {"gemv", "gemm_w4a16", "i8_gemm", "grouped", "mlp", "delta_scan"}) {
         if (!first) s += ",";
         first = false;
         s += std::string("\"") + f + "\":\"" + dz::variant_name(f, variant(ctx, f)) + "\"";

@@ -149,7 +149,7 @@ std::string json_field(const std::string &s, const std::string &name) {
 std::string tuning_key(dz_ctx *ctx) {
     Sha256 h;
     h.update("pplx-tuning-v1\n" + ctx_device_key(ctx) + "\n" + DZ_SOURCE_HASH + "\n");
-    for (const char *f : {"gemv", "gemm_w4a16", "i8_gemm", "grouped", "mlp"})
+    for (const char *f : {"gemv", "gemm_w4a16", "i8_gemm", "grouped", "mlp", "delta_scan"})
         for (int i = 0; i < variant_count(f); i++) h.update(std::string(f) + "/" + variant_name(f, i) + "\n");
     return h.hex16();
 }

@@ -75,6 +75,29 @@ def test_forward_logits_match_the_reference_chunk(ctx, oracle, small, n):
     assert close(got, want, rel=1e-2), (float(cosine(got, want)), float(np.abs(got - want).max()))
 
 
+@pytest.mark.parametrize("scan", ["recurrent", "chunked64"])
+@pytest.mark.parametrize("n", [1, 37, 64, 130, 257])
+def test_delta_layer_matches_the_reference_for_both_scans(ctx, oracle, small, scan, n):
+    """The token-by-token scan and the chunked one (64-token chunks: one
+    partial chunk, exact chunks, a ragged tail) against the oracle's
+    sequential rule. Both regroup the rule's arithmetic, so an ulp now and
+    then flips one A8 code of out_proj's input; the bound is a cosine of
+    0.99999 with max-abs within 1% (a wrong scan lands far below 0.9999)."""
+    torch = pytest.importorskip("torch")
+    model, p = small
+    h = np.random.default_rng(100 + n).standard_normal((n, SMALL["hidden"])).astype(np.float32)
+    hd = dev(h)
+    ctx.select_variant("delta_scan", scan)
+    try:
+        p.layer(1, hd, n)
+    finally:
+        ctx.select_variant("delta_scan", "auto")
+    got = host(ctx, hd)
+    want = pplx_model.ref_layer(oracle, model, 1, h)
+    assert cosine(got, want) >= 0.99999 and close(got, want, rel=1e-2), (float(cosine(got, want)),
+                                                                         float(np.abs(got - want).max()))
+
+
 # four query heads per key/value head, as the reference model has
 GQA4 = dict(SMALL, attn_heads=8, attn_kv_heads=2)
 
