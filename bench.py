@@ -72,6 +72,16 @@ def timed_ms(torch, stream, fn, reps: int) -> float:
     return a.elapsed_time(b) / reps
 
 
+def warm(torch, fn, ms: float = 60.0, least: int = 2):
+    """Untimed calls of fn until about `ms` of wall time has passed (at least
+    `least` calls): the clocks reach their steady state before timing."""
+    start, r = time.perf_counter(), 0
+    while r < least or (time.perf_counter() - start) * 1e3 < ms:
+        fn(r)
+        torch.cuda.synchronize()
+        r += 1
+
+
 def graph_ms(torch, stream, step, launches: int, reps: int = 20) -> float:
     """Average launch duration of `step` (which enqueues `launches` launches)
     captured once as a HIP graph and replayed `reps` times back to back."""
@@ -228,8 +238,7 @@ def secondary(torch, ctx, rocm, stream, cpu=True) -> dict:
     y = torch.empty((m, n), dtype=torch.float32, device="cuda")
     ctx.sync()
     fn = lambda r: ctx.i8_gemm(qa, sa, m, qb, sb, n, k, y, raw=False)  # noqa: E731
-    for r in range(3):
-        fn(r)
+    warm(torch, fn)
     ms = timed_ms(torch, stream, fn, 20)
     tops = 2 * m * n * k / (ms * 1e-3) / 1e12
     out["int8_gemm_m8192_k4096_n4096"] = {"ms": round(ms, 4), "TOP/s": round(tops, 1),
@@ -246,8 +255,7 @@ def secondary(torch, ctx, rocm, stream, cpu=True) -> dict:
     y = torch.empty((m, n), dtype=torch.float32, device="cuda")
     torch.cuda.synchronize()
     fn = lambda r: ctx.linear(w, x, rocm.F16, m, y, rocm.W4A16)  # noqa: E731
-    for r in range(2):
-        fn(r)
+    warm(torch, fn)
     ms = timed_ms(torch, stream, fn, 10)
     tf = 2 * m * n * k / (ms * 1e-3) / 1e12
     out["q4_prefill_w4a16_m16384_k4096_n14336"] = {"ms": round(ms, 4), "TFLOP/s": round(tf, 1),
@@ -258,8 +266,7 @@ def secondary(torch, ctx, rocm, stream, cpu=True) -> dict:
     # the same product in prefill form: f16 out (what the next layer reads), one rounding
     y = torch.empty((m, n), dtype=torch.float16, device="cuda")
     fn = lambda r: ctx.linear_f16(w, x, m, y)  # noqa: E731
-    for r in range(2):
-        fn(r)
+    warm(torch, fn)
     ms = timed_ms(torch, stream, fn, 10)
     tf = 2 * m * n * k / (ms * 1e-3) / 1e12
     out["q4_prefill_w4a16_f16out_m16384_k4096_n14336"] = {
@@ -278,7 +285,7 @@ def secondary(torch, ctx, rocm, stream, cpu=True) -> dict:
     y = torch.empty((m, n), dtype=torch.float32, device="cuda")
     torch.cuda.synchronize()
     fn = lambda r: ctx.linear(w, x, rocm.F32, m, y, rocm.W4A8)  # noqa: E731
-    fn(0)
+    warm(torch, fn)
     ms = timed_ms(torch, stream, fn, 5)
     tops = 2 * m * n * k / (ms * 1e-3) / 1e12
     out["q4_prefill_w4a8_bitexact_m16384_k4096_n14336"] = {
@@ -293,8 +300,7 @@ def secondary(torch, ctx, rocm, stream, cpu=True) -> dict:
     ids = torch.from_numpy(np.random.default_rng(1).integers(0, 32000, 8 * 1024).astype(np.int32)).cuda()
     emb = torch.empty((8, 1024), dtype=torch.float32, device="cuda")
     torch.cuda.synchronize()
-    enc.forward(ids, 8, 1024, emb)
-    ctx.sync()
+    warm(torch, lambda r: enc.forward(ids, 8, 1024, emb))
     ms = timed_ms(torch, stream, lambda r: enc.forward(ids, 8, 1024, emb), 5)
     flops = 2 * 8192 * (4 * 1024 * 1024 + 2 * 1024 * 4096) * 24 + 4 * 8 * 16 * 1024 * 1024 * 64 * 24
     out["encoder_forward_b8_s1024"] = {"ms": round(ms, 3), "embeddings/s": round(8 / (ms * 1e-3), 1),
@@ -364,7 +370,7 @@ def pplx_line(torch, ctx, rocm, stream, n: int = 1024, layers: int = 32) -> dict
     markers = [n - 1, n // 2, n // 3, 0]
     logits = p.forward_rows(rows, n, markers)
     assert np.isfinite(logits).all()
-    torch.cuda.synchronize()
+    warm(torch, lambda r: p.forward_rows(rows, n, markers))
     reps = 5
     wall = time.perf_counter()
     ms = timed_ms(torch, stream, lambda r: p.forward_rows(rows, n, markers), reps)

@@ -1103,7 +1103,12 @@ __device__ __forceinline__ uint4_t unpack_codes_c(uint32_t w, uint32_t mlo, uint
 // A launch covers the n output columns that codes / scales / out / residual
 // point at (a multiple-of-16 slice of the weight); ldo is the row stride of
 // out and residual.
-template <int BM, int BN, int WGM, int WGN, bool G32, int EPI, int VALU_PER_MFMA = 2>
+// PERSIST: a grid of fewer blocks than tiles, each taking tiles blockIdx.x,
+// blockIdx.x + gridDim.x, ... (the same tile order and XCD placement as one
+// block per tile) as one stream of k-steps: the last step of a tile loads the
+// next tile's first stage, so those loads fly during the epilogue. Each
+// tile's arithmetic is unchanged, so both forms give the same bits.
+template <int BM, int BN, int WGM, int WGN, bool G32, int EPI, int VALU_PER_MFMA = 2, bool PERSIST = false>
 __global__ __launch_bounds__(WGM *WGN * 64) void w4a16_pipe_kernel(
     const uint8_t *__restrict__ codes, const uint8_t *__restrict__ scales, const half_t *__restrict__ x, int m,
     int k, int n, int kbs, void *__restrict__ out, const half_t *__restrict__ residual, int ldo) {
@@ -1122,13 +1127,29 @@ __global__ __launch_bounds__(WGM *WGN * 64) void w4a16_pipe_kernel(
     const int wm = wave / WGN, wn = wave % WGN;
     const int q = lane / 16, j = lane % 16;
     const int tiles_m = (m + BM - 1) / BM, tiles_n = (n + BN - 1) / BN;
-    int tm, tn;
-    xcd_tile(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
-    const int row0 = tm * BM, col0 = tn * BN;
-    const int tiles = (n + 15) / 16, tile0 = col0 / 16;
-    const int32x4_t rsx = buffer_rsrc(x + (size_t)row0 * k, (uint32_t)(min(BM, m - row0) * k * 2));
-    const int32x4_t rsw = buffer_rsrc(codes + (size_t)tile0 * kbs * 1024,
-                                      (uint32_t)(min(BN / 16, tiles - tile0) * kbs * 1024));
+    const int tiles = (n + 15) / 16;
+    const int total = tiles_m * tiles_n;
+    // a tile's origin and operand ranges (vb: the block index of the one-block-per-tile form)
+    struct Tile {
+        int row0, col0;
+        int32x4_t rsx, rsw;
+        size_t srec[NT];
+    };
+    auto setup = [&](int vb, Tile &T) {
+        int tm, tn;
+        xcd_tile(vb, PERSIST ? total : (int)gridDim.x, tiles_m, tiles_n, tm, tn);
+        T.row0 = tm * BM;
+        T.col0 = tn * BN;
+        const int tile0 = T.col0 / 16;
+        T.rsx = buffer_rsrc(x + (size_t)T.row0 * k, (uint32_t)(min(BM, m - T.row0) * k * 2));
+        T.rsw = buffer_rsrc(codes + (size_t)tile0 * kbs * 1024, (uint32_t)(min(BN / 16, tiles - tile0) * kbs * 1024));
+        // scale records of this wave's tiles (clamped to a real tile past n)
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) T.srec[nt] = (size_t)min(tile0 + wn * NT + nt, tiles - 1) * kbs * 128;
+    };
+    int vb = blockIdx.x;
+    Tile cur_t;
+    setup(vb, cur_t);
     const uint32_t xs_lds = lds_address(xs), ws_lds = lds_address(ws);
 
     // Activation DMA: lane (q, j) of instruction blk fills slot j of row
@@ -1156,13 +1177,9 @@ __global__ __launch_bounds__(WGM *WGN * 64) void w4a16_pipe_kernel(
             }
         }
     };
-    // scale records of this wave's tiles (clamped to a real tile past n): a
-    // uniform tile offset plus the lane's row
-    size_t srec[NT];
-#pragma unroll
-    for (int nt = 0; nt < NT; nt++) srec[nt] = (size_t)min(tile0 + wn * NT + nt, tiles - 1) * kbs * 128;
+    // scale records: a uniform tile offset plus the lane's row
     const uint8_t *const srow = scales + j * 8;
-    auto load_scales = [&](uint2_t *sc, int kb) {
+    auto load_scales = [&](uint2_t *sc, int kb, const size_t *srec) {
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) sc[nt] = *(const uint2_t *)(srow + srec[nt] + (size_t)kb * 128);
     };
@@ -1240,75 +1257,93 @@ __global__ __launch_bounds__(WGM *WGN * 64) void w4a16_pipe_kernel(
 
     uint2_t sc[NT], nsc[NT];
 #pragma unroll
-    for (int part = 0; part < DMA_GROUPS; part++) dma_part(0, 0, part, rsx, rsw);
+    for (int part = 0; part < DMA_GROUPS; part++) dma_part(0, 0, part, cur_t.rsx, cur_t.rsw);
     // the last step's "next" loads go to a zero-length buffer: no traffic, no branch
-    const int32x4_t none = {rsx[0], rsx[1], 0, rsx[3]};
-    load_scales(sc, 0);
-    for (int kb = 0; kb < kbs; kb++) {
-        const int cur = kb & 1;
-        // this wave's loads of step kb are done; the barrier covers every wave
-        // (and every wave has finished reading the stage the next loads overwrite)
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0); the compiler sees it too
-        __builtin_amdgcn_s_barrier();
-        const bool more = kb + 1 < kbs;
-        if (more) load_scales(nsc, kb + 1);
-        compute(xs + cur * XSTAGE, ws + cur * WSTAGE, sc, cur ^ 1, kb + 1, more ? rsx : none, more ? rsw : none);
-#pragma unroll
-        for (int nt = 0; nt < NT; nt++) sc[nt] = nsc[nt];
-    }
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // no LDS write in flight once the block ends
-
-    // epilogue: acc[mb][nt][v] = Y[row][col + v]
+    const int32x4_t none = {cur_t.rsx[0], cur_t.rsx[1], 0, cur_t.rsx[3]};
+    load_scales(sc, 0, cur_t.srec);
+    int stage = 0;
     const bool vec = (n & 3) == 0 && (ldo & 3) == 0 && ((uintptr_t)out & 15) == 0 &&
                      (EPI != 3 || ((uintptr_t)residual & 7) == 0);
+    for (;;) {
+        const int nvb = vb + (int)gridDim.x;
+        const bool has_next = PERSIST && nvb < total;
+        Tile nxt_t;
+        if (has_next) setup(nvb, nxt_t);
+        for (int kb = 0; kb < kbs; kb++) {
+            // this wave's loads of step kb are done; the barrier covers every wave
+            // (and every wave has finished reading the stage the next loads overwrite)
+            __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0); the compiler sees it too
+            __builtin_amdgcn_s_barrier();
+            const bool more = kb + 1 < kbs;
+            if (more) load_scales(nsc, kb + 1, cur_t.srec);
+            else if (has_next) load_scales(nsc, 0, nxt_t.srec);
+            const int32x4_t rx = more ? cur_t.rsx : (has_next ? nxt_t.rsx : none);
+            const int32x4_t rw = more ? cur_t.rsw : (has_next ? nxt_t.rsw : none);
+            compute(xs + stage * XSTAGE, ws + stage * WSTAGE, sc, stage ^ 1, more ? kb + 1 : 0, rx, rw);
 #pragma unroll
-    for (int mb = 0; mb < MB; mb++) {
-        const int r = row0 + wm * TM + mb * 16 + j;
-        if (r >= m) continue;
+            for (int nt = 0; nt < NT; nt++) sc[nt] = nsc[nt];
+            stage ^= 1;
+        }
+
+        // epilogue: acc[mb][nt][v] = Y[row][col + v]
+        const int row0 = cur_t.row0, col0 = cur_t.col0;
 #pragma unroll
-        for (int nt = 0; nt < NT; nt++) {
-            const int c = col0 + wn * TN + nt * 16 + 4 * q;
-            if (c >= n) continue;
-            const size_t at = (size_t)r * ldo + c;
-            float v[4] = {acc[mb][nt][0], acc[mb][nt][1], acc[mb][nt][2], acc[mb][nt][3]};
-            if (EPI == 0) {
-                if (vec) {
-                    *(float4_t *)((float *)out + at) = float4_t{v[0], v[1], v[2], v[3]};
-                } else {
-                    for (int e = 0; e < 4; e++)
-                        if (c + e < n) ((float *)out)[at + e] = v[e];
-                }
-            } else {
-                half_t o[4];
+        for (int mb = 0; mb < MB; mb++) {
+            const int r = row0 + wm * TM + mb * 16 + j;
+            if (r >= m) continue;
 #pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    if (EPI == 1) o[e] = (half_t)v[e];
-                    else if (EPI == 2) o[e] = (half_t)f32_rounded(gelu_erf(v[e]));
-                    else o[e] = (half_t)0.0f;
-                }
-                if (EPI == 3) {
+            for (int nt = 0; nt < NT; nt++) {
+                const int c = col0 + wn * TN + nt * 16 + 4 * q;
+                if (c >= n) continue;
+                const size_t at = (size_t)r * ldo + c;
+                float v[4] = {acc[mb][nt][0], acc[mb][nt][1], acc[mb][nt][2], acc[mb][nt][3]};
+                if (EPI == 0) {
                     if (vec) {
-                        const uint2_t rw = *(const uint2_t *)(residual + at);
-                        const half2_t r01 = word_as_half2(rw[0]), r23 = word_as_half2(rw[1]);
-                        o[0] = (half_t)f32_rounded(v[0] + (float)r01[0]);
-                        o[1] = (half_t)f32_rounded(v[1] + (float)r01[1]);
-                        o[2] = (half_t)f32_rounded(v[2] + (float)r23[0]);
-                        o[3] = (half_t)f32_rounded(v[3] + (float)r23[1]);
+                        *(float4_t *)((float *)out + at) = float4_t{v[0], v[1], v[2], v[3]};
                     } else {
                         for (int e = 0; e < 4; e++)
-                            if (c + e < n) o[e] = (half_t)f32_rounded(v[e] + (float)residual[at + e]);
+                            if (c + e < n) ((float *)out)[at + e] = v[e];
                     }
-                }
-                if (vec) {
-                    const half2_t o01 = {o[0], o[1]}, o23 = {o[2], o[3]};
-                    *(uint2_t *)((half_t *)out + at) = uint2_t{half2_as_word(o01), half2_as_word(o23)};
                 } else {
-                    for (int e = 0; e < 4; e++)
-                        if (c + e < n) ((half_t *)out)[at + e] = o[e];
+                    half_t o[4];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        if (EPI == 1) o[e] = (half_t)v[e];
+                        else if (EPI == 2) o[e] = (half_t)f32_rounded(gelu_erf(v[e]));
+                        else o[e] = (half_t)0.0f;
+                    }
+                    if (EPI == 3) {
+                        if (vec) {
+                            const uint2_t rw = *(const uint2_t *)(residual + at);
+                            const half2_t r01 = word_as_half2(rw[0]), r23 = word_as_half2(rw[1]);
+                            o[0] = (half_t)f32_rounded(v[0] + (float)r01[0]);
+                            o[1] = (half_t)f32_rounded(v[1] + (float)r01[1]);
+                            o[2] = (half_t)f32_rounded(v[2] + (float)r23[0]);
+                            o[3] = (half_t)f32_rounded(v[3] + (float)r23[1]);
+                        } else {
+                            for (int e = 0; e < 4; e++)
+                                if (c + e < n) o[e] = (half_t)f32_rounded(v[e] + (float)residual[at + e]);
+                        }
+                    }
+                    if (vec) {
+                        const half2_t o01 = {o[0], o[1]}, o23 = {o[2], o[3]};
+                        *(uint2_t *)((half_t *)out + at) = uint2_t{half2_as_word(o01), half2_as_word(o23)};
+                    } else {
+                        for (int e = 0; e < 4; e++)
+                            if (c + e < n) ((half_t *)out)[at + e] = o[e];
+                    }
                 }
             }
         }
+        if (!has_next) break;
+#pragma unroll
+        for (int a = 0; a < MB; a++)
+#pragma unroll
+            for (int b = 0; b < NT; b++) acc[a][b] = float4_t{0.f, 0.f, 0.f, 0.f};
+        vb = nvb;
+        cur_t = nxt_t;
     }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // no LDS write in flight once the block ends
 }
 
 // ============================================================================
@@ -1690,7 +1725,7 @@ inline unsigned cdiv(size_t a, size_t b) { return (unsigned)((a + b - 1) / b); }
 
 const char *const kGemvNames[] = {"w16", "w8"};
 const char *const kGemmNames[] = {"pipe-auto",   "256x256p2w8", "128x128p2w4", "128x256p2w8",
-                                   "256x128w2x2", "128x128w2x2", "128x64w2x2"};
+                                   "256x128w2x2", "128x128w2x2", "128x64w2x2", "256x256p2w8-persist"};
 const char *const kI8Names[] = {"256x256p2w8", "256x256p4k64w8", "256x128p3w8", "256x128p3",
                                  "128x128w2x2", "256x128w2x2", "64x64w2x2"};
 const char *const kGroupedNames[] = {"pipe-auto", "pipe256x128w8", "wave16x16", "pipe128x128w4", "pipe64x128w2"};
@@ -1742,7 +1777,9 @@ void gemm_launch(const Weight &w, const half_t *x, int m, void *y, const half_t 
 }
 
 // Columns [c0, c0 + nc) of the product (c0 a multiple of 16) with BM x BN tiles.
-template <int BM, int BN, int WGM, int WGN, int EPI>
+int device_cus();
+
+template <int BM, int BN, int WGM, int WGN, int EPI, bool PERSIST = false>
 bool w4a16_pipe_launch(const Weight &w, const half_t *x, int m, void *y, const half_t *res, hipStream_t s,
                        int c0 = 0, int nc = -1) {
     if (nc < 0) nc = w.rows - c0;
@@ -1756,13 +1793,15 @@ bool w4a16_pipe_launch(const Weight &w, const half_t *x, int m, void *y, const h
     const size_t esz = EPI == 0 ? 4 : 2;
     void *yo = (uint8_t *)y + (size_t)c0 * esz;
     const half_t *ro = res ? res + c0 : nullptr;
-    const unsigned blocks = cdiv(m, BM) * cdiv(nc, BN);
+    const unsigned tiles = cdiv(m, BM) * cdiv(nc, BN);
+    // persistent: one block per compute unit (a multiple of the 8 XCDs), each taking every gridDim-th tile
+    const unsigned blocks = PERSIST ? std::min(tiles, (unsigned)device_cus() / 8 * 8) : tiles;
     if (w.kind == WeightKind::Q4G32)
-        hipLaunchKernelGGL((w4a16_pipe_kernel<BM, BN, WGM, WGN, true, EPI>), dim3(blocks), dim3(WGM * WGN * 64), 0, s,
-                           codes, scales, x, m, w.cols, nc, w.kblocks(), yo, ro, w.rows);
+        hipLaunchKernelGGL((w4a16_pipe_kernel<BM, BN, WGM, WGN, true, EPI, 2, PERSIST>), dim3(blocks),
+                           dim3(WGM * WGN * 64), 0, s, codes, scales, x, m, w.cols, nc, w.kblocks(), yo, ro, w.rows);
     else
-        hipLaunchKernelGGL((w4a16_pipe_kernel<BM, BN, WGM, WGN, false, EPI>), dim3(blocks), dim3(WGM * WGN * 64), 0, s,
-                           codes, scales, x, m, w.cols, nc, w.kblocks(), yo, ro, w.rows);
+        hipLaunchKernelGGL((w4a16_pipe_kernel<BM, BN, WGM, WGN, false, EPI, 2, PERSIST>), dim3(blocks),
+                           dim3(WGM * WGN * 64), 0, s, codes, scales, x, m, w.cols, nc, w.kblocks(), yo, ro, w.rows);
     return true;
 }
 
@@ -1796,7 +1835,10 @@ void gemm_dispatch(const Weight &w, const half_t *x, int m, void *y, const half_
         case 0: {
             const unsigned cus = (unsigned)device_cus();
             const unsigned tm = cdiv(m, 256), tn = cdiv(w.rows, 256);
-            if (tm * tn >= cus) {
+            if (tm * tn >= 2 * cus && (tm * tn) % cus == 0) {
+                // whole waves of 256x256 tiles, two or more: one persistent block per compute unit
+                if (w4a16_pipe_launch<256, 256, 2, 4, EPI, true>(w, x, m, y, res, s)) return;
+            } else if (tm * tn >= cus) {
                 // 256-column blocks that fill whole waves; the rest on 128x256 tiles
                 unsigned lead = tn;
                 if ((tm * tn) % cus != 0 && tm <= cus && cus % tm == 0) lead = (tm * tn) / cus * (cus / tm);
@@ -1814,6 +1856,7 @@ void gemm_dispatch(const Weight &w, const half_t *x, int m, void *y, const half_
         case 1: if (w4a16_pipe_launch<256, 256, 2, 4, EPI>(w, x, m, y, res, s)) return; break;
         case 2: if (w4a16_pipe_launch<128, 128, 2, 2, EPI>(w, x, m, y, res, s)) return; break;
         case 3: if (w4a16_pipe_launch<128, 256, 2, 4, EPI>(w, x, m, y, res, s)) return; break;
+        case 7: if (w4a16_pipe_launch<256, 256, 2, 4, EPI, true>(w, x, m, y, res, s)) return; break;
         case 5: gemm_launch<128, 128, 2, 2, EPI>(w, x, m, y, res, s); return;
         case 6: gemm_launch<128, 64, 2, 2, EPI>(w, x, m, y, res, s); return;
         default: break;
@@ -1863,7 +1906,7 @@ void gv_launch(const Weight &w, const void *a, const float *sa, int m, int abits
 int variant_count(const char *family) {
     std::string f(family);
     if (f == "gemv") return 2;
-    if (f == "gemm_w4a16") return 7;
+    if (f == "gemm_w4a16") return 8;
     if (f == "i8_gemm") return 7;
     if (f == "grouped") return 5;
     if (f == "mlp") return 4;

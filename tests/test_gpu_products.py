@@ -325,7 +325,7 @@ def test_w4a16_rejects_misaligned_activations(ctx, oracle):
 
 
 W4A16_VARIANTS = ("pipe-auto", "256x256p2w8", "128x128p2w4", "128x256p2w8", "256x128w2x2", "128x128w2x2",
-                  "128x64w2x2")
+                  "128x64w2x2", "256x256p2w8-persist")
 
 
 @pytest.mark.parametrize("layout", [rocm.Q4_G32_F16, rocm.Q4_G64_F32])
@@ -391,6 +391,40 @@ def test_w4a16_f16_output_is_the_f32_product_rounded_once(ctx, oracle, epilogue,
         got = host(ctx, y)
         assert np.array_equal(got.view(np.uint16), want.view(np.uint16)), name
     ctx.select_variant("gemm_w4a16", W4A16_VARIANTS[0])
+
+
+@pytest.mark.parametrize("epilogue", [None, rocm.EPI_NONE, rocm.EPI_GELU, rocm.EPI_RESIDUAL])
+def test_persistent_gemm_walks_several_tiles_per_block(ctx, oracle, epilogue):
+    """The persistent W4A16 kernel (one block per compute unit) on 18 x 16 =
+    288 tiles of 256 x 256, so blocks take two tiles, with ragged last row and
+    column tiles: bitwise equal to one block per tile, for the f32 output and
+    every f16 epilogue; sampled rows against the float64 closed form."""
+    torch = pytest.importorskip("torch")
+    m, k, n = 4400, 256, 4000
+    rng = np.random.default_rng(77 + (epilogue if epilogue is not None else 9))
+    xh = oracle.f32_to_f16_bits(rng.standard_normal((m, k)).astype(np.float32))
+    wf = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    packed = oracle.pack_g32_f16(wf, n, k)
+    w = ctx.upload(packed, rocm.Q4_G32_F16, n, k)
+    x = dev(xh.view(np.float16))
+    rd = dev(rng.standard_normal((m, n)).astype(np.float16))
+    outs = []
+    for name in ("256x256p2w8", "256x256p2w8-persist"):
+        ctx.select_variant("gemm_w4a16", name)
+        if epilogue is None:
+            y = empty((m, n), torch.float32)
+            ctx.linear(w, x, rocm.F16, m, y, rocm.W4A16)
+        else:
+            y = empty((m, n), torch.float16)
+            ctx.linear_f16(w, x, m, y, epilogue, rd if epilogue == rocm.EPI_RESIDUAL else None)
+        outs.append(host(ctx, y))
+    ctx.select_variant("gemm_w4a16", W4A16_VARIANTS[0])
+    assert bits_equal(outs[1], outs[0])
+    if epilogue is None:
+        rows = np.array([0, 255, 256, 2047, 4351, 4399])
+        deq = oracle.unpack_g32_f16(packed).reshape(n, k)
+        want = oracle.w4a16(xh[rows], len(rows), k, deq, n)
+        assert np.abs(outs[1][rows] - want).max() <= MAX_ABS and cosine(outs[1][rows], want) >= MIN_COS
 
 
 def test_w4a16_f16_output_rejects_bad_arguments(ctx, oracle):
