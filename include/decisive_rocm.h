@@ -371,7 +371,19 @@ int32_t dz_pplx_forward_rows(dz_ctx *ctx, dz_pplx *model, const void *rows_host,
  * cache_out (cap bytes). budget_ms == 0 keeps the reference variants. */
 int32_t dz_tune(dz_ctx *ctx, uint32_t budget_ms, const char *cache_in, char *cache_out,
                 size_t cap);
-/* Forces a variant of a family by name (tests and benchmarks). */
+/* Forces a variant of a family by name (tests and benchmarks). Families and
+ * variants (the first of each is the default; every variant of a family
+ * gives the same bits):
+ *   "gemv"        w16, w8
+ *   "gemm_w4a16"  pipe-auto, 256x256p2w8, 128x128p2w4, 128x256p2w8, 256x128w2x2,
+ *                 128x128w2x2, 128x64w2x2, 256x256p2w8-persist
+ *   "i8_gemm"     256x256p2w8, 256x256p4k64w8, 256x128p3w8, 256x128p3, 128x128w2x2,
+ *                 256x128w2x2, 64x64w2x2
+ *   "grouped"     pipe-auto, pipe256x128w8, wave16x16, pipe128x128w4, pipe64x128w2
+ *   "mlp"         pipe-auto, pipe256x64w8, pipe128x64w4, wave16x64
+ *   "delta_scan"  auto, recurrent, chunked64 (the decider's gated delta rule;
+ *                 the two scans regroup its arithmetic differently, so they
+ *                 agree to rounding, not bit for bit) */
 int32_t dz_select_variant(dz_ctx *ctx, const char *family, const char *variant);
 
 #ifdef __cplusplus
