@@ -1052,9 +1052,8 @@ void launch_delta_scan(dz_ctx *ctx, dz_pplx *p, size_t n, hipStream_t s) {
     int dev = 0;
     hipGetDevice(&dev);
     if (dev >= 0 && dev < 64 && !configured[dev]) {
-        hipFuncSetAttribute((const void *)delta_chunk_prep_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)lds);
-        configured[dev] = true;
+        if (hipFuncSetAttribute((const void *)delta_chunk_prep_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)lds) == hipSuccess) configured[dev] = true;
     }
     const unsigned chunks = (unsigned)((n + kChunk - 1) / kChunk);
     hipLaunchKernelGGL(delta_chunk_prep_kernel, dim3(c.delta_heads, chunks), dim3(256), lds, s, p->qhat, p->khat,
@@ -1096,9 +1095,8 @@ void launch_attention(dz_ctx *ctx, dz_pplx *p, size_t nq, size_t n, hipStream_t 
         int dev = 0;
         hipGetDevice(&dev);
         if (dev >= 0 && dev < 64 && !configured[dev]) {
-            hipFuncSetAttribute((const void *)attention_mfma_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                kAttnLds);
-            configured[dev] = true;
+            if (hipFuncSetAttribute((const void *)attention_mfma_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                kAttnLds) == hipSuccess) configured[dev] = true;
         }
         hipLaunchKernelGGL(attention_mfma_kernel, dim3((unsigned)((nq + 15) / 16), c.attn_kv_heads),
                            dim3(64 * group), kAttnLds, s, p->query, p->key, p->value, kvw, (int)nq, (int)n,

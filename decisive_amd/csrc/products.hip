@@ -1740,8 +1740,9 @@ void gemv_launch_one(const Weight &w, const half_t *x, int m, float *y, hipStrea
     int dev = 0;
     hipGetDevice(&dev);
     if (dev >= 0 && dev < 64 && !configured[dev]) {
-        hipFuncSetAttribute((const void *)gemv_kernel<W, MPAD, G32>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        configured[dev] = true;
+        if (hipFuncSetAttribute((const void *)gemv_kernel<W, MPAD, G32>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)lds) == hipSuccess)
+            configured[dev] = true;
     }
     hipLaunchKernelGGL((gemv_kernel<W, MPAD, G32>), dim3(w.tiles()), dim3(W * 64), lds, s, w.codes, w.scales, x,
                        m, w.cols, w.rows, w.kblocks(), y);
@@ -1873,9 +1874,8 @@ void gv_launch_one(const Weight &w, const void *a, const float *sa, int m, int a
     int dev = 0;
     hipGetDevice(&dev);
     if (dev >= 0 && dev < 64 && !configured[dev]) {
-        hipFuncSetAttribute((const void *)grouped_gemv_kernel<BITS, MPAD, AMODE, PROJECT>,
-                            hipFuncAttributeMaxDynamicSharedMemorySize, S::BYTES);
-        configured[dev] = true;
+        if (hipFuncSetAttribute((const void *)grouped_gemv_kernel<BITS, MPAD, AMODE, PROJECT>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, S::BYTES) == hipSuccess) configured[dev] = true;
     }
     dim3 grid(w.tiles(), cdiv(m, 16));
     hipLaunchKernelGGL((grouped_gemv_kernel<BITS, MPAD, AMODE, PROJECT>), grid, dim3(kGvWaves * 64), S::BYTES, s,
