@@ -409,7 +409,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(the hot path shards along N with one all-gather; see DESIGN.md)", file=sys.stderr)
+              "(the hot path would shard along N, with one all-gather of the outputs)", file=sys.stderr)
         sys.exit(2)
 
     import torch

@@ -5,7 +5,7 @@
  * The reference (hyperlogue/decisive, Rust) has no FFI on this path: its
  * quantized products are Rust functions called in-process. Each entry point
  * below names the reference function whose behaviour it takes over; a Rust
- * `Rocm` backend binds these with `extern "C"`.
+ * `Rocm` backend binds these with `extern "C"` blocks of its own.
  *
  * Conventions
  *  - Every call returns a dz_status; on failure dz_last_error(ctx) holds a
