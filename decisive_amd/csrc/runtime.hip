@@ -28,7 +28,8 @@ struct dz_ctx {
     std::string arch;
     int cus = 0;
     int clock_khz = 0;
-    int *flag = nullptr;  // device int: validation / non-finite flag
+    int *flag = nullptr;  // device ints: [0] validation / non-finite flag, [1..62] product flags
+    uint64_t product_calls = 0;  // products since the context began (picks the product flag slot)
     void *work = nullptr; // activation quantization workspace
     size_t work_bytes = 0;
     std::map<std::string, int> variants;
@@ -115,6 +116,17 @@ int32_t flagged_sync(dz_ctx *ctx, F enqueue, int *value) {
            "flag readback");
     DZ_HIP(ctx, hipStreamSynchronize(ctx->stream), "stream synchronize");
     return DZ_OK;
+}
+
+// The non-finite-activation flag of one asynchronous product: slot
+// 1 + (call % 62) of the flag buffer, so that a call never reads a flag that
+// an earlier call set. The 62 slots are cleared together, by one launch that
+// the stream orders after every earlier product, each time the ring starts
+// over (instead of one clearing launch per product).
+int *product_flag(dz_ctx *ctx) {
+    const int slot = (int)(ctx->product_calls++ % 62);
+    if (slot == 0) dz::launch_fill_i32(ctx->flag + 1, 0, 62, ctx->stream);
+    return ctx->flag + 1 + slot;
 }
 
 int32_t ensure_work(dz_ctx *ctx, size_t bytes) {
@@ -272,6 +284,7 @@ const char *dz_last_error(const dz_ctx *ctx) { return ctx ? ctx->error.c_str() :
 int32_t dz_set_stream(dz_ctx *ctx, void *hip_stream) {
     DZ_BEGIN(ctx);
     ctx->stream = hip_stream ? (hipStream_t)hip_stream : ctx->own;
+    ctx->product_calls = 0;
     return DZ_OK;
 }
 
@@ -476,10 +489,10 @@ int32_t grouped_linear(dz_ctx *ctx, const dz_weight *a, const dz_weight *b, cons
     if (rc) return rc;
     int8_t *q = (int8_t *)ctx->work;
     float *s = (float *)((uint8_t *)ctx->work + (qbytes + 255) / 256 * 256);
-    dz::launch_fill_i32(ctx->flag, 0, 1, ctx->stream);
-    dz::launch_act_quantize(x, (int)m, w.cols, abits, q, s, ctx->flag, ctx->stream);
-    dz::launch_grouped(w, q, s, (int)m, ya, ctx->flag, variant(ctx, "grouped"), ctx->stream);
-    if (b) dz::launch_grouped(b->w, q, s, (int)m, yb, ctx->flag, variant(ctx, "grouped"), ctx->stream);
+    int *bad = product_flag(ctx);
+    dz::launch_act_quantize(x, (int)m, w.cols, abits, q, s, bad, ctx->stream);
+    dz::launch_grouped(w, q, s, (int)m, ya, bad, variant(ctx, "grouped"), ctx->stream);
+    if (b) dz::launch_grouped(b->w, q, s, (int)m, yb, bad, variant(ctx, "grouped"), ctx->stream);
     return launched(ctx, "grouped linear");
 }
 
@@ -559,9 +572,9 @@ int32_t dz_mlp_requant(dz_ctx *ctx, const dz_weight *gate, const dz_weight *up, 
     if (rc) return rc;
     int8_t *q = (int8_t *)ctx->work;
     float *s = (float *)((uint8_t *)ctx->work + (qbytes + 255) / 256 * 256);
-    dz::launch_fill_i32(ctx->flag, 0, 1, ctx->stream);
-    dz::launch_act_quantize(x, (int)m, g.cols, 8, q, s, ctx->flag, ctx->stream);
-    dz::launch_mlp_requant(g, u, q, s, (int)m, qo, so, ctx->flag, variant(ctx, "mlp"), ctx->stream);
+    int *bad = product_flag(ctx);
+    dz::launch_act_quantize(x, (int)m, g.cols, 8, q, s, bad, ctx->stream);
+    dz::launch_mlp_requant(g, u, q, s, (int)m, qo, so, bad, variant(ctx, "mlp"), ctx->stream);
     return launched(ctx, "fused MLP");
 }
 

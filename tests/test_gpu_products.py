@@ -208,6 +208,34 @@ def test_fused_mlp_large_m_pipeline_equals_unfused(ctx, oracle):
     assert np.isnan(host(ctx, s)).all() and not host(ctx, q).any()
 
 
+def test_product_flags_do_not_leak_across_calls(ctx, oracle):
+    """Each asynchronous W4A8 product has its own non-finite flag: over 140
+    calls (past two wraps of the flag ring) only the calls given a NaN
+    activation produce NaN, every other call equals a clean call bit for bit."""
+    torch = pytest.importorskip("torch")
+    m, n, k = 40, 128, 256
+    rng = np.random.default_rng(21)
+    w = ctx.quantize(dev((rng.standard_normal((n, k)) * 0.02).astype(np.float32)), rocm.F32, n, k, 4, 64)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    bad = x.copy()
+    bad[3, 7] = np.nan
+    xd, bd = dev(x), dev(bad)
+    want = empty((m, n), torch.float32)
+    ctx.linear(w, xd, rocm.F32, m, want, rocm.W4A8)
+    want = host(ctx, want)
+    ys = [empty((m, n), torch.float32) for _ in range(140)]
+    nan_calls = {5, 100}
+    for i, y in enumerate(ys):
+        ctx.linear(w, bd if i in nan_calls else xd, rocm.F32, m, y, rocm.W4A8)
+    for i, y in enumerate(ys):
+        got = host(ctx, y)
+        if i in nan_calls:
+            assert np.isnan(got).any(), i
+        else:
+            assert bits_equal(got, want), i
+    w.free()
+
+
 def test_fused_mlp_requant_equals_unfused(ctx, oracle):
     """grouped_q4.rs:313-354: fused gate/up/SiLU/requant == unfused, word-exact;
     both against the oracle composition within one code."""
