@@ -1545,14 +1545,19 @@ __global__ __launch_bounds__(WGM *WGN * 64) void grouped_pipe_kernel(
 // as mlp_requant_kernel computes them. BM/32 waves stacked along M (wave tile
 // 32 x 64): a row's 64 columns are held by the four lanes j, j+16, j+32,
 // j+48 of one wave, so the row maximum is two shuffles. Q4 weights. BM is
-// 256 (8 waves) or 128 (4 waves, half the LDS: two blocks fit a CU).
-template <int BM>
+// 256 (8 waves) or 128 (4 waves, half the LDS: two blocks fit a CU). With
+// WN = 2 the waves are paired along N instead (wave tile 64 rows x 32 columns
+// of each weight): a weight fragment is unpacked once for four row blocks
+// rather than two, and the row maximum takes one exchange through LDS between
+// the pair.
+template <int BM, int WN = 1>
 __global__ __launch_bounds__(BM / 32 * 64) void mlp_pipe_kernel(
     const uint8_t *__restrict__ gcodes, const uint8_t *__restrict__ gscales, const uint8_t *__restrict__ ucodes,
     const uint8_t *__restrict__ uscales, const int8_t *__restrict__ q, const float *__restrict__ sx, int m, int n,
     int groups, int kbs, int8_t *__restrict__ qo, float *__restrict__ so, const int *__restrict__ bad) {
     static_assert(BM == 256 || BM == 128, "8 or 4 waves");
-    constexpr int WAVES = BM / 32, MB = 2, NT = 4;
+    static_assert(WN == 1 || WN == 2, "one or two waves across the 64 columns");
+    constexpr int WAVES = BM / 32, MB = 2 * WN, NT = 4 / WN, WR = 32 * WN;
     constexpr int XSTAGE = BM * 128;   // activation codes, 2 groups per step
     constexpr int CSTAGE = 8 * 1024;   // gate tiles 0-3, up tiles 0-3: one tile16x128 chunk each
     constexpr int SWSTAGE = 2 * 1024;  // scale records: [weight][8 tiles x 128 B], tiles 0-3 used
@@ -1562,8 +1567,10 @@ __global__ __launch_bounds__(BM / 32 * 64) void mlp_pipe_kernel(
     __shared__ __align__(16) uint8_t cs[2 * CSTAGE];
     __shared__ __align__(16) uint8_t sws[2 * SWSTAGE];
     __shared__ __align__(16) uint8_t sxs[2 * SXSTAGE];
+    __shared__ float pair_max[WN == 2 ? BM * 2 : 1];
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), lane = threadIdx.x % 64;
+    const int wm = wave / WN, wn = wave % WN;
     const int qd = lane / 16, j = lane % 16;
     const int tiles_m = (m + BM - 1) / BM, tiles_n = n / 64;
     int tm, tn;
@@ -1631,11 +1638,12 @@ __global__ __launch_bounds__(BM / 32 * 64) void mlp_pipe_kernel(
         for (int nt = 0; nt < NT; nt++) {
 #pragma unroll
             for (int wgt = 0; wgt < 2; wgt++) {
-                const uint2_t wds = *(const uint2_t *)(cst + (wgt * 4 + nt) * 1024 + lane * 16 + gp * 8);
+                const int t = wn * NT + nt;
+                const uint2_t wds = *(const uint2_t *)(cst + (wgt * 4 + t) * 1024 + lane * 16 + gp * 8);
                 const uint2_t lo = nibbles_to_i8(wds[0]), hi = nibbles_to_i8(wds[1]);
                 const int4_t b = int4_t{(int)lo[0], (int)lo[1], (int)hi[0], (int)hi[1]};
-                const float4_t s01 = *(const float4_t *)(swst + wgt * 1024 + nt * 128 + qd * 32);
-                const float4_t s23 = *(const float4_t *)(swst + wgt * 1024 + nt * 128 + qd * 32 + 16);
+                const float4_t s01 = *(const float4_t *)(swst + wgt * 1024 + t * 128 + qd * 32);
+                const float4_t s23 = *(const float4_t *)(swst + wgt * 1024 + t * 128 + qd * 32 + 16);
                 const float4_t sv = gp ? float4_t{s01[1], s01[3], s23[1], s23[3]} : float4_t{s01[0], s01[2], s23[0], s23[2]};
                 if (wgt == 0) {
                     gb[nt] = b;
@@ -1648,7 +1656,7 @@ __global__ __launch_bounds__(BM / 32 * 64) void mlp_pipe_kernel(
         }
 #pragma unroll
         for (int mb = 0; mb < MB; mb++) {
-            const int r = wave * 32 + mb * 16 + j;
+            const int r = wm * WR + mb * 16 + j;
             const int c1 = 4 * gp + qd / 2, c2 = c1 + 2;
             const uint2_t a0 = *(const uint2_t *)(xst + r * 128 + ((c1 ^ ((r >> 1) & 7)) * 16) + 8 * (qd & 1));
             const uint2_t a1 = *(const uint2_t *)(xst + r * 128 + ((c2 ^ ((r >> 1) & 7)) * 16) + 8 * (qd & 1));
@@ -1684,10 +1692,10 @@ __global__ __launch_bounds__(BM / 32 * 64) void mlp_pipe_kernel(
 
     // silu(g) * u and the A8 requantization of the row's 64 columns
     const int blocks = n / 64;
+    float val[MB][NT][4];
+    float rmax[MB];
 #pragma unroll
     for (int mb = 0; mb < MB; mb++) {
-        const int r = row0 + wave * 32 + mb * 16 + j;
-        float val[NT][4];
         float local = 0.0f;
 #pragma unroll
         for (int nt = 0; nt < NT; nt++)
@@ -1695,12 +1703,25 @@ __global__ __launch_bounds__(BM / 32 * 64) void mlp_pipe_kernel(
             for (int v = 0; v < 4; v++) {
                 const float gv = ga[mb][nt][v];
                 const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-gv)));
-                val[nt][v] = __fmul_rn(__fmul_rn(gv, sig), ua[mb][nt][v]);
-                local = fmaxf(local, fabsf(val[nt][v]));
+                val[mb][nt][v] = __fmul_rn(__fmul_rn(gv, sig), ua[mb][nt][v]);
+                local = fmaxf(local, fabsf(val[mb][nt][v]));
             }
         local = fmaxf(local, __shfl_xor(local, 16));
         local = fmaxf(local, __shfl_xor(local, 32));
-        const float scale = fmaxf(__fdiv_rn(local, 127.0f), FLT_MIN);
+        rmax[mb] = local;
+    }
+    if (WN == 2) {  // the other half of each row's columns is in the paired wave
+#pragma unroll
+        for (int mb = 0; mb < MB; mb++)
+            if (qd == 0) pair_max[(wm * WR + mb * 16 + j) * 2 + wn] = rmax[mb];
+        __syncthreads();
+#pragma unroll
+        for (int mb = 0; mb < MB; mb++) rmax[mb] = fmaxf(rmax[mb], pair_max[(wm * WR + mb * 16 + j) * 2 + (wn ^ 1)]);
+    }
+#pragma unroll
+    for (int mb = 0; mb < MB; mb++) {
+        const int r = row0 + wm * WR + mb * 16 + j;
+        const float scale = fmaxf(__fdiv_rn(rmax[mb], 127.0f), FLT_MIN);
         const float inverse = __frcp_rn(scale);
         if (r >= m) continue;
 #pragma unroll
@@ -1709,13 +1730,13 @@ __global__ __launch_bounds__(BM / 32 * 64) void mlp_pipe_kernel(
             if (!nan_out) {
 #pragma unroll
                 for (int v = 0; v < 4; v++) {
-                    const float c = fminf(fmaxf(__builtin_rintf(__fmul_rn(val[nt][v], inverse)), -127.0f), 127.0f);
+                    const float c = fminf(fmaxf(__builtin_rintf(__fmul_rn(val[mb][nt][v], inverse)), -127.0f), 127.0f);
                     packed |= ((uint32_t)(uint8_t)(int8_t)(int)c) << (8 * v);
                 }
             }
-            *(uint32_t *)(qo + (size_t)r * n + col0 + nt * 16 + 4 * qd) = packed;
+            *(uint32_t *)(qo + (size_t)r * n + col0 + (wn * NT + nt) * 16 + 4 * qd) = packed;
         }
-        if (qd == 0) so[(size_t)r * blocks + tn] = nan_out ? __builtin_nanf("") : scale;
+        if (qd == 0 && wn == 0) so[(size_t)r * blocks + tn] = nan_out ? __builtin_nanf("") : scale;
     }
 }
 
@@ -1728,8 +1749,9 @@ const char *const kGemmNames[] = {"pipe-auto",   "256x256p2w8", "128x128p2w4", "
                                    "256x128w2x2", "128x128w2x2", "128x64w2x2", "256x256p2w8-persist"};
 const char *const kI8Names[] = {"256x256p2w8", "256x256p4k64w8", "256x128p3w8", "256x128p3",
                                  "128x128w2x2", "256x128w2x2", "64x64w2x2"};
-const char *const kGroupedNames[] = {"pipe-auto", "pipe256x128w8", "wave16x16", "pipe128x128w4", "pipe64x128w2"};
-const char *const kMlpNames[] = {"pipe-auto", "pipe256x64w8", "pipe128x64w4", "wave16x64"};
+const char *const kGroupedNames[] = {"pipe-auto",    "pipe256x128w8", "wave16x16",   "pipe128x128w4",
+                                     "pipe64x128w2", "pipe128x128m8", "pipe128x128n8"};
+const char *const kMlpNames[] = {"pipe-auto", "pipe256x64w8", "pipe128x64w4", "wave16x64", "pipe256x64n2", "pipe128x64n2"};
 const char *const kDeltaNames[] = {"auto", "recurrent", "chunked64"};
 
 template <int W, int MPAD, bool G32>
@@ -1908,8 +1930,8 @@ int variant_count(const char *family) {
     if (f == "gemv") return 2;
     if (f == "gemm_w4a16") return 8;
     if (f == "i8_gemm") return 7;
-    if (f == "grouped") return 5;
-    if (f == "mlp") return 4;
+    if (f == "grouped") return 7;
+    if (f == "mlp") return 6;
     if (f == "delta_scan") return 3;
     return 0;
 }
@@ -1974,19 +1996,24 @@ bool grouped_pipe_launch(const Weight &w, const int8_t *q, const float *sx, int 
     return true;
 }
 
-// Variants: 1 pipelined 256x128 tiles (8 waves), 3 128x128 (4 waves), 4 64x128
-// (2 waves), 2 one wave per 16x16 tile. 0 picks 128x128 tiles when their grid
-// covers half the compute units, else 64x128 tiles when that grid covers a
-// quarter, else the one-wave tiles (measured: 128x128 beats 256x128 by 5-15% at
-// every shape from 229x2560x12288 to 16384x4096x14336, and 64x128 wins below
-// the half-wave mark). Every variant folds in group order: all are bitwise equal.
+// Variants: 1 pipelined 256x128 tiles (8 waves), 3 128x128 (4 waves as 2x2),
+// 5 128x128 (4 waves side by side, each 128 rows x 32 columns), 6 128x128 (4
+// waves stacked, each 32 rows x 128 columns), 4 64x128 (2 waves), 2 one wave
+// per 16x16 tile. 0 picks 128x128 tiles when their grid covers half the compute
+// units, else 64x128 tiles when that grid covers a quarter, else the one-wave
+// tiles (measured: 128x128 beats 256x128 by 5-15% at every shape from
+// 229x2560x12288 to 16384x4096x14336, and 64x128 wins below the half-wave
+// mark). Among the 128x128 layouts, the side-by-side one unpacks each weight
+// fragment once for 8 row blocks instead of 4; it is 4-11% faster from 4096
+// rows up and 1-3% slower at 1024, so 0 takes it from 2048 rows. Every variant
+// folds in group order: all are bitwise equal.
 void launch_grouped(const Weight &w, const int8_t *q, const float *sx, int m, float *y,
                     const int *bad, int variant, hipStream_t s) {
     if (m == 0) return;
     const unsigned cus = (unsigned)device_cus(), tn = cdiv(w.rows, 128);
     int pick = variant;
     if (variant == 0) {
-        if (cdiv(m, 128) * tn >= cus / 2) pick = 3;
+        if (cdiv(m, 128) * tn >= cus / 2) pick = m >= 2048 ? 5 : 3;
         else if (cdiv(m, 64) * tn >= cus / 4) pick = 4;
         else pick = 2;
     }
@@ -1994,6 +2021,8 @@ void launch_grouped(const Weight &w, const int8_t *q, const float *sx, int m, fl
         case 1: if (grouped_pipe_launch<256, 2, 4>(w, q, sx, m, y, bad, s)) return; break;
         case 3: if (grouped_pipe_launch<128, 2, 2>(w, q, sx, m, y, bad, s)) return; break;
         case 4: if (grouped_pipe_launch<64, 1, 2>(w, q, sx, m, y, bad, s)) return; break;
+        case 5: if (grouped_pipe_launch<128, 1, 4>(w, q, sx, m, y, bad, s)) return; break;
+        case 6: if (grouped_pipe_launch<128, 4, 1>(w, q, sx, m, y, bad, s)) return; break;
         default: break;
     }
     dim3 grid(cdiv(w.tiles(), 4), cdiv(m, 16));
@@ -2006,11 +2035,13 @@ void launch_grouped(const Weight &w, const int8_t *q, const float *sx, int m, fl
 }
 
 // Variants: 1 pipelined 256x64 blocks (8 waves), 2 128x64 blocks (4 waves),
-// 3 one wave per 16x64 block. 0 picks the 256-row blocks when their grid
-// covers half the compute units but not all of them, else the 128-row blocks
-// when theirs covers half, else the one-wave blocks (measured at K=2560,
-// N=9216: 128-row blocks are 3-14% faster from M=1024 to 4096, 256-row blocks
-// 4% faster at M=229). All variants are word-exact with the unfused composition.
+// 4 and 5 the same blocks with the waves paired along N (wave tile 64 x 32), 3
+// one wave per 16x64 block. 0 picks the paired 256-row blocks when their grid
+// covers half the compute units but not all of them, else the paired 128-row
+// blocks when theirs covers half, else the one-wave blocks (measured at K=2560,
+// N=9216: the paired layouts are 7-16% faster than the stacked ones at every M
+// from 229 to 4096, and 128-row blocks beat 256-row blocks from M=1024 up).
+// All variants are word-exact with the unfused composition.
 void launch_mlp_requant(const Weight &gate, const Weight &up, const int8_t *q, const float *sx,
                         int m, int8_t *qo, float *so, const int *bad, int variant, hipStream_t s) {
     if (m == 0) return;
@@ -2021,8 +2052,8 @@ void launch_mlp_requant(const Weight &gate, const Weight &up, const int8_t *q, c
     int pick = variant;
     if (variant == 0) {
         const unsigned b256 = cdiv(m, 256) * tn, b128 = cdiv(m, 128) * tn;
-        if (2 * b256 >= cus && b256 < cus) pick = 1;
-        else if (2 * b128 >= cus) pick = 2;
+        if (2 * b256 >= cus && b256 < cus) pick = 4;
+        else if (2 * b128 >= cus) pick = 5;
         else pick = 3;
     }
     if (fits && pick == 1) {
@@ -2033,6 +2064,18 @@ void launch_mlp_requant(const Weight &gate, const Weight &up, const int8_t *q, c
     if (fits && pick == 2) {
         hipLaunchKernelGGL(mlp_pipe_kernel<128>, dim3(cdiv(m, 128) * tn), dim3(256), 0, s, gate.codes, gate.scales,
                            up.codes, up.scales, q, sx, m, gate.rows, gate.groups, gate.kblocks(), qo, so, bad);
+        return;
+    }
+    if (fits && pick == 4) {
+        hipLaunchKernelGGL((mlp_pipe_kernel<256, 2>), dim3(cdiv(m, 256) * tn), dim3(512), 0, s, gate.codes,
+                           gate.scales, up.codes, up.scales, q, sx, m, gate.rows, gate.groups, gate.kblocks(), qo,
+                           so, bad);
+        return;
+    }
+    if (fits && pick == 5) {
+        hipLaunchKernelGGL((mlp_pipe_kernel<128, 2>), dim3(cdiv(m, 128) * tn), dim3(256), 0, s, gate.codes,
+                           gate.scales, up.codes, up.scales, q, sx, m, gate.rows, gate.groups, gate.kblocks(), qo,
+                           so, bad);
         return;
     }
     dim3 grid(gate.rows / 64, cdiv(m, 16));

@@ -53,7 +53,7 @@ def test_grouped_large_m_pipeline_bit_exact(ctx, oracle, wb, ab, m, k, n):
     w = ctx.quantize(dev(raw), rocm.BF16, n, k, wb, 64)
     mode = rocm.W4A4 if ab == 4 else rocm.W4A8
     outs = []
-    names = ("pipe256x128w8", "wave16x16", "pipe128x128w4", "pipe64x128w2", "pipe-auto")
+    names = ("pipe256x128w8", "wave16x16", "pipe128x128w4", "pipe64x128w2", "pipe128x128m8", "pipe128x128n8", "pipe-auto")
     for name in names:
         ctx.select_variant("grouped", name)
         y = empty((m, n), torch.float32)
@@ -196,7 +196,7 @@ def test_fused_mlp_large_m_pipeline_equals_unfused(ctx, oracle):
     ctx.act_quantize(g, m, n, 8, q2, s2)
     q = empty((m, n), torch.int8)
     s = empty((m, n // 64), torch.float32)
-    for name in ("pipe256x64w8", "pipe128x64w4", "wave16x64", "pipe-auto"):
+    for name in ("pipe256x64w8", "pipe128x64w4", "wave16x64", "pipe256x64n2", "pipe128x64n2", "pipe-auto"):
         ctx.select_variant("mlp", name)
         q.zero_()
         ctx.mlp_requant(gate, up, xd, m, q, s)
@@ -260,7 +260,7 @@ def test_fused_mlp_requant_equals_unfused(ctx, oracle):
     ctx.act_quantize(g, m, n, 8, q2, s2)
     q = empty((m, n), torch.int8)
     s = empty((m, n // 64), torch.float32)
-    for name in ("pipe256x64w8", "pipe128x64w4", "wave16x64", "pipe-auto"):
+    for name in ("pipe256x64w8", "pipe128x64w4", "wave16x64", "pipe256x64n2", "pipe128x64n2", "pipe-auto"):
         ctx.select_variant("mlp", name)
         q.zero_()
         ctx.mlp_requant(gate, up, xd, m, q, s)
