@@ -42,6 +42,8 @@ void weight_free(dz_weight *h);
 int32_t ctx_readout_rows(dz_ctx *ctx, const Weight &w, const float *norm, const void *hidden, int dtype,
                          const int32_t *select, size_t rows, float eps, float *logits);
 int ctx_variant(dz_ctx *ctx, const char *family);
+int32_t ctx_product_add(dz_ctx *ctx, const dz_weight *w, const float *x, const int8_t *q, const float *qs,
+                        size_t m, float *h, bool *fused);
 
 namespace {
 
@@ -1014,6 +1016,20 @@ int32_t linear(dz_ctx *ctx, const dz_weight *w, const float *x, size_t m, float 
     return dz_linear(ctx, w, x, DZ_F32, m, y, DZ_W4A8);
 }
 
+// The residual connection h += W·x (x f32, or A8 codes q with scales qs): in
+// the product's epilogue when the pipelined kernel takes the rows, else the
+// product into tmp and an add. Both give the same bits.
+int32_t product_add(dz_ctx *ctx, const dz_weight *w, const float *x, const int8_t *q, const float *qs, size_t m,
+                    float *h, float *tmp) {
+    bool fused = false;
+    int32_t rc = ctx_product_add(ctx, w, x, q, qs, m, h, &fused);
+    if (rc || fused) return rc;
+    rc = x ? linear(ctx, w, x, m, tmp) : dz_linear_q8(ctx, w, q, qs, m, tmp);
+    if (rc) return rc;
+    launch_add(h, tmp, 0, m * (size_t)weight_of(w).rows, ctx_stream(ctx));
+    return DZ_OK;
+}
+
 // backbone.rs:232-250: post-norm MLP with residual, in place on hidden
 int32_t mlp(dz_ctx *ctx, dz_pplx *p, const dz_pplx::Layer &L, size_t n) {
     const dz_pplx_config &c = p->cfg;
@@ -1023,15 +1039,13 @@ int32_t mlp(dz_ctx *ctx, dz_pplx *p, const dz_pplx::Layer &L, size_t n) {
     if (weight_of(L.gate).kind == WeightKind::Q4G64 && weight_of(L.up).kind == WeightKind::Q4G64) {
         // gate/up, silu(gate)*up and the A8 codes of the down projection in one pass
         rc = dz_mlp_requant(ctx, L.gate, L.up, p->normed, n, p->codes, p->code_scales);
-        if (!rc) rc = dz_linear_q8(ctx, L.down, p->codes, p->code_scales, n, p->projected);
+        if (!rc) rc = product_add(ctx, L.down, nullptr, p->codes, p->code_scales, n, p->hidden, p->projected);
     } else {
         rc = dz_linear_pair(ctx, L.gate, L.up, p->normed, n, p->gate, p->up, DZ_W4A8);
         if (!rc) launch_silu_mul(p->gate, p->up, n * (size_t)c.ff, s);
-        if (!rc) rc = linear(ctx, L.down, p->gate, n, p->projected);
+        if (!rc) rc = product_add(ctx, L.down, p->gate, nullptr, nullptr, n, p->hidden, p->projected);
     }
-    if (rc) return rc;
-    launch_add(p->hidden, p->projected, 0, n * (size_t)c.hidden, s);
-    return DZ_OK;
+    return rc;
 }
 
 // Variant 1 runs the token-by-token scan, 2 the chunked one; 0 picks the
@@ -1078,10 +1092,7 @@ int32_t delta_layer(dz_ctx *ctx, dz_pplx *p, const dz_pplx::Layer &L, size_t n) 
     launch_delta_scan(ctx, p, n, s);
     hipLaunchKernelGGL(delta_gate_kernel, dim3((unsigned)n, c.delta_heads), dim3(64), 0, s, p->heads, (int)n,
                        c.delta_heads, L.norm, p->z, p->ctx);
-    rc = linear(ctx, L.out, p->ctx, n, p->projected);
-    if (rc) return rc;
-    launch_add(p->hidden, p->projected, 0, n * (size_t)c.hidden, s);
-    return DZ_OK;
+    return product_add(ctx, L.out, p->ctx, nullptr, nullptr, n, p->hidden, p->projected);
 }
 
 // The MFMA kernel for query-head groups of up to 8 (the reference's 4) and
@@ -1136,15 +1147,14 @@ int32_t attention_layer(dz_ctx *ctx, dz_pplx *p, const dz_pplx::Layer &L, size_t
     launch_attention(ctx, p, nq, n, s);
     hipLaunchKernelGGL(attention_gate_kernel, dim3(blocks_of(nq * c.attn_heads * kAd, 256)), dim3(256), 0, s,
                        p->heads, (int)nq, c.attn_heads, p->wide + kAd, qw, 2 * kAd, p->ctx);
-    rc = linear(ctx, L.o, p->ctx, nq, p->projected);
-    if (rc) return rc;
-    if (markers) {
+    if (markers) {  // the residual rows of the markers, before o_proj adds onto them
         hipLaunchKernelGGL(gather_rows_kernel, dim3(blocks_of(count * d, 256)), dim3(256), 0, s, p->hidden, markers,
                            (int)count, (int)d, p->picked);
         hipError_t e = hipMemcpyAsync(p->hidden, p->picked, count * d * sizeof(float), hipMemcpyDeviceToDevice, s);
         if (e != hipSuccess) return ctx_hip_fail(ctx, e, "pplx prune");
     }
-    launch_add(p->hidden, p->projected, 0, nq * d, s);
+    rc = product_add(ctx, L.o, p->ctx, nullptr, nullptr, nq, p->hidden, p->projected);
+    if (rc) return rc;
     *rows_out = nq;
     return DZ_OK;
 }

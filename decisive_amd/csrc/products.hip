@@ -1371,7 +1371,7 @@ __global__ __launch_bounds__(WGM *WGN * 64) void w4a16_pipe_kernel(
 template <int BITS, int BM, int BN, int WGM, int WGN>
 __global__ __launch_bounds__(WGM *WGN * 64) void grouped_pipe_kernel(
     const uint8_t *__restrict__ codes, const uint8_t *__restrict__ scales, const int8_t *__restrict__ q,
-    const float *__restrict__ sx, int m, int n, int groups, int kbs, float *__restrict__ y,
+    const float *__restrict__ sx, int m, int n, int groups, int kbs, float *y, const float *res,
     const int *__restrict__ bad) {
     constexpr int WAVES = WGM * WGN;
     constexpr int TM = BM / WGM, TN = BN / WGN, MB = TM / 16, NT = TN / 16;
@@ -1516,8 +1516,9 @@ __global__ __launch_bounds__(WGM *WGN * 64) void grouped_pipe_kernel(
         __builtin_amdgcn_s_waitcnt(0x0F70);  // no LDS write in flight once the block ends
     }
 
-    // acc[mb][nt][v] = Y[row][col + v]
-    const bool vec = (n & 3) == 0 && ((uintptr_t)y & 15) == 0;
+    // acc[mb][nt][v] = Y[row][col + v]; with `res` (which may be y itself) the
+    // kernel stores res + Y, the same float add as a separate residual pass
+    const bool vec = (n & 3) == 0 && ((uintptr_t)y & 15) == 0 && ((uintptr_t)res & 15) == 0;
 #pragma unroll
     for (int mb = 0; mb < MB; mb++) {
         const int r = row0 + wm * TM + mb * 16 + j;
@@ -1529,11 +1530,16 @@ __global__ __launch_bounds__(WGM *WGN * 64) void grouped_pipe_kernel(
             float4_t v = acc[mb][nt];
             if (nan_out) v = float4_t{__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf("")};
             float *dst = y + (size_t)r * n + c;
+            const float *add = res + (size_t)r * n + c;
             if (vec) {
+                if (res && !nan_out) {
+                    const float4_t h = *(const float4_t *)add;
+                    for (int e = 0; e < 4; e++) v[e] = __fadd_rn(h[e], v[e]);
+                }
                 *(float4_t *)dst = v;
             } else {
                 for (int e = 0; e < 4; e++)
-                    if (c + e < n) dst[e] = v[e];
+                    if (c + e < n) dst[e] = res && !nan_out ? __fadd_rn(add[e], v[e]) : v[e];
             }
         }
     }
@@ -1983,16 +1989,16 @@ void launch_grouped_records(const Weight &w, const uint32_t *records, int m, flo
 // All fold in the reference order, so all give the same bits.
 template <int BM, int WGM, int WGN>
 bool grouped_pipe_launch(const Weight &w, const int8_t *q, const float *sx, int m, float *y, const int *bad,
-                         hipStream_t s) {
+                         hipStream_t s, const float *res) {
     if ((size_t)BM * w.groups * 64 >= ((size_t)1 << 31) || (size_t)8 * w.kblocks() * 1024 >= ((size_t)1 << 31))
         return false;
     const dim3 blocks(cdiv(m, BM) * cdiv(w.rows, 128));
     if (w.bits == 4)
         hipLaunchKernelGGL((grouped_pipe_kernel<4, BM, 128, WGM, WGN>), blocks, dim3(WGM * WGN * 64), 0, s, w.codes,
-                           w.scales, q, sx, m, w.rows, w.groups, w.kblocks(), y, bad);
+                           w.scales, q, sx, m, w.rows, w.groups, w.kblocks(), y, res, bad);
     else
         hipLaunchKernelGGL((grouped_pipe_kernel<8, BM, 128, WGM, WGN>), blocks, dim3(WGM * WGN * 64), 0, s, w.codes,
-                           w.scales, q, sx, m, w.rows, w.groups, w.kblocks(), y, bad);
+                           w.scales, q, sx, m, w.rows, w.groups, w.kblocks(), y, res, bad);
     return true;
 }
 
@@ -2007,24 +2013,32 @@ bool grouped_pipe_launch(const Weight &w, const int8_t *q, const float *sx, int 
 // fragment once for 8 row blocks instead of 4; it is 4-11% faster from 4096
 // rows up and 1-3% slower at 1024, so 0 takes it from 2048 rows. Every variant
 // folds in group order: all are bitwise equal.
-void launch_grouped(const Weight &w, const int8_t *q, const float *sx, int m, float *y,
-                    const int *bad, int variant, hipStream_t s) {
-    if (m == 0) return;
+int grouped_pick(const Weight &w, int m, int variant) {
+    if (variant != 0) return variant;
     const unsigned cus = (unsigned)device_cus(), tn = cdiv(w.rows, 128);
-    int pick = variant;
-    if (variant == 0) {
-        if (cdiv(m, 128) * tn >= cus / 2) pick = m >= 2048 ? 5 : 3;
-        else if (cdiv(m, 64) * tn >= cus / 4) pick = 4;
-        else pick = 2;
-    }
-    switch (pick) {
-        case 1: if (grouped_pipe_launch<256, 2, 4>(w, q, sx, m, y, bad, s)) return; break;
-        case 3: if (grouped_pipe_launch<128, 2, 2>(w, q, sx, m, y, bad, s)) return; break;
-        case 4: if (grouped_pipe_launch<64, 1, 2>(w, q, sx, m, y, bad, s)) return; break;
-        case 5: if (grouped_pipe_launch<128, 1, 4>(w, q, sx, m, y, bad, s)) return; break;
-        case 6: if (grouped_pipe_launch<128, 4, 1>(w, q, sx, m, y, bad, s)) return; break;
+    if (cdiv(m, 128) * tn >= cus / 2) return m >= 2048 ? 5 : 3;
+    if (cdiv(m, 64) * tn >= cus / 4) return 4;
+    return 2;
+}
+
+bool grouped_adds_residual(const Weight &w, int m, int variant) {
+    const int pick = grouped_pick(w, m, variant);
+    return m > 16 && w.kind != WeightKind::Q4G32 && pick != 2 && pick >= 1 && pick <= 6 &&
+           (size_t)256 * w.groups * 64 < ((size_t)1 << 31) && (size_t)8 * w.kblocks() * 1024 < ((size_t)1 << 31);
+}
+
+void launch_grouped(const Weight &w, const int8_t *q, const float *sx, int m, float *y,
+                    const int *bad, int variant, hipStream_t s, const float *res) {
+    if (m == 0) return;
+    switch (grouped_pick(w, m, variant)) {
+        case 1: if (grouped_pipe_launch<256, 2, 4>(w, q, sx, m, y, bad, s, res)) return; break;
+        case 3: if (grouped_pipe_launch<128, 2, 2>(w, q, sx, m, y, bad, s, res)) return; break;
+        case 4: if (grouped_pipe_launch<64, 1, 2>(w, q, sx, m, y, bad, s, res)) return; break;
+        case 5: if (grouped_pipe_launch<128, 1, 4>(w, q, sx, m, y, bad, s, res)) return; break;
+        case 6: if (grouped_pipe_launch<128, 4, 1>(w, q, sx, m, y, bad, s, res)) return; break;
         default: break;
     }
+    if (res) return;  // callers ask grouped_adds_residual first: the pipelined kernels take every such case
     dim3 grid(cdiv(w.tiles(), 4), cdiv(m, 16));
     if (w.bits == 4)
         hipLaunchKernelGGL(grouped_kernel<4>, grid, dim3(256), 0, s, w.codes, w.scales, q, sx, m, w.rows,

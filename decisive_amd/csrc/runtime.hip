@@ -875,6 +875,33 @@ int32_t ctx_hip_fail(dz_ctx *ctx, hipError_t e, const char *what) { return hip_f
 hipStream_t ctx_stream(dz_ctx *ctx) { return ctx->stream; }
 int *ctx_flag(dz_ctx *ctx) { return ctx->flag; }
 int ctx_variant(dz_ctx *ctx, const char *family) { return variant(ctx, family); }
+
+// h += the W4A8 product of x (f32 rows, quantized here to A8 codes) or of the
+// codes q with scales qs, in the product kernel's epilogue, when the
+// pipelined grouped kernel takes m rows (*fused set); otherwise nothing is
+// launched and the caller runs the product and the add.
+int32_t ctx_product_add(dz_ctx *ctx, const dz_weight *w, const float *x, const int8_t *q, const float *qs,
+                        size_t m, float *h, bool *fused) {
+    *fused = false;
+    const int v = variant(ctx, "grouped");
+    if (!dz::grouped_adds_residual(w->w, (int)m, v)) return DZ_OK;
+    const int *bad = nullptr;
+    if (x) {
+        const size_t qbytes = m * (size_t)w->w.groups * 64, sbytes = m * (size_t)w->w.groups * sizeof(float);
+        int32_t rc = ensure_work(ctx, qbytes + sbytes + 256);
+        if (rc) return rc;
+        int8_t *codes = (int8_t *)ctx->work;
+        float *scales = (float *)((uint8_t *)ctx->work + (qbytes + 255) / 256 * 256);
+        int *flag = product_flag(ctx);
+        dz::launch_act_quantize(x, (int)m, w->w.cols, 8, codes, scales, flag, ctx->stream);
+        q = codes;
+        qs = scales;
+        bad = flag;
+    }
+    dz::launch_grouped(w->w, q, qs, (int)m, h, bad, v, ctx->stream, h);
+    *fused = true;
+    return launched(ctx, "grouped linear");
+}
 void ctx_set_variant(dz_ctx *ctx, const char *family, int index) { ctx->variants[family] = index; }
 void ctx_set_tuning(dz_ctx *ctx, const std::string &json) { ctx->tuning = json; }
 std::string ctx_device_key(dz_ctx *ctx) {

@@ -155,3 +155,27 @@ def test_missing_weights_and_bad_names_are_rejected(ctx, oracle):
         ctx.pplx_create(rocm.PplxConfig(**dict(SMALL, delta_head_dim=64)))
     assert e.value.code == "INVALID_PARAMETERS"
     p.close()
+
+
+@pytest.mark.parametrize("layer,n,markers", [(1, 37, None), (1, 130, None), (3, 77, None), (3, 77, [76, 3, 40])])
+def test_residual_added_in_the_product_epilogue_gives_the_same_bits(ctx, oracle, small, layer, n, markers):
+    """The pipelined W4A8 kernels add the residual in their epilogue (out_proj,
+    o_proj and down_proj onto the hidden rows); the one-wave kernel leaves it
+    to a separate add. The grouped products are bitwise equal across variants
+    and the add is the same float add, so the layer outputs match bit for bit."""
+    torch = pytest.importorskip("torch")
+    model, p = small
+    h = np.random.default_rng(500 + n).standard_normal((n, SMALL["hidden"])).astype(np.float32)
+    out = {}
+    for v in ("wave16x16", "pipe128x128w4", "pipe64x128w2"):
+        hd = dev(h)
+        ctx.select_variant("grouped", v)
+        try:
+            p.layer(layer, hd, n, markers)
+        finally:
+            ctx.select_variant("grouped", "pipe-auto")
+        out[v] = host(ctx, hd)[:n if markers is None else len(markers)]
+    assert np.array_equal(out["wave16x16"].view(np.uint32), out["pipe128x128w4"].view(np.uint32))
+    assert np.array_equal(out["wave16x16"].view(np.uint32), out["pipe64x128w2"].view(np.uint32))
+    want = pplx_model.ref_layer(oracle, model, layer, h, markers)
+    assert close(out["pipe128x128w4"], want)
