@@ -38,9 +38,10 @@ void launch_fill_i32(int *p, int value, int count, hipStream_t s);
 // ---- products.hip --------------------------------------------------------------
 // Grouped W{4,8}A{8,4}: bit-exact AVX2 order. bad (may be null): NaN outputs.
 // With `res` (which may equal y) the product is added onto it in the kernel;
-// only for the cases grouped_adds_residual accepts.
+// only for the cases grouped_adds_residual accepts. Returns false when no
+// kernel was launched (a residual product that no pipelined kernel takes).
 bool grouped_adds_residual(const Weight &w, int m, int variant);
-void launch_grouped(const Weight &w, const int8_t *q, const float *sx, int m, float *y,
+bool launch_grouped(const Weight &w, const int8_t *q, const float *sx, int m, float *y,
                     const int *bad, int variant, hipStream_t s, const float *res = nullptr);
 // Few-row grouped products (any m; one launch, 16 rows per block row):
 //  from f32 x quantized in the kernel (m <= 16 keeps the all-NaN semantics of

@@ -1987,11 +1987,17 @@ void launch_grouped_records(const Weight &w, const uint32_t *records, int m, flo
 // one-wave-per-16x16-tile grouped_kernel, variant 0 ("auto") the first when
 // its grid covers at least half the compute units and the second otherwise.
 // All fold in the reference order, so all give the same bits.
+// The pipelined grouped kernels address a BM-row activation panel and a
+// weight tile column with 32-bit byte offsets.
+bool grouped_pipe_fits(const Weight &w, int bm) {
+    return bm > 0 && (size_t)bm * w.groups * 64 < ((size_t)1 << 31) &&
+           (size_t)8 * w.kblocks() * 1024 < ((size_t)1 << 31);
+}
+
 template <int BM, int WGM, int WGN>
 bool grouped_pipe_launch(const Weight &w, const int8_t *q, const float *sx, int m, float *y, const int *bad,
                          hipStream_t s, const float *res) {
-    if ((size_t)BM * w.groups * 64 >= ((size_t)1 << 31) || (size_t)8 * w.kblocks() * 1024 >= ((size_t)1 << 31))
-        return false;
+    if (!grouped_pipe_fits(w, BM)) return false;
     const dim3 blocks(cdiv(m, BM) * cdiv(w.rows, 128));
     if (w.bits == 4)
         hipLaunchKernelGGL((grouped_pipe_kernel<4, BM, 128, WGM, WGN>), blocks, dim3(WGM * WGN * 64), 0, s, w.codes,
@@ -2021,24 +2027,34 @@ int grouped_pick(const Weight &w, int m, int variant) {
     return 2;
 }
 
-bool grouped_adds_residual(const Weight &w, int m, int variant) {
-    const int pick = grouped_pick(w, m, variant);
-    return m > 16 && w.kind != WeightKind::Q4G32 && pick != 2 && pick >= 1 && pick <= 6 &&
-           (size_t)256 * w.groups * 64 < ((size_t)1 << 31) && (size_t)8 * w.kblocks() * 1024 < ((size_t)1 << 31);
+// Activation rows per block of a pipelined pick (0: not a pipelined kernel).
+int grouped_pipe_rows(int pick) {
+    switch (pick) {
+        case 1: return 256;
+        case 3: case 5: case 6: return 128;
+        case 4: return 64;
+        default: return 0;
+    }
 }
 
-void launch_grouped(const Weight &w, const int8_t *q, const float *sx, int m, float *y,
+// The same predicate decides here and in launch_grouped whether a pipelined
+// kernel (the only ones with the residual epilogue) takes the product.
+bool grouped_adds_residual(const Weight &w, int m, int variant) {
+    return m > 16 && w.kind != WeightKind::Q4G32 && grouped_pipe_fits(w, grouped_pipe_rows(grouped_pick(w, m, variant)));
+}
+
+bool launch_grouped(const Weight &w, const int8_t *q, const float *sx, int m, float *y,
                     const int *bad, int variant, hipStream_t s, const float *res) {
-    if (m == 0) return;
+    if (m == 0) return true;
     switch (grouped_pick(w, m, variant)) {
-        case 1: if (grouped_pipe_launch<256, 2, 4>(w, q, sx, m, y, bad, s, res)) return; break;
-        case 3: if (grouped_pipe_launch<128, 2, 2>(w, q, sx, m, y, bad, s, res)) return; break;
-        case 4: if (grouped_pipe_launch<64, 1, 2>(w, q, sx, m, y, bad, s, res)) return; break;
-        case 5: if (grouped_pipe_launch<128, 1, 4>(w, q, sx, m, y, bad, s, res)) return; break;
-        case 6: if (grouped_pipe_launch<128, 4, 1>(w, q, sx, m, y, bad, s, res)) return; break;
+        case 1: if (grouped_pipe_launch<256, 2, 4>(w, q, sx, m, y, bad, s, res)) return true; break;
+        case 3: if (grouped_pipe_launch<128, 2, 2>(w, q, sx, m, y, bad, s, res)) return true; break;
+        case 4: if (grouped_pipe_launch<64, 1, 2>(w, q, sx, m, y, bad, s, res)) return true; break;
+        case 5: if (grouped_pipe_launch<128, 1, 4>(w, q, sx, m, y, bad, s, res)) return true; break;
+        case 6: if (grouped_pipe_launch<128, 4, 1>(w, q, sx, m, y, bad, s, res)) return true; break;
         default: break;
     }
-    if (res) return;  // callers ask grouped_adds_residual first: the pipelined kernels take every such case
+    if (res) return false;  // only the pipelined kernels add a residual
     dim3 grid(cdiv(w.tiles(), 4), cdiv(m, 16));
     if (w.bits == 4)
         hipLaunchKernelGGL(grouped_kernel<4>, grid, dim3(256), 0, s, w.codes, w.scales, q, sx, m, w.rows,
@@ -2046,6 +2062,7 @@ void launch_grouped(const Weight &w, const int8_t *q, const float *sx, int m, fl
     else
         hipLaunchKernelGGL(grouped_kernel<8>, grid, dim3(256), 0, s, w.codes, w.scales, q, sx, m, w.rows,
                            w.groups, w.kblocks(), y, bad);
+    return true;
 }
 
 // Variants: 1 pipelined 256x64 blocks (8 waves), 2 128x64 blocks (4 waves),

@@ -11,6 +11,7 @@
 
 #include <map>
 #include <string>
+#include <vector>
 
 #include "../../include/decisive_rocm.h"
 #include "kernels.hpp"
@@ -28,10 +29,15 @@ struct dz_ctx {
     std::string arch;
     int cus = 0;
     int clock_khz = 0;
-    int *flag = nullptr;  // device ints: [0] validation / non-finite flag, [1..62] product flags
-    uint64_t product_calls = 0;  // products since the context began (picks the product flag slot)
+    // device ints: [0] validation / non-finite flag, [1..62] the product flag
+    // ring, [kCaptureSlot0 ..] one flag per product recorded under stream capture
+    int *flag = nullptr;
+    uint64_t product_calls = 0;  // ring products since the last stream change (picks the slot)
+    int captured_flags = 0;      // capture slots handed out so far
     void *work = nullptr; // activation quantization workspace
     size_t work_bytes = 0;
+    bool work_captured = false;        // a captured graph refers to `work`
+    std::vector<void *> retired_work;  // workspaces captured graphs may still use; freed at dz_destroy
     std::map<std::string, int> variants;
     std::string tuning;   // JSON of the last selection
 };
@@ -105,9 +111,22 @@ int variant(dz_ctx *ctx, const char *family) {
     return it == ctx->variants.end() ? 0 : it->second;
 }
 
+constexpr int kRingSlots = 62;
+constexpr int kCaptureSlot0 = 64;
+constexpr int kCaptureSlots = 4032;  // 16 KiB flag buffer
+constexpr size_t kFlagBytes = (size_t)(kCaptureSlot0 + kCaptureSlots) * sizeof(int);
+
+// True while the context stream records a graph (hipStreamBeginCapture).
+bool capturing(dz_ctx *ctx) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(ctx->stream, &st) == hipSuccess && st != hipStreamCaptureStatusNone;
+}
+
 // Resets the flag, then returns its value after running `enqueue` and syncing.
+// Synchronous calls cannot be recorded into a graph.
 template <class F>
 int32_t flagged_sync(dz_ctx *ctx, F enqueue, int *value) {
+    if (capturing(ctx)) return fail(ctx, DZ_INVALID_REQUEST, "synchronous call during stream capture");
     dz::launch_fill_i32(ctx->flag, 0, 1, ctx->stream);
     enqueue();
     hipError_t e = hipGetLastError();
@@ -118,24 +137,52 @@ int32_t flagged_sync(dz_ctx *ctx, F enqueue, int *value) {
     return DZ_OK;
 }
 
-// The non-finite-activation flag of one asynchronous product: slot
-// 1 + (call % 62) of the flag buffer, so that a call never reads a flag that
-// an earlier call set. The 62 slots are cleared together, by one launch that
-// the stream orders after every earlier product, each time the ring starts
-// over (instead of one clearing launch per product).
-int *product_flag(dz_ctx *ctx) {
-    const int slot = (int)(ctx->product_calls++ % 62);
-    if (slot == 0) dz::launch_fill_i32(ctx->flag + 1, 0, 62, ctx->stream);
-    return ctx->flag + 1 + slot;
+// The non-finite-activation flag of one asynchronous product.
+//  - Eager calls take slot 1 + (call % 62) of the flag buffer, so a call never
+//    reads a flag an earlier call set. The 62 slots are cleared together, by
+//    one launch the stream orders after every earlier product, each time the
+//    ring starts over (instead of one clearing launch per product).
+//  - A call recorded under stream capture takes a slot of its own, which no
+//    other call uses, and clears it with a fill kernel recorded just before the
+//    product, so every replay starts from a clear flag. Replays of one graph
+//    must not overlap each other.
+int32_t product_flag(dz_ctx *ctx, int **out) {
+    if (capturing(ctx)) {
+        if (ctx->captured_flags >= kCaptureSlots)
+            return fail(ctx, DZ_RESOURCE_LIMIT, "too many products recorded under stream capture on this context");
+        int *slot = ctx->flag + kCaptureSlot0 + ctx->captured_flags++;
+        dz::launch_fill_i32(slot, 0, 1, ctx->stream);
+        *out = slot;
+        return DZ_OK;
+    }
+    const int slot = (int)(ctx->product_calls++ % kRingSlots);
+    if (slot == 0) dz::launch_fill_i32(ctx->flag + 1, 0, kRingSlots, ctx->stream);
+    *out = ctx->flag + 1 + slot;
+    return DZ_OK;
 }
 
+// Makes the context workspace at least `bytes` long. Growing it waits for the
+// context stream; a workspace that a captured graph refers to is kept alive
+// (until dz_destroy) instead of being freed. Under capture the workspace cannot
+// grow: the caller runs the same call once before capturing it.
 int32_t ensure_work(dz_ctx *ctx, size_t bytes) {
-    if (ctx->work_bytes >= bytes) return DZ_OK;
+    const bool cap = capturing(ctx);
+    if (ctx->work_bytes >= bytes) {
+        if (cap) ctx->work_captured = true;
+        return DZ_OK;
+    }
+    if (cap)
+        return fail(ctx, DZ_INVALID_REQUEST,
+                    "the workspace cannot grow during stream capture: run the call once before capturing it");
     if (ctx->work) {
         DZ_HIP(ctx, hipStreamSynchronize(ctx->stream), "stream synchronize");
-        hipFree(ctx->work);
+        if (ctx->work_captured)
+            ctx->retired_work.push_back(ctx->work);
+        else
+            hipFree(ctx->work);
         ctx->work = nullptr;
         ctx->work_bytes = 0;
+        ctx->work_captured = false;
     }
     size_t want = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
     DZ_HIP(ctx, hipMalloc(&ctx->work, want), "workspace allocation");
@@ -260,7 +307,7 @@ int32_t dz_init(int32_t device, dz_ctx **out) {
     ctx->cus = prop.multiProcessorCount;
     ctx->clock_khz = prop.clockRate;
     if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&ctx->own, hipStreamNonBlocking) != hipSuccess ||
-        hipMalloc(&ctx->flag, 256) != hipSuccess) {
+        hipMalloc(&ctx->flag, kFlagBytes) != hipSuccess || hipMemset(ctx->flag, 0, kFlagBytes) != hipSuccess) {
         delete ctx;
         return DZ_GPU_UNAVAILABLE;
     }
@@ -274,6 +321,7 @@ void dz_destroy(dz_ctx *ctx) {
     hipSetDevice(ctx->device);
     hipStreamSynchronize(ctx->stream);
     if (ctx->work) hipFree(ctx->work);
+    for (void *p : ctx->retired_work) hipFree(p);
     if (ctx->flag) hipFree(ctx->flag);
     if (ctx->own) hipStreamDestroy(ctx->own);
     delete ctx;
@@ -283,7 +331,14 @@ const char *dz_last_error(const dz_ctx *ctx) { return ctx ? ctx->error.c_str() :
 
 int32_t dz_set_stream(dz_ctx *ctx, void *hip_stream) {
     DZ_BEGIN(ctx);
-    ctx->stream = hip_stream ? (hipStream_t)hip_stream : ctx->own;
+    hipStream_t next = hip_stream ? (hipStream_t)hip_stream : ctx->own;
+    if (next == ctx->stream) return DZ_OK;
+    // The workspace and the product flag ring are shared by every call on the
+    // context: work still queued on the old stream must finish before calls on
+    // the new one may reuse them.
+    if (capturing(ctx)) return fail(ctx, DZ_INVALID_REQUEST, "stream change while the stream records a graph");
+    DZ_HIP(ctx, hipStreamSynchronize(ctx->stream), "stream synchronize");
+    ctx->stream = next;
     ctx->product_calls = 0;
     return DZ_OK;
 }
@@ -489,7 +544,9 @@ int32_t grouped_linear(dz_ctx *ctx, const dz_weight *a, const dz_weight *b, cons
     if (rc) return rc;
     int8_t *q = (int8_t *)ctx->work;
     float *s = (float *)((uint8_t *)ctx->work + (qbytes + 255) / 256 * 256);
-    int *bad = product_flag(ctx);
+    int *bad = nullptr;
+    rc = product_flag(ctx, &bad);
+    if (rc) return rc;
     dz::launch_act_quantize(x, (int)m, w.cols, abits, q, s, bad, ctx->stream);
     dz::launch_grouped(w, q, s, (int)m, ya, bad, variant(ctx, "grouped"), ctx->stream);
     if (b) dz::launch_grouped(b->w, q, s, (int)m, yb, bad, variant(ctx, "grouped"), ctx->stream);
@@ -505,7 +562,6 @@ int32_t dz_linear(dz_ctx *ctx, const dz_weight *w, const void *x, int32_t x_dtyp
     if (m > (1u << 24)) return fail(ctx, DZ_INPUT_TOO_LONG, "input budget exceeded");
     if (mode == DZ_W4A8 || mode == DZ_W4A4) {
         if (x_dtype != DZ_F32) return fail(ctx, DZ_INVALID_PARAMETERS, "grouped int8 mode takes f32 activations");
-        if (mode == DZ_W4A4 && w->w.bits != 4) return fail(ctx, DZ_INVALID_PARAMETERS, "W4A4 needs a Q4 weight");
         return grouped_linear(ctx, w, nullptr, (const float *)x, m, y, nullptr, mode);
     }
     if (mode == DZ_W4A16) {
@@ -572,7 +628,9 @@ int32_t dz_mlp_requant(dz_ctx *ctx, const dz_weight *gate, const dz_weight *up, 
     if (rc) return rc;
     int8_t *q = (int8_t *)ctx->work;
     float *s = (float *)((uint8_t *)ctx->work + (qbytes + 255) / 256 * 256);
-    int *bad = product_flag(ctx);
+    int *bad = nullptr;
+    rc = product_flag(ctx, &bad);
+    if (rc) return rc;
     dz::launch_act_quantize(x, (int)m, g.cols, 8, q, s, bad, ctx->stream);
     dz::launch_mlp_requant(g, u, q, s, (int)m, qo, so, bad, variant(ctx, "mlp"), ctx->stream);
     return launched(ctx, "fused MLP");
@@ -892,13 +950,16 @@ int32_t ctx_product_add(dz_ctx *ctx, const dz_weight *w, const float *x, const i
         if (rc) return rc;
         int8_t *codes = (int8_t *)ctx->work;
         float *scales = (float *)((uint8_t *)ctx->work + (qbytes + 255) / 256 * 256);
-        int *flag = product_flag(ctx);
+        int *flag = nullptr;
+        rc = product_flag(ctx, &flag);
+        if (rc) return rc;
         dz::launch_act_quantize(x, (int)m, w->w.cols, 8, codes, scales, flag, ctx->stream);
         q = codes;
         qs = scales;
         bad = flag;
     }
-    dz::launch_grouped(w->w, q, qs, (int)m, h, bad, v, ctx->stream, h);
+    if (!dz::launch_grouped(w->w, q, qs, (int)m, h, bad, v, ctx->stream, h))
+        return fail(ctx, DZ_INFERENCE_FAILED, "residual product: no pipelined kernel takes the shape");
     *fused = true;
     return launched(ctx, "grouped linear");
 }

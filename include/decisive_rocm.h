@@ -17,6 +17,15 @@
  *    and is asynchronous unless stated; dz_sync waits for it.
  *  - A context is not thread-safe; the caller serialises calls, as the
  *    reference's `Backend::predict(&mut self, ..)` does.
+ *  - Stream capture (HIP graphs): the asynchronous products may be recorded.
+ *    Products that quantize their activations (dz_linear and dz_linear_pair
+ *    in a grouped mode with m > 16, dz_mlp_requant) use the context workspace
+ *    and a non-finite flag of their own, which the recorded graph clears on
+ *    every replay; run such a call once before capturing it (the workspace
+ *    cannot grow under capture: DZ_INVALID_REQUEST), and replay the graph on
+ *    the context stream or ordered with it, one replay at a time. A workspace
+ *    that a graph refers to lives until dz_destroy. Synchronous entry points
+ *    return DZ_INVALID_REQUEST under capture.
  */
 #ifndef DECISIVE_ROCM_H
 #define DECISIVE_ROCM_H
@@ -69,7 +78,8 @@ typedef enum dz_mode {
      * acc = fma(f32(dot), sw*sx, acc) (int8.rs:524-585). Bit-exact with the
      * reference CPU path. x is f32. W8A8 when the weight is Q8. */
     DZ_W4A8 = 0,
-    /* As DZ_W4A8 with 4-bit activation codes (int8.rs:59-69 Precision bits). */
+    /* As DZ_W4A8 with 4-bit activation codes (int8.rs:59-69 Precision bits);
+     * W8A4 when the weight is Q8 (int8.rs:61-64 takes any of the four pairs). */
     DZ_W4A4 = 1,
     /* f16 activations times dequantized Q4 weights, f32 accumulation. */
     DZ_W4A16 = 2
@@ -85,7 +95,10 @@ const char *dz_status_name(int32_t status);
 int32_t dz_init(int32_t device, dz_ctx **out);
 void dz_destroy(dz_ctx *ctx);
 const char *dz_last_error(const dz_ctx *ctx);
-/* Replaces the context stream (a hipStream_t); NULL restores its own. */
+/* Replaces the context stream (a hipStream_t); NULL restores its own. Waits
+ * for the work queued on the old stream first (the workspace and the product
+ * flags are shared by the context's calls); DZ_INVALID_REQUEST while the
+ * current stream is capturing. */
 int32_t dz_set_stream(dz_ctx *ctx, void *hip_stream);
 int32_t dz_sync(dz_ctx *ctx);
 /* JSON description of the device and the selected kernel variants. */

@@ -92,7 +92,7 @@ def test_records_need_whole_groups(ctx):
     assert e.value.code == "INVALID_PARAMETERS"
 
 
-@pytest.mark.parametrize("wb,ab", [(4, 8), (8, 8), (4, 4)])
+@pytest.mark.parametrize("wb,ab", [(4, 8), (8, 8), (4, 4), (8, 4)])
 @pytest.mark.parametrize("k,n", [(100, 17), (1000, 50), (4096, 64)])
 def test_every_row_count_up_to_16_matches_the_avx2_order(ctx, oracle, wb, ab, k, n):
     """M = 1..16 runs the few-row kernel (quantization inside, tails zero

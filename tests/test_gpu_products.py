@@ -40,7 +40,7 @@ def test_grouped_matches_avx2_order_bit_exact(ctx, oracle, wb, ab):
         assert bits_equal(got, want), (m, k, n, float(np.abs(got - want).max()))
 
 
-@pytest.mark.parametrize("wb,ab", [(4, 8), (8, 8), (4, 4)])
+@pytest.mark.parametrize("wb,ab", [(4, 8), (8, 8), (4, 4), (8, 4)])
 @pytest.mark.parametrize("m,k,n", [(300, 4096, 520), (257, 1088, 200), (513, 64, 129), (40, 640, 1040)])
 def test_grouped_large_m_pipeline_bit_exact(ctx, oracle, wb, ab, m, k, n):
     """M > 16 runs the pipelined grouped kernel: bit for bit the AVX2 fold
