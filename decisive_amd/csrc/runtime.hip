@@ -10,6 +10,7 @@
 #include <string.h>
 
 #include <map>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -37,10 +38,20 @@ struct dz_ctx {
     void *work = nullptr; // activation quantization workspace
     size_t work_bytes = 0;
     bool work_captured = false;        // a captured graph refers to `work`
+    uint8_t *scratch = nullptr;        // device address of this device's `scratch` array
     std::vector<void *> retired_work;  // workspaces captured graphs may still use; freed at dz_destroy
     std::map<std::string, int> variants;
     std::string tuning;   // JSON of the last selection
 };
+
+// The workspace of dz_linear_noalloc: the A8 codes and scales of its
+// activations and its non-finite flag, in a device array that the library
+// never allocates or frees (each device holds its own copy until the process
+// ends). Host code must not use the name `scratch` as an address: dz_init
+// looks up this device's address of the array once (hipGetSymbolAddress) and
+// every kernel argument uses that address.
+constexpr size_t kScratchBytes = (size_t)16 << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
 namespace dz {
 int32_t encoder_create_random(dz_ctx *ctx, const dz_encoder_config *cfg, uint64_t seed,
@@ -231,6 +242,26 @@ int32_t readout_rows(dz_ctx *ctx, const dz::Weight &w, const float *norm, const 
     return DZ_OK;
 }
 
+// This device's address of `scratch`, looked up once per device with that
+// device current.
+hipError_t scratch_address(int device, uint8_t **out) {
+    static std::mutex mu;
+    static std::map<int, uint8_t *> addresses;
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = addresses.find(device);
+    if (it != addresses.end()) {
+        *out = it->second;
+        return hipSuccess;
+    }
+    void *p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (!p) return hipErrorInvalidSymbol;
+    addresses[device] = (uint8_t *)p;
+    *out = (uint8_t *)p;
+    return hipSuccess;
+}
+
 bool valid_dtype(int32_t d) { return d == DZ_F32 || d == DZ_F16 || d == DZ_BF16; }
 
 int32_t alloc_weight(dz_ctx *ctx, dz::WeightKind kind, size_t rows, size_t cols, dz_weight **out) {
@@ -308,6 +339,12 @@ int32_t dz_init(int32_t device, dz_ctx **out) {
     ctx->clock_khz = prop.clockRate;
     if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&ctx->own, hipStreamNonBlocking) != hipSuccess ||
         hipMalloc(&ctx->flag, kFlagBytes) != hipSuccess || hipMemset(ctx->flag, 0, kFlagBytes) != hipSuccess) {
+        delete ctx;
+        return DZ_GPU_UNAVAILABLE;
+    }
+    if (scratch_address(device, &ctx->scratch) != hipSuccess) {
+        hipStreamDestroy(ctx->own);
+        hipFree(ctx->flag);
         delete ctx;
         return DZ_GPU_UNAVAILABLE;
     }
@@ -575,6 +612,35 @@ int32_t dz_linear(dz_ctx *ctx, const dz_weight *w, const void *x, int32_t x_dtyp
         return launched(ctx, "w4a16 linear");
     }
     return fail(ctx, DZ_INVALID_PARAMETERS, "unknown mode");
+}
+
+int32_t dz_linear_noalloc(dz_ctx *ctx, const dz_weight *w, const void *x, int32_t x_dtype, size_t m, float *y,
+                          int32_t mode) {
+    DZ_BEGIN(ctx);
+    if (!w || (m && (!x || !y))) return fail(ctx, DZ_INVALID_REQUEST, "null pointer");
+    if (m > (1u << 24)) return fail(ctx, DZ_INPUT_TOO_LONG, "input budget exceeded");
+    if (mode == DZ_W4A16 || m <= 16) return dz_linear(ctx, w, x, x_dtype, m, y, mode);  // no workspace on these paths
+    if (mode != DZ_W4A8 && mode != DZ_W4A4) return fail(ctx, DZ_INVALID_PARAMETERS, "unknown mode");
+    if (x_dtype != DZ_F32) return fail(ctx, DZ_INVALID_PARAMETERS, "grouped int8 mode takes f32 activations");
+    const dz::Weight &wt = w->w;
+    if (wt.kind == dz::WeightKind::Q4G32)
+        return fail(ctx, DZ_INVALID_PARAMETERS, "grouped int8 mode needs a group-64 weight");
+    // [0, 256) the flag, then the codes, then the scales (256-byte aligned)
+    const size_t qbytes = m * (size_t)wt.groups * 64, sbytes = m * (size_t)wt.groups * sizeof(float);
+    const size_t need = 256 + (qbytes + 255) / 256 * 256 + sbytes;
+    if (need > kScratchBytes)
+        return fail(ctx, DZ_RESOURCE_LIMIT,
+                    "dz_linear_noalloc: " + std::to_string(m) + " rows of " + std::to_string(wt.cols) +
+                        " need " + std::to_string(need) + " bytes of its " + std::to_string(kScratchBytes) +
+                        "-byte scratch");
+    int *bad = (int *)ctx->scratch;
+    int8_t *q = (int8_t *)(ctx->scratch + 256);
+    float *sx = (float *)(ctx->scratch + 256 + (qbytes + 255) / 256 * 256);
+    const int abits = mode == DZ_W4A4 ? 4 : 8;
+    dz::launch_fill_i32(bad, 0, 1, ctx->stream);  // a kernel, not a memset: graph replays clear it too
+    dz::launch_act_quantize((const float *)x, (int)m, wt.cols, abits, q, sx, bad, ctx->stream);
+    dz::launch_grouped(wt, q, sx, (int)m, y, bad, variant(ctx, "grouped"), ctx->stream);
+    return launched(ctx, "grouped linear (no allocation)");
 }
 
 int32_t dz_linear_f16(dz_ctx *ctx, const dz_weight *w, const void *x, size_t m, void *y, int32_t epilogue,

@@ -78,6 +78,7 @@ _SIGNATURES = {
     "dz_dequant_rows": (I32, [P, P, P, SZ, P, I32]),
     "dz_act_quantize": (I32, [P, P, SZ, SZ, I32, P, P]),
     "dz_linear": (I32, [P, P, P, I32, SZ, P, I32]),
+    "dz_linear_noalloc": (I32, [P, P, P, I32, SZ, P, I32]),
     "dz_linear_pair": (I32, [P, P, P, P, SZ, P, P, I32]),
     "dz_linear_f16": (I32, [P, P, P, SZ, P, I32, P]),
     "dz_mlp_requant": (I32, [P, P, P, P, SZ, P, P]),
@@ -255,6 +256,9 @@ class Context:
 
     def linear(self, w: Weight, x, x_dtype: int, m: int, y, mode: int):
         self._check(load().dz_linear(self.handle, w.handle, _addr(x), x_dtype, m, _addr(y), mode))
+
+    def linear_noalloc(self, w: Weight, x, x_dtype: int, m: int, y, mode: int):
+        self._check(load().dz_linear_noalloc(self.handle, w.handle, _addr(x), x_dtype, m, _addr(y), mode))
 
     def linear_f16(self, w: Weight, x, m: int, y, epilogue: int = 0, residual=None):
         self._check(load().dz_linear_f16(self.handle, w.handle, _addr(x), m, _addr(y), epilogue, _addr(residual)))

@@ -152,6 +152,18 @@ int32_t dz_act_quantize(dz_ctx *ctx, const float *x_dev, size_t m, size_t k, int
  * (x f16). y_dev f32 [m x rows(w)]. m may be 0. */
 int32_t dz_linear(dz_ctx *ctx, const dz_weight *w, const void *x_dev, int32_t x_dtype, size_t m,
                   float *y_dev, int32_t mode);
+/* No counterpart in the reference: dz_linear for callers that cannot
+ * allocate device memory (code recorded under graph capture, serving loops,
+ * harnesses that forbid hipMalloc). Same arguments, results and bits as
+ * dz_linear; it calls no allocator. The grouped modes at m > 16 keep the A8
+ * codes, scales and non-finite flag in a static 16 MiB device array (one per
+ * GPU, held until the process ends), so 256 + round256(m*G*64) + m*G*4 bytes
+ * (G = ceil(cols/64)) must fit 16 MiB: up to 3,855 rows at cols 4096, 6,168 at
+ * 2560; more is DZ_RESOURCE_LIMIT with nothing launched. Every call on a GPU
+ * shares that array: calls that overlap on one GPU (other streams, other
+ * contexts, concurrent graph replays) race; serialise them. */
+int32_t dz_linear_noalloc(dz_ctx *ctx, const dz_weight *w, const void *x_dev, int32_t x_dtype, size_t m,
+                          float *y_dev, int32_t mode);
 /* int8.rs:204-227 Matrix::apply_pair: one activation quantization shared by
  * two weights with the same cols. */
 int32_t dz_linear_pair(dz_ctx *ctx, const dz_weight *a, const dz_weight *b, const float *x_dev,
