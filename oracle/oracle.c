@@ -13,6 +13,7 @@
 #include <float.h>
 #include <math.h>
 #include <pthread.h>
+#include <unistd.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -825,36 +826,73 @@ void or_rope(float *x, size_t rows, int heads, int ad, const size_t *pos, const 
         }
 }
 
+typedef struct {
+    const float *q, *k, *v;
+    size_t nq, nk;
+    int ah, akv, ad, next_head;
+    float scale;
+    float *out;
+    pthread_mutex_t mu;
+} gqa_job;
+
+// One head of or_attention_gqa: every query row against every key, in f64.
+static void gqa_head(const gqa_job *j, int h, double *p, double *acc) {
+    const int kh = h / (j->ah / j->akv), ad = j->ad, ah = j->ah, akv = j->akv;
+    for (size_t t = 0; t < j->nq; t++) {
+        const float *qr = j->q + (t * ah + h) * (size_t)ad;
+        double mx = -INFINITY;
+        for (size_t s = 0; s < j->nk; s++) {
+            const float *kr = j->k + (s * akv + kh) * (size_t)ad;
+            double d = 0.0;
+            for (int i = 0; i < ad; i++) d += (double)qr[i] * kr[i];
+            p[s] = d * j->scale;
+            if (p[s] > mx) mx = p[s];
+        }
+        double sum = 0.0;
+        for (size_t s = 0; s < j->nk; s++) {
+            p[s] = exp(p[s] - mx);
+            sum += p[s];
+        }
+        // each output sums p[s] * v[s][i] over s in key order; the key loop is
+        // outermost so that the value rows are read contiguously
+        float *o = j->out + ((size_t)h * j->nq + t) * ad;
+        for (int i = 0; i < ad; i++) acc[i] = 0.0;
+        for (size_t s = 0; s < j->nk; s++) {
+            const float *vr = j->v + (s * akv + kh) * (size_t)ad;
+            const double ps = p[s];
+            for (int i = 0; i < ad; i++) acc[i] += ps * vr[i];
+        }
+        for (int i = 0; i < ad; i++) o[i] = (float)(acc[i] / sum);
+    }
+}
+
+static void *gqa_worker(void *arg) {
+    gqa_job *j = (gqa_job *)arg;
+    double *p = (double *)malloc(j->nk * sizeof(double));
+    double *acc = (double *)malloc((size_t)j->ad * sizeof(double));
+    for (;;) {
+        pthread_mutex_lock(&j->mu);
+        const int h = j->next_head++;
+        pthread_mutex_unlock(&j->mu);
+        if (h >= j->ah) break;
+        gqa_head(j, h, p, acc);
+    }
+    free(acc);
+    free(p);
+    return NULL;
+}
+
+// Heads are independent, so they run on up to 16 threads; each head's
+// arithmetic does not depend on the thread count.
 void or_attention_gqa(const float *q, const float *k, const float *v, size_t nq, size_t nk, int ah, int akv,
                       int ad, float scale, float *out) {
-    const int group = ah / akv;
-    double *p = (double *)malloc(nk * sizeof(double));
-    for (int h = 0; h < ah; h++) {
-        const int kh = h / group;
-        for (size_t t = 0; t < nq; t++) {
-            const float *qr = q + (t * ah + h) * (size_t)ad;
-            double mx = -INFINITY;
-            for (size_t j = 0; j < nk; j++) {
-                const float *kr = k + (j * akv + kh) * (size_t)ad;
-                double d = 0.0;
-                for (int i = 0; i < ad; i++) d += (double)qr[i] * kr[i];
-                p[j] = d * scale;
-                if (p[j] > mx) mx = p[j];
-            }
-            double sum = 0.0;
-            for (size_t j = 0; j < nk; j++) {
-                p[j] = exp(p[j] - mx);
-                sum += p[j];
-            }
-            float *o = out + ((size_t)h * nq + t) * ad;
-            for (int i = 0; i < ad; i++) {
-                double acc = 0.0;
-                for (size_t j = 0; j < nk; j++) acc += p[j] * v[(j * akv + kh) * (size_t)ad + i];
-                o[i] = (float)(acc / sum);
-            }
-        }
-    }
-    free(p);
+    gqa_job job = {q, k, v, nq, nk, ah, akv, ad, 0, scale, out, PTHREAD_MUTEX_INITIALIZER};
+    long cpus = sysconf(_SC_NPROCESSORS_ONLN);
+    int threads = cpus < 1 ? 1 : (cpus > 16 ? 16 : (int)cpus);
+    if (threads > ah) threads = ah;
+    pthread_t ids[16];
+    for (int t = 0; t < threads; t++) pthread_create(&ids[t], NULL, gqa_worker, &job);
+    for (int t = 0; t < threads; t++) pthread_join(ids[t], NULL);
 }
 
 void or_attention_gate(const float *heads, size_t n, int ah, int ad, const float *z, float *out) {

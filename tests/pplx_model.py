@@ -21,15 +21,19 @@ class Model:
     quant: dict = field(default_factory=dict)    # name -> (codes, scales, rows, cols)
     vectors: dict = field(default_factory=dict)  # name -> f32 values (checkpoint order)
     embedding: np.ndarray = None                 # packed wire rows [vocab x hidden]
+    panels: dict = field(default_factory=dict)   # name -> the oracle's AVX2 panel form of quant[name]
+    bits: int = 4                                # weight code bits
 
 
 def conv_width(c):
     return 2 * c["delta_key_heads"] * LD + c["delta_heads"] * LD
 
 
-def random_model(oracle, cfg, vocab=64, seed=0, bits=4):
+def random_model(oracle, cfg, vocab=64, seed=0, bits=4, reuse=None):
+    """`reuse` maps a layer index to an earlier layer of the same kind whose
+    tensors it shares (real-size models with one layer of each kind)."""
     rng = np.random.default_rng(seed)
-    m = Model(cfg=dict(cfg))
+    m = Model(cfg=dict(cfg), bits=bits)
     d, ff, lh, ah, akv = cfg["hidden"], cfg["ff"], cfg["delta_heads"], cfg["attn_heads"], cfg["attn_kv_heads"]
     cw, lv = conv_width(cfg), lh * LD
 
@@ -47,6 +51,13 @@ def random_model(oracle, cfg, vocab=64, seed=0, bits=4):
 
     for i in range(cfg["layers"]):
         p = f"language_model.layers.{i}."
+        src = (reuse or {}).get(i)
+        if src is not None:
+            sp = f"language_model.layers.{src}."
+            for table in (m.packed, m.quant, m.vectors):
+                for name in [t for t in table if t.startswith(sp)]:
+                    table[p + name[len(sp):]] = table[name]
+            continue
         vec(p + "input_layernorm.weight", rng.standard_normal(d) * 0.1)
         vec(p + "post_attention_layernorm.weight", rng.standard_normal(d) * 0.1)
         if i % 4 == 3:
@@ -89,8 +100,18 @@ def load(ctx, rocm, model):
 # ---- the oracle forward (backbone.rs:207-250, mod.rs:149-185) ----
 
 def _apply(oracle, model, name, x):
+    """int8.rs:166-176 apply. From 16 rows of finite input the oracle's
+    threaded AVX2 panel path runs (int8.rs:229-585), which equals the scalar
+    fused order bit for bit (tests/test_oracle.py); below, the scalar one."""
     codes, scales, rows, cols = model.quant[name]
-    return oracle.matrix_apply(x, x.shape[0], codes, scales, rows, cols)
+    m = x.shape[0]
+    if m < 16 or not oracle.has_avx2() or not np.isfinite(x).all():
+        return oracle.matrix_apply(x, m, codes, scales, rows, cols)
+    if name not in model.panels:
+        model.panels[name] = oracle.panel_pack(codes, scales, rows, cols, model.bits)
+    data, ps = model.panels[name]
+    qx, sx = oracle.act_quantize(x, m, cols, 8)
+    return oracle.panel_apply_avx2(data, ps, rows, cols, model.bits, qx, sx, m, oracle.nprocs_env_default())
 
 
 def _head_norm(oracle, x, heads, w):

@@ -10,6 +10,8 @@ from decisive_amd import rocm
 from tests.gpu_util import bits_equal, cosine, dev, empty, host
 
 pytestmark = pytest.mark.gpu
+MAX_ABS = 1e-2  # north_star tolerance for f16/f32 GEMM and layer outputs
+MIN_COS = 0.9999
 
 
 def test_layernorm_gelu_rms_softmax_mean(ctx, oracle):
@@ -122,7 +124,7 @@ def test_attention_rejects_sequences_past_32bit_offsets(ctx):
     assert e.value.code == "INPUT_TOO_LONG"
 
 
-def _encoder_reference(ctx, enc, cfg, ids, batch, seq):
+def _encoder_reference(ctx, enc, cfg, ids, batch, seq, hidden=False):
     """float32 composition of the dequantized encoder weights, rounding to f16
     where the GPU stores activations."""
     torch = pytest.importorskip("torch")
@@ -148,9 +150,19 @@ def _encoder_reference(ctx, enc, cfg, ids, batch, seq):
         att = f16(att)
         h = f16(ctx_ln(f16(att @ wo.T + h), ones, zeros, cfg.ln_eps))
         ff = h @ w1.T
-        ff = f16(0.5 * ff * (1 + np.vectorize(math.erf)(ff / math.sqrt(2))))
+        ff = f16(0.5 * ff * (1 + _erf(ff / math.sqrt(2))))
         h = f16(ctx_ln(f16(ff @ w2.T + h), ones, zeros, cfg.ln_eps))
-    return h.reshape(batch, seq, d).mean(1)
+    pooled = h.reshape(batch, seq, d).mean(1)
+    return (pooled, h) if hidden else pooled
+
+
+def _erf(x):
+    """erf in float64 (scipy's vectorized routine, else math.erf per element)."""
+    try:
+        from scipy.special import erf
+        return erf(np.asarray(x, np.float64))
+    except ImportError:
+        return np.vectorize(math.erf)(np.asarray(x, np.float64))
 
 
 def ctx_ln(x, w, b, eps):
@@ -217,6 +229,33 @@ def test_encoder_bits_do_not_depend_on_the_gemm_variant(ctx):
     for name, o in outs[1:]:
         assert bits_equal(o, outs[0][1]), name
     enc.close()
+
+
+def test_config3_width_encoder_matches_composition(ctx, oracle):
+    """Config 3's layer shape (hidden 1024, 16 heads of 64, FFN 4096, vocab
+    32000) at 2 layers over two 1024-token sequences: the kernels that run at
+    full size (wave-per-row LayerNorm at 1024, 16-head attention over 1024
+    keys, the 256x256 and 128x256 pipelined GEMM tiles with their GELU and
+    residual epilogues) against the float32 composition, to the north-star
+    tolerance on the pooled embeddings and on the last layer's hidden rows."""
+    torch = pytest.importorskip("torch")
+    cfg = rocm.EncoderConfig(layers=2, hidden=1024, heads=16, head_dim=64, ffn=4096, vocab=32000, ln_eps=1e-5)
+    enc = ctx.encoder_random(cfg, 1)
+    batch, seq = 2, 1024
+    ids = np.random.default_rng(1).integers(0, cfg.vocab, batch * seq).astype(np.int32)
+    out = empty((batch, cfg.hidden), torch.float32)
+    enc.forward(dev(ids), batch, seq, out)
+    got = host(ctx, out)
+    hidden = empty((seq, cfg.hidden), torch.float32)
+    enc.hidden_rows(enc.read_rows(ids[:seq]), seq, hidden)
+    got_h = host(ctx, hidden)
+    want, want_h = _encoder_reference(ctx, enc, cfg, ids, batch, seq, hidden=True)
+    enc.close()
+    assert cosine(got, want) >= MIN_COS and np.abs(got - want).max() <= MAX_ABS, (
+        cosine(got, want), float(np.abs(got - want).max()))
+    want_h = want_h[:seq]
+    assert cosine(got_h, want_h) >= MIN_COS and np.abs(got_h - want_h).max() <= MAX_ABS, (
+        cosine(got_h, want_h), float(np.abs(got_h - want_h).max()), float(np.abs(want_h).max()))
 
 
 def test_config3_encoder_full_size_runs_finite_and_deterministic(ctx):

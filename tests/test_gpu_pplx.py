@@ -157,7 +157,11 @@ def test_missing_weights_and_bad_names_are_rejected(ctx, oracle):
     p.close()
 
 
-@pytest.mark.parametrize("layer,n,markers", [(1, 37, None), (1, 130, None), (3, 77, None), (3, 77, [76, 3, 40])])
+MANY = [int(t) for t in np.random.default_rng(40).permutation(130)[:40]]  # more than 16 rows after pruning
+
+
+@pytest.mark.parametrize("layer,n,markers", [(1, 37, None), (1, 130, None), (3, 77, None), (3, 77, [76, 3, 40]),
+                                             (3, 130, MANY)])
 def test_residual_added_in_the_product_epilogue_gives_the_same_bits(ctx, oracle, small, layer, n, markers):
     """The pipelined W4A8 kernels add the residual in their epilogue (out_proj,
     o_proj and down_proj onto the hidden rows); the one-wave kernel leaves it
