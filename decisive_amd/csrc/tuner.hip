@@ -2,15 +2,27 @@
 //
 // Semantics of the reference's WebGPU tuner (src/models/pplx_flash/webgpu/
 // checkpoint.rs): candidates of a kernel family are timed in three rounds with
-// a rotating order; after the first round only the three fastest and the
-// family's reference variant keep running, and no round starts past the
-// deadline (:428-475). The fastest candidate that is at least 1% faster than
-// the reference (MARGIN 0.99, :41) and whose output is bitwise equal to the
-// reference's replaces it (:480-563). Selections are cached under a key that
-// hashes the device, the tuning version and the kernel sources (:279-294); a
-// cached choice is only re-checked for equality (:498-513). Inputs are hashed
-// packed words with small positive scales (:847-852).
-#include <ctype.h>
+// a rotating order; after the first round only the fastest few (three for the
+// products, two for the fused MLP) and the family's reference variant keep
+// running, and no round starts past the deadline (:428-475). The fastest
+// candidate that is at least 1% faster than the reference (MARGIN 0.99, :41)
+// and whose output is bitwise equal to the reference's replaces it
+// (:480-652). Selections are cached under a key that hashes the device, the
+// tuning version and the kernel sources (:279-294); a cached choice is only
+// re-checked for equality (:498-513). Inputs are hashed packed words with
+// small positive scales (:847-852).
+//
+// Families, in the order they are tuned:
+//   grouped     the W4A8 grouped product (select_gemm, :480-563) at
+//               (M, N, K) = (256, 8192, 2560)
+//   mlp         the fused gate/up + SiLU + A8 requant (select_mlp, :568-652)
+//               at (128, 9216, 2560)
+//   gemv, gemm_w4a16, i8_gemm   this library's W4A16 GEMV / prefill GEMM and
+//               per-row int8 GEMM (no reference counterpart) at (1 or 256,
+//               8192, 2560)
+// The decider's delta scan is not tuned: its two scans regroup the rule's
+// arithmetic differently, so the reference's bitwise rule could only ever keep
+// the baseline (select_delta_scan, :328-421, admits bit-equal scans only).
 #include <string.h>
 
 #include <algorithm>
@@ -20,6 +32,8 @@
 #include <vector>
 
 #include "../../include/decisive_rocm.h"
+#include "../host/json.hpp"
+#include "../host/sha256.hpp"
 #include "kernels.hpp"
 
 #ifndef DZ_SOURCE_HASH
@@ -38,120 +52,261 @@ std::string ctx_device_key(dz_ctx *ctx);
 
 namespace {
 
-// ---- SHA-256 (FIPS 180-4) ---------------------------------------------------------
+using decisive::Json;
 
-struct Sha256 {
-    uint32_t h[8] = {0x6a09e667, 0xbb67ae85, 0x3c6ef372, 0xa54ff53a,
-                     0x510e527f, 0x9b05688c, 0x1f83d9ab, 0x5be0cd19};
-    uint8_t buf[64];
-    size_t len = 0;
-    uint64_t total = 0;
-    static uint32_t rotr(uint32_t x, int n) { return (x >> n) | (x << (32 - n)); }
-    void block(const uint8_t *p) {
-        static const uint32_t k[64] = {
-            0x428a2f98, 0x71374491, 0xb5c0fbcf, 0xe9b5dba5, 0x3956c25b, 0x59f111f1, 0x923f82a4, 0xab1c5ed5,
-            0xd807aa98, 0x12835b01, 0x243185be, 0x550c7dc3, 0x72be5d74, 0x80deb1fe, 0x9bdc06a7, 0xc19bf174,
-            0xe49b69c1, 0xefbe4786, 0x0fc19dc6, 0x240ca1cc, 0x2de92c6f, 0x4a7484aa, 0x5cb0a9dc, 0x76f988da,
-            0x983e5152, 0xa831c66d, 0xb00327c8, 0xbf597fc7, 0xc6e00bf3, 0xd5a79147, 0x06ca6351, 0x14292967,
-            0x27b70a85, 0x2e1b2138, 0x4d2c6dfc, 0x53380d13, 0x650a7354, 0x766a0abb, 0x81c2c92e, 0x92722c85,
-            0xa2bfe8a1, 0xa81a664b, 0xc24b8b70, 0xc76c51a3, 0xd192e819, 0xd6990624, 0xf40e3585, 0x106aa070,
-            0x19a4c116, 0x1e376c08, 0x2748774c, 0x34b0bcb5, 0x391c0cb3, 0x4ed8aa4a, 0x5b9cca4f, 0x682e6ff3,
-            0x748f82ee, 0x78a5636f, 0x84c87814, 0x8cc70208, 0x90befffa, 0xa4506ceb, 0xbef9a3f7, 0xc67178f2};
-        uint32_t w[64];
-        for (int i = 0; i < 16; i++)
-            w[i] = (uint32_t)p[4 * i] << 24 | (uint32_t)p[4 * i + 1] << 16 | (uint32_t)p[4 * i + 2] << 8 | p[4 * i + 3];
-        for (int i = 16; i < 64; i++) {
-            uint32_t s0 = rotr(w[i - 15], 7) ^ rotr(w[i - 15], 18) ^ (w[i - 15] >> 3);
-            uint32_t s1 = rotr(w[i - 2], 17) ^ rotr(w[i - 2], 19) ^ (w[i - 2] >> 10);
-            w[i] = w[i - 16] + s0 + w[i - 7] + s1;
-        }
-        uint32_t a = h[0], b = h[1], c = h[2], d = h[3], e = h[4], f = h[5], g = h[6], hh = h[7];
-        for (int i = 0; i < 64; i++) {
-            uint32_t t1 = hh + (rotr(e, 6) ^ rotr(e, 11) ^ rotr(e, 25)) + ((e & f) ^ (~e & g)) + k[i] + w[i];
-            uint32_t t2 = (rotr(a, 2) ^ rotr(a, 13) ^ rotr(a, 22)) + ((a & b) ^ (a & c) ^ (b & c));
-            hh = g; g = f; f = e; e = d + t1; d = c; c = b; b = a; a = t1 + t2;
-        }
-        h[0] += a; h[1] += b; h[2] += c; h[3] += d; h[4] += e; h[5] += f; h[6] += g; h[7] += hh;
-    }
-    void update(const void *data, size_t n) {
-        const uint8_t *p = (const uint8_t *)data;
-        total += n;
-        while (n) {
-            size_t take = std::min(n, (size_t)64 - len);
-            memcpy(buf + len, p, take);
-            len += take;
-            p += take;
-            n -= take;
-            if (len == 64) {
-                block(buf);
-                len = 0;
-            }
-        }
-    }
-    void update(const std::string &s) { update(s.data(), s.size()); }
-    std::string hex16() {
-        uint64_t bits = total * 8;
-        uint8_t pad = 0x80;
-        update(&pad, 1);
-        uint8_t zero = 0;
-        while (len != 56) update(&zero, 1);
-        uint8_t lenb[8];
-        for (int i = 0; i < 8; i++) lenb[i] = (uint8_t)(bits >> (56 - 8 * i));
-        update(lenb, 8);
-        static const char *hexd = "0123456789abcdef";
-        std::string out;
-        for (int i = 0; i < 4; i++)
-            for (int b = 3; b >= 0; b--) {
-                uint8_t v = (uint8_t)(h[i] >> (8 * b));
-                out += hexd[v >> 4];
-                out += hexd[v & 15];
-            }
-        return out;
-    }
-};
+constexpr double kMargin = 0.99;
 
 double now_ms() {
     using namespace std::chrono;
     return duration<double, std::milli>(steady_clock::now().time_since_epoch()).count();
 }
 
-// checkpoint.rs:847-852: hashed words; every `stride`-th word a small positive scale.
+// checkpoint.rs:847-852: hashed words.
 uint32_t test_hash(size_t i, size_t seed) {
     uint32_t v = (uint32_t)(i + seed) * 2654435761u;
     v = (v << 13) | (v >> 19);
     return v * 2246822519u;
 }
 
+// checkpoint.rs:850: a small positive f32 scale, 0.001 + (hash % 1000) * 1e-5.
+float test_scale(size_t i, size_t seed) { return 0.001f + (float)(test_hash(i, seed) % 1000) * 1e-5f; }
+
+enum class Kind { Grouped, Mlp, Gemv, GemmW4A16, I8Gemm };
+
 struct Family {
     const char *name;
-    int m, n, k;  // tuning shape
+    Kind kind;
+    int m, n, k;
+    int keep;  // candidates that stay after the first round (besides the reference)
 };
 
-// The string value of the first `"name": "value"` member in s (the tuner's own
-// output, possibly re-serialized with whitespace around the colon).
-std::string json_field(const std::string &s, const std::string &name) {
-    const std::string pat = "\"" + name + "\"";
-    for (size_t at = s.find(pat); at != std::string::npos; at = s.find(pat, at + 1)) {
-        size_t p = at + pat.size();
-        while (p < s.size() && isspace((unsigned char)s[p])) p++;
-        if (p >= s.size() || s[p] != ':') continue;
-        p++;
-        while (p < s.size() && isspace((unsigned char)s[p])) p++;
-        if (p >= s.size() || s[p] != '"') continue;
-        size_t end = s.find('"', p + 1);
-        return end == std::string::npos ? "" : s.substr(p + 1, end - p - 1);
+const Family kFamilies[] = {
+    {"grouped", Kind::Grouped, 256, 8192, 2560, 3},
+    {"mlp", Kind::Mlp, 128, 9216, 2560, 2},
+    {"gemv", Kind::Gemv, 1, 8192, 2560, 3},
+    {"gemm_w4a16", Kind::GemmW4A16, 256, 8192, 2560, 3},
+    {"i8_gemm", Kind::I8Gemm, 256, 8192, 2560, 3},
+};
+
+// Device buffers of one family's selection, freed when it goes out of scope.
+struct DeviceBuffers {
+    hipStream_t s;
+    std::vector<void *> ptrs;
+    hipError_t err = hipSuccess;
+    explicit DeviceBuffers(hipStream_t stream) : s(stream) {}
+    ~DeviceBuffers() {
+        hipStreamSynchronize(s);
+        for (void *p : ptrs) hipFree(p);
     }
-    return "";
+    void *alloc(size_t bytes) {
+        void *p = nullptr;
+        if (err == hipSuccess) err = hipMalloc(&p, bytes);
+        if (err != hipSuccess) return nullptr;
+        ptrs.push_back(p);
+        return p;
+    }
+    template <class T>
+    void *upload(const std::vector<T> &host) {
+        void *p = alloc(host.size() * sizeof(T));
+        if (p) err = hipMemcpyAsync(p, host.data(), host.size() * sizeof(T), hipMemcpyHostToDevice, s);
+        return p;
+    }
+};
+
+std::vector<uint32_t> hashed_words(size_t bytes, size_t seed) {
+    std::vector<uint32_t> w((bytes + 3) / 4);
+    for (size_t i = 0; i < w.size(); i++) w[i] = test_hash(i, seed);
+    return w;
+}
+
+std::vector<float> small_scales(size_t count, size_t seed) {
+    std::vector<float> v(count);
+    for (size_t i = 0; i < count; i++) v[i] = test_scale(i, seed);
+    return v;
+}
+
+// A weight of the native layout over hashed codes: Q4 g32/f16 (the W4A16
+// families) or Q4 g64/f32 (the grouped families).
+Weight test_weight(DeviceBuffers &buf, WeightKind kind, int n, int k, size_t seed) {
+    Weight w;
+    w.kind = kind;
+    w.bits = 4;
+    w.group = kind == WeightKind::Q4G32 ? 32 : 64;
+    w.rows = n;
+    w.cols = k;
+    w.groups = k / 64;
+    w.np = n;
+    w.kp = (k + 127) / 128 * 128;
+    w.code_bytes = (size_t)w.np * w.kp / 2;
+    w.scale_bytes = (size_t)w.np * (w.kp / 128) * 8;
+    w.codes = (uint8_t *)buf.upload(hashed_words(w.code_bytes, seed));
+    if (kind == WeightKind::Q4G32) {
+        std::vector<uint16_t> h(w.scale_bytes / 2);
+        for (size_t i = 0; i < h.size(); i++) h[i] = (uint16_t)(0x1400 + (test_hash(i, seed + 4) % 0xC00));  // 2^-10..2^-7
+        w.scales = (uint8_t *)buf.upload(h);
+    } else {
+        w.scales = (uint8_t *)buf.upload(small_scales(w.scale_bytes / 4, seed + 4));
+    }
+    return w;
+}
+
+// One family's inputs, candidate outputs and launch.
+struct Bench {
+    Kind kind;
+    int m, n, k;
+    hipStream_t s;
+    Weight w, w2;            // the product weight (gate and up for the MLP)
+    const void *x = nullptr;  // f16 rows (W4A16), int8 A8 codes (grouped, MLP) or int8 rows (i8)
+    const float *sx = nullptr, *sw = nullptr;
+    const int8_t *b = nullptr;
+    std::vector<std::vector<std::pair<void *, size_t>>> outs;  // per candidate: output buffers
+
+    void run(int v) {
+        auto &o = outs[v];
+        switch (kind) {
+            case Kind::Grouped:
+                launch_grouped(w, (const int8_t *)x, sx, m, (float *)o[0].first, nullptr, v, s);
+                break;
+            case Kind::Mlp:
+                launch_mlp_requant(w, w2, (const int8_t *)x, sx, m, (int8_t *)o[0].first, (float *)o[1].first,
+                                   nullptr, v, s);
+                break;
+            case Kind::Gemv:
+                launch_w4a16(w, (const half_t *)x, m, (float *)o[0].first, v, 0, s);
+                break;
+            case Kind::GemmW4A16:
+                launch_w4a16(w, (const half_t *)x, m, (float *)o[0].first, 0, v, s);
+                break;
+            case Kind::I8Gemm:
+                launch_i8_gemm((const int8_t *)x, sx, m, b, sw, n, k, o[0].first, 1, v, s);
+                break;
+        }
+    }
+
+    // Every output byte of candidate v, in order.
+    std::vector<uint8_t> read(int v) {
+        size_t total = 0;
+        for (auto &p : outs[v]) total += p.second;
+        std::vector<uint8_t> h(total);
+        size_t at = 0;
+        for (auto &p : outs[v]) {
+            hipMemcpyAsync(h.data() + at, p.first, p.second, hipMemcpyDeviceToHost, s);
+            at += p.second;
+        }
+        hipStreamSynchronize(s);
+        return h;
+    }
+};
+
+bool build_bench(DeviceBuffers &buf, const Family &f, int count, Bench *b) {
+    b->kind = f.kind;
+    b->m = f.m;
+    b->n = f.n;
+    b->k = f.k;
+    b->s = buf.s;
+    const size_t M = f.m, N = f.n, K = f.k;
+    switch (f.kind) {
+        case Kind::Grouped:
+        case Kind::Mlp:
+            b->w = test_weight(buf, WeightKind::Q4G64, f.n, f.k, 7);
+            if (f.kind == Kind::Mlp) b->w2 = test_weight(buf, WeightKind::Q4G64, f.n, f.k, 11);
+            b->x = buf.upload(hashed_words(M * K, 0));         // any int8 codes
+            b->sx = (const float *)buf.upload(small_scales(M * K / 64, 17));
+            break;
+        case Kind::Gemv:
+        case Kind::GemmW4A16: {
+            b->w = test_weight(buf, WeightKind::Q4G32, f.n, f.k, 7);
+            std::vector<uint16_t> hx(M * K);
+            for (size_t i = 0; i < hx.size(); i++) {
+                uint32_t v = test_hash(i, 0);
+                hx[i] = (uint16_t)(0x3000 + (v % 0x0800)) | (uint16_t)((v >> 16) & 0x8000);  // |x| in [2^-3, 2^-1)
+            }
+            b->x = buf.upload(hx);
+            break;
+        }
+        case Kind::I8Gemm:
+            b->x = buf.upload(hashed_words(M * K, 0));
+            b->b = (const int8_t *)buf.upload(hashed_words(N * K, 7));
+            b->sx = (const float *)buf.upload(small_scales(M, 17));
+            b->sw = (const float *)buf.upload(small_scales(N, 19));
+            break;
+    }
+    b->outs.resize(count);
+    for (int v = 0; v < count; v++) {
+        if (f.kind == Kind::Mlp) {
+            b->outs[v].push_back({buf.alloc(M * N), M * N});
+            b->outs[v].push_back({buf.alloc(M * N / 64 * 4), M * N / 64 * 4});
+        } else {
+            b->outs[v].push_back({buf.alloc(M * N * 4), M * N * 4});
+        }
+    }
+    if (buf.err == hipSuccess) buf.err = hipStreamSynchronize(buf.s);
+    return buf.err == hipSuccess;
+}
+
+// time_candidates (checkpoint.rs:428-475): the best time per run of each
+// candidate and whether it stayed for the later rounds.
+void time_candidates(Bench &b, int count, int keep, double deadline, std::vector<double> *best,
+                     std::vector<bool> *kept) {
+    for (int v = 0; v < count; v++) b.run(v);  // warm every candidate
+    hipStreamSynchronize(b.s);
+    hipEvent_t e0, e1;
+    hipEventCreate(&e0);
+    hipEventCreate(&e1);
+    auto batch = [&](int v, int reps) {
+        hipEventRecord(e0, b.s);
+        for (int r = 0; r < reps; r++) b.run(v);
+        hipEventRecord(e1, b.s);
+        hipEventSynchronize(e1);
+        float ms = 0.f;
+        hipEventElapsedTime(&ms, e0, e1);
+        return (double)ms / reps;
+    };
+    // batches of about 2 ms of GPU work (the reference's 30 ms works around
+    // Safari's whole-millisecond timer; HIP events resolve microseconds)
+    const double per_run = std::max(batch(0, 2), 1e-4);
+    const int reps = (int)std::min(64.0, std::max(2.0, std::ceil(2.0 / per_run)));
+    best->assign(count, 1e30);
+    std::vector<int> active(count);
+    for (int v = 0; v < count; v++) active[v] = v;
+    for (int round = 0; round < 3; round++) {
+        if (round == 1) {
+            std::sort(active.begin(), active.end(), [&](int a, int c) { return (*best)[a] < (*best)[c]; });
+            if ((int)active.size() > keep) active.resize(keep);
+            if (std::find(active.begin(), active.end(), 0) == active.end()) active.push_back(0);
+        }
+        if (round > 0 && now_ms() >= deadline) break;
+        for (size_t j = 0; j < active.size(); j++) {
+            const int v = active[(j + round) % active.size()];
+            (*best)[v] = std::min((*best)[v], batch(v, reps));
+        }
+    }
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    kept->assign(count, false);
+    for (int v : active) (*kept)[v] = true;
+}
+
+// The cached selection of `family` when the cache's key matches, else "".
+std::string cached_choice(const Json &cache, const std::string &key, const char *family) {
+    if (!cache.is_object() || !cache["key"].is_string() || cache["key"].as_string() != key) return "";
+    const Json &sel = cache["selected"];
+    if (!sel.is_object() || !sel[family].is_string()) return "";
+    return sel[family].as_string();
 }
 
 }  // namespace
 
 std::string tuning_key(dz_ctx *ctx) {
-    Sha256 h;
-    h.update("pplx-tuning-v1\n" + ctx_device_key(ctx) + "\n" + DZ_SOURCE_HASH + "\n");
-    for (const char *f : {"gemv", "gemm_w4a16", "i8_gemm", "grouped", "mlp", "delta_scan"})
-        for (int i = 0; i < variant_count(f); i++) h.update(std::string(f) + "/" + variant_name(f, i) + "\n");
-    return h.hex16();
+    decisive::Sha256 h;
+    const std::string head = "pplx-tuning-v1\n" + ctx_device_key(ctx) + "\n" + DZ_SOURCE_HASH + "\n";
+    h.update(head.data(), head.size());
+    for (const Family &f : kFamilies)
+        for (int i = 0; i < variant_count(f.name); i++) {
+            const std::string line = std::string(f.name) + "/" + variant_name(f.name, i) + "\n";
+            h.update(line.data(), line.size());
+        }
+    return h.hex().substr(0, 32);  // the first 16 bytes, as checkpoint.rs:293
 }
 
 int32_t tune(dz_ctx *ctx, uint32_t budget_ms, const char *cache_in, char *cache_out, size_t cap) {
@@ -159,190 +314,95 @@ int32_t tune(dz_ctx *ctx, uint32_t budget_ms, const char *cache_in, char *cache_
     const double deadline = started + budget_ms;
     hipStream_t s = ctx_stream(ctx);
     const std::string key = tuning_key(ctx);
-    const std::string cached = cache_in ? cache_in : "";
-    const bool cache_ok = !cached.empty() && json_field(cached, "key") == key;
-    const Family families[] = {{"gemv", 1, 8192, 2560}, {"gemm_w4a16", 256, 8192, 2560}, {"i8_gemm", 256, 8192, 2560}};
-
-    std::string report = "{\"key\":\"" + key + "\",\"budget_ms\":" + std::to_string(budget_ms) + ",\"families\":{";
-    std::string selected_json = "\"selected\":{";
-    bool first_family = true;
-    for (const Family &fam : families) {
+    Json cache;
+    if (cache_in && *cache_in) {
+        try {
+            cache = Json::parse(cache_in);
+        } catch (const std::exception &) {
+            cache = Json();  // an unreadable cache is ignored, as a missing one
+        }
+    }
+    Json report = Json::object(), families = Json::object(), selected = Json::object();
+    report["key"] = key;
+    report["budget_ms"] = (int64_t)budget_ms;
+    for (const Family &fam : kFamilies) {
         const int count = variant_count(fam.name);
-        const int M = fam.m, N = fam.n, K = fam.k;
-        // synthetic inputs
-        Weight w;
-        w.kind = WeightKind::Q4G32;
-        w.bits = 4; w.group = 32; w.rows = N; w.cols = K; w.groups = K / 64;
-        w.np = N; w.kp = (K + 127) / 128 * 128;
-        w.code_bytes = (size_t)w.np * w.kp / 2;
-        w.scale_bytes = (size_t)w.np * (w.kp / 128) * 8;
-        std::vector<uint32_t> hcodes(w.code_bytes / 4);
-        for (size_t i = 0; i < hcodes.size(); i++) hcodes[i] = test_hash(i, 7);
-        std::vector<uint16_t> hscales(w.scale_bytes / 2);
-        for (size_t i = 0; i < hscales.size(); i++) {
-            // small positive f16 scales 2^-10 .. 2^-7
-            hscales[i] = (uint16_t)(0x1400 + (test_hash(i, 11) % 0xC00));
-        }
-        size_t abytes = strcmp(fam.name, "i8_gemm") == 0 ? (size_t)M * K : (size_t)M * K * 2;
-        (void)0;
-        std::vector<uint16_t> hx(abytes / 2);
-        for (size_t i = 0; i < hx.size(); i++) {
-            uint32_t v = test_hash(i, 0);
-            hx[i] = (uint16_t)(0x3000 + (v % 0x0800)) | (uint16_t)((v >> 16) & 0x8000);  // |x| in [2^-3, 2^-1)
-        }
-        const bool i8 = strcmp(fam.name, "i8_gemm") == 0;
-        // int8 rows of B for the i8 family, packed Q4 codes otherwise
-        const size_t bbytes = i8 ? (size_t)N * K : w.code_bytes;
-        if (hcodes.size() * 4 < bbytes) hcodes.resize(bbytes / 4 + 1);
-        for (size_t i = 0; i < hcodes.size(); i++) hcodes[i] = test_hash(i, 7);
-        void *dcodes = nullptr, *dscales = nullptr, *dx = nullptr, *dsa = nullptr, *dsb = nullptr;
-        std::vector<void *> outs(count, nullptr);
-        hipError_t err = hipMalloc(&dcodes, bbytes);
-        if (err == hipSuccess) err = hipMalloc(&dscales, w.scale_bytes);
-        if (err == hipSuccess) err = hipMalloc(&dx, abytes);
-        if (err == hipSuccess) err = hipMalloc(&dsa, (size_t)std::max(M, N) * 4);
-        if (err == hipSuccess) err = hipMalloc(&dsb, (size_t)std::max(M, N) * 4);
-        for (int i = 0; i < count && err == hipSuccess; i++) err = hipMalloc(&outs[i], (size_t)M * N * 4);
-        if (err == hipSuccess) err = hipMemcpyAsync(dcodes, hcodes.data(), bbytes, hipMemcpyHostToDevice, s);
-        if (err == hipSuccess) err = hipMemcpyAsync(dscales, hscales.data(), w.scale_bytes, hipMemcpyHostToDevice, s);
-        if (err == hipSuccess) err = hipMemcpyAsync(dx, hx.data(), abytes, hipMemcpyHostToDevice, s);
-        if (err == hipSuccess) {
-            launch_fill_f32((float *)dsa, (size_t)std::max(M, N), 0.01f, s);
-            launch_fill_f32((float *)dsb, (size_t)std::max(M, N), 0.02f, s);
-            err = hipStreamSynchronize(s);
-        }
-        auto cleanup = [&]() {
-            hipStreamSynchronize(s);
-            for (void *p : {dcodes, dscales, dx, dsa, dsb})
-                if (p) hipFree(p);
-            for (void *p : outs)
-                if (p) hipFree(p);
-        };
-        if (err != hipSuccess) {
-            cleanup();
-            return ctx_hip_fail(ctx, err, "tuner inputs");
-        }
-        w.codes = (uint8_t *)dcodes;
-        w.scales = (uint8_t *)dscales;
-        auto run = [&](int v) {
-            if (strcmp(fam.name, "gemv") == 0)
-                launch_w4a16(w, (const half_t *)dx, M, (float *)outs[v], v, 0, s);
-            else if (strcmp(fam.name, "gemm_w4a16") == 0)
-                launch_w4a16(w, (const half_t *)dx, M, (float *)outs[v], 0, v, s);
-            else
-                launch_i8_gemm((const int8_t *)dx, (const float *)dsa, M, (const int8_t *)dcodes,
-                               (const float *)dsb, N, K, outs[v], 1, v, s);
-        };
-        auto read = [&](int v) {
-            std::vector<uint32_t> h((size_t)M * N);
-            hipMemcpyAsync(h.data(), outs[v], h.size() * 4, hipMemcpyDeviceToHost, s);
-            hipStreamSynchronize(s);
-            return h;
-        };
+        DeviceBuffers buf(s);
+        Bench bench;
+        if (!build_bench(buf, fam, count, &bench)) return ctx_hip_fail(ctx, buf.err, "tuner inputs");
         int fastest = -1;
-        std::string detail;
-        // a cached choice is only checked for equality again
-        std::string want = cache_ok ? json_field(cached.substr(cached.find("\"selected\"") == std::string::npos ? 0 : cached.find("\"selected\"")), fam.name) : "";
-        int cached_idx = want.empty() ? -1 : variant_index(fam.name, want.c_str());
+        Json detail = Json::object();
+        const std::string want = cached_choice(cache, key, fam.name);
+        const int cached_idx = want.empty() ? -1 : variant_index(fam.name, want.c_str());
         if (cached_idx >= 0) {
             bool agrees = cached_idx == 0;
             if (!agrees) {
-                run(0);
-                run(cached_idx);
-                agrees = read(0) == read(cached_idx);
+                bench.run(0);
+                bench.run(cached_idx);
+                agrees = bench.read(0) == bench.read(cached_idx);
             }
             if (agrees) {
                 fastest = cached_idx;
-                detail = "{\"cached\":true";
+                detail["cached"] = true;
             }
         }
         if (fastest < 0 && now_ms() >= deadline) {
             // TuningBudget::permits (parameters.rs:305-322): no new selection stage past the deadline
-            detail = "{\"skipped\":\"budget\"";
+            detail["skipped"] = "budget";
         } else if (fastest < 0) {
-            // warm every candidate, size timed batches to ~2 ms of GPU work
-            for (int v = 0; v < count; v++) run(v);
-            hipStreamSynchronize(s);
-            hipEvent_t e0, e1;
-            hipEventCreate(&e0);
-            hipEventCreate(&e1);
-            auto time_batch = [&](int v, int reps) {
-                hipEventRecord(e0, s);
-                for (int r = 0; r < reps; r++) run(v);
-                hipEventRecord(e1, s);
-                hipEventSynchronize(e1);
-                float ms = 0.f;
-                hipEventElapsedTime(&ms, e0, e1);
-                return (double)ms / reps;
-            };
-            double per_run = std::max(time_batch(0, 2), 1e-4);
-            int reps = (int)std::min(64.0, std::max(2.0, std::ceil(2.0 / per_run)));
-            std::vector<double> best(count, 1e30);
-            std::vector<int> active(count);
-            for (int v = 0; v < count; v++) active[v] = v;
-            for (int round = 0; round < 3; round++) {
-                if (round == 1) {
-                    std::sort(active.begin(), active.end(), [&](int a, int b) { return best[a] < best[b]; });
-                    if ((int)active.size() > 3) active.resize(3);
-                    if (std::find(active.begin(), active.end(), 0) == active.end()) active.push_back(0);
-                }
-                if (round > 0 && now_ms() >= deadline) break;
-                for (size_t jdx = 0; jdx < active.size(); jdx++) {
-                    int v = active[(jdx + round) % active.size()];
-                    best[v] = std::min(best[v], time_batch(v, reps));
-                }
-            }
-            hipEventDestroy(e0);
-            hipEventDestroy(e1);
+            std::vector<double> best;
+            std::vector<bool> kept;
+            time_candidates(bench, count, fam.keep, deadline, &best, &kept);
             std::vector<int> order;
             for (int v = 1; v < count; v++)
-                if (std::find(active.begin(), active.end(), v) != active.end() && best[v] < best[0] * 0.99)
-                    order.push_back(v);
-            std::sort(order.begin(), order.end(), [&](int a, int b) { return best[a] < best[b]; });
-            std::vector<std::string> agrees(count, "null");
-            agrees[0] = "true";
-            std::vector<uint32_t> ref;
+                if (kept[v] && best[v] < best[0] * kMargin) order.push_back(v);
+            std::sort(order.begin(), order.end(), [&](int a, int c) { return best[a] < best[c]; });
+            // only candidates fast enough to replace the reference are read back
+            Json agrees = Json::array();
+            std::vector<Json> agree(count);
+            agree[0] = true;
+            std::vector<uint8_t> ref;
             if (!order.empty()) {
-                run(0);
-                ref = read(0);
+                bench.run(0);
+                ref = bench.read(0);
             }
             for (int v : order) {
-                run(v);
-                bool eq = read(v) == ref;
-                agrees[v] = eq ? "true" : "false";
+                bench.run(v);
+                const bool eq = bench.read(v) == ref;
+                agree[v] = eq;
                 if (eq) {
                     fastest = v;
                     break;
                 }
             }
-            detail = "{\"shape\":[" + std::to_string(M) + "," + std::to_string(N) + "," + std::to_string(K) +
-                     "],\"candidates\":[";
-            for (int v = 0; v < count; v++) detail += std::string(v ? "," : "") + "\"" + variant_name(fam.name, v) + "\"";
-            detail += "],\"ms_per_run\":[";
-            for (int v = 0; v < count; v++)
-                detail += std::string(v ? "," : "") + (best[v] >= 1e29 ? std::string("null") : std::to_string(best[v]));
-            detail += "],\"kept\":[";
-            for (int v = 0; v < count; v++)
-                detail += std::string(v ? "," : "") +
-                          (std::find(active.begin(), active.end(), v) != active.end() ? "true" : "false");
-            detail += "],\"agrees\":[";
-            for (int v = 0; v < count; v++) detail += std::string(v ? "," : "") + agrees[v];
-            detail += "]";
+            Json shape = Json::array(), cands = Json::array(), ms = Json::array(), keptj = Json::array();
+            for (int d : {fam.m, fam.n, fam.k}) shape.push_back(d);
+            for (int v = 0; v < count; v++) {
+                cands.push_back(variant_name(fam.name, v));
+                ms.push_back(best[v] >= 1e29 ? Json() : Json(best[v]));
+                keptj.push_back((bool)kept[v]);
+                agrees.push_back(agree[v]);
+            }
+            detail["shape"] = shape;
+            detail["candidates"] = cands;
+            detail["ms_per_run"] = ms;
+            detail["kept"] = keptj;
+            detail["agrees"] = agrees;
         }
         if (fastest < 0) fastest = 0;
         ctx_set_variant(ctx, fam.name, fastest);
-        detail += ",\"selected\":\"" + std::string(variant_name(fam.name, fastest)) + "\"}";
-        report += std::string(first_family ? "" : ",") + "\"" + fam.name + "\":" + detail;
-        selected_json += std::string(first_family ? "" : ",") + "\"" + fam.name + "\":\"" +
-                         variant_name(fam.name, fastest) + "\"";
-        first_family = false;
-        cleanup();
+        detail["selected"] = variant_name(fam.name, fastest);
+        families[fam.name] = detail;
+        selected[fam.name] = variant_name(fam.name, fastest);
     }
-    report += "}," + selected_json + "},\"elapsed_ms\":" + std::to_string(now_ms() - started) + "}";
-    ctx_set_tuning(ctx, report);
+    report["families"] = families;
+    report["selected"] = selected;
+    report["elapsed_ms"] = now_ms() - started;
+    const std::string text = report.dump();
+    ctx_set_tuning(ctx, text);
     if (cache_out) {
-        if (cap < report.size() + 1) return ctx_fail(ctx, DZ_RESOURCE_LIMIT, "tuning cache buffer too small");
-        memcpy(cache_out, report.c_str(), report.size() + 1);
+        if (cap < text.size() + 1) return ctx_fail(ctx, DZ_RESOURCE_LIMIT, "tuning cache buffer too small");
+        memcpy(cache_out, text.c_str(), text.size() + 1);
     }
     return DZ_OK;
 }

@@ -388,10 +388,15 @@ int32_t dz_pplx_forward_rows(dz_ctx *ctx, dz_pplx *model, const void *rows_host,
 
 /* ---- kernel tuner (webgpu/checkpoint.rs:95-294, 428-652) ------------------------ */
 
-/* Times the tile variants of every tuned kernel family at the reference's
- * tuning shapes within budget_ms, keeps the fastest variant whose output is
- * bitwise equal to the family's reference variant and faster than 0.99x it.
- * cache_in (JSON from an earlier cache_out, or NULL) is reused while its key
+/* Times the tile variants of every tuned kernel family within budget_ms and
+ * keeps the fastest variant whose output is bitwise equal to the family's
+ * reference variant and faster than 0.99x it. Families, in order: "grouped"
+ * (the W4A8 product, checkpoint.rs:480-563 select_gemm at M,N,K = 256, 8192,
+ * 2560), "mlp" (the fused MLP, :568-652 select_mlp at 128, 9216, 2560), then
+ * "gemv", "gemm_w4a16" and "i8_gemm" (no reference counterpart). The delta
+ * scan is not tuned: its scans are not bit-equal, which the reference's
+ * select_delta_scan (:328-421) requires. cache_in (JSON from an earlier
+ * cache_out, or NULL; unreadable text is ignored) is reused while its key
  * still matches, re-checking equality only. The selection JSON is written to
  * cache_out (cap bytes). budget_ms == 0 keeps the reference variants. */
 int32_t dz_tune(dz_ctx *ctx, uint32_t budget_ms, const char *cache_in, char *cache_out,
@@ -410,7 +415,10 @@ int32_t dz_tune(dz_ctx *ctx, uint32_t budget_ms, const char *cache_in, char *cac
  *                 pipe128x64n2
  *   "delta_scan"  auto, recurrent, chunked64 (the decider's gated delta rule;
  *                 the two scans regroup its arithmetic differently, so they
- *                 agree to rounding, not bit for bit) */
+ *                 agree to rounding, not bit for bit; "auto" runs the
+ *                 recurrent scan below 384 tokens and the chunked one from
+ *                 there, so a decider's bits depend on its chunk length
+ *                 across that mark) */
 int32_t dz_select_variant(dz_ctx *ctx, const char *family, const char *variant);
 
 #ifdef __cplusplus
