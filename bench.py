@@ -19,6 +19,10 @@ int8 GEMM, the Q4 prefill GEMM and the encoder forward) are reported under
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-secondary] [--no-cpu]
                     [--no-graph] [--calibrate-copy] [--tune MS]
+    python bench.py --only pplx                      (the decider line alone)
+    python bench.py --only tune [--tune MS] [--tune-cache F] [--tune-out F]
+                    (the tuner's selection, then each family's reference and
+                     selected variants at the tuning shape, for rocprofv3)
 """
 from __future__ import annotations
 
@@ -385,6 +389,69 @@ def pplx_line(torch, ctx, rocm, stream, n: int = 1024, layers: int = 32) -> dict
                     "host rows in and logits out inside the timed region"}
 
 
+TUNE_SHAPES = {"grouped": (256, 8192, 2560), "mlp": (128, 9216, 2560), "gemv": (1, 8192, 2560),
+               "gemm_w4a16": (256, 8192, 2560), "i8_gemm": (256, 8192, 2560)}
+TUNE_REFERENCE = {"grouped": "pipe-auto", "mlp": "pipe-auto", "gemv": "w16", "gemm_w4a16": "pipe-auto",
+                  "i8_gemm": "256x256p2w8"}
+
+
+def tune_line(torch, ctx, rocm, stream, budget_ms: int, cache_in: str | None, cache_out: str | None,
+              reps: int = 30) -> dict:
+    """dz_tune (or a cached selection re-checked for equality), then each
+    family's reference variant and its selected variant at the tuning shape
+    on real-valued inputs, `reps` launches each, timed by HIP events: the
+    dispatches a rocprofv3 run attributes to each variant's kernel."""
+    cache = Path(cache_in).read_text() if cache_in else None
+    sel = ctx.tune(budget_ms, cache)
+    if cache_out:
+        Path(cache_out).write_text(json.dumps(sel))
+    gen = lambda seed: torch.Generator(device="cuda").manual_seed(seed)  # noqa: E731
+    out = {}
+    for fam, (m, n, k) in TUNE_SHAPES.items():
+        wf = torch.randn((n, k), generator=gen(1), device="cuda") * 0.02
+        torch.cuda.synchronize()
+        if fam in ("grouped", "mlp"):
+            w = ctx.quantize(wf, rocm.F32, n, k, 4, 64)
+            w2 = ctx.quantize(wf.flip(0).contiguous(), rocm.F32, n, k, 4, 64)
+            x = torch.randn((m, k), generator=gen(0), device="cuda")
+            q = torch.empty((m, k), dtype=torch.int8, device="cuda")
+            sx = torch.empty((m, k // 64), device="cuda")
+            ctx.act_quantize(x, m, k, 8, q, sx)
+            if fam == "grouped":
+                y = torch.empty((m, n), device="cuda")
+                fn = lambda r: ctx.linear_q8(w, q, sx, m, y)  # noqa: E731
+            else:
+                qo = torch.empty((m, n), dtype=torch.int8, device="cuda")
+                so = torch.empty((m, n // 64), device="cuda")
+                fn = lambda r: ctx.mlp_requant(w, w2, x, m, qo, so)  # noqa: E731
+        elif fam in ("gemv", "gemm_w4a16"):
+            w = ctx.quantize(wf, rocm.F32, n, k, 4, 32)
+            w2 = None
+            x = torch.randn((m, k), generator=gen(0), device="cuda").half()
+            y = torch.empty((m, n), device="cuda")
+            fn = lambda r: ctx.linear(w, x, rocm.F16, m, y, rocm.W4A16)  # noqa: E731
+        else:
+            w = w2 = None
+            a = torch.empty((m, k), dtype=torch.int8, device="cuda")
+            b = torch.empty((n, k), dtype=torch.int8, device="cuda")
+            sa, sb = torch.empty(m, device="cuda"), torch.empty(n, device="cuda")
+            ctx.i8_quantize_rows(torch.randn((m, k), generator=gen(0), device="cuda"), m, k, a, sa)
+            ctx.i8_quantize_rows(wf, n, k, b, sb)
+            y = torch.empty((m, n), device="cuda")
+            fn = lambda r: ctx.i8_gemm(a, sa, m, b, sb, n, k, y, raw=False)  # noqa: E731
+        line = {"shape": [m, n, k]}
+        for role, name in (("reference", TUNE_REFERENCE[fam]), ("selected", sel["selected"][fam])):
+            ctx.select_variant(fam, name)
+            warm(torch, fn, ms=20.0)
+            line[role] = {"variant": name, "us": round(timed_ms(torch, stream, fn, reps) * 1e3, 3)}
+        ctx.select_variant(fam, sel["selected"][fam])
+        out[fam] = line
+        for t in (w, w2):
+            if t is not None:
+                t.free()
+    return {"tuning": sel, "variants": out}
+
+
 def traffic_per_launch():
     """HBM bytes per GEMV launch from the committed rocprofv3 counter summary."""
     try:
@@ -405,7 +472,10 @@ def main():
     ap.add_argument("--calibrate-copy", action="store_true",
                     help=f"also run a {COPY_BYTES >> 20} MiB device copy (counter calibration)")
     ap.add_argument("--tune", type=int, default=0, help="tuner budget in ms (0 keeps reference variants)")
-    ap.add_argument("--only", choices=["pplx"], help="run one secondary line alone and print it (for profiling)")
+    ap.add_argument("--only", choices=["pplx", "tune"],
+                    help="run one secondary line alone and print it (for profiling)")
+    ap.add_argument("--tune-cache", help="with --only tune: a selection JSON from an earlier run to reuse")
+    ap.add_argument("--tune-out", help="with --only tune: write the selection JSON here")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -416,6 +486,14 @@ def main():
     from decisive_amd import rocm
 
     ctx = rocm.Context(0)
+    if args.only == "tune":
+        stream = torch.cuda.Stream()
+        ctx.set_stream(stream.cuda_stream)
+        with torch.cuda.stream(stream):
+            line = tune_line(torch, ctx, rocm, stream, args.tune or 2000, args.tune_cache, args.tune_out)
+        ctx.set_stream(None)
+        print(json.dumps(line), flush=True)
+        return
     if args.tune:
         ctx.tune(args.tune)
     log(f"[bench] device {ctx.info()}")
