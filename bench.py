@@ -101,43 +101,90 @@ def graph_ms(torch, stream, step, launches: int, reps: int = 20) -> float:
     return ms / launches
 
 
-def cpu_baseline(seconds: float = 10.0) -> dict:
+def host_cpu() -> dict:
+    """The host the CPU baselines run on: model, the vector extensions the
+    reference's kernels could use, and the CPUs this process may run on (its
+    affinity set, capped by a cgroup CPU quota when one is set)."""
+    model, flags = None, []
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name") and model is None:
+                model = line.split(":", 1)[1].strip()
+            if line.startswith("flags") and not flags:
+                flags = line.split(":", 1)[1].split()
+    except OSError:
+        pass
+    usable = len(os.sched_getaffinity(0))
+    quota = None
+    try:
+        q, period = open("/sys/fs/cgroup/cpu.max").read().split()
+        if q != "max":
+            quota = int(q) / int(period)
+            usable = max(1, min(usable, int(quota)))
+    except (OSError, ValueError):
+        pass
+    return {"model": model, "logical_cpus": os.cpu_count(), "usable_threads": usable, "cgroup_cpu_quota": quota,
+            "avx2": "avx2" in flags and "fma" in flags, "avx512f": "avx512f" in flags}
+
+
+def _timed_loop(body, seconds: float, least: int = 1):
+    reps, start = 0, time.perf_counter()
+    while reps < least or time.perf_counter() - start < seconds:
+        body()
+        reps += 1
+    return reps, time.perf_counter() - start
+
+
+def cpu_baseline(seconds: float = 8.0) -> dict:
     """The reference's CPU W4A8 algorithm (C restatement of int8.rs:229-585,
-    AVX2 rows<4,Q4>, threaded over 32-column tiles) on the same GEMV shape."""
+    AVX2 rows<4,Q4>, threaded over 32-column tiles like int8.rs:235-256) on
+    the same GEMV shape, on one thread and on every usable thread of the host.
+    `value` and `cores` are the all-threads figure."""
     from oracle import oracle as o
-    threads = max(1, min(16, os.cpu_count() or 1))
+    host = host_cpu()
+    threads = host["usable_threads"]
+    if not o.has_avx2():
+        return {"value": None, "unit": "GB/s", "cores": 0, "kind": "port", "sample": "AVX2 unavailable", "host": host}
     rng = np.random.default_rng(1)
     w = (rng.standard_normal((N_DIM, K_DIM)) * 0.02).astype(np.float32)
     codes, scales = o.weight_quantize(o.f32_to_bf16(w), N_DIM, K_DIM, 4)
     data, ps = o.panel_pack(codes, scales, N_DIM, K_DIM, 4)
     x = np.random.default_rng(0).standard_normal((M_ROWS, K_DIM)).astype(np.float32)
-    if not o.has_avx2():
-        return {"value": None, "unit": "GB/s", "cores": 0, "kind": "port", "sample": "AVX2 unavailable"}
-    reps, start = 0, time.perf_counter()
-    while time.perf_counter() - start < seconds:
-        qx, sx = o.act_quantize(x, M_ROWS, K_DIM, 8)
-        o.panel_apply_avx2(data, ps, N_DIM, K_DIM, 4, qx, sx, M_ROWS, threads)
-        reps += 1
-    elapsed = time.perf_counter() - start
-    gbs = reps * gemv_bytes(M_ROWS, K_DIM, N_DIM) / elapsed / 1e9
-    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{reps} W4A8 GEMVs M={M_ROWS} K=N={K_DIM} (reference CPU algorithm, C restatement, "
-                      f"AVX2, {threads} threads) in {elapsed:.1f} s, priced at the W4A16 launch's bytes; "
+
+    def leg(t):
+        def body():
+            qx, sx = o.act_quantize(x, M_ROWS, K_DIM, 8)
+            o.panel_apply_avx2(data, ps, N_DIM, K_DIM, 4, qx, sx, M_ROWS, t)
+        reps, elapsed = _timed_loop(body, seconds)
+        return reps, elapsed, reps * gemv_bytes(M_ROWS, K_DIM, N_DIM) / elapsed / 1e9
+
+    r1, e1, g1 = leg(1)
+    rn, en, gn = leg(threads)
+    return {"value": round(gn, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "single_thread": {"value": round(g1, 3), "cores": 1},
+            "host": host,
+            "sample": f"W4A8 GEMVs M={M_ROWS} K=N={K_DIM} by the reference CPU algorithm (C restatement of "
+                      f"int8.rs rows<4,Q4>, AVX2 as the reference; the host also has AVX-512: "
+                      f"{host['avx512f']}), priced at the W4A16 launch's bytes: {rn} in {en:.1f} s on {threads} "
+                      f"threads (every usable CPU of the host, {host['model']}), {r1} in {e1:.1f} s on 1 thread; "
                       f"Rust toolchain unavailable"}
 
 
-def encoder_cpu_baseline(seconds: float = 10.0) -> dict:
+def encoder_cpu_baseline(seconds: float = 8.0) -> dict:
     """Config 3's encoder layer on the host cores, for one 1024-token sequence:
     the four projections by the reference's CPU W4A8 algorithm (C restatement
     of int8.rs:229-585, AVX2 rows<4,Q4>, threaded), attention by numpy float32
     matrix products (the reference's CPU attention is an sgemm), LayerNorm and
-    GELU vectorized in numpy. Layers run until `seconds` have passed; the
-    per-layer time is scaled to the 24-layer forward."""
+    GELU vectorized in numpy. Layers run until `seconds` have passed, on one
+    thread (numpy's BLAS limited to one thread too) and on every usable
+    thread; the per-layer time is scaled to the 24-layer forward."""
     from oracle import oracle as o
     from scipy.special import erf
+    host = host_cpu()
     if not o.has_avx2():
-        return {"value": None, "unit": "embeddings/s", "cores": 0, "kind": "port", "sample": "AVX2 unavailable"}
-    threads = max(1, min(16, os.cpu_count() or 1))
+        return {"value": None, "unit": "embeddings/s", "cores": 0, "kind": "port", "sample": "AVX2 unavailable",
+                "host": host}
+    threads = host["usable_threads"]
     d, heads, hd, ff, seq, layers = 1024, 16, 64, 4096, 1024, 24
     rng = np.random.default_rng(1)
     panels = []
@@ -147,41 +194,52 @@ def encoder_cpu_baseline(seconds: float = 10.0) -> dict:
         panels.append((o.panel_pack(codes, scales, rows, cols, 4), rows, cols))
     del w
 
-    def apply(i, x):
-        (data, ps), rows, cols = panels[i]
-        qx, sx = o.act_quantize(x, x.shape[0], cols, 8)
-        return o.panel_apply_avx2(data, ps, rows, cols, 4, qx, sx, x.shape[0], threads)
-
     def layernorm(x):
         mu = x.mean(1, keepdims=True)
         c = x - mu
         return (c / np.sqrt((c * c).mean(1, keepdims=True) + 1e-5)).astype(np.float32)
 
-    def layer(h):
-        qkv = apply(0, h)
-        att = np.empty((seq, d), np.float32)
-        for a in range(heads):
-            q, k, v = (qkv[:, j * d + a * hd:j * d + (a + 1) * hd] for j in range(3))
-            sc = (q @ k.T) * np.float32(1 / 8)
-            p = np.exp(sc - sc.max(1, keepdims=True))
-            att[:, a * hd:(a + 1) * hd] = (p @ v) / p.sum(1, keepdims=True)
-        h = layernorm(apply(1, att) + h)
-        f = apply(2, h)
-        f = (0.5 * f * (1.0 + erf(f * np.float32(0.70710678)))).astype(np.float32)
-        return layernorm(apply(3, f) + h)
+    def run(t):
+        def apply(i, x):
+            (data, ps), rows, cols = panels[i]
+            qx, sx = o.act_quantize(x, x.shape[0], cols, 8)
+            return o.panel_apply_avx2(data, ps, rows, cols, 4, qx, sx, x.shape[0], t)
 
-    h = layernorm(rng.standard_normal((seq, d)).astype(np.float32))
-    done, start = 0, time.perf_counter()
-    while done < 2 or time.perf_counter() - start < seconds:
-        h = layer(h)
-        done += 1
-    elapsed = time.perf_counter() - start
-    assert np.isfinite(h).all()
-    per_sequence = elapsed / done * layers
-    return {"value": float(f"{1.0 / per_sequence:.4g}"), "unit": "embeddings/s", "cores": threads, "kind": "port",
-            "sample": f"{done} encoder layers of one 1024-token sequence in {elapsed:.1f} s, scaled to 24 layers "
-                      f"(W4A8 AVX2 products on {threads} threads, numpy f32 attention/LayerNorm/GELU; one "
-                      f"layer's weights reused); Rust toolchain unavailable"}
+        def layer(h):
+            qkv = apply(0, h)
+            att = np.empty((seq, d), np.float32)
+            for a in range(heads):
+                q, k, v = (qkv[:, j * d + a * hd:j * d + (a + 1) * hd] for j in range(3))
+                sc = (q @ k.T) * np.float32(1 / 8)
+                p = np.exp(sc - sc.max(1, keepdims=True))
+                att[:, a * hd:(a + 1) * hd] = (p @ v) / p.sum(1, keepdims=True)
+            h = layernorm(apply(1, att) + h)
+            f = apply(2, h)
+            f = (0.5 * f * (1.0 + erf(f * np.float32(0.70710678)))).astype(np.float32)
+            return layernorm(apply(3, f) + h)
+
+        state = [layernorm(np.random.default_rng(1).standard_normal((seq, d)).astype(np.float32))]
+
+        def body():
+            state[0] = layer(state[0])
+        try:
+            from threadpoolctl import threadpool_limits
+            with threadpool_limits(limits=t):
+                done, elapsed = _timed_loop(body, seconds, least=2)
+        except ImportError:
+            done, elapsed = _timed_loop(body, seconds, least=2)
+        assert np.isfinite(state[0]).all()
+        return done, elapsed, 1.0 / (elapsed / done * layers)
+
+    d1, e1, v1 = run(1)
+    dn, en, vn = run(threads)
+    return {"value": float(f"{vn:.4g}"), "unit": "embeddings/s", "cores": threads, "kind": "port",
+            "single_thread": {"value": float(f"{v1:.4g}"), "cores": 1},
+            "host": host,
+            "sample": f"encoder layers of one 1024-token sequence scaled to 24 layers: {dn} in {en:.1f} s on "
+                      f"{threads} threads ({host['model']}), {d1} in {e1:.1f} s on 1 thread (W4A8 AVX2 products "
+                      f"by the reference CPU algorithm, numpy f32 attention/LayerNorm/GELU; one layer's weights "
+                      f"reused); Rust toolchain unavailable"}
 
 
 def gemv_lines(torch, ctx, rocm, weights, stream) -> dict:
