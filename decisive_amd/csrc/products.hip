@@ -415,19 +415,27 @@ __global__ __launch_bounds__(256) void mlp_requant_kernel(
 // load latency plus whatever runs after the last bytes land. The kernel is
 // shaped so that every load of a wave is in flight at once and little work
 // follows them:
-//  - one block per 16-row tile, K split into kGemvChunks fixed chunks; a wave
-//    owns PW chunks and walks them two k-blocks at a time;
-//  - per sub-step a wave issues ONE full-width load for its activation rows
-//    and the two scale records (staged through the wave's own LDS slice), and
-//    one 16-byte code load per k-block, with no branch or select between them
-//    (out-of-range lanes read a zero page or a clamped valid block), so the
-//    three requests leave back to back;
+//  - one block per 16-row tile; K is split into kGemvChunks fixed chunks,
+//    chunk c holding the k-blocks c, c + 16, c + 32, ... (interleaved: the
+//    16 waves' first loads then cover 16 adjacent KiB of the tile, which
+//    streams faster than each wave reading adjacent k-blocks); a wave owns PW
+//    chunks and takes their k-blocks two at a time ("pairs");
+//  - a round issues every load of up to NP pairs before using any: per pair
+//    ONE full-width staging load for the activation rows and the two scale
+//    records, then one 16-byte code load per k-block, each in a straight line
+//    with no branch or select between them (out-of-range lanes read a zero page
+//    or a clamped valid block), so the compiler waits for each load just before
+//    its first use;
 //  - codes become exact f16 with 9 VALU ops per 8 codes (v_and_or with the
 //    1024 exponent, one shift per word, packed add/fma to remove the bias);
+//    the MFMAs of a pair are issued back to back and their scale FMAs after
+//    them. Every lane reads an activation row for the MFMA (row i % MPAD):
+//    rows >= MPAD only feed output rows that are never stored;
 //  - only the MFMA output rows that hold live activation rows get the scale
 //    FMA; chunk partials are summed in chunk order by wave 0.
-// Every output is  sum_c ( sum_{kb in c} sum_s fma(p_s, scale_s, .) ), chunks
-// added in order, whatever WAVES or MPAD is, so all variants are bitwise equal.
+// Every output is  sum_c ( sum_{kb in c, ascending} sum_s fma(p_s, scale_s, .) ),
+// chunks added in order, whatever WAVES, MPAD or NP is, so all variants and row
+// counts give the same bits.
 
 constexpr int kGemvChunks = 16;
 
@@ -461,11 +469,12 @@ struct GemvShape {
     static constexpr int LIVE = MPAD < 4 ? MPAD : 4;     // MFMA output rows per lane that are live
     static constexpr int XROW = 512 + 16;                // staged activation row: 256 f16 + pad
     static constexpr int SLICE = MPAD * XROW + 256;      // per wave: rows, then 2 scale records
-    static constexpr int UNITS = MPAD * 32 + 16;         // 16-byte units staged per sub-step
+    static constexpr int UNITS = MPAD * 32 + 16;         // 16-byte units staged per pair
     static constexpr int LOADS = (UNITS + 63) / 64;
+    static constexpr int NPMAX = MPAD >= 16 ? 1 : (MPAD >= 8 ? 2 : 4);  // pairs per round (staging VGPRs)
 };
 
-template <int WAVES, int MPAD, bool G32>
+template <int WAVES, int MPAD, bool G32, int NP>
 __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const uint8_t *__restrict__ codes,
                                                           const uint8_t *__restrict__ scales,
                                                           const half_t *__restrict__ x, int m,
@@ -473,71 +482,94 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const uint8_t *__restr
                                                           float *__restrict__ y) {
     using S = GemvShape<MPAD>;
     constexpr int PW = kGemvChunks / WAVES;
+    constexpr int C = kGemvChunks;
     extern __shared__ __align__(16) uint8_t lds[];
     const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
     const int t = blockIdx.x;
     const int qd = lane / 16, i = lane % 16, j = i;
     uint8_t *slice = lds + wave * S::SLICE;
     const uint8_t *cbase = codes + q4_lane(t, 0, kbs, qd, j);
-    const int per = (kbs + kGemvChunks - 1) / kGemvChunks;
+    const uint8_t *arow = slice + (i % MPAD) * S::XROW + qd * 16;
     const uint32_t magic = 0x64006400u;
     const float4_t fz = {0.f, 0.f, 0.f, 0.f};
     float part[PW][S::LIVE];
-
 #pragma unroll
     for (int cc = 0; cc < PW; cc++) {
         const int chunk = wave * PW + cc;
-        const int kb0 = chunk * per;
-        const int kb1 = min(kbs, kb0 + per);
+        const int count = chunk < kbs ? (kbs - chunk + C - 1) / C : 0;  // k-blocks of the chunk
         float acc[S::LIVE];
 #pragma unroll
         for (int v = 0; v < S::LIVE; v++) acc[v] = 0.0f;
-        uint4_t st[S::LOADS], c0, c1;
-        auto issue = [&](int kb) {
+        for (int p0 = 0; 2 * p0 < count; p0 += NP) {
+            uint4_t st[NP][S::LOADS], cw[NP][2];
+            // pair q holds k-blocks chunk + (2q)C and chunk + (2q+1)C; a k-block past K
+            // reads k-block `chunk` (valid) with zero activations and scales: it adds 0
 #pragma unroll
-            for (int L = 0; L < S::LOADS; L++) {
-                const int u = L * 64 + lane;
-                const uint8_t *p = (const uint8_t *)g_zero_unit;
-                if (u < MPAD * 32) {
-                    const int r = u / 32, kk = kb * 128 + (u % 32) * 8;
-                    if (r < m && kk < k && kb + (u % 32) / 16 < kb1) p = (const uint8_t *)(x + (size_t)r * k + kk);
-                } else if (u < S::UNITS) {
-                    const int q = u - MPAD * 32, kbq = kb + q / 8;
-                    if (kbq < kb1) p = scales + ((size_t)t * kbs + kbq) * 128 + (q % 8) * 16;
+            for (int q = 0; q < NP; q++) {
+#pragma unroll
+                for (int L = 0; L < S::LOADS; L++) {
+                    const int u = L * 64 + lane;
+                    const uint8_t *p = (const uint8_t *)g_zero_unit;
+                    if (u < MPAD * 32) {
+                        const int r = u / 32, kbu = chunk + (2 * (p0 + q) + (u % 32) / 16) * C;
+                        const int kk = kbu * 128 + (u % 16) * 8;
+                        if (r < m && kbu < kbs && kk < k) p = (const uint8_t *)(x + (size_t)r * k + kk);
+                    } else if (u < S::UNITS) {
+                        const int v = u - MPAD * 32, kbq = chunk + (2 * (p0 + q) + v / 8) * C;
+                        if (kbq < kbs) p = scales + ((size_t)t * kbs + kbq) * 128 + (v % 8) * 16;
+                    }
+                    st[q][L] = *(const uint4_t *)p;
                 }
-                st[L] = *(const uint4_t *)p;
-            }
-            // a k-block past the chunk end reads a valid block: its activations
-            // and scales are zero, so it adds exactly 0
-            c0 = __builtin_nontemporal_load((const uint4_t *)(cbase + (size_t)(kb < kb1 ? kb : kb0) * 1024));
-            c1 = __builtin_nontemporal_load((const uint4_t *)(cbase + (size_t)(kb + 1 < kb1 ? kb + 1 : kb0) * 1024));
-        };
-        if (kb0 < kb1) issue(kb0);
-        for (int kb = kb0; kb < kb1; kb += 2) {
+                __builtin_amdgcn_sched_barrier(0);  // the staging load leaves first: it is used first
 #pragma unroll
-            for (int L = 0; L < S::LOADS; L++) {
-                const int u = L * 64 + lane;
-                if (u < MPAD * 32) *(uint4_t *)(slice + (u / 32) * S::XROW + (u % 32) * 16) = st[L];
-                else if (u < S::UNITS) *(uint4_t *)(slice + MPAD * S::XROW + (u - MPAD * 32) * 16) = st[L];
-            }
-            const uint4_t cw[2] = {c0, c1};
-            if (kb + 2 < kb1) issue(kb + 2);
-#pragma unroll
-            for (int uu = 0; uu < 2; uu++) {
-                const uint2_t sc = *(const uint2_t *)(slice + MPAD * S::XROW + uu * 128 + j * 8);
-#pragma unroll
-                for (int s = 0; s < 4; s++) {
-                    half8_t a = half8_t{};
-                    if (i < MPAD) a = *(const half8_t *)(slice + i * S::XROW + (uu * 128 + s * 32 + qd * 8) * 2);
-                    const float4_t p = mfma_f16(a, as_half8(unpack_codes(cw[uu][s], magic)), fz);
-                    float scale;
-                    if (G32)
-                        scale = f16_bits_to_float((sc[s >> 1] >> (16 * (s & 1))) & 0xffffu);
-                    else
-                        scale = word_as_float(sc[s >> 1]);
-#pragma unroll
-                    for (int v = 0; v < S::LIVE; v++) acc[v] = __builtin_fmaf(p[v], scale, acc[v]);
+                for (int h = 0; h < 2; h++) {
+                    const int kb = chunk + (2 * (p0 + q) + h) * C;
+                    cw[q][h] = __builtin_nontemporal_load((const uint4_t *)(cbase + (size_t)(kb < kbs ? kb : chunk) * 1024));
                 }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+#pragma unroll
+            for (int q = 0; q < NP; q++) {
+                if (2 * (p0 + q) >= count) break;
+                // the previous pair's LDS reads completed before its MFMAs: the slice is free
+#pragma unroll
+                for (int L = 0; L < S::LOADS; L++) {
+                    const int u = L * 64 + lane;
+                    if (u < MPAD * 32) *(uint4_t *)(slice + (u / 32) * S::XROW + (u % 32) * 16) = st[q][L];
+                    else if (u < S::UNITS) *(uint4_t *)(slice + MPAD * S::XROW + (u - MPAD * 32) * 16) = st[q][L];
+                }
+                half8_t a[2][4];
+                uint2_t sc[2];
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    sc[h] = *(const uint2_t *)(slice + MPAD * S::XROW + h * 128 + j * 8);
+#pragma unroll
+                    for (int s = 0; s < 4; s++) a[h][s] = *(const half8_t *)(arow + (h * 128 + s * 32) * 2);
+                }
+                float4_t pr[2][4];
+#pragma unroll
+                for (int h = 0; h < 2; h++)
+#pragma unroll
+                    for (int s = 0; s < 4; s++) pr[h][s] = mfma_f16(a[h][s], as_half8(unpack_codes(cw[q][h][s], magic)), fz);
+                // Every register of every MFMA result stays allocated until here. Left
+                // to itself the compiler hands the registers of the unused result rows
+                // to the next unpack while the MFMA is still writing them.
+#pragma unroll
+                for (int h = 0; h < 2; h++)
+#pragma unroll
+                    for (int s = 0; s < 4; s++) asm volatile("" : "+v"(pr[h][s]));
+#pragma unroll
+                for (int h = 0; h < 2; h++)
+#pragma unroll
+                    for (int s = 0; s < 4; s++) {
+                        float scale;
+                        if (G32)
+                            scale = f16_bits_to_float((sc[h][s >> 1] >> (16 * (s & 1))) & 0xffffu);
+                        else
+                            scale = word_as_float(sc[h][s >> 1]);
+#pragma unroll
+                        for (int v = 0; v < S::LIVE; v++) acc[v] = __builtin_fmaf(pr[h][s][v], scale, acc[v]);
+                    }
             }
         }
 #pragma unroll
@@ -1760,20 +1792,32 @@ const char *const kGroupedNames[] = {"pipe-auto",    "pipe256x128w8", "wave16x16
 const char *const kMlpNames[] = {"pipe-auto", "pipe256x64w8", "pipe128x64w4", "wave16x64", "pipe256x64n2", "pipe128x64n2"};
 const char *const kDeltaNames[] = {"auto", "recurrent", "chunked64"};
 
-template <int W, int MPAD, bool G32>
-void gemv_launch_one(const Weight &w, const half_t *x, int m, float *y, hipStream_t s) {
+template <int W, int MPAD, bool G32, int NP>
+void gemv_launch_np(const Weight &w, const half_t *x, int m, float *y, hipStream_t s) {
     using S = GemvShape<MPAD>;
     const size_t lds = (size_t)W * S::SLICE;
     static bool configured[64] = {};  // the LDS limit is a per-device function attribute
     int dev = 0;
     hipGetDevice(&dev);
     if (dev >= 0 && dev < 64 && !configured[dev]) {
-        if (hipFuncSetAttribute((const void *)gemv_kernel<W, MPAD, G32>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)lds) == hipSuccess)
+        if (hipFuncSetAttribute((const void *)gemv_kernel<W, MPAD, G32, NP>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) == hipSuccess)
             configured[dev] = true;
     }
-    hipLaunchKernelGGL((gemv_kernel<W, MPAD, G32>), dim3(w.tiles()), dim3(W * 64), lds, s, w.codes, w.scales, x,
+    hipLaunchKernelGGL((gemv_kernel<W, MPAD, G32, NP>), dim3(w.tiles()), dim3(W * 64), lds, s, w.codes, w.scales, x,
                        m, w.cols, w.rows, w.kblocks(), y);
+}
+
+// NP: k-block pairs a wave keeps in flight per round, the pairs its chunks
+// need up to the staging limit (rounds repeat beyond it).
+template <int W, int MPAD, bool G32>
+void gemv_launch_one(const Weight &w, const half_t *x, int m, float *y, hipStream_t s) {
+    constexpr int NPMAX = GemvShape<MPAD>::NPMAX;
+    const int pairs = (cdiv(w.kblocks(), kGemvChunks) + 1) / 2;
+    if (pairs <= 1 || NPMAX == 1) gemv_launch_np<W, MPAD, G32, 1>(w, x, m, y, s);
+    else if (pairs <= 2 || NPMAX == 2) gemv_launch_np<W, MPAD, G32, (NPMAX < 2 ? NPMAX : 2)>(w, x, m, y, s);
+    else if (pairs <= 3) gemv_launch_np<W, MPAD, G32, (NPMAX < 3 ? NPMAX : 3)>(w, x, m, y, s);
+    else gemv_launch_np<W, MPAD, G32, NPMAX>(w, x, m, y, s);
 }
 
 template <int W, bool G32>
