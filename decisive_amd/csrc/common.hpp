@@ -104,6 +104,42 @@ __device__ __forceinline__ float f16_bits_to_float(uint32_t h) {
     return (float)__builtin_bit_cast(half_t, (unsigned short)h);
 }
 
+// Blocks are dispatched to the 8 XCDs round-robin (block b on XCD b % 8), and
+// each XCD has its own L2. A kernel that reads rows another kernel just wrote
+// reads them fastest on the XCD that wrote them. The products give XCD x the
+// output rows [x M / 8, (x + 1) M / 8) (whole row bands, xcd_tile); this maps
+// block b of nblocks to work unit u of nunits so that XCD x takes the units
+// [x nunits / 8, (x + 1) nunits / 8) in order, the same share (identity when
+// the counts do not divide by 8).
+constexpr int kXcds = 8;
+__device__ __forceinline__ int xcd_unit(int b, int nblocks) {
+    return nblocks % kXcds == 0 ? (b % kXcds) * (nblocks / kXcds) + b / kXcds : b;
+}
+
+// Sum over the 64 lanes of a wave, left in every lane: four DPP adds inside
+// each 16-lane row (xor 1, xor 2, rotate 4, rotate 8), then v_permlane16_swap
+// (odd rows of the first operand trade places with even rows of the second)
+// and v_permlane32_swap (upper half of the first with the lower half of the
+// second) add the rows in pairs. The swaps are issued as asm with nops for
+// the VALU-write / permlane-read wait states on either side.
+template <int CTRL>
+__device__ __forceinline__ float dpp_move_f32(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v += dpp_move_f32<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_move_f32<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_move_f32<0x124>(v);  // row_ror:4
+    v += dpp_move_f32<0x128>(v);  // row_ror:8
+    float a = v, b = v;
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+    v = a + b;
+    a = v;
+    b = v;
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+    return a + b;
+}
+
 // erf(x) by Abramowitz & Stegun, Handbook of Mathematical Functions (1964),
 // formula 7.1.26: erf(x) = 1 - (a1 t + a2 t^2 + a3 t^3 + a4 t^4 + a5 t^5) e^(-x^2)
 // with t = 1 / (1 + p x) for x >= 0, |error| <= 1.5e-7, odd extension for x < 0.

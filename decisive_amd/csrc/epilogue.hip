@@ -84,7 +84,9 @@ __global__ __launch_bounds__(256) void layernorm_f16_rows_kernel(const half_t *_
     constexpr int D = 512 * C;
     const int lane = threadIdx.x % 64;
     const int stride = gridDim.x * 4;
-    int row = blockIdx.x * 4 + threadIdx.x / 64;
+    // row-band order per XCD (xcd_unit): a wave normalises rows the same XCD's
+    // product blocks wrote, and writes rows the next product reads there
+    int row = xcd_unit(blockIdx.x, gridDim.x) * 4 + threadIdx.x / 64;
     if (row >= rows) return;  // whole wave
     float ww[C][8], bb[C][8];
 #pragma unroll
@@ -119,7 +121,7 @@ __global__ __launch_bounds__(256) void layernorm_f16_rows_kernel(const half_t *_
         for (int c = 0; c < C; c++)
 #pragma unroll
             for (int e = 0; e < 8; e++) s += v[c][e];
-        for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
+        s = wave_sum_dpp(s);
         const float mean = s / (float)D;
         float q = 0.0f;
 #pragma unroll
@@ -129,7 +131,7 @@ __global__ __launch_bounds__(256) void layernorm_f16_rows_kernel(const half_t *_
                 const float d0 = v[c][e] - mean;
                 q += d0 * d0;
             }
-        for (int off = 32; off > 0; off >>= 1) q += __shfl_xor(q, off);
+        q = wave_sum_dpp(q);
         const float inv = 1.0f / sqrtf(q / (float)D + eps);
         half_t *dst = y + (size_t)row * D;
 #pragma unroll
@@ -288,6 +290,47 @@ __global__ __launch_bounds__(1024) void mean_rows_kernel(const void *__restrict_
     }
 }
 
+// The f16 form with 16-byte loads: block (b, group of 128 columns); thread
+// (g, c8) sums rows g, g + 64, ... of the 8 columns 8*c8 .. 8*c8 + 7, four
+// rows in flight at a time; then the 64 partial sums of a column are added in
+// g order (a fixed order).
+__global__ __launch_bounds__(1024) void mean_rows_f16_kernel(const half_t *__restrict__ x, int rows, int d,
+                                                             float *__restrict__ out) {
+    __shared__ float part[64][129];
+    const int c8 = threadIdx.x % 16, g = threadIdx.x / 16;
+    // (column group, sequence) units, a contiguous share per XCD (xcd_unit)
+    const int groups = (d + 127) / 128, unit = xcd_unit(blockIdx.x, gridDim.x);
+    const int cg = unit % groups, b = unit / groups;
+    const int col = cg * 128 + c8 * 8;
+    float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (col < d) {
+        const half_t *base = x + (size_t)b * rows * d + col;
+        int r = g;
+        for (; r + 192 < rows; r += 256) {
+            half8_t v[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) v[u] = *(const half8_t *)(base + (size_t)(r + 64 * u) * d);
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) s[e] += (float)v[u][e];
+        }
+        for (; r < rows; r += 64) {
+            const half8_t v = *(const half8_t *)(base + (size_t)r * d);
+#pragma unroll
+            for (int e = 0; e < 8; e++) s[e] += (float)v[e];
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; e++) part[g][c8 * 8 + e] = s[e];
+    __syncthreads();
+    if (threadIdx.x < 128 && cg * 128 + (int)threadIdx.x < d) {
+        float t = 0.0f;
+        for (int i = 0; i < 64; i++) t += part[i][threadIdx.x];
+        out[(size_t)b * d + cg * 128 + threadIdx.x] = t / (float)rows;
+    }
+}
+
 // ---- flash attention, head_dim 64 ----------------------------------------------------
 //
 // Block = 8 waves x 32 queries of one (batch, head); keys in steps of 64,
@@ -319,7 +362,12 @@ __global__ __launch_bounds__(kAttnWaves * 64, 4) void attention_kernel(const hal
     __shared__ __align__(16) uint8_t vs[2 * kAttnKeys * 128];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), lane = threadIdx.x % 64;
     const int q4 = lane / 16, j = lane % 16;
-    const int h = blockIdx.y, b = blockIdx.z;
+    // blocks in (query block, head, batch) order, a contiguous share per XCD
+    // (xcd_unit): the 8 sequences of 1024 tokens of configuration 3 each run on
+    // the XCD whose product blocks wrote their qkv rows
+    const int qblocks = (seq + kAttnQueries - 1) / kAttnQueries;
+    const int unit = xcd_unit(blockIdx.x, gridDim.x);
+    const int qblk = unit % qblocks, h = (unit / qblocks) % heads, b = unit / (qblocks * heads);
     const int width = heads * 64;
     const size_t ld3 = (size_t)3 * width;  // halves per token row of qkv
     const half_t *base = qkv + (size_t)b * seq * ld3;
@@ -327,7 +375,7 @@ __global__ __launch_bounds__(kAttnWaves * 64, 4) void attention_kernel(const hal
     const uint32_t ks_lds = lds_address(ks), vs_lds = lds_address(vs);
 
     // Q^T fragments: lane (q4, j) holds Q[query j][dh 32ds + 8q4 + e]
-    const int q0 = blockIdx.x * kAttnQueries + wave * (kAttnQB * 16);
+    const int q0 = qblk * kAttnQueries + wave * (kAttnQB * 16);
     half8_t qf[kAttnQB][2];
 #pragma unroll
     for (int qb = 0; qb < kAttnQB; qb++) {
@@ -510,8 +558,13 @@ void launch_layernorm(const void *x, void *y, int dtype, int rows, int d, const 
     const bool fast = dtype == 1 && (d == 512 || d == 1024 || d == 2048) &&
                       (((uintptr_t)x | (uintptr_t)y | (uintptr_t)w | (uintptr_t)b) & 15) == 0;
     if (fast) {
-        // one row per wave (4-wave blocks): every row's load is in flight at once
-        const dim3 grid(cdiv(rows, 4));
+        // 4-wave blocks, two per compute unit (or fewer when rows are few): a
+        // wave keeps the gains and biases in registers over its rows and has the
+        // next row's load in flight while it normalises the current one
+        // one wave per row at a time, the block count rounded to a multiple of
+        // the XCD count; past 2 blocks per compute unit waves walk several rows
+        const unsigned want = std::min((unsigned)cdiv(rows, 4), (unsigned)(8 * device_cus()));
+        const dim3 grid(want >= 64 ? (want + 7) / 8 * 8 : want);
         const half_t *xh = (const half_t *)x;
         half_t *yh = (half_t *)y;
         if (d == 512) hipLaunchKernelGGL(layernorm_f16_rows_kernel<1>, grid, dim3(256), 0, s, xh, yh, rows, w, b, eps);
@@ -558,13 +611,19 @@ void launch_softmax_rows(float *x, int rows, int n, hipStream_t s) {
 }
 void launch_mean_rows(const void *x, int dtype, int batch, int rows, int d, float *out,
                       hipStream_t s) {
-    if (batch && d) hipLaunchKernelGGL(mean_rows_kernel, dim3(cdiv(d, 64), batch), dim3(1024), 0, s, x, dtype, batch, rows, d, out);
+    if (!batch || !d) return;
+    if (dtype == 1 && d % 8 == 0 && ((uintptr_t)x & 15) == 0) {
+        hipLaunchKernelGGL(mean_rows_f16_kernel, dim3(cdiv(d, 128) * batch), dim3(1024), 0, s, (const half_t *)x, rows,
+                           d, out);
+        return;
+    }
+    hipLaunchKernelGGL(mean_rows_kernel, dim3(cdiv(d, 64), batch), dim3(1024), 0, s, x, dtype, batch, rows, d, out);
 }
 void launch_attention(const half_t *qkv, half_t *out, int batch, int seq, int heads, int dh,
                       float scale, hipStream_t s) {
     (void)dh;
     if (!batch || !seq) return;
-    dim3 grid(cdiv(seq, kAttnQueries), heads, batch);
+    const dim3 grid(cdiv(seq, kAttnQueries) * heads * batch);
     hipLaunchKernelGGL(attention_kernel, grid, dim3(kAttnWaves * 64), 0, s, qkv, out, seq, heads,
                        scale * 1.4426950408889634f);
 }

@@ -98,6 +98,9 @@ void launch_attention(const half_t *qkv, half_t *out, int batch, int seq, int he
 void launch_fill_normal_f32(float *p, size_t n, uint64_t seed, float stddev, hipStream_t s);
 void launch_fill_f32(float *p, size_t n, float v, hipStream_t s);
 
+// Compute units of the current device (cached per device).
+int device_cus();
+
 // ---- variants (tuner) --------------------------------------------------------------
 struct VariantFamily {
     const char *family;

@@ -1850,8 +1850,6 @@ void gemm_launch(const Weight &w, const half_t *x, int m, void *y, const half_t 
 }
 
 // Columns [c0, c0 + nc) of the product (c0 a multiple of 16) with BM x BN tiles.
-int device_cus();
-
 template <int BM, int BN, int WGM, int WGN, int EPI, bool PERSIST = false>
 bool w4a16_pipe_launch(const Weight &w, const half_t *x, int m, void *y, const half_t *res, hipStream_t s,
                        int c0 = 0, int nc = -1) {
@@ -1879,18 +1877,6 @@ bool w4a16_pipe_launch(const Weight &w, const half_t *x, int m, void *y, const h
 }
 
 // Compute units of the current device (queried once per device).
-int device_cus() {
-    static int cus[64] = {};
-    int dev = 0;
-    hipGetDevice(&dev);
-    if (dev < 0 || dev >= 64) return 256;
-    if (!cus[dev]) {
-        int v = 0;
-        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
-        cus[dev] = v;
-    }
-    return cus[dev];
-}
 
 // Variants 0-3 are the pipelined kernel: "auto", 256x256 tiles on 8 waves
 // (one block per CU), 128x128 tiles on 4 waves (two blocks per CU) and
@@ -2230,6 +2216,19 @@ void launch_i8_gemm(const int8_t *a, const float *sa, int m, const int8_t *b, co
         i8_gemm_dispatch<true>(a, sa, m, b, sb, n, k, y, raw, variant, s);
     else
         i8_gemm_dispatch<false>(a, sa, m, b, sb, n, k, y, raw, variant, s);
+}
+
+int device_cus() {
+    static int cus[64] = {};
+    int dev = 0;
+    hipGetDevice(&dev);
+    if (dev < 0 || dev >= 64) return 256;
+    if (!cus[dev]) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+        cus[dev] = v;
+    }
+    return cus[dev];
 }
 
 }  // namespace dz

@@ -53,6 +53,13 @@ def test_layernorm_gelu_rms_softmax_mean(ctx, oracle):
     ctx.mean_rows(dev(xs.reshape(150, 100)), rocm.F16, 3, 50, 100, means)
     for bi in range(3):
         assert np.allclose(host(ctx, means)[bi], oracle.mean_rows(xs[bi].astype(np.float32)), atol=1e-5)
+    # the 16-byte f16 path: 128-column groups (one partial), rows not a multiple of 64
+    for batch, rows_, d_ in ((3, 1000, 1024), (2, 77, 136)):
+        xs = (rng.standard_normal((batch, rows_, d_)) * 3).astype(np.float16)
+        means = empty((batch, d_), torch.float32)
+        ctx.mean_rows(dev(xs.reshape(batch * rows_, d_)), rocm.F16, batch, rows_, d_, means)
+        for bi in range(batch):
+            assert np.allclose(host(ctx, means)[bi], oracle.mean_rows(xs[bi].astype(np.float32)), atol=1e-5)
     a = dev(x.copy())
     ctx.add(a, dev(up), rocm.F32, x.size)
     assert bits_equal(host(ctx, a), x + up)
@@ -79,13 +86,14 @@ def test_gelu_erf_against_float64(ctx):
     assert got[-2] == np.float32(3.0e38) and got[-1] == np.inf
 
 
-@pytest.mark.parametrize("d", [512, 1024, 2048, 768])
-def test_layernorm_f16_rows(ctx, oracle, d):
-    """f16 LayerNorm: one wave per row for d in {512, 1024, 2048}, the block
-    kernel otherwise; both against the float64 closed form (ragged row count)."""
+@pytest.mark.parametrize("d,rows", [(512, 21), (1024, 21), (2048, 21), (768, 21), (1024, 5003), (512, 4099)])
+def test_layernorm_f16_rows(ctx, oracle, d, rows):
+    """f16 LayerNorm: one wave per row at a time for d in {512, 1024, 2048}
+    (waves walk several rows when the rows outnumber two blocks per compute
+    unit), the block kernel otherwise; both against the float64 closed form
+    (ragged row counts)."""
     torch = pytest.importorskip("torch")
-    rng = np.random.default_rng(d)
-    rows = 21
+    rng = np.random.default_rng(d + rows)
     x = (rng.standard_normal((rows, d)) * 2 - 0.5).astype(np.float16)
     w = rng.standard_normal(d).astype(np.float32)
     b = rng.standard_normal(d).astype(np.float32)
