@@ -140,6 +140,22 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
     return a + b;
 }
 
+// Maximum over the 64 lanes of a wave, left in every lane (wave_sum_dpp's
+// pattern with fmaxf; the maximum does not depend on the order).
+__device__ __forceinline__ float wave_max_dpp(float v) {
+    v = fmaxf(v, dpp_move_f32<0xB1>(v));
+    v = fmaxf(v, dpp_move_f32<0x4E>(v));
+    v = fmaxf(v, dpp_move_f32<0x124>(v));
+    v = fmaxf(v, dpp_move_f32<0x128>(v));
+    float a = v, b = v;
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+    v = fmaxf(a, b);
+    a = v;
+    b = v;
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+    return fmaxf(a, b);
+}
+
 // erf(x) by Abramowitz & Stegun, Handbook of Mathematical Functions (1964),
 // formula 7.1.26: erf(x) = 1 - (a1 t + a2 t^2 + a3 t^3 + a4 t^4 + a5 t^5) e^(-x^2)
 // with t = 1 / (1 + p x) for x >= 0, |error| <= 1.5e-7, odd extension for x < 0.

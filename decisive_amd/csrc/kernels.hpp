@@ -27,6 +27,13 @@ void launch_act_quantize(const float *x, int m, int k, int bits, int8_t *q, floa
 // grouped_q4.rs:3-25: the same codes and scales as 17-word records per group.
 void launch_act_quantize_records(const float *x, int m, int k, uint32_t *records, int *bad,
                                  hipStream_t s);
+// pplx_flash/cpu.rs:310-333 zero-centred RMSNorm (the readout norm's bits)
+// of f32 rows h [rows x d] (d % 64 == 0, d <= kRmsQuantizeMaxCols) into y
+// (may be null) and the A8 codes q / scales sc of the normed rows, equal to
+// act_quantize of y; sets *bad (may be null) on a non-finite normed value.
+constexpr int kRmsQuantizeMaxCols = 8192;
+void launch_rms_quantize(const float *h, int rows, int d, const float *w, float eps, int zero_centered, float *y,
+                         int8_t *q, float *sc, int *bad, hipStream_t s);
 // webgpu/int8.rs:107-145.
 void launch_i8_quantize_rows(const float *x, int rows, int k, int8_t *q, float *scales,
                              int32_t *sums, hipStream_t s);

@@ -43,7 +43,12 @@ int32_t ctx_readout_rows(dz_ctx *ctx, const Weight &w, const float *norm, const 
                          const int32_t *select, size_t rows, float eps, float *logits);
 int ctx_variant(dz_ctx *ctx, const char *family);
 int32_t ctx_product_add(dz_ctx *ctx, const dz_weight *w, const float *x, const int8_t *q, const float *qs,
-                        size_t m, float *h, bool *fused);
+                        size_t m, float *h, bool *fused, const int *qbad = nullptr);
+int32_t ctx_product_flag(dz_ctx *ctx, int **flag);
+int32_t ctx_codes_product(dz_ctx *ctx, const dz_weight *w, const int8_t *q, const float *qs, size_t m, float *y,
+                          const int *bad);
+int32_t ctx_mlp_codes(dz_ctx *ctx, const dz_weight *gate, const dz_weight *up, const int8_t *q, const float *qs,
+                      size_t m, int8_t *qo, float *so, const int *bad);
 
 namespace {
 
@@ -754,8 +759,10 @@ struct dz_pplx {
           *qhat = nullptr, *khat = nullptr, *gb = nullptr, *heads = nullptr, *ctx = nullptr, *projected = nullptr,
           *key = nullptr, *value = nullptr, *query = nullptr, *picked = nullptr, *gate = nullptr, *up = nullptr,
           *logits = nullptr, *chunk_ws = nullptr;
-    int8_t *codes = nullptr;
+    int8_t *codes = nullptr;     // the MLP's down_proj input codes
     float *code_scales = nullptr;
+    int8_t *ncodes = nullptr;    // the A8 codes of a layer norm's output, shared by its products
+    float *nscales = nullptr;
     int32_t *markers = nullptr;
     uint8_t *rows_dev = nullptr;
     dz::Weight rows_weight;
@@ -809,6 +816,8 @@ int32_t ensure_capacity(dz_ctx *ctx, dz_pplx *p, size_t n) {
     get(&p->up, n * (size_t)c.ff * 4);
     get(&p->codes, n * (size_t)c.ff);
     get(&p->code_scales, n * (size_t)(c.ff / 64) * 4);
+    get(&p->ncodes, n * d);
+    get(&p->nscales, n * (d / 64) * 4);
     get(&p->markers, (size_t)DZ_READOUT_MAX_MARKERS * 4);
     get(&p->logits, (size_t)DZ_READOUT_MAX_MARKERS * DZ_READOUT_CODES * 4);
     get(&p->rows_dev, n * (d / 64) * 36);
@@ -1030,18 +1039,57 @@ int32_t product_add(dz_ctx *ctx, const dz_weight *w, const float *x, const int8_
     return DZ_OK;
 }
 
+// The zero-centred RMSNorm of the hidden rows (cpu.rs:310-333). With the
+// "fused" norm variant and more than 16 rows, one kernel also writes the A8
+// codes of the normed rows (p->ncodes / p->nscales, equal to act_quantize of
+// them) and every product of the norm's output reads those codes, with one
+// non-finite flag (*flag); the normed f32 rows are written only when `need_f32`.
+// Otherwise ("separate", or few rows) the normed rows go to p->normed and each
+// product quantizes them itself. Both give the same bits.
+int32_t layer_norm(dz_ctx *ctx, dz_pplx *p, const float *w, size_t n, bool need_f32, bool *codes, int **flag) {
+    const dz_pplx_config &c = p->cfg;
+    hipStream_t s = ctx_stream(ctx);
+    *codes = false;
+    *flag = nullptr;
+    if (n <= 16 || ctx_variant(ctx, "norm") != 0 || c.hidden % 64 != 0 || c.hidden > kRmsQuantizeMaxCols) {
+        launch_readout_rms(p->hidden, 0, nullptr, (int)n, c.hidden, w, 1e-6f, 1, p->normed, s);
+        return DZ_OK;
+    }
+    int32_t rc = ctx_product_flag(ctx, flag);
+    if (rc) return rc;
+    launch_rms_quantize(p->hidden, (int)n, c.hidden, w, 1e-6f, 1, need_f32 ? p->normed : nullptr, p->ncodes,
+                        p->nscales, *flag, s);
+    *codes = true;
+    return DZ_OK;
+}
+
+// y = W . normed rows: from the norm's codes, or from p->normed (dz_linear)
+int32_t normed_product(dz_ctx *ctx, dz_pplx *p, const dz_weight *w, bool codes, const int *flag, size_t n, float *y) {
+    return codes ? ctx_codes_product(ctx, w, p->ncodes, p->nscales, n, y, flag) : linear(ctx, w, p->normed, n, y);
+}
+
 // backbone.rs:232-250: post-norm MLP with residual, in place on hidden
 int32_t mlp(dz_ctx *ctx, dz_pplx *p, const dz_pplx::Layer &L, size_t n) {
     const dz_pplx_config &c = p->cfg;
     hipStream_t s = ctx_stream(ctx);
-    launch_readout_rms(p->hidden, 0, nullptr, (int)n, c.hidden, L.post_norm, 1e-6f, 1, p->normed, s);
-    int32_t rc;
+    bool codes = false;
+    int *flag = nullptr;
+    int32_t rc = layer_norm(ctx, p, L.post_norm, n, false, &codes, &flag);
+    if (rc) return rc;
     if (weight_of(L.gate).kind == WeightKind::Q4G64 && weight_of(L.up).kind == WeightKind::Q4G64) {
         // gate/up, silu(gate)*up and the A8 codes of the down projection in one pass
-        rc = dz_mlp_requant(ctx, L.gate, L.up, p->normed, n, p->codes, p->code_scales);
+        if (codes)
+            rc = ctx_mlp_codes(ctx, L.gate, L.up, p->ncodes, p->nscales, n, p->codes, p->code_scales, flag);
+        else
+            rc = dz_mlp_requant(ctx, L.gate, L.up, p->normed, n, p->codes, p->code_scales);
         if (!rc) rc = product_add(ctx, L.down, nullptr, p->codes, p->code_scales, n, p->hidden, p->projected);
     } else {
-        rc = dz_linear_pair(ctx, L.gate, L.up, p->normed, n, p->gate, p->up, DZ_W4A8);
+        if (codes) {
+            rc = normed_product(ctx, p, L.gate, true, flag, n, p->gate);
+            if (!rc) rc = normed_product(ctx, p, L.up, true, flag, n, p->up);
+        } else {
+            rc = dz_linear_pair(ctx, L.gate, L.up, p->normed, n, p->gate, p->up, DZ_W4A8);
+        }
         if (!rc) launch_silu_mul(p->gate, p->up, n * (size_t)c.ff, s);
         if (!rc) rc = product_add(ctx, L.down, p->gate, nullptr, nullptr, n, p->hidden, p->projected);
     }
@@ -1080,9 +1128,19 @@ int32_t delta_layer(dz_ctx *ctx, dz_pplx *p, const dz_pplx::Layer &L, size_t n) 
     const dz_pplx_config &c = p->cfg;
     hipStream_t s = ctx_stream(ctx);
     const size_t cw = conv_width(c), lh = c.delta_heads;
-    launch_readout_rms(p->hidden, 0, nullptr, (int)n, c.hidden, L.input_norm, 1e-6f, 1, p->normed, s);
-    int32_t rc = dz_linear_pair(ctx, L.qkv, L.z, p->normed, n, p->wide, p->z, DZ_W4A8);
-    if (!rc) rc = dz_linear_pair(ctx, L.a, L.b, p->normed, n, p->ab, p->ab + n * lh, DZ_W4A8);
+    bool codes = false;
+    int *flag = nullptr;
+    int32_t rc = layer_norm(ctx, p, L.input_norm, n, false, &codes, &flag);
+    if (rc) return rc;
+    if (codes) {  // the four input projections share the norm's codes
+        rc = normed_product(ctx, p, L.qkv, true, flag, n, p->wide);
+        if (!rc) rc = normed_product(ctx, p, L.z, true, flag, n, p->z);
+        if (!rc) rc = normed_product(ctx, p, L.a, true, flag, n, p->ab);
+        if (!rc) rc = normed_product(ctx, p, L.b, true, flag, n, p->ab + n * lh);
+    } else {
+        rc = dz_linear_pair(ctx, L.qkv, L.z, p->normed, n, p->wide, p->z, DZ_W4A8);
+        if (!rc) rc = dz_linear_pair(ctx, L.a, L.b, p->normed, n, p->ab, p->ab + n * lh, DZ_W4A8);
+    }
     if (rc) return rc;
     hipLaunchKernelGGL(conv_silu_kernel, dim3(blocks_of(n * cw, 256)), dim3(256), 0, s, p->wide, (int)n, (int)cw,
                        L.conv, p->conv_out);
@@ -1127,17 +1185,25 @@ int32_t attention_layer(dz_ctx *ctx, dz_pplx *p, const dz_pplx::Layer &L, size_t
     const dz_pplx_config &c = p->cfg;
     hipStream_t s = ctx_stream(ctx);
     const size_t d = c.hidden, kvw = (size_t)c.attn_kv_heads * kAd, qw = 2 * (size_t)c.attn_heads * kAd;
-    launch_readout_rms(p->hidden, 0, nullptr, (int)n, c.hidden, L.input_norm, 1e-6f, 1, p->normed, s);
-    int32_t rc = dz_linear_pair(ctx, L.k, L.v, p->normed, n, p->key, p->value, DZ_W4A8);
+    bool codes = false;
+    int *flag = nullptr;
+    int32_t rc = layer_norm(ctx, p, L.input_norm, n, markers != nullptr, &codes, &flag);
+    if (rc) return rc;
+    if (codes) {
+        rc = normed_product(ctx, p, L.k, true, flag, n, p->key);
+        if (!rc) rc = normed_product(ctx, p, L.v, true, flag, n, p->value);
+    } else {
+        rc = dz_linear_pair(ctx, L.k, L.v, p->normed, n, p->key, p->value, DZ_W4A8);
+    }
     if (rc) return rc;
     const size_t nq = markers ? count : n;
-    const float *qin = p->normed;
-    if (markers) {
+    if (markers) {  // the marker rows' queries from their normed rows
         hipLaunchKernelGGL(gather_rows_kernel, dim3(blocks_of(count * d, 256)), dim3(256), 0, s, p->normed, markers,
                            (int)count, (int)d, p->picked);
-        qin = p->picked;
+        rc = linear(ctx, L.q, p->picked, nq, p->wide);
+    } else {
+        rc = normed_product(ctx, p, L.q, codes, flag, n, p->wide);
     }
-    rc = linear(ctx, L.q, qin, nq, p->wide);
     if (rc) return rc;
     // queries: [q | z] per head; keys in place
     hipLaunchKernelGGL(head_norm_rope_kernel, dim3((unsigned)nq, c.attn_heads), dim3(64), 0, s, p->wide, qw, 2 * kAd,

@@ -1791,6 +1791,7 @@ const char *const kGroupedNames[] = {"pipe-auto",    "pipe256x128w8", "wave16x16
                                      "pipe64x128w2", "pipe128x128m8", "pipe128x128n8"};
 const char *const kMlpNames[] = {"pipe-auto", "pipe256x64w8", "pipe128x64w4", "wave16x64", "pipe256x64n2", "pipe128x64n2"};
 const char *const kDeltaNames[] = {"auto", "recurrent", "chunked64"};
+const char *const kNormNames[] = {"fused", "separate"};
 
 template <int W, int MPAD, bool G32, int NP>
 void gemv_launch_np(const Weight &w, const half_t *x, int m, float *y, hipStream_t s) {
@@ -1969,6 +1970,7 @@ int variant_count(const char *family) {
     if (f == "grouped") return 7;
     if (f == "mlp") return 6;
     if (f == "delta_scan") return 3;
+    if (f == "norm") return 2;
     return 0;
 }
 
@@ -1981,6 +1983,7 @@ const char *variant_name(const char *family, int index) {
     if (f == "grouped") return kGroupedNames[index];
     if (f == "mlp") return kMlpNames[index];
     if (f == "delta_scan") return kDeltaNames[index];
+    if (f == "norm") return kNormNames[index];
     return nullptr;
 }
 

@@ -288,6 +288,75 @@ __global__ void act_quantize_kernel(const float *__restrict__ x, int m, int k, i
     if (l == 0) sc[(size_t)r * groups + g] = scale;
 }
 
+// ---- zero-centred RMSNorm fused with the A8 quantizer -------------------------------
+//
+// One block per row of d floats (d % 64 == 0). The row's squares are summed in
+// row order by one lane, as pplx_flash/cpu.rs:310-333 does (the readout norm's
+// arithmetic, bit for bit); the lane's LDS reads run 32 squares ahead of its
+// adds, so the chain of d dependent adds is the only wait. Then every wave
+// takes 64-column groups: v = (x * scale) * (1 + w) (w when not zero-centred),
+// written to y when y is set, and the group's A8 codes and scale exactly as
+// act_quantize_kernel computes them from v (int8.rs:178-202), so a product of
+// these codes equals the product of y. A non-finite v sets *bad.
+__global__ __launch_bounds__(256) void rms_quantize_kernel(const float *__restrict__ h, int d,
+                                                           const float *__restrict__ w, float eps, int zero_centered,
+                                                           float *__restrict__ y, int8_t *__restrict__ q,
+                                                           float *__restrict__ sc, int *bad) {
+    extern __shared__ __align__(16) float lds_f[];
+    float *xs = lds_f, *sq = lds_f + d;
+    __shared__ float scale_sh;
+    const size_t row = blockIdx.x, base = row * (size_t)d;
+    for (int i = threadIdx.x * 4; i < d; i += 1024) {
+        const float4_t v = *(const float4_t *)(h + base + i);
+        *(float4_t *)(xs + i) = v;
+        *(float4_t *)(sq + i) = float4_t{__fmul_rn(v[0], v[0]), __fmul_rn(v[1], v[1]), __fmul_rn(v[2], v[2]),
+                                         __fmul_rn(v[3], v[3])};
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        // ping-pong buffers of 32 squares: the adds of one wait only for its own reads
+        const float4_t *p4 = (const float4_t *)sq;
+        const int n4 = d / 4;  // a multiple of 16
+        float4_t a[8], b[8];
+        float ss = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) a[j] = p4[j];
+        for (int i = 0; i < n4; i += 16) {
+#pragma unroll
+            for (int j = 0; j < 8; j++) b[j] = p4[i + 8 + j];
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) ss = __fadd_rn(ss, a[j][e]);
+            if (i + 16 < n4) {
+#pragma unroll
+                for (int j = 0; j < 8; j++) a[j] = p4[i + 16 + j];
+            }
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) ss = __fadd_rn(ss, b[j][e]);
+        }
+        // the square root taken in f64 and rounded once (v_sqrt_f32 is not correctly rounded)
+        const float t = __fadd_rn(__fdiv_rn(ss, (float)d), eps);
+        scale_sh = __fdiv_rn(1.0f, __double2float_rn(__dsqrt_rn((double)t)));
+    }
+    __syncthreads();
+    const float scale = scale_sh;
+    const int wave = threadIdx.x / 64, lane = threadIdx.x % 64, groups = d / 64;
+    for (int g = wave; g < groups; g += 4) {
+        const int col = g * 64 + lane;
+        const float gain = zero_centered ? __fadd_rn(1.0f, w[col]) : w[col];
+        const float v = __fmul_rn(__fmul_rn(xs[col], scale), gain);
+        if (y) y[base + col] = v;
+        if (!__builtin_isfinite(v) && bad) atomicOr(bad, 1);
+        const float maximum = wave_max_dpp(fabsf(v));
+        const float s = fmaxf(__fdiv_rn(maximum, 127.0f), FLT_MIN);
+        q[(row * groups + g) * 64 + lane] = (int8_t)quantize_code(v, __frcp_rn(s), 127.0f);
+        if (lane == 0) sc[row * groups + g] = s;
+    }
+}
+
 // ---- per-row int8 quantizer (a11) -------------------------------------------------------
 
 __global__ __launch_bounds__(256) void i8_quantize_rows_kernel(const float *__restrict__ x, int k,
@@ -457,6 +526,13 @@ void launch_act_quantize_records(const float *x, int m, int k, uint32_t *records
     if (!lanes) return;
     hipLaunchKernelGGL(act_quantize_kernel, dim3(blocks_for(lanes, 256)), dim3(256), 0, s, x, m, k,
                        8, (int8_t *)nullptr, (float *)nullptr, bad, records);
+}
+
+void launch_rms_quantize(const float *h, int rows, int d, const float *w, float eps, int zero_centered, float *y,
+                         int8_t *q, float *sc, int *bad, hipStream_t s) {
+    if (!rows) return;
+    hipLaunchKernelGGL(rms_quantize_kernel, dim3(rows), dim3(256), (size_t)2 * d * sizeof(float), s, h, d, w, eps,
+                       zero_centered, y, q, sc, bad);
 }
 
 void launch_i8_quantize_rows(const float *x, int rows, int k, int8_t *q, float *scales,

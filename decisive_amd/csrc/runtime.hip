@@ -391,7 +391,7 @@ int32_t dz_info(dz_ctx *ctx, char *buf, size_t cap) {
     std::string s = "{\"arch\":\"" + ctx->arch + "\",\"compute_units\":" + std::to_string(ctx->cus) +
                     ",\"clock_khz\":" + std::to_string(ctx->clock_khz) + ",\"variants\":{";
     bool first = true;
-    for (const char *f : {"gemv", "gemm_w4a16", "i8_gemm", "grouped", "mlp", "delta_scan"}) {
+    for (const char *f : {"gemv", "gemm_w4a16", "i8_gemm", "grouped", "mlp", "delta_scan", "norm"}) {
         if (!first) s += ",";
         first = false;
         s += std::string("\"") + f + "\":\"" + dz::variant_name(f, variant(ctx, f)) + "\"";
@@ -1005,11 +1005,11 @@ int ctx_variant(dz_ctx *ctx, const char *family) { return variant(ctx, family); 
 // pipelined grouped kernel takes m rows (*fused set); otherwise nothing is
 // launched and the caller runs the product and the add.
 int32_t ctx_product_add(dz_ctx *ctx, const dz_weight *w, const float *x, const int8_t *q, const float *qs,
-                        size_t m, float *h, bool *fused) {
+                        size_t m, float *h, bool *fused, const int *qbad) {
     *fused = false;
     const int v = variant(ctx, "grouped");
     if (!dz::grouped_adds_residual(w->w, (int)m, v)) return DZ_OK;
-    const int *bad = nullptr;
+    const int *bad = qbad;
     if (x) {
         const size_t qbytes = m * (size_t)w->w.groups * 64, sbytes = m * (size_t)w->w.groups * sizeof(float);
         int32_t rc = ensure_work(ctx, qbytes + sbytes + 256);
@@ -1028,6 +1028,21 @@ int32_t ctx_product_add(dz_ctx *ctx, const dz_weight *w, const float *x, const i
         return fail(ctx, DZ_INFERENCE_FAILED, "residual product: no pipelined kernel takes the shape");
     *fused = true;
     return launched(ctx, "grouped linear");
+}
+// A non-finite flag for a product (or several sharing one set of codes).
+int32_t ctx_product_flag(dz_ctx *ctx, int **flag) { return product_flag(ctx, flag); }
+// y = the W4A8 product of the A8 codes q / scales qs of m > 16 rows (the
+// grouped kernel dz_linear uses); NaN outputs when *bad is set.
+int32_t ctx_codes_product(dz_ctx *ctx, const dz_weight *w, const int8_t *q, const float *qs, size_t m, float *y,
+                          const int *bad) {
+    dz::launch_grouped(w->w, q, qs, (int)m, y, bad, variant(ctx, "grouped"), ctx->stream);
+    return launched(ctx, "grouped linear");
+}
+// dz_mlp_requant on already-quantized activations (the codes of a norm)
+int32_t ctx_mlp_codes(dz_ctx *ctx, const dz_weight *gate, const dz_weight *up, const int8_t *q, const float *qs,
+                      size_t m, int8_t *qo, float *so, const int *bad) {
+    dz::launch_mlp_requant(gate->w, up->w, q, qs, (int)m, qo, so, bad, variant(ctx, "mlp"), ctx->stream);
+    return launched(ctx, "fused MLP");
 }
 void ctx_set_variant(dz_ctx *ctx, const char *family, int index) { ctx->variants[family] = index; }
 void ctx_set_tuning(dz_ctx *ctx, const std::string &json) { ctx->tuning = json; }

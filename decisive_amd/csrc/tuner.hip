@@ -17,6 +17,9 @@
 //               (M, N, K) = (256, 8192, 2560)
 //   mlp         the fused gate/up + SiLU + A8 requant (select_mlp, :568-652)
 //               at (128, 9216, 2560)
+//   norm        the decider's layer norm with its A8 codes in one kernel
+//               against the norm and the quantizer apart (select_norm,
+//               :652-684: 64 rows of 2560, its input and weight generators)
 //   gemv, gemm_w4a16, i8_gemm   this library's W4A16 GEMV / prefill GEMM and
 //               per-row int8 GEMM (no reference counterpart) at (1 or 256,
 //               8192, 2560)
@@ -71,7 +74,7 @@ uint32_t test_hash(size_t i, size_t seed) {
 // checkpoint.rs:850: a small positive f32 scale, 0.001 + (hash % 1000) * 1e-5.
 float test_scale(size_t i, size_t seed) { return 0.001f + (float)(test_hash(i, seed) % 1000) * 1e-5f; }
 
-enum class Kind { Grouped, Mlp, Gemv, GemmW4A16, I8Gemm };
+enum class Kind { Grouped, Mlp, Norm, Gemv, GemmW4A16, I8Gemm };
 
 struct Family {
     const char *name;
@@ -83,6 +86,7 @@ struct Family {
 const Family kFamilies[] = {
     {"grouped", Kind::Grouped, 256, 8192, 2560, 3},
     {"mlp", Kind::Mlp, 128, 9216, 2560, 2},
+    {"norm", Kind::Norm, 64, 2560, 2560, 2},
     {"gemv", Kind::Gemv, 1, 8192, 2560, 3},
     {"gemm_w4a16", Kind::GemmW4A16, 256, 8192, 2560, 3},
     {"i8_gemm", Kind::I8Gemm, 256, 8192, 2560, 3},
@@ -171,6 +175,16 @@ struct Bench {
                 launch_mlp_requant(w, w2, (const int8_t *)x, sx, m, (int8_t *)o[0].first, (float *)o[1].first,
                                    nullptr, v, s);
                 break;
+            case Kind::Norm:
+                if (v == 0) {
+                    launch_rms_quantize((const float *)x, m, k, sw, 1e-6f, 1, nullptr, (int8_t *)o[0].first,
+                                        (float *)o[1].first, nullptr, s);
+                } else {
+                    launch_readout_rms(x, 0, nullptr, m, k, sw, 1e-6f, 1, (float *)o[2].first, s);
+                    launch_act_quantize((const float *)o[2].first, m, k, 8, (int8_t *)o[0].first,
+                                        (float *)o[1].first, nullptr, s);
+                }
+                break;
             case Kind::Gemv:
                 launch_w4a16(w, (const half_t *)x, m, (float *)o[0].first, v, 0, s);
                 break;
@@ -213,6 +227,18 @@ bool build_bench(DeviceBuffers &buf, const Family &f, int count, Bench *b) {
             b->x = buf.upload(hashed_words(M * K, 0));         // any int8 codes
             b->sx = (const float *)buf.upload(small_scales(M * K / 64, 17));
             break;
+        case Kind::Norm: {
+            // checkpoint.rs:655-658: x = ((i * 7919 % 2003) - 1001) / 97, w the bf16 of ((i * 13 % 97) - 48) / 50
+            std::vector<float> hx(M * K), hw(K);
+            for (size_t i = 0; i < hx.size(); i++) hx[i] = ((float)(i * 7919 % 2003) - 1001.0f) / 97.0f;
+            for (size_t i = 0; i < K; i++) {
+                const uint32_t bits = __builtin_bit_cast(uint32_t, ((float)(i * 13 % 97) - 48.0f) / 50.0f) >> 16;
+                hw[i] = __builtin_bit_cast(float, bits << 16);
+            }
+            b->x = buf.upload(hx);
+            b->sw = (const float *)buf.upload(hw);
+            break;
+        }
         case Kind::Gemv:
         case Kind::GemmW4A16: {
             b->w = test_weight(buf, WeightKind::Q4G32, f.n, f.k, 7);
@@ -233,9 +259,11 @@ bool build_bench(DeviceBuffers &buf, const Family &f, int count, Bench *b) {
     }
     b->outs.resize(count);
     for (int v = 0; v < count; v++) {
-        if (f.kind == Kind::Mlp) {
+        if (f.kind == Kind::Mlp || f.kind == Kind::Norm) {
+            // codes, scales (and for the separate norm its normed rows, not compared)
             b->outs[v].push_back({buf.alloc(M * N), M * N});
             b->outs[v].push_back({buf.alloc(M * N / 64 * 4), M * N / 64 * 4});
+            if (f.kind == Kind::Norm) b->outs[v].push_back({buf.alloc(M * N * 4), 0});
         } else {
             b->outs[v].push_back({buf.alloc(M * N * 4), M * N * 4});
         }

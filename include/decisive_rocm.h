@@ -392,8 +392,10 @@ int32_t dz_pplx_forward_rows(dz_ctx *ctx, dz_pplx *model, const void *rows_host,
  * keeps the fastest variant whose output is bitwise equal to the family's
  * reference variant and faster than 0.99x it. Families, in order: "grouped"
  * (the W4A8 product, checkpoint.rs:480-563 select_gemm at M,N,K = 256, 8192,
- * 2560), "mlp" (the fused MLP, :568-652 select_mlp at 128, 9216, 2560), then
- * "gemv", "gemm_w4a16" and "i8_gemm" (no reference counterpart). The delta
+ * 2560), "mlp" (the fused MLP, :568-652 select_mlp at 128, 9216, 2560),
+ * "norm" (:652-684 select_norm: 64 rows of 2560, the fused norm and codes
+ * against the separate ones), then "gemv", "gemm_w4a16" and "i8_gemm" (no
+ * reference counterpart). The delta
  * scan is not tuned: its scans are not bit-equal, which the reference's
  * select_delta_scan (:328-421) requires. cache_in (JSON from an earlier
  * cache_out, or NULL; unreadable text is ignored) is reused while its key
@@ -418,7 +420,11 @@ int32_t dz_tune(dz_ctx *ctx, uint32_t budget_ms, const char *cache_in, char *cac
  *                 agree to rounding, not bit for bit; "auto" runs the
  *                 recurrent scan below 384 tokens and the chunked one from
  *                 there, so a decider's bits depend on its chunk length
- *                 across that mark) */
+ *                 across that mark)
+ *   "norm"        fused, separate (the decider's layer norms above 16 rows:
+ *                 one kernel for the RMSNorm and the A8 codes its products
+ *                 share, or the norm then one quantization per product; the
+ *                 same bits) */
 int32_t dz_select_variant(dz_ctx *ctx, const char *family, const char *variant);
 
 #ifdef __cplusplus

@@ -281,7 +281,7 @@ def test_config3_encoder_full_size_runs_finite_and_deterministic(ctx):
     enc.close()
 
 
-TUNED = ("grouped", "mlp", "gemv", "gemm_w4a16", "i8_gemm")
+TUNED = ("grouped", "mlp", "norm", "gemv", "gemm_w4a16", "i8_gemm")
 
 
 def test_tuner_selects_bitwise_equal_variants_and_caches(ctx):
@@ -314,6 +314,7 @@ def _tuner_checks(ctx):
         for v, a in enumerate(f["agrees"]):
             assert a in (True, False, None)
     assert fams["grouped"]["shape"] == [256, 8192, 2560] and fams["mlp"]["shape"] == [128, 9216, 2560]
+    assert fams["norm"]["shape"][0] == 64 and fams["norm"]["shape"][2] == 2560
     again = ctx.tune(5000, cache=__import__("json").dumps(sel))
     assert again["key"] == sel["key"]
     for fam in TUNED:
@@ -371,4 +372,4 @@ def test_tuned_grouped_and_mlp_variants_agree_on_real_inputs(ctx, oracle):
 
 def rocm_reference(fam):
     return {"gemv": "w16", "gemm_w4a16": "pipe-auto", "i8_gemm": "256x256p2w8", "grouped": "pipe-auto",
-            "mlp": "pipe-auto"}[fam]
+            "mlp": "pipe-auto", "norm": "fused"}[fam]

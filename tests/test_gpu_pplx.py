@@ -183,3 +183,57 @@ def test_residual_added_in_the_product_epilogue_gives_the_same_bits(ctx, oracle,
     assert np.array_equal(out["wave16x16"].view(np.uint32), out["pipe64x128w2"].view(np.uint32))
     want = pplx_model.ref_layer(oracle, model, layer, h, markers)
     assert close(out["pipe128x128w4"], want)
+
+
+@pytest.mark.parametrize("layer,n,markers", [(1, 37, None), (1, 130, None), (3, 77, None), (3, 130, MANY), (0, 400, None)])
+def test_fused_norm_codes_give_the_separate_norms_bits(ctx, oracle, small, layer, n, markers):
+    """The "fused" norm writes the RMSNorm and the A8 codes its products share
+    in one kernel; the "separate" norm writes the normed rows and each product
+    quantizes them (act_quantize). Both are bit-exact with cpu::rms_from and
+    int8.rs's quantizer, so the layers give the same bits."""
+    torch = pytest.importorskip("torch")
+    model, p = small
+    h = np.random.default_rng(900 + n).standard_normal((n, SMALL["hidden"])).astype(np.float32)
+    out = {}
+    for v in ("fused", "separate"):
+        hd = dev(h)
+        ctx.select_variant("norm", v)
+        try:
+            p.layer(layer, hd, n, markers)
+        finally:
+            ctx.select_variant("norm", "fused")
+        out[v] = host(ctx, hd)[:n if markers is None else len(markers)]
+    assert np.array_equal(out["fused"].view(np.uint32), out["separate"].view(np.uint32))
+    want = pplx_model.ref_layer(oracle, model, layer, h, markers)
+    assert close(out["fused"], want, rel=1e-2), (float(cosine(out["fused"], want)),)
+
+
+def test_fused_norm_forward_and_nonfinite_rows(ctx, oracle, small):
+    """A whole chunk forward gives the same logits under both norms; a
+    non-finite hidden value makes the fused norm's products NaN as the
+    separate quantizer's flag does (int8.rs:170-173)."""
+    torch = pytest.importorskip("torch")
+    model, p = small
+    n = 300
+    ids = np.random.default_rng(31).integers(0, 64, n)
+    markers = [n - 1, 5, n // 2]
+    got = {}
+    for v in ("fused", "separate"):
+        ctx.select_variant("norm", v)
+        try:
+            got[v] = p.forward_rows(model.embedding[ids], n, markers)
+        finally:
+            ctx.select_variant("norm", "fused")
+    assert np.array_equal(got["fused"].view(np.uint32), got["separate"].view(np.uint32))
+    h = np.random.default_rng(32).standard_normal((40, SMALL["hidden"])).astype(np.float32)
+    h[7, 3] = np.inf
+    outs = {}
+    for v in ("fused", "separate"):
+        hd = dev(h)
+        ctx.select_variant("norm", v)
+        try:
+            p.layer(0, hd, 40)
+        finally:
+            ctx.select_variant("norm", "fused")
+        outs[v] = host(ctx, hd)
+    assert np.isnan(outs["fused"]).all() and np.isnan(outs["separate"]).all()
