@@ -303,8 +303,16 @@ def secondary(torch, ctx, rocm, stream, cpu=True) -> dict:
     warm(torch, fn)
     ms = timed_ms(torch, stream, fn, 20)
     tops = 2 * m * n * k / (ms * 1e-3) / 1e12
+    # the same launch on all-zero codes: the difference is the power the operand
+    # bits draw (the clock drops under toggling data), not work
+    qa.zero_()
+    qb.zero_()
+    torch.cuda.synchronize()
+    warm(torch, fn)
+    ms_zero = timed_ms(torch, stream, fn, 20)
     out["int8_gemm_m8192_k4096_n4096"] = {"ms": round(ms, 4), "TOP/s": round(tops, 1),
                                           "frac_of_i8_peak": round(tops / I8_PEAK_TOPS, 4),
+                                          "ms_on_zero_codes": round(ms_zero, 4),
                                           "variant": ctx.info()["variants"]["i8_gemm"]}
     del a, b, qa, qb, y
     # config 5: Q4 prefill M=16384 K=4096 N=14336

@@ -1096,6 +1096,237 @@ __global__ __launch_bounds__(WGM *WGN * 64) void i8_gemm_pipe_kernel(const int8_
     }
 }
 
+// Persistent form of i8_gemm_pipe_kernel: a grid of at most one block per
+// compute unit, block b taking tiles b, b + grid, ... (xcd_tile order over all
+// tiles) as ONE stream of k-steps, so the loads of a tile's first steps are in
+// flight while the previous tile's last steps compute. Each tile's epilogue
+// stores straight from the accumulators (lane (i, h) of a 32x32 block holds
+// column i of rows 8(e/4) + 4h + e%4: a store instruction writes two 128-byte
+// row pieces), which leaves the LDS stages to the next tile and lets those
+// stores drain under its MFMAs. Outputs equal i8_gemm_pipe_kernel's (exact
+// int32 dots; the f32 epilogue (f32(dot) * sa) * sb).
+template <int BM, int BN, int BK, int NS, int WGM, int WGN, bool MID>
+__global__ __launch_bounds__(WGM *WGN * 64, 2) void i8_gemm_stream_kernel(const int8_t *__restrict__ a,
+                                                                     const float *__restrict__ sa, int m,
+                                                                     const int8_t *__restrict__ b,
+                                                                     const float *__restrict__ sb, int n, int k,
+                                                                     void *__restrict__ y, int raw) {
+    static_assert(NS >= 2 && NS <= 4, "2 to 4 stages");
+    constexpr int WAVES = WGM * WGN, THREADS = WAVES * 64;
+    constexpr int TM = BM / WGM, TN = BN / WGN, MB = TM / 32, NB = TN / 32;
+    constexpr int CPR = BK / 16;
+    constexpr int RPI = 64 / CPR;
+    constexpr int STAGE = (BM + BN) * BK;
+    constexpr int DPW = (BM + BN) / RPI / WAVES;
+    static_assert(DPW * WAVES * RPI == BM + BN, "DMA blocks split evenly over the waves");
+    constexpr int SUBS = BK / 32;
+    static_assert((NS - 2) * DPW <= 63, "vmcnt range");
+    __shared__ __align__(16) uint8_t stages[NS * STAGE];
+    __shared__ __align__(16) float scale_rows[2][BM], scale_cols[2][BN];  // by tile parity
+
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), lane = threadIdx.x % 64;
+    const int wm = wave / WGN, wn = wave % WGN;
+    const int h = lane / 32, i = lane % 32;
+    const int tiles_m = (m + BM - 1) / BM, tiles_n = (n + BN - 1) / BN, total = tiles_m * tiles_n;
+    const int grid = gridDim.x, blk = blockIdx.x;
+    if (blk >= total) return;
+    const int my_tiles = (total - blk + grid - 1) / grid;
+    const int steps = (k + BK - 1) / BK;
+    const int stream = my_tiles * steps;
+    auto tile_origin = [&](int j, int &row0, int &col0) {
+        int tm, tn;
+        xcd_tile(blk + j * grid, total, tiles_m, tiles_n, tm, tn);
+        row0 = tm * BM;
+        col0 = tn * BN;
+    };
+    static_assert(DPW % 2 == 0, "instruction parity known at compile time");
+    const int lrow = lane / CPR;
+    const int c16[2] = {pipe_slot<BK>(lane % CPR, lrow) * 16, pipe_slot<BK>(lane % CPR, lrow + RPI) * 16};
+    const uint32_t lane_off[2] = {(uint32_t)(lrow * k + c16[0]), (uint32_t)(lrow * k + c16[1])};
+    // the tile the loads are filling (they run NS - 1 steps ahead of the MFMAs)
+    __amdgpu_buffer_rsrc_t rsa, rsb;
+    auto load_tile = [&](int j) {
+        int row0, col0;
+        tile_origin(j, row0, col0);
+        rsa = __builtin_amdgcn_make_buffer_rsrc((void *)(a + (size_t)row0 * k), (short)0, min(BM, m - row0) * k,
+                                                0x00020000);
+        rsb = __builtin_amdgcn_make_buffer_rsrc((void *)(b + (size_t)col0 * k), (short)0, min(BN, n - col0) * k,
+                                                0x00020000);
+    };
+    auto dma = [&](uint8_t *stage, int st, int p0, int p1) {
+        const int kk = st * BK;
+        const uint32_t voff0 = kk + c16[0] < k ? lane_off[0] + (uint32_t)kk : 0x80000000u;
+        const uint32_t voff1 = kk + c16[1] < k ? lane_off[1] + (uint32_t)kk : 0x80000000u;
+#pragma unroll
+        for (int p = p0; p < p1; p++) {
+            const int bl = wave * DPW + p;
+            const uint32_t voff = (p & 1) ? voff1 : voff0;
+            auto *dst = (__attribute__((address_space(3))) void *)(stage + __builtin_amdgcn_readfirstlane(bl * 1024));
+            if (bl * RPI < BM)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, dst, 16, voff + (uint32_t)(bl * RPI * k), 0, 0, 0);
+            else
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb, dst, 16, voff + (uint32_t)((bl * RPI - BM) * k), 0, 0, 0);
+        }
+    };
+    auto read_frags = [&](const uint8_t *stage, int sub, int4_t *af, int4_t *bf) {
+        const uint8_t *la = stage, *lb = stage + BM * BK;
+        const int c = sub * 2 + h;
+#pragma unroll
+        for (int x = 0; x < MB; x++) {
+            const int r = wm * TM + x * 32 + i;
+            af[x] = *(const int4_t *)(la + r * BK + pipe_slot<BK>(c, r) * 16);
+        }
+#pragma unroll
+        for (int z = 0; z < NB; z++) {
+            const int r = wn * TN + z * 32 + i;
+            bf[z] = *(const int4_t *)(lb + r * BK + pipe_slot<BK>(c, r) * 16);
+        }
+    };
+    int16_t_v acc[MB][NB];
+    auto compute = [&](const uint8_t *stage, uint8_t *next, int next_step) {
+        int4_t af[2][MB], bf[2][NB];
+        read_frags(stage, 0, af[0], bf[0]);
+#pragma unroll
+        for (int sub = 0; sub < SUBS; sub++) {
+            const int cur = sub & 1;
+            if (next) dma(next, next_step, sub * DPW / SUBS, (sub + 1) * DPW / SUBS);
+            if (sub + 1 < SUBS) read_frags(stage, sub + 1, af[cur ^ 1], bf[cur ^ 1]);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int x = 0; x < MB; x++)
+#pragma unroll
+                for (int z = 0; z < NB; z++)
+                    acc[x][z] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[cur][x], bf[cur][z], acc[x][z], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    // tile j's scales into buffer j % 2 (its epilogue reads them several barriers later)
+    auto load_scales = [&](int j) {
+        if (raw) return;
+        int row0, col0;
+        tile_origin(j, row0, col0);
+        for (int r = threadIdx.x; r < BM; r += THREADS) scale_rows[j & 1][r] = row0 + r < m ? sa[row0 + r] : 0.0f;
+        for (int c = threadIdx.x; c < BN; c += THREADS) scale_cols[j & 1][c] = col0 + c < n ? sb[col0 + c] : 0.0f;
+    };
+    // Buffer stores: rows past m fall outside the resource's range, columns past
+    // n take an offset beyond any range; both are dropped by the hardware.
+    auto epilogue = [&](int j) {
+        int row0, col0;
+        tile_origin(j, row0, col0);
+        const __amdgpu_buffer_rsrc_t rsy = __builtin_amdgcn_make_buffer_rsrc(
+            (void *)((uint32_t *)y + (size_t)row0 * n), (short)0, min(BM, m - row0) * n * 4, 0x00020000);
+        const float *rs = scale_rows[j & 1];
+#pragma unroll
+        for (int z = 0; z < NB; z++) {
+            const int cl = wn * TN + z * 32 + i;
+            const uint32_t lane_col = col0 + cl < n ? (uint32_t)((wm * TM + 4 * h) * n + col0 + cl) * 4u : 0x80000000u;
+            const float cs = raw ? 0.0f : scale_cols[j & 1][cl];
+#pragma unroll
+            for (int x = 0; x < MB; x++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const int rl = wm * TM + x * 32 + 8 * q + 4 * h;
+                    float4 r4 = raw ? float4{} : *(const float4 *)(rs + rl);
+                    const float rv[4] = {r4.x, r4.y, r4.z, r4.w};
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const int32_t d = acc[x][z][4 * q + e];
+                        const uint32_t v = raw ? (uint32_t)d
+                                               : __builtin_bit_cast(uint32_t, __fmul_rn(__fmul_rn((float)d, rv[e]), cs));
+                        const uint32_t soff = __builtin_amdgcn_readfirstlane((uint32_t)((x * 32 + 8 * q + e) * n) * 4u);
+                        __builtin_amdgcn_raw_buffer_store_b32(v, rsy, lane_col + soff, 0, 0);
+                    }
+                }
+        }
+    };
+
+    load_tile(0);
+    load_scales(0);
+    // the first NS - 1 steps (NS with the boundary inside the last k-slice, which
+    // loads step g + NS rather than g + NS - 1)
+#pragma unroll
+    for (int j = 0; j < (MID ? NS : NS - 1); j++)
+        if (j < stream) {
+            if (j > 0 && j % steps == 0) load_tile(j / steps);
+            dma(stages + j * STAGE, j % steps, 0, DPW);
+        }
+    // tiles in the outer loop, so the accumulators restart at zero unconditionally
+    // (a conditional restart would keep two copies of them alive)
+    if constexpr (!MID) {
+        int g = 0, slot = 0;
+        for (int j = 0; j < my_tiles; j++) {
+            if (j > 0) load_scales(j);
+#pragma unroll
+            for (int x = 0; x < MB; x++)
+#pragma unroll
+                for (int z = 0; z < NB; z++) acc[x][z] = int16_t_v{};
+            for (int st = 0; st < steps; st++, g++, slot = slot + 1 == NS ? 0 : slot + 1) {
+                if (g + NS - 2 < stream)
+                    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((NS - 2) * DPW) : "memory");
+                else
+                    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+                const int nx = g + NS - 1;
+                if (nx < stream && nx % steps == 0) load_tile(nx / steps);
+                const int nslot = slot == 0 ? NS - 1 : slot - 1;
+                compute(stages + slot * STAGE, nx < stream ? stages + nslot * STAGE : nullptr, nx % steps);
+            }
+            epilogue(j);
+        }
+    } else {
+        // The step boundary sits inside the last k-slice: once this wave's
+        // fragment reads of step g and its loads of step g + 1 are done, one
+        // barrier frees slot g (its loads of step g + NS go there at once, a
+        // whole step ahead) and publishes step g + 1, whose first fragments are
+        // read before the last MFMAs of step g issue.
+        static_assert(SUBS % 2 == 0, "the first fragments of a step land in buffer 0");
+        static_assert((NS - 1) * DPW <= 63, "vmcnt range");
+        int4_t af[2][MB], bf[2][NB];
+        if (NS - 1 < stream)
+            asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((NS - 1) * DPW) : "memory");
+        else
+            asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+        read_frags(stages, 0, af[0], bf[0]);
+        int g = 0, slot = 0;
+        for (int j = 0; j < my_tiles; j++) {
+            if (j > 0) load_scales(j);
+#pragma unroll
+            for (int x = 0; x < MB; x++)
+#pragma unroll
+                for (int z = 0; z < NB; z++) acc[x][z] = int16_t_v{};
+            for (int st = 0; st < steps; st++, g++, slot = slot + 1 == NS ? 0 : slot + 1) {
+                const uint8_t *stage = stages + slot * STAGE;
+#pragma unroll
+                for (int sub = 0; sub < SUBS; sub++) {
+                    const int cur = sub & 1;
+                    if (sub + 1 < SUBS) {
+                        read_frags(stage, sub + 1, af[cur ^ 1], bf[cur ^ 1]);
+                    } else if (g + 1 < stream) {
+                        if (g + NS - 1 < stream)
+                            asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"((NS - 2) * DPW) : "memory");
+                        else
+                            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+                        const int nx = g + NS;
+                        if (nx < stream) {
+                            if (nx % steps == 0) load_tile(nx / steps);
+                            dma(stages + slot * STAGE, nx % steps, 0, DPW);
+                        }
+                        read_frags(stages + (slot + 1 == NS ? 0 : slot + 1) * STAGE, 0, af[cur ^ 1], bf[cur ^ 1]);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int x = 0; x < MB; x++)
+#pragma unroll
+                        for (int z = 0; z < NB; z++)
+                            acc[x][z] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[cur][x], bf[cur][z], acc[x][z], 0, 0, 0);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+            if (steps == 1 && !raw) __syncthreads();  // a one-step tile's scales have no barrier after them
+            epilogue(j);
+        }
+    }
+}
+
 // ============================================================================
 // pipelined W4A16 GEMM (large M)
 // ============================================================================
@@ -1786,7 +2017,8 @@ const char *const kGemvNames[] = {"w16", "w8"};
 const char *const kGemmNames[] = {"pipe-auto",   "256x256p2w8", "128x128p2w4", "128x256p2w8",
                                    "256x128w2x2", "128x128w2x2", "128x64w2x2", "256x256p2w8-persist"};
 const char *const kI8Names[] = {"256x256p2w8", "256x256p4k64w8", "256x128p3w8", "256x128p3",
-                                 "128x128w2x2", "256x128w2x2", "64x64w2x2"};
+                                 "128x128w2x2", "256x128w2x2", "64x64w2x2", "256x256p2w8-stream",
+                                 "256x256p2w8-stream-mid", "256x128k64p2-stream2"};
 const char *const kGroupedNames[] = {"pipe-auto",    "pipe256x128w8", "wave16x16",   "pipe128x128w4",
                                      "pipe64x128w2", "pipe128x128m8", "pipe128x128n8"};
 const char *const kMlpNames[] = {"pipe-auto", "pipe256x64w8", "pipe128x64w4", "wave16x64", "pipe256x64n2", "pipe128x64n2"};
@@ -1966,7 +2198,7 @@ int variant_count(const char *family) {
     std::string f(family);
     if (f == "gemv") return 2;
     if (f == "gemm_w4a16") return 8;
-    if (f == "i8_gemm") return 7;
+    if (f == "i8_gemm") return 10;
     if (f == "grouped") return 7;
     if (f == "mlp") return 6;
     if (f == "delta_scan") return 3;
@@ -2180,8 +2412,23 @@ bool i8_pipe_launch(const int8_t *a, const float *sa, int m, const int8_t *b, co
     return true;
 }
 
-// Variants 0-3 are the pipelined buffer-to-LDS kernels (int8 B, k % 16 == 0);
-// 4-6 stage through registers and take any k and the per-row Q4 B operand.
+// BPC blocks per compute unit (what the kernel's LDS and registers allow).
+template <int BM, int BN, int BK, int NS, int WGM, int WGN, int BPC, bool MID>
+bool i8_stream_launch(const int8_t *a, const float *sa, int m, const int8_t *b, const float *sb, int n, int k,
+                      void *y, int raw, hipStream_t s) {
+    if (k % 16 != 0 || (size_t)BM * k >= ((size_t)1 << 31) || (size_t)BN * k >= ((size_t)1 << 31) ||
+        (size_t)BM * n * 4 >= ((size_t)1 << 31))
+        return false;
+    const unsigned tiles = cdiv(m, BM) * cdiv(n, BN);
+    const unsigned grid = std::min(tiles, (unsigned)(BPC * device_cus() / 8 * 8));
+    hipLaunchKernelGGL((i8_gemm_stream_kernel<BM, BN, BK, NS, WGM, WGN, MID>), dim3(grid ? grid : 1), dim3(WGM * WGN * 64), 0, s,
+                       a, sa, m, b, sb, n, k, y, raw);
+    return true;
+}
+
+// Variants 0-3 are the pipelined buffer-to-LDS kernels and 7-9 their
+// persistent stream form (int8 B, k % 16 == 0); 4-6 stage through registers
+// and take any k and the per-row Q4 B operand.
 // Every variant computes exact int32 dots, so all are bitwise equal; when a
 // pipelined variant cannot take a shape, the register-staged 128x128 runs.
 template <bool Q4B>
@@ -2193,6 +2440,9 @@ void i8_gemm_dispatch(const int8_t *a, const float *sa, int m, const int8_t *b, 
             case 1: if (i8_pipe_launch<256, 256, 64, 4, 2, 4>(a, sa, m, b, sb, n, k, y, raw, s)) return; break;
             case 2: if (i8_pipe_launch<256, 128, 128, 3, 2, 4>(a, sa, m, b, sb, n, k, y, raw, s)) return; break;
             case 3: if (i8_pipe_launch<256, 128, 128, 3, 2, 2>(a, sa, m, b, sb, n, k, y, raw, s)) return; break;
+            case 7: if (i8_stream_launch<256, 256, 128, 2, 2, 4, 1, false>(a, sa, m, b, sb, n, k, y, raw, s)) return; break;
+            case 8: if (i8_stream_launch<256, 256, 128, 2, 2, 4, 1, true>(a, sa, m, b, sb, n, k, y, raw, s)) return; break;
+            case 9: if (i8_stream_launch<256, 128, 64, 2, 2, 2, 2, false>(a, sa, m, b, sb, n, k, y, raw, s)) return; break;
             default: break;
         }
     }

@@ -410,7 +410,9 @@ int32_t dz_tune(dz_ctx *ctx, uint32_t budget_ms, const char *cache_in, char *cac
  *   "gemm_w4a16"  pipe-auto, 256x256p2w8, 128x128p2w4, 128x256p2w8, 256x128w2x2,
  *                 128x128w2x2, 128x64w2x2, 256x256p2w8-persist
  *   "i8_gemm"     256x256p2w8, 256x256p4k64w8, 256x128p3w8, 256x128p3, 128x128w2x2,
- *                 256x128w2x2, 64x64w2x2
+ *                 256x128w2x2, 64x64w2x2, 256x256p2w8-stream, 256x256p2w8-stream-mid,
+ *                 256x128k64p2-stream2 (the "-stream" forms are persistent: one
+ *                 or two blocks per compute unit, each walking several tiles)
  *   "grouped"     pipe-auto, pipe256x128w8, wave16x16, pipe128x128w4, pipe64x128w2,
  *                 pipe128x128m8, pipe128x128n8
  *   "mlp"         pipe-auto, pipe256x64w8, pipe128x64w4, wave16x64, pipe256x64n2,

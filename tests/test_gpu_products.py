@@ -529,7 +529,7 @@ def test_config5_prefill_rows_vs_fp32(ctx, oracle):
 # ---- per-row int8 ----------------------------------------------------------------------
 
 I8_VARIANTS = ("256x256p2w8", "256x256p4k64w8", "256x128p3w8", "256x128p3", "128x128w2x2", "256x128w2x2",
-               "64x64w2x2")
+               "64x64w2x2", "256x256p2w8-stream", "256x256p2w8-stream-mid", "256x128k64p2-stream2")
 
 
 @pytest.mark.parametrize("m,n,k", GOLDEN["q4_raw_check_shapes"]["mnk"] + [[77, 45, 100], [1, 1, 4], [130, 260, 4100],
@@ -583,6 +583,19 @@ def test_config4_int8_full_size(ctx, oracle):
     # every row: sum_j C[i, j] == A[i] . (sum_j B[j]) exactly (integer checksum)
     colsum = oqb.astype(np.int64).sum(axis=0)
     assert np.array_equal(got.astype(np.int64).sum(axis=1), oqa.astype(np.int64) @ colsum)
+    # every variant (the persistent ones walk several tiles per block) gives the same bits
+    yf = empty((m, n), torch.float32)
+    ctx.i8_gemm(qa, sa, m, qb, sb, n, k, yf, raw=False)
+    for name in I8_VARIANTS:
+        ctx.select_variant("i8_gemm", name)
+        rv = torch.full((m, n), -7, dtype=torch.int32, device="cuda")
+        yv = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
+        ctx.i8_gemm(qa, sa, m, qb, sb, n, k, rv, raw=True)
+        ctx.i8_gemm(qa, sa, m, qb, sb, n, k, yv, raw=False)
+        ctx.sync()
+        assert torch.equal(rv, r), name
+        assert torch.equal(yv.view(torch.int32), yf.view(torch.int32)), name
+    ctx.select_variant("i8_gemm", I8_VARIANTS[0])
 
 
 # ---- per-row Q4 product (webgpu/q4.rs:99-105) ----------------------------------------
