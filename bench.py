@@ -303,6 +303,19 @@ def secondary(torch, ctx, rocm, stream, cpu=True) -> dict:
     warm(torch, fn)
     ms = timed_ms(torch, stream, fn, 20)
     tops = 2 * m * n * k / (ms * 1e-3) / 1e12
+    # the vendor library on the same codes (torch._int_mm: int8 x int8 -> int32,
+    # the raw product without the f32 rescale), operands made contiguous first
+    try:
+        qbt = qb.t().contiguous()
+        ri = torch.empty((m, n), dtype=torch.int32, device="cuda")
+        torch.cuda.synchronize()
+        lib = lambda r: torch._int_mm(qa, qbt, out=ri)  # noqa: E731
+        warm(torch, lib)
+        vendor = {"ms": round(timed_ms(torch, torch.cuda.current_stream(), lib, 20), 4),
+                  "what": "torch._int_mm (hipBLASLt), raw int32 output"}
+        del qbt, ri
+    except Exception as e:  # the library may not take this shape on every build
+        vendor = {"error": str(e)[:200]}
     # the same launch on all-zero codes: the difference is the power the operand
     # bits draw (the clock drops under toggling data), not work
     qa.zero_()
@@ -313,6 +326,7 @@ def secondary(torch, ctx, rocm, stream, cpu=True) -> dict:
     out["int8_gemm_m8192_k4096_n4096"] = {"ms": round(ms, 4), "TOP/s": round(tops, 1),
                                           "frac_of_i8_peak": round(tops / I8_PEAK_TOPS, 4),
                                           "ms_on_zero_codes": round(ms_zero, 4),
+                                          "vendor_library": vendor,
                                           "variant": ctx.info()["variants"]["i8_gemm"]}
     del a, b, qa, qb, y
     # config 5: Q4 prefill M=16384 K=4096 N=14336

@@ -70,6 +70,9 @@ void launch_w4a16_f16(const Weight &w, const half_t *x, int m, half_t *y, int ep
 // word buffer of launch_q4_quantize_rows (codes expanded to int8 in registers).
 void launch_i8_gemm(const int8_t *a, const float *sa, int m, const int8_t *b, const float *sb,
                     int n, int k, void *y, int raw, int variant, hipStream_t s, bool b_q4 = false);
+// webgpu/int8.rs:226-230 gemm(fused=true): y = silu(gate) * up of two per-row int8 products sharing a
+void launch_i8_gemm_fused(const int8_t *a, const float *sa, int m, const int8_t *wg, const float *sg,
+                          const int8_t *wu, const float *su, int n, int k, float *y, hipStream_t s);
 // Fused gate/up W4A8 + SiLU + A8 requantization (grouped_q4_mlp.wgsl).
 void launch_mlp_requant(const Weight &gate, const Weight &up, const int8_t *q, const float *sx,
                         int m, int8_t *qo, float *so, const int *bad, int variant, hipStream_t s);

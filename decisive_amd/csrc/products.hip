@@ -754,16 +754,25 @@ __device__ __forceinline__ uint2_t row_nibbles_to_i8(uint32_t w) {
     return out;
 }
 
-template <int BM, int BN, int WM, int WN, bool Q4B>
+// FUSED (webgpu/int8.rs:226-230): the B tile is BN/2 rows of b (the gate
+// weights) over BN/2 rows of u (the up weights) for the same BN/2 output
+// columns; each wave's first NB/2 fragments are gate columns and the last NB/2
+// the up rows of the same columns, so the epilogue finds both dots of an
+// output in one lane: y = (g / (1 + exp(-g))) * up with g and up rescaled like
+// the plain output, exp the f32 rounding of the f64 exponential.
+template <int BM, int BN, int WM, int WN, bool Q4B, bool FUSED = false>
 __global__ __launch_bounds__(WM *WN * 64) void i8_gemm_kernel(const int8_t *__restrict__ a,
                                                               const float *__restrict__ sa, int m,
                                                               const int8_t *__restrict__ b,
                                                               const float *__restrict__ sb, int n,
                                                               int k, void *__restrict__ y,
-                                                              int raw) {
+                                                              int raw, const int8_t *__restrict__ u = nullptr,
+                                                              const float *__restrict__ su = nullptr) {
     constexpr int THREADS = WM * WN * 64;
     constexpr int TM = BM / WM, TN = BN / WN;
     constexpr int MB = TM / 16, NB = TN / 16;
+    static_assert(!FUSED || (NB % 2 == 0 && !Q4B), "fused tiles pair gate and up fragments");
+    constexpr int OUT_N = FUSED ? BN / 2 : BN;  // output columns per tile
     constexpr int ACH = BM * 4, BCH = BN * 4;
     constexpr int PA = (ACH + THREADS - 1) / THREADS, PB = (BCH + THREADS - 1) / THREADS;
     __shared__ __align__(16) uint8_t la[2][BM * 64];
@@ -772,7 +781,7 @@ __global__ __launch_bounds__(WM *WN * 64) void i8_gemm_kernel(const int8_t *__re
     const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
     const int wm = wave / WN, wn = wave % WN;
     const int qd = lane / 16, i = lane % 16;
-    const int row0 = blockIdx.y * BM, col0 = blockIdx.x * BN;
+    const int row0 = blockIdx.y * BM, col0 = blockIdx.x * OUT_N;
     const int steps = (k + 63) / 64;
 
     int4_t acc[MB][NB];
@@ -816,9 +825,15 @@ __global__ __launch_bounds__(WM *WN * 64) void i8_gemm_kernel(const int8_t *__re
 #pragma unroll
         for (int p = 0; p < PB; p++) {
             int idx = threadIdx.x + p * THREADS;
-            if (idx < BCH)
-                rb[p] = Q4B ? load_q4_chunk(col0 + idx / 4, step * 64 + (idx % 4) * 16)
-                            : load_chunk(b, n, col0 + idx / 4, step * 64 + (idx % 4) * 16);
+            if (idx < BCH) {
+                if (FUSED) {
+                    const int r = idx / 4;
+                    rb[p] = load_chunk(r < BN / 2 ? b : u, n, col0 + r % (BN / 2), step * 64 + (idx % 4) * 16);
+                } else {
+                    rb[p] = Q4B ? load_q4_chunk(col0 + idx / 4, step * 64 + (idx % 4) * 16)
+                                : load_chunk(b, n, col0 + idx / 4, step * 64 + (idx % 4) * 16);
+                }
+            }
         }
     };
     auto store = [&](int buf) {
@@ -849,7 +864,8 @@ __global__ __launch_bounds__(WM *WN * 64) void i8_gemm_kernel(const int8_t *__re
         int4_t bfrag[NB];
 #pragma unroll
         for (int z = 0; z < NB; z++) {
-            int r = wn * TN + z * 16 + i;
+            const int r = FUSED ? (z < NB / 2 ? 0 : BN / 2) + wn * (TN / 2) + (z % (NB / 2)) * 16 + i
+                                : wn * TN + z * 16 + i;
             bfrag[z] = *(const int4_t *)(lb[buf] + r * 64 + ((qd ^ ((r >> 2) & 3)) * 16));
         }
 #pragma unroll
@@ -861,6 +877,26 @@ __global__ __launch_bounds__(WM *WN * 64) void i8_gemm_kernel(const int8_t *__re
         }
         if (st + 1 < steps) store(buf ^ 1);
         __syncthreads();
+    }
+    if constexpr (FUSED) {
+#pragma unroll
+        for (int x = 0; x < MB; x++) {
+#pragma unroll
+            for (int z = 0; z < NB / 2; z++) {
+                const int col = col0 + wn * (TN / 2) + z * 16 + i;
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const int r = row0 + wm * TM + x * 16 + qd * 4 + v;
+                    if (r < m && col < n) {
+                        const float g = __fmul_rn(__fmul_rn((float)acc[x][z][v], sa[r]), sb[col]);
+                        const float up = __fmul_rn(__fmul_rn((float)acc[x][z + NB / 2][v], sa[r]), su[col]);
+                        const float e = __double2float_rn(exp(-(double)g));
+                        ((float *)y)[(size_t)r * n + col] = __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, e)), up);
+                    }
+                }
+            }
+        }
+        return;
     }
 #pragma unroll
     for (int x = 0; x < MB; x++) {
@@ -2469,6 +2505,13 @@ void launch_i8_gemm(const int8_t *a, const float *sa, int m, const int8_t *b, co
         i8_gemm_dispatch<true>(a, sa, m, b, sb, n, k, y, raw, variant, s);
     else
         i8_gemm_dispatch<false>(a, sa, m, b, sb, n, k, y, raw, variant, s);
+}
+
+void launch_i8_gemm_fused(const int8_t *a, const float *sa, int m, const int8_t *wg, const float *sg,
+                          const int8_t *wu, const float *su, int n, int k, float *y, hipStream_t s) {
+    if (m == 0 || n == 0) return;
+    hipLaunchKernelGGL((i8_gemm_kernel<128, 128, 2, 2, false, true>), dim3(cdiv(n, 64), cdiv(m, 128)), dim3(256), 0,
+                       s, a, sa, m, wg, sg, n, k, (void *)y, 0, wu, su);
 }
 
 int device_cus() {

@@ -779,6 +779,15 @@ int32_t dz_i8_gemm(dz_ctx *ctx, const int8_t *a, const float *sa, size_t m, cons
     return launched(ctx, "i8 gemm");
 }
 
+int32_t dz_i8_gemm_fused(dz_ctx *ctx, const int8_t *a, const float *sa, size_t m, const int8_t *wg,
+                         const float *sg, const int8_t *wu, const float *su, size_t n, size_t k, float *y) {
+    DZ_BEGIN(ctx);
+    if ((m && n) && (!a || !sa || !wg || !sg || !wu || !su || !y)) return fail(ctx, DZ_INVALID_REQUEST, "null pointer");
+    if (k == 0 || k > 32768) return fail(ctx, DZ_INVALID_PARAMETERS, "INT8 reduction must be 1..32768");
+    dz::launch_i8_gemm_fused(a, sa, (int)m, wg, sg, wu, su, (int)n, (int)k, y, ctx->stream);
+    return launched(ctx, "i8 gemm fused");
+}
+
 int32_t dz_q4_quantize_rows(dz_ctx *ctx, const void *values, int32_t dtype, size_t rows, size_t k,
                             uint32_t *out) {
     DZ_BEGIN(ctx);

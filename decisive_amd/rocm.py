@@ -88,6 +88,7 @@ _SIGNATURES = {
     "dz_linear_records": (I32, [P, P, P, SZ, P]),
     "dz_i8_quantize_rows": (I32, [P, P, SZ, SZ, P, P, P]),
     "dz_i8_gemm": (I32, [P, P, P, SZ, P, P, SZ, SZ, P, I32]),
+    "dz_i8_gemm_fused": (I32, [P, P, P, SZ, P, P, P, P, SZ, SZ, P]),
     "dz_q4_quantize_rows": (I32, [P, P, I32, SZ, SZ, P]),
     "dz_q4_rows_gemm": (I32, [P, P, P, SZ, P, SZ, SZ, P, I32]),
     "dz_layernorm": (I32, [P, P, P, I32, SZ, SZ, P, P, F]),
@@ -292,6 +293,12 @@ class Context:
     def i8_gemm(self, a, sa, m: int, w, sw, n: int, k: int, y, raw: bool):
         self._check(load().dz_i8_gemm(self.handle, _addr(a), _addr(sa), m, _addr(w), _addr(sw), n, k, _addr(y),
                                       1 if raw else 0))
+
+    def i8_gemm_fused(self, a, sa, m: int, wg, sg, wu, su, n: int, k: int, y):
+        """silu(gate) * up of two per-row int8 products of the same codes
+        (webgpu/int8.rs gemm(fused=true)); y f32 [m x n]."""
+        self._check(load().dz_i8_gemm_fused(self.handle, _addr(a), _addr(sa), m, _addr(wg), _addr(sg), _addr(wu),
+                                            _addr(su), n, k, _addr(y)))
 
     # ---- epilogues ----
     def q4_quantize_rows(self, values, dtype: int, rows: int, k: int, out):

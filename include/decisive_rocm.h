@@ -220,6 +220,14 @@ int32_t dz_i8_quantize_rows(dz_ctx *ctx, const float *x_dev, size_t rows, size_t
 int32_t dz_i8_gemm(dz_ctx *ctx, const int8_t *a_dev, const float *sa_dev, size_t m,
                    const int8_t *w_dev, const float *sw_dev, size_t n, size_t k, void *y_dev,
                    int32_t raw);
+/* webgpu/int8.rs:147-242 gemm(fused=true), epilogue :226-230: two per-row
+ * products of the same codes a, gate = (f32(a.wg)*sa)*sg and
+ * up = (f32(a.wu)*sa)*su, and y f32 [m x n] = (gate / (1 + exp(-gate))) * up.
+ * exp is the f32 rounding of the f64 exponential (the reference leaves its
+ * accuracy to the WGSL implementation). wg_dev, wu_dev int8 [n x k]. */
+int32_t dz_i8_gemm_fused(dz_ctx *ctx, const int8_t *a_dev, const float *sa_dev, size_t m,
+                         const int8_t *wg_dev, const float *sg_dev, const int8_t *wu_dev,
+                         const float *su_dev, size_t n, size_t k, float *y_dev);
 
 /* webgpu/q4.rs:48-73 quantize_q4 (the per-output-channel Q4 mode): per row
  * scale = absmax/7 (f32 division, no floor), code = clamp(rne(x/scale), +-7)

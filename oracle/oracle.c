@@ -609,6 +609,28 @@ void or_i8_gemm(const int8_t *qa, const float *sa, size_t m, const int8_t *qw, c
     free(ids);
 }
 
+/* webgpu/int8.rs:226-230, gemm(fused=true): gate and up are two rescaled
+ * per-row products of the same codes (the f32 epilogue above), and
+ * y = (gate / (1 + exp(-gate))) * up in f32 operations, exp being the f32
+ * rounding of the f64 exponential. */
+void or_i8_gemm_fused(const int8_t *qa, const float *sa, size_t m, const int8_t *qg, const float *sg,
+                      const int8_t *qu, const float *su, size_t n, size_t k, float *y) {
+    for (size_t r = 0; r < m; r++) {
+        const int8_t *a = qa + r * k;
+        for (size_t c = 0; c < n; c++) {
+            int32_t dg = 0, du = 0;
+            for (size_t i = 0; i < k; i++) {
+                dg += (int32_t)a[i] * (int32_t)qg[c * k + i];
+                du += (int32_t)a[i] * (int32_t)qu[c * k + i];
+            }
+            const float gate = ((float)dg * sa[r]) * sg[c];
+            const float up = ((float)du * sa[r]) * su[c];
+            const float e = (float)exp(-(double)gate);
+            y[r * n + c] = (gate / (1.0f + e)) * up;
+        }
+    }
+}
+
 /* ------------------------------------------------------------------------ */
 /* W4A16 closed form                                                         */
 /* ------------------------------------------------------------------------ */

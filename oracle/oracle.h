@@ -105,6 +105,8 @@ void or_q4_rows_codes(const uint32_t *words, size_t rows, size_t k, int8_t *code
 void or_i8_gemm(const int8_t *qa, const float *sa, size_t m, const int8_t *qw,
                 const float *sw, size_t n, size_t k, int threads, int32_t *raw,
                 float *y);
+void or_i8_gemm_fused(const int8_t *qa, const float *sa, size_t m, const int8_t *qg, const float *sg,
+                      const int8_t *qu, const float *su, size_t n, size_t k, float *y);
 
 /* ---- W4A16 closed form (no reference kernel; see D2) ----
  * y[m x n] = sum_k f16(x)[i,k] * w[j,k] in f64, w already dequantized f32. */

@@ -66,6 +66,7 @@ def _declare(L):
         "or_has_avx2": (I, []),
         "or_i8_quantize_rows": (None, [P, SZ, SZ, P, P, P]),
         "or_i8_gemm": (None, [P, P, SZ, P, P, SZ, SZ, I, P, P]),
+        "or_i8_gemm_fused": (None, [P, P, SZ, P, P, P, P, SZ, SZ, P]),
         "or_q4_quantize_rows": (I, [P, SZ, SZ, P]),
         "or_q4_rows_codes": (None, [P, SZ, SZ, P]),
         "or_w4a16": (None, [P, SZ, SZ, P, SZ, P]),
@@ -303,6 +304,14 @@ def i8_gemm(qa, sa, m, qw, sw, n, k, threads=1, raw=True, scaled=True):
                      _p(_c(sw, np.float32)), n, k, threads,
                      _p(r) if raw else None, _p(y) if scaled else None)
     return r, y
+
+
+def i8_gemm_fused(qa, sa, m, qg, sg, qu, su, n, k):
+    """or_i8_gemm_fused: webgpu/int8.rs:226-230 -> f32 [m, n] = silu(gate) * up."""
+    y = np.empty((m, n), np.float32)
+    lib().or_i8_gemm_fused(_p(_c(qa, np.int8)), _p(_c(sa, np.float32)), m, _p(_c(qg, np.int8)),
+                           _p(_c(sg, np.float32)), _p(_c(qu, np.int8)), _p(_c(su, np.float32)), n, k, _p(y))
+    return y
 
 
 def q4_quantize_rows(x_f16_bits, rows, k) -> np.ndarray:

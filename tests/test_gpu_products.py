@@ -556,6 +556,35 @@ def test_i8_gemm_exact(ctx, oracle, m, n, k):
     ctx.select_variant("i8_gemm", I8_VARIANTS[0])
 
 
+@pytest.mark.parametrize("m,n,k", [[1, 1, 4], [77, 45, 100], [130, 260, 4100], [256, 512, 4096], [513, 257, 80]])
+def test_i8_gemm_fused_silu(ctx, oracle, m, n, k):
+    """webgpu/int8.rs:226-230 fused mode against the oracle: bit for bit but
+    for the rare value where the device and host f64 exponentials round to
+    different f32 exp (then one ulp); and equal to silu applied to the two
+    plain products of the same codes."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(m + 7 * n + k)
+    qa, sa, _ = oracle.i8_quantize_rows(rng.standard_normal((m, k)).astype(np.float32), m, k)
+    qg, sg, _ = oracle.i8_quantize_rows(rng.standard_normal((n, k)).astype(np.float32), n, k)
+    qu, su, _ = oracle.i8_quantize_rows(rng.standard_normal((n, k)).astype(np.float32), n, k)
+    sa = (sa * np.float32(4.0 / np.sqrt(k))).astype(np.float32)  # gates of a few units
+    want = oracle.i8_gemm_fused(qa, sa, m, qg, sg, qu, su, n, k)
+    y = empty((m, n), torch.float32)
+    ctx.i8_gemm_fused(dev(qa), dev(sa), m, dev(qg), dev(sg), dev(qu), dev(su), n, k, y)
+    got = host(ctx, y)
+    ulps = np.abs(got.view(np.int32).astype(np.int64) - want.view(np.int32).astype(np.int64))
+    assert ulps.max() <= 1
+    assert np.count_nonzero(ulps) <= max(1, got.size // 10000)
+    gate = empty((m, n), torch.float32)
+    up = empty((m, n), torch.float32)
+    ctx.i8_gemm(dev(qa), dev(sa), m, dev(qg), dev(sg), n, k, gate, raw=False)
+    ctx.i8_gemm(dev(qa), dev(sa), m, dev(qu), dev(su), n, k, up, raw=False)
+    g, u = host(ctx, gate), host(ctx, up)
+    composed = ((g / (np.float32(1.0) + np.exp(-g.astype(np.float64)).astype(np.float32))) * u).astype(np.float32)
+    ulps = np.abs(got.view(np.int32).astype(np.int64) - composed.view(np.int32).astype(np.int64))
+    assert ulps.max() <= 1
+
+
 def test_config4_int8_full_size(ctx, oracle):
     """W f32 [4096 x 4096] N(0,0.02) per-channel, A f32
     [8192 x 4096] N(0,1) per-token; quantized on the GPU (bit-exact with the

@@ -276,6 +276,35 @@ def test_i8_quantizer_division_and_zero_rows(oracle):
     assert np.array_equal(y1, (r1.astype(np.float32) * s[:, None]).astype(np.float32) * s[None, :])
 
 
+def test_i8_gemm_fused_silu_epilogue(oracle):
+    """webgpu/int8.rs:226-230 fused mode: the gate and up products of the same
+    codes (each pinned above) feed (gate / (1 + exp(-gate))) * up; checked in
+    numpy f32 operations, against the f64 closed form, and at the extremes
+    (exp overflow gives a signed zero, a large gate passes gate * up)."""
+    rng = np.random.default_rng(11)
+    m, n, k = 13, 9, 200
+    qa, sa, _ = oracle.i8_quantize_rows(rng.standard_normal((m, k)).astype(np.float32), m, k)
+    qg, sg, _ = oracle.i8_quantize_rows(rng.standard_normal((n, k)).astype(np.float32), n, k)
+    qu, su, _ = oracle.i8_quantize_rows(rng.standard_normal((n, k)).astype(np.float32), n, k)
+    sa = sa * np.float32(4.0)  # gates of a few units, both signs
+    y = oracle.i8_gemm_fused(qa, sa, m, qg, sg, qu, su, n, k)
+    _, gate = oracle.i8_gemm(qa, sa, m, qg, sg, n, k)
+    _, up = oracle.i8_gemm(qa, sa, m, qu, su, n, k)
+    e = np.exp(-gate.astype(np.float64)).astype(np.float32)
+    want = ((gate / (np.float32(1.0) + e)).astype(np.float32) * up).astype(np.float32)
+    assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
+    g64 = gate.astype(np.float64)
+    closed = g64 / (1.0 + np.exp(-g64)) * up.astype(np.float64)
+    assert np.allclose(y, closed, rtol=1e-6, atol=1e-30)
+    assert np.abs(gate).max() > 4.0 and (gate < 0).any() and (gate > 0).any()
+    # extremes: one-element products with scales chosen to hit exp overflow
+    one = np.ones((1, 1), np.int8)
+    big = oracle.i8_gemm_fused(one, np.float32([1.0]), 1, one, np.float32([-200.0]), one, np.float32([3.0]), 1, 1)
+    assert big[0, 0] == 0.0 and np.signbit(big[0, 0])  # -200 / inf * 3 = -0
+    pos = oracle.i8_gemm_fused(one, np.float32([1.0]), 1, one, np.float32([200.0]), one, np.float32([3.0]), 1, 1)
+    assert pos[0, 0] == np.float32(600.0)
+
+
 # ---- g32/f16 layout (D1) --------------------------------------------------------
 
 def test_g32_f16_layout_invariants(oracle):
