@@ -541,6 +541,52 @@ def traffic_per_launch():
         return None
 
 
+def floors_line(torch, ctx, rocm, stream) -> dict:
+    """What a launch of the headline GEMV's size costs with no product in it,
+    over the same rotation of 96 copies as the headline, each a HIP graph of
+    one launch per copy: a one-element fill (the launch floor in a graph), a
+    device copy moving the GEMV's byte count (half read, half written) and the
+    GEMV itself."""
+    per_launch = gemv_bytes(M_ROWS, K_DIM, N_DIM)
+    bufs = [torch.empty(per_launch // 4, dtype=torch.float32, device="cuda").uniform_() for _ in range(WEIGHT_COPIES)]
+    halves = [torch.empty(per_launch // 8, dtype=torch.float32, device="cuda") for _ in range(WEIGHT_COPIES)]
+    tiny = torch.zeros(1, dtype=torch.float32, device="cuda")
+    x = torch.randn((M_ROWS, K_DIM), generator=torch.Generator(device="cuda").manual_seed(0), device="cuda").half()
+    weights = []
+    tmp = torch.empty((N_DIM, K_DIM), dtype=torch.float32, device="cuda")
+    for c in range(WEIGHT_COPIES):
+        tmp.normal_(0.0, 0.02, generator=torch.Generator(device="cuda").manual_seed(1 + c))
+        torch.cuda.synchronize()
+        weights.append(ctx.quantize(tmp, rocm.F32, N_DIM, K_DIM, 4, 32))
+    del tmp
+    y = torch.empty((WEIGHT_COPIES, M_ROWS, N_DIM), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+
+    def fills():
+        for c in range(WEIGHT_COPIES):
+            tiny.fill_(float(c + 1))
+
+    def copies():
+        for c in range(WEIGHT_COPIES):
+            halves[c].copy_(bufs[c][:per_launch // 8])
+
+    def gemvs():
+        for c in range(WEIGHT_COPIES):
+            ctx.linear(weights[c], x, rocm.F16, M_ROWS, y[c], rocm.W4A16)
+
+    out = {}
+    for name, fn in (("fill_1_element", fills), ("copy_same_bytes", copies), ("gemv_w4a16", gemvs)):
+        us = graph_ms(torch, stream, fn, WEIGHT_COPIES, reps=200) * 1e3
+        out[name] = {"us_per_launch": round(us, 3), "launch": "hip graph"}
+        if name != "fill_1_element":
+            out[name]["GB/s"] = round(per_launch / (us * 1e-6) / 1e9, 1)
+    assert torch.isfinite(y).all()
+    for wgt in weights:
+        wgt.free()
+    out["bytes_per_launch"] = per_launch
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -552,7 +598,7 @@ def main():
     ap.add_argument("--calibrate-copy", action="store_true",
                     help=f"also run a {COPY_BYTES >> 20} MiB device copy (counter calibration)")
     ap.add_argument("--tune", type=int, default=0, help="tuner budget in ms (0 keeps reference variants)")
-    ap.add_argument("--only", choices=["pplx", "tune"],
+    ap.add_argument("--only", choices=["pplx", "tune", "floors"],
                     help="run one secondary line alone and print it (for profiling)")
     ap.add_argument("--tune-cache", help="with --only tune: a selection JSON from an earlier run to reuse")
     ap.add_argument("--tune-out", help="with --only tune: write the selection JSON here")
@@ -577,6 +623,14 @@ def main():
     if args.tune:
         ctx.tune(args.tune)
     log(f"[bench] device {ctx.info()}")
+    if args.only == "floors":
+        stream = torch.cuda.Stream()
+        ctx.set_stream(stream.cuda_stream)
+        with torch.cuda.stream(stream):
+            line = floors_line(torch, ctx, rocm, stream)
+        ctx.set_stream(None)
+        print(json.dumps({"launch_floors_q4_gemv_size": line}), flush=True)
+        return
     if args.only == "pplx":
         stream = torch.cuda.Stream()
         ctx.set_stream(stream.cuda_stream)
