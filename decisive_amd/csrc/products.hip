@@ -1679,12 +1679,12 @@ __global__ __launch_bounds__(WGM *WGN * 64) void grouped_pipe_kernel(
     constexpr int CSTAGE = TILES * (BITS == 4 ? 1024 : 2048);
     constexpr int SWSTAGE = TILES * 128;
     constexpr int SXSTAGE = BM * 8;
-    constexpr int XPW = BM / 8 / WAVES;          // 8-row activation loads per wave
-    constexpr int CPW = CSTAGE / 1024 / WAVES;   // code-chunk loads per wave
-    static_assert(XPW * 8 * WAVES == BM && XPW % 2 == 0, "activation rows split evenly, even count per wave");
-    static_assert(CPW * 1024 * WAVES == CSTAGE && CPW >= 1, "code chunks split evenly");
+    // 1 KiB loads of a stage, dealt round robin to the waves: XI of 8
+    // activation rows, CI code chunks, SI of 64 activation-scale pairs
+    constexpr int XI = BM / 8, CI = CSTAGE / 1024, SI = BM / 32;
+    constexpr int XPW = (XI + WAVES - 1) / WAVES, CPW = (CI + WAVES - 1) / WAVES, SPW = (SI + WAVES - 1) / WAVES;
+    static_assert(BM % 32 == 0 && XI * 8 == BM && SI * 32 == BM, "whole 1 KiB activation and 256 B scale loads");
     static_assert(TILES == 8, "one 1 KiB weight-scale load per stage");
-    static_assert(BM * 2 == WAVES * 64, "one 4-byte activation-scale load per wave");
     __shared__ __align__(16) uint8_t xs[2 * XSTAGE];
     __shared__ __align__(16) uint8_t cs[2 * CSTAGE];
     __shared__ __align__(16) uint8_t sws[2 * SWSTAGE];
@@ -1721,27 +1721,32 @@ __global__ __launch_bounds__(WGM *WGN * 64) void grouped_pipe_kernel(
         const int32x4_t ns = live ? rs : int32x4_t{rs[0], rs[1], 0, rs[3]};
 #pragma unroll
         for (int p = 0; p < XPW; p++) {
-            const int blk = wave * XPW + p;
-            dma16(__builtin_amdgcn_readfirstlane(xs_lds + stage * XSTAGE + blk * 1024),
-                  xoff[p & 1] + (uint32_t)(blk * 8) * rowbytes + (uint32_t)st * 128, nq);
+            const int blk = wave + p * WAVES;
+            if (XI % WAVES == 0 || blk < XI)
+                dma16(__builtin_amdgcn_readfirstlane(xs_lds + stage * XSTAGE + blk * 1024),
+                      xoff[blk & 1] + (uint32_t)(blk * 8) * rowbytes + (uint32_t)st * 128, nq);
         }
 #pragma unroll
         for (int p = 0; p < CPW; p++) {
-            const int ci = wave * CPW + p;  // Q4: tile; Q8: tile * 2 + group of the step
+            const int ci = wave + p * WAVES;  // Q4: tile; Q8: tile * 2 + group of the step
             const int t = BITS == 4 ? ci : ci / 2;
             const int kc = BITS == 4 ? st : 2 * st + ci % 2;
-            dma16(__builtin_amdgcn_readfirstlane(cs_lds + stage * CSTAGE + ci * 1024),
-                  (uint32_t)((t * kbs + kc) * 1024 + lane * 16), nc);
+            if (CI % WAVES == 0 || ci < CI)
+                dma16(__builtin_amdgcn_readfirstlane(cs_lds + stage * CSTAGE + ci * 1024),
+                      (uint32_t)((t * kbs + kc) * 1024 + lane * 16), nc);
         }
-        if (wave == 0) {
+        if (wave == WAVES - 1) {
             const int t = lane / 8;
             const uint32_t off = BITS == 4 ? (uint32_t)(t * kbs + st) * 128 : (uint32_t)(t * groups + 2 * st) * 64;
             dma16(__builtin_amdgcn_readfirstlane(sws_lds + stage * SWSTAGE), off + (uint32_t)(lane % 8) * 16, nw);
         }
-        {
-            const int r = wave * 32 + lane / 2;
-            dma4(__builtin_amdgcn_readfirstlane(sxs_lds + stage * SXSTAGE + wave * 256),
-                 (uint32_t)((r * groups + 2 * st + (lane & 1)) * 4), ns);
+#pragma unroll
+        for (int p = 0; p < SPW; p++) {
+            const int si = wave + p * WAVES;
+            const int r = si * 32 + lane / 2;
+            if (SI % WAVES == 0 || si < SI)
+                dma4(__builtin_amdgcn_readfirstlane(sxs_lds + stage * SXSTAGE + si * 256),
+                     (uint32_t)((r * groups + 2 * st + (lane & 1)) * 4), ns);
         }
     };
 
@@ -2056,7 +2061,8 @@ const char *const kI8Names[] = {"256x256p2w8", "256x256p4k64w8", "256x128p3w8", 
                                  "128x128w2x2", "256x128w2x2", "64x64w2x2", "256x256p2w8-stream",
                                  "256x256p2w8-stream-mid", "256x128k64p2-stream2"};
 const char *const kGroupedNames[] = {"pipe-auto",    "pipe256x128w8", "wave16x16",   "pipe128x128w4",
-                                     "pipe64x128w2", "pipe128x128m8", "pipe128x128n8"};
+                                     "pipe64x128w2", "pipe128x128m8", "pipe128x128n8", "pipe32x128w8",
+                                     "pipe64x128w8"};
 const char *const kMlpNames[] = {"pipe-auto", "pipe256x64w8", "pipe128x64w4", "wave16x64", "pipe256x64n2", "pipe128x64n2"};
 const char *const kDeltaNames[] = {"auto", "recurrent", "chunked64"};
 const char *const kNormNames[] = {"fused", "separate"};
@@ -2235,7 +2241,7 @@ int variant_count(const char *family) {
     if (f == "gemv") return 2;
     if (f == "gemm_w4a16") return 8;
     if (f == "i8_gemm") return 10;
-    if (f == "grouped") return 7;
+    if (f == "grouped") return 9;
     if (f == "mlp") return 6;
     if (f == "delta_scan") return 3;
     if (f == "norm") return 2;
@@ -2311,21 +2317,23 @@ bool grouped_pipe_launch(const Weight &w, const int8_t *q, const float *sx, int 
 
 // Variants: 1 pipelined 256x128 tiles (8 waves), 3 128x128 (4 waves as 2x2),
 // 5 128x128 (4 waves side by side, each 128 rows x 32 columns), 6 128x128 (4
-// waves stacked, each 32 rows x 128 columns), 4 64x128 (2 waves), 2 one wave
-// per 16x16 tile. 0 picks 128x128 tiles when their grid covers half the compute
-// units, else 64x128 tiles when that grid covers a quarter, else the one-wave
-// tiles (measured: 128x128 beats 256x128 by 5-15% at every shape from
-// 229x2560x12288 to 16384x4096x14336, and 64x128 wins below the half-wave
-// mark). Among the 128x128 layouts, the side-by-side one unpacks each weight
-// fragment once for 8 row blocks instead of 4; it is 4-11% faster from 4096
-// rows up and 1-3% slower at 1024, so 0 takes it from 2048 rows. Every variant
-// folds in group order: all are bitwise equal.
+// waves stacked, each 32 rows x 128 columns), 4 64x128 (2 waves), 7 32x128 (8
+// waves side by side, each 32 rows x 16 columns), 8 64x128 (8 waves as 2x4), 2
+// one wave per 16x16 tile. The fold is VALU work, so what decides is how many
+// waves keep every SIMD busy: 0 picks the side-by-side 128x128 tiles when
+// their grid gives every compute unit two blocks, else 64x128 on 8 waves when
+// that grid does, else 32x128 on 8 waves. Measured (us, 1024 rows unless
+// stated, 32x128w8 / 64x128w8 / 128x128 side by side): N=1024 K=2560 22 / 28
+// / 52; N=2560 K=9216 107 / 112 / 165; N=4096 K=2560 43 / 42 / 55; N=8192
+// K=2560 76 / 72 / 71; 4096 rows, N=8192: 271 / 238 / 218; 40 rows, N=8192:
+// 18 / 24 / 47 (the one-wave tiles 27). Every variant folds in group order:
+// all are bitwise equal.
 int grouped_pick(const Weight &w, int m, int variant) {
     if (variant != 0) return variant;
     const unsigned cus = (unsigned)device_cus(), tn = cdiv(w.rows, 128);
-    if (cdiv(m, 128) * tn >= cus / 2) return m >= 2048 ? 5 : 3;
-    if (cdiv(m, 64) * tn >= cus / 4) return 4;
-    return 2;
+    if (cdiv(m, 128) * tn >= 2 * cus) return 5;
+    if (cdiv(m, 64) * tn >= 2 * cus) return 8;
+    return 7;
 }
 
 // Activation rows per block of a pipelined pick (0: not a pipelined kernel).
@@ -2333,7 +2341,8 @@ int grouped_pipe_rows(int pick) {
     switch (pick) {
         case 1: return 256;
         case 3: case 5: case 6: return 128;
-        case 4: return 64;
+        case 4: case 8: return 64;
+        case 7: return 32;
         default: return 0;
     }
 }
@@ -2353,6 +2362,8 @@ bool launch_grouped(const Weight &w, const int8_t *q, const float *sx, int m, fl
         case 4: if (grouped_pipe_launch<64, 1, 2>(w, q, sx, m, y, bad, s, res)) return true; break;
         case 5: if (grouped_pipe_launch<128, 1, 4>(w, q, sx, m, y, bad, s, res)) return true; break;
         case 6: if (grouped_pipe_launch<128, 4, 1>(w, q, sx, m, y, bad, s, res)) return true; break;
+        case 7: if (grouped_pipe_launch<32, 1, 8>(w, q, sx, m, y, bad, s, res)) return true; break;
+        case 8: if (grouped_pipe_launch<64, 2, 4>(w, q, sx, m, y, bad, s, res)) return true; break;
         default: break;
     }
     if (res) return false;  // only the pipelined kernels add a residual
