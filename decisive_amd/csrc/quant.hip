@@ -290,70 +290,148 @@ __global__ void act_quantize_kernel(const float *__restrict__ x, int m, int k, i
 
 // ---- zero-centred RMSNorm fused with the A8 quantizer -------------------------------
 //
-// One block per row of d floats (d % 64 == 0). The row's squares are summed in
-// row order by one lane, as pplx_flash/cpu.rs:310-333 does (the readout norm's
-// arithmetic, bit for bit); the lane's LDS reads run 32 squares ahead of its
-// adds, so the chain of d dependent adds is the only wait. Then every wave
-// takes 64-column groups: v = (x * scale) * (1 + w) (w when not zero-centred),
-// written to y when y is set, and the group's A8 codes and scale exactly as
-// act_quantize_kernel computes them from v (int8.rs:178-202), so a product of
-// these codes equals the product of y. A non-finite v sets *bad.
-__global__ __launch_bounds__(256) void rms_quantize_kernel(const float *__restrict__ h, int d,
-                                                           const float *__restrict__ w, float eps, int zero_centered,
-                                                           float *__restrict__ y, int8_t *__restrict__ q,
-                                                           float *__restrict__ sc, int *bad) {
-    extern __shared__ __align__(16) float lds_f[];
-    float *xs = lds_f, *sq = lds_f + d;
-    __shared__ float scale_sh;
-    const size_t row = blockIdx.x, base = row * (size_t)d;
-    for (int i = threadIdx.x * 4; i < d; i += 1024) {
-        const float4_t v = *(const float4_t *)(h + base + i);
-        *(float4_t *)(xs + i) = v;
-        *(float4_t *)(sq + i) = float4_t{__fmul_rn(v[0], v[0]), __fmul_rn(v[1], v[1]), __fmul_rn(v[2], v[2]),
-                                         __fmul_rn(v[3], v[3])};
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        // ping-pong buffers of 32 squares: the adds of one wait only for its own reads
-        const float4_t *p4 = (const float4_t *)sq;
-        const int n4 = d / 4;  // a multiple of 16
-        float4_t a[8], b[8];
-        float ss = 0.0f;
+// Rows of d floats (d % 64 == 0), in two launches:
+//  1. rms_row_scale_kernel: lane l of wave 0 owns row 16 * block + l % 16
+//     and adds the row's squares in row order, as pplx_flash/cpu.rs:310-333
+//     does (the readout norm's arithmetic, bit for bit). Wave 1 streams
+//     64-column tiles of the block's 16 rows into 16 LDS stages by
+//     buffer_load ... lds, 14 tiles ahead, and squares each tile in place one
+//     tile ahead of wave 0, so wave 0's chain of d dependent adds is all it
+//     waits for. A tile row's 16-byte chunk c sits at slot c ^ row, so the 16
+//     rows' reads of one chunk index hit distinct banks. The row scale
+//     1 / sqrt(ss / d + eps) goes to sc[row * groups], the first of the row's
+//     group-scale slots.
+//  2. rms_apply_quantize_kernel: one block per row takes that scale, then every
+//     wave takes 64-column groups: v = (x * scale) * (1 + w) (w when not
+//     zero-centred), written to y when y is set, and the group's A8 codes and
+//     scale exactly as act_quantize_kernel computes them from v
+//     (int8.rs:178-202), so a product of these codes equals the product of y.
+//     A non-finite v sets *bad.
+constexpr int kRmsRows = 16;    // rows (chains) per block
+constexpr int kRmsStages = 16;  // 64-column tiles in LDS
+
+__global__ __launch_bounds__(128) void rms_row_scale_kernel(const float *__restrict__ h, int rows, int d, float eps,
+                                                            float *__restrict__ sc) {
+    __shared__ __align__(16) float stages[kRmsStages][kRmsRows * 64];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), lane = threadIdx.x % 64;
+    const int row0 = blockIdx.x * kRmsRows;
+    const int nrows = min(kRmsRows, rows - row0), tiles = d / 64;
+    constexpr int PER_TILE = kRmsRows / 4;  // DMA instructions per tile
+    static_assert((kRmsStages - 2) * PER_TILE <= 63, "vmcnt range");
+    if (wave == 1) {
+        const int32x4_t rs = buffer_rsrc(h + (size_t)row0 * d, (uint32_t)(nrows * d * 4));
+        const uint32_t base = lds_address(&stages[0][0]);
+        // DMA instruction i of a tile fills rows 4i..4i+3: lane j -> row 4i + j / 16,
+        // slot j % 16, which holds the row's chunk (j % 16) ^ row
+        auto dma_tile = [&](int t) {
+            const int slot = t % kRmsStages;
 #pragma unroll
-        for (int j = 0; j < 8; j++) a[j] = p4[j];
-        for (int i = 0; i < n4; i += 16) {
-#pragma unroll
-            for (int j = 0; j < 8; j++) b[j] = p4[i + 8 + j];
-#pragma unroll
-            for (int j = 0; j < 8; j++)
-#pragma unroll
-                for (int e = 0; e < 4; e++) ss = __fadd_rn(ss, a[j][e]);
-            if (i + 16 < n4) {
-#pragma unroll
-                for (int j = 0; j < 8; j++) a[j] = p4[i + 16 + j];
+            for (int i = 0; i < PER_TILE; i++) {
+                const int r = 4 * i + lane / 16, c = (lane % 16) ^ r;
+                dma16(base + (uint32_t)(slot * kRmsRows * 64 * 4 + i * 1024),
+                      (uint32_t)((r * d + t * 64 + 4 * c) * 4), rs);
             }
+        };
+        auto square_tile = [&](int t) {
+            float4_t *p = (float4_t *)stages[t % kRmsStages];
+            float4_t v[4];
 #pragma unroll
-            for (int j = 0; j < 8; j++)
+            for (int i = 0; i < 4; i++) v[i] = p[lane + 64 * i];
 #pragma unroll
-                for (int e = 0; e < 4; e++) ss = __fadd_rn(ss, b[j][e]);
+            for (int i = 0; i < 4; i++)
+                p[lane + 64 * i] = float4_t{__fmul_rn(v[i][0], v[i][0]), __fmul_rn(v[i][1], v[i][1]),
+                                            __fmul_rn(v[i][2], v[i][2]), __fmul_rn(v[i][3], v[i][3])};
+        };
+#pragma unroll
+        for (int t = 0; t < kRmsStages - 1; t++)
+            if (t < tiles) dma_tile(t);
+        if (kRmsStages - 2 < tiles)
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"((kRmsStages - 2) * PER_TILE) : "memory");
+        else
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        square_tile(0);
+        __syncthreads();
+        for (int t = 0; t < tiles; t++) {
+            if (t + 1 < tiles) {
+                // tile t + 1 landed (tiles up to t + NS - 2 are issued)
+                if (t + kRmsStages - 2 < tiles)
+                    asm volatile("s_waitcnt vmcnt(%0)" ::"n"((kRmsStages - 3) * PER_TILE) : "memory");
+                else
+                    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                square_tile(t + 1);
+                // wave 0 read tile t - 1 before the last barrier
+                if (t + kRmsStages - 1 < tiles) dma_tile(t + kRmsStages - 1);
+            }
+            __syncthreads();
         }
-        // the square root taken in f64 and rounded once (v_sqrt_f32 is not correctly rounded)
-        const float t = __fadd_rn(__fdiv_rn(ss, (float)d), eps);
-        scale_sh = __fdiv_rn(1.0f, __double2float_rn(__dsqrt_rn((double)t)));
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no LDS write in flight once the block ends
+        return;
     }
-    __syncthreads();
-    const float scale = scale_sh;
-    const int wave = threadIdx.x / 64, lane = threadIdx.x % 64, groups = d / 64;
-    for (int g = wave; g < groups; g += 4) {
-        const int col = g * 64 + lane;
-        const float gain = zero_centered ? __fadd_rn(1.0f, w[col]) : w[col];
-        const float v = __fmul_rn(__fmul_rn(xs[col], scale), gain);
-        if (y) y[base + col] = v;
-        if (!__builtin_isfinite(v) && bad) atomicOr(bad, 1);
-        const float maximum = wave_max_dpp(fabsf(v));
-        const float s = fmaxf(__fdiv_rn(maximum, 127.0f), FLT_MIN);
-        q[(row * groups + g) * 64 + lane] = (int8_t)quantize_code(v, __frcp_rn(s), 127.0f);
-        if (lane == 0) sc[row * groups + g] = s;
+    const int r = lane % kRmsRows;
+    auto read_half = [&](int t, int half, float4_t *v) {
+        const float *row = &stages[t % kRmsStages][r * 64];
+#pragma unroll
+        for (int c = 0; c < 8; c++) v[c] = *(const float4_t *)(row + 4 * ((8 * half + c) ^ r));
+    };
+    float ss = 0.0f;
+    auto add_half = [&](const float4_t *v) {
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int c = 0; c < 8; c++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) ss = __fadd_rn(ss, v[c][e]);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    float4_t x0[8], x1[8];
+    __syncthreads();  // tile 0 squared
+    for (int t = 0; t < tiles; t++) {
+        read_half(t, 0, x0);
+        read_half(t, 1, x1);
+        add_half(x0);
+        add_half(x1);
+        __syncthreads();  // tile t read; tile t + 1 squared
+    }
+    if (lane < nrows) {
+        // the square root taken in f64 and rounded once (v_sqrt_f32 is not correctly rounded)
+        const float q = __fadd_rn(__fdiv_rn(ss, (float)d), eps);
+        sc[(size_t)(row0 + lane) * (d / 64)] = __fdiv_rn(1.0f, __double2float_rn(__dsqrt_rn((double)q)));
+    }
+}
+
+__global__ __launch_bounds__(256) void rms_apply_quantize_kernel(const float *__restrict__ h, int d,
+                                                                 const float *__restrict__ w, int zero_centered,
+                                                                 float *__restrict__ y, int8_t *__restrict__ q,
+                                                                 float *__restrict__ sc, int *bad) {
+    const size_t row = blockIdx.x, base = row * (size_t)d;
+    const int groups = d / 64;
+    const float scale = sc[row * groups];
+    __syncthreads();  // every wave has the row scale before group 0's scale replaces it
+    const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    // a wave's groups g = wave + 4j in batches of 8, every load of a batch in
+    // flight before the first group is computed
+    constexpr int BATCH = 8;
+    for (int g0 = wave; g0 < groups; g0 += 4 * BATCH) {
+        float xv[BATCH], wv[BATCH];
+#pragma unroll
+        for (int j = 0; j < BATCH; j++) {
+            const int g = g0 + 4 * j;
+            xv[j] = g < groups ? h[base + g * 64 + lane] : 0.0f;
+            wv[j] = g < groups ? w[g * 64 + lane] : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < BATCH; j++) {
+            const int g = g0 + 4 * j;
+            if (g >= groups) break;
+            const int col = g * 64 + lane;
+            const float gain = zero_centered ? __fadd_rn(1.0f, wv[j]) : wv[j];
+            const float v = __fmul_rn(__fmul_rn(xv[j], scale), gain);
+            if (y) y[base + col] = v;
+            if (!__builtin_isfinite(v) && bad) atomicOr(bad, 1);
+            const float maximum = wave_max_dpp(fabsf(v));
+            const float s = fmaxf(__fdiv_rn(maximum, 127.0f), FLT_MIN);
+            q[(row * groups + g) * 64 + lane] = (int8_t)quantize_code(v, __frcp_rn(s), 127.0f);
+            if (lane == 0) sc[row * groups + g] = s;
+        }
     }
 }
 
@@ -531,8 +609,9 @@ void launch_act_quantize_records(const float *x, int m, int k, uint32_t *records
 void launch_rms_quantize(const float *h, int rows, int d, const float *w, float eps, int zero_centered, float *y,
                          int8_t *q, float *sc, int *bad, hipStream_t s) {
     if (!rows) return;
-    hipLaunchKernelGGL(rms_quantize_kernel, dim3(rows), dim3(256), (size_t)2 * d * sizeof(float), s, h, d, w, eps,
-                       zero_centered, y, q, sc, bad);
+    hipLaunchKernelGGL(rms_row_scale_kernel, dim3((unsigned)((rows + kRmsRows - 1) / kRmsRows)), dim3(128), 0, s, h,
+                       rows, d, eps, sc);
+    hipLaunchKernelGGL(rms_apply_quantize_kernel, dim3(rows), dim3(256), 0, s, h, d, w, zero_centered, y, q, sc, bad);
 }
 
 void launch_i8_quantize_rows(const float *x, int rows, int k, int8_t *q, float *scales,
