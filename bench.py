@@ -284,6 +284,23 @@ def w4a8_line(torch, ctx, rocm, stream) -> dict:
             "note": "one launch per product: activation quantization inside the grouped kernel (hip graph)"}
 
 
+def encoder_line(torch, ctx, rocm, stream) -> dict:
+    """Config 3: the encoder forward, 24 x (1024, 16x64, 4096), batch 8 x 1024
+    tokens, random Q4 g32 weights."""
+    cfg = rocm.EncoderConfig(layers=24, hidden=1024, heads=16, head_dim=64, ffn=4096, vocab=32000, ln_eps=1e-5)
+    enc = ctx.encoder_random(cfg, 1)
+    ids = torch.from_numpy(np.random.default_rng(1).integers(0, 32000, 8 * 1024).astype(np.int32)).cuda()
+    emb = torch.empty((8, 1024), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    warm(torch, lambda r: enc.forward(ids, 8, 1024, emb))
+    ms = timed_ms(torch, stream, lambda r: enc.forward(ids, 8, 1024, emb), 5)
+    flops = 2 * 8192 * (4 * 1024 * 1024 + 2 * 1024 * 4096) * 24 + 4 * 8 * 16 * 1024 * 1024 * 64 * 24
+    enc.close()
+    return {"ms": round(ms, 3), "embeddings/s": round(8 / (ms * 1e-3), 1),
+            "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1),
+            "frac_of_f16_peak": round(flops / (ms * 1e-3) / 1e12 / F16_PEAK_TFLOPS, 4)}
+
+
 def secondary(torch, ctx, rocm, stream, cpu=True) -> dict:
     out = {}
     # config 4: int8 GEMM M=8192 K=N=4096
@@ -378,19 +395,7 @@ def secondary(torch, ctx, rocm, stream, cpu=True) -> dict:
         "note": "includes the A8 quantization of the f32 activations; VALU-bound fold (3 ops per output per group)"}
     w.free()
     del x, y
-    # config 3: encoder forward, 24 x (1024, 16x64, 4096), batch 8 x 1024 tokens
-    cfg = rocm.EncoderConfig(layers=24, hidden=1024, heads=16, head_dim=64, ffn=4096, vocab=32000, ln_eps=1e-5)
-    enc = ctx.encoder_random(cfg, 1)
-    ids = torch.from_numpy(np.random.default_rng(1).integers(0, 32000, 8 * 1024).astype(np.int32)).cuda()
-    emb = torch.empty((8, 1024), dtype=torch.float32, device="cuda")
-    torch.cuda.synchronize()
-    warm(torch, lambda r: enc.forward(ids, 8, 1024, emb))
-    ms = timed_ms(torch, stream, lambda r: enc.forward(ids, 8, 1024, emb), 5)
-    flops = 2 * 8192 * (4 * 1024 * 1024 + 2 * 1024 * 4096) * 24 + 4 * 8 * 16 * 1024 * 1024 * 64 * 24
-    out["encoder_forward_b8_s1024"] = {"ms": round(ms, 3), "embeddings/s": round(8 / (ms * 1e-3), 1),
-                                       "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1),
-                                       "frac_of_f16_peak": round(flops / (ms * 1e-3) / 1e12 / F16_PEAK_TFLOPS, 4)}
-    enc.close()
+    out["encoder_forward_b8_s1024"] = encoder_line(torch, ctx, rocm, stream)
     if cpu:
         out["encoder_forward_b8_s1024"]["cpu_baseline"] = encoder_cpu_baseline()
     # the Pplx decider at real size, one 1024-token chunk
@@ -598,7 +603,7 @@ def main():
     ap.add_argument("--calibrate-copy", action="store_true",
                     help=f"also run a {COPY_BYTES >> 20} MiB device copy (counter calibration)")
     ap.add_argument("--tune", type=int, default=0, help="tuner budget in ms (0 keeps reference variants)")
-    ap.add_argument("--only", choices=["pplx", "tune", "floors"],
+    ap.add_argument("--only", choices=["pplx", "tune", "floors", "encoder"],
                     help="run one secondary line alone and print it (for profiling)")
     ap.add_argument("--tune-cache", help="with --only tune: a selection JSON from an earlier run to reuse")
     ap.add_argument("--tune-out", help="with --only tune: write the selection JSON here")
@@ -631,13 +636,16 @@ def main():
         ctx.set_stream(None)
         print(json.dumps({"launch_floors_q4_gemv_size": line}), flush=True)
         return
-    if args.only == "pplx":
+    if args.only in ("pplx", "encoder"):
         stream = torch.cuda.Stream()
         ctx.set_stream(stream.cuda_stream)
         with torch.cuda.stream(stream):
-            line = pplx_line(torch, ctx, rocm, stream)
+            if args.only == "pplx":
+                line = {"pplx_decider_forward_s1024": pplx_line(torch, ctx, rocm, stream)}
+            else:
+                line = {"encoder_forward_b8_s1024": encoder_line(torch, ctx, rocm, stream)}
         ctx.set_stream(None)
-        print(json.dumps({"pplx_decider_forward_s1024": line}), flush=True)
+        print(json.dumps(line), flush=True)
         return
 
     if args.calibrate_copy:

@@ -354,6 +354,7 @@ constexpr int kAttnQueries = kAttnWaves * kAttnQB * 16;  // per block
 constexpr int kAttnKeys = 64;                             // per step
 
 typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef float float8_t __attribute__((ext_vector_type(8)));
 
 __global__ __launch_bounds__(kAttnWaves * 64, 4) void attention_kernel(const half_t *__restrict__ qkv,
                                                                     half_t *__restrict__ out, int seq,
@@ -400,12 +401,18 @@ __global__ __launch_bounds__(kAttnWaves * 64, 4) void attention_kernel(const hal
     };
 
     const float4_t fz = {0.f, 0.f, 0.f, 0.f};
+    // the softmax denominators come from the MFMA pipe: an all-ones V^T operand
+    // makes every row of lacc the running sum of the f16 P values of query j,
+    // the same values the numerator O^T accumulates
+    const half8_t ones = {(half_t)1.0f, (half_t)1.0f, (half_t)1.0f, (half_t)1.0f,
+                          (half_t)1.0f, (half_t)1.0f, (half_t)1.0f, (half_t)1.0f};
     float4_t o[kAttnQB][4];  // O^T[dh 16db + 4q4 + v][query j]
-    float mrow[kAttnQB], lsum[kAttnQB];
+    float4_t lacc[kAttnQB];  // every component: sum of P over keys, query j
+    float mrow[kAttnQB];
 #pragma unroll
     for (int qb = 0; qb < kAttnQB; qb++) {
         mrow[qb] = -INFINITY;
-        lsum[qb] = 0.0f;
+        lacc[qb] = fz;
 #pragma unroll
         for (int db = 0; db < 4; db++) o[qb][db] = fz;
     }
@@ -462,21 +469,23 @@ __global__ __launch_bounds__(kAttnWaves * 64, 4) void attention_kernel(const hal
             // (skipping a multiply by exactly 1 changes nothing)
             if (__builtin_amdgcn_ballot_w64(mnew != mrow[qb])) {
                 const float alpha = __builtin_amdgcn_exp2f((mrow[qb] - mnew) * scale_log2);
-                lsum[qb] *= alpha;
+#pragma unroll
+                for (int v = 0; v < 4; v++) lacc[qb][v] *= alpha;
 #pragma unroll
                 for (int db = 0; db < 4; db++)
 #pragma unroll
                     for (int v = 0; v < 4; v++) o[qb][db][v] *= alpha;
             }
             mrow[qb] = mnew;
+            // P^T of the two 32-key blocks, converted two values per instruction
 #pragma unroll
-            for (int kb = 0; kb < 4; kb++)
+            for (int c = 0; c < 2; c++) {
+                float8_t e;
 #pragma unroll
-                for (int v = 0; v < 4; v++) {
-                    const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[qb][kb][v], scale_log2, moff));
-                    lsum[qb] += e;
-                    pf[qb][kb / 2][(kb % 2) * 4 + v] = (half_t)e;
-                }
+                for (int i = 0; i < 8; i++)
+                    e[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[qb][2 * c + i / 4][i % 4], scale_log2, moff));
+                pf[qb][c] = __builtin_convertvector(e, half8_t);
+            }
         }
         // O^T += V^T P^T over the two 32-key blocks; the V^T operand (8 keys
         // of dh 16db + j) is read just before the MFMAs that use it
@@ -498,6 +507,10 @@ __global__ __launch_bounds__(kAttnWaves * 64, 4) void attention_kernel(const hal
 #pragma unroll
                 for (int qb = 0; qb < kAttnQB; qb++) o[qb][db] = mfma_f16(vf, pf[qb][c], o[qb][db]);
             }
+#pragma unroll
+        for (int c = 0; c < 2; c++)
+#pragma unroll
+            for (int qb = 0; qb < kAttnQB; qb++) lacc[qb] = mfma_f16(ones, pf[qb][c], lacc[qb]);
     };
     load_step(0, 0);
     const int full = seq / kAttnKeys;  // steps with 64 live keys
@@ -507,9 +520,7 @@ __global__ __launch_bounds__(kAttnWaves * 64, 4) void attention_kernel(const hal
     __builtin_amdgcn_s_waitcnt(0x0F70);  // no LDS write in flight once the block ends
 #pragma unroll
     for (int qb = 0; qb < kAttnQB; qb++) {
-        float l = lsum[qb];
-        l += __shfl_xor(l, 16);
-        l += __shfl_xor(l, 32);
+        const float l = lacc[qb][0];
         const int query = q0 + qb * 16 + j;
         if (query >= seq) continue;
         const float inv = 1.0f / l;
