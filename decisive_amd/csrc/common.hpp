@@ -156,6 +156,14 @@ __device__ __forceinline__ float wave_max_dpp(float v) {
     return fmaxf(a, b);
 }
 
+// The grouped activation quantizer's code (int8.rs:178-202): rint(v * (1/scale))
+// clamped to +-limit, with the correctly rounded reciprocal passed in.
+__device__ __forceinline__ int quantize_code(float v, float inverse, float limit) {
+    float r = __builtin_rintf(__fmul_rn(v, inverse));
+    r = fminf(fmaxf(r, -limit), limit);
+    return (int)r;
+}
+
 // erf(x) by Abramowitz & Stegun, Handbook of Mathematical Functions (1964),
 // formula 7.1.26: erf(x) = 1 - (a1 t + a2 t^2 + a3 t^3 + a4 t^4 + a5 t^5) e^(-x^2)
 // with t = 1 / (1 + p x) for x >= 0, |error| <= 1.5e-7, odd extension for x < 0.

@@ -19,6 +19,7 @@
 // Those are tolerance-checked against the oracle's restatement; the
 // reference's own orders (sequential sums, unfused products) are kept where
 // they cost nothing.
+#include <float.h>
 #include <string.h>
 
 #include <algorithm>
@@ -488,18 +489,37 @@ __global__ __launch_bounds__(256) void delta_chunk_scan_kernel(const float *__re
     }
 }
 
-// ctx[t][h*ld + i] = ((src*s)*norm[i])*silu(z), s = 1/sqrt(mean(src^2) + 1e-6)
+// ctx[t][h*ld + i] = ((src*s)*norm[i])*silu(z), s = 1/sqrt(mean(src^2) + 1e-6).
+// CODES: instead of ctx, the A8 codes and scales of its two 64-groups per head
+// (the activation quantizer's arithmetic, int8.rs:178-202, so they equal
+// act_quantize of ctx word for word), with *bad raised on a non-finite value.
+template <bool CODES>
 __global__ __launch_bounds__(64) void delta_gate_kernel(const float *__restrict__ heads, int n, int lh,
                                                         const float *__restrict__ norm,
-                                                        const float *__restrict__ z, float *__restrict__ ctx) {
+                                                        const float *__restrict__ z, float *__restrict__ ctx,
+                                                        int8_t *__restrict__ q, float *__restrict__ qs, int *bad) {
     const int t = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
     const float *src = heads + ((size_t)h * n + t) * kLd;
     const float s0 = src[lane], s1 = src[lane + 64];
     const float scale = rsqrt_rn(__fadd_rn(wave_sum(s0 * s0 + s1 * s1) / (float)kLd, 1e-6f));
     const size_t at = (size_t)t * lh * kLd + (size_t)h * kLd;
-    ctx[at + lane] = __fmul_rn(__fmul_rn(__fmul_rn(s0, scale), norm[lane]), silu_ref(z[at + lane]));
-    ctx[at + lane + 64] =
-        __fmul_rn(__fmul_rn(__fmul_rn(s1, scale), norm[lane + 64]), silu_ref(z[at + lane + 64]));
+    const float v0 = __fmul_rn(__fmul_rn(__fmul_rn(s0, scale), norm[lane]), silu_ref(z[at + lane]));
+    const float v1 = __fmul_rn(__fmul_rn(__fmul_rn(s1, scale), norm[lane + 64]), silu_ref(z[at + lane + 64]));
+    if constexpr (!CODES) {
+        ctx[at + lane] = v0;
+        ctx[at + lane + 64] = v1;
+    } else {
+        if ((!__builtin_isfinite(v0) || !__builtin_isfinite(v1)) && bad) atomicOr(bad, 1);
+        const float m0 = wave_max_dpp(fabsf(v0)), m1 = wave_max_dpp(fabsf(v1));
+        const float c0 = fmaxf(__fdiv_rn(m0, 127.0f), FLT_MIN), c1 = fmaxf(__fdiv_rn(m1, 127.0f), FLT_MIN);
+        q[at + lane] = (int8_t)quantize_code(v0, __frcp_rn(c0), 127.0f);
+        q[at + lane + 64] = (int8_t)quantize_code(v1, __frcp_rn(c1), 127.0f);
+        if (lane == 0) {
+            const size_t g = at / 64;
+            qs[g] = c0;
+            qs[g + 1] = c1;
+        }
+    }
 }
 
 // Per (row, head): zero-centred RMSNorm of the 256 values at src + row*src_row
@@ -1029,9 +1049,9 @@ int32_t linear(dz_ctx *ctx, const dz_weight *w, const float *x, size_t m, float 
 // the product's epilogue when the pipelined kernel takes the rows, else the
 // product into tmp and an add. Both give the same bits.
 int32_t product_add(dz_ctx *ctx, const dz_weight *w, const float *x, const int8_t *q, const float *qs, size_t m,
-                    float *h, float *tmp) {
+                    float *h, float *tmp, const int *qbad = nullptr) {
     bool fused = false;
-    int32_t rc = ctx_product_add(ctx, w, x, q, qs, m, h, &fused);
+    int32_t rc = ctx_product_add(ctx, w, x, q, qs, m, h, &fused, qbad);
     if (rc || fused) return rc;
     rc = x ? linear(ctx, w, x, m, tmp) : dz_linear_q8(ctx, w, q, qs, m, tmp);
     if (rc) return rc;
@@ -1148,8 +1168,19 @@ int32_t delta_layer(dz_ctx *ctx, dz_pplx *p, const dz_pplx::Layer &L, size_t n) 
                        c.delta_heads, c.delta_key_heads, p->ab, p->ab + n * lh, L.decay, L.dt, p->qhat, p->khat,
                        p->gb);
     launch_delta_scan(ctx, p, n, s);
-    hipLaunchKernelGGL(delta_gate_kernel, dim3((unsigned)n, c.delta_heads), dim3(64), 0, s, p->heads, (int)n,
-                       c.delta_heads, L.norm, p->z, p->ctx);
+    // out_proj adds onto the hidden rows in its epilogue; then the gate hands it
+    // A8 codes (in the MLP's code buffer, free until the MLP) instead of f32 rows
+    if (n > 16 && (size_t)c.ff >= lh * kLd &&
+        grouped_adds_residual(weight_of(L.out), (int)n, ctx_variant(ctx, "grouped"))) {
+        int *gflag = nullptr;
+        rc = ctx_product_flag(ctx, &gflag);
+        if (rc) return rc;
+        hipLaunchKernelGGL(delta_gate_kernel<true>, dim3((unsigned)n, c.delta_heads), dim3(64), 0, s, p->heads,
+                           (int)n, c.delta_heads, L.norm, p->z, nullptr, p->codes, p->code_scales, gflag);
+        return product_add(ctx, L.out, nullptr, p->codes, p->code_scales, n, p->hidden, p->projected, gflag);
+    }
+    hipLaunchKernelGGL(delta_gate_kernel<false>, dim3((unsigned)n, c.delta_heads), dim3(64), 0, s, p->heads, (int)n,
+                       c.delta_heads, L.norm, p->z, p->ctx, nullptr, nullptr, nullptr);
     return product_add(ctx, L.out, p->ctx, nullptr, nullptr, n, p->hidden, p->projected);
 }
 

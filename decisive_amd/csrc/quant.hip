@@ -16,12 +16,6 @@ namespace dz {
 
 namespace {
 
-__device__ __forceinline__ int quantize_code(float v, float inverse, float limit) {
-    float r = __builtin_rintf(__fmul_rn(v, inverse));
-    r = fminf(fmaxf(r, -limit), limit);
-    return (int)r;
-}
-
 __device__ __forceinline__ uint32_t place_nibble(int e, uint32_t nib) {
     return nib << ((e & 1) * 16 + (e >> 1) * 4);
 }
