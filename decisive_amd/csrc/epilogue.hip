@@ -356,6 +356,17 @@ constexpr int kAttnKeys = 64;                             // per step
 typedef short short4_t __attribute__((ext_vector_type(4)));
 typedef float float8_t __attribute__((ext_vector_type(8)));
 
+// max over lanes l, l ^ 16, l ^ 32 and l ^ 48, in registers (permlane swaps)
+__device__ __forceinline__ float rows_max4(float v) {
+    float a = v, b = v;
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+    v = fmaxf(a, b);
+    a = v;
+    b = v;
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+    return fmaxf(a, b);
+}
+
 __global__ __launch_bounds__(kAttnWaves * 64, 4) void attention_kernel(const half_t *__restrict__ qkv,
                                                                     half_t *__restrict__ out, int seq,
                                                                     int heads, float scale_log2) {
@@ -406,6 +417,10 @@ __global__ __launch_bounds__(kAttnWaves * 64, 4) void attention_kernel(const hal
     // the same values the numerator O^T accumulates
     const half8_t ones = {(half_t)1.0f, (half_t)1.0f, (half_t)1.0f, (half_t)1.0f,
                           (half_t)1.0f, (half_t)1.0f, (half_t)1.0f, (half_t)1.0f};
+    // The running maximum is raised only when a block's maximum exceeds it by
+    // more than tau (8 in the log2 domain), so P stays below 2^8 and most steps
+    // skip the rescale; any reference maximum gives the same quotient.
+    const float tau = 8.0f / scale_log2;
     float4_t o[kAttnQB][4];  // O^T[dh 16db + 4q4 + v][query j]
     float4_t lacc[kAttnQB];  // every component: sum of P over keys, query j
     float mrow[kAttnQB];
@@ -461,13 +476,9 @@ __global__ __launch_bounds__(kAttnWaves * 64, 4) void attention_kernel(const hal
             for (int kb = 0; kb < 4; kb++)
 #pragma unroll
                 for (int v = 0; v < 4; v++) bmax = fmaxf(bmax, sc[qb][kb][v]);
-            bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
-            bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
-            const float mnew = fmaxf(mrow[qb], bmax);
-            const float moff = -mnew * scale_log2;
-            // rescale only when some query of the wave has a new maximum
-            // (skipping a multiply by exactly 1 changes nothing)
-            if (__builtin_amdgcn_ballot_w64(mnew != mrow[qb])) {
+            bmax = rows_max4(bmax);
+            if (__builtin_amdgcn_ballot_w64(bmax > mrow[qb] + tau)) {
+                const float mnew = fmaxf(mrow[qb], bmax);
                 const float alpha = __builtin_amdgcn_exp2f((mrow[qb] - mnew) * scale_log2);
 #pragma unroll
                 for (int v = 0; v < 4; v++) lacc[qb][v] *= alpha;
@@ -475,8 +486,9 @@ __global__ __launch_bounds__(kAttnWaves * 64, 4) void attention_kernel(const hal
                 for (int db = 0; db < 4; db++)
 #pragma unroll
                     for (int v = 0; v < 4; v++) o[qb][db][v] *= alpha;
+                mrow[qb] = mnew;
             }
-            mrow[qb] = mnew;
+            const float moff = -mrow[qb] * scale_log2;
             // P^T of the two 32-key blocks, converted two values per instruction
 #pragma unroll
             for (int c = 0; c < 2; c++) {

@@ -122,6 +122,32 @@ def test_attention_matches_closed_form(ctx, oracle, batch, seq, heads):
         assert cosine(got[sl], ref) >= 0.9999
 
 
+@pytest.mark.parametrize("gain,ramp", [(3.0, False), (1.0, True), (6.0, True)])
+def test_attention_rescales_when_the_maximum_rises(ctx, oracle, gain, ramp):
+    """The kernel keeps a query's running maximum until a 64-key step exceeds
+    it by more than 8 in the log2 domain. Keys whose norms grow along the
+    sequence raise the maximum step after step, and large gains make the
+    softmax sharp (scores spanning hundreds of log2 units)."""
+    torch = pytest.importorskip("torch")
+    batch, seq, heads = 2, 700, 2
+    rng = np.random.default_rng(int(gain * 10) + ramp)
+    width = heads * 64
+    qkv = rng.standard_normal((batch * seq, 3 * width)) * 0.8
+    qkv[:, :2 * width] *= gain
+    if ramp:
+        qkv[:, width:2 * width] *= np.tile(np.linspace(0.2, 2.5, seq), batch)[:, None]
+    qkv = qkv.astype(np.float16)
+    out = empty((batch * seq, width), torch.float16)
+    ctx.attention(dev(qkv), out, batch, seq, heads, 64, 1 / 8)
+    got = host(ctx, out).astype(np.float32)
+    for b in range(batch):
+        sl = slice(b * seq, (b + 1) * seq)
+        q, k, v = (qkv[sl, i * width:(i + 1) * width].astype(np.float32) for i in range(3))
+        ref = oracle.attention(q, k, v, heads, 1 / 8)
+        assert np.abs(got[sl] - ref).max() <= 5e-3
+        assert cosine(got[sl], ref) >= 0.9999
+
+
 def test_attention_rejects_sequences_past_32bit_offsets(ctx):
     """Rejected on the host before any launch (the kernel's byte offsets are 32-bit)."""
     torch = pytest.importorskip("torch")
