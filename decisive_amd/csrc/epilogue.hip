@@ -350,7 +350,6 @@ __global__ __launch_bounds__(1024) void mean_rows_f16_kernel(const half_t *__res
 //   V: 8-byte unit u of row r at unit u ^ (4 * ((r >> 1) & 3))
 constexpr int kAttnWaves = 8;
 constexpr int kAttnQB = 2;                                // 16-query blocks per wave
-constexpr int kAttnQueries = kAttnWaves * kAttnQB * 16;  // per block
 constexpr int kAttnKeys = 64;                             // per step
 
 typedef short short4_t __attribute__((ext_vector_type(4)));
@@ -367,7 +366,8 @@ __device__ __forceinline__ float rows_max4(float v) {
     return fmaxf(a, b);
 }
 
-__global__ __launch_bounds__(kAttnWaves * 64, 4) void attention_kernel(const half_t *__restrict__ qkv,
+template <int W>
+__global__ __launch_bounds__(W * 64, 4) void attention_kernel(const half_t *__restrict__ qkv,
                                                                     half_t *__restrict__ out, int seq,
                                                                     int heads, float scale_log2) {
     __shared__ __align__(16) uint8_t ks[2 * kAttnKeys * 128];
@@ -377,7 +377,9 @@ __global__ __launch_bounds__(kAttnWaves * 64, 4) void attention_kernel(const hal
     // blocks in (query block, head, batch) order, a contiguous share per XCD
     // (xcd_unit): the 8 sequences of 1024 tokens of configuration 3 each run on
     // the XCD whose product blocks wrote their qkv rows
-    const int qblocks = (seq + kAttnQueries - 1) / kAttnQueries;
+    constexpr int QUERIES = W * kAttnQB * 16;  // per block
+    constexpr int ROWS = kAttnKeys / W;        // K and V rows each wave copies per step
+    const int qblocks = (seq + QUERIES - 1) / QUERIES;
     const int unit = xcd_unit(blockIdx.x, gridDim.x);
     const int qblk = unit % qblocks, h = (unit / qblocks) % heads, b = unit / (qblocks * heads);
     const int width = heads * 64;
@@ -387,7 +389,7 @@ __global__ __launch_bounds__(kAttnWaves * 64, 4) void attention_kernel(const hal
     const uint32_t ks_lds = lds_address(ks), vs_lds = lds_address(vs);
 
     // Q^T fragments: lane (q4, j) holds Q[query j][dh 32ds + 8q4 + e]
-    const int q0 = qblk * kAttnQueries + wave * (kAttnQB * 16);
+    const int q0 = qblk * QUERIES + wave * (kAttnQB * 16);
     half8_t qf[kAttnQB][2];
 #pragma unroll
     for (int qb = 0; qb < kAttnQB; qb++) {
@@ -400,15 +402,20 @@ __global__ __launch_bounds__(kAttnWaves * 64, 4) void attention_kernel(const hal
         }
     }
 
-    // Stage loads: wave w copies K rows 8w..8w+7 and V rows 8w..8w+7 of a
-    // step (one instruction each; lane l -> row 8w + l/8, 16-byte slot l%8).
-    const int lrow = wave * 8 + lane / 8, lslot = lane % 8;
-    const uint32_t koff = (uint32_t)(lrow * ld3 * 2 + width * 2 + h * 128 + ((lslot ^ ((lrow >> 1) & 7)) * 16));
-    const uint32_t voff = (uint32_t)(lrow * ld3 * 2 + 2 * width * 2 + h * 128 + ((lslot ^ (2 * ((lrow >> 1) & 3))) * 16));
+    // Stage loads: wave w copies K rows and V rows ROWS*w .. ROWS*w + ROWS - 1
+    // of a step, 8 rows per instruction (lane l -> row + l/8, 16-byte slot l%8).
     const uint32_t step_bytes = (uint32_t)(kAttnKeys * ld3 * 2);
     auto load_step = [&](int stage, int step) {
-        dma16(__builtin_amdgcn_readfirstlane(ks_lds + stage * kAttnKeys * 128 + wave * 1024), koff + step * step_bytes, rs);
-        dma16(__builtin_amdgcn_readfirstlane(vs_lds + stage * kAttnKeys * 128 + wave * 1024), voff + step * step_bytes, rs);
+#pragma unroll
+        for (int i = 0; i < ROWS / 8; i++) {
+            const int lrow = wave * ROWS + i * 8 + lane / 8, lslot = lane % 8;
+            const uint32_t koff = (uint32_t)(lrow * ld3 * 2 + width * 2 + h * 128 + ((lslot ^ ((lrow >> 1) & 7)) * 16));
+            const uint32_t voff =
+                (uint32_t)(lrow * ld3 * 2 + 2 * width * 2 + h * 128 + ((lslot ^ (2 * ((lrow >> 1) & 3))) * 16));
+            const uint32_t at = (uint32_t)((wave * ROWS + i * 8) * 128);
+            dma16(__builtin_amdgcn_readfirstlane(ks_lds + stage * kAttnKeys * 128 + at), koff + step * step_bytes, rs);
+            dma16(__builtin_amdgcn_readfirstlane(vs_lds + stage * kAttnKeys * 128 + at), voff + step * step_bytes, rs);
+        }
     };
 
     const float4_t fz = {0.f, 0.f, 0.f, 0.f};
@@ -646,8 +653,8 @@ void launch_attention(const half_t *qkv, half_t *out, int batch, int seq, int he
                       float scale, hipStream_t s) {
     (void)dh;
     if (!batch || !seq) return;
-    const dim3 grid(cdiv(seq, kAttnQueries) * heads * batch);
-    hipLaunchKernelGGL(attention_kernel, grid, dim3(kAttnWaves * 64), 0, s, qkv, out, seq, heads,
+    const dim3 grid(cdiv(seq, kAttnWaves * kAttnQB * 16) * heads * batch);
+    hipLaunchKernelGGL(attention_kernel<kAttnWaves>, grid, dim3(kAttnWaves * 64), 0, s, qkv, out, seq, heads,
                        scale * 1.4426950408889634f);
 }
 void launch_fill_normal_f32(float *p, size_t n, uint64_t seed, float stddev, hipStream_t s) {
