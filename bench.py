@@ -89,10 +89,12 @@ def warm(torch, fn, ms: float = 60.0, least: int = 2):
 def graph_ms(torch, stream, step, launches: int, reps: int = 20) -> float:
     """Average launch duration of `step` (which enqueues `launches` launches)
     captured once as a HIP graph and replayed `reps` times back to back."""
+    from decisive_amd import rocm
+
     step()
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=stream):
+    with rocm.capture(graph, stream):
         step()
     torch.cuda.synchronize()
     for _ in range(3):
@@ -684,7 +686,7 @@ def main():
             run = step
         else:
             graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graph, stream=side):
+            with rocm.capture(graph, side):
                 step()
             torch.cuda.synchronize()
             run = graph.replay

@@ -7,7 +7,9 @@ when the shared library is missing or the GPU is not a gfx950, calls raise.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
+import gc
 import json
 import re
 from pathlib import Path
@@ -36,6 +38,28 @@ class DzError(RuntimeError):
         self.status = status
         self.code = STATUS_NAMES.get(status, "UNKNOWN")
         super().__init__(f"{self.code}: {message}")
+
+
+@contextlib.contextmanager
+def capture(graph, stream):
+    """`torch.cuda.graph(graph, stream=stream)` with Python's cyclic garbage
+    collector held off while the graph records. The finalizers of `Weight` and
+    `Context` free device memory (hipFree), and a free made while any stream
+    records in the default (global) capture mode invalidates the recording. A
+    collection pass can run at any allocation and finalize objects kept alive by
+    reference cycles (an earlier exception's traceback, say), so one pass runs
+    before the recording starts and none during it."""
+    import torch
+
+    gc.collect()
+    enabled = gc.isenabled()
+    gc.disable()
+    try:
+        with torch.cuda.graph(graph, stream=stream):
+            yield
+    finally:
+        if enabled:
+            gc.enable()
 
 
 class EncoderConfig(ctypes.Structure):

@@ -65,7 +65,7 @@ def test_captured_products_replay_nan_then_clean(ctx, oracle):
             record()  # sizes the workspace before capture
             torch.cuda.synchronize()
             graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graph, stream=stream):
+            with rocm.capture(graph, stream):
                 record()
             for i, src in enumerate([bad, x, x, bad, bad, x]):
                 xin.copy_(torch.from_numpy(src))
@@ -105,7 +105,7 @@ def test_workspace_a_graph_uses_outlives_growth(fresh, oracle):
             fresh.linear(w, xin, rocm.F32, m, y, rocm.W4A8)
             torch.cuda.synchronize()
             graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graph, stream=stream):
+            with rocm.capture(graph, stream):
                 fresh.linear(w, xin, rocm.F32, m, y, rocm.W4A8)
             # an eager product that replaces the 1 MiB first workspace
             big_m, big_k = 2048, 1024
@@ -142,7 +142,7 @@ def test_capture_refuses_growth_stream_changes_and_synchronous_calls(fresh, orac
                          lambda: fresh.project(w, x, 1, y)):
                 graph = torch.cuda.CUDAGraph()
                 with pytest.raises(rocm.DzError) as e:
-                    with torch.cuda.graph(graph, stream=stream):
+                    with rocm.capture(graph, stream):
                         y.zero_()
                         call()
                 assert e.value.code == "INVALID_REQUEST"

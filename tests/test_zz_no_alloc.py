@@ -119,7 +119,7 @@ def test_noalloc_records_on_a_context_without_workspace(oracle):
                 xin, y = torch.from_numpy(x).cuda(), torch.empty((m, n), device="cuda")
                 torch.cuda.synchronize()
                 graph = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(graph, stream=stream):
+                with rocm.capture(graph, stream):
                     fresh.linear_noalloc(w, xin, rocm.F32, m, y, rocm.W4A8)
                 for src in (x, bad, x, x):
                     xin.copy_(torch.from_numpy(src))
