@@ -466,11 +466,26 @@ def pplx_line(torch, ctx, rocm, stream, n: int = 1024, layers: int = 32) -> dict
     wall = time.perf_counter()
     ms = timed_ms(torch, stream, lambda r: p.forward_rows(rows, n, markers), reps)
     wall = (time.perf_counter() - wall) * 1e3 / reps
+    # the same model with its layer projections streamed from pinned host memory
+    # through two device banks (webgpu/streaming.rs): same kernels, same bits
+    p.set_residency(rocm.PPLX_STREAMED)
+    info = p.residency_info()
+    if not np.array_equal(p.forward_rows(rows, n, markers).view(np.uint32), logits.view(np.uint32)):
+        raise AssertionError("streamed decider logits differ from the resident ones")
+    warm(torch, lambda r: p.forward_rows(rows, n, markers))
+    s_ms = timed_ms(torch, stream, lambda r: p.forward_rows(rows, n, markers), 3)
+    streamed = {"ms": round(s_ms, 3), "sequences/s": round(1e3 / s_ms, 2),
+                "device_layer_weight_bytes": info["device_layer_weight_bytes"],
+                "resident_layer_weight_bytes": info["layer_weight_bytes"],
+                "host_to_device_GB/s": round(info["host_layer_weight_bytes"] / (s_ms * 1e-3) / 1e9, 1),
+                "note": "every layer's projections copied host-to-device once per forward, one layer ahead of "
+                        "the compute; logits bitwise equal to the resident forward"}
     p.close()
     prods = 24 * 2 * n * (d * (cw + 32 * ld + 64) + 32 * ld * d) + 8 * 2 * n * (d * (2 * 16 * ad + 8 * ad) + 16 * ad * d)
     prods += layers * 2 * n * 3 * d * ff
     return {"ms": round(ms, 3), "wall_ms": round(wall, 3), "sequences/s": round(1e3 / ms, 2),
             "tokens/s": round(n * 1e3 / ms, 1), "product_TOP/s": round(prods / (ms * 1e-3) / 1e12, 1),
+            "streamed_weights": streamed,
             "note": f"{layers} layers (24 gated-delta, 8 gated-attention), hidden 2560, one chunk of {n} tokens, "
                     "4 markers; W4A8 products bit-exact with the CPU path; random Q4 g64 wire weights; "
                     "host rows in and logits out inside the timed region"}

@@ -37,6 +37,7 @@ int32_t ctx_hip_fail(dz_ctx *ctx, hipError_t e, const char *what);
 hipStream_t ctx_stream(dz_ctx *ctx);
 int *ctx_flag(dz_ctx *ctx);
 const Weight &weight_of(const dz_weight *h);
+Weight &weight_mut(dz_weight *h);
 int32_t weight_upload(dz_ctx *ctx, const void *packed, size_t bytes, int32_t layout, size_t rows, size_t cols,
                       dz_weight **out);
 void weight_free(dz_weight *h);
@@ -799,6 +800,25 @@ struct dz_pplx {
     int32_t *markers = nullptr;
     uint8_t *rows_dev = nullptr;
     dz::Weight rows_weight;
+    // Streamed residency (webgpu/streaming.rs:16-369): the layers' projections
+    // live in pinned host memory, already in the device layout, and layer i
+    // runs from device bank i % 2. The copy stream fills a bank once the layer
+    // that used it last has finished (`done`); the compute stream waits for the
+    // copy (`copied`). A layer's weight handles point into its bank for good;
+    // only the bank's contents change. At most two layers are in flight: one
+    // computing, the next one copying.
+    struct Streaming {
+        bool on = false;
+        uint8_t *host = nullptr;            // every layer's projections, layer after layer
+        size_t host_bytes = 0;
+        std::vector<size_t> offset, bytes;  // per layer, in `host`
+        uint8_t *bank[2] = {nullptr, nullptr};
+        size_t bank_bytes = 0;
+        hipStream_t copy = nullptr;
+        hipEvent_t copied[2] = {nullptr, nullptr}, done[2] = {nullptr, nullptr};
+        int held[2] = {-1, -1};             // the layer each bank holds (or is receiving)
+        uint64_t uploads = 0, reuses = 0, upload_bytes = 0;
+    } st;
 };
 
 namespace dz {
@@ -806,6 +826,37 @@ namespace dz {
 namespace {
 
 size_t conv_width(const dz_pplx_config &c) { return 2 * (size_t)c.delta_key_heads * kLd + (size_t)c.delta_heads * kLd; }
+
+// The projections of one layer, in the order their bytes sit in host memory
+// and in the layer's bank when the weights are streamed.
+std::vector<dz_weight *> projections(const dz_pplx::Layer &L) {
+    if (L.attention) return {L.q, L.k, L.v, L.o, L.gate, L.up, L.down};
+    return {L.qkv, L.z, L.a, L.b, L.out, L.gate, L.up, L.down};
+}
+
+int32_t stream_replace(dz_ctx *ctx, dz_pplx *p, int layer, const dz_weight *slot, const dz_weight *w);
+
+// Frees the streamed state's banks, events, copy stream and host copy (the
+// caller has synchronized both streams and re-pointed the weight handles).
+void streaming_release(dz_pplx *p) {
+    auto &st = p->st;
+    for (int b = 0; b < 2; b++) {
+        if (st.bank[b]) hipFree(st.bank[b]);
+        if (st.copied[b]) hipEventDestroy(st.copied[b]);
+        if (st.done[b]) hipEventDestroy(st.done[b]);
+        st.bank[b] = nullptr;
+        st.copied[b] = st.done[b] = nullptr;
+        st.held[b] = -1;
+    }
+    if (st.copy) hipStreamDestroy(st.copy);
+    if (st.host) hipHostFree(st.host);
+    st.copy = nullptr;
+    st.host = nullptr;
+    st.host_bytes = st.bank_bytes = 0;
+    st.offset.clear();
+    st.bytes.clear();
+    st.on = false;
+}
 
 void free_activations(dz_pplx *p) {
     for (void *b : p->buffers) hipFree(b);
@@ -898,6 +949,13 @@ bool starts(const std::string &s, const char *p, std::string *rest) {
 void pplx_destroy(dz_ctx *ctx, dz_pplx *p) {
     if (!p) return;
     hipStreamSynchronize(ctx_stream(ctx));
+    if (p->st.on) {  // the handles point into the banks, which streaming_release frees
+        hipStreamSynchronize(p->st.copy);
+        for (auto &l : p->layers)
+            for (dz_weight *w : projections(l))
+                if (w) weight_mut(w).codes = weight_mut(w).scales = nullptr;
+    }
+    streaming_release(p);
     for (auto &l : p->layers) {
         for (dz_weight *w : {l.qkv, l.z, l.a, l.b, l.out, l.q, l.k, l.v, l.o, l.gate, l.up, l.down}) weight_free(w);
         for (float *f : {l.input_norm, l.post_norm, l.conv, l.decay, l.dt, l.norm, l.qnorm, l.knorm})
@@ -947,6 +1005,7 @@ int32_t pplx_set_weight(dz_ctx *ctx, dz_pplx *p, const char *name, const void *p
     std::string s(name), rest;
     dz_weight **slot = nullptr;
     size_t want_r = 0, want_c = 0;
+    int layer = -1;
     if (s == "readout") {
         slot = &p->readout;
         want_r = DZ_READOUT_CODES;
@@ -983,6 +1042,7 @@ int32_t pplx_set_weight(dz_ctx *ctx, dz_pplx *p, const char *name, const void *p
                 slot = sl.w;
                 want_r = sl.r;
                 want_c = sl.c;
+                layer = i;
             }
     }
     if (!slot) return ctx_fail(ctx, DZ_INVALID_CHECKPOINT, "unknown pplx tensor: " + s);
@@ -990,6 +1050,17 @@ int32_t pplx_set_weight(dz_ctx *ctx, dz_pplx *p, const char *name, const void *p
     dz_weight *w = nullptr;
     int32_t rc = weight_upload(ctx, packed, bytes, layout, rows, cols, &w);
     if (rc) return rc;
+    if (p->st.on && layer >= 0) {  // streamed: the new bytes replace the host copy
+        const Weight &a = weight_of(w), &b = weight_of(*slot);
+        if (a.kind != b.kind || a.code_bytes != b.code_bytes || a.scale_bytes != b.scale_bytes) {
+            weight_free(w);
+            return ctx_fail(ctx, DZ_INVALID_REQUEST,
+                            "a streamed projection keeps its layout: set resident residency to change it: " + s);
+        }
+        rc = stream_replace(ctx, p, layer, *slot, w);
+        weight_free(w);
+        return rc;
+    }
     weight_free(*slot);
     *slot = w;
     return DZ_OK;
@@ -1051,6 +1122,171 @@ bool complete(const dz_pplx *p, std::string *missing) {
         return false;
     }
     return true;
+}
+
+// ---- streamed residency (webgpu/streaming.rs:16-369) -------------------------------
+
+// Every part of a layer's bank is 256-byte aligned.
+inline size_t bank_align(size_t v) { return (v + 255) / 256 * 256; }
+
+// Bytes of one layer in the bank layout: each projection's codes, then its
+// scales, in projections() order.
+size_t layer_bank_bytes(const dz_pplx::Layer &L) {
+    size_t b = 0;
+    for (dz_weight *w : projections(L)) b += bank_align(weight_of(w).code_bytes) + bank_align(weight_of(w).scale_bytes);
+    return b;
+}
+
+// Offset of projection `w` inside its layer's bank.
+size_t bank_offset(const dz_pplx::Layer &L, const dz_weight *w) {
+    size_t off = 0;
+    for (dz_weight *x : projections(L)) {
+        if (x == w) break;
+        off += bank_align(weight_of(x).code_bytes) + bank_align(weight_of(x).scale_bytes);
+    }
+    return off;
+}
+
+// Moves every layer projection into pinned host memory (the device layout,
+// copied as it is) and points layer i's handles into bank i % 2. The device
+// copies are freed only after every byte has reached the host.
+int32_t stream_on(dz_ctx *ctx, dz_pplx *p) {
+    std::string missing;
+    if (!complete(p, &missing)) return ctx_fail(ctx, DZ_INVALID_CHECKPOINT, "missing pplx weights: " + missing);
+    auto &st = p->st;
+    const size_t layers = p->layers.size();
+    st.offset.assign(layers, 0);
+    st.bytes.assign(layers, 0);
+    size_t total = 0, bank = 0;
+    for (size_t i = 0; i < layers; i++) {
+        st.offset[i] = total;
+        st.bytes[i] = layer_bank_bytes(p->layers[i]);
+        total += st.bytes[i];
+        bank = std::max(bank, st.bytes[i]);
+    }
+    hipStream_t s = ctx_stream(ctx);
+    hipError_t e = hipHostMalloc((void **)&st.host, total, hipHostMallocDefault);
+    for (int b = 0; b < 2 && e == hipSuccess; b++) e = hipMalloc(&st.bank[b], bank);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&st.copy, hipStreamNonBlocking);
+    for (int b = 0; b < 2 && e == hipSuccess; b++) {
+        e = hipEventCreateWithFlags(&st.copied[b], hipEventDisableTiming);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&st.done[b], hipEventDisableTiming);
+        // recorded once, so that every later wait on them has an event to wait for
+        if (e == hipSuccess) e = hipEventRecord(st.copied[b], st.copy);
+        if (e == hipSuccess) e = hipEventRecord(st.done[b], s);
+    }
+    for (size_t i = 0; i < layers && e == hipSuccess; i++) {
+        uint8_t *dst = st.host + st.offset[i];
+        for (dz_weight *w : projections(p->layers[i])) {
+            const Weight &x = weight_of(w);
+            e = hipMemcpyAsync(dst, x.codes, x.code_bytes, hipMemcpyDeviceToHost, s);
+            dst += bank_align(x.code_bytes);
+            if (e == hipSuccess) e = hipMemcpyAsync(dst, x.scales, x.scale_bytes, hipMemcpyDeviceToHost, s);
+            dst += bank_align(x.scale_bytes);
+            if (e != hipSuccess) break;
+        }
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) {
+        hipStreamSynchronize(s);
+        streaming_release(p);
+        return ctx_hip_fail(ctx, e, "streamed residency");
+    }
+    st.host_bytes = total;
+    st.bank_bytes = bank;
+    for (size_t i = 0; i < layers; i++) {
+        uint8_t *base = st.bank[i % 2];
+        for (dz_weight *w : projections(p->layers[i])) {
+            Weight &x = weight_mut(w);
+            hipFree(x.codes);
+            hipFree(x.scales);
+            const size_t off = bank_offset(p->layers[i], w);
+            x.codes = base + off;
+            x.scales = base + off + bank_align(x.code_bytes);
+        }
+    }
+    st.held[0] = st.held[1] = -1;
+    st.uploads = st.reuses = st.upload_bytes = 0;
+    st.on = true;
+    return DZ_OK;
+}
+
+// Gives every layer projection its own device memory again, filled from the
+// host copy; the streamed state is released only once all of it is there.
+int32_t stream_off(dz_ctx *ctx, dz_pplx *p) {
+    auto &st = p->st;
+    hipStream_t s = ctx_stream(ctx);
+    hipError_t e = hipStreamSynchronize(st.copy);
+    std::vector<uint8_t *> fresh;
+    for (size_t i = 0; i < p->layers.size() && e == hipSuccess; i++) {
+        const uint8_t *src = st.host + st.offset[i];
+        for (dz_weight *w : projections(p->layers[i])) {
+            const Weight &x = weight_of(w);
+            uint8_t *c = nullptr, *sc = nullptr;
+            e = hipMalloc(&c, x.code_bytes);
+            if (e == hipSuccess) fresh.push_back(c);
+            if (e == hipSuccess) e = hipMalloc(&sc, x.scale_bytes);
+            if (e == hipSuccess) fresh.push_back(sc);
+            if (e == hipSuccess) e = hipMemcpyAsync(c, src, x.code_bytes, hipMemcpyHostToDevice, s);
+            src += bank_align(x.code_bytes);
+            if (e == hipSuccess) e = hipMemcpyAsync(sc, src, x.scale_bytes, hipMemcpyHostToDevice, s);
+            src += bank_align(x.scale_bytes);
+            if (e != hipSuccess) break;
+        }
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) {
+        hipStreamSynchronize(s);
+        for (uint8_t *f : fresh) hipFree(f);
+        return ctx_hip_fail(ctx, e, "resident weights");
+    }
+    size_t k = 0;
+    for (auto &L : p->layers)
+        for (dz_weight *w : projections(L)) {
+            Weight &x = weight_mut(w);
+            x.codes = fresh[k++];
+            x.scales = fresh[k++];
+        }
+    streaming_release(p);
+    return DZ_OK;
+}
+
+// Starts the copy of layer i into bank i % 2, after the layer that used the
+// bank last has finished, unless the bank already holds layer i.
+int32_t stream_in(dz_ctx *ctx, dz_pplx *p, int i) {
+    auto &st = p->st;
+    const int b = i % 2;
+    if (st.held[b] == i) return DZ_OK;
+    hipError_t e = hipStreamWaitEvent(st.copy, st.done[b], 0);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(st.bank[b], st.host + st.offset[i], st.bytes[i], hipMemcpyHostToDevice, st.copy);
+    if (e == hipSuccess) e = hipEventRecord(st.copied[b], st.copy);
+    if (e != hipSuccess) {
+        st.held[b] = -1;
+        return ctx_hip_fail(ctx, e, "layer weight upload");
+    }
+    if (st.held[b] >= 0) st.reuses++;
+    st.held[b] = i;
+    st.uploads++;
+    st.upload_bytes += st.bytes[i];
+    return DZ_OK;
+}
+
+// Replaces the host copy of a streamed projection with the device-layout
+// bytes of `w` (same shape); the bank is refilled on the layer's next run.
+int32_t stream_replace(dz_ctx *ctx, dz_pplx *p, int layer, const dz_weight *slot, const dz_weight *w) {
+    auto &st = p->st;
+    const Weight &x = weight_of(w);
+    uint8_t *dst = st.host + st.offset[layer] + bank_offset(p->layers[layer], slot);
+    hipStream_t s = ctx_stream(ctx);
+    hipError_t e = hipStreamSynchronize(st.copy);  // no copy is reading the host bytes
+    if (e == hipSuccess) e = hipMemcpyAsync(dst, x.codes, x.code_bytes, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(dst + bank_align(x.code_bytes), x.scales, x.scale_bytes, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return ctx_hip_fail(ctx, e, "streamed weight replacement");
+    if (st.held[layer % 2] == layer) st.held[layer % 2] = -1;
+    return DZ_OK;
 }
 
 // dz_linear_pair / dz_linear / the MLP, on the context's stream
@@ -1289,19 +1525,65 @@ int32_t attention_layer(dz_ctx *ctx, dz_pplx *p, const dz_pplx::Layer &L, size_t
 int32_t pplx_run_layer(dz_ctx *ctx, dz_pplx *p, int index, size_t n, const int32_t *markers, size_t count,
                        size_t *rows_out) {
     const auto &L = p->layers[index];
+    auto &st = p->st;
     int32_t rc;
+    if (st.on) {  // the layer's bank, then the next layer's copy behind it
+        rc = stream_in(ctx, p, index);
+        if (rc) return rc;
+        hipError_t e = hipStreamWaitEvent(ctx_stream(ctx), st.copied[index % 2], 0);
+        if (e != hipSuccess) return ctx_hip_fail(ctx, e, "layer weight wait");
+        if (index + 1 < (int)p->layers.size()) {
+            rc = stream_in(ctx, p, index + 1);
+            if (rc) return rc;
+        }
+    }
     size_t rows = n;
     if (L.attention) {
         rc = attention_layer(ctx, p, L, n, markers, count, &rows);
     } else {
         rc = delta_layer(ctx, p, L, n);
     }
-    if (rc) return rc;
-    rc = mlp(ctx, p, L, rows);
+    if (!rc) rc = mlp(ctx, p, L, rows);
+    if (st.on) {  // the bank is free again once this layer's kernels have run
+        hipError_t e = hipEventRecord(st.done[index % 2], ctx_stream(ctx));
+        if (!rc && e != hipSuccess) return ctx_hip_fail(ctx, e, "layer weight release");
+    }
     if (rc) return rc;
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return ctx_hip_fail(ctx, e, "pplx layer");
     *rows_out = rows;
+    return DZ_OK;
+}
+
+int32_t pplx_set_residency(dz_ctx *ctx, dz_pplx *p, int32_t residency) {
+    if (!p) return ctx_fail(ctx, DZ_INVALID_REQUEST, "null pointer");
+    if (residency != DZ_PPLX_RESIDENT && residency != DZ_PPLX_STREAMED)
+        return ctx_fail(ctx, DZ_INVALID_PARAMETERS, "residency is DZ_PPLX_RESIDENT or DZ_PPLX_STREAMED");
+    const bool streamed = residency == DZ_PPLX_STREAMED;
+    if (streamed == p->st.on) return DZ_OK;
+    hipError_t e = hipStreamSynchronize(ctx_stream(ctx));
+    if (e != hipSuccess) return ctx_hip_fail(ctx, e, "stream synchronize");
+    return streamed ? stream_on(ctx, p) : stream_off(ctx, p);
+}
+
+int32_t pplx_residency_info(dz_ctx *ctx, dz_pplx *p, char *json, size_t cap) {
+    if (!p) return ctx_fail(ctx, DZ_INVALID_REQUEST, "null pointer");
+    const auto &st = p->st;
+    size_t resident = 0;
+    for (const auto &L : p->layers)
+        for (dz_weight *w : projections(L))
+            if (w) resident += weight_of(w).code_bytes + weight_of(w).scale_bytes;
+    auto held = [&](int b) { return st.held[b] < 0 ? std::string("null") : std::to_string(st.held[b]); };
+    std::string s = "{\"residency\":\"" + std::string(st.on ? "streamed" : "resident") + "\"";
+    s += ",\"layer_weight_bytes\":" + std::to_string(resident);
+    s += ",\"device_layer_weight_bytes\":" + std::to_string(st.on ? 2 * st.bank_bytes : resident);
+    s += ",\"host_layer_weight_bytes\":" + std::to_string(st.host_bytes);
+    s += ",\"banks\":" + std::to_string(st.on ? 2 : 0) + ",\"bank_bytes\":" + std::to_string(st.bank_bytes);
+    s += ",\"bank_layers\":[" + held(0) + "," + held(1) + "]";
+    s += ",\"layer_uploads\":" + std::to_string(st.uploads) + ",\"bank_reuses\":" + std::to_string(st.reuses);
+    s += ",\"upload_bytes\":" + std::to_string(st.upload_bytes) + ",\"max_in_flight_layers\":2}";
+    if (!json || cap < s.size() + 1) return ctx_fail(ctx, DZ_RESOURCE_LIMIT, "info buffer too small");
+    memcpy(json, s.c_str(), s.size() + 1);
     return DZ_OK;
 }
 

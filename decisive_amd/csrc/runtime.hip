@@ -74,6 +74,8 @@ int32_t pplx_set_weight(dz_ctx *ctx, dz_pplx *p, const char *name, const void *p
 int32_t pplx_set_vector(dz_ctx *ctx, dz_pplx *p, const char *name, const float *values, size_t count);
 int32_t pplx_layer(dz_ctx *ctx, dz_pplx *p, int index, float *hidden, size_t n, const int32_t *markers_host,
                    size_t count);
+int32_t pplx_set_residency(dz_ctx *ctx, dz_pplx *p, int32_t residency);
+int32_t pplx_residency_info(dz_ctx *ctx, dz_pplx *p, char *json, size_t cap);
 int32_t pplx_forward_rows(dz_ctx *ctx, dz_pplx *p, const void *rows_host, size_t n, const int32_t *markers,
                           size_t count, float *logits_host);
 int32_t encoder_forward(dz_ctx *ctx, dz_encoder *enc, const int32_t *ids_dev, const void *rows_host,
@@ -981,6 +983,17 @@ int32_t dz_pplx_forward_rows(dz_ctx *ctx, dz_pplx *model, const void *rows, size
     return dz::pplx_forward_rows(ctx, model, rows, n, markers, count, logits);
 }
 
+int32_t dz_pplx_set_residency(dz_ctx *ctx, dz_pplx *model, int32_t residency) {
+    DZ_BEGIN(ctx);
+    if (capturing(ctx)) return fail(ctx, DZ_INVALID_REQUEST, "residency change during stream capture");
+    return dz::pplx_set_residency(ctx, model, residency);
+}
+
+int32_t dz_pplx_residency_info(dz_ctx *ctx, dz_pplx *model, char *json, size_t cap) {
+    DZ_BEGIN(ctx);
+    return dz::pplx_residency_info(ctx, model, json, cap);
+}
+
 // ---- tuner ---------------------------------------------------------------------------
 
 int32_t dz_tune(dz_ctx *ctx, uint32_t budget_ms, const char *cache_in, char *cache_out, size_t cap) {
@@ -1059,6 +1072,9 @@ std::string ctx_device_key(dz_ctx *ctx) {
     return ctx->arch + "/" + std::to_string(ctx->cus) + "cu/" + std::to_string(ctx->clock_khz) + "khz";
 }
 const Weight &weight_of(const dz_weight *h) { return h->w; }
+// The device pointers of a weight whose memory another owner manages (the
+// decider's streamed banks): codes and scales are re-pointed, never freed here.
+Weight &weight_mut(dz_weight *h) { return h->w; }
 int32_t weight_quantize(dz_ctx *ctx, const void *values, int dtype, size_t rows, size_t cols, int bits,
                         int group, dz_weight **out) {
     return dz_weight_quantize(ctx, values, dtype, rows, cols, bits, group, out);

@@ -49,8 +49,11 @@ public:
         return c;
     }
 
+    // `residency` DZ_PPLX_STREAMED keeps the layer projections in pinned host
+    // memory and runs each layer from one of two device banks
+    // (webgpu/streaming.rs:16-369); the answers are the same bits.
     static Result<RocmPplx> open(int device, const std::string &dir, const dz_pplx_config &config,
-                                 const PackedModel &model = PackedModel{}) {
+                                 const PackedModel &model = PackedModel{}, int32_t residency = DZ_PPLX_RESIDENT) {
         if ((size_t)config.layers != model.layers || (size_t)config.hidden != model.hidden)
             return Error("INVALID_PARAMETERS", "decoder shape differs from the checkpoint's");
         auto ck = PackedCheckpoint::open(dir, model);
@@ -84,6 +87,8 @@ public:
         auto norm = c.norm();
         if (!norm) return norm.error();
         rc = dz_pplx_set_vector(r.ctx_, r.model_, "language_model.norm.weight", norm.value().data(), norm.value().size());
+        if (rc != DZ_OK) return r.fail(rc);
+        rc = dz_pplx_set_residency(r.ctx_, r.model_, residency);
         if (rc != DZ_OK) return r.fail(rc);
         auto t = c.temperature();
         if (!t) return t.error();

@@ -288,6 +288,15 @@ TEST(rocm_pplx_answers_from_a_packed_checkpoint) {
     CHECK(dot / std::sqrt(gg * ww) >= 0.9999);
     CHECK(maxerr <= 1e-2 * scale);
     printf("pplx logits vs oracle: cos %.9f, max |d| %.5f of %.3f\n", dot / std::sqrt(gg * ww), maxerr, scale);
+    {  // the same checkpoint with streamed layer weights: the same bits
+        auto streamed = RocmPplx::open(0, dir, cfg, pm, DZ_PPLX_STREAMED);
+        CHECK(streamed.ok());
+        if (streamed.ok()) {
+            auto sl = streamed.value().logits(rows.value(), ids.size(), markers);
+            CHECK(sl.ok() && sl.value().size() == lg.value().size() &&
+                  memcmp(sl.value().data(), lg.value().data(), lg.value().size() * sizeof(float)) == 0);
+        }
+    }
     // answers through Model<RocmPplx>: the answer step over those logits
     Request req;
     Json chunk = Json::object();

@@ -29,6 +29,7 @@ Q4_G64_F32, Q8_G64_F32, Q4_G32_F16 = 0, 1, 2
 F32, F16, BF16 = 0, 1, 2
 EPI_NONE, EPI_GELU, EPI_RESIDUAL = 0, 1, 2
 W4A8, W4A4, W4A16 = 0, 1, 2
+PPLX_RESIDENT, PPLX_STREAMED = 0, 1
 
 
 class DzError(RuntimeError):
@@ -141,6 +142,8 @@ _SIGNATURES = {
     "dz_pplx_set_vector": (I32, [P, P, ctypes.c_char_p, P, SZ]),
     "dz_pplx_layer": (I32, [P, P, I32, P, SZ, P, SZ]),
     "dz_pplx_forward_rows": (I32, [P, P, P, SZ, P, SZ, P]),
+    "dz_pplx_set_residency": (I32, [P, P, I32]),
+    "dz_pplx_residency_info": (I32, [P, P, ctypes.c_char_p, SZ]),
     "dz_tune": (I32, [P, U32, ctypes.c_char_p, ctypes.c_char_p, SZ]),
     "dz_select_variant": (I32, [P, ctypes.c_char_p, ctypes.c_char_p]),
 }
@@ -482,6 +485,15 @@ class Pplx:
         self.ctx._check(load().dz_pplx_forward_rows(self.ctx.handle, self.handle, rows_host.ctypes.data, n,
                                                     m.ctypes.data, m.size, out.ctypes.data))
         return out
+
+    def set_residency(self, residency: int):
+        """PPLX_RESIDENT or PPLX_STREAMED (two device banks, layers copied in turn)."""
+        self.ctx._check(load().dz_pplx_set_residency(self.ctx.handle, self.handle, residency))
+
+    def residency_info(self) -> dict:
+        buf = ctypes.create_string_buffer(1024)
+        self.ctx._check(load().dz_pplx_residency_info(self.ctx.handle, self.handle, buf, len(buf)))
+        return json.loads(buf.value.decode())
 
     def close(self):
         if self.handle:

@@ -394,6 +394,33 @@ int32_t dz_pplx_layer(dz_ctx *ctx, dz_pplx *model, int32_t layer, float *hidden_
 int32_t dz_pplx_forward_rows(dz_ctx *ctx, dz_pplx *model, const void *rows_host, size_t n,
                              const int32_t *markers_host, size_t count, float *logits_host);
 
+/* Where the decider's layer projections live (webgpu/streaming.rs:16-369, the
+ * reference's two-bank weight buffers; browser_gpu.rs:336-378 keeps at most
+ * two layers queued).
+ *  - DZ_PPLX_RESIDENT (the default): every projection in device memory.
+ *  - DZ_PPLX_STREAMED: every layer projection in pinned host memory, already
+ *    in the device layout, and two device banks of the largest layer's size.
+ *    Layer i runs from bank i % 2 (streaming.rs:220 banks[layer % 2]). While
+ *    layer i computes, a copy stream fills the other bank with layer i + 1,
+ *    once the layer that used that bank last has finished; layer i + 1 waits
+ *    for its copy. Device memory for layer weights drops from the whole model
+ *    to two layers; a forward then moves every layer's bytes over the host
+ *    link once. Outputs are bitwise equal to the resident ones.
+ * Switching needs a complete model (every layer projection set) and waits
+ * for the context stream. Under DZ_PPLX_STREAMED, dz_pplx_set_weight replaces
+ * a layer projection's host copy (same layout and shape, else
+ * DZ_INVALID_REQUEST). Not recordable under stream capture. */
+#define DZ_PPLX_RESIDENT 0
+#define DZ_PPLX_STREAMED 1
+int32_t dz_pplx_set_residency(dz_ctx *ctx, dz_pplx *model, int32_t residency);
+/* streaming.rs:176-191 diagnostics as JSON: "residency", "layer_weight_bytes"
+ * (every layer projection), "device_layer_weight_bytes" (what the device
+ * holds for them now), "host_layer_weight_bytes", "banks", "bank_bytes",
+ * "bank_layers" (the layer each bank holds, or null), "layer_uploads",
+ * "bank_reuses" (uploads into a bank that held another layer), "upload_bytes"
+ * and "max_in_flight_layers". DZ_RESOURCE_LIMIT when cap is too small. */
+int32_t dz_pplx_residency_info(dz_ctx *ctx, dz_pplx *model, char *json, size_t cap);
+
 /* ---- kernel tuner (webgpu/checkpoint.rs:95-294, 428-652) ------------------------ */
 
 /* Times the tile variants of every tuned kernel family within budget_ms and
