@@ -20,6 +20,8 @@ int8 GEMM, the Q4 prefill GEMM and the encoder forward) are reported under
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-secondary] [--no-cpu]
                     [--no-graph] [--calibrate-copy] [--tune MS]
     python bench.py --only pplx                      (the decider line alone)
+    python bench.py --only encoder / floors / probes (the encoder line; launch floors
+                     at the GEMV's size; sustained unit rates from register-only loops)
     python bench.py --only tune [--tune MS] [--tune-cache F] [--tune-out F]
                     (the tuner's selection, then each family's reference and
                      selected variants at the tuning shape, for rocprofv3)
@@ -563,6 +565,37 @@ def traffic_per_launch():
         return None
 
 
+def probes_line(ctx) -> dict:
+    """Sustained unit rates from register-only loops (dz_probe_rate): the MFMA
+    rates on random and on all-zero operands beside the published peaks, and
+    the cycles per wave instruction of v_fma_f32 and v_exp_f32 at the
+    device's maximum clock (the attention softmax is bound by their ratio)."""
+    info = ctx.info()
+    simds, clock = info["compute_units"] * 4, info["clock_khz"] * 1e3
+
+    def rate_of(what, zero=False):
+        # about 300 ms of the same loop first: the clocks of an idle device ramp up under load
+        start = time.perf_counter()
+        while time.perf_counter() - start < 0.3:
+            ctx.probe_rate(what, zero)
+        return max(ctx.probe_rate(what, zero) for _ in range(3))
+
+    out = {}
+    for what, peak, unit in (("mfma_f16", F16_PEAK_TFLOPS, "TFLOP/s"), ("mfma_i8", I8_PEAK_TOPS, "TOP/s")):
+        for zero in (False, True):
+            rate = rate_of(what, zero) / 1e12
+            out[f"{what}_{'zero' if zero else 'random'}_operands"] = {
+                unit: round(rate, 1), "frac_of_spec_peak": round(rate / peak, 4)}
+    for what in ("fma_f32", "exp_f32"):
+        rate = rate_of(what)
+        out[what] = {"lane_ops_per_s": round(rate / 1e12, 3) * 1e12,
+                     "cycles_per_wave_instruction_at_max_clock": round(simds * clock * 64 / rate, 2)}
+    out["note"] = ("register-only loops on every compute unit, eight waves per SIMD, each kind after 300 ms of "
+                   "the same load; MFMA operands change from one instruction to the next (random f16 / int8 from "
+                   "a hash, or all zero)")
+    return out
+
+
 def floors_line(torch, ctx, rocm, stream) -> dict:
     """What a launch of the headline GEMV's size costs with no product in it,
     over the same rotation of 96 copies as the headline, each a HIP graph of
@@ -620,7 +653,7 @@ def main():
     ap.add_argument("--calibrate-copy", action="store_true",
                     help=f"also run a {COPY_BYTES >> 20} MiB device copy (counter calibration)")
     ap.add_argument("--tune", type=int, default=0, help="tuner budget in ms (0 keeps reference variants)")
-    ap.add_argument("--only", choices=["pplx", "tune", "floors", "encoder"],
+    ap.add_argument("--only", choices=["pplx", "tune", "floors", "encoder", "probes"],
                     help="run one secondary line alone and print it (for profiling)")
     ap.add_argument("--tune-cache", help="with --only tune: a selection JSON from an earlier run to reuse")
     ap.add_argument("--tune-out", help="with --only tune: write the selection JSON here")
@@ -645,6 +678,9 @@ def main():
     if args.tune:
         ctx.tune(args.tune)
     log(f"[bench] device {ctx.info()}")
+    if args.only == "probes":
+        print(json.dumps({"unit_rate_probes": probes_line(ctx)}), flush=True)
+        return
     if args.only == "floors":
         stream = torch.cuda.Stream()
         ctx.set_stream(stream.cuda_stream)

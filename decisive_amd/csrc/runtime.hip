@@ -74,6 +74,7 @@ int32_t pplx_set_weight(dz_ctx *ctx, dz_pplx *p, const char *name, const void *p
 int32_t pplx_set_vector(dz_ctx *ctx, dz_pplx *p, const char *name, const float *values, size_t count);
 int32_t pplx_layer(dz_ctx *ctx, dz_pplx *p, int index, float *hidden, size_t n, const int32_t *markers_host,
                    size_t count);
+int32_t probe_rate(dz_ctx *ctx, int cus, const char *what, int zero, double *rate);
 int32_t pplx_set_residency(dz_ctx *ctx, dz_pplx *p, int32_t residency);
 int32_t pplx_residency_info(dz_ctx *ctx, dz_pplx *p, char *json, size_t cap);
 int32_t pplx_forward_rows(dz_ctx *ctx, dz_pplx *p, const void *rows_host, size_t n, const int32_t *markers,
@@ -992,6 +993,12 @@ int32_t dz_pplx_set_residency(dz_ctx *ctx, dz_pplx *model, int32_t residency) {
 int32_t dz_pplx_residency_info(dz_ctx *ctx, dz_pplx *model, char *json, size_t cap) {
     DZ_BEGIN(ctx);
     return dz::pplx_residency_info(ctx, model, json, cap);
+}
+
+int32_t dz_probe_rate(dz_ctx *ctx, const char *what, int32_t zero_operands, double *ops_per_second) {
+    DZ_BEGIN(ctx);
+    if (capturing(ctx)) return fail(ctx, DZ_INVALID_REQUEST, "synchronous call during stream capture");
+    return dz::probe_rate(ctx, ctx->cus, what, zero_operands, ops_per_second);
 }
 
 // ---- tuner ---------------------------------------------------------------------------

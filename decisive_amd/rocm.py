@@ -144,6 +144,7 @@ _SIGNATURES = {
     "dz_pplx_forward_rows": (I32, [P, P, P, SZ, P, SZ, P]),
     "dz_pplx_set_residency": (I32, [P, P, I32]),
     "dz_pplx_residency_info": (I32, [P, P, ctypes.c_char_p, SZ]),
+    "dz_probe_rate": (I32, [P, ctypes.c_char_p, I32, ctypes.POINTER(ctypes.c_double)]),
     "dz_tune": (I32, [P, U32, ctypes.c_char_p, ctypes.c_char_p, SZ]),
     "dz_select_variant": (I32, [P, ctypes.c_char_p, ctypes.c_char_p]),
 }
@@ -380,6 +381,12 @@ class Context:
 
     def select_variant(self, family: str, name: str):
         self._check(load().dz_select_variant(self.handle, family.encode(), name.encode()))
+
+    def probe_rate(self, what: str, zero_operands: bool = False) -> float:
+        """dz_probe_rate: the sustained operations per second of one unit."""
+        out = ctypes.c_double()
+        self._check(load().dz_probe_rate(self.handle, what.encode(), int(zero_operands), ctypes.byref(out)))
+        return out.value
 
 
 class Encoder:

@@ -421,6 +421,19 @@ int32_t dz_pplx_set_residency(dz_ctx *ctx, dz_pplx *model, int32_t residency);
  * and "max_in_flight_layers". DZ_RESOURCE_LIMIT when cap is too small. */
 int32_t dz_pplx_residency_info(dz_ctx *ctx, dz_pplx *model, char *json, size_t cap);
 
+/* ---- rate probes (diagnostics; no reference counterpart) ------------------------- */
+
+/* The sustained rate of one unit of this device, from a register-only loop
+ * over every compute unit (eight waves per SIMD), as operations per second:
+ *   "mfma_f16"  v_mfma_f32_16x16x32_f16 FLOP/s, successive instructions on
+ *               different random operands (zero_operands 1: all-zero ones)
+ *   "mfma_i8"   v_mfma_i32_32x32x32_i8 OP/s, the same way
+ *   "fma_f32"   v_fma_f32 lane operations per second (zero_operands 0)
+ *   "exp_f32"   v_exp_f32 lane operations per second (zero_operands 0)
+ * These are the ceilings the kernels' roofline fractions are read against
+ * beside the published peaks. Synchronous; not recordable under capture. */
+int32_t dz_probe_rate(dz_ctx *ctx, const char *what, int32_t zero_operands, double *ops_per_second);
+
 /* ---- kernel tuner (webgpu/checkpoint.rs:95-294, 428-652) ------------------------ */
 
 /* Times the tile variants of every tuned kernel family within budget_ms and

@@ -105,7 +105,8 @@ def test_layernorm_f16_rows(ctx, oracle, d, rows):
     assert np.allclose(got, ref, atol=1e-2, rtol=2e-3)
 
 
-@pytest.mark.parametrize("batch,seq,heads", [(1, 64, 1), (2, 100, 3), (1, 1024, 2), (3, 300, 2), (1, 513, 1), (2, 1, 2)])
+@pytest.mark.parametrize("batch,seq,heads", [(1, 64, 1), (2, 100, 3), (1, 1024, 2), (3, 300, 2), (1, 513, 1), (2, 1, 2),
+                                             (1, 128, 1), (1, 129, 2)])
 def test_attention_matches_closed_form(ctx, oracle, batch, seq, heads):
     torch = pytest.importorskip("torch")
     rng = np.random.default_rng(seq)

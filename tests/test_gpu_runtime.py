@@ -188,3 +188,17 @@ def test_stream_change_waits_for_products_on_the_old_stream(ctx, oracle):
         else:
             assert bits_equal(got, want), i
     w.free()
+
+
+def test_rate_probes_report_rates_and_reject_unknown_kinds(ctx):
+    """dz_probe_rate: positive rates for every kind; all-zero MFMA operands are
+    not slower than random ones beyond noise; unknown kinds and zero operands
+    on the VALU kinds are INVALID_PARAMETERS."""
+    rates = {w: ctx.probe_rate(w) for w in ("mfma_f16", "mfma_i8", "fma_f32", "exp_f32")}
+    assert all(r > 0 for r in rates.values()), rates
+    # a transcendental costs more than a fused multiply-add
+    assert rates["exp_f32"] < rates["fma_f32"]
+    for what, zero in (("mfma_f64", False), ("fma_f32", True)):
+        with pytest.raises(rocm.DzError) as e:
+            ctx.probe_rate(what, zero)
+        assert e.value.code == "INVALID_PARAMETERS"
