@@ -1415,9 +1415,9 @@ __global__ __launch_bounds__(WGM *WGN * 64) void w4a16_pipe_kernel(
     constexpr int TM = BM / WGM, TN = BN / WGN, MB = TM / 16, NT = TN / 16;
     constexpr int XSTAGE = BM * 256, WSTAGE = BN / 16 * 1024;
     constexpr int XPW = BM / 4 / WAVES;   // 4-row activation DMA instructions per wave per step
-    constexpr int WPW = BN / 16 / WAVES;  // code-chunk DMA instructions per wave per step
+    constexpr int WPW = (BN / 16 + WAVES - 1) / WAVES;  // code-chunk DMA instructions per wave per step (at most)
     static_assert(XPW * 4 * WAVES == BM && XPW % 4 == 0, "a wave's first DMA row is a multiple of 16");
-    static_assert(WPW * 16 * WAVES == BN && WPW >= 1, "code chunks split evenly over the waves");
+    static_assert(WPW * 16 * WAVES >= BN && WPW >= 1, "every code chunk has a wave");
     static_assert(MB % 2 == 0, "activation fragments are read in two halves");
     __shared__ __align__(16) uint8_t xs[2 * XSTAGE];
     __shared__ __align__(16) uint8_t ws[2 * WSTAGE];
@@ -1470,9 +1470,10 @@ __global__ __launch_bounds__(WGM *WGN * 64) void w4a16_pipe_kernel(
                 const uint32_t voff = xlane + (uint32_t)(blk * 4 * k * 2 + kk * 2) + (uint32_t)(c * 16);
                 dma16(__builtin_amdgcn_readfirstlane(xs_lds + stage * XSTAGE + blk * 1024), voff, rx);
             } else {
-                const int t = wave * WPW + (p - XPW);
-                dma16(__builtin_amdgcn_readfirstlane(ws_lds + stage * WSTAGE + t * 1024),
-                      (uint32_t)((t * kbs + kb) * 1024 + lane * 16), rw);
+                const int t = wave * WPW + (p - XPW);  // uniform; past the tile's chunks when BN / 16 is not a multiple of WAVES
+                if (BN / 16 % WAVES == 0 || t < BN / 16)
+                    dma16(__builtin_amdgcn_readfirstlane(ws_lds + stage * WSTAGE + t * 1024),
+                          (uint32_t)((t * kbs + kb) * 1024 + lane * 16), rw);
             }
         }
     };
@@ -2056,7 +2057,8 @@ inline unsigned cdiv(size_t a, size_t b) { return (unsigned)((a + b - 1) / b); }
 
 const char *const kGemvNames[] = {"w16", "w8"};
 const char *const kGemmNames[] = {"pipe-auto",   "256x256p2w8", "128x128p2w4", "128x256p2w8",
-                                   "256x128w2x2", "128x128w2x2", "128x64w2x2", "256x256p2w8-persist"};
+                                   "256x128w2x2", "128x128w2x2", "128x64w2x2", "256x256p2w8-persist",
+                                   "256x192p2w8-persist"};
 const char *const kI8Names[] = {"256x256p2w8", "256x256p4k64w8", "256x128p3w8", "256x128p3",
                                  "128x128w2x2", "256x128w2x2", "64x64w2x2", "256x256p2w8-stream",
                                  "256x256p2w8-stream-mid", "256x128k64p2-stream2"};
@@ -2155,7 +2157,9 @@ bool w4a16_pipe_launch(const Weight &w, const half_t *x, int m, void *y, const h
 
 // Variants 0-3 are the pipelined kernel: "auto", 256x256 tiles on 8 waves
 // (one block per CU), 128x128 tiles on 4 waves (two blocks per CU) and
-// 128x256 tiles on 8 waves. "auto" runs 256x256 tiles over the leading
+// 128x256 tiles on 8 waves. "auto" runs persistent 256x256 tiles when they
+// fill two or more whole waves of compute units, else persistent 256x192
+// tiles when those do, else 256x256 tiles over the leading
 // columns that fill whole waves of compute units and 128x256 tiles over the
 // rest (one launch each), or, below one wave of 256x256 tiles, the largest of
 // 128x256 and 128x128 that gives at least one tile per unit. 4-6 stage
@@ -2169,9 +2173,13 @@ void gemm_dispatch(const Weight &w, const half_t *x, int m, void *y, const half_
         case 0: {
             const unsigned cus = (unsigned)device_cus();
             const unsigned tm = cdiv(m, 256), tn = cdiv(w.rows, 256);
+            const unsigned t192 = w.rows % 192 == 0 ? tm * (unsigned)(w.rows / 192) : 0;
             if (tm * tn >= 2 * cus && (tm * tn) % cus == 0) {
                 // whole waves of 256x256 tiles, two or more: one persistent block per compute unit
                 if (w4a16_pipe_launch<256, 256, 2, 4, EPI, true>(w, x, m, y, res, s)) return;
+            } else if (t192 >= 2 * cus && t192 % cus == 0) {
+                // whole waves of 256x192 tiles instead (the encoder's QKV projection: one launch)
+                if (w4a16_pipe_launch<256, 192, 2, 4, EPI, true>(w, x, m, y, res, s)) return;
             } else if (tm * tn >= cus) {
                 // 256-column blocks that fill whole waves; the rest on 128x256 tiles
                 unsigned lead = tn;
@@ -2191,6 +2199,7 @@ void gemm_dispatch(const Weight &w, const half_t *x, int m, void *y, const half_
         case 2: if (w4a16_pipe_launch<128, 128, 2, 2, EPI>(w, x, m, y, res, s)) return; break;
         case 3: if (w4a16_pipe_launch<128, 256, 2, 4, EPI>(w, x, m, y, res, s)) return; break;
         case 7: if (w4a16_pipe_launch<256, 256, 2, 4, EPI, true>(w, x, m, y, res, s)) return; break;
+        case 8: if (w4a16_pipe_launch<256, 192, 2, 4, EPI, true>(w, x, m, y, res, s)) return; break;
         case 5: gemm_launch<128, 128, 2, 2, EPI>(w, x, m, y, res, s); return;
         case 6: gemm_launch<128, 64, 2, 2, EPI>(w, x, m, y, res, s); return;
         default: break;
@@ -2239,7 +2248,7 @@ void gv_launch(const Weight &w, const void *a, const float *sa, int m, int abits
 int variant_count(const char *family) {
     std::string f(family);
     if (f == "gemv") return 2;
-    if (f == "gemm_w4a16") return 8;
+    if (f == "gemm_w4a16") return 9;
     if (f == "i8_gemm") return 10;
     if (f == "grouped") return 9;
     if (f == "mlp") return 6;

@@ -354,7 +354,7 @@ def test_w4a16_rejects_misaligned_activations(ctx, oracle):
 
 
 W4A16_VARIANTS = ("pipe-auto", "256x256p2w8", "128x128p2w4", "128x256p2w8", "256x128w2x2", "128x128w2x2",
-                  "128x64w2x2", "256x256p2w8-persist")
+                  "128x64w2x2", "256x256p2w8-persist", "256x192p2w8-persist")
 
 
 @pytest.mark.parametrize("layout", [rocm.Q4_G32_F16, rocm.Q4_G64_F32])
@@ -473,10 +473,11 @@ def test_w4a16_f16_output_rejects_bad_arguments(ctx, oracle):
 
 @pytest.mark.parametrize("n", [3072, 3120])
 def test_w4a16_column_split_matches_register_kernel(ctx, oracle, n):
-    """M=8192, K=1024: 256x256 tiles fill whole waves of compute units over
-    the leading columns and 128x256 tiles take the rest (two launches); the
-    bits equal the register-staged kernel's, and sampled rows the float64
-    product of the dequantized weights."""
+    """M=8192, K=1024: n = 3072 runs on persistent 256x192 tiles (two whole
+    waves of compute units, the encoder's QKV shape); at n = 3120 256x256
+    tiles fill whole waves over the leading columns and 128x256 tiles take the
+    rest (two launches). The bits equal the register-staged kernel's, and
+    sampled rows the float64 product of the dequantized weights."""
     torch = pytest.importorskip("torch")
     m, k = 8192, 1024
     g = torch.Generator(device="cuda").manual_seed(n)
