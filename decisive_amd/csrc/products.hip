@@ -2058,7 +2058,7 @@ inline unsigned cdiv(size_t a, size_t b) { return (unsigned)((a + b - 1) / b); }
 const char *const kGemvNames[] = {"w16", "w8"};
 const char *const kGemmNames[] = {"pipe-auto",   "256x256p2w8", "128x128p2w4", "128x256p2w8",
                                    "256x128w2x2", "128x128w2x2", "128x64w2x2", "256x256p2w8-persist",
-                                   "256x192p2w8-persist"};
+                                   "256x192p2w8-persist", "256x128p2w8"};
 const char *const kI8Names[] = {"256x256p2w8", "256x256p4k64w8", "256x128p3w8", "256x128p3",
                                  "128x128w2x2", "256x128w2x2", "64x64w2x2", "256x256p2w8-stream",
                                  "256x256p2w8-stream-mid", "256x128k64p2-stream2"};
@@ -2162,7 +2162,7 @@ bool w4a16_pipe_launch(const Weight &w, const half_t *x, int m, void *y, const h
 // tiles when those do, else 256x256 tiles over the leading
 // columns that fill whole waves of compute units and 128x256 tiles over the
 // rest (one launch each), or, below one wave of 256x256 tiles, the largest of
-// 128x256 and 128x128 that gives at least one tile per unit. 4-6 stage
+// 256x128, 128x256 and 128x128 that gives at least one tile per unit. 4-6 stage
 // through registers. All give the same bits (same f16 dequantization, one MFMA per
 // 32-k run in k order); the pipelined ones need k % 128 == 0 and fall back to
 // 256x128w2x2 otherwise.
@@ -2188,6 +2188,10 @@ void gemm_dispatch(const Weight &w, const half_t *x, int m, void *y, const half_
                 if (w4a16_pipe_launch<256, 256, 2, 4, EPI>(w, x, m, y, res, s, 0, c1) &&
                     w4a16_pipe_launch<128, 256, 2, 4, EPI>(w, x, m, y, res, s, c1, w.rows - c1))
                     return;
+            } else if (tm * cdiv(w.rows, 128) >= cus) {
+                // 256x128 tiles: per MAC half the dequantization of 128x256 tiles
+                // (the encoder's N = 1024 projections: 25 against 27 us at K = 1024, 65 against 73 at 4096)
+                if (w4a16_pipe_launch<256, 128, 2, 4, EPI>(w, x, m, y, res, s)) return;
             } else if (cdiv(m, 128) * cdiv(w.rows, 256) >= cus) {
                 if (w4a16_pipe_launch<128, 256, 2, 4, EPI>(w, x, m, y, res, s)) return;
             } else {
@@ -2200,6 +2204,7 @@ void gemm_dispatch(const Weight &w, const half_t *x, int m, void *y, const half_
         case 3: if (w4a16_pipe_launch<128, 256, 2, 4, EPI>(w, x, m, y, res, s)) return; break;
         case 7: if (w4a16_pipe_launch<256, 256, 2, 4, EPI, true>(w, x, m, y, res, s)) return; break;
         case 8: if (w4a16_pipe_launch<256, 192, 2, 4, EPI, true>(w, x, m, y, res, s)) return; break;
+        case 9: if (w4a16_pipe_launch<256, 128, 2, 4, EPI>(w, x, m, y, res, s)) return; break;
         case 5: gemm_launch<128, 128, 2, 2, EPI>(w, x, m, y, res, s); return;
         case 6: gemm_launch<128, 64, 2, 2, EPI>(w, x, m, y, res, s); return;
         default: break;
@@ -2248,7 +2253,7 @@ void gv_launch(const Weight &w, const void *a, const float *sa, int m, int abits
 int variant_count(const char *family) {
     std::string f(family);
     if (f == "gemv") return 2;
-    if (f == "gemm_w4a16") return 9;
+    if (f == "gemm_w4a16") return 10;
     if (f == "i8_gemm") return 10;
     if (f == "grouped") return 9;
     if (f == "mlp") return 6;

@@ -456,7 +456,8 @@ int32_t dz_tune(dz_ctx *ctx, uint32_t budget_ms, const char *cache_in, char *cac
  * gives the same bits):
  *   "gemv"        w16, w8
  *   "gemm_w4a16"  pipe-auto, 256x256p2w8, 128x128p2w4, 128x256p2w8, 256x128w2x2,
- *                 128x128w2x2, 128x64w2x2, 256x256p2w8-persist, 256x192p2w8-persist
+ *                 128x128w2x2, 128x64w2x2, 256x256p2w8-persist, 256x192p2w8-persist,
+ *                 256x128p2w8
  *   "i8_gemm"     256x256p2w8, 256x256p4k64w8, 256x128p3w8, 256x128p3, 128x128w2x2,
  *                 256x128w2x2, 64x64w2x2, 256x256p2w8-stream, 256x256p2w8-stream-mid,
  *                 256x128k64p2-stream2 (the "-stream" forms are persistent: one

@@ -254,7 +254,7 @@ def test_encoder_bits_do_not_depend_on_the_gemm_variant(ctx):
     ids = np.random.default_rng(5).integers(0, cfg.vocab, batch * seq).astype(np.int32)
     outs = []
     for name in ("pipe-auto", "256x256p2w8", "128x128p2w4", "128x256p2w8", "256x128w2x2", "128x128w2x2",
-                  "128x64w2x2", "256x256p2w8-persist", "256x192p2w8-persist"):
+                  "128x64w2x2", "256x256p2w8-persist", "256x192p2w8-persist", "256x128p2w8"):
         ctx.select_variant("gemm_w4a16", name)
         out = empty((batch, cfg.hidden), torch.float32)
         enc.forward(dev(ids), batch, seq, out)

@@ -354,7 +354,7 @@ def test_w4a16_rejects_misaligned_activations(ctx, oracle):
 
 
 W4A16_VARIANTS = ("pipe-auto", "256x256p2w8", "128x128p2w4", "128x256p2w8", "256x128w2x2", "128x128w2x2",
-                  "128x64w2x2", "256x256p2w8-persist", "256x192p2w8-persist")
+                  "128x64w2x2", "256x256p2w8-persist", "256x192p2w8-persist", "256x128p2w8")
 
 
 @pytest.mark.parametrize("layout", [rocm.Q4_G32_F16, rocm.Q4_G64_F32])
