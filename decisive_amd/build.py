@@ -30,6 +30,10 @@ FLAGS = [
     "-ffp-contract=off",
     # no packed FP32 instructions anywhere in device code
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in VGPRs: in the AGPR form the compiler copied every int32
+    # group dot of the bit-exact products back with v_accvgpr_read before the
+    # fold (4 of about 18 VALU instructions per MFMA in those VALU-bound loops)
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wno-unused-result",
     "-Wno-unused-value",
 ]
