@@ -41,6 +41,7 @@ Weight &weight_mut(dz_weight *h);
 int32_t weight_upload(dz_ctx *ctx, const void *packed, size_t bytes, int32_t layout, size_t rows, size_t cols,
                       dz_weight **out);
 void weight_free(dz_weight *h);
+int32_t weight_concat_rows(dz_ctx *ctx, const dz_weight *const *parts, int count, dz_weight **out);
 int32_t ctx_readout_rows(dz_ctx *ctx, const Weight &w, const float *norm, const void *hidden, int dtype,
                          const int32_t *select, size_t rows, float eps, float *logits);
 int ctx_variant(dz_ctx *ctx, const char *family);
@@ -93,7 +94,7 @@ __global__ void conv_silu_kernel(const float *__restrict__ x, int n, int width, 
 // 1/sqrt(ld)) and their dot product; threads below lh compute the decay g and
 // beta of head h. Record (t, h) of gb holds {g, beta, k.q of h's key head, log g}.
 __global__ void delta_prep_kernel(const float *__restrict__ conv, int lh, int lk, const float *__restrict__ a,
-                                  const float *__restrict__ b, const float *__restrict__ decay,
+                                  const float *__restrict__ b, int ab_ld, const float *__restrict__ decay,
                                   const float *__restrict__ dt, float *__restrict__ qhat,
                                   float *__restrict__ khat, float *__restrict__ gb) {
     const int t = blockIdx.x, wave = threadIdx.x / 64, lane = threadIdx.x % 64;
@@ -117,11 +118,11 @@ __global__ void delta_prep_kernel(const float *__restrict__ conv, int lh, int lk
         if (lane < per) gb[((size_t)t * lh + wave * per + lane) * 4 + 2] = kq;
     }
     for (int h = threadIdx.x; h < lh; h += blockDim.x) {
-        const float x = __fadd_rn(a[(size_t)t * lh + h], dt[h]);
+        const float x = __fadd_rn(a[(size_t)t * ab_ld + h], dt[h]);
         const float softplus = x > 20.0f ? x : log1pf(expf(x));
         const float logg = __fmul_rn(-decay[h], softplus);
         gb[((size_t)t * lh + h) * 4] = expf(logg);
-        gb[((size_t)t * lh + h) * 4 + 1] = sigmoid_ref(b[(size_t)t * lh + h]);
+        gb[((size_t)t * lh + h) * 4 + 1] = sigmoid_ref(b[(size_t)t * ab_ld + h]);
         gb[((size_t)t * lh + h) * 4 + 3] = logg;
     }
 }
@@ -497,15 +498,16 @@ __global__ __launch_bounds__(256) void delta_chunk_scan_kernel(const float *__re
 template <bool CODES>
 __global__ __launch_bounds__(64) void delta_gate_kernel(const float *__restrict__ heads, int n, int lh,
                                                         const float *__restrict__ norm,
-                                                        const float *__restrict__ z, float *__restrict__ ctx,
+                                                        const float *__restrict__ z, int z_ld, float *__restrict__ ctx,
                                                         int8_t *__restrict__ q, float *__restrict__ qs, int *bad) {
     const int t = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
     const float *src = heads + ((size_t)h * n + t) * kLd;
     const float s0 = src[lane], s1 = src[lane + 64];
     const float scale = rsqrt_rn(__fadd_rn(wave_sum(s0 * s0 + s1 * s1) / (float)kLd, 1e-6f));
     const size_t at = (size_t)t * lh * kLd + (size_t)h * kLd;
-    const float v0 = __fmul_rn(__fmul_rn(__fmul_rn(s0, scale), norm[lane]), silu_ref(z[at + lane]));
-    const float v1 = __fmul_rn(__fmul_rn(__fmul_rn(s1, scale), norm[lane + 64]), silu_ref(z[at + lane + 64]));
+    const float *zr = z + (size_t)t * z_ld + (size_t)h * kLd;
+    const float v0 = __fmul_rn(__fmul_rn(__fmul_rn(s0, scale), norm[lane]), silu_ref(zr[lane]));
+    const float v1 = __fmul_rn(__fmul_rn(__fmul_rn(s1, scale), norm[lane + 64]), silu_ref(zr[lane + 64]));
     if constexpr (!CODES) {
         ctx[at + lane] = v0;
         ctx[at + lane + 64] = v1;
@@ -781,6 +783,10 @@ struct dz_pplx {
         dz_weight *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr;
         float *qnorm = nullptr, *knorm = nullptr;
         dz_weight *gate = nullptr, *up = nullptr, *down = nullptr;
+        // in_proj_z, in_proj_a and in_proj_b as one weight (rows z, then a, then
+        // b), so one product launch covers the three: derived from them, while
+        // the weights are resident
+        dz_weight *zab = nullptr;
     };
     std::vector<Layer> layers;
     dz_weight *readout = nullptr;
@@ -882,7 +888,7 @@ int32_t ensure_capacity(dz_ctx *ctx, dz_pplx *p, size_t n) {
     get(&p->hidden, n * d * 4);
     get(&p->normed, n * d * 4);
     get(&p->wide, n * wide * 4);
-    get(&p->z, n * lv * 4);
+    get(&p->z, n * (lv + 2 * ((size_t)c.delta_heads + 15) / 16 * 16) * 4);  // z, or z | a | b of the joined weight
     get(&p->ab, n * c.delta_heads * 2 * 4);
     get(&p->conv_out, n * cw * 4);
     get(&p->qhat, n * c.delta_key_heads * kLd * 4);
@@ -957,7 +963,8 @@ void pplx_destroy(dz_ctx *ctx, dz_pplx *p) {
     }
     streaming_release(p);
     for (auto &l : p->layers) {
-        for (dz_weight *w : {l.qkv, l.z, l.a, l.b, l.out, l.q, l.k, l.v, l.o, l.gate, l.up, l.down}) weight_free(w);
+        for (dz_weight *w : {l.qkv, l.z, l.a, l.b, l.out, l.q, l.k, l.v, l.o, l.gate, l.up, l.down, l.zab})
+            weight_free(w);
         for (float *f : {l.input_norm, l.post_norm, l.conv, l.decay, l.dt, l.norm, l.qnorm, l.knorm})
             if (f) hipFree(f);
     }
@@ -993,6 +1000,19 @@ int32_t pplx_create(dz_ctx *ctx, const dz_pplx_config *cfg, dz_pplx **out) {
     }
     *out = p;
     return DZ_OK;
+}
+
+// (Re)builds a delta layer's joined z | a | b weight from its three parts,
+// while the weights are resident and the parts share one layout; otherwise
+// the layer runs the three products. A joining that fails only costs speed.
+void join_zab(dz_ctx *ctx, dz_pplx *p, dz_pplx::Layer &L) {
+    weight_free(L.zab);
+    L.zab = nullptr;
+    if (p->st.on || L.attention || !L.z || !L.a || !L.b) return;
+    const auto kind = weight_of(L.z).kind;
+    if (weight_of(L.a).kind != kind || weight_of(L.b).kind != kind) return;
+    const dz_weight *parts[3] = {L.z, L.a, L.b};
+    if (weight_concat_rows(ctx, parts, 3, &L.zab) != DZ_OK) L.zab = nullptr;
 }
 
 int32_t pplx_set_weight(dz_ctx *ctx, dz_pplx *p, const char *name, const void *packed, size_t bytes, int32_t layout,
@@ -1063,6 +1083,8 @@ int32_t pplx_set_weight(dz_ctx *ctx, dz_pplx *p, const char *name, const void *p
     }
     weight_free(*slot);
     *slot = w;
+    if (layer >= 0 && (slot == &p->layers[layer].z || slot == &p->layers[layer].a || slot == &p->layers[layer].b))
+        join_zab(ctx, p, p->layers[layer]);
     return DZ_OK;
 }
 
@@ -1208,6 +1230,7 @@ int32_t stream_on(dz_ctx *ctx, dz_pplx *p) {
     st.held[0] = st.held[1] = -1;
     st.uploads = st.reuses = st.upload_bytes = 0;
     st.on = true;
+    for (auto &L : p->layers) join_zab(ctx, p, L);  // frees the joined copies: the banks hold the parts
     return DZ_OK;
 }
 
@@ -1248,6 +1271,7 @@ int32_t stream_off(dz_ctx *ctx, dz_pplx *p) {
             x.scales = fresh[k++];
         }
     streaming_release(p);
+    for (auto &L : p->layers) join_zab(ctx, p, L);
     return DZ_OK;
 }
 
@@ -1401,11 +1425,26 @@ int32_t delta_layer(dz_ctx *ctx, dz_pplx *p, const dz_pplx::Layer &L, size_t n) 
     int *flag = nullptr;
     int32_t rc = layer_norm(ctx, p, L.input_norm, n, false, &codes, &flag);
     if (rc) return rc;
-    if (codes) {  // the four input projections share the norm's codes
+    // z, a and b: one product of the joined weight when it exists, its output
+    // rows z | a | b (each part from a 16-row tile on), else three products
+    const float *za = p->z, *aa = p->ab, *ba = p->ab + n * lh;
+    int z_ld = (int)(lh * kLd), ab_ld = (int)lh;
+    if (L.zab) {
+        z_ld = ab_ld = weight_of(L.zab).rows;
+        aa = p->z + lh * kLd;
+        ba = aa + (lh + 15) / 16 * 16;
+    }
+    if (codes) {  // the input projections share the norm's codes
         rc = normed_product(ctx, p, L.qkv, true, flag, n, p->wide);
-        if (!rc) rc = normed_product(ctx, p, L.z, true, flag, n, p->z);
-        if (!rc) rc = normed_product(ctx, p, L.a, true, flag, n, p->ab);
-        if (!rc) rc = normed_product(ctx, p, L.b, true, flag, n, p->ab + n * lh);
+        if (L.zab) {
+            if (!rc) rc = normed_product(ctx, p, L.zab, true, flag, n, p->z);
+        } else {
+            if (!rc) rc = normed_product(ctx, p, L.z, true, flag, n, p->z);
+            if (!rc) rc = normed_product(ctx, p, L.a, true, flag, n, p->ab);
+            if (!rc) rc = normed_product(ctx, p, L.b, true, flag, n, p->ab + n * lh);
+        }
+    } else if (L.zab) {
+        rc = dz_linear_pair(ctx, L.qkv, L.zab, p->normed, n, p->wide, p->z, DZ_W4A8);
     } else {
         rc = dz_linear_pair(ctx, L.qkv, L.z, p->normed, n, p->wide, p->z, DZ_W4A8);
         if (!rc) rc = dz_linear_pair(ctx, L.a, L.b, p->normed, n, p->ab, p->ab + n * lh, DZ_W4A8);
@@ -1414,8 +1453,7 @@ int32_t delta_layer(dz_ctx *ctx, dz_pplx *p, const dz_pplx::Layer &L, size_t n) 
     hipLaunchKernelGGL(conv_silu_kernel, dim3(blocks_of(n * cw, 256)), dim3(256), 0, s, p->wide, (int)n, (int)cw,
                        L.conv, p->conv_out);
     hipLaunchKernelGGL(delta_prep_kernel, dim3((unsigned)n), dim3(64 * c.delta_key_heads), 0, s, p->conv_out,
-                       c.delta_heads, c.delta_key_heads, p->ab, p->ab + n * lh, L.decay, L.dt, p->qhat, p->khat,
-                       p->gb);
+                       c.delta_heads, c.delta_key_heads, aa, ba, ab_ld, L.decay, L.dt, p->qhat, p->khat, p->gb);
     launch_delta_scan(ctx, p, n, s);
     // out_proj adds onto the hidden rows in its epilogue; then the gate hands it
     // A8 codes (in the MLP's code buffer, free until the MLP) instead of f32 rows
@@ -1425,11 +1463,11 @@ int32_t delta_layer(dz_ctx *ctx, dz_pplx *p, const dz_pplx::Layer &L, size_t n) 
         rc = ctx_product_flag(ctx, &gflag);
         if (rc) return rc;
         hipLaunchKernelGGL(delta_gate_kernel<true>, dim3((unsigned)n, c.delta_heads), dim3(64), 0, s, p->heads,
-                           (int)n, c.delta_heads, L.norm, p->z, nullptr, p->codes, p->code_scales, gflag);
+                           (int)n, c.delta_heads, L.norm, za, z_ld, nullptr, p->codes, p->code_scales, gflag);
         return product_add(ctx, L.out, nullptr, p->codes, p->code_scales, n, p->hidden, p->projected, gflag);
     }
     hipLaunchKernelGGL(delta_gate_kernel<false>, dim3((unsigned)n, c.delta_heads), dim3(64), 0, s, p->heads, (int)n,
-                       c.delta_heads, L.norm, p->z, p->ctx, nullptr, nullptr, nullptr);
+                       c.delta_heads, L.norm, za, z_ld, p->ctx, nullptr, nullptr, nullptr);
     return product_add(ctx, L.out, p->ctx, nullptr, nullptr, n, p->hidden, p->projected);
 }
 
@@ -1569,14 +1607,16 @@ int32_t pplx_set_residency(dz_ctx *ctx, dz_pplx *p, int32_t residency) {
 int32_t pplx_residency_info(dz_ctx *ctx, dz_pplx *p, char *json, size_t cap) {
     if (!p) return ctx_fail(ctx, DZ_INVALID_REQUEST, "null pointer");
     const auto &st = p->st;
-    size_t resident = 0;
-    for (const auto &L : p->layers)
+    size_t resident = 0, joined = 0;
+    for (const auto &L : p->layers) {
         for (dz_weight *w : projections(L))
             if (w) resident += weight_of(w).code_bytes + weight_of(w).scale_bytes;
+        if (L.zab) joined += weight_of(L.zab).code_bytes + weight_of(L.zab).scale_bytes;
+    }
     auto held = [&](int b) { return st.held[b] < 0 ? std::string("null") : std::to_string(st.held[b]); };
     std::string s = "{\"residency\":\"" + std::string(st.on ? "streamed" : "resident") + "\"";
     s += ",\"layer_weight_bytes\":" + std::to_string(resident);
-    s += ",\"device_layer_weight_bytes\":" + std::to_string(st.on ? 2 * st.bank_bytes : resident);
+    s += ",\"device_layer_weight_bytes\":" + std::to_string(st.on ? 2 * st.bank_bytes : resident + joined);
     s += ",\"host_layer_weight_bytes\":" + std::to_string(st.host_bytes);
     s += ",\"banks\":" + std::to_string(st.on ? 2 : 0) + ",\"bank_bytes\":" + std::to_string(st.bank_bytes);
     s += ",\"bank_layers\":[" + held(0) + "," + held(1) + "]";

@@ -1087,6 +1087,44 @@ int32_t weight_quantize(dz_ctx *ctx, const void *values, int dtype, size_t rows,
     return dz_weight_quantize(ctx, values, dtype, rows, cols, bits, group, out);
 }
 void weight_free(dz_weight *h) { free_weight(h); }
+// One weight holding the parts' rows in order, each part starting on a
+// 16-row tile: part i's rows begin at row sum_{j<i} ceil16(rows_j), and the
+// rows between parts are the parts' own padding (code 0, scale 0), whose
+// products are 0. Same kind and columns for all parts. The native layouts are
+// tile-major, so the codes and scales are the parts' arrays one after the
+// other. Synchronous.
+int32_t weight_concat_rows(dz_ctx *ctx, const dz_weight *const *parts, int count, dz_weight **out) {
+    *out = nullptr;
+    if (count < 1) return fail(ctx, DZ_INVALID_REQUEST, "no weights to join");
+    size_t rows = 0;
+    for (int i = 0; i < count; i++) {
+        const Weight &p = parts[i]->w;
+        if (p.kind != parts[0]->w.kind || p.cols != parts[0]->w.cols)
+            return fail(ctx, DZ_INVALID_PARAMETERS, "joined weights need one layout and one width");
+        rows += i + 1 < count ? (size_t)p.np : (size_t)p.rows;
+    }
+    dz_weight *h = nullptr;
+    int32_t rc = alloc_weight(ctx, parts[0]->w.kind, rows, (size_t)parts[0]->w.cols, &h);
+    if (rc) return rc;
+    size_t co = 0, so = 0;
+    hipError_t e = hipSuccess;
+    for (int i = 0; i < count && e == hipSuccess; i++) {
+        const Weight &p = parts[i]->w;
+        e = hipMemcpyAsync(h->w.codes + co, p.codes, p.code_bytes, hipMemcpyDeviceToDevice, ctx->stream);
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(h->w.scales + so, p.scales, p.scale_bytes, hipMemcpyDeviceToDevice, ctx->stream);
+        co += p.code_bytes;
+        so += p.scale_bytes;
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        hipStreamSynchronize(ctx->stream);
+        free_weight(h);
+        return hip_fail(ctx, e, "joined weight");
+    }
+    *out = h;
+    return DZ_OK;
+}
 int32_t weight_upload(dz_ctx *ctx, const void *packed, size_t bytes, int32_t layout, size_t rows, size_t cols,
                       dz_weight **out) {
     return dz_weight_upload(ctx, packed, bytes, layout, rows, cols, out);

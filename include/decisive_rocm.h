@@ -415,7 +415,8 @@ int32_t dz_pplx_forward_rows(dz_ctx *ctx, dz_pplx *model, const void *rows_host,
 int32_t dz_pplx_set_residency(dz_ctx *ctx, dz_pplx *model, int32_t residency);
 /* streaming.rs:176-191 diagnostics as JSON: "residency", "layer_weight_bytes"
  * (every layer projection), "device_layer_weight_bytes" (what the device
- * holds for them now), "host_layer_weight_bytes", "banks", "bank_bytes",
+ * holds for them now: resident, the projections plus the joined z|a|b copy
+ * of each delta layer; streamed, the two banks), "host_layer_weight_bytes", "banks", "bank_bytes",
  * "bank_layers" (the layer each bank holds, or null), "layer_uploads",
  * "bank_reuses" (uploads into a bank that held another layer), "upload_bytes"
  * and "max_in_flight_layers". DZ_RESOURCE_LIMIT when cap is too small. */

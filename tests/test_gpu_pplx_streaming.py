@@ -142,3 +142,55 @@ def test_streaming_needs_every_layer_projection(ctx, model):
         assert p.residency_info()["residency"] == "resident"
     finally:
         p.close()
+
+
+def test_joined_delta_input_projections_follow_replacement(ctx, oracle, model):
+    """A resident model keeps each delta layer's in_proj_z, in_proj_a and
+    in_proj_b joined as one weight, which a streamed model does not: after a
+    and b of layer 0 are replaced, the resident run (one product over the
+    rebuilt joined weight) equals the streamed run (three products) bit for bit.
+    A part in another layout leaves the layer unjoined until it is replaced by
+    one in the common layout again."""
+    torch = pytest.importorskip("torch")
+    n = 77
+    hidden, heads = CFG["hidden"], CFG["delta_heads"]
+    rng = np.random.default_rng(91)
+    new = {}
+    for part in ("a", "b"):
+        raw = oracle.f32_to_bf16((rng.standard_normal((heads, hidden)) * 0.05).astype(np.float32))
+        new[part] = (f"language_model.layers.0.linear_attn.in_proj_{part}.weight", raw)
+    h = rng.standard_normal((n, hidden)).astype(np.float32)
+    resident = pplx_model.load(ctx, rocm, model)
+    streamed = pplx_model.load(ctx, rocm, model)
+
+    def run(p):
+        hd = dev(h)
+        p.layer(0, hd, n)
+        return host(ctx, hd).copy()
+
+    try:
+        joined = resident.residency_info()
+        assert joined["device_layer_weight_bytes"] > joined["layer_weight_bytes"]
+        before = run(resident)
+        streamed.set_residency(rocm.PPLX_STREAMED)
+        assert np.array_equal(bits(run(streamed)), bits(before))
+        for name, raw in new.values():
+            wire = oracle.pack_g64(raw, heads, hidden, 4)
+            resident.set_weight(name, wire, rocm.Q4_G64_F32, heads, hidden)
+            streamed.set_weight(name, wire, rocm.Q4_G64_F32, heads, hidden)
+        after = run(resident)
+        assert not np.array_equal(bits(after), bits(before))
+        assert np.array_equal(bits(after), bits(run(streamed)))
+        # b in Q8: layer 0 runs three products; back in Q4, joined again
+        name, raw = new["b"]
+        resident.set_weight(name, oracle.pack_g64(raw, heads, hidden, 8), rocm.Q8_G64_F32, heads, hidden)
+        split = resident.residency_info()
+        assert split["device_layer_weight_bytes"] - split["layer_weight_bytes"] < \
+            joined["device_layer_weight_bytes"] - joined["layer_weight_bytes"]
+        run(resident)
+        resident.set_weight(name, oracle.pack_g64(raw, heads, hidden, 4), rocm.Q4_G64_F32, heads, hidden)
+        assert resident.residency_info()["device_layer_weight_bytes"] == joined["device_layer_weight_bytes"]
+        assert np.array_equal(bits(run(resident)), bits(after))
+    finally:
+        resident.close()
+        streamed.close()
