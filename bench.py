@@ -569,7 +569,8 @@ def probes_line(ctx) -> dict:
     """Sustained unit rates from register-only loops (dz_probe_rate): the MFMA
     rates on random and on all-zero operands beside the published peaks, and
     the cycles per wave instruction of v_fma_f32 and v_exp_f32 at the
-    device's maximum clock (the attention softmax is bound by their ratio)."""
+    device's maximum clock (the attention softmax is bound by their ratio), and
+    the LDS read bandwidth per compute unit (ds_read_b128)."""
     info = ctx.info()
     simds, clock = info["compute_units"] * 4, info["clock_khz"] * 1e3
 
@@ -590,6 +591,9 @@ def probes_line(ctx) -> dict:
         rate = rate_of(what)
         out[what] = {"lane_ops_per_s": round(rate / 1e12, 3) * 1e12,
                      "cycles_per_wave_instruction_at_max_clock": round(simds * clock * 64 / rate, 2)}
+    rate = rate_of("lds_b128")
+    out["lds_b128"] = {"TB/s": round(rate / 1e12, 2),
+                       "bytes_per_clock_per_cu_at_max_clock": round(rate / (info["compute_units"] * clock), 1)}
     out["note"] = ("register-only loops on every compute unit, eight waves per SIMD, each kind after 300 ms of "
                    "the same load; MFMA operands change from one instruction to the next (random f16 / int8 from "
                    "a hash, or all zero)")

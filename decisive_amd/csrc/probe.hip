@@ -9,6 +9,8 @@
 //   mfma_i8   v_mfma_i32_32x32x32_i8, 4 independent accumulators per wave
 //   fma_f32   v_fma_f32, 8 independent chains per wave
 //   exp_f32   v_exp_f32, 8 independent chains per wave
+//   lds_b128  ds_read_b128 from LDS, 8 loads in flight per wave (bytes per
+//             second, not operations)
 // Operands are hashed from the thread index (or all zero, for the MFMA kinds
 // with zero_operands), so the data toggles as a GEMM's does. One timed launch
 // runs for several milliseconds; callers load the device first, since the
@@ -128,6 +130,33 @@ __global__ __launch_bounds__(kProbeThreads) void probe_valu_kernel(int iters, fl
     sink[t] = s;
 }
 
+// LDS read bandwidth: every wave reads 8 KB per iteration with ds_read_b128
+// (64 lanes x 16 bytes of one 1 KB row per instruction, no bank conflicts).
+// Lane l reads element (l + it) % 64 of each row, so the loads stay in the
+// loop; two v_xor3 per load keep every byte live.
+constexpr int kProbeLdsBytes = 8192;
+__global__ __launch_bounds__(kProbeThreads) void probe_lds_kernel(int iters, float *sink) {
+    __shared__ __align__(16) uint4_t buf[kProbeLdsBytes / 16];
+    const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+    for (int i = threadIdx.x; i < kProbeLdsBytes / 16; i += kProbeThreads) {
+        const uint32_t h = probe_hash(blockIdx.x * 4096 + i);
+        buf[i] = uint4_t{h, h ^ 0x9e3779b9u, h + 7u, h * 3u};
+    }
+    __syncthreads();
+    const int lane = threadIdx.x % 64;
+    uint32_t x0 = 0, x1 = 0;
+    for (int it = 0; it < iters; it++) {
+        const uint4_t *p = buf + ((lane + it) & 63);
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const uint4_t v = p[u * 64];
+            x0 = x0 ^ v[0] ^ v[1];
+            x1 = x1 ^ v[2] ^ v[3];
+        }
+    }
+    sink[t] = (float)(x0 ^ x1);
+}
+
 }  // namespace
 
 int32_t probe_rate(dz_ctx *ctx, int cus, const char *what, int zero, double *rate) {
@@ -158,9 +187,15 @@ int32_t probe_rate(dz_ctx *ctx, int cus, const char *what, int zero, double *rat
         per_iter = 8;
         iters = 16384;
         kernel = probe_valu_kernel<1>;
+    } else if (w == "lds_b128" && !zero) {
+        ops_per_inst = 64 * 16;  // bytes
+        per_iter = 8;
+        iters = 32768;
+        kernel = probe_lds_kernel;
     } else {
         return ctx_fail(ctx, DZ_INVALID_PARAMETERS,
-                        "probe is mfma_f16, mfma_i8 (zero_operands 0 or 1), fma_f32 or exp_f32 (zero_operands 0)");
+                        "probe is mfma_f16, mfma_i8 (zero_operands 0 or 1), fma_f32, exp_f32 or lds_b128 "
+                        "(zero_operands 0)");
     }
     const int blocks = cus * kProbeBlocksPerCu;
     hipStream_t s = ctx_stream(ctx);

@@ -431,6 +431,7 @@ int32_t dz_pplx_residency_info(dz_ctx *ctx, dz_pplx *model, char *json, size_t c
  *   "mfma_i8"   v_mfma_i32_32x32x32_i8 OP/s, the same way
  *   "fma_f32"   v_fma_f32 lane operations per second (zero_operands 0)
  *   "exp_f32"   v_exp_f32 lane operations per second (zero_operands 0)
+ *   "lds_b128"  ds_read_b128 bytes per second read from LDS (zero_operands 0)
  * These are the ceilings the kernels' roofline fractions are read against
  * beside the published peaks. Synchronous; not recordable under capture. */
 int32_t dz_probe_rate(dz_ctx *ctx, const char *what, int32_t zero_operands, double *ops_per_second);

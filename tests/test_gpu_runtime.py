@@ -194,11 +194,14 @@ def test_rate_probes_report_rates_and_reject_unknown_kinds(ctx):
     """dz_probe_rate: positive rates for every kind; all-zero MFMA operands are
     not slower than random ones beyond noise; unknown kinds and zero operands
     on the VALU kinds are INVALID_PARAMETERS."""
-    rates = {w: ctx.probe_rate(w) for w in ("mfma_f16", "mfma_i8", "fma_f32", "exp_f32")}
+    rates = {w: ctx.probe_rate(w) for w in ("mfma_f16", "mfma_i8", "fma_f32", "exp_f32", "lds_b128")}
     assert all(r > 0 for r in rates.values()), rates
     # a transcendental costs more than a fused multiply-add
     assert rates["exp_f32"] < rates["fma_f32"]
-    for what, zero in (("mfma_f64", False), ("fma_f32", True)):
+    # LDS reads: at least 32 bytes per clock per compute unit at a 1 GHz clock, at most 1 KB at 3 GHz
+    cus = ctx.info()["compute_units"]
+    assert cus * 32 * 1e9 < rates["lds_b128"] < cus * 1024 * 3e9, rates["lds_b128"]
+    for what, zero in (("mfma_f64", False), ("fma_f32", True), ("lds_b128", True)):
         with pytest.raises(rocm.DzError) as e:
             ctx.probe_rate(what, zero)
         assert e.value.code == "INVALID_PARAMETERS"
