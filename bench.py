@@ -604,8 +604,9 @@ def floors_line(torch, ctx, rocm, stream) -> dict:
     """What a launch of the headline GEMV's size costs with no product in it,
     over the same rotation of 96 copies as the headline, each a HIP graph of
     one launch per copy: a one-element fill (the launch floor in a graph), a
-    device copy moving the GEMV's byte count (half read, half written) and the
-    GEMV itself."""
+    device copy moving the GEMV's byte count (half read, half written), the
+    vendor library's f16 GEMV over an f16 matrix of the GEMV's byte count
+    (1155 x 4096, torch.mv) and the GEMV itself."""
     per_launch = gemv_bytes(M_ROWS, K_DIM, N_DIM)
     bufs = [torch.empty(per_launch // 4, dtype=torch.float32, device="cuda").uniform_() for _ in range(WEIGHT_COPIES)]
     halves = [torch.empty(per_launch // 8, dtype=torch.float32, device="cuda") for _ in range(WEIGHT_COPIES)]
@@ -633,8 +634,22 @@ def floors_line(torch, ctx, rocm, stream) -> dict:
         for c in range(WEIGHT_COPIES):
             ctx.linear(weights[c], x, rocm.F16, M_ROWS, y[c], rocm.W4A16)
 
+    # f16 matrices of the same byte count for the vendor GEMV
+    vrows = per_launch // (2 * K_DIM)
+    assert vrows * 2 * K_DIM == per_launch
+    mats = [torch.randn((vrows, K_DIM), generator=torch.Generator(device="cuda").manual_seed(200 + c), device="cuda",
+                        dtype=torch.float16) * 0.02 for c in range(WEIGHT_COPIES)]
+    xv = x[0].contiguous()
+    yv = torch.empty((WEIGHT_COPIES, vrows), dtype=torch.float16, device="cuda")
+    torch.cuda.synchronize()
+
+    def vendor():
+        for c in range(WEIGHT_COPIES):
+            torch.mv(mats[c], xv, out=yv[c])
+
     out = {}
-    for name, fn in (("fill_1_element", fills), ("copy_same_bytes", copies), ("gemv_w4a16", gemvs)):
+    for name, fn in (("fill_1_element", fills), ("copy_same_bytes", copies), ("vendor_f16_gemv_same_bytes", vendor),
+                     ("gemv_w4a16", gemvs)):
         us = graph_ms(torch, stream, fn, WEIGHT_COPIES, reps=200) * 1e3
         out[name] = {"us_per_launch": round(us, 3), "launch": "hip graph"}
         if name != "fill_1_element":
@@ -642,6 +657,8 @@ def floors_line(torch, ctx, rocm, stream) -> dict:
     assert torch.isfinite(y).all()
     for wgt in weights:
         wgt.free()
+    del mats
+    out["vendor_f16_gemv_same_bytes"]["what"] = f"torch.mv, f16 [{vrows} x {K_DIM}] matrix times an f16 vector"
     out["bytes_per_launch"] = per_launch
     return out
 
