@@ -113,6 +113,15 @@ int32_t hip_fail(dz_ctx *ctx, hipError_t e, const char *what) {
         if (e_ != hipSuccess) return hip_fail(ctx, e_, "hipSetDevice");             \
     } while (0)
 
+// Entry points that wait for the stream, allocate, or read host memory: under
+// stream capture they return before enqueueing anything, so nothing of theirs
+// lands in the recorded graph.
+#define DZ_NOT_CAPTURING(ctx)                                                      \
+    do {                                                                           \
+        if (capturing(ctx))                                                        \
+            return fail(ctx, DZ_INVALID_REQUEST, "synchronous call during stream capture"); \
+    } while (0)
+
 // Launch status of the kernels just enqueued.
 int32_t launched(dz_ctx *ctx, const char *what) {
     hipError_t e = hipGetLastError();
@@ -385,6 +394,7 @@ int32_t dz_set_stream(dz_ctx *ctx, void *hip_stream) {
 
 int32_t dz_sync(dz_ctx *ctx) {
     DZ_BEGIN(ctx);
+    DZ_NOT_CAPTURING(ctx);
     DZ_HIP(ctx, hipStreamSynchronize(ctx->stream), "stream synchronize");
     return DZ_OK;
 }
@@ -407,6 +417,7 @@ int32_t dz_info(dz_ctx *ctx, char *buf, size_t cap) {
 
 int32_t dz_alloc(dz_ctx *ctx, size_t bytes, void **dev) {
     DZ_BEGIN(ctx);
+    DZ_NOT_CAPTURING(ctx);
     if (!dev) return fail(ctx, DZ_INVALID_REQUEST, "null output");
     DZ_HIP(ctx, hipMalloc(dev, bytes ? bytes : 1), "hipMalloc");
     return DZ_OK;
@@ -414,6 +425,7 @@ int32_t dz_alloc(dz_ctx *ctx, size_t bytes, void **dev) {
 
 int32_t dz_free(dz_ctx *ctx, void *dev) {
     DZ_BEGIN(ctx);
+    DZ_NOT_CAPTURING(ctx);
     DZ_HIP(ctx, hipStreamSynchronize(ctx->stream), "stream synchronize");
     if (dev) DZ_HIP(ctx, hipFree(dev), "hipFree");
     return DZ_OK;
@@ -421,6 +433,7 @@ int32_t dz_free(dz_ctx *ctx, void *dev) {
 
 int32_t dz_copy_h2d(dz_ctx *ctx, void *dst, const void *src, size_t bytes) {
     DZ_BEGIN(ctx);
+    DZ_NOT_CAPTURING(ctx);
     if (bytes && (!dst || !src)) return fail(ctx, DZ_INVALID_REQUEST, "null pointer");
     DZ_HIP(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream), "copy to device");
     DZ_HIP(ctx, hipStreamSynchronize(ctx->stream), "stream synchronize");
@@ -429,6 +442,7 @@ int32_t dz_copy_h2d(dz_ctx *ctx, void *dst, const void *src, size_t bytes) {
 
 int32_t dz_copy_d2h(dz_ctx *ctx, void *dst, const void *src, size_t bytes) {
     DZ_BEGIN(ctx);
+    DZ_NOT_CAPTURING(ctx);
     if (bytes && (!dst || !src)) return fail(ctx, DZ_INVALID_REQUEST, "null pointer");
     DZ_HIP(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream), "copy to host");
     DZ_HIP(ctx, hipStreamSynchronize(ctx->stream), "stream synchronize");
@@ -440,6 +454,7 @@ int32_t dz_copy_d2h(dz_ctx *ctx, void *dst, const void *src, size_t bytes) {
 int32_t dz_weight_upload(dz_ctx *ctx, const void *packed, size_t bytes, int32_t layout,
                          size_t rows, size_t cols, dz_weight **out) {
     DZ_BEGIN(ctx);
+    DZ_NOT_CAPTURING(ctx);
     if (!out || (!packed && bytes)) return fail(ctx, DZ_INVALID_REQUEST, "null pointer");
     *out = nullptr;
     dz::WeightKind kind;
@@ -486,6 +501,7 @@ int32_t dz_weight_upload(dz_ctx *ctx, const void *packed, size_t bytes, int32_t 
 int32_t dz_weight_quantize(dz_ctx *ctx, const void *values, int32_t dtype, size_t rows,
                            size_t cols, int32_t bits, int32_t group, dz_weight **out) {
     DZ_BEGIN(ctx);
+    DZ_NOT_CAPTURING(ctx);
     if (!out || !values) return fail(ctx, DZ_INVALID_REQUEST, "null pointer");
     *out = nullptr;
     if (!valid_dtype(dtype)) return fail(ctx, DZ_INVALID_PARAMETERS, "unknown dtype");
@@ -513,6 +529,7 @@ int32_t dz_weight_quantize(dz_ctx *ctx, const void *values, int32_t dtype, size_
 
 int32_t dz_weight_free(dz_ctx *ctx, dz_weight *w) {
     DZ_BEGIN(ctx);
+    DZ_NOT_CAPTURING(ctx);
     DZ_HIP(ctx, hipStreamSynchronize(ctx->stream), "stream synchronize");
     free_weight(w);
     return DZ_OK;
@@ -539,6 +556,7 @@ int32_t dz_dequant(dz_ctx *ctx, const dz_weight *w, float *y) {
 int32_t dz_dequant_rows(dz_ctx *ctx, const dz_weight *w, const int32_t *ids, size_t count, void *y,
                         int32_t dtype) {
     DZ_BEGIN(ctx);
+    DZ_NOT_CAPTURING(ctx);
     if (!w || (count && (!ids || !y))) return fail(ctx, DZ_INVALID_REQUEST, "null pointer");
     if (dtype != DZ_F32 && dtype != DZ_F16) return fail(ctx, DZ_INVALID_PARAMETERS, "dtype must be f32 or f16");
     int bad = 0;
@@ -720,6 +738,7 @@ int32_t dz_linear_q8(dz_ctx *ctx, const dz_weight *w, const int8_t *q, const flo
 
 int32_t dz_project(dz_ctx *ctx, const dz_weight *w, const float *x, size_t m, float *y) {
     DZ_BEGIN(ctx);
+    DZ_NOT_CAPTURING(ctx);
     if (!w || (m && (!x || !y))) return fail(ctx, DZ_INVALID_REQUEST, "null pointer");
     if (w->w.kind == dz::WeightKind::Q4G32 || w->w.cols % 64 != 0)
         return fail(ctx, DZ_INVALID_PARAMETERS, "invalid packed readout shape");
@@ -794,6 +813,7 @@ int32_t dz_i8_gemm_fused(dz_ctx *ctx, const int8_t *a, const float *sa, size_t m
 int32_t dz_q4_quantize_rows(dz_ctx *ctx, const void *values, int32_t dtype, size_t rows, size_t k,
                             uint32_t *out) {
     DZ_BEGIN(ctx);
+    DZ_NOT_CAPTURING(ctx);
     if (dtype != DZ_F32 && dtype != DZ_F16) return fail(ctx, DZ_INVALID_PARAMETERS, "dtype must be f32 or f16");
     if (k == 0 || k % 8 != 0 || k > 32768)
         return fail(ctx, DZ_INVALID_PARAMETERS, "Q4 reduction must be a multiple of eight, at most 32768");
@@ -894,6 +914,7 @@ int32_t dz_attention(dz_ctx *ctx, const void *qkv, void *out, size_t batch, size
 int32_t dz_encoder_create_random(dz_ctx *ctx, const dz_encoder_config *cfg, uint64_t seed,
                                  dz_encoder **out) {
     DZ_BEGIN(ctx);
+    DZ_NOT_CAPTURING(ctx);
     return dz::encoder_create_random(ctx, cfg, seed, out);
 }
 
@@ -914,6 +935,7 @@ const dz_weight *dz_encoder_weight(const dz_encoder *enc, int32_t layer, int32_t
 int32_t dz_encoder_read_rows(dz_ctx *ctx, const dz_encoder *enc, const int32_t *ids, size_t count,
                              void *out) {
     DZ_BEGIN(ctx);
+    DZ_NOT_CAPTURING(ctx);
     return dz::encoder_read_rows(ctx, enc, ids, count, out);
 }
 
@@ -926,11 +948,13 @@ int32_t dz_encoder_forward(dz_ctx *ctx, dz_encoder *enc, const int32_t *ids, siz
 int32_t dz_encoder_forward_rows(dz_ctx *ctx, dz_encoder *enc, const void *rows, size_t batch,
                                 size_t seq, float *out) {
     DZ_BEGIN(ctx);
+    DZ_NOT_CAPTURING(ctx);
     return dz::encoder_forward(ctx, enc, nullptr, rows, batch, seq, out);
 }
 
 int32_t dz_encoder_hidden_rows(dz_ctx *ctx, dz_encoder *enc, const void *rows, size_t seq, float *hidden) {
     DZ_BEGIN(ctx);
+    DZ_NOT_CAPTURING(ctx);
     return dz::encoder_hidden_rows(ctx, enc, rows, seq, hidden);
 }
 
@@ -941,12 +965,14 @@ int32_t dz_encoder_readout_params(const dz_encoder *enc, const dz_weight **w, co
 int32_t dz_encoder_set_readout(dz_ctx *ctx, dz_encoder *enc, const void *packed, size_t bytes, int32_t layout,
                                const float *norm_host) {
     DZ_BEGIN(ctx);
+    DZ_NOT_CAPTURING(ctx);
     return dz::encoder_set_readout(ctx, enc, packed, bytes, layout, norm_host);
 }
 
 int32_t dz_encoder_readout_rows(dz_ctx *ctx, dz_encoder *enc, const void *rows, size_t seq,
                                 const int32_t *markers, size_t count, float *logits) {
     DZ_BEGIN(ctx);
+    DZ_NOT_CAPTURING(ctx);
     return dz::encoder_readout(ctx, enc, rows, seq, markers, count, logits);
 }
 
@@ -954,6 +980,7 @@ int32_t dz_encoder_readout_rows(dz_ctx *ctx, dz_encoder *enc, const void *rows, 
 
 int32_t dz_pplx_create(dz_ctx *ctx, const dz_pplx_config *cfg, dz_pplx **out) {
     DZ_BEGIN(ctx);
+    DZ_NOT_CAPTURING(ctx);
     return dz::pplx_create(ctx, cfg, out);
 }
 
@@ -964,23 +991,27 @@ void dz_pplx_destroy(dz_ctx *ctx, dz_pplx *model) {
 int32_t dz_pplx_set_weight(dz_ctx *ctx, dz_pplx *model, const char *name, const void *packed, size_t bytes,
                            int32_t layout, size_t rows, size_t cols) {
     DZ_BEGIN(ctx);
+    DZ_NOT_CAPTURING(ctx);
     return dz::pplx_set_weight(ctx, model, name, packed, bytes, layout, rows, cols);
 }
 
 int32_t dz_pplx_set_vector(dz_ctx *ctx, dz_pplx *model, const char *name, const float *values, size_t count) {
     DZ_BEGIN(ctx);
+    DZ_NOT_CAPTURING(ctx);
     return dz::pplx_set_vector(ctx, model, name, values, count);
 }
 
 int32_t dz_pplx_layer(dz_ctx *ctx, dz_pplx *model, int32_t layer, float *hidden, size_t n, const int32_t *markers,
                       size_t count) {
     DZ_BEGIN(ctx);
+    DZ_NOT_CAPTURING(ctx);
     return dz::pplx_layer(ctx, model, layer, hidden, n, markers, count);
 }
 
 int32_t dz_pplx_forward_rows(dz_ctx *ctx, dz_pplx *model, const void *rows, size_t n, const int32_t *markers,
                              size_t count, float *logits) {
     DZ_BEGIN(ctx);
+    DZ_NOT_CAPTURING(ctx);
     return dz::pplx_forward_rows(ctx, model, rows, n, markers, count, logits);
 }
 
@@ -1005,6 +1036,7 @@ int32_t dz_probe_rate(dz_ctx *ctx, const char *what, int32_t zero_operands, doub
 
 int32_t dz_tune(dz_ctx *ctx, uint32_t budget_ms, const char *cache_in, char *cache_out, size_t cap) {
     DZ_BEGIN(ctx);
+    DZ_NOT_CAPTURING(ctx);
     return dz::tune(ctx, budget_ms, cache_in, cache_out, cap);
 }
 

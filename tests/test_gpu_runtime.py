@@ -132,14 +132,26 @@ def test_capture_refuses_growth_stream_changes_and_synchronous_calls(fresh, orac
     w = _weight(fresh, n, k, 51)
     x = torch.randn((m, k), device="cuda")
     y = torch.empty((m, n), device="cuda")
+    raw = oracle.f32_to_bf16((np.random.default_rng(52).standard_normal((n, 256)) * 0.02).astype(np.float32))
+    wire = oracle.pack_g64(raw, n, 256, 4)
+    wire_a = oracle.pack_g64(np.ascontiguousarray(raw[:4]), 4, 256, 4)
+    values = torch.randn((n, 256), device="cuda")
+    model = fresh.pplx_create(rocm.PplxConfig(layers=1, hidden=256, ff=512, delta_heads=4, delta_key_heads=2,
+                                              delta_head_dim=128, attn_heads=4, attn_kv_heads=2, attn_head_dim=256))
     stream = torch.cuda.Stream()
     fresh.set_stream(stream.cuda_stream)
     try:
         with torch.cuda.stream(stream):
             torch.cuda.synchronize()
+            # each call returns before enqueueing anything (the weight upload used to record its memsets first)
             for call in (lambda: fresh.linear(w, x, rocm.F32, m, y, rocm.W4A8),
                          lambda: fresh.set_stream(None),
-                         lambda: fresh.project(w, x, 1, y)):
+                         lambda: fresh.project(w, x, 1, y),
+                         lambda: fresh.sync(),
+                         lambda: fresh.upload(wire, rocm.Q4_G64_F32, n, 256),
+                         lambda: fresh.quantize(values, rocm.F32, n, 256, 4, 64),
+                         lambda: model.set_weight("language_model.layers.0.linear_attn.in_proj_a.weight", wire_a,
+                                                  rocm.Q4_G64_F32, 4, 256)):
                 graph = torch.cuda.CUDAGraph()
                 with pytest.raises(rocm.DzError) as e:
                     with rocm.capture(graph, stream):
@@ -148,8 +160,10 @@ def test_capture_refuses_growth_stream_changes_and_synchronous_calls(fresh, orac
                 assert e.value.code == "INVALID_REQUEST"
             fresh.linear(w, x, rocm.F32, m, y, rocm.W4A8)
             got = host(fresh, y)
+            fresh.upload(wire, rocm.Q4_G64_F32, n, 256).free()  # eager again: fine
     finally:
         fresh.set_stream(None)
+        model.close()
     xs = x[:40].cpu().numpy()
     assert bits_equal(got[:40], _eager(torch, fresh, w, xs, 40, n))
     w.free()
