@@ -24,8 +24,17 @@
  *    every replay; run such a call once before capturing it (the workspace
  *    cannot grow under capture: DZ_INVALID_REQUEST), and replay the graph on
  *    the context stream or ordered with it, one replay at a time. A workspace
- *    that a graph refers to lives until dz_destroy. Synchronous entry points
- *    return DZ_INVALID_REQUEST under capture.
+ *    that a graph refers to lives until dz_destroy. Entry points that wait
+ *    for the stream, allocate, or read host memory return DZ_INVALID_REQUEST
+ *    under capture before enqueueing anything: dz_sync, dz_alloc, dz_free,
+ *    dz_copy_h2d, dz_copy_d2h, dz_set_stream, dz_weight_upload,
+ *    dz_weight_quantize, dz_weight_free, dz_dequant_rows, dz_project,
+ *    dz_q4_quantize_rows, dz_encoder_create_random, dz_encoder_read_rows,
+ *    dz_encoder_forward_rows, dz_encoder_hidden_rows, dz_encoder_set_readout,
+ *    dz_encoder_readout_rows, dz_pplx_create, dz_pplx_set_weight,
+ *    dz_pplx_set_vector, dz_pplx_layer (it may grow the model's activation
+ *    buffers), dz_pplx_forward_rows, dz_pplx_set_residency, dz_probe_rate and
+ *    dz_tune.
  */
 #ifndef DECISIVE_ROCM_H
 #define DECISIVE_ROCM_H
