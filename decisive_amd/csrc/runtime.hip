@@ -942,6 +942,7 @@ int32_t dz_encoder_read_rows(dz_ctx *ctx, const dz_encoder *enc, const int32_t *
 int32_t dz_encoder_forward(dz_ctx *ctx, dz_encoder *enc, const int32_t *ids, size_t batch, size_t seq,
                            float *out) {
     DZ_BEGIN(ctx);
+    DZ_NOT_CAPTURING(ctx);
     return dz::encoder_forward(ctx, enc, ids, nullptr, batch, seq, out);
 }
 

@@ -30,6 +30,7 @@
  *    dz_copy_h2d, dz_copy_d2h, dz_set_stream, dz_weight_upload,
  *    dz_weight_quantize, dz_weight_free, dz_dequant_rows, dz_project,
  *    dz_q4_quantize_rows, dz_encoder_create_random, dz_encoder_read_rows,
+ *    dz_encoder_forward (it reads back the token-range flag),
  *    dz_encoder_forward_rows, dz_encoder_hidden_rows, dz_encoder_set_readout,
  *    dz_encoder_readout_rows, dz_pplx_create, dz_pplx_set_weight,
  *    dz_pplx_set_vector, dz_pplx_layer (it may grow the model's activation
