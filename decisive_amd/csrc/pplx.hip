@@ -74,20 +74,28 @@ __device__ __forceinline__ float wave_max(float v) {
 // 1/sqrt(t) with the square root correctly rounded (taken in f64)
 __device__ __forceinline__ float rsqrt_rn(float t) { return __fdiv_rn(1.0f, __double2float_rn(__dsqrt_rn((double)t))); }
 
-// out[t][c] = silu(sum_tap x[t-3+tap][c] * w[tap][c]); rows before 0 are zero
+// out[t][c] = silu(sum_tap x[t-3+tap][c] * w[tap][c]); rows before 0 are zero.
+// Grid (width / 4 / 256 blocks, n rows): a thread takes four consecutive
+// columns of row blockIdx.y (width % 4 == 0, 16-byte aligned rows), so no
+// index is divided; each column's arithmetic is the scalar order above.
 __global__ void conv_silu_kernel(const float *__restrict__ x, int n, int width, const float *__restrict__ w,
                                  float *__restrict__ out) {
-    const size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
-    if (i >= (size_t)n * width) return;
-    const int t = (int)(i / width), c = (int)(i % width);
-    float sum = 0.0f;
+    const int t = blockIdx.y;
+    const int c = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
+    if (t >= n || c >= width) return;
+    float4_t sum = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int tap = 0; tap < 4; tap++) {
         const int row = t - 3 + tap;
-        const float v = row < 0 ? 0.0f : x[(size_t)row * width + c];
-        sum = __fadd_rn(sum, __fmul_rn(v, w[(size_t)tap * width + c]));
+        const float4_t v = row < 0 ? float4_t{0.0f, 0.0f, 0.0f, 0.0f} : *(const float4_t *)(x + (size_t)row * width + c);
+        const float4_t k = *(const float4_t *)(w + (size_t)tap * width + c);
+#pragma unroll
+        for (int e = 0; e < 4; e++) sum[e] = __fadd_rn(sum[e], __fmul_rn(v[e], k[e]));
     }
-    out[i] = silu_ref(sum);
+    float4_t o;
+#pragma unroll
+    for (int e = 0; e < 4; e++) o[e] = silu_ref(sum[e]);
+    *(float4_t *)(out + (size_t)t * width + c) = o;
 }
 
 // One block per token, one wave per key head: unit q and k (q also scaled by
@@ -1450,8 +1458,10 @@ int32_t delta_layer(dz_ctx *ctx, dz_pplx *p, const dz_pplx::Layer &L, size_t n) 
         if (!rc) rc = dz_linear_pair(ctx, L.a, L.b, p->normed, n, p->ab, p->ab + n * lh, DZ_W4A8);
     }
     if (rc) return rc;
-    hipLaunchKernelGGL(conv_silu_kernel, dim3(blocks_of(n * cw, 256)), dim3(256), 0, s, p->wide, (int)n, (int)cw,
-                       L.conv, p->conv_out);
+    // cw is a multiple of kLd (128), so of 4; rows of p->wide, L.conv and p->conv_out are 16-byte aligned
+    static_assert(kLd % 4 == 0, "whole float4 columns");
+    hipLaunchKernelGGL(conv_silu_kernel, dim3(blocks_of(cw / 4, 256), (unsigned)n), dim3(256), 0, s, p->wide, (int)n,
+                       (int)cw, L.conv, p->conv_out);
     hipLaunchKernelGGL(delta_prep_kernel, dim3((unsigned)n), dim3(64 * c.delta_key_heads), 0, s, p->conv_out,
                        c.delta_heads, c.delta_key_heads, aa, ba, ab_ld, L.decay, L.dt, p->qhat, p->khat, p->gb);
     launch_delta_scan(ctx, p, n, s);
