@@ -399,33 +399,51 @@ __global__ __launch_bounds__(256) void rms_apply_quantize_kernel(const float *__
     const size_t row = blockIdx.x, base = row * (size_t)d;
     const int groups = d / 64;
     const float scale = sc[row * groups];
-    __syncthreads();  // every wave has the row scale before group 0's scale replaces it
-    const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
-    // a wave's groups g = wave + 4j in batches of 8, every load of a batch in
-    // flight before the first group is computed
-    constexpr int BATCH = 8;
-    for (int g0 = wave; g0 < groups; g0 += 4 * BATCH) {
-        float xv[BATCH], wv[BATCH];
+    __syncthreads();  // every thread has the row scale before group 0's scale replaces it
+    // thread t takes columns 4t, 4t + 1, 4t + 2, 4t + 3 of every 1024-column
+    // chunk: a 64-column group is 16 consecutive lanes of one wave. Every
+    // load of the row is in flight before the first group is computed.
+    constexpr int CHUNKS = 4;  // 4096 columns per pass
+    const int lane16 = threadIdx.x % 16;
+    for (int c0 = 0; c0 < d; c0 += CHUNKS * 1024) {
+    float4_t xv[CHUNKS], wv[CHUNKS];
 #pragma unroll
-        for (int j = 0; j < BATCH; j++) {
-            const int g = g0 + 4 * j;
-            xv[j] = g < groups ? h[base + g * 64 + lane] : 0.0f;
-            wv[j] = g < groups ? w[g * 64 + lane] : 0.0f;
-        }
+    for (int u = 0; u < CHUNKS; u++) {
+        const int col = c0 + u * 1024 + 4 * (int)threadIdx.x;
+        xv[u] = col < d ? *(const float4_t *)(h + base + col) : float4_t{0.f, 0.f, 0.f, 0.f};
+        wv[u] = col < d ? *(const float4_t *)(w + col) : float4_t{0.f, 0.f, 0.f, 0.f};
+    }
 #pragma unroll
-        for (int j = 0; j < BATCH; j++) {
-            const int g = g0 + 4 * j;
-            if (g >= groups) break;
-            const int col = g * 64 + lane;
-            const float gain = zero_centered ? __fadd_rn(1.0f, wv[j]) : wv[j];
-            const float v = __fmul_rn(__fmul_rn(xv[j], scale), gain);
-            if (y) y[base + col] = v;
-            if (!__builtin_isfinite(v) && bad) atomicOr(bad, 1);
-            const float maximum = wave_max_dpp(fabsf(v));
-            const float s = fmaxf(__fdiv_rn(maximum, 127.0f), FLT_MIN);
-            q[(row * groups + g) * 64 + lane] = (int8_t)quantize_code(v, __frcp_rn(s), 127.0f);
-            if (lane == 0) sc[row * groups + g] = s;
+    for (int u = 0; u < CHUNKS; u++) {
+        const int col = c0 + u * 1024 + 4 * (int)threadIdx.x;
+        if (c0 + u * 1024 >= d) break;  // uniform
+        const bool live = col < d;  // the columns of a group are all live or all not
+        float4_t v;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float gain = zero_centered ? __fadd_rn(1.0f, wv[u][e]) : wv[u][e];
+            v[e] = __fmul_rn(__fmul_rn(xv[u][e], scale), gain);
         }
+        float maximum = fabsf(v[0]);
+#pragma unroll
+        for (int e = 1; e < 4; e++) maximum = fmaxf(maximum, fabsf(v[e]));
+        // the group's maximum over its 16 lanes
+#pragma unroll
+        for (int off = 8; off > 0; off >>= 1) maximum = fmaxf(maximum, __shfl_xor(maximum, off, 16));
+        if (!live) continue;
+        if (y) *(float4_t *)(y + base + col) = v;
+        bool finite = true;
+#pragma unroll
+        for (int e = 0; e < 4; e++) finite = finite && __builtin_isfinite(v[e]);
+        if (!finite && bad) atomicOr(bad, 1);
+        const float s = fmaxf(__fdiv_rn(maximum, 127.0f), FLT_MIN);
+        const float inverse = __frcp_rn(s);
+        uint32_t word = 0;
+#pragma unroll
+        for (int e = 0; e < 4; e++) word |= (uint32_t)(uint8_t)(int8_t)quantize_code(v[e], inverse, 127.0f) << (8 * e);
+        *(uint32_t *)(q + base + col) = word;
+        if (lane16 == 0) sc[row * groups + col / 64] = s;
+    }
     }
 }
 
