@@ -748,15 +748,18 @@ __global__ __launch_bounds__(kAttnMaxGroup * 64) void attention_mfma_kernel(
 // out[t][h*256 + i] = heads[h][t][i] * sigmoid(z), z at zsrc + t*z_row + h*z_head + i.
 // CODES: instead of out, the A8 codes and scales of each 64-group (one wave per
 // group; the activation quantizer's arithmetic, int8.rs:178-202), with *bad
-// raised on a non-finite value. A row's n*ah*256 values fill whole waves.
+// raised on a non-finite value. Grid (ah blocks of 256 threads, n rows):
+// block (h, t) takes head h of token t, so no index is divided and a wave
+// holds one 64-group.
 template <bool CODES>
 __global__ void attention_gate_kernel(const float *__restrict__ heads, int n, int ah,
                                       const float *__restrict__ zsrc, size_t z_row, int z_head,
                                       float *__restrict__ out, int8_t *__restrict__ q, float *__restrict__ qs,
                                       int *bad) {
-    const size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
-    if (i >= (size_t)n * ah * kAd) return;
-    const int t = (int)(i / ((size_t)ah * kAd)), h = (int)((i / kAd) % ah), d = (int)(i % kAd);
+    static_assert(kAd == 256, "one block of 256 threads per head");
+    const int t = blockIdx.y, h = blockIdx.x, d = threadIdx.x;
+    if (t >= n || h >= ah) return;  // whole block
+    const size_t i = ((size_t)t * ah + h) * kAd + d;
     const float z = zsrc[(size_t)t * z_row + (size_t)h * z_head + d];
     const float v = __fmul_rn(heads[((size_t)h * n + t) * kAd + d], sigmoid_ref(z));
     if constexpr (!CODES) {
@@ -1539,21 +1542,21 @@ int32_t attention_layer(dz_ctx *ctx, dz_pplx *p, const dz_pplx::Layer &L, size_t
     hipLaunchKernelGGL(head_norm_rope_kernel, dim3((unsigned)n, c.attn_kv_heads), dim3(64), 0, s, p->key, kvw, kAd,
                        c.attn_kv_heads, L.knorm, nullptr, p->freq, p->key);
     launch_attention(ctx, p, nq, n, s);
-    const unsigned gate_blocks = blocks_of(nq * c.attn_heads * kAd, 256);
+    const dim3 gate_blocks((unsigned)c.attn_heads, (unsigned)nq);  // head, token
     if (!markers && n > 16 && (size_t)c.ff >= (size_t)c.attn_heads * kAd &&
         grouped_adds_residual(weight_of(L.o), (int)n, ctx_variant(ctx, "grouped"))) {
         // as in the delta layer: o_proj reads A8 codes from the MLP's code buffer
         int *gflag = nullptr;
         rc = ctx_product_flag(ctx, &gflag);
         if (rc) return rc;
-        hipLaunchKernelGGL(attention_gate_kernel<true>, dim3(gate_blocks), dim3(256), 0, s, p->heads, (int)nq,
+        hipLaunchKernelGGL(attention_gate_kernel<true>, gate_blocks, dim3(kAd), 0, s, p->heads, (int)nq,
                            c.attn_heads, p->wide + kAd, qw, 2 * kAd, nullptr, p->codes, p->code_scales, gflag);
         rc = product_add(ctx, L.o, nullptr, p->codes, p->code_scales, nq, p->hidden, p->projected, gflag);
         if (rc) return rc;
         *rows_out = nq;
         return DZ_OK;
     }
-    hipLaunchKernelGGL(attention_gate_kernel<false>, dim3(gate_blocks), dim3(256), 0, s, p->heads, (int)nq,
+    hipLaunchKernelGGL(attention_gate_kernel<false>, gate_blocks, dim3(kAd), 0, s, p->heads, (int)nq,
                        c.attn_heads, p->wide + kAd, qw, 2 * kAd, p->ctx, nullptr, nullptr, nullptr);
     if (markers) {  // the residual rows of the markers, before o_proj adds onto them
         hipLaunchKernelGGL(gather_rows_kernel, dim3(blocks_of(count * d, 256)), dim3(256), 0, s, p->hidden, markers,
