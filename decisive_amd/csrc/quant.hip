@@ -406,44 +406,44 @@ __global__ __launch_bounds__(256) void rms_apply_quantize_kernel(const float *__
     constexpr int CHUNKS = 4;  // 4096 columns per pass
     const int lane16 = threadIdx.x % 16;
     for (int c0 = 0; c0 < d; c0 += CHUNKS * 1024) {
-    float4_t xv[CHUNKS], wv[CHUNKS];
+        float4_t xv[CHUNKS], wv[CHUNKS];
 #pragma unroll
-    for (int u = 0; u < CHUNKS; u++) {
-        const int col = c0 + u * 1024 + 4 * (int)threadIdx.x;
-        xv[u] = col < d ? *(const float4_t *)(h + base + col) : float4_t{0.f, 0.f, 0.f, 0.f};
-        wv[u] = col < d ? *(const float4_t *)(w + col) : float4_t{0.f, 0.f, 0.f, 0.f};
-    }
-#pragma unroll
-    for (int u = 0; u < CHUNKS; u++) {
-        const int col = c0 + u * 1024 + 4 * (int)threadIdx.x;
-        if (c0 + u * 1024 >= d) break;  // uniform
-        const bool live = col < d;  // the columns of a group are all live or all not
-        float4_t v;
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const float gain = zero_centered ? __fadd_rn(1.0f, wv[u][e]) : wv[u][e];
-            v[e] = __fmul_rn(__fmul_rn(xv[u][e], scale), gain);
+        for (int u = 0; u < CHUNKS; u++) {
+            const int col = c0 + u * 1024 + 4 * (int)threadIdx.x;
+            xv[u] = col < d ? *(const float4_t *)(h + base + col) : float4_t{0.f, 0.f, 0.f, 0.f};
+            wv[u] = col < d ? *(const float4_t *)(w + col) : float4_t{0.f, 0.f, 0.f, 0.f};
         }
-        float maximum = fabsf(v[0]);
 #pragma unroll
-        for (int e = 1; e < 4; e++) maximum = fmaxf(maximum, fabsf(v[e]));
-        // the group's maximum over its 16 lanes
+        for (int u = 0; u < CHUNKS; u++) {
+            const int col = c0 + u * 1024 + 4 * (int)threadIdx.x;
+            if (c0 + u * 1024 >= d) break;  // uniform
+            const bool live = col < d;  // the columns of a group are all live or all not
+            float4_t v;
 #pragma unroll
-        for (int off = 8; off > 0; off >>= 1) maximum = fmaxf(maximum, __shfl_xor(maximum, off, 16));
-        if (!live) continue;
-        if (y) *(float4_t *)(y + base + col) = v;
-        bool finite = true;
+            for (int e = 0; e < 4; e++) {
+                const float gain = zero_centered ? __fadd_rn(1.0f, wv[u][e]) : wv[u][e];
+                v[e] = __fmul_rn(__fmul_rn(xv[u][e], scale), gain);
+            }
+            float maximum = fabsf(v[0]);
 #pragma unroll
-        for (int e = 0; e < 4; e++) finite = finite && __builtin_isfinite(v[e]);
-        if (!finite && bad) atomicOr(bad, 1);
-        const float s = fmaxf(__fdiv_rn(maximum, 127.0f), FLT_MIN);
-        const float inverse = __frcp_rn(s);
-        uint32_t word = 0;
+            for (int e = 1; e < 4; e++) maximum = fmaxf(maximum, fabsf(v[e]));
+            // the group's maximum over its 16 lanes
 #pragma unroll
-        for (int e = 0; e < 4; e++) word |= (uint32_t)(uint8_t)(int8_t)quantize_code(v[e], inverse, 127.0f) << (8 * e);
-        *(uint32_t *)(q + base + col) = word;
-        if (lane16 == 0) sc[row * groups + col / 64] = s;
-    }
+            for (int off = 8; off > 0; off >>= 1) maximum = fmaxf(maximum, __shfl_xor(maximum, off, 16));
+            if (!live) continue;
+            if (y) *(float4_t *)(y + base + col) = v;
+            bool finite = true;
+#pragma unroll
+            for (int e = 0; e < 4; e++) finite = finite && __builtin_isfinite(v[e]);
+            if (!finite && bad) atomicOr(bad, 1);
+            const float s = fmaxf(__fdiv_rn(maximum, 127.0f), FLT_MIN);
+            const float inverse = __frcp_rn(s);
+            uint32_t word = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) word |= (uint32_t)(uint8_t)(int8_t)quantize_code(v[e], inverse, 127.0f) << (8 * e);
+            *(uint32_t *)(q + base + col) = word;
+            if (lane16 == 0) sc[row * groups + col / 64] = s;
+        }
     }
 }
 
