@@ -20,8 +20,8 @@ int8 GEMM, the Q4 prefill GEMM and the encoder forward) are reported under
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-secondary] [--no-cpu]
                     [--no-graph] [--calibrate-copy] [--tune MS]
     python bench.py --only pplx                      (the decider line alone)
-    python bench.py --only encoder / floors / probes (the encoder line; launch floors
-                     at the GEMV's size; sustained unit rates from register-only loops)
+    python bench.py --only encoder / floors / gemv (the encoder line; launch floors
+                     at the GEMV's size; the GEMV at N = 16384 and 65536)
     python bench.py --only tune [--tune MS] [--tune-cache F] [--tune-out F]
                     (the tuner's selection, then each family's reference and
                      selected variants at the tuning shape, for rocprofv3)
@@ -260,6 +260,39 @@ def gemv_lines(torch, ctx, rocm, weights, stream) -> dict:
         gbs = gemv_bytes(m, K_DIM, N_DIM) / (ms * 1e-3) / 1e9
         out[f"q4_gemv_w4a16_m{m}_k4096_n4096"] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
                                                   "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+    return out
+
+
+def wide_gemv_lines(torch, ctx, rocm, stream) -> dict:
+    """The W4A16 GEMV's streaming rate where a launch's fixed cost is small:
+    K = 4096 at N = 16384 and 65536 (37.7 and 151 MB per launch), M = 1, 4 and
+    8, over rotating copies of about 906 MB (24 and 6 copies), each a HIP
+    graph of one launch per copy; the library's default variant ("auto")."""
+    out = {}
+    for n, copies in ((16384, 24), (65536, 6)):
+        tmp = torch.empty((n, K_DIM), dtype=torch.float32, device="cuda")
+        ws = []
+        for c in range(copies):
+            tmp.normal_(0.0, 0.02, generator=torch.Generator(device="cuda").manual_seed(1 + c))
+            torch.cuda.synchronize()
+            ws.append(ctx.quantize(tmp, rocm.F32, n, K_DIM, 4, 32))
+        del tmp
+        for m in (1, 4, 8):
+            x = torch.randn((m, K_DIM), generator=torch.Generator(device="cuda").manual_seed(0), device="cuda").half()
+            y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+            torch.cuda.synchronize()
+
+            def step():
+                for w in ws:
+                    ctx.linear(w, x, rocm.F16, m, y, rocm.W4A16)
+            ms = graph_ms(torch, stream, step, len(ws))
+            gbs = gemv_bytes(m, K_DIM, n) / (ms * 1e-3) / 1e9
+            out[f"q4_gemv_w4a16_m{m}_k4096_n{n}"] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
+                                                     "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+                                                     "weight_copies": copies}
+        for w in ws:
+            w.free()
+        del ws
     return out
 
 
@@ -569,41 +602,6 @@ def traffic_per_launch():
         return None
 
 
-def probes_line(ctx) -> dict:
-    """Sustained unit rates from register-only loops (dz_probe_rate): the MFMA
-    rates on random and on all-zero operands beside the published peaks, and
-    the cycles per wave instruction of v_fma_f32 and v_exp_f32 at the
-    device's maximum clock (the attention softmax is bound by their ratio), and
-    the LDS read bandwidth per compute unit (ds_read_b128)."""
-    info = ctx.info()
-    simds, clock = info["compute_units"] * 4, info["clock_khz"] * 1e3
-
-    def rate_of(what, zero=False):
-        # about 300 ms of the same loop first: the clocks of an idle device ramp up under load
-        start = time.perf_counter()
-        while time.perf_counter() - start < 0.3:
-            ctx.probe_rate(what, zero)
-        return max(ctx.probe_rate(what, zero) for _ in range(3))
-
-    out = {}
-    for what, peak, unit in (("mfma_f16", F16_PEAK_TFLOPS, "TFLOP/s"), ("mfma_i8", I8_PEAK_TOPS, "TOP/s")):
-        for zero in (False, True):
-            rate = rate_of(what, zero) / 1e12
-            out[f"{what}_{'zero' if zero else 'random'}_operands"] = {
-                unit: round(rate, 1), "frac_of_spec_peak": round(rate / peak, 4)}
-    for what in ("fma_f32", "exp_f32"):
-        rate = rate_of(what)
-        out[what] = {"lane_ops_per_s": round(rate / 1e12, 3) * 1e12,
-                     "cycles_per_wave_instruction_at_max_clock": round(simds * clock * 64 / rate, 2)}
-    rate = rate_of("lds_b128")
-    out["lds_b128"] = {"TB/s": round(rate / 1e12, 2),
-                       "bytes_per_clock_per_cu_at_max_clock": round(rate / (info["compute_units"] * clock), 1)}
-    out["note"] = ("register-only loops on every compute unit, eight waves per SIMD, each kind after 300 ms of "
-                   "the same load; MFMA operands change from one instruction to the next (random f16 / int8 from "
-                   "a hash, or all zero)")
-    return out
-
-
 def floors_line(torch, ctx, rocm, stream) -> dict:
     """What a launch of the headline GEMV's size costs with no product in it,
     over the same rotation of 96 copies as the headline, each a HIP graph of
@@ -678,7 +676,7 @@ def main():
     ap.add_argument("--calibrate-copy", action="store_true",
                     help=f"also run a {COPY_BYTES >> 20} MiB device copy (counter calibration)")
     ap.add_argument("--tune", type=int, default=0, help="tuner budget in ms (0 keeps reference variants)")
-    ap.add_argument("--only", choices=["pplx", "tune", "floors", "encoder", "probes"],
+    ap.add_argument("--only", choices=["pplx", "tune", "floors", "encoder", "gemv"],
                     help="run one secondary line alone and print it (for profiling)")
     ap.add_argument("--tune-cache", help="with --only tune: a selection JSON from an earlier run to reuse")
     ap.add_argument("--tune-out", help="with --only tune: write the selection JSON here")
@@ -703,8 +701,13 @@ def main():
     if args.tune:
         ctx.tune(args.tune)
     log(f"[bench] device {ctx.info()}")
-    if args.only == "probes":
-        print(json.dumps({"unit_rate_probes": probes_line(ctx)}), flush=True)
+    if args.only == "gemv":
+        stream = torch.cuda.Stream()
+        ctx.set_stream(stream.cuda_stream)
+        with torch.cuda.stream(stream):
+            line = wide_gemv_lines(torch, ctx, rocm, stream)
+        ctx.set_stream(None)
+        print(json.dumps({"wide_gemv": line}), flush=True)
         return
     if args.only == "floors":
         stream = torch.cuda.Stream()
@@ -824,6 +827,7 @@ def main():
             for wgt in weights:
                 wgt.free()
             weights.clear()
+            sec.update(wide_gemv_lines(torch, ctx, rocm, stream))
             sec["q4_gemv_w4a8_m1_k4096_n4096_g64f32"] = w4a8_line(torch, ctx, rocm, stream)
             sec.update(secondary(torch, ctx, rocm, stream, cpu=not args.no_cpu))
         result["secondary"] = sec

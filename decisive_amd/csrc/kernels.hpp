@@ -111,6 +111,10 @@ void launch_fill_f32(float *p, size_t n, float v, hipStream_t s);
 // Compute units of the current device (cached per device).
 int device_cus();
 
+// The decider's token-by-token gated delta scan (pplx.hip), for the tuner.
+void launch_delta_scan_tokens(const float *qhat, const float *khat, const float *conv, const float *gb, int n,
+                              int lh, int lk, float *out, int variant, hipStream_t s);
+
 // ---- variants (tuner) --------------------------------------------------------------
 struct VariantFamily {
     const char *family;
@@ -118,6 +122,9 @@ struct VariantFamily {
     int count;
 };
 int variant_count(const char *family);
+// Variants the tuner may choose among (the first `tuned_count`, all bitwise
+// equal to variant 0); the rest are explicit opt-ins.
+int tuned_count(const char *family);
 const char *variant_name(const char *family, int index);
 int variant_index(const char *family, const char *name);
 

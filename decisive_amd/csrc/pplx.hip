@@ -173,6 +173,11 @@ constexpr int kScanChunk = 16;  // tokens staged in LDS at a time
 constexpr int kScanWaves = 4;
 constexpr int kScanCols = 2 * kScanWaves;  // state columns per block
 
+// UNROLL: whole 16-token stages run unrolled (constant LDS offsets, no loop
+// counter per token; the scan issues its VALU work back to back, so the
+// instructions per token set its rate); the arithmetic and its order are the
+// same either way, so both forms give the same bits.
+template <bool UNROLL>
 __global__ __launch_bounds__(kScanWaves * 64) void delta_scan_kernel(const float *__restrict__ qhat,
                                                                      const float *__restrict__ khat,
                                                                      const float *__restrict__ conv,
@@ -226,12 +231,15 @@ __global__ __launch_bounds__(kScanWaves * 64) void delta_scan_kernel(const float
         if (more) load(t0 + T);  // in flight while this chunk computes
         const int count = min(T, n - t0);
         float keep = 0.0f;
-        for (int tt = 0; tt < count; tt++) {
-            const float g = gs[buf][tt * 4], beta = gs[buf][tt * 4 + 1], kq = gs[buf][tt * 4 + 2];
+        // one token: S^T k and S^T q over the previous state, reduced together;
+        // then S = g S + k delta^T with delta = (v - g S^T k) beta and
+        // out = g S^T q + delta (k.q)
+        auto step = [&](int tt) {
+            const float4_t gq = *(const float4_t *)(&gs[buf][tt * 4]);
             const float v = vs[buf][tt * kScanCols + 2 * wave + c];
             const float4_t k4 = *(const float4_t *)(&ks[buf][tt * kLd + 4 * r]);
             const float4_t q4 = *(const float4_t *)(&qs[buf][tt * kLd + 4 * r]);
-            // S^T k and S^T q over the previous state, reduced together
+            const float g = gq[0], beta = gq[1], kq = gq[2];
             float m0 = S[0] * k4[0], m1 = S[1] * k4[1], p0 = S[0] * q4[0], p1 = S[1] * q4[1];
             m0 = __builtin_fmaf(S[2], k4[2], m0);
             m1 = __builtin_fmaf(S[3], k4[3], m1);
@@ -240,12 +248,18 @@ __global__ __launch_bounds__(kScanWaves * 64) void delta_scan_kernel(const float
 #pragma unroll
             for (int e = 0; e < 4; e++) S[e] *= g;
             const float sk = half_sum(m0 + m1), sq = half_sum(p0 + p1);
-            // S = g S + k delta^T with delta = (v - g S^T k) beta; out = g S^T q + delta (k.q)
             const float delta = (v - g * sk) * beta;
 #pragma unroll
             for (int e = 0; e < 4; e++) S[e] = __builtin_fmaf(k4[e], delta, S[e]);
             const float total = __builtin_fmaf(g, sq, delta * kq);
             keep = r == tt ? total : keep;
+        };
+        if (UNROLL && count == T) {
+            // a whole stage: constant LDS offsets and no loop counter per token
+#pragma unroll
+            for (int tt = 0; tt < T; tt++) step(tt);
+        } else {
+            for (int tt = 0; tt < count; tt++) step(tt);
         }
         if (r < count) out[((size_t)h * n + t0 + r) * kLd + j] = keep;
         if (more) store(buf ^ 1);  // the other buffer: last read a whole chunk ago
@@ -782,6 +796,21 @@ __global__ void gather_rows_kernel(const float *__restrict__ src, const int32_t 
 }
 
 }  // namespace
+
+// The token-by-token scan alone (the decider's launch and the tuner's): qhat
+// and khat [n][lk][128], conv [n][2 lk 128 + lh 128] (v from column
+// 2 lk 128 on), gb [n][lh][4] = {g, beta, k.q, -}, out [lh][n][128].
+// variant 1 is the rolled loop, any other the unrolled one; the same bits.
+void launch_delta_scan_tokens(const float *qhat, const float *khat, const float *conv, const float *gb, int n,
+                              int lh, int lk, float *out, int variant, hipStream_t s) {
+    if (variant == 1)
+        hipLaunchKernelGGL(delta_scan_kernel<false>, dim3(lh, kLd / kScanCols), dim3(64 * kScanWaves), 0, s, qhat,
+                           khat, conv, gb, n, lh, lk, out);
+    else
+        hipLaunchKernelGGL(delta_scan_kernel<true>, dim3(lh, kLd / kScanCols), dim3(64 * kScanWaves), 0, s, qhat,
+                           khat, conv, gb, n, lh, lk, out);
+}
+
 }  // namespace dz
 
 struct dz_pplx {
@@ -817,6 +846,18 @@ struct dz_pplx {
     int32_t *markers = nullptr;
     uint8_t *rows_dev = nullptr;
     dz::Weight rows_weight;
+    // What the last layer call left in the activation buffers, for
+    // dz_pplx_activation: the layer, its kind and row counts, which norm and
+    // gate outputs were written in which form, and where z, a and b sit.
+    struct Trace {
+        int layer = -1;
+        bool attention = false;
+        size_t n = 0, nq = 0, rows = 0;
+        bool mixer = false;  // the mixer half ran (its activations are the layer's)
+        bool norm_codes = false, normed = false, gate_codes = false, gate_f32 = false, mlp_codes = false;
+        const float *a = nullptr, *b = nullptr;
+        int z_ld = 0, ab_ld = 0;
+    } trace;
     // Streamed residency (webgpu/streaming.rs:16-369): the layers' projections
     // live in pinned host memory, already in the device layout, and layer i
     // runs from device bank i % 2. The copy stream fills a bank once the layer
@@ -1357,6 +1398,8 @@ int32_t layer_norm(dz_ctx *ctx, dz_pplx *p, const float *w, size_t n, bool need_
     *flag = nullptr;
     if (n <= 16 || ctx_variant(ctx, "norm") != 0 || c.hidden % 64 != 0 || c.hidden > kRmsQuantizeMaxCols) {
         launch_readout_rms(p->hidden, 0, nullptr, (int)n, c.hidden, w, 1e-6f, 1, p->normed, s);
+        p->trace.norm_codes = false;
+        p->trace.normed = true;
         return DZ_OK;
     }
     int32_t rc = ctx_product_flag(ctx, flag);
@@ -1364,6 +1407,8 @@ int32_t layer_norm(dz_ctx *ctx, dz_pplx *p, const float *w, size_t n, bool need_
     launch_rms_quantize(p->hidden, (int)n, c.hidden, w, 1e-6f, 1, need_f32 ? p->normed : nullptr, p->ncodes,
                         p->nscales, *flag, s);
     *codes = true;
+    p->trace.norm_codes = true;
+    p->trace.normed = need_f32;
     return DZ_OK;
 }
 
@@ -1386,6 +1431,8 @@ int32_t mlp(dz_ctx *ctx, dz_pplx *p, const dz_pplx::Layer &L, size_t n) {
             rc = ctx_mlp_codes(ctx, L.gate, L.up, p->ncodes, p->nscales, n, p->codes, p->code_scales, flag);
         else
             rc = dz_mlp_requant(ctx, L.gate, L.up, p->normed, n, p->codes, p->code_scales);
+        p->trace.mlp_codes = true;
+        p->trace.gate_codes = false;  // the MLP's codes replace the gate's
         if (!rc) rc = product_add(ctx, L.down, nullptr, p->codes, p->code_scales, n, p->hidden, p->projected);
     } else {
         if (codes) {
@@ -1400,17 +1447,18 @@ int32_t mlp(dz_ctx *ctx, dz_pplx *p, const dz_pplx::Layer &L, size_t n) {
     return rc;
 }
 
-// Variant 1 runs the token-by-token scan, 2 the chunked one; 0 picks the
-// chunked scan from six chunks of tokens on (measured at the reference's
-// sizes: the chunked scan is 2% slower at 229 tokens, 2% faster at 512, 9%
-// faster at 1024 and 2048, over three delta layers and one attention layer).
+// Variants 0 ("recurrent", whole stages unrolled) and 1 ("recurrent-rolled")
+// run the token-by-token scan, with the same arithmetic;
+// 2 ("chunked64") the chunked one, whose regrouped arithmetic gives other
+// bits; 3 ("auto") picks the chunked scan from six chunks of tokens on, so
+// its bits depend on the chunk's length. Only 0 and 1 are tuned.
 void launch_delta_scan(dz_ctx *ctx, dz_pplx *p, size_t n, hipStream_t s) {
     const dz_pplx_config &c = p->cfg;
     const int v = ctx_variant(ctx, "delta_scan");
-    const bool chunked = v == 2 || (v == 0 && n >= (size_t)6 * kChunk);
+    const bool chunked = v == 2 || (v == 3 && n >= (size_t)6 * kChunk);
     if (!chunked) {
-        hipLaunchKernelGGL(delta_scan_kernel, dim3(c.delta_heads, kLd / kScanCols), dim3(64 * kScanWaves), 0, s,
-                           p->qhat, p->khat, p->conv_out, p->gb, (int)n, c.delta_heads, c.delta_key_heads, p->heads);
+        launch_delta_scan_tokens(p->qhat, p->khat, p->conv_out, p->gb, (int)n, c.delta_heads, c.delta_key_heads,
+                                 p->heads, v, s);
         return;
     }
     constexpr size_t lds = (size_t)(kChunk * kChunkRow + kChunk * kChunk + 3 * kChunk) * 4;
@@ -1445,6 +1493,10 @@ int32_t delta_layer(dz_ctx *ctx, dz_pplx *p, const dz_pplx::Layer &L, size_t n) 
         aa = p->z + lh * kLd;
         ba = aa + (lh + 15) / 16 * 16;
     }
+    p->trace.a = aa;
+    p->trace.b = ba;
+    p->trace.z_ld = z_ld;
+    p->trace.ab_ld = ab_ld;
     if (codes) {  // the input projections share the norm's codes
         rc = normed_product(ctx, p, L.qkv, true, flag, n, p->wide);
         if (L.zab) {
@@ -1477,10 +1529,12 @@ int32_t delta_layer(dz_ctx *ctx, dz_pplx *p, const dz_pplx::Layer &L, size_t n) 
         if (rc) return rc;
         hipLaunchKernelGGL(delta_gate_kernel<true>, dim3((unsigned)n, c.delta_heads), dim3(64), 0, s, p->heads,
                            (int)n, c.delta_heads, L.norm, za, z_ld, nullptr, p->codes, p->code_scales, gflag);
+        p->trace.gate_codes = true;
         return product_add(ctx, L.out, nullptr, p->codes, p->code_scales, n, p->hidden, p->projected, gflag);
     }
     hipLaunchKernelGGL(delta_gate_kernel<false>, dim3((unsigned)n, c.delta_heads), dim3(64), 0, s, p->heads, (int)n,
                        c.delta_heads, L.norm, za, z_ld, p->ctx, nullptr, nullptr, nullptr);
+    p->trace.gate_f32 = true;
     return product_add(ctx, L.out, p->ctx, nullptr, nullptr, n, p->hidden, p->projected);
 }
 
@@ -1551,6 +1605,7 @@ int32_t attention_layer(dz_ctx *ctx, dz_pplx *p, const dz_pplx::Layer &L, size_t
         if (rc) return rc;
         hipLaunchKernelGGL(attention_gate_kernel<true>, gate_blocks, dim3(kAd), 0, s, p->heads, (int)nq,
                            c.attn_heads, p->wide + kAd, qw, 2 * kAd, nullptr, p->codes, p->code_scales, gflag);
+        p->trace.gate_codes = true;
         rc = product_add(ctx, L.o, nullptr, p->codes, p->code_scales, nq, p->hidden, p->projected, gflag);
         if (rc) return rc;
         *rows_out = nq;
@@ -1558,6 +1613,7 @@ int32_t attention_layer(dz_ctx *ctx, dz_pplx *p, const dz_pplx::Layer &L, size_t
     }
     hipLaunchKernelGGL(attention_gate_kernel<false>, gate_blocks, dim3(kAd), 0, s, p->heads, (int)nq,
                        c.attn_heads, p->wide + kAd, qw, 2 * kAd, p->ctx, nullptr, nullptr, nullptr);
+    p->trace.gate_f32 = true;
     if (markers) {  // the residual rows of the markers, before o_proj adds onto them
         hipLaunchKernelGGL(gather_rows_kernel, dim3(blocks_of(count * d, 256)), dim3(256), 0, s, p->hidden, markers,
                            (int)count, (int)d, p->picked);
@@ -1573,8 +1629,15 @@ int32_t attention_layer(dz_ctx *ctx, dz_pplx *p, const dz_pplx::Layer &L, size_t
 }  // namespace
 
 // Layer `index` on hidden rows already in p->hidden (tests and the forward).
+void trace_reset(dz_pplx *p, int index, bool attention, size_t n) {
+    p->trace = dz_pplx::Trace{};
+    p->trace.layer = index;
+    p->trace.attention = attention;
+    p->trace.n = n;
+}
+
 int32_t pplx_run_layer(dz_ctx *ctx, dz_pplx *p, int index, size_t n, const int32_t *markers, size_t count,
-                       size_t *rows_out) {
+                       size_t *rows_out, int part = DZ_PPLX_WHOLE) {
     const auto &L = p->layers[index];
     auto &st = p->st;
     int32_t rc;
@@ -1589,12 +1652,20 @@ int32_t pplx_run_layer(dz_ctx *ctx, dz_pplx *p, int index, size_t n, const int32
         }
     }
     size_t rows = n;
-    if (L.attention) {
-        rc = attention_layer(ctx, p, L, n, markers, count, &rows);
+    trace_reset(p, index, L.attention, n);
+    if (part != DZ_PPLX_MLP) {
+        p->trace.mixer = true;
+        if (L.attention) {
+            rc = attention_layer(ctx, p, L, n, markers, count, &rows);
+        } else {
+            rc = delta_layer(ctx, p, L, n);
+        }
     } else {
-        rc = delta_layer(ctx, p, L, n);
+        rc = DZ_OK;
     }
-    if (!rc) rc = mlp(ctx, p, L, rows);
+    p->trace.nq = rows;
+    if (!rc && part != DZ_PPLX_MIXER) rc = mlp(ctx, p, L, rows);
+    p->trace.rows = rows;
     if (st.on) {  // the bank is free again once this layer's kernels have run
         hipError_t e = hipEventRecord(st.done[index % 2], ctx_stream(ctx));
         if (!rc && e != hipSuccess) return ctx_hip_fail(ctx, e, "layer weight release");
@@ -1641,8 +1712,12 @@ int32_t pplx_residency_info(dz_ctx *ctx, dz_pplx *p, char *json, size_t cap) {
 }
 
 int32_t pplx_layer(dz_ctx *ctx, dz_pplx *p, int index, float *hidden, size_t n, const int32_t *markers_host,
-                   size_t count) {
+                   size_t count, int part) {
     if (!p || !hidden) return ctx_fail(ctx, DZ_INVALID_REQUEST, "null pointer");
+    if (part != DZ_PPLX_WHOLE && part != DZ_PPLX_MIXER && part != DZ_PPLX_MLP)
+        return ctx_fail(ctx, DZ_INVALID_PARAMETERS, "unknown layer part");
+    if (part == DZ_PPLX_MLP && markers_host)
+        return ctx_fail(ctx, DZ_INVALID_REQUEST, "markers cut the mixer's rows: the MLP half takes none");
     if (index < 0 || index >= p->cfg.layers) return ctx_fail(ctx, DZ_INVALID_REQUEST, "layer index out of range");
     if (n == 0 || n > (size_t)kMaxKeys) return ctx_fail(ctx, DZ_INPUT_TOO_LONG, "sequence length outside 1..8192");
     std::string missing;
@@ -1663,11 +1738,64 @@ int32_t pplx_layer(dz_ctx *ctx, dz_pplx *p, int index, float *hidden, size_t n, 
         e = hipMemcpyAsync(p->markers, markers_host, count * 4, hipMemcpyHostToDevice, s);
     if (e != hipSuccess) return ctx_hip_fail(ctx, e, "pplx layer input");
     size_t rows = n;
-    rc = pplx_run_layer(ctx, p, index, n, markers_host ? p->markers : nullptr, count, &rows);
+    rc = pplx_run_layer(ctx, p, index, n, markers_host ? p->markers : nullptr, count, &rows, part);
     if (rc) return rc;
     e = hipMemcpyAsync(hidden, p->hidden, rows * d * 4, hipMemcpyDeviceToDevice, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) return ctx_hip_fail(ctx, e, "pplx layer output");
+    return DZ_OK;
+}
+
+// A copy of the activation `name` that the last layer call left (rows of
+// `width` bytes, `pitch` apart in the model's buffer) into out_dev.
+int32_t pplx_activation(dz_ctx *ctx, dz_pplx *p, const char *name, void *out, size_t bytes) {
+    if (!p || !name || !out) return ctx_fail(ctx, DZ_INVALID_REQUEST, "null pointer");
+    const auto &t = p->trace;
+    if (t.layer < 0) return ctx_fail(ctx, DZ_INVALID_REQUEST, "no layer has run");
+    const dz_pplx_config &c = p->cfg;
+    const size_t d = c.hidden, cw = conv_width(c), lh = c.delta_heads, lv = lh * kLd;
+    const size_t ah = c.attn_heads, qw = 2 * ah * kAd, kvw = (size_t)c.attn_kv_heads * kAd;
+    const size_t gw = t.attention ? ah * kAd : lv;  // the gate's width
+    const std::string nm(name);
+    const void *src = nullptr;
+    size_t width = 0, pitch = 0, rows = 0;
+    bool ok = true;
+    auto set = [&](const void *ptr, size_t row_bytes, size_t count, size_t row_pitch, bool valid) {
+        src = ptr;
+        width = row_bytes;
+        rows = count;
+        pitch = row_pitch ? row_pitch : row_bytes;
+        ok = valid;
+    };
+    if (nm == "hidden") set(p->hidden, d * 4, t.rows, 0, true);
+    else if (nm == "norm_codes") set(p->ncodes, d, t.n, 0, t.norm_codes);
+    else if (nm == "norm_scales") set(p->nscales, d / 64 * 4, t.n, 0, t.norm_codes);
+    else if (nm == "normed") set(p->normed, d * 4, t.n, 0, t.normed);
+    else if (nm == "gate_codes") set(p->codes, gw, t.nq, 0, t.gate_codes);
+    else if (nm == "gate_scales") set(p->code_scales, gw / 64 * 4, t.nq, 0, t.gate_codes);
+    else if (nm == "gate") set(p->ctx, gw * 4, t.nq, 0, t.gate_f32);
+    else if (nm == "mlp_codes") set(p->codes, (size_t)c.ff, t.rows, 0, t.mlp_codes);
+    else if (nm == "mlp_scales") set(p->code_scales, (size_t)c.ff / 64 * 4, t.rows, 0, t.mlp_codes);
+    else if (!t.attention && nm == "qkv") set(p->wide, cw * 4, t.n, 0, t.mixer);
+    else if (!t.attention && nm == "z") set(p->z, lv * 4, t.n, (size_t)t.z_ld * 4, t.mixer && t.z_ld > 0);
+    else if (!t.attention && nm == "a") set(t.a, lh * 4, t.n, (size_t)t.ab_ld * 4, t.mixer && t.a != nullptr);
+    else if (!t.attention && nm == "b") set(t.b, lh * 4, t.n, (size_t)t.ab_ld * 4, t.mixer && t.b != nullptr);
+    else if (!t.attention && nm == "conv") set(p->conv_out, cw * 4, t.n, 0, t.mixer);
+    else if (!t.attention && nm == "heads") set(p->heads, kLd * 4, lh * t.n, 0, t.mixer);
+    else if (t.attention && nm == "q") set(p->wide, qw * 4, t.nq, 0, t.mixer);
+    else if (t.attention && nm == "query") set(p->query, ah * kAd * 4, t.nq, 0, t.mixer);
+    else if (t.attention && nm == "key") set(p->key, kvw * 4, t.n, 0, t.mixer);
+    else if (t.attention && nm == "value") set(p->value, kvw * 4, t.n, 0, t.mixer);
+    else if (t.attention && nm == "heads") set(p->heads, kAd * 4, ah * t.nq, 0, t.mixer);
+    else return ctx_fail(ctx, DZ_INVALID_PARAMETERS, "unknown activation for this layer: " + nm);
+    if (!ok) return ctx_fail(ctx, DZ_INVALID_REQUEST, "the last layer call did not produce " + nm);
+    if (bytes != width * rows)
+        return ctx_fail(ctx, DZ_INVALID_PARAMETERS,
+                        nm + " holds " + std::to_string(width * rows) + " bytes, not " + std::to_string(bytes));
+    hipStream_t s = ctx_stream(ctx);
+    hipError_t e = hipMemcpy2DAsync(out, width, src, pitch, width, rows, hipMemcpyDeviceToDevice, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return ctx_hip_fail(ctx, e, "pplx activation copy");
     return DZ_OK;
 }
 

@@ -538,38 +538,47 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const uint8_t *__restr
                     if (u < MPAD * 32) *(uint4_t *)(slice + (u / 32) * S::XROW + (u % 32) * 16) = st[q][L];
                     else if (u < S::UNITS) *(uint4_t *)(slice + MPAD * S::XROW + (u - MPAD * 32) * 16) = st[q][L];
                 }
-                half8_t a[2][4];
-                uint2_t sc[2];
+                // One k-block's four MFMAs at a time where four output rows are live
+                // (fewer registers, more resident waves); both k-blocks' eight back to
+                // back otherwise. The scale FMAs run in the same order either way.
+                constexpr int HB = S::LIVE >= 4 ? 1 : 2;
 #pragma unroll
-                for (int h = 0; h < 2; h++) {
-                    sc[h] = *(const uint2_t *)(slice + MPAD * S::XROW + h * 128 + j * 8);
+                for (int h0 = 0; h0 < 2; h0 += HB) {
+                    half8_t a[HB][4];
+                    uint2_t sc[HB];
 #pragma unroll
-                    for (int s = 0; s < 4; s++) a[h][s] = *(const half8_t *)(arow + (h * 128 + s * 32) * 2);
-                }
-                float4_t pr[2][4];
+                    for (int hh = 0; hh < HB; hh++) {
+                        const int h = h0 + hh;
+                        sc[hh] = *(const uint2_t *)(slice + MPAD * S::XROW + h * 128 + j * 8);
 #pragma unroll
-                for (int h = 0; h < 2; h++)
-#pragma unroll
-                    for (int s = 0; s < 4; s++) pr[h][s] = mfma_f16(a[h][s], as_half8(unpack_codes(cw[q][h][s], magic)), fz);
-                // Every register of every MFMA result stays allocated until here. Left
-                // to itself the compiler hands the registers of the unused result rows
-                // to the next unpack while the MFMA is still writing them.
-#pragma unroll
-                for (int h = 0; h < 2; h++)
-#pragma unroll
-                    for (int s = 0; s < 4; s++) asm volatile("" : "+v"(pr[h][s]));
-#pragma unroll
-                for (int h = 0; h < 2; h++)
-#pragma unroll
-                    for (int s = 0; s < 4; s++) {
-                        float scale;
-                        if (G32)
-                            scale = f16_bits_to_float((sc[h][s >> 1] >> (16 * (s & 1))) & 0xffffu);
-                        else
-                            scale = word_as_float(sc[h][s >> 1]);
-#pragma unroll
-                        for (int v = 0; v < S::LIVE; v++) acc[v] = __builtin_fmaf(pr[h][s][v], scale, acc[v]);
+                        for (int s = 0; s < 4; s++) a[hh][s] = *(const half8_t *)(arow + (h * 128 + s * 32) * 2);
                     }
+                    float4_t pr[HB][4];
+#pragma unroll
+                    for (int hh = 0; hh < HB; hh++)
+#pragma unroll
+                        for (int s = 0; s < 4; s++)
+                            pr[hh][s] = mfma_f16(a[hh][s], as_half8(unpack_codes(cw[q][h0 + hh][s], magic)), fz);
+                    // Every register of every MFMA result stays allocated until here. Left
+                    // to itself the compiler hands the registers of the unused result rows
+                    // to the next unpack while the MFMA is still writing them.
+#pragma unroll
+                    for (int hh = 0; hh < HB; hh++)
+#pragma unroll
+                        for (int s = 0; s < 4; s++) asm volatile("" : "+v"(pr[hh][s]));
+#pragma unroll
+                    for (int hh = 0; hh < HB; hh++)
+#pragma unroll
+                        for (int s = 0; s < 4; s++) {
+                            float scale;
+                            if (G32)
+                                scale = f16_bits_to_float((sc[hh][s >> 1] >> (16 * (s & 1))) & 0xffffu);
+                            else
+                                scale = word_as_float(sc[hh][s >> 1]);
+#pragma unroll
+                            for (int v = 0; v < S::LIVE; v++) acc[v] = __builtin_fmaf(pr[hh][s][v], scale, acc[v]);
+                        }
+                }
             }
         }
 #pragma unroll
@@ -593,6 +602,100 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const uint8_t *__restr
     const int col = t * 16 + j;
 #pragma unroll
     for (int v = 0; v < S::LIVE; v++) {
+        const int r = qd * 4 + v;
+        if (r < m && col < n) y[(size_t)r * n + col] = total[v];
+    }
+}
+
+// Streaming form for wide products (several 16-row tiles per SIMD): one wave
+// owns a whole tile, so no partial sum crosses waves, and it keeps D k-blocks
+// of codes and scale records in flight while it computes. The block's
+// activation rows are staged in LDS once. The wave walks the tile chunk by
+// chunk (chunk c = k-blocks c, c + 16, ...; K a multiple of 2048, so every
+// chunk holds kbs / 16 of them), folds each chunk into one accumulator with
+// the per-32-run scale FMAs, and adds a finished chunk to the total in chunk
+// order: the arithmetic of gemv_kernel, so the outputs are bitwise equal.
+template <int WAVES, int MPAD, bool G32, int D>
+__global__ __launch_bounds__(WAVES * 64) void gemv_stream_kernel(const uint8_t *__restrict__ codes,
+                                                                 const uint8_t *__restrict__ scales,
+                                                                 const half_t *__restrict__ x, int m,
+                                                                 int k, int n, int kbs,
+                                                                 float *__restrict__ y) {
+    constexpr int LIVE = GemvShape<MPAD>::LIVE;
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int xrow = kbs * 256 + 16;  // staged row: kbs * 128 f16 + 16 bytes of pad
+    const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const int qd = lane / 16, j = lane % 16;
+    const int units = MPAD * kbs * 16;  // 16-byte units of the MPAD staged rows
+    for (int u = threadIdx.x; u < units; u += WAVES * 64) {
+        const int r = u / (kbs * 16), c = u % (kbs * 16);
+        uint4_t v = {0u, 0u, 0u, 0u};
+        if (r < m && c * 8 < k) v = *(const uint4_t *)(x + (size_t)r * k + c * 8);
+        *(uint4_t *)(lds + r * xrow + c * 16) = v;
+    }
+    __syncthreads();
+    const int t = blockIdx.x * WAVES + wave;
+    if (t * 16 >= n) return;
+    const uint8_t *cbase = codes + q4_lane(t, 0, kbs, qd, j);
+    const uint8_t *sbase = scales + (size_t)t * kbs * 128 + j * 8;
+    const uint8_t *arow = lds + (j % MPAD) * xrow + qd * 16;
+    const int per = kbs / kGemvChunks;  // k-blocks per chunk (kbs % 16 == 0)
+    const uint32_t magic = 0x64006400u;
+    const float4_t fz = {0.f, 0.f, 0.f, 0.f};
+    uint4_t cw[D];
+    uint2_t sc[D];
+#pragma unroll
+    for (int r = 0; r < D; r++) {
+        const int kb = r < kbs ? r / per + kGemvChunks * (r % per) : 0;
+        cw[r] = __builtin_nontemporal_load((const uint4_t *)(cbase + (size_t)kb * 1024));
+        sc[r] = *(const uint2_t *)(sbase + (size_t)kb * 128);
+    }
+    float acc[LIVE], total[LIVE];
+#pragma unroll
+    for (int v = 0; v < LIVE; v++) acc[v] = total[v] = 0.0f;
+    for (int p0 = 0; p0 < kbs; p0 += D) {
+#pragma unroll
+        for (int r = 0; r < D; r++) {
+            const int p = p0 + r;
+            if (p >= kbs) break;
+            const int kb = p / per + kGemvChunks * (p % per);
+            half8_t a[4];
+#pragma unroll
+            for (int s = 0; s < 4; s++) a[s] = *(const half8_t *)(arow + (kb * 128 + s * 32) * 2);
+            float4_t pr[4];
+#pragma unroll
+            for (int s = 0; s < 4; s++) pr[s] = mfma_f16(a[s], as_half8(unpack_codes(cw[r][s], magic)), fz);
+#pragma unroll
+            for (int s = 0; s < 4; s++) asm volatile("" : "+v"(pr[s]));
+            const uint2_t scr = sc[r];
+            // refill the slot with the k-block D positions ahead (a valid block past the end)
+            const int pn = p + D;
+            const int kbn = pn < kbs ? pn / per + kGemvChunks * (pn % per) : 0;
+            cw[r] = __builtin_nontemporal_load((const uint4_t *)(cbase + (size_t)kbn * 1024));
+            sc[r] = *(const uint2_t *)(sbase + (size_t)kbn * 128);
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                float scale;
+                if (G32)
+                    scale = f16_bits_to_float((scr[s >> 1] >> (16 * (s & 1))) & 0xffffu);
+                else
+                    scale = word_as_float(scr[s >> 1]);
+#pragma unroll
+                for (int v = 0; v < LIVE; v++) acc[v] = __builtin_fmaf(pr[s][v], scale, acc[v]);
+            }
+            if (p % per == per - 1) {
+#pragma unroll
+                for (int v = 0; v < LIVE; v++) {
+                    total[v] = p == per - 1 ? acc[v] : __fadd_rn(total[v], acc[v]);
+                    acc[v] = 0.0f;
+                }
+            }
+        }
+    }
+    if (qd * 4 >= MPAD) return;
+    const int col = t * 16 + j;
+#pragma unroll
+    for (int v = 0; v < LIVE; v++) {
         const int r = qd * 4 + v;
         if (r < m && col < n) y[(size_t)r * n + col] = total[v];
     }
@@ -2055,7 +2158,7 @@ inline unsigned cdiv(size_t a, size_t b) { return (unsigned)((a + b - 1) / b); }
 
 // ---- variant tables -------------------------------------------------------------
 
-const char *const kGemvNames[] = {"w16", "w8"};
+const char *const kGemvNames[] = {"auto", "w16", "w8", "stream8", "stream4"};
 const char *const kGemmNames[] = {"pipe-auto",   "256x256p2w8", "128x128p2w4", "128x256p2w8",
                                    "256x128w2x2", "128x128w2x2", "128x64w2x2", "256x256p2w8-persist",
                                    "256x192p2w8-persist", "256x128p2w8"};
@@ -2066,7 +2169,7 @@ const char *const kGroupedNames[] = {"pipe-auto",    "pipe256x128w8", "wave16x16
                                      "pipe64x128w2", "pipe128x128m8", "pipe128x128n8", "pipe32x128w8",
                                      "pipe64x128w8"};
 const char *const kMlpNames[] = {"pipe-auto", "pipe256x64w8", "pipe128x64w4", "wave16x64", "pipe256x64n2", "pipe128x64n2"};
-const char *const kDeltaNames[] = {"auto", "recurrent", "chunked64"};
+const char *const kDeltaNames[] = {"recurrent", "recurrent-rolled", "chunked64", "auto"};
 const char *const kNormNames[] = {"fused", "separate"};
 
 template <int W, int MPAD, bool G32, int NP>
@@ -2104,6 +2207,42 @@ void gemv_launch_m(const Weight &w, const half_t *x, int m, float *y, hipStream_
     else if (m <= 4) gemv_launch_one<W, 4, G32>(w, x, m, y, s);
     else if (m <= 8) gemv_launch_one<W, 8, G32>(w, x, m, y, s);
     else gemv_launch_one<W, 16, G32>(w, x, m, y, s);
+}
+
+// The streaming GEMV: one wave per 16-row tile, WAVES tiles per block. False
+// (nothing launched) when K is not a multiple of 2048 or the staged rows
+// would not leave room for two blocks per compute unit.
+template <int WAVES, int MPAD, bool G32, int D>
+bool gemv_stream_launch(const Weight &w, const half_t *x, int m, float *y, hipStream_t s) {
+    const int kbs = w.kblocks();
+    const size_t lds = (size_t)MPAD * ((size_t)kbs * 256 + 16);
+    if (kbs % kGemvChunks != 0 || lds > 80 * 1024) return false;
+    static bool configured[64] = {};  // the LDS limit is a per-device function attribute
+    int dev = 0;
+    hipGetDevice(&dev);
+    if (dev >= 0 && dev < 64 && !configured[dev]) {
+        if (hipFuncSetAttribute((const void *)gemv_stream_kernel<WAVES, MPAD, G32, D>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) == hipSuccess)
+            configured[dev] = true;
+    }
+    hipLaunchKernelGGL((gemv_stream_kernel<WAVES, MPAD, G32, D>), dim3(cdiv(w.tiles(), WAVES)), dim3(WAVES * 64),
+                       lds, s, w.codes, w.scales, x, m, w.cols, w.rows, kbs, y);
+    return true;
+}
+
+template <int WAVES, bool G32, int D>
+bool gemv_stream_m(const Weight &w, const half_t *x, int m, float *y, hipStream_t s) {
+    if (m <= 1) return gemv_stream_launch<WAVES, 1, G32, D>(w, x, m, y, s);
+    if (m <= 2) return gemv_stream_launch<WAVES, 2, G32, D>(w, x, m, y, s);
+    if (m <= 4) return gemv_stream_launch<WAVES, 4, G32, D>(w, x, m, y, s);
+    if (m <= 8) return gemv_stream_launch<WAVES, 8, G32, D>(w, x, m, y, s);
+    return false;
+}
+
+template <int WAVES, int D>
+bool gemv_stream(const Weight &w, const half_t *x, int m, float *y, hipStream_t s) {
+    if (w.kind == WeightKind::Q4G32) return gemv_stream_m<WAVES, true, D>(w, x, m, y, s);
+    return gemv_stream_m<WAVES, false, D>(w, x, m, y, s);
 }
 
 template <int W>
@@ -2252,14 +2391,20 @@ void gv_launch(const Weight &w, const void *a, const float *sa, int m, int abits
 
 int variant_count(const char *family) {
     std::string f(family);
-    if (f == "gemv") return 2;
+    if (f == "gemv") return 5;
     if (f == "gemm_w4a16") return 10;
     if (f == "i8_gemm") return 10;
     if (f == "grouped") return 9;
     if (f == "mlp") return 6;
-    if (f == "delta_scan") return 3;
+    if (f == "delta_scan") return 4;
     if (f == "norm") return 2;
     return 0;
+}
+
+int tuned_count(const char *family) {
+    // the chunked and "auto" delta scans regroup the rule's arithmetic
+    if (std::string(family) == "delta_scan") return 2;
+    return variant_count(family);
 }
 
 const char *variant_name(const char *family, int index) {
@@ -2444,7 +2589,22 @@ void launch_w4a16(const Weight &w, const half_t *x, int m, float *y, int gemv_va
                   int gemm_variant, hipStream_t s) {
     if (m == 0) return;
     if (m <= 16) {
-        if (gemv_variant == 1)
+        int v = gemv_variant;
+        if (v == 0) {
+            // "auto": the split kernel, except at 2..8 rows over wide weights (eight or
+            // more 16-row tiles per compute unit), where the streaming kernel keeps more
+            // bytes in flight per compute unit (measured at K = 4096: M = 4, N = 65536
+            // 33 against 39 us; M = 8, 36 against 51 us; at N = 16384 the split kernel
+            // is faster, and at M = 1 the two are within 2-6% up to N = 131072)
+            const int cus = device_cus();
+            if (m >= 2 && m <= 8 && w.tiles() >= 8 * cus) v = m > 4 && w.tiles() >= 16 * cus ? 3 : 4;
+            else v = 1;
+        }
+        bool done = false;
+        if (v == 3) done = gemv_stream<8, 8>(w, x, m, y, s);
+        else if (v == 4) done = gemv_stream<4, 8>(w, x, m, y, s);
+        if (done) return;
+        if (v == 2)
             gemv_launch<8>(w, x, m, y, s);
         else
             gemv_launch<16>(w, x, m, y, s);

@@ -10,6 +10,7 @@
 #include <string.h>
 
 #include <map>
+#include <set>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -34,12 +35,17 @@ struct dz_ctx {
     // ring, [kCaptureSlot0 ..] one flag per product recorded under stream capture
     int *flag = nullptr;
     uint64_t product_calls = 0;  // ring products since the last stream change (picks the slot)
-    int captured_flags = 0;      // capture slots handed out so far
+    int captured_flags = 0;      // capture slots ever handed out (the high-water mark)
+    std::vector<int> free_capture_slots;                          // slots given back, reused first
+    std::map<unsigned long long, std::vector<int>> capture_slots;  // capture id -> slots it holds
     void *work = nullptr; // activation quantization workspace
     size_t work_bytes = 0;
-    bool work_captured = false;        // a captured graph refers to `work`
     uint8_t *scratch = nullptr;        // device address of this device's `scratch` array
-    std::vector<void *> retired_work;  // workspaces captured graphs may still use; freed at dz_destroy
+    // workspace -> ids of the captures that recorded it; a workspace replaced
+    // while a capture still holds it is retired, and freed when the last of
+    // its captures is released (or at dz_destroy)
+    std::map<void *, std::set<unsigned long long>> work_users;
+    std::vector<void *> retired_work;
     std::map<std::string, int> variants;
     std::string tuning;   // JSON of the last selection
 };
@@ -73,8 +79,8 @@ int32_t pplx_set_weight(dz_ctx *ctx, dz_pplx *p, const char *name, const void *p
                         size_t rows, size_t cols);
 int32_t pplx_set_vector(dz_ctx *ctx, dz_pplx *p, const char *name, const float *values, size_t count);
 int32_t pplx_layer(dz_ctx *ctx, dz_pplx *p, int index, float *hidden, size_t n, const int32_t *markers_host,
-                   size_t count);
-int32_t probe_rate(dz_ctx *ctx, int cus, const char *what, int zero, double *rate);
+                   size_t count, int part);
+int32_t pplx_activation(dz_ctx *ctx, dz_pplx *p, const char *name, void *out, size_t bytes);
 int32_t pplx_set_residency(dz_ctx *ctx, dz_pplx *p, int32_t residency);
 int32_t pplx_residency_info(dz_ctx *ctx, dz_pplx *p, char *json, size_t cap);
 int32_t pplx_forward_rows(dz_ctx *ctx, dz_pplx *p, const void *rows_host, size_t n, const int32_t *markers,
@@ -145,6 +151,36 @@ bool capturing(dz_ctx *ctx) {
     return hipStreamIsCapturing(ctx->stream, &st) == hipSuccess && st != hipStreamCaptureStatusNone;
 }
 
+// The id of the capture the context stream is recording (valid while capturing).
+unsigned long long capture_id(dz_ctx *ctx) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    unsigned long long id = 0;
+    if (hipStreamGetCaptureInfo(ctx->stream, &st, &id) != hipSuccess || st == hipStreamCaptureStatusNone) return 0;
+    return id;
+}
+
+// Frees the retired workspaces no capture holds any more. Not while the
+// context stream records: a free during a global-mode capture invalidates it.
+void free_unused_retired(dz_ctx *ctx) {
+    if (capturing(ctx)) return;
+    bool synced = false;
+    for (size_t i = 0; i < ctx->retired_work.size();) {
+        void *p = ctx->retired_work[i];
+        auto it = ctx->work_users.find(p);
+        if (it != ctx->work_users.end() && !it->second.empty()) {
+            i++;
+            continue;
+        }
+        if (!synced) {
+            hipStreamSynchronize(ctx->stream);
+            synced = true;
+        }
+        hipFree(p);
+        if (it != ctx->work_users.end()) ctx->work_users.erase(it);
+        ctx->retired_work.erase(ctx->retired_work.begin() + i);
+    }
+}
+
 // Resets the flag, then returns its value after running `enqueue` and syncing.
 // Synchronous calls cannot be recorded into a graph.
 template <class F>
@@ -166,14 +202,26 @@ int32_t flagged_sync(dz_ctx *ctx, F enqueue, int *value) {
 //    one launch the stream orders after every earlier product, each time the
 //    ring starts over (instead of one clearing launch per product).
 //  - A call recorded under stream capture takes a slot of its own, which no
-//    other call uses, and clears it with a fill kernel recorded just before the
+//    other call uses until dz_capture_release gives back the slots of its
+//    capture, and clears it with a fill kernel recorded just before the
 //    product, so every replay starts from a clear flag. Replays of one graph
-//    must not overlap each other.
+//    must not overlap each other. At most kCaptureSlots recorded products hold
+//    slots at once.
 int32_t product_flag(dz_ctx *ctx, int **out) {
     if (capturing(ctx)) {
-        if (ctx->captured_flags >= kCaptureSlots)
-            return fail(ctx, DZ_RESOURCE_LIMIT, "too many products recorded under stream capture on this context");
-        int *slot = ctx->flag + kCaptureSlot0 + ctx->captured_flags++;
+        int index;
+        if (!ctx->free_capture_slots.empty()) {
+            index = ctx->free_capture_slots.back();
+            ctx->free_capture_slots.pop_back();
+        } else if (ctx->captured_flags < kCaptureSlots) {
+            index = ctx->captured_flags++;
+        } else {
+            return fail(ctx, DZ_RESOURCE_LIMIT,
+                        "4032 products recorded under stream capture hold flag slots on this context: release the "
+                        "captures of destroyed graphs with dz_capture_release");
+        }
+        ctx->capture_slots[capture_id(ctx)].push_back(index);
+        int *slot = ctx->flag + kCaptureSlot0 + index;
         dz::launch_fill_i32(slot, 0, 1, ctx->stream);
         *out = slot;
         return DZ_OK;
@@ -185,13 +233,14 @@ int32_t product_flag(dz_ctx *ctx, int **out) {
 }
 
 // Makes the context workspace at least `bytes` long. Growing it waits for the
-// context stream; a workspace that a captured graph refers to is kept alive
-// (until dz_destroy) instead of being freed. Under capture the workspace cannot
-// grow: the caller runs the same call once before capturing it.
+// context stream; a workspace that a captured graph refers to is retired
+// instead of freed, and freed once every capture that recorded it has been
+// released (dz_capture_release) or at dz_destroy. Under capture the workspace
+// cannot grow: the caller runs the same call once before capturing it.
 int32_t ensure_work(dz_ctx *ctx, size_t bytes) {
     const bool cap = capturing(ctx);
     if (ctx->work_bytes >= bytes) {
-        if (cap) ctx->work_captured = true;
+        if (cap) ctx->work_users[ctx->work].insert(capture_id(ctx));
         return DZ_OK;
     }
     if (cap)
@@ -199,13 +248,15 @@ int32_t ensure_work(dz_ctx *ctx, size_t bytes) {
                     "the workspace cannot grow during stream capture: run the call once before capturing it");
     if (ctx->work) {
         DZ_HIP(ctx, hipStreamSynchronize(ctx->stream), "stream synchronize");
-        if (ctx->work_captured)
+        auto it = ctx->work_users.find(ctx->work);
+        if (it != ctx->work_users.end() && !it->second.empty()) {
             ctx->retired_work.push_back(ctx->work);
-        else
+        } else {
+            if (it != ctx->work_users.end()) ctx->work_users.erase(it);
             hipFree(ctx->work);
+        }
         ctx->work = nullptr;
         ctx->work_bytes = 0;
-        ctx->work_captured = false;
     }
     size_t want = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
     DZ_HIP(ctx, hipMalloc(&ctx->work, want), "workspace allocation");
@@ -399,6 +450,39 @@ int32_t dz_sync(dz_ctx *ctx) {
     return DZ_OK;
 }
 
+int32_t dz_capture_id(dz_ctx *ctx, uint64_t *id) {
+    DZ_BEGIN(ctx);
+    if (!id) return fail(ctx, DZ_INVALID_REQUEST, "null output");
+    if (!capturing(ctx)) return fail(ctx, DZ_INVALID_REQUEST, "the context stream is not recording a graph");
+    *id = capture_id(ctx);
+    return DZ_OK;
+}
+
+int32_t dz_capture_release(dz_ctx *ctx, uint64_t id) {
+    DZ_BEGIN(ctx);
+    if (capturing(ctx) && capture_id(ctx) == id)
+        return fail(ctx, DZ_INVALID_REQUEST, "the capture is still recording: release it after hipStreamEndCapture");
+    auto it = ctx->capture_slots.find(id);
+    if (it != ctx->capture_slots.end()) {
+        for (int index : it->second) ctx->free_capture_slots.push_back(index);
+        ctx->capture_slots.erase(it);
+    }
+    for (auto &kv : ctx->work_users) kv.second.erase(id);
+    free_unused_retired(ctx);
+    return DZ_OK;
+}
+
+int32_t dz_capture_release_all(dz_ctx *ctx) {
+    DZ_BEGIN(ctx);
+    if (capturing(ctx)) return fail(ctx, DZ_INVALID_REQUEST, "the context stream is recording a graph");
+    ctx->capture_slots.clear();
+    ctx->free_capture_slots.clear();
+    ctx->captured_flags = 0;
+    ctx->work_users.clear();
+    free_unused_retired(ctx);
+    return DZ_OK;
+}
+
 int32_t dz_info(dz_ctx *ctx, char *buf, size_t cap) {
     DZ_BEGIN(ctx);
     std::string s = "{\"arch\":\"" + ctx->arch + "\",\"compute_units\":" + std::to_string(ctx->cus) +
@@ -409,7 +493,12 @@ int32_t dz_info(dz_ctx *ctx, char *buf, size_t cap) {
         first = false;
         s += std::string("\"") + f + "\":\"" + dz::variant_name(f, variant(ctx, f)) + "\"";
     }
-    s += "},\"tuning\":" + (ctx->tuning.empty() ? std::string("null") : ctx->tuning) + "}";
+    s += "},\"tuning\":" + (ctx->tuning.empty() ? std::string("null") : ctx->tuning);
+    size_t held = 0;
+    for (const auto &kv : ctx->capture_slots) held += kv.second.size();
+    s += ",\"capture_slots\":{\"held\":" + std::to_string(held) + ",\"limit\":" + std::to_string(kCaptureSlots) +
+         ",\"captures\":" + std::to_string(ctx->capture_slots.size()) +
+         ",\"retired_workspaces\":" + std::to_string(ctx->retired_work.size()) + "}}";
     if (!buf || cap < s.size() + 1) return fail(ctx, DZ_RESOURCE_LIMIT, "info buffer too small");
     memcpy(buf, s.c_str(), s.size() + 1);
     return DZ_OK;
@@ -1006,7 +1095,20 @@ int32_t dz_pplx_layer(dz_ctx *ctx, dz_pplx *model, int32_t layer, float *hidden,
                       size_t count) {
     DZ_BEGIN(ctx);
     DZ_NOT_CAPTURING(ctx);
-    return dz::pplx_layer(ctx, model, layer, hidden, n, markers, count);
+    return dz::pplx_layer(ctx, model, layer, hidden, n, markers, count, DZ_PPLX_WHOLE);
+}
+
+int32_t dz_pplx_layer_part(dz_ctx *ctx, dz_pplx *model, int32_t layer, int32_t part, float *hidden, size_t n,
+                           const int32_t *markers, size_t count) {
+    DZ_BEGIN(ctx);
+    DZ_NOT_CAPTURING(ctx);
+    return dz::pplx_layer(ctx, model, layer, hidden, n, markers, count, part);
+}
+
+int32_t dz_pplx_activation(dz_ctx *ctx, dz_pplx *model, const char *name, void *out_dev, size_t bytes) {
+    DZ_BEGIN(ctx);
+    DZ_NOT_CAPTURING(ctx);
+    return dz::pplx_activation(ctx, model, name, out_dev, bytes);
 }
 
 int32_t dz_pplx_forward_rows(dz_ctx *ctx, dz_pplx *model, const void *rows, size_t n, const int32_t *markers,
@@ -1025,12 +1127,6 @@ int32_t dz_pplx_set_residency(dz_ctx *ctx, dz_pplx *model, int32_t residency) {
 int32_t dz_pplx_residency_info(dz_ctx *ctx, dz_pplx *model, char *json, size_t cap) {
     DZ_BEGIN(ctx);
     return dz::pplx_residency_info(ctx, model, json, cap);
-}
-
-int32_t dz_probe_rate(dz_ctx *ctx, const char *what, int32_t zero_operands, double *ops_per_second) {
-    DZ_BEGIN(ctx);
-    if (capturing(ctx)) return fail(ctx, DZ_INVALID_REQUEST, "synchronous call during stream capture");
-    return dz::probe_rate(ctx, ctx->cus, what, zero_operands, ops_per_second);
 }
 
 // ---- tuner ---------------------------------------------------------------------------

@@ -74,7 +74,7 @@ uint32_t test_hash(size_t i, size_t seed) {
 // checkpoint.rs:850: a small positive f32 scale, 0.001 + (hash % 1000) * 1e-5.
 float test_scale(size_t i, size_t seed) { return 0.001f + (float)(test_hash(i, seed) % 1000) * 1e-5f; }
 
-enum class Kind { Grouped, Mlp, Norm, Gemv, GemmW4A16, I8Gemm };
+enum class Kind { DeltaScan, Grouped, Mlp, Norm, Gemv, GemmW4A16, I8Gemm };
 
 struct Family {
     const char *name;
@@ -83,10 +83,15 @@ struct Family {
     int keep;  // candidates that stay after the first round (besides the reference)
 };
 
+// The reference's stages in its order (checkpoint.rs:251-262: delta scan,
+// norm, gemm, mlp), then the families of its own. The delta scan runs 128
+// tokens (checkpoint.rs:331) of the decider's 32 value and 16 key heads
+// (m = tokens, n = value heads, k = key heads).
 const Family kFamilies[] = {
+    {"delta_scan", Kind::DeltaScan, 128, 32, 16, 1},
+    {"norm", Kind::Norm, 64, 2560, 2560, 2},
     {"grouped", Kind::Grouped, 256, 8192, 2560, 3},
     {"mlp", Kind::Mlp, 128, 9216, 2560, 2},
-    {"norm", Kind::Norm, 64, 2560, 2560, 2},
     {"gemv", Kind::Gemv, 1, 8192, 2560, 3},
     {"gemm_w4a16", Kind::GemmW4A16, 256, 8192, 2560, 3},
     {"i8_gemm", Kind::I8Gemm, 256, 8192, 2560, 3},
@@ -163,11 +168,15 @@ struct Bench {
     const void *x = nullptr;  // f16 rows (W4A16), int8 A8 codes (grouped, MLP) or int8 rows (i8)
     const float *sx = nullptr, *sw = nullptr;
     const int8_t *b = nullptr;
+    const float *qhat = nullptr, *khat = nullptr, *conv = nullptr, *gb = nullptr;  // the delta scan's inputs
     std::vector<std::vector<std::pair<void *, size_t>>> outs;  // per candidate: output buffers
 
     void run(int v) {
         auto &o = outs[v];
         switch (kind) {
+            case Kind::DeltaScan:
+                launch_delta_scan_tokens(qhat, khat, conv, gb, m, n, k, (float *)o[0].first, v, s);
+                break;
             case Kind::Grouped:
                 launch_grouped(w, (const int8_t *)x, sx, m, (float *)o[0].first, nullptr, v, s);
                 break;
@@ -220,6 +229,30 @@ bool build_bench(DeviceBuffers &buf, const Family &f, int count, Bench *b) {
     b->s = buf.s;
     const size_t M = f.m, N = f.n, K = f.k;
     switch (f.kind) {
+        case Kind::DeltaScan: {
+            // unit-scale q, k and v and decays below one, as checkpoint.rs:336-342 builds
+            // them: x_i = ((i * 7919 % 2003) / 1001.5 - 1) * 0.09; g = 0.9 + (i % 7) / 100,
+            // beta = 0.5, k.q from the same generator
+            auto unit = [](size_t i) { return ((float)(i * 7919 % 2003) / 1001.5f - 1.0f) * 0.09f; };
+            const size_t lkv = K * 128, width = 2 * lkv + N * 128;
+            std::vector<float> hq(M * lkv), hk(M * lkv), hc(M * width), hg(M * N * 4);
+            for (size_t i = 0; i < hq.size(); i++) {
+                hq[i] = unit(i);
+                hk[i] = unit(i + 4096);
+            }
+            for (size_t i = 0; i < hc.size(); i++) hc[i] = unit(i + 8192);
+            for (size_t i = 0; i < M * N; i++) {
+                hg[4 * i] = 0.9f + (float)(i % 7) * 0.01f;
+                hg[4 * i + 1] = 0.5f;
+                hg[4 * i + 2] = unit(i + 12288);
+                hg[4 * i + 3] = 0.0f;
+            }
+            b->qhat = (const float *)buf.upload(hq);
+            b->khat = (const float *)buf.upload(hk);
+            b->conv = (const float *)buf.upload(hc);
+            b->gb = (const float *)buf.upload(hg);
+            break;
+        }
         case Kind::Grouped:
         case Kind::Mlp:
             b->w = test_weight(buf, WeightKind::Q4G64, f.n, f.k, 7);
@@ -264,6 +297,8 @@ bool build_bench(DeviceBuffers &buf, const Family &f, int count, Bench *b) {
             b->outs[v].push_back({buf.alloc(M * N), M * N});
             b->outs[v].push_back({buf.alloc(M * N / 64 * 4), M * N / 64 * 4});
             if (f.kind == Kind::Norm) b->outs[v].push_back({buf.alloc(M * N * 4), 0});
+        } else if (f.kind == Kind::DeltaScan) {
+            b->outs[v].push_back({buf.alloc(N * M * 128 * 4), N * M * 128 * 4});
         } else {
             b->outs[v].push_back({buf.alloc(M * N * 4), M * N * 4});
         }
@@ -354,14 +389,15 @@ int32_t tune(dz_ctx *ctx, uint32_t budget_ms, const char *cache_in, char *cache_
     report["key"] = key;
     report["budget_ms"] = (int64_t)budget_ms;
     for (const Family &fam : kFamilies) {
-        const int count = variant_count(fam.name);
+        const int count = tuned_count(fam.name);
         DeviceBuffers buf(s);
         Bench bench;
         if (!build_bench(buf, fam, count, &bench)) return ctx_hip_fail(ctx, buf.err, "tuner inputs");
         int fastest = -1;
         Json detail = Json::object();
         const std::string want = cached_choice(cache, key, fam.name);
-        const int cached_idx = want.empty() ? -1 : variant_index(fam.name, want.c_str());
+        int cached_idx = want.empty() ? -1 : variant_index(fam.name, want.c_str());
+        if (cached_idx >= count) cached_idx = -1;  // not a tuned candidate: tune again
         if (cached_idx >= 0) {
             bool agrees = cached_idx == 0;
             if (!agrees) {

@@ -52,8 +52,16 @@ public:
     // `residency` DZ_PPLX_STREAMED keeps the layer projections in pinned host
     // memory and runs each layer from one of two device banks
     // (webgpu/streaming.rs:16-369); the answers are the same bits.
+    // `tuning` (parameters.rs:13-28) runs the kernel tuner's selection stages
+    // on open, as checkpoint_with_tuning does on every load
+    // (webgpu/checkpoint.rs:241-262): the delta scan, the norm, the grouped
+    // product and the fused MLP among variants that give their reference's
+    // bits, within budget_ms, reusing a cached selection whose key matches.
+    // The selection JSON is tuning(); mode "off" or a zero budget keeps the
+    // reference variants.
     static Result<RocmPplx> open(int device, const std::string &dir, const dz_pplx_config &config,
-                                 const PackedModel &model = PackedModel{}, int32_t residency = DZ_PPLX_RESIDENT) {
+                                 const PackedModel &model = PackedModel{}, int32_t residency = DZ_PPLX_RESIDENT,
+                                 const TuningOptions &tuning = TuningOptions{}) {
         if ((size_t)config.layers != model.layers || (size_t)config.hidden != model.hidden)
             return Error("INVALID_PARAMETERS", "decoder shape differs from the checkpoint's");
         auto ck = PackedCheckpoint::open(dir, model);
@@ -63,6 +71,13 @@ public:
         RocmPplx r;
         int32_t rc = dz_init(device, &r.ctx_);
         if (rc != DZ_OK) return Error(dz_status_name(rc), "no context");
+        if (tuning.mode == TuningMode::Auto && tuning.budget_ms > 0) {
+            const std::string cache_in = tuning.cache ? tuning.cache->dump() : std::string();
+            std::vector<char> out(1 << 16);
+            rc = dz_tune(r.ctx_, tuning.budget_ms, tuning.cache ? cache_in.c_str() : nullptr, out.data(), out.size());
+            if (rc != DZ_OK) return r.fail(rc);
+            r.tuning_ = Json::parse(out.data());
+        }
         rc = dz_pplx_create(r.ctx_, &config, &r.model_);
         if (rc != DZ_OK) return r.fail(rc);
         const PackedCheckpoint &c = ck.value();
@@ -105,6 +120,7 @@ public:
             model_ = std::exchange(o.model_, nullptr);
             temperature_ = o.temperature_;
             checkpoint_ = std::move(o.checkpoint_);
+            tuning_ = std::move(o.tuning_);
         }
         return *this;
     }
@@ -115,6 +131,8 @@ public:
     dz_ctx *context() const { return ctx_; }
     dz_pplx *model() const { return model_; }
     float temperature() const { return temperature_; }
+    // The tuner's selection JSON of the last open (null when it did not run).
+    const Json &tuning() const { return tuning_; }
     const PackedCheckpoint &checkpoint() const { return *checkpoint_; }
 
     Capabilities capabilities() const { return Capabilities{"pplx-flash", "rocm", {"embedding"}, "auto"}; }
@@ -171,6 +189,7 @@ private:
     dz_pplx *model_ = nullptr;
     float temperature_ = 1.0f;
     std::shared_ptr<PackedCheckpoint> checkpoint_;
+    Json tuning_;
 };
 
 }  // namespace decisive

@@ -246,12 +246,25 @@ TEST(rocm_pplx_answers_from_a_packed_checkpoint) {
     PackedModel pm;
     pm.layers = 4;
     pm.hidden = 256;
-    auto made = RocmPplx::open(0, dir, cfg, pm);
+    // opened with the tuner (checkpoint.rs:241-262): the selection covers the
+    // reference's four stages and this library's families, each selection one
+    // whose output equals the reference variant's
+    TuningOptions tuned;
+    tuned.budget_ms = 4000;
+    auto made = RocmPplx::open(0, dir, cfg, pm, DZ_PPLX_RESIDENT, tuned);
     CHECK(made.ok());
     if (!made.ok()) {
         fprintf(stderr, "%s\n", made.error().to_string().c_str());
         return;
     }
+    const Json selection = made.value().tuning();
+    CHECK(selection.is_object());
+    for (const char *fam : {"delta_scan", "norm", "grouped", "mlp", "gemv", "gemm_w4a16", "i8_gemm"}) {
+        CHECK(selection["selected"][fam].is_string());
+        CHECK(selection["families"][fam].is_object());
+        CHECK(selection["families"][fam]["skipped"].is_null());
+    }
+    CHECK(selection["families"]["delta_scan"]["candidates"].as_array().size() == 2);
     Model<RocmPplx> model(made.take());
     RocmPplx &pplx = model.backend();
     CHECK(pplx.temperature() == 1.5539091673122623f);
@@ -288,10 +301,26 @@ TEST(rocm_pplx_answers_from_a_packed_checkpoint) {
     CHECK(dot / std::sqrt(gg * ww) >= 0.9999);
     CHECK(maxerr <= 1e-2 * scale);
     printf("pplx logits vs oracle: cos %.9f, max |d| %.5f of %.3f\n", dot / std::sqrt(gg * ww), maxerr, scale);
-    {  // the same checkpoint with streamed layer weights: the same bits
-        auto streamed = RocmPplx::open(0, dir, cfg, pm, DZ_PPLX_STREAMED);
+    {  // the same checkpoint untuned (the reference variants): the same bits
+        auto plain = RocmPplx::open(0, dir, cfg, pm, DZ_PPLX_RESIDENT, no_tuning());
+        CHECK(plain.ok() && plain.value().tuning().is_null());
+        if (plain.ok()) {
+            auto pl = plain.value().logits(rows.value(), ids.size(), markers);
+            CHECK(pl.ok() && pl.value().size() == lg.value().size() &&
+                  memcmp(pl.value().data(), lg.value().data(), lg.value().size() * sizeof(float)) == 0);
+        }
+    }
+    {  // streamed layer weights, tuned from the cached selection: the same bits
+        TuningOptions cached;
+        cached.cache = selection;
+        auto streamed = RocmPplx::open(0, dir, cfg, pm, DZ_PPLX_STREAMED, cached);
         CHECK(streamed.ok());
         if (streamed.ok()) {
+            const Json &again = streamed.value().tuning();
+            for (const char *fam : {"delta_scan", "norm", "grouped", "mlp"}) {
+                CHECK(again["families"][fam]["cached"] == Json(true));
+                CHECK(again["selected"][fam] == selection["selected"][fam]);
+            }
             auto sl = streamed.value().logits(rows.value(), ids.size(), markers);
             CHECK(sl.ok() && sl.value().size() == lg.value().size() &&
                   memcmp(sl.value().data(), lg.value().data(), lg.value().size() * sizeof(float)) == 0);
@@ -333,7 +362,7 @@ TEST(rocm_pplx_answers_from_a_packed_checkpoint) {
              std::string("INVALID_REQUEST"));
     dz_pplx_config wide = cfg;
     wide.hidden = 512;
-    CHECK(RocmPplx::open(0, dir, wide, pm).error().code == "INVALID_PARAMETERS");
+    CHECK(RocmPplx::open(0, dir, wide, pm, DZ_PPLX_RESIDENT, no_tuning()).error().code == "INVALID_PARAMETERS");
 }
 
 TEST(rocm_answer_requests_are_validated) {

@@ -30,6 +30,7 @@ F32, F16, BF16 = 0, 1, 2
 EPI_NONE, EPI_GELU, EPI_RESIDUAL = 0, 1, 2
 W4A8, W4A4, W4A16 = 0, 1, 2
 PPLX_RESIDENT, PPLX_STREAMED = 0, 1
+PPLX_WHOLE, PPLX_MIXER, PPLX_MLP = 0, 1, 2  # dz_pplx_layer_part's parts
 
 
 class DzError(RuntimeError):
@@ -89,6 +90,9 @@ _SIGNATURES = {
     "dz_last_error": (ctypes.c_char_p, [P]),
     "dz_set_stream": (I32, [P, P]),
     "dz_sync": (I32, [P]),
+    "dz_capture_id": (I32, [P, ctypes.POINTER(ctypes.c_uint64)]),
+    "dz_capture_release": (I32, [P, ctypes.c_uint64]),
+    "dz_capture_release_all": (I32, [P]),
     "dz_info": (I32, [P, ctypes.c_char_p, SZ]),
     "dz_alloc": (I32, [P, SZ, PP]),
     "dz_free": (I32, [P, P]),
@@ -141,10 +145,11 @@ _SIGNATURES = {
     "dz_pplx_set_weight": (I32, [P, P, ctypes.c_char_p, P, SZ, I32, SZ, SZ]),
     "dz_pplx_set_vector": (I32, [P, P, ctypes.c_char_p, P, SZ]),
     "dz_pplx_layer": (I32, [P, P, I32, P, SZ, P, SZ]),
+    "dz_pplx_layer_part": (I32, [P, P, I32, I32, P, SZ, P, SZ]),
+    "dz_pplx_activation": (I32, [P, P, ctypes.c_char_p, P, SZ]),
     "dz_pplx_forward_rows": (I32, [P, P, P, SZ, P, SZ, P]),
     "dz_pplx_set_residency": (I32, [P, P, I32]),
     "dz_pplx_residency_info": (I32, [P, P, ctypes.c_char_p, SZ]),
-    "dz_probe_rate": (I32, [P, ctypes.c_char_p, I32, ctypes.POINTER(ctypes.c_double)]),
     "dz_tune": (I32, [P, U32, ctypes.c_char_p, ctypes.c_char_p, SZ]),
     "dz_select_variant": (I32, [P, ctypes.c_char_p, ctypes.c_char_p]),
 }
@@ -257,6 +262,19 @@ class Context:
         buf = ctypes.create_string_buffer(1 << 16)
         self._check(load().dz_info(self.handle, buf, len(buf)))
         return json.loads(buf.value.decode())
+
+    def capture_id(self) -> int:
+        """dz_capture_id: the id of the capture the context stream records."""
+        out = ctypes.c_uint64()
+        self._check(load().dz_capture_id(self.handle, ctypes.byref(out)))
+        return out.value
+
+    def capture_release(self, capture_id: int):
+        """dz_capture_release: gives back what a destroyed graph's capture holds."""
+        self._check(load().dz_capture_release(self.handle, capture_id))
+
+    def capture_release_all(self):
+        self._check(load().dz_capture_release_all(self.handle))
 
     # ---- weights ----
     def upload(self, packed, layout: int, rows: int, cols: int) -> Weight:
@@ -382,12 +400,6 @@ class Context:
     def select_variant(self, family: str, name: str):
         self._check(load().dz_select_variant(self.handle, family.encode(), name.encode()))
 
-    def probe_rate(self, what: str, zero_operands: bool = False) -> float:
-        """dz_probe_rate: the sustained operations per second of one unit."""
-        out = ctypes.c_double()
-        self._check(load().dz_probe_rate(self.handle, what.encode(), int(zero_operands), ctypes.byref(out)))
-        return out.value
-
 
 class Encoder:
     """dz_encoder: the configuration-3 encoder with device-resident weights."""
@@ -482,6 +494,20 @@ class Pplx:
         m = None if markers is None else np.ascontiguousarray(markers, dtype=np.int32)
         self.ctx._check(load().dz_pplx_layer(self.ctx.handle, self.handle, index, _addr(hidden_dev), n,
                                              None if m is None else m.ctypes.data, 0 if m is None else m.size))
+
+    def layer_part(self, index: int, part: int, hidden_dev, n: int, markers=None):
+        """dz_pplx_layer_part: PPLX_MIXER or PPLX_MLP half of layer `index` in place."""
+        import numpy as np
+        m = None if markers is None else np.ascontiguousarray(markers, dtype=np.int32)
+        self.ctx._check(load().dz_pplx_layer_part(self.ctx.handle, self.handle, index, part, _addr(hidden_dev), n,
+                                                  None if m is None else m.ctypes.data, 0 if m is None else m.size))
+
+    def activation(self, name: str, out_dev):
+        """dz_pplx_activation: the last layer call's activation `name` into out_dev (a device tensor of
+        exactly its size)."""
+        nbytes = out_dev.numel() * out_dev.element_size()
+        self.ctx._check(load().dz_pplx_activation(self.ctx.handle, self.handle, name.encode(), _addr(out_dev),
+                                                  nbytes))
 
     def forward_rows(self, rows_host, n: int, markers):
         """Logits f32 [len(markers) x 255]."""

@@ -23,8 +23,9 @@
  *    and a non-finite flag of their own, which the recorded graph clears on
  *    every replay; run such a call once before capturing it (the workspace
  *    cannot grow under capture: DZ_INVALID_REQUEST), and replay the graph on
- *    the context stream or ordered with it, one replay at a time. A workspace
- *    that a graph refers to lives until dz_destroy. Entry points that wait
+ *    the context stream or ordered with it, one replay at a time. The slots
+ *    and workspaces a capture holds are given back by dz_capture_release
+ *    (below), else at dz_destroy. Entry points that wait
  *    for the stream, allocate, or read host memory return DZ_INVALID_REQUEST
  *    under capture before enqueueing anything: dz_sync, dz_alloc, dz_free,
  *    dz_copy_h2d, dz_copy_d2h, dz_set_stream, dz_weight_upload,
@@ -33,9 +34,9 @@
  *    dz_encoder_forward (it reads back the token-range flag),
  *    dz_encoder_forward_rows, dz_encoder_hidden_rows, dz_encoder_set_readout,
  *    dz_encoder_readout_rows, dz_pplx_create, dz_pplx_set_weight,
- *    dz_pplx_set_vector, dz_pplx_layer (it may grow the model's activation
- *    buffers), dz_pplx_forward_rows, dz_pplx_set_residency, dz_probe_rate and
- *    dz_tune.
+ *    dz_pplx_set_vector, dz_pplx_layer and dz_pplx_layer_part (they may grow
+ *    the model's activation buffers), dz_pplx_activation,
+ *    dz_pplx_forward_rows, dz_pplx_set_residency and dz_tune.
  */
 #ifndef DECISIVE_ROCM_H
 #define DECISIVE_ROCM_H
@@ -111,8 +112,30 @@ const char *dz_last_error(const dz_ctx *ctx);
  * current stream is capturing. */
 int32_t dz_set_stream(dz_ctx *ctx, void *hip_stream);
 int32_t dz_sync(dz_ctx *ctx);
-/* JSON description of the device and the selected kernel variants. */
+/* JSON description of the device, the selected kernel variants and the
+ * capture state: "capture_slots" {"held", "limit", "captures",
+ * "retired_workspaces"}. */
 int32_t dz_info(dz_ctx *ctx, char *buf, size_t cap);
+
+/* Capture bookkeeping (no reference counterpart: the reference records no
+ * graphs). Each product recorded under stream capture that quantizes its
+ * activations holds one of 4032 flag slots of the context, and a graph that
+ * recorded the context workspace keeps it alive when it grows. These calls give
+ * both back once the caller has destroyed every graph instantiated from a
+ * capture (or will not replay it again) and its replays have finished:
+ *  - dz_capture_id: while the context stream records, the id of that capture
+ *    (hipStreamGetCaptureInfo's); DZ_INVALID_REQUEST when it is not recording;
+ *  - dz_capture_release: gives back the slots and workspaces held by the
+ *    capture `id`; DZ_INVALID_REQUEST while that capture is still recording;
+ *    an id that holds nothing is accepted;
+ *  - dz_capture_release_all: gives back everything every capture holds;
+ *    DZ_INVALID_REQUEST while the context stream records.
+ * Without them, a context in which more than 4032 such products have been
+ * recorded fails further recordings with DZ_RESOURCE_LIMIT. Retired workspaces
+ * are freed after a wait for the context stream. */
+int32_t dz_capture_id(dz_ctx *ctx, uint64_t *id);
+int32_t dz_capture_release(dz_ctx *ctx, uint64_t id);
+int32_t dz_capture_release_all(dz_ctx *ctx);
 
 /* Device memory for callers without an allocator of their own. */
 int32_t dz_alloc(dz_ctx *ctx, size_t bytes, void **dev);
@@ -395,6 +418,44 @@ int32_t dz_pplx_set_vector(dz_ctx *ctx, dz_pplx *model, const char *name, const 
  * the marker rows, in marker order (prune_last). */
 int32_t dz_pplx_layer(dz_ctx *ctx, dz_pplx *model, int32_t layer, float *hidden_dev, size_t n,
                       const int32_t *markers_host, size_t count);
+/* Which part of a decoder layer dz_pplx_layer_part runs. */
+enum { DZ_PPLX_WHOLE = 0, DZ_PPLX_MIXER = 1, DZ_PPLX_MLP = 2 };
+/* dz_pplx_layer restricted to one half of the layer (backbone.rs:207-250,
+ * the two residual blocks): DZ_PPLX_MIXER runs the input norm, the mixer
+ * (gated delta rule or gated attention; markers as dz_pplx_layer takes them)
+ * and the output projection with its residual; DZ_PPLX_MLP the post norm and
+ * the MLP with its residual (markers_host must be NULL). Running the two
+ * halves in turn gives dz_pplx_layer's bits. */
+int32_t dz_pplx_layer_part(dz_ctx *ctx, dz_pplx *model, int32_t layer, int32_t part, float *hidden_dev,
+                           size_t n, const int32_t *markers_host, size_t count);
+/* Diagnostics for op-by-op parity checks (no reference counterpart: the
+ * reference's layer ops are Rust functions a test can call one by one).
+ * Copies an activation that the last dz_pplx_layer / dz_pplx_layer_part call
+ * left in the model's buffers into out_dev; `bytes` must be its size. n is
+ * that call's rows, nq its query rows (the markers' count when it pruned,
+ * else n), rows its output rows, d = hidden, W the gate's width (delta:
+ * delta_heads x 128, attention: attn_heads x 256).
+ *   any layer:  "hidden" f32 [rows x d]; "norm_codes" int8 [n x d] and
+ *               "norm_scales" f32 [n x d/64] (the last norm's A8 codes, when
+ *               it wrote codes: above 16 rows) or "normed" f32 [n x d];
+ *               "gate_codes" int8 [nq x W] and "gate_scales" f32 [nq x W/64]
+ *               (the mixer gate's A8 codes, when it wrote codes; a later MLP
+ *               half replaces them) or "gate" f32 [nq x W]; "mlp_codes" int8
+ *               [rows x ff] and "mlp_scales" f32 [rows x ff/64] (the fused
+ *               MLP's codes for down_proj)
+ *   delta:      "qkv" f32 [n x conv width], "z" f32 [n x delta_heads*128],
+ *               "a" and "b" f32 [n x delta_heads], "conv" f32 [n x conv
+ *               width] (after the causal conv and SiLU), "heads" f32
+ *               [delta_heads x n x 128] (the scan's output)
+ *   attention:  "q" f32 [nq x attn_heads*512] (q_proj: each head's query then
+ *               its gate), "query" f32 [nq x attn_heads*256] (after the head
+ *               norm and rotary), "key" f32 [n x attn_kv_heads*256] (after
+ *               the head norm and rotary), "value" f32 [n x attn_kv_heads*256],
+ *               "heads" f32 [attn_heads x nq x 256] (attention's output)
+ * DZ_INVALID_PARAMETERS for a name this layer kind does not have or a wrong
+ * size, DZ_INVALID_REQUEST when the last call did not produce it.
+ * Synchronous. */
+int32_t dz_pplx_activation(dz_ctx *ctx, dz_pplx *model, const char *name, void *out_dev, size_t bytes);
 /* native.rs:193-274 for one chunk: packed embedding rows (rows_host, n rows
  * of the group-64 wire layout), every layer (the last one cut to the
  * markers when it is an attention layer), the final zero-centred RMSNorm
@@ -432,32 +493,19 @@ int32_t dz_pplx_set_residency(dz_ctx *ctx, dz_pplx *model, int32_t residency);
  * and "max_in_flight_layers". DZ_RESOURCE_LIMIT when cap is too small. */
 int32_t dz_pplx_residency_info(dz_ctx *ctx, dz_pplx *model, char *json, size_t cap);
 
-/* ---- rate probes (diagnostics; no reference counterpart) ------------------------- */
-
-/* The sustained rate of one unit of this device, from a register-only loop
- * over every compute unit (eight waves per SIMD), as operations per second:
- *   "mfma_f16"  v_mfma_f32_16x16x32_f16 FLOP/s, successive instructions on
- *               different random operands (zero_operands 1: all-zero ones)
- *   "mfma_i8"   v_mfma_i32_32x32x32_i8 OP/s, the same way
- *   "fma_f32"   v_fma_f32 lane operations per second (zero_operands 0)
- *   "exp_f32"   v_exp_f32 lane operations per second (zero_operands 0)
- *   "lds_b128"  ds_read_b128 bytes per second read from LDS (zero_operands 0)
- * These are the ceilings the kernels' roofline fractions are read against
- * beside the published peaks. Synchronous; not recordable under capture. */
-int32_t dz_probe_rate(dz_ctx *ctx, const char *what, int32_t zero_operands, double *ops_per_second);
-
 /* ---- kernel tuner (webgpu/checkpoint.rs:95-294, 428-652) ------------------------ */
 
 /* Times the tile variants of every tuned kernel family within budget_ms and
  * keeps the fastest variant whose output is bitwise equal to the family's
- * reference variant and faster than 0.99x it. Families, in order: "grouped"
- * (the W4A8 product, checkpoint.rs:480-563 select_gemm at M,N,K = 256, 8192,
- * 2560), "mlp" (the fused MLP, :568-652 select_mlp at 128, 9216, 2560),
+ * reference variant and faster than 0.99x it. Families, in the reference's
+ * stage order (checkpoint.rs:251-262): "delta_scan" (:328-421
+ * select_delta_scan: 128 tokens of 32 value and 16 key heads; only the two
+ * token scans, which keep the rule's summation order, are candidates),
  * "norm" (:652-684 select_norm: 64 rows of 2560, the fused norm and codes
- * against the separate ones), then "gemv", "gemm_w4a16" and "i8_gemm" (no
- * reference counterpart). The delta
- * scan is not tuned: its scans are not bit-equal, which the reference's
- * select_delta_scan (:328-421) requires. cache_in (JSON from an earlier
+ * against the separate ones), "grouped" (the W4A8 product, :480-563
+ * select_gemm at M,N,K = 256, 8192, 2560), "mlp" (the fused MLP, :568-652
+ * select_mlp at 128, 9216, 2560), then "gemv", "gemm_w4a16" and "i8_gemm"
+ * (no reference counterpart). cache_in (JSON from an earlier
  * cache_out, or NULL; unreadable text is ignored) is reused while its key
  * still matches, re-checking equality only. The selection JSON is written to
  * cache_out (cap bytes). budget_ms == 0 keeps the reference variants. */
@@ -465,8 +513,12 @@ int32_t dz_tune(dz_ctx *ctx, uint32_t budget_ms, const char *cache_in, char *cac
                 size_t cap);
 /* Forces a variant of a family by name (tests and benchmarks). Families and
  * variants (the first of each is the default; every variant of a family
- * gives the same bits):
- *   "gemv"        w16, w8
+ * gives the same bits, except the delta scan's two opt-ins below):
+ *   "gemv"        auto, w16, w8, stream8, stream4 (w16/w8: 16 or 8 waves share
+ *                 one 16-row tile, each wave a fixed chunk of K; stream8/stream4:
+ *                 one wave per tile, 8 or 4 tiles per block, for K a multiple of
+ *                 2048 and up to 8 rows, else w16; "auto" takes w16, or stream4 /
+ *                 stream8 for 2..8 rows over eight or more tiles per compute unit)
  *   "gemm_w4a16"  pipe-auto, 256x256p2w8, 128x128p2w4, 128x256p2w8, 256x128w2x2,
  *                 128x128w2x2, 128x64w2x2, 256x256p2w8-persist, 256x192p2w8-persist,
  *                 256x128p2w8
@@ -478,12 +530,16 @@ int32_t dz_tune(dz_ctx *ctx, uint32_t budget_ms, const char *cache_in, char *cac
  *                 pipe128x128m8, pipe128x128n8, pipe32x128w8, pipe64x128w8
  *   "mlp"         pipe-auto, pipe256x64w8, pipe128x64w4, wave16x64, pipe256x64n2,
  *                 pipe128x64n2
- *   "delta_scan"  auto, recurrent, chunked64 (the decider's gated delta rule;
- *                 the two scans regroup its arithmetic differently, so they
- *                 agree to rounding, not bit for bit; "auto" runs the
- *                 recurrent scan below 384 tokens and the chunked one from
- *                 there, so a decider's bits depend on its chunk length
- *                 across that mark)
+ *   "delta_scan"  recurrent, recurrent-rolled, chunked64, auto (the
+ *                 decider's gated delta rule. The two token scans give the
+ *                 same bits: the default runs whole 16-token stages
+ *                 unrolled. The chunked scan regroups the arithmetic, so
+ *                 it agrees with them to rounding, not bit for bit; "auto"
+ *                 runs the token scan below 384 tokens and the chunked one
+ *                 from there, so a decider's bits then depend on its chunk
+ *                 length. chunked64 and auto are explicit opt-ins that the
+ *                 tuner never selects, and the only variants anywhere that
+ *                 do not give their family's reference bits)
  *   "norm"        fused, separate (the decider's layer norms above 16 rows:
  *                 one kernel for the RMSNorm and the A8 codes its products
  *                 share, or the norm then one quantization per product; the

@@ -21,6 +21,20 @@
 #include <immintrin.h>
 #endif
 
+/* Runs `fn(job)` on up to `threads` threads that take their work from a shared
+ * counter in `job`: joins exactly the threads that started, and runs the
+ * worker on the calling thread when none could start, so every unit of work is
+ * done whatever pthread_create returns. */
+static void run_workers(void *(*fn)(void *), void *job, int threads) {
+    pthread_t *ids = threads > 0 ? (pthread_t *)malloc(sizeof(pthread_t) * (size_t)threads) : NULL;
+    int started = 0;
+    for (int t = 0; ids && t < threads; t++)
+        if (pthread_create(&ids[started], NULL, fn, job) == 0) started++;
+    if (started == 0) fn(job);
+    for (int t = 0; t < started; t++) pthread_join(ids[t], NULL);
+    free(ids);
+}
+
 /* ------------------------------------------------------------------------ */
 /* IEEE conversions (half 2.7.1: bf16::from_f32 / f16::from_f32 round to    */
 /* nearest even; widening is exact).                                        */
@@ -478,10 +492,7 @@ int or_panel_apply_avx2(const uint8_t *data, const float *pscales, size_t n, siz
         panel_worker(&job);
         return 0;
     }
-    pthread_t *ids = (pthread_t *)malloc(sizeof(pthread_t) * (size_t)threads);
-    for (int t = 0; t < threads; t++) pthread_create(&ids[t], NULL, panel_worker, &job);
-    for (int t = 0; t < threads; t++) pthread_join(ids[t], NULL);
-    free(ids);
+    run_workers(panel_worker, &job, threads);
     return 0;
 #else
     (void)data; (void)pscales; (void)n; (void)k; (void)bits; (void)qx; (void)sx; (void)m;
@@ -603,10 +614,7 @@ void or_i8_gemm(const int8_t *qa, const float *sa, size_t m, const int8_t *qw, c
         i8_worker(&job);
         return;
     }
-    pthread_t *ids = (pthread_t *)malloc(sizeof(pthread_t) * (size_t)threads);
-    for (int t = 0; t < threads; t++) pthread_create(&ids[t], NULL, i8_worker, &job);
-    for (int t = 0; t < threads; t++) pthread_join(ids[t], NULL);
-    free(ids);
+    run_workers(i8_worker, &job, threads);
 }
 
 /* webgpu/int8.rs:226-230, gemm(fused=true): gate and up are two rescaled
@@ -912,9 +920,7 @@ void or_attention_gqa(const float *q, const float *k, const float *v, size_t nq,
     long cpus = sysconf(_SC_NPROCESSORS_ONLN);
     int threads = cpus < 1 ? 1 : (cpus > 16 ? 16 : (int)cpus);
     if (threads > ah) threads = ah;
-    pthread_t ids[16];
-    for (int t = 0; t < threads; t++) pthread_create(&ids[t], NULL, gqa_worker, &job);
-    for (int t = 0; t < threads; t++) pthread_join(ids[t], NULL);
+    run_workers(gqa_worker, &job, threads);
 }
 
 void or_attention_gate(const float *heads, size_t n, int ah, int ad, const float *z, float *out) {

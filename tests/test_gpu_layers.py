@@ -308,13 +308,14 @@ def test_config3_encoder_full_size_runs_finite_and_deterministic(ctx):
     enc.close()
 
 
-TUNED = ("grouped", "mlp", "norm", "gemv", "gemm_w4a16", "i8_gemm")
+TUNED = ("delta_scan", "norm", "grouped", "mlp", "gemv", "gemm_w4a16", "i8_gemm")
 
 
 def test_tuner_selects_bitwise_equal_variants_and_caches(ctx):
-    """checkpoint.rs:428-652 under a budget that covers every family: the
-    reference's grouped W4A8 (256, 8192, 2560) and fused MLP (128, 9216, 2560)
-    families and this library's three are timed; a selected variant other
+    """checkpoint.rs:251-262 and :328-652 under a budget that covers every
+    family: the reference's delta scan (128 tokens), norm, grouped W4A8 (256,
+    8192, 2560) and fused MLP (128, 9216, 2560) stages, in its order, and this
+    library's three are timed; a selected variant other
     than the reference is at least 1% faster and bitwise equal to it; a cached
     selection is reused (equality re-checked only); a zero budget keeps the
     reference variants."""
@@ -341,6 +342,10 @@ def _tuner_checks(ctx):
         for v, a in enumerate(f["agrees"]):
             assert a in (True, False, None)
     assert fams["grouped"]["shape"] == [256, 8192, 2560] and fams["mlp"]["shape"] == [128, 9216, 2560]
+    # the delta scan's candidates are the token scans only (select_delta_scan, checkpoint.rs:328-421)
+    assert fams["delta_scan"]["candidates"] == ["recurrent", "recurrent-rolled"]
+    assert fams["delta_scan"]["shape"] == [128, 32, 16]
+    assert list(sel["selected"]) == list(TUNED)
     assert fams["norm"]["shape"][0] == 64 and fams["norm"]["shape"][2] == 2560
     again = ctx.tune(5000, cache=__import__("json").dumps(sel))
     assert again["key"] == sel["key"]
@@ -398,5 +403,5 @@ def test_tuned_grouped_and_mlp_variants_agree_on_real_inputs(ctx, oracle):
 
 
 def rocm_reference(fam):
-    return {"gemv": "w16", "gemm_w4a16": "pipe-auto", "i8_gemm": "256x256p2w8", "grouped": "pipe-auto",
-            "mlp": "pipe-auto", "norm": "fused"}[fam]
+    return {"gemv": "auto", "gemm_w4a16": "pipe-auto", "i8_gemm": "256x256p2w8", "grouped": "pipe-auto",
+            "mlp": "pipe-auto", "norm": "fused", "delta_scan": "recurrent"}[fam]

@@ -13,7 +13,7 @@ import pytest
 
 from decisive_amd import rocm
 from tests import pplx_model
-from tests.gpu_util import cosine, dev, empty, host
+from tests.gpu_util import bits_equal, cosine, dev, empty, host
 
 pytestmark = pytest.mark.gpu
 
@@ -75,14 +75,15 @@ def test_forward_logits_match_the_reference_chunk(ctx, oracle, small, n):
     assert close(got, want, rel=1e-2), (float(cosine(got, want)), float(np.abs(got - want).max()))
 
 
-@pytest.mark.parametrize("scan", ["recurrent", "chunked64"])
+@pytest.mark.parametrize("scan", ["recurrent", "recurrent-rolled", "chunked64"])
 @pytest.mark.parametrize("n", [1, 37, 64, 130, 257])
 def test_delta_layer_matches_the_reference_for_both_scans(ctx, oracle, small, scan, n):
-    """The token-by-token scan and the chunked one (64-token chunks: one
-    partial chunk, exact chunks, a ragged tail) against the oracle's
-    sequential rule. Both regroup the rule's arithmetic, so an ulp now and
-    then flips one A8 code of out_proj's input; the bound is a cosine of
-    0.99999 with max-abs within 1% (a wrong scan lands far below 0.9999)."""
+    """The token-by-token scan (its unrolled and rolled forms) and the
+    chunked one (64-token chunks: one partial chunk, exact chunks, a ragged
+    tail) against the oracle's sequential rule. Both regroup the rule's
+    arithmetic, so an ulp now and then flips one A8 code of out_proj's input;
+    the bound is a cosine of 0.99999 with max-abs within 1% (a wrong scan
+    lands far below 0.9999)."""
     torch = pytest.importorskip("torch")
     model, p = small
     h = np.random.default_rng(100 + n).standard_normal((n, SMALL["hidden"])).astype(np.float32)
@@ -91,11 +92,35 @@ def test_delta_layer_matches_the_reference_for_both_scans(ctx, oracle, small, sc
     try:
         p.layer(1, hd, n)
     finally:
-        ctx.select_variant("delta_scan", "auto")
+        ctx.select_variant("delta_scan", "recurrent")
     got = host(ctx, hd)
     want = pplx_model.ref_layer(oracle, model, 1, h)
     assert cosine(got, want) >= 0.99999 and close(got, want, rel=1e-2), (float(cosine(got, want)),
                                                                          float(np.abs(got - want).max()))
+
+
+@pytest.mark.parametrize("n", [1, 16, 17, 130, 400])
+def test_recurrent_scan_forms_are_bitwise_equal(ctx, oracle, small, n):
+    """The unrolled token scan (whole 16-token stages) and the rolled one run
+    the same arithmetic in the same order: a delta layer gives the same
+    bits with either, at lengths inside one 16-token stage, across stages and
+    past the 384 tokens where "auto" switches to the chunked scan; "auto" equals
+    the token scan below 384 tokens."""
+    torch = pytest.importorskip("torch")
+    model, p = small
+    h = np.random.default_rng(300 + n).standard_normal((n, SMALL["hidden"])).astype(np.float32)
+    got = {}
+    try:
+        for scan in ("recurrent", "recurrent-rolled", "auto"):
+            ctx.select_variant("delta_scan", scan)
+            hd = dev(h)
+            p.layer(1, hd, n)
+            got[scan] = host(ctx, hd).copy()
+    finally:
+        ctx.select_variant("delta_scan", "recurrent")
+    assert bits_equal(got["recurrent"], got["recurrent-rolled"])
+    if n < 384:
+        assert bits_equal(got["auto"], got["recurrent"])
 
 
 # four query heads per key/value head, as the reference model has

@@ -75,7 +75,7 @@ def test_real_delta_layer_matches_the_reference_layer(ctx, oracle, real, scan):
     try:
         p.layer(0, hd, N)
     finally:
-        ctx.select_variant("delta_scan", "auto")
+        ctx.select_variant("delta_scan", "recurrent")
     got = host(ctx, hd)
     if "delta" not in wants:
         wants["delta"] = one_ulp_sensitivity(oracle, model, 0, h, None)

@@ -304,12 +304,12 @@ def test_config2_gemv_vs_closed_form(ctx, oracle, m):
     assert np.abs(got - want).max() <= MAX_ABS
     assert cosine(got, want) >= MIN_COS
     # every GEMV variant keeps the reduction order: bitwise equal outputs
-    for name in ("w16", "w8"):
+    for name in ("auto", "w16", "w8", "stream8", "stream4"):
         ctx.select_variant("gemv", name)
         y2 = empty((m, n), torch.float32)
         ctx.linear(w, dev(xh.view(np.float16)), rocm.F16, m, y2, rocm.W4A16)
         assert bits_equal(host(ctx, y2), got), name
-    ctx.select_variant("gemv", "w16")
+    ctx.select_variant("gemv", "auto")
 
 
 @pytest.mark.parametrize("k,n", [(96, 17), (2560, 300), (4160, 33), (8, 1)])
@@ -340,6 +340,40 @@ def test_gemv_ragged_rows_are_independent_of_m(ctx, oracle, k, n):
         ctx.linear(w, xd, rocm.F16, m, y, rocm.W4A16)
         got = host(ctx, y)
         assert bits_equal(got, alone[:m]), m
+
+
+@pytest.mark.parametrize("k,n", [(2048, 1000), (6144, 4099), (4160, 300)])
+def test_gemv_stream_variants_equal_the_split_kernel(ctx, oracle, k, n):
+    """The streaming GEMV (one wave per 16-row tile, K a multiple of 2048) keeps
+    the split kernel's chunk order: for every row count 1..8 and ragged N its
+    outputs equal the default kernel's bit for bit and the closed form within
+    tolerance. At K = 4160 it does not apply and the split kernel runs."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(k + n)
+    x = rng.standard_normal((8, k)).astype(np.float32)
+    wf = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    w = ctx.quantize(dev(wf), rocm.F32, n, k, 4, 32)
+    deq = empty((n, k), torch.float32)
+    ctx.dequant(w, deq)
+    deq = host(ctx, deq)
+    xh = oracle.f32_to_f16_bits(x)
+    xd = dev(xh.view(np.float16))
+    want = oracle.w4a16(xh, 8, k, deq, n)
+    try:
+        for m in range(1, 9):
+            ctx.select_variant("gemv", "w16")
+            y = empty((m, n), torch.float32)
+            ctx.linear(w, xd, rocm.F16, m, y, rocm.W4A16)
+            base = host(ctx, y).copy()
+            assert np.abs(base - want[:m]).max() <= MAX_ABS
+            for name in ("stream8", "stream4", "auto"):
+                ctx.select_variant("gemv", name)
+                y.fill_(7.0)
+                ctx.linear(w, xd, rocm.F16, m, y, rocm.W4A16)
+                assert bits_equal(host(ctx, y), base), (name, m)
+    finally:
+        ctx.select_variant("gemv", "auto")
+    w.free()
 
 
 def test_w4a16_rejects_misaligned_activations(ctx, oracle):

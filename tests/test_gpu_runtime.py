@@ -204,18 +204,124 @@ def test_stream_change_waits_for_products_on_the_old_stream(ctx, oracle):
     w.free()
 
 
-def test_rate_probes_report_rates_and_reject_unknown_kinds(ctx):
-    """dz_probe_rate: positive rates for every kind; all-zero MFMA operands are
-    not slower than random ones beyond noise; unknown kinds and zero operands
-    on the VALU kinds are INVALID_PARAMETERS."""
-    rates = {w: ctx.probe_rate(w) for w in ("mfma_f16", "mfma_i8", "fma_f32", "exp_f32", "lds_b128")}
-    assert all(r > 0 for r in rates.values()), rates
-    # a transcendental costs more than a fused multiply-add
-    assert rates["exp_f32"] < rates["fma_f32"]
-    # LDS reads: at least 32 bytes per clock per compute unit at a 1 GHz clock, at most 1 KB at 3 GHz
-    cus = ctx.info()["compute_units"]
-    assert cus * 32 * 1e9 < rates["lds_b128"] < cus * 1024 * 3e9, rates["lds_b128"]
-    for what, zero in (("mfma_f64", False), ("fma_f32", True), ("lds_b128", True)):
-        with pytest.raises(rocm.DzError) as e:
-            ctx.probe_rate(what, zero)
-        assert e.value.code == "INVALID_PARAMETERS"
+def test_capture_release_gives_flag_slots_back(fresh, oracle):
+    """45 graphs of 100 recorded W4A8 products at M=40 (4,500 recordings, more
+    than the 4,032 flag slots), each destroyed and released before the next:
+    every recording succeeds and every replay keeps the eager bits, NaN replays
+    stay NaN on reused slots, and the context reports no held slot at the end.
+    Two graphs kept at once are given back by dz_capture_release_all. The
+    current capture cannot be released while it records, and dz_capture_id
+    outside a capture is INVALID_REQUEST."""
+    torch = pytest.importorskip("torch")
+    m, n, k = 40, 64, 256
+    w = _weight(fresh, n, k, 71)
+    rng = np.random.default_rng(72)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    bad = x.copy()
+    bad[5, 9] = np.nan
+    want = _eager(torch, fresh, w, x, m, n)
+    with pytest.raises(rocm.DzError) as e:
+        fresh.capture_id()
+    assert e.value.code == "INVALID_REQUEST"
+    stream = torch.cuda.Stream()
+    fresh.set_stream(stream.cuda_stream)
+    try:
+        with torch.cuda.stream(stream):
+            xin, y = torch.from_numpy(x).cuda(), torch.empty((m, n), device="cuda")
+            fresh.linear(w, xin, rocm.F32, m, y, rocm.W4A8)  # sizes the workspace
+            torch.cuda.synchronize()
+            for rep in range(45):
+                graph = torch.cuda.CUDAGraph()
+                with rocm.capture(graph, stream):
+                    cid = fresh.capture_id()
+                    for _ in range(100):
+                        fresh.linear(w, xin, rocm.F32, m, y, rocm.W4A8)
+                    if rep == 0:
+                        for call in (lambda: fresh.capture_release(cid), fresh.capture_release_all):
+                            with pytest.raises(rocm.DzError) as e:
+                                call()
+                            assert e.value.code == "INVALID_REQUEST"
+                slots = fresh.info()["capture_slots"]
+                assert slots["held"] == 100 and slots["captures"] == 1, (rep, slots)
+                for src in ([bad, x] if rep % 10 == 9 else [x]):
+                    xin.copy_(torch.from_numpy(src))
+                    y.fill_(2.0)
+                    graph.replay()
+                    got = host(fresh, y)
+                    if src is bad:
+                        assert np.isnan(got).all(), rep
+                    else:
+                        assert bits_equal(got, want), rep
+                torch.cuda.synchronize()
+                graph.reset()
+                fresh.capture_release(cid)
+                assert fresh.info()["capture_slots"]["held"] == 0, rep
+            graphs = []
+            for _ in range(2):
+                graph = torch.cuda.CUDAGraph()
+                with rocm.capture(graph, stream):
+                    for _ in range(100):
+                        fresh.linear(w, xin, rocm.F32, m, y, rocm.W4A8)
+                graphs.append(graph)
+            slots = fresh.info()["capture_slots"]
+            assert slots["held"] == 200 and slots["captures"] == 2, slots
+            for graph in graphs:
+                y.fill_(2.0)
+                graph.replay()
+                assert bits_equal(host(fresh, y), want)
+            torch.cuda.synchronize()
+            for graph in graphs:
+                graph.reset()
+            fresh.capture_release_all()
+            assert fresh.info()["capture_slots"]["held"] == 0
+            assert fresh.info()["capture_slots"]["captures"] == 0
+    finally:
+        fresh.set_stream(None)
+    w.free()
+
+
+def test_capture_release_frees_the_retired_workspace(fresh, oracle):
+    """A graph recorded at M=40 keeps its workspace alive when an eager call
+    grows the context workspace (one retired workspace); once the graph is
+    destroyed and its capture released, the retired workspace is freed, and a
+    new recording on the grown workspace keeps the eager bits."""
+    torch = pytest.importorskip("torch")
+    m, n, k = 40, 128, 256
+    w = _weight(fresh, n, k, 81)
+    x = np.random.default_rng(82).standard_normal((m, k)).astype(np.float32)
+    want = _eager(torch, fresh, w, x, m, n)
+    stream = torch.cuda.Stream()
+    fresh.set_stream(stream.cuda_stream)
+    try:
+        with torch.cuda.stream(stream):
+            xin, y = torch.from_numpy(x).cuda(), torch.empty((m, n), device="cuda")
+            fresh.linear(w, xin, rocm.F32, m, y, rocm.W4A8)
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with rocm.capture(graph, stream):
+                cid = fresh.capture_id()
+                fresh.linear(w, xin, rocm.F32, m, y, rocm.W4A8)
+            big_m, big_k = 2048, 1024
+            wb = _weight(fresh, 64, big_k, 83)
+            xb = torch.randn((big_m, big_k), device="cuda")
+            yb = torch.empty((big_m, 64), device="cuda")
+            fresh.linear(wb, xb, rocm.F32, big_m, yb, rocm.W4A8)
+            assert fresh.info()["capture_slots"]["retired_workspaces"] == 1
+            y.fill_(-1.0)
+            graph.replay()
+            assert bits_equal(host(fresh, y), want)
+            torch.cuda.synchronize()
+            graph.reset()
+            fresh.capture_release(cid)
+            assert fresh.info()["capture_slots"]["retired_workspaces"] == 0
+            graph = torch.cuda.CUDAGraph()
+            with rocm.capture(graph, stream):
+                fresh.linear(w, xin, rocm.F32, m, y, rocm.W4A8)
+            for _ in range(2):
+                y.fill_(-1.0)
+                graph.replay()
+                assert bits_equal(host(fresh, y), want)
+            wb.free()
+    finally:
+        fresh.set_stream(None)
+    w.free()
