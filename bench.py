@@ -21,7 +21,7 @@ int8 GEMM, the Q4 prefill GEMM and the encoder forward) are reported under
                     [--no-graph] [--calibrate-copy] [--tune MS]
     python bench.py --only pplx                      (the decider line alone)
     python bench.py --only encoder / floors / gemv (the encoder line; launch floors
-                     at the GEMV's size; the GEMV at N = 16384 and 65536)
+                     at the GEMV's size; the GEMV at N = 16384 to 131072)
     python bench.py --only tune [--tune MS] [--tune-cache F] [--tune-out F]
                     (the tuner's selection, then each family's reference and
                      selected variants at the tuning shape, for rocprofv3)
@@ -265,11 +265,12 @@ def gemv_lines(torch, ctx, rocm, weights, stream) -> dict:
 
 def wide_gemv_lines(torch, ctx, rocm, stream) -> dict:
     """The W4A16 GEMV's streaming rate where a launch's fixed cost is small:
-    K = 4096 at N = 16384 and 65536 (37.7 and 151 MB per launch), M = 1, 4 and
-    8, over rotating copies of about 906 MB (24 and 6 copies), each a HIP
-    graph of one launch per copy; the library's default variant ("auto")."""
+    K = 4096 at N = 16384, 65536 and 131072 (37.7, 151 and 302 MB per launch),
+    M = 1, 4 and 8, over rotating copies of about 906 MB (24, 6 and 3 copies),
+    each a HIP graph of one launch per copy; the library's default variant
+    ("auto")."""
     out = {}
-    for n, copies in ((16384, 24), (65536, 6)):
+    for n, copies in ((16384, 24), (65536, 6), (131072, 3)):
         tmp = torch.empty((n, K_DIM), dtype=torch.float32, device="cuda")
         ws = []
         for c in range(copies):
@@ -532,7 +533,7 @@ def pplx_line(torch, ctx, rocm, stream, n: int = 1024, layers: int = 32) -> dict
 
 TUNE_SHAPES = {"grouped": (256, 8192, 2560), "mlp": (128, 9216, 2560), "gemv": (1, 8192, 2560),
                "gemm_w4a16": (256, 8192, 2560), "i8_gemm": (256, 8192, 2560)}
-TUNE_REFERENCE = {"grouped": "pipe-auto", "mlp": "pipe-auto", "gemv": "w16", "gemm_w4a16": "pipe-auto",
+TUNE_REFERENCE = {"grouped": "pipe-auto", "mlp": "pipe-auto", "gemv": "auto", "gemm_w4a16": "pipe-auto",
                   "i8_gemm": "256x256p2w8"}
 
 
@@ -662,6 +663,20 @@ def floors_line(torch, ctx, rocm, stream) -> dict:
     del mats
     out["vendor_f16_gemv_same_bytes"]["what"] = f"torch.mv, f16 [{vrows} x {K_DIM}] matrix times an f16 vector"
     out["bytes_per_launch"] = per_launch
+    del bufs, halves, y
+    torch.cuda.empty_cache()
+    # the HBM rates plain framework kernels reach where a launch's fixed cost is
+    # negligible: a 1 GiB device copy (read + write) and a 1 GiB f32 sum (read)
+    big = torch.empty(1 << 28, dtype=torch.float32, device="cuda").normal_()
+    dst = torch.empty_like(big)
+    torch.cuda.synchronize()
+    warm(torch, lambda r: dst.copy_(big))
+    ms = timed_ms(torch, torch.cuda.current_stream(), lambda r: dst.copy_(big), 10)
+    out["copy_1GiB"] = {"TB/s_read_plus_write": round((2 << 30) / (ms * 1e-3) / 1e12, 3), "what": "torch copy_"}
+    warm(torch, lambda r: big.sum())
+    ms = timed_ms(torch, torch.cuda.current_stream(), lambda r: big.sum(), 10)
+    out["sum_1GiB"] = {"TB/s_read": round((1 << 30) / (ms * 1e-3) / 1e12, 3), "what": "torch sum over f32"}
+    del big, dst
     return out
 
 
