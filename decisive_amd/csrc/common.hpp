@@ -52,6 +52,12 @@ struct Weight {
     uint8_t *codes = nullptr;     // device
     uint8_t *scales = nullptr;    // device
     size_t code_bytes = 0, scale_bytes = 0;
+    // Fitted Q4 (quantization.rs): `fitted` for any fitted form; `offsets`,
+    // for the affine form, an f32 offset per (row, 64-group) laid out as the
+    // group-64 scales ([tile][k-block][16 rows][2 f32], scale_bytes long);
+    // `nf4` when the codes index the NF4 codebook.
+    uint8_t *offsets = nullptr;
+    bool fitted = false, nf4 = false;
     int tiles() const { return np / 16; }
     int kblocks() const { return bits == 4 ? kp / 128 : kp / 64; }
 };

@@ -7,8 +7,8 @@ namespace dz {
 
 // ---- quant.hip ----------------------------------------------------------------
 // Wire layout -> native layout; sets *bad (device int) when a scale is not
-// finite and positive.
-void launch_upload(const Weight &w, const uint8_t *wire, int *bad, hipStream_t s);
+// finite and positive (fitted: not finite and nonzero).
+void launch_upload(const Weight &w, const uint8_t *wire, int *bad, hipStream_t s, bool fitted = false);
 // Device quantizer from f32/f16/bf16 values (dtype 0/1/2); sets *bad on a
 // non-finite weight.
 void launch_quantize_weight(const Weight &w, const void *values, int dtype, int *bad,
@@ -24,6 +24,9 @@ void launch_export_q4g64(const Weight &w, uint8_t *wire, hipStream_t s);
 // int8.rs:178-202 prepare: q [m x G*64], s [m x G]; sets *bad on non-finite x.
 void launch_act_quantize(const float *x, int m, int k, int bits, int8_t *q, float *sc, int *bad,
                          hipStream_t s);
+// sxq [m x groups] = sx * f32(sum of each group's 64 codes): the affine offset
+// term's activation factor (int8.rs:568-569).
+void launch_act_sums(const int8_t *q, const float *sx, int m, int groups, float *sxq, hipStream_t s);
 // grouped_q4.rs:3-25: the same codes and scales as 17-word records per group.
 void launch_act_quantize_records(const float *x, int m, int k, uint32_t *records, int *bad,
                                  hipStream_t s);
@@ -48,8 +51,10 @@ void launch_fill_i32(int *p, int value, int count, hipStream_t s);
 // only for the cases grouped_adds_residual accepts. Returns false when no
 // kernel was launched (a residual product that no pipelined kernel takes).
 bool grouped_adds_residual(const Weight &w, int m, int variant);
+// Fitted affine weights (w.offsets) take sxq [m x groups] (launch_act_sums).
 bool launch_grouped(const Weight &w, const int8_t *q, const float *sx, int m, float *y,
-                    const int *bad, int variant, hipStream_t s, const float *res = nullptr);
+                    const int *bad, int variant, hipStream_t s, const float *res = nullptr,
+                    const float *sxq = nullptr);
 // Few-row grouped products (any m; one launch, 16 rows per block row):
 //  from f32 x quantized in the kernel (m <= 16 keeps the all-NaN semantics of
 //  a non-finite x; bad_out, may be null, is set when x holds one);

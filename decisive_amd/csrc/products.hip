@@ -34,13 +34,17 @@ __device__ __forceinline__ size_t q4_lane(int t, int kb, int kbs, int q, int j) 
 // ============================================================================
 
 // One wave per 16x16 output tile; a block of 4 waves covers 64 columns.
-template <int BITS>
+// AFF (fitted affine Q4, int8.rs:566-571): after each group's fold,
+// acc = fma(offset[c][g], sxq[r][g], acc), sxq = sx * f32(sum of the codes).
+template <int BITS, bool AFF = false>
 __global__ __launch_bounds__(256) void grouped_kernel(const uint8_t *__restrict__ codes,
                                                       const uint8_t *__restrict__ scales,
                                                       const int8_t *__restrict__ q,
                                                       const float *__restrict__ sx, int m, int n,
                                                       int groups, int kbs, float *__restrict__ y,
-                                                      const int *__restrict__ bad) {
+                                                      const int *__restrict__ bad,
+                                                      const uint8_t *__restrict__ offsets = nullptr,
+                                                      const float *__restrict__ sxq = nullptr) {
     const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
     const int t = blockIdx.x * 4 + wave;
     const int mt = blockIdx.y;
@@ -59,6 +63,7 @@ __global__ __launch_bounds__(256) void grouped_kernel(const uint8_t *__restrict_
     struct Batch {
         int4_t a[B], b[B];
         float sw[B], sx[B][4];
+        float ofs[AFF ? B : 1], sq[AFF ? B : 1][4];
     };
     auto fetch = [&](Batch &bt, int g0) {
 #pragma unroll
@@ -90,6 +95,14 @@ __global__ __launch_bounds__(256) void grouped_kernel(const uint8_t *__restrict_
                 const int r = mt * 16 + qd * 4 + v;
                 bt.sx[u][v] = r < m ? sx[(size_t)r * groups + g] : 0.0f;
             }
+            if (AFF) {  // Q4 only: offsets share the group-64 scale layout
+                bt.ofs[u] = ((const float *)(offsets + (((size_t)t * kbs + (g >> 1)) * 16 + j) * 8))[g & 1];
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const int r = mt * 16 + qd * 4 + v;
+                    bt.sq[u][v] = r < m ? sxq[(size_t)r * groups + g] : 0.0f;
+                }
+            }
         }
     };
     auto fold = [&](const Batch &bt, int g0) {
@@ -98,7 +111,10 @@ __global__ __launch_bounds__(256) void grouped_kernel(const uint8_t *__restrict_
             if (g0 + u >= groups) break;
             const int4_t d = mfma_i8(bt.a[u], bt.b[u], zero);
 #pragma unroll
-            for (int v = 0; v < 4; v++) acc[v] = __builtin_fmaf((float)d[v], __fmul_rn(bt.sw[u], bt.sx[u][v]), acc[v]);
+            for (int v = 0; v < 4; v++) {
+                acc[v] = __builtin_fmaf((float)d[v], __fmul_rn(bt.sw[u], bt.sx[u][v]), acc[v]);
+                if (AFF) acc[v] = __builtin_fmaf(bt.ofs[AFF ? u : 0], bt.sq[AFF ? u : 0][v], acc[v]);
+            }
         }
     };
     if (!nan_out) {
@@ -142,7 +158,7 @@ constexpr int kGvWaves = 16;
 constexpr int kGvSub = 4;
 constexpr int kGvWindow = kGvWaves * kGvSub;
 
-template <int MPAD>
+template <int MPAD, bool AFF = false>
 struct GvShape {
     static constexpr int ASTRIDE = kGvSub * 64 + 16;           // staged codes per row (+ pad)
     static constexpr int ACODE = MPAD * ASTRIDE;                // per wave
@@ -150,20 +166,28 @@ struct GvShape {
     static constexpr int ASX = MPAD * kGvWindow * 4;            // activation scales of a window
     static constexpr int SW = kGvWindow * 16 * 4;               // weight scales of a window
     static constexpr int DOTS = kGvWindow * MPAD * 16 * 4;      // int32 group dots of a window
-    static constexpr int BYTES = ACODE_ALL + ASX + SW + DOTS + 16;
+    static constexpr int AFFB = AFF ? ASX + SW : 0;             // sx * sum q and the offsets of a window
+    static constexpr int BYTES = ACODE_ALL + ASX + SW + DOTS + 16 + AFFB;
 };
 
-template <int BITS, int MPAD, int AMODE, bool PROJECT>
+// AFF (fitted affine Q4 weights, AMODE 0): each group's fold is followed by
+// acc = fma(offset, sx * f32(sum of the row's group codes), acc), the term
+// int8.rs:566-571 adds; the code sums come from the quantization here.
+template <int BITS, int MPAD, int AMODE, bool PROJECT, bool AFF = false>
 __global__ __launch_bounds__(kGvWaves * 64) void grouped_gemv_kernel(
     const uint8_t *__restrict__ codes, const uint8_t *__restrict__ scales, const void *__restrict__ a,
     const float *__restrict__ sa, int m, int k, int n, int groups, int kbs, int abits,
-    float *__restrict__ y, const int *__restrict__ bad_in, int *__restrict__ bad_out) {
-    using S = GvShape<MPAD>;
+    float *__restrict__ y, const int *__restrict__ bad_in, int *__restrict__ bad_out,
+    const uint8_t *__restrict__ offsets = nullptr) {
+    static_assert(!AFF || (AMODE == 0 && !PROJECT && BITS == 4), "affine offsets: Q4 weights, f32 activations");
+    using S = GvShape<MPAD, AFF>;
     extern __shared__ __align__(16) uint8_t lds[];
     float *asx = (float *)(lds + S::ACODE_ALL);
     float *sw = (float *)(lds + S::ACODE_ALL + S::ASX);
     int32_t *dots = (int32_t *)(lds + S::ACODE_ALL + S::ASX + S::SW);
     int *flag = (int *)(lds + S::ACODE_ALL + S::ASX + S::SW + S::DOTS);
+    float *asq = (float *)(lds + S::ACODE_ALL + S::ASX + S::SW + S::DOTS + 16);  // AFF only
+    float *ofs = asq + MPAD * kGvWindow;                                         // AFF only
     const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
     const int t = blockIdx.x, row0 = blockIdx.y * 16;
     const int qd = lane / 16, i = lane % 16, j = i;
@@ -187,10 +211,11 @@ __global__ __launch_bounds__(kGvWaves * 64) void grouped_gemv_kernel(
             bq[u] = *(const uint4_t *)(codes + q4_lane(t, blk, kbs, qd, j));
         }
         // ---- weight scales of the wave's groups: 256 contiguous bytes, 16 lanes x 16 B
-        uint4_t swv = {0u, 0u, 0u, 0u};
+        uint4_t swv = {0u, 0u, 0u, 0u}, ofv = {0u, 0u, 0u, 0u};
         const int first_blk = BITS == 4 ? g0 / 2 : g0;
         const int blk_of_lane = BITS == 4 ? first_blk + lane / 8 : first_blk + lane / 4;
         if (lane < 16 && blk_of_lane < kbs) swv = *(const uint4_t *)(scales + ((size_t)t * kbs + first_blk) * (BITS == 4 ? 128 : 64) + lane * 16);
+        if (AFF && lane < 16 && blk_of_lane < kbs) ofv = *(const uint4_t *)(offsets + ((size_t)t * kbs + first_blk) * 128 + lane * 16);
         // ---- activation codes and scales
         if (AMODE == 0) {
             const float *x = (const float *)a;
@@ -223,13 +248,19 @@ __global__ __launch_bounds__(kGvWaves * 64) void grouped_gemv_kernel(
                 const float scale = fmaxf(__fdiv_rn(maximum, limit), FLT_MIN);
                 const float inverse = __frcp_rn(scale);
                 uint32_t word = 0;
+                int qsum = 0;
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     float q = fminf(fmaxf(__builtin_rintf(__fmul_rn(xv[r][e], inverse)), -limit), limit);
                     word |= ((uint32_t)(uint8_t)(int8_t)(int)q) << (8 * e);
+                    qsum += (int)q;
                 }
                 *(uint32_t *)(acode + r * S::ASTRIDE + (lane / 16) * 64 + (lane % 16) * 4) = word;
                 if (lane % 16 == 0) asx[r * kGvWindow + (g0 - w0) + lane / 16] = scale;
+                if (AFF) {
+                    for (int off = 8; off > 0; off >>= 1) qsum += __shfl_xor(qsum, off, 16);
+                    if (lane % 16 == 0) asq[r * kGvWindow + (g0 - w0) + lane / 16] = __fmul_rn(scale, (float)qsum);
+                }
             }
         } else if (AMODE == 1) {
             const int8_t *q = (const int8_t *)a;
@@ -271,6 +302,10 @@ __global__ __launch_bounds__(kGvWaves * 64) void grouped_gemv_kernel(
                     const int gl = g0 - w0 + (lane / 8) * 2;
                     sw[gl * 16 + col] = word_as_float(swv[h * 2]);
                     sw[(gl + 1) * 16 + col] = word_as_float(swv[h * 2 + 1]);
+                    if (AFF) {
+                        ofs[gl * 16 + col] = word_as_float(ofv[h * 2]);
+                        ofs[(gl + 1) * 16 + col] = word_as_float(ofv[h * 2 + 1]);
+                    }
                 }
             } else {
 #pragma unroll
@@ -312,6 +347,7 @@ __global__ __launch_bounds__(kGvWaves * 64) void grouped_gemv_kernel(
                     acc = __fadd_rn(acc, __fmul_rn(dot, __fmul_rn(sxv, swv2)));
                 else
                     acc = __builtin_fmaf(dot, __fmul_rn(swv2, sxv), acc);
+                if (AFF) acc = __builtin_fmaf(ofs[gw * 16 + fc], asq[fr * kGvWindow + gw], acc);
             }
         }
         __syncthreads();
@@ -1771,11 +1807,16 @@ __global__ __launch_bounds__(WGM *WGN * 64) void w4a16_pipe_kernel(
 // convert, the scale product and the fma per output and group) is VALU work
 // and bounds the kernel; the MFMAs take about a third of its time.
 // Groups past `groups` (the odd tail of a k-step) are not folded.
-template <int BITS, int BM, int BN, int WGM, int WGN>
+// AFF (fitted affine Q4, int8.rs:566-571): the offsets (the group-64 scale
+// layout) and sxq = sx * f32(sum of the row's group codes) are staged like the
+// scales, and each group's fold is followed by acc = fma(offset, sxq, acc).
+template <int BITS, int BM, int BN, int WGM, int WGN, bool AFF = false>
 __global__ __launch_bounds__(WGM *WGN * 64) void grouped_pipe_kernel(
     const uint8_t *__restrict__ codes, const uint8_t *__restrict__ scales, const int8_t *__restrict__ q,
     const float *__restrict__ sx, int m, int n, int groups, int kbs, float *y, const float *res,
-    const int *__restrict__ bad) {
+    const int *__restrict__ bad, const uint8_t *__restrict__ offsets = nullptr,
+    const float *__restrict__ sxq = nullptr) {
+    static_assert(!AFF || BITS == 4, "affine offsets are a Q4 form");
     constexpr int WAVES = WGM * WGN;
     constexpr int TM = BM / WGM, TN = BN / WGN, MB = TM / 16, NT = TN / 16;
     constexpr int TILES = BN / 16;
@@ -1793,6 +1834,8 @@ __global__ __launch_bounds__(WGM *WGN * 64) void grouped_pipe_kernel(
     __shared__ __align__(16) uint8_t cs[2 * CSTAGE];
     __shared__ __align__(16) uint8_t sws[2 * SWSTAGE];
     __shared__ __align__(16) uint8_t sxs[2 * SXSTAGE];
+    __shared__ __align__(16) uint8_t ofs[AFF ? 2 * SWSTAGE : 16];
+    __shared__ __align__(16) uint8_t sqs[AFF ? 2 * SXSTAGE : 16];
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), lane = threadIdx.x % 64;
     const int wm = wave / WGN, wn = wave % WGN;
@@ -1811,6 +1854,14 @@ __global__ __launch_bounds__(WGM *WGN * 64) void grouped_pipe_kernel(
     const int32x4_t rs = buffer_rsrc(sx + (size_t)row0 * groups, (uint32_t)(rvalid * groups * 4));
     const uint32_t xs_lds = lds_address(xs), cs_lds = lds_address(cs);
     const uint32_t sws_lds = lds_address(sws), sxs_lds = lds_address(sxs);
+    int32x4_t ro = rw, rsq = rs;
+    uint32_t ofs_lds = 0, sqs_lds = 0;
+    if (AFF) {
+        ro = buffer_rsrc(offsets + (size_t)tile0 * swtile, (uint32_t)tvalid * swtile);
+        rsq = buffer_rsrc(sxq + (size_t)row0 * groups, (uint32_t)(rvalid * groups * 4));
+        ofs_lds = lds_address(ofs);
+        sqs_lds = lds_address(sqs);
+    }
 
     // activation loads: lane l of instruction blk fills slot l % 8 of row
     // 8*blk + l/8; the swizzle depends on blk only through its parity
@@ -1823,6 +1874,8 @@ __global__ __launch_bounds__(WGM *WGN * 64) void grouped_pipe_kernel(
         const int32x4_t nc = live ? rc : int32x4_t{rc[0], rc[1], 0, rc[3]};
         const int32x4_t nw = live ? rw : int32x4_t{rw[0], rw[1], 0, rw[3]};
         const int32x4_t ns = live ? rs : int32x4_t{rs[0], rs[1], 0, rs[3]};
+        const int32x4_t no = live ? ro : int32x4_t{ro[0], ro[1], 0, ro[3]};
+        const int32x4_t nsq = live ? rsq : int32x4_t{rsq[0], rsq[1], 0, rsq[3]};
 #pragma unroll
         for (int p = 0; p < XPW; p++) {
             const int blk = wave + p * WAVES;
@@ -1843,14 +1896,20 @@ __global__ __launch_bounds__(WGM *WGN * 64) void grouped_pipe_kernel(
             const int t = lane / 8;
             const uint32_t off = BITS == 4 ? (uint32_t)(t * kbs + st) * 128 : (uint32_t)(t * groups + 2 * st) * 64;
             dma16(__builtin_amdgcn_readfirstlane(sws_lds + stage * SWSTAGE), off + (uint32_t)(lane % 8) * 16, nw);
+            if (AFF)
+                dma16(__builtin_amdgcn_readfirstlane(ofs_lds + stage * SWSTAGE), off + (uint32_t)(lane % 8) * 16, no);
         }
 #pragma unroll
         for (int p = 0; p < SPW; p++) {
             const int si = wave + p * WAVES;
             const int r = si * 32 + lane / 2;
-            if (SI % WAVES == 0 || si < SI)
+            if (SI % WAVES == 0 || si < SI) {
                 dma4(__builtin_amdgcn_readfirstlane(sxs_lds + stage * SXSTAGE + si * 256),
                      (uint32_t)((r * groups + 2 * st + (lane & 1)) * 4), ns);
+                if (AFF)
+                    dma4(__builtin_amdgcn_readfirstlane(sqs_lds + stage * SXSTAGE + si * 256),
+                         (uint32_t)((r * groups + 2 * st + (lane & 1)) * 4), nsq);
+            }
         }
     };
 
@@ -1865,9 +1924,10 @@ __global__ __launch_bounds__(WGM *WGN * 64) void grouped_pipe_kernel(
 
     // one group of a stage: weight fragments and scales once, then per row
     // block the activation fragment, its scale, NT MFMAs and the fold
-    auto fold_group = [&](const uint8_t *xst, const uint8_t *cst, const uint8_t *swst, const uint8_t *sxst, int gp) {
+    auto fold_group = [&](const uint8_t *xst, const uint8_t *cst, const uint8_t *swst, const uint8_t *sxst,
+                          const uint8_t *ofst, const uint8_t *sqst, int gp) {
         int4_t bfr[NT];
-        float4_t swv[NT];
+        float4_t swv[NT], ofv[AFF ? NT : 1];
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) {
             const int t = wn * NT + nt;
@@ -1878,6 +1938,12 @@ __global__ __launch_bounds__(WGM *WGN * 64) void grouped_pipe_kernel(
                 const float4_t s01 = *(const float4_t *)(swst + t * 128 + qd * 32);       // rows 4qd, 4qd+1
                 const float4_t s23 = *(const float4_t *)(swst + t * 128 + qd * 32 + 16);  // rows 4qd+2, 4qd+3
                 swv[nt] = gp ? float4_t{s01[1], s01[3], s23[1], s23[3]} : float4_t{s01[0], s01[2], s23[0], s23[2]};
+                if (AFF) {
+                    const float4_t o01 = *(const float4_t *)(ofst + t * 128 + qd * 32);
+                    const float4_t o23 = *(const float4_t *)(ofst + t * 128 + qd * 32 + 16);
+                    ofv[AFF ? nt : 0] =
+                        gp ? float4_t{o01[1], o01[3], o23[1], o23[3]} : float4_t{o01[0], o01[2], o23[0], o23[2]};
+                }
             } else {
                 bfr[nt] = *(const int4_t *)(cst + (t * 2 + gp) * 1024 + lane * 16);
                 swv[nt] = *(const float4_t *)(swst + t * 128 + gp * 64 + qd * 16);
@@ -1897,12 +1963,15 @@ __global__ __launch_bounds__(WGM *WGN * 64) void grouped_pipe_kernel(
                 afr = *(const int4_t *)(xst + r * 128 + ((c ^ ((r >> 1) & 7)) * 16));
             }
             const float sxv = *(const float *)(sxst + r * 8 + gp * 4);
+            const float sqv = AFF ? *(const float *)(sqst + r * 8 + gp * 4) : 0.0f;
 #pragma unroll
             for (int nt = 0; nt < NT; nt++) {
                 const int4_t d = mfma_i8(bfr[nt], afr, zero);
 #pragma unroll
-                for (int v = 0; v < 4; v++)
+                for (int v = 0; v < 4; v++) {
                     acc[mb][nt][v] = __builtin_fmaf((float)d[v], __fmul_rn(swv[nt][v], sxv), acc[mb][nt][v]);
+                    if (AFF) acc[mb][nt][v] = __builtin_fmaf(ofv[AFF ? nt : 0][v], sqv, acc[mb][nt][v]);
+                }
             }
         }
     };
@@ -1918,8 +1987,9 @@ __global__ __launch_bounds__(WGM *WGN * 64) void grouped_pipe_kernel(
             load_stage(cur ^ 1, st + 1, st + 1 < steps);
             const uint8_t *xst = xs + cur * XSTAGE, *cst = cs + cur * CSTAGE;
             const uint8_t *swst = sws + cur * SWSTAGE, *sxst = sxs + cur * SXSTAGE;
-            fold_group(xst, cst, swst, sxst, 0);
-            if (2 * st + 1 < groups) fold_group(xst, cst, swst, sxst, 1);
+            const uint8_t *ofst = ofs + (AFF ? cur * SWSTAGE : 0), *sqst = sqs + (AFF ? cur * SXSTAGE : 0);
+            fold_group(xst, cst, swst, sxst, ofst, sqst, 0);
+            if (2 * st + 1 < groups) fold_group(xst, cst, swst, sxst, ofst, sqst, 1);
         }
         __builtin_amdgcn_s_waitcnt(0x0F70);  // no LDS write in flight once the block ends
     }
@@ -2352,30 +2422,31 @@ void gemm_dispatch(const Weight &w, const half_t *x, int m, void *y, const half_
 }
 
 
-template <int BITS, int MPAD, int AMODE, bool PROJECT>
+template <int BITS, int MPAD, int AMODE, bool PROJECT, bool AFF = false>
 void gv_launch_one(const Weight &w, const void *a, const float *sa, int m, int abits, float *y,
                    const int *bad_in, int *bad_out, hipStream_t s) {
-    using S = GvShape<MPAD>;
+    using S = GvShape<MPAD, AFF>;
     static bool configured[64] = {};  // the LDS limit is a per-device function attribute
     int dev = 0;
     hipGetDevice(&dev);
     if (dev >= 0 && dev < 64 && !configured[dev]) {
-        if (hipFuncSetAttribute((const void *)grouped_gemv_kernel<BITS, MPAD, AMODE, PROJECT>,
+        if (hipFuncSetAttribute((const void *)grouped_gemv_kernel<BITS, MPAD, AMODE, PROJECT, AFF>,
                             hipFuncAttributeMaxDynamicSharedMemorySize, S::BYTES) == hipSuccess) configured[dev] = true;
     }
     dim3 grid(w.tiles(), cdiv(m, 16));
-    hipLaunchKernelGGL((grouped_gemv_kernel<BITS, MPAD, AMODE, PROJECT>), grid, dim3(kGvWaves * 64), S::BYTES, s,
-                       w.codes, w.scales, a, sa, m, w.cols, w.rows, w.groups, w.kblocks(), abits, y, bad_in, bad_out);
+    hipLaunchKernelGGL((grouped_gemv_kernel<BITS, MPAD, AMODE, PROJECT, AFF>), grid, dim3(kGvWaves * 64), S::BYTES,
+                       s, w.codes, w.scales, a, sa, m, w.cols, w.rows, w.groups, w.kblocks(), abits, y, bad_in,
+                       bad_out, w.offsets);
 }
 
-template <int BITS, int AMODE, bool PROJECT>
+template <int BITS, int AMODE, bool PROJECT, bool AFF = false>
 void gv_launch_m(const Weight &w, const void *a, const float *sa, int m, int abits, float *y,
                  const int *bad_in, int *bad_out, hipStream_t s) {
-    if (m <= 1) gv_launch_one<BITS, 1, AMODE, PROJECT>(w, a, sa, m, abits, y, bad_in, bad_out, s);
-    else if (m <= 2) gv_launch_one<BITS, 2, AMODE, PROJECT>(w, a, sa, m, abits, y, bad_in, bad_out, s);
-    else if (m <= 4) gv_launch_one<BITS, 4, AMODE, PROJECT>(w, a, sa, m, abits, y, bad_in, bad_out, s);
-    else if (m <= 8) gv_launch_one<BITS, 8, AMODE, PROJECT>(w, a, sa, m, abits, y, bad_in, bad_out, s);
-    else gv_launch_one<BITS, 16, AMODE, PROJECT>(w, a, sa, m, abits, y, bad_in, bad_out, s);
+    if (m <= 1) gv_launch_one<BITS, 1, AMODE, PROJECT, AFF>(w, a, sa, m, abits, y, bad_in, bad_out, s);
+    else if (m <= 2) gv_launch_one<BITS, 2, AMODE, PROJECT, AFF>(w, a, sa, m, abits, y, bad_in, bad_out, s);
+    else if (m <= 4) gv_launch_one<BITS, 4, AMODE, PROJECT, AFF>(w, a, sa, m, abits, y, bad_in, bad_out, s);
+    else if (m <= 8) gv_launch_one<BITS, 8, AMODE, PROJECT, AFF>(w, a, sa, m, abits, y, bad_in, bad_out, s);
+    else gv_launch_one<BITS, 16, AMODE, PROJECT, AFF>(w, a, sa, m, abits, y, bad_in, bad_out, s);
 }
 
 template <int AMODE, bool PROJECT>
@@ -2429,6 +2500,10 @@ int variant_index(const char *family, const char *name) {
 void launch_grouped_small(const Weight &w, const float *x, int m, int abits, float *y, int *bad_out,
                           bool project, hipStream_t s) {
     if (m == 0) return;
+    if (w.offsets && !project) {  // fitted affine Q4 (the runtime refuses the other combinations)
+        gv_launch_m<4, 0, false, true>(w, x, nullptr, m, abits, y, nullptr, bad_out, s);
+        return;
+    }
     if (project)
         gv_launch<0, true>(w, x, nullptr, m, abits, y, nullptr, bad_out, s);
     else
@@ -2462,10 +2537,13 @@ bool grouped_pipe_fits(const Weight &w, int bm) {
 
 template <int BM, int WGM, int WGN>
 bool grouped_pipe_launch(const Weight &w, const int8_t *q, const float *sx, int m, float *y, const int *bad,
-                         hipStream_t s, const float *res) {
+                         hipStream_t s, const float *res, const float *sxq) {
     if (!grouped_pipe_fits(w, BM)) return false;
     const dim3 blocks(cdiv(m, BM) * cdiv(w.rows, 128));
-    if (w.bits == 4)
+    if (w.offsets)
+        hipLaunchKernelGGL((grouped_pipe_kernel<4, BM, 128, WGM, WGN, true>), blocks, dim3(WGM * WGN * 64), 0, s,
+                           w.codes, w.scales, q, sx, m, w.rows, w.groups, w.kblocks(), y, res, bad, w.offsets, sxq);
+    else if (w.bits == 4)
         hipLaunchKernelGGL((grouped_pipe_kernel<4, BM, 128, WGM, WGN>), blocks, dim3(WGM * WGN * 64), 0, s, w.codes,
                            w.scales, q, sx, m, w.rows, w.groups, w.kblocks(), y, res, bad);
     else
@@ -2513,21 +2591,24 @@ bool grouped_adds_residual(const Weight &w, int m, int variant) {
 }
 
 bool launch_grouped(const Weight &w, const int8_t *q, const float *sx, int m, float *y,
-                    const int *bad, int variant, hipStream_t s, const float *res) {
+                    const int *bad, int variant, hipStream_t s, const float *res, const float *sxq) {
     if (m == 0) return true;
     switch (grouped_pick(w, m, variant)) {
-        case 1: if (grouped_pipe_launch<256, 2, 4>(w, q, sx, m, y, bad, s, res)) return true; break;
-        case 3: if (grouped_pipe_launch<128, 2, 2>(w, q, sx, m, y, bad, s, res)) return true; break;
-        case 4: if (grouped_pipe_launch<64, 1, 2>(w, q, sx, m, y, bad, s, res)) return true; break;
-        case 5: if (grouped_pipe_launch<128, 1, 4>(w, q, sx, m, y, bad, s, res)) return true; break;
-        case 6: if (grouped_pipe_launch<128, 4, 1>(w, q, sx, m, y, bad, s, res)) return true; break;
-        case 7: if (grouped_pipe_launch<32, 1, 8>(w, q, sx, m, y, bad, s, res)) return true; break;
-        case 8: if (grouped_pipe_launch<64, 2, 4>(w, q, sx, m, y, bad, s, res)) return true; break;
+        case 1: if (grouped_pipe_launch<256, 2, 4>(w, q, sx, m, y, bad, s, res, sxq)) return true; break;
+        case 3: if (grouped_pipe_launch<128, 2, 2>(w, q, sx, m, y, bad, s, res, sxq)) return true; break;
+        case 4: if (grouped_pipe_launch<64, 1, 2>(w, q, sx, m, y, bad, s, res, sxq)) return true; break;
+        case 5: if (grouped_pipe_launch<128, 1, 4>(w, q, sx, m, y, bad, s, res, sxq)) return true; break;
+        case 6: if (grouped_pipe_launch<128, 4, 1>(w, q, sx, m, y, bad, s, res, sxq)) return true; break;
+        case 7: if (grouped_pipe_launch<32, 1, 8>(w, q, sx, m, y, bad, s, res, sxq)) return true; break;
+        case 8: if (grouped_pipe_launch<64, 2, 4>(w, q, sx, m, y, bad, s, res, sxq)) return true; break;
         default: break;
     }
     if (res) return false;  // only the pipelined kernels add a residual
     dim3 grid(cdiv(w.tiles(), 4), cdiv(m, 16));
-    if (w.bits == 4)
+    if (w.offsets)
+        hipLaunchKernelGGL((grouped_kernel<4, true>), grid, dim3(256), 0, s, w.codes, w.scales, q, sx, m, w.rows,
+                           w.groups, w.kblocks(), y, bad, w.offsets, sxq);
+    else if (w.bits == 4)
         hipLaunchKernelGGL(grouped_kernel<4>, grid, dim3(256), 0, s, w.codes, w.scales, q, sx, m, w.rows,
                            w.groups, w.kblocks(), y, bad);
     else

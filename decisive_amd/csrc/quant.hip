@@ -28,9 +28,11 @@ __device__ __forceinline__ size_t q4_word(int t, int kb, int kbs, int q, int j, 
 // ---- wire -> native ----------------------------------------------------------
 
 // One thread per (row n, k-block kb, lane q): builds that lane's 16 bytes.
+// fitted: the scales of fitted Q4 weights (quantization.rs mse) may be
+// negative; any finite nonzero scale is accepted then.
 __global__ void upload_q4_kernel(const uint8_t *__restrict__ wire, uint8_t *__restrict__ codes,
                                  uint8_t *__restrict__ scales, int rows, int cols, int np,
-                                 int kbs, int g32, int *bad) {
+                                 int kbs, int g32, int fitted, int *bad) {
     size_t id = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
     size_t total = (size_t)np * kbs * 4;
     if (id >= total) return;
@@ -84,7 +86,8 @@ __global__ void upload_q4_kernel(const uint8_t *__restrict__ wire, uint8_t *__re
                 const uint8_t *group = wire + n * row_bytes + (size_t)g * 36;
                 uint32_t bits = group[32] | (group[33] << 8) | (group[34] << 16) | ((uint32_t)group[35] << 24);
                 v = __builtin_bit_cast(float, bits);
-                if (!(v > 0.0f && v <= FLT_MAX)) atomicOr(bad, 1);
+                const bool ok = fitted ? (v != 0.0f && fabsf(v) <= FLT_MAX) : (v > 0.0f && v <= FLT_MAX);
+                if (!ok) atomicOr(bad, 1);
             }
             fs[h] = v;
         }
@@ -196,11 +199,21 @@ __global__ void quantize_weight_kernel(const void *__restrict__ values, int dtyp
 
 // ---- dequantization ------------------------------------------------------------------
 
-// One thread per (output row r, 8 consecutive k).
+// The NF4 codebook (QLoRA, Dettmers et al. 2023: quantiles of N(0, 1)
+// normalized to [-1, 1] with an exact zero), quantization.rs:3-20.
+__constant__ float kNf4[16] = {
+    -1.0f, -0.6961928009986877f, -0.5250730514526367f, -0.39491748809814453f,
+    -0.28444138169288635f, -0.18477343022823334f, -0.09105003625154495f, 0.0f,
+    0.07958029955625534f, 0.16093020141124725f, 0.24611230194568634f, 0.33791524171829224f,
+    0.44070982933044434f, 0.5626170039176941f, 0.7229568362236023f, 1.0f};
+
+// One thread per (output row r, 8 consecutive k). Fitted Q4 weights decode as
+// quantized_rows.rs:89-110 append: value = f32(code) or NF4[code + 8], times
+// the scale, then plus the group's offset (affine), each step rounded.
 __global__ void dequant_kernel(const uint8_t *__restrict__ codes, const uint8_t *__restrict__ scales,
                                const int32_t *__restrict__ ids, int count, int rows, int cols,
                                int kbs, int bits, int g32, void *__restrict__ y, int dtype,
-                               int *bad) {
+                               int *bad, const uint8_t *__restrict__ offsets, int nf4) {
     int k8s = (cols + 7) / 8;
     size_t id = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
     if (id >= (size_t)count * k8s) return;
@@ -218,8 +231,12 @@ __global__ void dequant_kernel(const uint8_t *__restrict__ codes, const uint8_t 
         const uint8_t *rec = scales + (((size_t)t * kbs + kb) * 16 + j) * 8;
         float scale = g32 ? (float)((const half_t *)rec)[s] : ((const float *)rec)[(k0 % 128) / 64];
         for (int e = 0; e < 8; e++) {
-            int code = (int)((w >> ((e & 1) * 16 + (e >> 1) * 4)) & 15u) - 8;
-            out[e] = __fmul_rn((float)code, scale);
+            const int nib = (int)((w >> ((e & 1) * 16 + (e >> 1) * 4)) & 15u);
+            out[e] = __fmul_rn(nf4 ? kNf4[nib] : (float)(nib - 8), scale);
+        }
+        if (offsets) {
+            const float o = ((const float *)(offsets + (((size_t)t * kbs + kb) * 16 + j) * 8))[(k0 % 128) / 64];
+            for (int e = 0; e < 8; e++) out[e] = __fadd_rn(out[e], o);
         }
     } else {
         int kb = k0 / 64, q = (k0 % 64) / 16, off = k0 % 16;
@@ -565,9 +582,31 @@ __global__ void fill_i32_kernel(int *p, int value, int count) {
 
 inline unsigned blocks_for(size_t n, unsigned per) { return (unsigned)((n + per - 1) / per); }
 
+// int8.rs:191-193 and :568-569: the factor the affine offset term takes per
+// (row, 64-group), sx * f32(sum of the group's codes), rounded to f32. One
+// thread per (row, group).
+__global__ void act_sums_kernel(const int8_t *__restrict__ q, const float *__restrict__ sx, int m, int groups,
+                                float *__restrict__ sxq) {
+    const size_t id = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+    if (id >= (size_t)m * groups) return;
+    const int4_t *p = (const int4_t *)(q + id * 64);
+    int sum = 0;
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int4_t v = p[u];
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const uint32_t word = (uint32_t)v[w];
+#pragma unroll
+            for (int b = 0; b < 4; b++) sum += (int)(int8_t)(word >> (8 * b));
+        }
+    }
+    sxq[id] = __fmul_rn(sx[id], (float)sum);
+}
+
 }  // namespace
 
-void launch_upload(const Weight &w, const uint8_t *wire, int *bad, hipStream_t s) {
+void launch_upload(const Weight &w, const uint8_t *wire, int *bad, hipStream_t s, bool fitted) {
     size_t total = (size_t)w.np * w.kblocks() * 4;
     if (w.kind == WeightKind::Q8G64) {
         hipLaunchKernelGGL(upload_q8_kernel, dim3(blocks_for(total, 256)), dim3(256), 0, s, wire,
@@ -575,7 +614,7 @@ void launch_upload(const Weight &w, const uint8_t *wire, int *bad, hipStream_t s
     } else {
         hipLaunchKernelGGL(upload_q4_kernel, dim3(blocks_for(total, 256)), dim3(256), 0, s, wire,
                            w.codes, w.scales, w.rows, w.cols, w.np, w.kblocks(),
-                           w.kind == WeightKind::Q4G32 ? 1 : 0, bad);
+                           w.kind == WeightKind::Q4G32 ? 1 : 0, fitted ? 1 : 0, bad);
     }
 }
 
@@ -594,7 +633,7 @@ void launch_dequant_checked(const Weight &w, const int32_t *ids, int count, void
     if (!total) return;
     hipLaunchKernelGGL(dequant_kernel, dim3(blocks_for(total, 256)), dim3(256), 0, s, w.codes,
                        w.scales, ids, count, w.rows, w.cols, w.kblocks(), w.bits,
-                       w.kind == WeightKind::Q4G32 ? 1 : 0, y, dtype, bad);
+                       w.kind == WeightKind::Q4G32 ? 1 : 0, y, dtype, bad, w.offsets, w.nf4 ? 1 : 0);
 }
 
 void launch_dequant(const Weight &w, const int32_t *ids, int count, void *y, int dtype,
@@ -608,6 +647,12 @@ void launch_act_quantize(const float *x, int m, int k, int bits, int8_t *q, floa
     if (!lanes) return;
     hipLaunchKernelGGL(act_quantize_kernel, dim3(blocks_for(lanes, 256)), dim3(256), 0, s, x, m, k,
                        bits, q, sc, bad, (uint32_t *)nullptr);
+}
+
+void launch_act_sums(const int8_t *q, const float *sx, int m, int groups, float *sxq, hipStream_t s) {
+    const size_t n = (size_t)m * groups;
+    if (!n) return;
+    hipLaunchKernelGGL(act_sums_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, q, sx, m, groups, sxq);
 }
 
 void launch_act_quantize_records(const float *x, int m, int k, uint32_t *records, int *bad,

@@ -6,6 +6,7 @@
 // context stream; device-side validation (scales, non-finite inputs, token
 // ids) reports through a device flag that the synchronous entry points read.
 #include <float.h>
+#include <math.h>
 #include <stdio.h>
 #include <string.h>
 
@@ -361,7 +362,23 @@ void free_weight(dz_weight *h) {
     if (!h) return;
     if (h->w.codes) hipFree(h->w.codes);
     if (h->w.scales) hipFree(h->w.scales);
+    if (h->w.offsets) hipFree(h->w.offsets);
     delete h;
+}
+
+// The fitted forms (bit DZ_FIT_*) a product takes; weights that are not
+// fitted run everywhere.
+constexpr int kFitGrouped = 1 << DZ_FIT_SCALED | 1 << DZ_FIT_AFFINE;
+constexpr int kFitW4A16 = 1 << DZ_FIT_SCALED;
+constexpr int kFitNone = 0;
+const char *const kFitNames[] = {"scaled", "affine", "NF4"};
+
+int32_t fitted_form_ok(dz_ctx *ctx, const dz_weight *w, int forms, const char *what) {
+    if (!w || !w->w.fitted) return DZ_OK;
+    const int form = w->w.nf4 ? DZ_FIT_NF4 : w->w.offsets ? DZ_FIT_AFFINE : DZ_FIT_SCALED;
+    if (forms >> form & 1) return DZ_OK;
+    return fail(ctx, DZ_INVALID_PARAMETERS,
+                std::string(what) + " does not take " + kFitNames[form] + " fitted weights");
 }
 
 }  // namespace
@@ -540,10 +557,10 @@ int32_t dz_copy_d2h(dz_ctx *ctx, void *dst, const void *src, size_t bytes) {
 
 // ---- weights ------------------------------------------------------------------------
 
-int32_t dz_weight_upload(dz_ctx *ctx, const void *packed, size_t bytes, int32_t layout,
-                         size_t rows, size_t cols, dz_weight **out) {
-    DZ_BEGIN(ctx);
-    DZ_NOT_CAPTURING(ctx);
+namespace {
+
+int32_t upload_weight(dz_ctx *ctx, const void *packed, size_t bytes, int32_t layout, size_t rows, size_t cols,
+                      bool fitted, dz_weight **out) {
     if (!out || (!packed && bytes)) return fail(ctx, DZ_INVALID_REQUEST, "null pointer");
     *out = nullptr;
     dz::WeightKind kind;
@@ -570,7 +587,7 @@ int32_t dz_weight_upload(dz_ctx *ctx, const void *packed, size_t bytes, int32_t 
     e = hipMemcpyAsync(staging, packed, bytes, hipMemcpyHostToDevice, ctx->stream);
     int bad = 0;
     if (e == hipSuccess) {
-        rc = flagged_sync(ctx, [&] { dz::launch_upload(h->w, staging, ctx->flag, ctx->stream); }, &bad);
+        rc = flagged_sync(ctx, [&] { dz::launch_upload(h->w, staging, ctx->flag, ctx->stream, fitted); }, &bad);
     } else {
         rc = hip_fail(ctx, e, "copy to device");
     }
@@ -582,6 +599,55 @@ int32_t dz_weight_upload(dz_ctx *ctx, const void *packed, size_t bytes, int32_t 
     if (bad) {
         free_weight(h);
         return fail(ctx, DZ_INVALID_CHECKPOINT, "invalid packed scale");
+    }
+    *out = h;
+    return DZ_OK;
+}
+
+}  // namespace
+
+int32_t dz_weight_upload(dz_ctx *ctx, const void *packed, size_t bytes, int32_t layout,
+                         size_t rows, size_t cols, dz_weight **out) {
+    DZ_BEGIN(ctx);
+    DZ_NOT_CAPTURING(ctx);
+    return upload_weight(ctx, packed, bytes, layout, rows, cols, false, out);
+}
+
+int32_t dz_weight_upload_fitted(dz_ctx *ctx, const void *packed, size_t bytes, size_t rows, size_t cols,
+                                int32_t form, const float *offsets, dz_weight **out) {
+    DZ_BEGIN(ctx);
+    DZ_NOT_CAPTURING(ctx);
+    if (form != DZ_FIT_SCALED && form != DZ_FIT_AFFINE && form != DZ_FIT_NF4)
+        return fail(ctx, DZ_INVALID_PARAMETERS, "unknown fitted form");
+    if ((form == DZ_FIT_AFFINE) != (offsets != nullptr))
+        return fail(ctx, DZ_INVALID_REQUEST, "affine weights take offsets and the other forms none");
+    dz_weight *h = nullptr;
+    int32_t rc = upload_weight(ctx, packed, bytes, DZ_Q4_G64_F32, rows, cols, true, &h);
+    if (rc) return rc;
+    h->w.fitted = true;
+    h->w.nf4 = form == DZ_FIT_NF4;
+    if (offsets) {
+        // [rows x groups] -> the group-64 scale layout: [tile][k-block][16 rows][2]
+        dz::Weight &w = h->w;
+        const size_t groups = cols / 64, kbs = (size_t)w.kblocks();
+        std::vector<float> native(w.scale_bytes / sizeof(float), 0.0f);
+        for (size_t r = 0; r < rows; r++)
+            for (size_t g = 0; g < groups; g++) {
+                const float v = offsets[r * groups + g];
+                if (!isfinite(v)) {
+                    free_weight(h);
+                    return fail(ctx, DZ_INVALID_CHECKPOINT, "non-finite affine offset");
+                }
+                native[(((r / 16) * kbs + g / 2) * 16 + r % 16) * 2 + g % 2] = v;
+            }
+        hipError_t e = hipMalloc(&w.offsets, w.scale_bytes);
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(w.offsets, native.data(), w.scale_bytes, hipMemcpyHostToDevice, ctx->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) {
+            free_weight(h);
+            return hip_fail(ctx, e, "affine offsets");
+        }
     }
     *out = h;
     return DZ_OK;
@@ -631,7 +697,7 @@ int32_t dz_weight_info(const dz_weight *h, size_t *rows, size_t *cols, int32_t *
     if (cols) *cols = (size_t)h->w.cols;
     if (bits) *bits = h->w.bits;
     if (group) *group = h->w.group;
-    if (device_bytes) *device_bytes = h->w.code_bytes + h->w.scale_bytes;
+    if (device_bytes) *device_bytes = h->w.code_bytes + h->w.scale_bytes + (h->w.offsets ? h->w.scale_bytes : 0);
     return DZ_OK;
 }
 
@@ -678,6 +744,8 @@ int32_t grouped_linear(dz_ctx *ctx, const dz_weight *a, const dz_weight *b, cons
         return fail(ctx, DZ_INVALID_PARAMETERS, "grouped int8 mode needs a group-64 weight");
     if (b && (b->w.cols != w.cols || b->w.kind == dz::WeightKind::Q4G32))
         return fail(ctx, DZ_INVALID_PARAMETERS, "paired weights must share the input width");
+    if (int32_t rc = fitted_form_ok(ctx, a, kFitGrouped, "the grouped product")) return rc;
+    if (int32_t rc = fitted_form_ok(ctx, b, kFitGrouped, "the grouped product")) return rc;
     if (m == 0) return DZ_OK;
     const int abits = mode == DZ_W4A4 ? 4 : 8;
     if (m <= 16) {
@@ -686,17 +754,22 @@ int32_t grouped_linear(dz_ctx *ctx, const dz_weight *a, const dz_weight *b, cons
         if (b) dz::launch_grouped_small(b->w, x, (int)m, abits, yb, nullptr, false, ctx->stream);
         return launched(ctx, "grouped linear");
     }
+    // codes, their scales and, for affine weights, sx * f32(sum of the codes) per group
+    const bool sums = w.offsets || (b && b->w.offsets);
     size_t qbytes = m * (size_t)w.groups * 64, sbytes = m * (size_t)w.groups * sizeof(float);
-    int32_t rc = ensure_work(ctx, qbytes + sbytes + 256);
+    const size_t sq_at = (qbytes + 255) / 256 * 256 + (sbytes + 255) / 256 * 256;
+    int32_t rc = ensure_work(ctx, sums ? sq_at + sbytes : qbytes + sbytes + 256);
     if (rc) return rc;
     int8_t *q = (int8_t *)ctx->work;
     float *s = (float *)((uint8_t *)ctx->work + (qbytes + 255) / 256 * 256);
+    float *sq = sums ? (float *)((uint8_t *)ctx->work + sq_at) : nullptr;
     int *bad = nullptr;
     rc = product_flag(ctx, &bad);
     if (rc) return rc;
     dz::launch_act_quantize(x, (int)m, w.cols, abits, q, s, bad, ctx->stream);
-    dz::launch_grouped(w, q, s, (int)m, ya, bad, variant(ctx, "grouped"), ctx->stream);
-    if (b) dz::launch_grouped(b->w, q, s, (int)m, yb, bad, variant(ctx, "grouped"), ctx->stream);
+    if (sums) dz::launch_act_sums(q, s, (int)m, w.groups, sq, ctx->stream);
+    dz::launch_grouped(w, q, s, (int)m, ya, bad, variant(ctx, "grouped"), ctx->stream, nullptr, sq);
+    if (b) dz::launch_grouped(b->w, q, s, (int)m, yb, bad, variant(ctx, "grouped"), ctx->stream, nullptr, sq);
     return launched(ctx, "grouped linear");
 }
 
@@ -716,6 +789,7 @@ int32_t dz_linear(dz_ctx *ctx, const dz_weight *w, const void *x, int32_t x_dtyp
         if (w->w.bits != 4) return fail(ctx, DZ_INVALID_PARAMETERS, "W4A16 needs a Q4 weight");
         if (w->w.cols % 8 != 0) return fail(ctx, DZ_INVALID_PARAMETERS, "W4A16 needs cols % 8 == 0");
         if (((uintptr_t)x & 15) != 0) return fail(ctx, DZ_INVALID_PARAMETERS, "W4A16 activations must be 16-byte aligned");
+        if (int32_t rc = fitted_form_ok(ctx, w, kFitW4A16, "W4A16")) return rc;
         if (m == 0) return DZ_OK;
         dz::launch_w4a16(w->w, (const dz::half_t *)x, (int)m, y, variant(ctx, "gemv"),
                          variant(ctx, "gemm_w4a16"), ctx->stream);
@@ -735,9 +809,12 @@ int32_t dz_linear_noalloc(dz_ctx *ctx, const dz_weight *w, const void *x, int32_
     const dz::Weight &wt = w->w;
     if (wt.kind == dz::WeightKind::Q4G32)
         return fail(ctx, DZ_INVALID_PARAMETERS, "grouped int8 mode needs a group-64 weight");
-    // [0, 256) the flag, then the codes, then the scales (256-byte aligned)
+    if (int32_t rc = fitted_form_ok(ctx, w, kFitGrouped, "the grouped product")) return rc;
+    // [0, 256) the flag, then the codes, then the scales, then for affine
+    // weights sx * sum of the codes (each part 256-byte aligned)
     const size_t qbytes = m * (size_t)wt.groups * 64, sbytes = m * (size_t)wt.groups * sizeof(float);
-    const size_t need = 256 + (qbytes + 255) / 256 * 256 + sbytes;
+    const size_t sq_at = 256 + (qbytes + 255) / 256 * 256 + (sbytes + 255) / 256 * 256;
+    const size_t need = wt.offsets ? sq_at + sbytes : 256 + (qbytes + 255) / 256 * 256 + sbytes;
     if (need > kScratchBytes)
         return fail(ctx, DZ_RESOURCE_LIMIT,
                     "dz_linear_noalloc: " + std::to_string(m) + " rows of " + std::to_string(wt.cols) +
@@ -748,8 +825,10 @@ int32_t dz_linear_noalloc(dz_ctx *ctx, const dz_weight *w, const void *x, int32_
     float *sx = (float *)(ctx->scratch + 256 + (qbytes + 255) / 256 * 256);
     const int abits = mode == DZ_W4A4 ? 4 : 8;
     dz::launch_fill_i32(bad, 0, 1, ctx->stream);  // a kernel, not a memset: graph replays clear it too
+    float *sq = wt.offsets ? (float *)(ctx->scratch + sq_at) : nullptr;
     dz::launch_act_quantize((const float *)x, (int)m, wt.cols, abits, q, sx, bad, ctx->stream);
-    dz::launch_grouped(wt, q, sx, (int)m, y, bad, variant(ctx, "grouped"), ctx->stream);
+    if (sq) dz::launch_act_sums(q, sx, (int)m, wt.groups, sq, ctx->stream);
+    dz::launch_grouped(wt, q, sx, (int)m, y, bad, variant(ctx, "grouped"), ctx->stream, nullptr, sq);
     return launched(ctx, "grouped linear (no allocation)");
 }
 
@@ -761,6 +840,7 @@ int32_t dz_linear_f16(dz_ctx *ctx, const dz_weight *w, const void *x, size_t m, 
         return fail(ctx, DZ_INVALID_PARAMETERS, "unknown epilogue");
     if (epilogue == DZ_EPI_RESIDUAL && m && !residual) return fail(ctx, DZ_INVALID_REQUEST, "null residual");
     if (w->w.bits != 4) return fail(ctx, DZ_INVALID_PARAMETERS, "W4A16 needs a Q4 weight");
+    if (int32_t rc = fitted_form_ok(ctx, w, kFitW4A16, "dz_linear_f16")) return rc;
     if (w->w.cols % 8 != 0) return fail(ctx, DZ_INVALID_PARAMETERS, "W4A16 needs cols % 8 == 0");
     if (((uintptr_t)x & 15) != 0) return fail(ctx, DZ_INVALID_PARAMETERS, "W4A16 activations must be 16-byte aligned");
     if (m == 0) return DZ_OK;
@@ -796,6 +876,8 @@ int32_t dz_mlp_requant(dz_ctx *ctx, const dz_weight *gate, const dz_weight *up, 
     const dz::Weight &g = gate->w, &u = up->w;
     if (g.kind != dz::WeightKind::Q4G64 || u.kind != dz::WeightKind::Q4G64)
         return fail(ctx, DZ_INVALID_PARAMETERS, "fused MLP needs Q4 group-64 weights");
+    if (int32_t rc = fitted_form_ok(ctx, gate, kFitNone, "dz_mlp_requant")) return rc;
+    if (int32_t rc = fitted_form_ok(ctx, up, kFitNone, "dz_mlp_requant")) return rc;
     if (g.rows != u.rows || g.cols != u.cols || g.rows % 64 != 0)
         return fail(ctx, DZ_INVALID_PARAMETERS, "fused MLP shapes must match with rows % 64 == 0");
     if (m == 0) return DZ_OK;
@@ -818,6 +900,7 @@ int32_t dz_linear_q8(dz_ctx *ctx, const dz_weight *w, const int8_t *q, const flo
     if (!w || (m && (!q || !s || !y))) return fail(ctx, DZ_INVALID_REQUEST, "null pointer");
     if (w->w.kind == dz::WeightKind::Q4G32)
         return fail(ctx, DZ_INVALID_PARAMETERS, "grouped int8 mode needs a group-64 weight");
+    if (int32_t rc = fitted_form_ok(ctx, w, kFitNone, "dz_linear_q8")) return rc;
     if (m <= 16)
         dz::launch_grouped_codes(w->w, q, s, (int)m, y, nullptr, false, ctx->stream);
     else
@@ -831,6 +914,7 @@ int32_t dz_project(dz_ctx *ctx, const dz_weight *w, const float *x, size_t m, fl
     if (!w || (m && (!x || !y))) return fail(ctx, DZ_INVALID_REQUEST, "null pointer");
     if (w->w.kind == dz::WeightKind::Q4G32 || w->w.cols % 64 != 0)
         return fail(ctx, DZ_INVALID_PARAMETERS, "invalid packed readout shape");
+    if (int32_t rc = fitted_form_ok(ctx, w, kFitNone, "dz_project")) return rc;
     if (m == 0) return DZ_OK;
     if (m > (1u << 24)) return fail(ctx, DZ_INPUT_TOO_LONG, "input budget exceeded");
     int32_t rc = ensure_work(ctx, project_work_bytes(w->w, m));
@@ -848,6 +932,7 @@ int32_t dz_readout(dz_ctx *ctx, const dz_weight *w, const float *norm, const flo
     if (!w || !norm || (rows && (!hidden || !logits))) return fail(ctx, DZ_INVALID_REQUEST, "null pointer");
     if (w->w.kind == dz::WeightKind::Q4G32 || w->w.cols % 64 != 0 || w->w.cols > dz::kReadoutMaxCols)
         return fail(ctx, DZ_INVALID_PARAMETERS, "invalid packed readout shape");
+    if (int32_t rc = fitted_form_ok(ctx, w, kFitNone, "dz_readout")) return rc;
     if (rows == 0) return DZ_OK;
     if (rows > (1u << 20)) return fail(ctx, DZ_INPUT_TOO_LONG, "input budget exceeded");
     return readout_rows(ctx, w->w, norm, hidden, 0, nullptr, rows, eps, logits);
@@ -866,6 +951,7 @@ int32_t dz_linear_records(dz_ctx *ctx, const dz_weight *w, const uint32_t *recor
     if (!w || (m && (!records || !y))) return fail(ctx, DZ_INVALID_REQUEST, "null pointer");
     if (w->w.kind == dz::WeightKind::Q4G32 || w->w.cols % 64 != 0)
         return fail(ctx, DZ_INVALID_PARAMETERS, "records products need a group-64 weight with cols % 64 == 0");
+    if (int32_t rc = fitted_form_ok(ctx, w, kFitNone, "dz_linear_records")) return rc;
     if (m > (1u << 24)) return fail(ctx, DZ_INPUT_TOO_LONG, "input budget exceeded");
     dz::launch_grouped_records(w->w, records, (int)m, y, ctx->stream);
     return launched(ctx, "grouped records linear");

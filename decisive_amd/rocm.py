@@ -31,6 +31,7 @@ EPI_NONE, EPI_GELU, EPI_RESIDUAL = 0, 1, 2
 W4A8, W4A4, W4A16 = 0, 1, 2
 PPLX_RESIDENT, PPLX_STREAMED = 0, 1
 PPLX_WHOLE, PPLX_MIXER, PPLX_MLP = 0, 1, 2  # dz_pplx_layer_part's parts
+FIT_SCALED, FIT_AFFINE, FIT_NF4 = 0, 1, 2  # dz_weight_upload_fitted's forms
 
 
 class DzError(RuntimeError):
@@ -99,6 +100,7 @@ _SIGNATURES = {
     "dz_copy_h2d": (I32, [P, P, P, SZ]),
     "dz_copy_d2h": (I32, [P, P, P, SZ]),
     "dz_weight_upload": (I32, [P, P, SZ, I32, SZ, SZ, PP]),
+    "dz_weight_upload_fitted": (I32, [P, P, SZ, SZ, SZ, I32, P, PP]),
     "dz_weight_quantize": (I32, [P, P, I32, SZ, SZ, I32, I32, PP]),
     "dz_weight_free": (I32, [P, P]),
     "dz_weight_info": (I32, [P, ctypes.POINTER(SZ), ctypes.POINTER(SZ), ctypes.POINTER(I32),
@@ -283,6 +285,18 @@ class Context:
         h = ctypes.c_void_p()
         self._check(load().dz_weight_upload(self.handle, packed.ctypes.data, packed.nbytes, layout, rows, cols,
                                             ctypes.byref(h)))
+        return Weight(self, h.value)
+
+    def upload_fitted(self, packed, rows: int, cols: int, form: int, offsets=None) -> Weight:
+        """dz_weight_upload_fitted: a fitted Q4 g64/f32 wire matrix (full code range,
+        signed scales) of `form` (FIT_SCALED, FIT_AFFINE with f32 offsets
+        [rows x cols/64], FIT_NF4)."""
+        import numpy as np
+        packed = np.ascontiguousarray(packed, dtype=np.uint8)
+        off = None if offsets is None else np.ascontiguousarray(offsets, dtype=np.float32)
+        h = ctypes.c_void_p()
+        self._check(load().dz_weight_upload_fitted(self.handle, packed.ctypes.data, packed.nbytes, rows, cols, form,
+                                                   None if off is None else off.ctypes.data, ctypes.byref(h)))
         return Weight(self, h.value)
 
     def quantize(self, values, dtype: int, rows: int, cols: int, bits: int = 4, group: int = 64) -> Weight:

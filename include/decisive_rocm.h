@@ -153,6 +153,41 @@ int32_t dz_copy_d2h(dz_ctx *ctx, void *dst_host, const void *src_dev, size_t byt
  * Synchronous. */
 int32_t dz_weight_upload(dz_ctx *ctx, const void *packed_host, size_t bytes, int32_t layout,
                          size_t rows, size_t cols, dz_weight **out);
+/* Fitted Q4 forms (quantization.rs), each a [rows x cols] matrix in the
+ * DZ_Q4_G64_F32 wire layout whose codes may take the whole nibble range
+ * (-8..7) and whose f32 scales may be any finite nonzero value:
+ *  - DZ_FIT_SCALED: y = code * scale; quantization.rs:25-71 mse (its scales
+ *    may be negative), int8.rs:51-152 from_bf16_optimized with `optimized`;
+ *  - DZ_FIT_AFFINE: y = code * scale + offset, one f32 offset per row and
+ *    64-group; quantization.rs:147-200 affine, from_bf16_optimized with
+ *    `affine`;
+ *  - DZ_FIT_NF4: y = NF4[code + 8] * scale, the codebook of
+ *    quantization.rs:3-20; quantization.rs:260-302 nf4, the embedding rows of
+ *    quantized_rows.rs:21-87 (int8.rs Matrix has no codebook form). */
+#define DZ_FIT_SCALED 0
+#define DZ_FIT_AFFINE 1
+#define DZ_FIT_NF4 2
+/* Takes over the fitted forms above at load: `offsets_host` is f32
+ * [rows x cols/64] for DZ_FIT_AFFINE and NULL otherwise (DZ_INVALID_REQUEST).
+ * The fitting stays with the caller (the reference fits on the CPU at load).
+ * Where each form runs:
+ *  - dz_dequant / dz_dequant_rows decode every form as quantized_rows.rs:89-110
+ *    append does: y = f32(value_code) * scale, then + offset (two roundings);
+ *  - the grouped products (dz_linear, dz_linear_pair, dz_linear_noalloc in
+ *    W4A8/W4A4 mode) take DZ_FIT_SCALED and DZ_FIT_AFFINE, folding each group
+ *    as int8.rs:524-571 does:
+ *      acc = fma(f32(dot), sw * sx, acc);
+ *      acc = fma(offset, sx * f32(sum of the row's 64 activation codes), acc)
+ *  - the W4A16 products (dz_linear in W4A16 mode, dz_linear_f16) take
+ *    DZ_FIT_SCALED;
+ *  - the remaining products (dz_mlp_requant, dz_linear_q8, dz_project,
+ *    dz_readout, dz_linear_records) take no fitted weight.
+ * A product refuses a form it does not take with DZ_INVALID_PARAMETERS.
+ * cols % 64 == 0 (the wire layout's); a zero or non-finite scale or a
+ * non-finite offset is DZ_INVALID_CHECKPOINT; an unknown form
+ * DZ_INVALID_PARAMETERS. Synchronous. */
+int32_t dz_weight_upload_fitted(dz_ctx *ctx, const void *packed_host, size_t bytes, size_t rows, size_t cols,
+                                int32_t form, const float *offsets_host, dz_weight **out);
 /* Takes over int8.rs:51-152 Matrix::from_bf16_optimized (plain mode; bits 4
  * or 8, group 64, f32 scales; any cols, zero padded) and, with group == 32
  * and bits == 4, the group-32/f16 quantizer. `values_dev` is [rows x cols] of
@@ -192,7 +227,9 @@ int32_t dz_linear(dz_ctx *ctx, const dz_weight *w, const void *x_dev, int32_t x_
  * codes, scales and non-finite flag in a static 16 MiB device array (one per
  * GPU, held until the process ends), so 256 + round256(m*G*64) + m*G*4 bytes
  * (G = ceil(cols/64)) must fit 16 MiB: up to 3,855 rows at cols 4096, 6,168 at
- * 2560; more is DZ_RESOURCE_LIMIT with nothing launched. Every call on a GPU
+ * 2560; affine fitted weights add round256(m*G*4) + m*G*4 bytes for the code
+ * sums (3,640 rows at cols 4096); more is DZ_RESOURCE_LIMIT with nothing
+ * launched. Every call on a GPU
  * shares that array: calls that overlap on one GPU (other streams, other
  * contexts, concurrent graph replays) race; serialise them. */
 int32_t dz_linear_noalloc(dz_ctx *ctx, const dz_weight *w, const void *x_dev, int32_t x_dtype, size_t m,

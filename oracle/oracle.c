@@ -329,6 +329,321 @@ void or_grouped_gemm(const int8_t *qx, const float *sx, size_t m, const int8_t *
     }
 }
 
+/* int8.rs:259-287 (scalar) and :524-585 (AVX2 rows) with the affine offset
+ * term of a fitted matrix: per group, after the scale term,
+ *   fused:  acc = fmaf(offset, sx * f32(sum q), acc)         int8.rs:566-571
+ *   scalar: acc = acc + offset * (sx * f32(sum q))            int8.rs:279-282
+ * where sum q is the exact sum of the row's group codes (int8.rs:191-193). */
+void or_grouped_gemm_affine(const int8_t *qx, const float *sx, size_t m, const int8_t *qw, const float *sw,
+                            const float *offsets, size_t n, size_t k, int fused, float *y) {
+    size_t groups = (k + 63) / 64;
+    for (size_t r = 0; r < m; r++) {
+        for (size_t c = 0; c < n; c++) {
+            float acc = 0.0f;
+            for (size_t g = 0; g < groups; g++) {
+                const int8_t *a = qx + (r * groups + g) * 64;
+                const int8_t *b = qw + (c * groups + g) * 64;
+                int32_t dot = 0, sum = 0;
+                for (int i = 0; i < 64; i++) {
+                    dot += (int32_t)a[i] * (int32_t)b[i];
+                    sum += a[i];
+                }
+                const float sxv = sx[r * groups + g], off = offsets[c * groups + g];
+                if (fused) {
+                    acc = fmaf((float)dot, sw[c * groups + g] * sxv, acc);
+                    acc = fmaf(off, sxv * (float)sum, acc);
+                } else {
+                    acc = acc + (float)dot * (sxv * sw[c * groups + g]);
+                    acc = acc + off * (sxv * (float)sum);
+                }
+            }
+            y[r * n + c] = acc;
+        }
+    }
+}
+
+/* ---- fitted Q4 quantizers (quantization.rs) -------------------------------
+ * The AVX2 forms keep eight lane sums (lane l takes elements l, l+8, ... of
+ * the whole 8-wide part), each a separate multiply and add, then add the
+ * lanes in order to a -0.0 start (Rust's f32 Sum) and that to the scalar
+ * sums of the tail. */
+/* f32::clamp(-8, 7), which passes NaN through (as do the AVX2 min/max with
+ * the rounded value second), and Rust's saturating `as i8`, NaN -> 0. */
+static float clamp_code(float v) { return v < -8.0f ? -8.0f : (v > 7.0f ? 7.0f : v); }
+static int8_t code_i8(float v) { return isnan(v) ? 0 : (int8_t)v; }
+
+static float f32_sum_lanes(const float *lanes) {
+    float s = -0.0f;
+    for (int l = 0; l < 8; l++) s += lanes[l];
+    return s;
+}
+
+/* quantization.rs:73-129 stats: (sum v q, sum q q, sum (v - q s)^2). */
+static void mse_stats(const float *x, size_t n, float scale, int avx2, float out[3]) {
+    const float inverse = 1.0f / scale;
+    size_t end = avx2 ? n / 8 * 8 : 0;
+    float lanes[3][8] = {{0}};
+    for (size_t i = 0; i < end; i++) {
+        const float q = clamp_code(rintf(x[i] * inverse));
+        const float e = x[i] - q * scale;
+        lanes[0][i % 8] += x[i] * q;
+        lanes[1][i % 8] += q * q;
+        lanes[2][i % 8] += e * e;
+    }
+    float t[3] = {0.0f, 0.0f, 0.0f};
+    for (size_t i = end; i < n; i++) {
+        const float q = clamp_code(rintf(x[i] * inverse));
+        const float e = x[i] - q * scale;
+        t[0] += x[i] * q;
+        t[1] += q * q;
+        t[2] += e * e;
+    }
+    for (int j = 0; j < 3; j++) out[j] = avx2 ? f32_sum_lanes(lanes[j]) + t[j] : t[j];
+}
+
+/* quantization.rs:25-71 mse: the symmetric scale, then alternating least
+ * squares from six starts (signs -1, 1 x ratios 0.8, 0.95, 1.1 of 1/7), four
+ * steps each, keeping the codes of the lowest error. Codes in [-8, 7]; the
+ * returned scale may be negative. */
+float or_fit_mse(const float *x, size_t n, int avx2, int8_t *out) {
+    float maximum = 0.0f;
+    for (size_t i = 0; i < n; i++) maximum = fmaxf(maximum, fabsf(x[i]));
+    const float baseline = or_group_scale(x, n, 4);
+    or_group_codes(x, n, baseline, 4, out);
+    if (maximum == 0.0f) return baseline;
+    float normalized[64];
+    for (size_t i = 0; i < n; i++) normalized[i] = x[i] / maximum;
+    float best_error = 0.0f;
+    {
+        const float ratio = baseline / maximum;
+        for (size_t i = 0; i < n; i++) {
+            const float e = normalized[i] - (float)out[i] * ratio;
+            best_error += e * e;
+        }
+    }
+    float best = baseline;
+    const float signs[2] = {-1.0f, 1.0f}, ratios[3] = {0.8f, 0.95f, 1.1f};
+    for (int si = 0; si < 2; si++) {
+        for (int ri = 0; ri < 3; ri++) {
+            float scale = signs[si] * ratios[ri] / 7.0f;
+            for (int step = 0; step < 4; step++) {
+                float st[3];
+                mse_stats(normalized, n, scale, avx2, st);
+                if (st[2] < best_error) {
+                    best_error = st[2];
+                    best = scale * maximum;
+                    const float inverse = 1.0f / scale;
+                    for (size_t i = 0; i < n; i++)
+                        out[i] = code_i8(clamp_code(rintf(normalized[i] * inverse)));
+                }
+                if (st[1] == 0.0f) break;
+                const float next = st[0] / st[1];
+                if (!isfinite(next) || fabsf(next) < FLT_MIN || next == scale) break;
+                scale = next;
+            }
+        }
+    }
+    return best;
+}
+
+/* quantization.rs:202-262 affine_stats: (sum v q, sum q q, sum e^2, sum q),
+ * e = v - (q s + o). */
+static void affine_stats(const float *x, size_t n, float scale, float offset, int avx2, float out[4]) {
+    const float inverse = 1.0f / scale;
+    size_t end = avx2 ? n / 8 * 8 : 0;
+    float lanes[4][8] = {{0}};
+    for (size_t i = 0; i < end; i++) {
+        const float q = clamp_code(rintf((x[i] - offset) * inverse));
+        const float e = x[i] - (q * scale + offset);
+        lanes[0][i % 8] += x[i] * q;
+        lanes[1][i % 8] += q * q;
+        lanes[2][i % 8] += e * e;
+        lanes[3][i % 8] += q;
+    }
+    float t[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (size_t i = end; i < n; i++) {
+        const float q = clamp_code(rintf((x[i] - offset) * inverse));
+        const float e = x[i] - (q * scale + offset);
+        t[0] += x[i] * q;
+        t[1] += q * q;
+        t[2] += e * e;
+        t[3] += q;
+    }
+    for (int j = 0; j < 4; j++) out[j] = avx2 ? t[j] + f32_sum_lanes(lanes[j]) : t[j];
+}
+
+/* quantization.rs:147-200 affine: values normalized by the largest magnitude,
+ * three starts (ratios 0.8, 1, 1.2 of the range / 15) with the offset at the
+ * range's centre plus half a step, four least-squares steps each, keeping the
+ * lowest error. A zero group gives (FLT_MIN, 0) and zero codes; a constant one
+ * (FLT_MIN, x[0]). Codes in [-8, 7]; scale > 0. */
+void or_fit_affine(const float *x, size_t n, int avx2, int8_t *out, float *scale_out, float *offset_out) {
+    float maximum = 0.0f;
+    for (size_t i = 0; i < n; i++) maximum = fmaxf(maximum, fabsf(x[i]));
+    if (maximum == 0.0f) {
+        memset(out, 0, n);
+        *scale_out = FLT_MIN;
+        *offset_out = 0.0f;
+        return;
+    }
+    float v[64];
+    for (size_t i = 0; i < n; i++) v[i] = x[i] / maximum;
+    float low = INFINITY, high = -INFINITY;
+    for (size_t i = 0; i < n; i++) {
+        low = fminf(low, v[i]);
+        high = fmaxf(high, v[i]);
+    }
+    if (low == high) {
+        memset(out, 0, n);
+        *scale_out = FLT_MIN;
+        *offset_out = x[0];
+        return;
+    }
+    float total = -0.0f;
+    for (size_t i = 0; i < n; i++) total += v[i];
+    const float mean = total / (float)n;
+    float best_error = INFINITY, best_s = 0.0f, best_o = 0.0f;
+    const float ratios[3] = {0.8f, 1.0f, 1.2f};
+    for (int ri = 0; ri < 3; ri++) {
+        float scale = (high - low) / 15.0f * ratios[ri];
+        float offset = (high + low + scale) * 0.5f;
+        for (int step = 0; step < 4; step++) {
+            float st[4];
+            affine_stats(v, n, scale, offset, avx2, st);
+            if (st[2] < best_error) {
+                best_error = st[2];
+                best_s = scale * maximum;
+                best_o = offset * maximum;
+                const float inverse = 1.0f / scale;
+                for (size_t i = 0; i < n; i++)
+                    out[i] = code_i8(clamp_code(rintf((v[i] - offset) * inverse)));
+            }
+            const float mean_q = st[3] / (float)n;
+            const float denominator = st[1] - st[3] * mean_q;
+            if (denominator <= 0.0f) break;
+            const float next = (st[0] - st[3] * mean) / denominator;
+            if (!isfinite(next) || next <= 0.0f) break;
+            const float next_offset = mean - next * mean_q;
+            if (next == scale && next_offset == offset) break;
+            scale = next;
+            offset = next_offset;
+        }
+    }
+    *scale_out = best_s;
+    *offset_out = best_o;
+}
+
+/* quantization.rs:3-20: the NF4 codebook as the reference writes it. */
+static const float kNf4[16] = {-1.0f,        -0.6961928f,  -0.52507305f, -0.3949175f,
+                               -0.28444138f, -0.18477343f, -0.091050036f, 0.0f,
+                               0.0795803f,   0.1609302f,   0.2461123f,   0.33791524f,
+                               0.44070983f,  0.562617f,    0.72295684f,  1.0f};
+
+float or_nf4_value(int index) { return kNf4[index & 15]; }
+
+/* quantization.rs:131-145 nf4_code: binary search over the midpoints. */
+static int nf4_code(float value) {
+    int low = 0, high = 15;
+    while (low < high) {
+        const int middle = (low + high) / 2;
+        if (value > (kNf4[middle] + kNf4[middle + 1]) * 0.5f)
+            low = middle + 1;
+        else
+            high = middle;
+    }
+    return low;
+}
+
+/* quantization.rs:260-302 nf4: normalized by the largest magnitude, three
+ * starts (0.85, 1, 1.15), four least-squares steps each, the lowest error
+ * kept. A zero group gives codes -1 (NF4 zero) and FLT_MIN. */
+float or_fit_nf4(const float *x, size_t n, int8_t *out) {
+    float maximum = 0.0f;
+    for (size_t i = 0; i < n; i++) maximum = fmaxf(maximum, fabsf(x[i]));
+    if (maximum == 0.0f) {
+        memset(out, 0xff, n);
+        return FLT_MIN;
+    }
+    float v[64];
+    for (size_t i = 0; i < n; i++) v[i] = x[i] / maximum;
+    float best_error = INFINITY, best_scale = maximum;
+    const float initials[3] = {0.85f, 1.0f, 1.15f};
+    for (int ii = 0; ii < 3; ii++) {
+        float scale = initials[ii];
+        for (int step = 0; step < 4; step++) {
+            int8_t codes[64];
+            float numerator = 0.0f, denominator = 0.0f, error = 0.0f;
+            for (size_t i = 0; i < n; i++) {
+                const int index = nf4_code(v[i] / scale);
+                codes[i] = (int8_t)(index - 8);
+                const float q = kNf4[index];
+                numerator += v[i] * q;
+                denominator += q * q;
+                const float e = v[i] - scale * q;
+                error += e * e;
+            }
+            if (error < best_error) {
+                best_error = error;
+                best_scale = scale * maximum;
+                memcpy(out, codes, n);
+            }
+            if (denominator == 0.0f) break;
+            const float next = numerator / denominator;
+            if (next == scale || next <= 0.0f) break;
+            scale = next;
+        }
+    }
+    return best_scale;
+}
+
+/* quantized_rows.rs:89-110 append for a Q4 row of `cols` codes: value =
+ * f32(code) or NF4[code + 8], times the group's scale, then plus its offset
+ * (offsets may be NULL), each step rounded to f32. */
+void or_rows_decode(const int8_t *codes, const float *scales, const float *offsets, int nf4, size_t rows,
+                    size_t cols, float *y) {
+    const size_t groups = cols / 64;
+    for (size_t r = 0; r < rows; r++)
+        for (size_t i = 0; i < cols; i++) {
+            const int8_t c = codes[r * cols + i];
+            const float value = nf4 ? kNf4[(c + 8) & 15] : (float)c;
+            float out = value * scales[r * groups + i / 64];
+            if (offsets) out = out + offsets[r * groups + i / 64];
+            y[r * cols + i] = out;
+        }
+}
+
+/* int8.rs:86-117 from_bf16_optimized with `optimized` (mode 1: mse) or
+ * `affine` (mode 2), or quantized_rows.rs:56-66 with `nf4` (mode 3; the codes
+ * index the codebook): BF16 [n x k] -> codes [n x G*64] (tail zero), scales
+ * [n x G], offsets [n x G] (mode 2; zero otherwise). Returns 0, -2 on a
+ * non-finite weight. */
+int or_weight_quantize_fitted(const uint16_t *bf16, size_t n, size_t k, int mode, int avx2, int8_t *codes,
+                              float *scales, float *offsets) {
+    const size_t groups = (k + 63) / 64;
+    for (size_t c = 0; c < n; c++) {
+        for (size_t g = 0; g < groups; g++) {
+            const size_t count = k - g * 64 < 64 ? k - g * 64 : 64;
+            float values[64];
+            for (size_t i = 0; i < count; i++) {
+                values[i] = or_bf16_to_f32(bf16[c * k + g * 64 + i]);
+                if (!isfinite(values[i])) return -2;
+            }
+            int8_t *out = codes + (c * groups + g) * 64;
+            memset(out, 0, 64);
+            float s, o = 0.0f;
+            if (mode == 2)
+                or_fit_affine(values, count, avx2, out, &s, &o);
+            else if (mode == 3)
+                s = or_fit_nf4(values, count, out);
+            else
+                s = or_fit_mse(values, count, avx2, out);
+            scales[c * groups + g] = s;
+            offsets[c * groups + g] = o;
+        }
+    }
+    return 0;
+}
+
 void or_matrix_apply(const float *x, size_t m, const int8_t *qw, const float *sw, size_t n,
                      size_t k, int act_bits, int fused, float *y) {
     for (size_t i = 0; i < m * k; i++) {
@@ -399,6 +714,7 @@ struct panel_job {
     int bits;
     const int8_t *qx;
     const float *sx;
+    const float *poffsets; /* panel layout like pscales, NULL for none */
     float *y;
     size_t tiles;
     size_t next; /* atomic tile counter */
@@ -441,6 +757,14 @@ __attribute__((target("avx2,fma"))) static void panel_rows(const struct panel_jo
         for (size_t r = 0; r < rows; r++) {
             __m256 s = _mm256_mul_ps(sw, _mm256_set1_ps(j->sx[(first + r) * groups + g]));
             sums[r] = _mm256_fmadd_ps(_mm256_cvtepi32_ps(acc[r]), s, sums[r]);
+            if (j->poffsets) { /* int8.rs:566-571, with the code sums of int8.rs:197-199 */
+                const int8_t *q = j->qx + ((first + r) * groups + g) * 64;
+                int32_t total = 0;
+                for (int i = 0; i < 64; i++) total += q[i];
+                __m256 offset = _mm256_loadu_ps(j->poffsets + (panel * groups + g) * 8);
+                const float sxs = j->sx[(first + r) * groups + g] * (float)total;
+                sums[r] = _mm256_fmadd_ps(offset, _mm256_set1_ps(sxs), sums[r]);
+            }
         }
     }
     for (size_t r = 0; r < rows; r++) {
@@ -483,11 +807,11 @@ __attribute__((target("avx2,fma"))) static void *panel_worker(void *arg) {
 }
 #endif
 
-int or_panel_apply_avx2(const uint8_t *data, const float *pscales, size_t n, size_t k, int bits,
-                        const int8_t *qx, const float *sx, size_t m, int threads, float *y) {
+int or_panel_apply_avx2(const uint8_t *data, const float *pscales, const float *poffsets, size_t n, size_t k,
+                        int bits, const int8_t *qx, const float *sx, size_t m, int threads, float *y) {
 #if defined(__x86_64__)
     if (!or_has_avx2()) return -1;
-    struct panel_job job = {data, pscales, n, k, m, bits, qx, sx, y, (n + 31) / 32, 0};
+    struct panel_job job = {data, pscales, n, k, m, bits, qx, sx, poffsets, y, (n + 31) / 32, 0};
     if (threads <= 1) {
         panel_worker(&job);
         return 0;
@@ -495,7 +819,7 @@ int or_panel_apply_avx2(const uint8_t *data, const float *pscales, size_t n, siz
     run_workers(panel_worker, &job, threads);
     return 0;
 #else
-    (void)data; (void)pscales; (void)n; (void)k; (void)bits; (void)qx; (void)sx; (void)m;
+    (void)data; (void)pscales; (void)poffsets; (void)n; (void)k; (void)bits; (void)qx; (void)sx; (void)m;
     (void)threads; (void)y;
     return -1;
 #endif

@@ -74,6 +74,23 @@ void or_act_quantize(const float *x, size_t m, size_t k, int bits, int8_t *q, fl
 void or_grouped_gemm(const int8_t *qx, const float *sx, size_t m,
                      const int8_t *qw, const float *sw, size_t n, size_t k,
                      int fused, float *y);
+/* The same with the affine offset term of a fitted matrix (offsets [n x G]):
+ * fused int8.rs:566-571 acc = fmaf(off, sx*f32(sum q), acc); scalar
+ * :279-282 acc = acc + off*(sx*f32(sum q)); sum q the row's group codes. */
+void or_grouped_gemm_affine(const int8_t *qx, const float *sx, size_t m, const int8_t *qw, const float *sw,
+                            const float *offsets, size_t n, size_t k, int fused, float *y);
+/* ---- fitted Q4 quantizers (quantization.rs; avx2 selects the 8-lane sum order) ----
+ * :25-71 mse over one group (n <= 64): codes [-8, 7], returns the scale (may be < 0).
+ * :147-200 affine: codes [-8, 7], scale > 0 and offset.
+ * int8.rs:86-117 from_bf16_optimized, mode 1 mse / 2 affine; offsets zero for mse. */
+float or_fit_mse(const float *x, size_t n, int avx2, int8_t *out);
+void or_fit_affine(const float *x, size_t n, int avx2, int8_t *out, float *scale, float *offset);
+float or_fit_nf4(const float *x, size_t n, int8_t *out);
+float or_nf4_value(int index);
+void or_rows_decode(const int8_t *codes, const float *scales, const float *offsets, int nf4, size_t rows,
+                    size_t cols, float *y);
+int or_weight_quantize_fitted(const uint16_t *bf16, size_t n, size_t k, int mode, int avx2, int8_t *codes,
+                              float *scales, float *offsets);
 /* int8.rs:166-176 Matrix::apply: finiteness check + prepare + product. */
 void or_matrix_apply(const float *x, size_t m, const int8_t *qw, const float *sw,
                      size_t n, size_t k, int act_bits, int fused, float *y);
@@ -84,10 +101,11 @@ void or_matrix_apply(const float *x, size_t m, const int8_t *qw, const float *sw
 size_t or_panel_bytes(size_t n, size_t k, int bits);
 void or_panel_pack(const int8_t *codes, const float *scales, size_t n, size_t k,
                    int bits, uint8_t *data, float *pscales);
-/* int8.rs:229-256 + :404-585, threads over ceil(n/32) tiles. Returns 0, or -1
- * when AVX2 is not available on this CPU. */
-int or_panel_apply_avx2(const uint8_t *data, const float *pscales, size_t n, size_t k,
-                        int bits, const int8_t *qx, const float *sx, size_t m,
+/* int8.rs:229-256 + :404-585, threads over ceil(n/32) tiles; poffsets (the
+ * affine offsets in the pscales layout, or NULL) adds int8.rs:566-571. Returns
+ * 0, or -1 when AVX2 is not available on this CPU. */
+int or_panel_apply_avx2(const uint8_t *data, const float *pscales, const float *poffsets, size_t n,
+                        size_t k, int bits, const int8_t *qx, const float *sx, size_t m,
                         int threads, float *y);
 int or_has_avx2(void);
 

@@ -59,10 +59,17 @@ def _declare(L):
         "or_weight_quantize": (I, [P, SZ, SZ, I, P, P]),
         "or_act_quantize": (None, [P, SZ, SZ, I, P, P]),
         "or_grouped_gemm": (None, [P, P, SZ, P, P, SZ, SZ, I, P]),
+        "or_grouped_gemm_affine": (None, [P, P, SZ, P, P, P, SZ, SZ, I, P]),
+        "or_fit_mse": (F, [P, SZ, I, P]),
+        "or_fit_affine": (None, [P, SZ, I, P, P, P]),
+        "or_weight_quantize_fitted": (I, [P, SZ, SZ, I, I, P, P, P]),
+        "or_fit_nf4": (F, [P, SZ, P]),
+        "or_nf4_value": (F, [I]),
+        "or_rows_decode": (None, [P, P, P, I, SZ, SZ, P]),
         "or_matrix_apply": (None, [P, SZ, P, P, SZ, SZ, I, I, P]),
         "or_panel_bytes": (SZ, [SZ, SZ, I]),
         "or_panel_pack": (None, [P, P, SZ, SZ, I, P, P]),
-        "or_panel_apply_avx2": (I, [P, P, SZ, SZ, I, P, P, SZ, I, P]),
+        "or_panel_apply_avx2": (I, [P, P, P, SZ, SZ, I, P, P, SZ, I, P]),
         "or_has_avx2": (I, []),
         "or_i8_quantize_rows": (None, [P, SZ, SZ, P, P, P]),
         "or_i8_gemm": (None, [P, P, SZ, P, P, SZ, SZ, I, P, P]),
@@ -250,6 +257,83 @@ def grouped_gemm(qx, sx, m, qw, sw, n, k, fused=True) -> np.ndarray:
     return y
 
 
+def grouped_gemm_affine(qx, sx, m, qw, sw, offsets, n, k, fused=True) -> np.ndarray:
+    """or_grouped_gemm_affine: int8.rs:524-571 (fused) / :259-287 (scalar) with the offset term."""
+    y = np.empty((m, n), np.float32)
+    if m and n:
+        lib().or_grouped_gemm_affine(_p(_c(qx, np.int8)), _p(_c(sx, np.float32)), m, _p(_c(qw, np.int8)),
+                                     _p(_c(sw, np.float32)), _p(_c(offsets, np.float32)), n, k,
+                                     1 if fused else 0, _p(y))
+    return y
+
+
+def fit_mse(x, avx2=True):
+    """or_fit_mse: quantization.rs:25-71 over one group -> (codes, scale)."""
+    x = _c(x, np.float32).reshape(-1)
+    out = np.zeros(x.size, np.int8)
+    s = lib().or_fit_mse(_p(x), x.size, 1 if avx2 else 0, _p(out))
+    return out, np.float32(s)
+
+
+def fit_affine(x, avx2=True):
+    """or_fit_affine: quantization.rs:147-200 over one group -> (codes, scale, offset)."""
+    x = _c(x, np.float32).reshape(-1)
+    out = np.zeros(x.size, np.int8)
+    s, o = np.zeros(1, np.float32), np.zeros(1, np.float32)
+    lib().or_fit_affine(_p(x), x.size, 1 if avx2 else 0, _p(out), _p(s), _p(o))
+    return out, s[0], o[0]
+
+
+def fit_nf4(x):
+    """or_fit_nf4: quantization.rs:260-302 over one group -> (codes, scale)."""
+    x = _c(x, np.float32).reshape(-1)
+    out = np.zeros(x.size, np.int8)
+    s = lib().or_fit_nf4(_p(x), x.size, _p(out))
+    return out, np.float32(s)
+
+
+def nf4_table() -> np.ndarray:
+    """quantization.rs:3-20, as the oracle holds it."""
+    return np.array([lib().or_nf4_value(i) for i in range(16)], np.float32)
+
+
+def rows_decode(codes, scales, offsets, nf4, rows, cols) -> np.ndarray:
+    """or_rows_decode: quantized_rows.rs:89-110 append over Q4 rows."""
+    y = np.empty((rows, cols), np.float32)
+    off = None if offsets is None else _p(_c(offsets, np.float32))
+    lib().or_rows_decode(_p(_c(codes, np.int8)), _p(_c(scales, np.float32)), off, 1 if nf4 else 0, rows, cols,
+                         _p(y))
+    return y
+
+
+def weight_quantize_fitted(bf16, n, k, mode, avx2=True):
+    """or_weight_quantize_fitted: int8.rs:86-117, mode "mse" or "affine", or
+    quantized_rows.rs:56-66 "nf4" -> (codes [n x G*64], scales [n x G],
+    offsets [n x G])."""
+    bf16 = _c(bf16, np.uint16).reshape(-1)
+    g = (k + 63) // 64
+    codes = np.empty((n, g * 64), np.int8)
+    scales = np.empty((n, g), np.float32)
+    offsets = np.empty((n, g), np.float32)
+    rc = lib().or_weight_quantize_fitted(_p(bf16), n, k, {"mse": 1, "affine": 2, "nf4": 3}[mode], 1 if avx2 else 0,
+                                         _p(codes), _p(scales), _p(offsets))
+    if rc:
+        raise OracleError("non-finite INT8 weight")
+    return codes, scales, offsets
+
+
+def pack_wire_codes(codes, scales, n, k):
+    """A fitted Q4 matrix (codes in [-8, 7], any scales) in the g64/f32 wire
+    layout of packed.rs:3-56: per 64-run, (code + 8) nibbles, low nibble the
+    even k, then the f32 LE scale. k % 64 == 0."""
+    g = k // 64
+    c = (np.asarray(codes, np.int16).reshape(n, g, 64) + 8).astype(np.uint8)
+    wire = np.empty((n, g, 36), np.uint8)
+    wire[..., :32] = c[..., 0::2] | (c[..., 1::2] << 4)
+    wire[..., 32:] = np.asarray(scales, np.float32).reshape(n, g, 1).view(np.uint8)
+    return wire.reshape(-1)
+
+
 def matrix_apply(x, m, qw, sw, n, k, act_bits=8, fused=True) -> np.ndarray:
     """or_matrix_apply: int8.rs:166-176."""
     x = _c(x, np.float32).reshape(-1)
@@ -274,10 +358,13 @@ def has_avx2() -> bool:
     return bool(lib().or_has_avx2())
 
 
-def panel_apply_avx2(data, ps, n, k, bits, qx, sx, m, threads=1) -> np.ndarray:
-    """or_panel_apply_avx2: int8.rs:229-256 + :404-585."""
+def panel_apply_avx2(data, ps, n, k, bits, qx, sx, m, threads=1, poffsets=None) -> np.ndarray:
+    """or_panel_apply_avx2: int8.rs:229-256 + :404-585; poffsets (affine offsets
+    in the panel scale layout, e.g. panel_pack(codes, offsets, ...)[1]) adds
+    int8.rs:566-571."""
     y = np.empty((m, n), np.float32)
-    rc = lib().or_panel_apply_avx2(_p(data), _p(ps), n, k, bits, _p(_c(qx, np.int8)),
+    off = None if poffsets is None else _p(_c(poffsets, np.float32))
+    rc = lib().or_panel_apply_avx2(_p(data), _p(ps), off, n, k, bits, _p(_c(qx, np.int8)),
                                    _p(_c(sx, np.float32)), m, threads, _p(y))
     if rc:
         raise OracleError("AVX2/FMA unavailable")

@@ -586,3 +586,202 @@ def test_attention_gqa_maps_heads_to_kv_heads(oracle):
     assert np.allclose(zero[0, 0], v[:, :ad].mean(axis=0), rtol=1e-5, atol=1e-6)
     perm = rng.permutation(nk)
     assert np.allclose(oracle.attention_gqa(q, k[perm], v[perm], ah, akv, ad, 0.5), out, rtol=1e-5, atol=1e-6)
+
+
+# ---- fitted Q4 weights: quantization.rs fits and the affine fold -------------
+
+def _fit_modes(oracle):
+    return [False, True] if oracle.has_avx2() else [False]
+
+
+def test_affine_fit_preserves_constants_and_offset_grids(oracle):
+    """quantization.rs:306-325: constant groups reconstruct exactly, and values
+    on a 16-level grid with an offset reconstruct to 1e-5."""
+    for avx2 in _fit_modes(oracle):
+        for n in (1, 7, 16, 63, 64):
+            for v in (0.0, -3.25, 12.0):
+                codes, s, b = oracle.fit_affine(np.full(n, v, np.float32), avx2)
+                assert (codes.astype(np.float32) * s + b == np.float32(v)).all(), (avx2, n, v)
+            values = np.array([4.0 + (i * 15 // max(n - 1, 1)) * 0.25 for i in range(n)], np.float32)
+            codes, s, b = oracle.fit_affine(values, avx2)
+            assert s > 0
+            assert (codes >= -8).all() and (codes <= 7).all()
+            assert np.all(np.abs(values - (codes.astype(np.float32) * s + b)) < 1e-5), (avx2, n)
+
+
+def test_mse_fit_reduces_error_and_handles_tails(oracle):
+    """quantization.rs:327-356: the fit never reconstructs worse than the
+    symmetric Q4 quantizer (int8.rs group_scale_bits/pack_bits), keeps codes in
+    [-8, 7] and maps a zero group to zero codes and a finite scale."""
+    for avx2 in _fit_modes(oracle):
+        for n in (1, 7, 8, 31, 63, 64):
+            for seed in range(32):
+                i = np.arange(n)
+                values = (((i * 137 + seed * 19) % 101) - 50.0).astype(np.float32)
+                values[0] *= np.float32(3.7)
+                s = oracle.group_scale(values, 4)
+                base = oracle.group_codes(values, s, 4)
+                codes, fit = oracle.fit_mse(values, avx2)
+
+                def error(q, scale):
+                    return float(((values.astype(np.float64) - q.astype(np.float64) * float(scale)) ** 2).sum())
+
+                assert error(codes, fit) <= error(base, s) + 1e-5, (avx2, n, seed)
+                assert (codes >= -8).all() and (codes <= 7).all()
+        codes, s = oracle.fit_mse(np.zeros(64, np.float32), avx2)
+        assert np.isfinite(s) and (codes == 0).all()
+
+
+def _dequantized_dots(codes, scales, offsets, q, sx, m, n, k):
+    """f64 sum over k of (code * scale + offset) * q * sx, int8.rs:612-637."""
+    g = (k + 63) // 64
+    w = (codes.astype(np.float64).reshape(n, g, 64) * scales.astype(np.float64)[:, :, None]
+         + offsets.astype(np.float64)[:, :, None])
+    a = q.astype(np.float64).reshape(m, g, 64) * sx.astype(np.float64)[:, :, None]
+    wk = w.reshape(n, g * 64)[:, :k]
+    ak = a.reshape(m, g * 64)[:, :k]
+    return ak @ wk.T
+
+
+def test_affine_offsets_match_independent_dequantized_dots(oracle):
+    """int8.rs:591-642: k = 65, n = 9; both fold orders within
+    1e-3 + |expected| * 4e-6 of the float64 dequantized product, and the fused
+    order bit-for-bit equal to the AVX2 panel kernel with its offset term."""
+    k, n = 65, 9
+    i = np.arange(k * n)
+    vals = np.where(i // k % 3 == 0, (i // k) + 3.0, (((i * 31) % 97) - 48.0) / 17.0 + 9.0)
+    bf16 = half_bf16(vals, oracle)
+    for avx2 in _fit_modes(oracle):
+        codes, scales, offsets = oracle.weight_quantize_fitted(bf16, n, k, "affine", avx2)
+        assert (scales > 0).all() and np.isfinite(offsets).all()
+        assert (codes.reshape(n, 2, 64)[:, 1, 1:] == 0).all()  # the group tail past k
+        for m in (1, 15, 16, 17):
+            x = ((((np.arange(m * k) * 13) % 255) - 127.0) / 17.0 + 3.0).astype(np.float32)
+            q, sx = oracle.act_quantize(x, m, k)
+            expected = _dequantized_dots(codes, scales, offsets, q, sx, m, n, k)
+            for fused in (True, False):
+                got = oracle.grouped_gemm_affine(q, sx, m, codes, scales, offsets, n, k, fused)
+                assert np.all(np.abs(got - expected) < 1e-3 + np.abs(expected) * 4e-6), (avx2, m, fused)
+            # the offset term is live: without it the product is far off
+            plain = oracle.grouped_gemm(q, sx, m, codes, scales, n, k)
+            assert np.abs(plain - expected).max() > 1.0
+            if oracle.has_avx2():
+                data, ps = oracle.panel_pack(codes, scales, n, k, 4)
+                _, po = oracle.panel_pack(codes, offsets, n, k, 4)
+                fused = oracle.grouped_gemm_affine(q, sx, m, codes, scales, offsets, n, k, True)
+                for threads in (1, 3):
+                    avx = oracle.panel_apply_avx2(data, ps, n, k, 4, q, sx, m, threads, poffsets=po)
+                    assert np.array_equal(avx.view(np.uint32), fused.view(np.uint32)), (m, threads)
+
+
+def test_fitted_signed_scales_and_full_code_range(oracle):
+    """int8.rs:645-676: the MSE fit gives negative scales and -8 codes; the
+    scalar and fused folds agree within 1e-4 + |a| * 2e-6; the fused fold is
+    bit-for-bit the AVX2 panel kernel and within tolerance of float64."""
+    for k, n in ((65, 9), (128, 33)):
+        i = np.arange(k * n)
+        bf16 = half_bf16((((i * 37) % 251) - 125.0) / 31.0, oracle)
+        codes, scales, offsets = oracle.weight_quantize_fitted(bf16, n, k, "mse", True)
+        assert (scales < 0).any()
+        assert (codes == -8).any()
+        assert (offsets == 0).all()
+        for m in (1, 15, 16, 17):
+            x = ((((np.arange(m * k) * 13) % 255) - 127.0) / 17.0).astype(np.float32)
+            q, sx = oracle.act_quantize(x, m, k)
+            scalar = oracle.grouped_gemm(q, sx, m, codes, scales, n, k, fused=False)
+            simd = oracle.grouped_gemm(q, sx, m, codes, scales, n, k, fused=True)
+            assert np.all(np.abs(scalar - simd) < 1e-4 + np.abs(scalar) * 2e-6), (k, m)
+            expected = _dequantized_dots(codes, scales, offsets, q, sx, m, n, k)
+            assert np.all(np.abs(simd - expected) < 1e-3 + np.abs(expected) * 4e-6)
+            if oracle.has_avx2():
+                data, ps = oracle.panel_pack(codes, scales, n, k, 4)
+                avx = oracle.panel_apply_avx2(data, ps, n, k, 4, q, sx, m, 1)
+                assert np.array_equal(avx.view(np.uint32), simd.view(np.uint32)), (k, m)
+
+
+def test_fitted_weights_reject_nonfinite_and_wire_pack_round_trips(oracle):
+    """int8.rs:98-101 refuses non-finite weights; the wire packing of fitted
+    codes decodes (packed.rs:59-73) to code * scale, signed scales included."""
+    with pytest.raises(oracle.OracleError):
+        oracle.weight_quantize_fitted(np.array([0x7f80] + [0] * 63, np.uint16), 1, 64, "mse")
+    rng = np.random.default_rng(3)
+    n, k = 5, 128
+    codes = rng.integers(-8, 8, (n, k)).astype(np.int8)
+    scales = (rng.standard_normal((n, k // 64)) * 0.1).astype(np.float32)
+    wire = oracle.pack_wire_codes(codes, scales, n, k)
+    assert wire.size == n * (k // 64) * 36
+    # packed.rs's decoder takes positive scales only: decode the same codes
+    # with |scale| and check the signed scale bytes separately
+    positive = oracle.pack_wire_codes(codes, np.abs(scales), n, k)
+    got = oracle.unpack_g64(positive, 4).reshape(n, k)
+    want = codes.astype(np.float32).reshape(n, 2, 64) * np.abs(scales)[:, :, None]
+    assert np.array_equal(got.view(np.uint32), want.reshape(n, k).view(np.uint32))
+    runs = wire.reshape(n, k // 64, 36)
+    assert np.array_equal(runs[..., :32], positive.reshape(n, k // 64, 36)[..., :32])
+    assert np.array_equal(runs[..., 32:].copy().view("<f4")[..., 0], scales)
+
+
+def test_nf4_table_is_the_normal_quantile_codebook(oracle):
+    """quantization.rs:3-20 against its definition (QLoRA's NF4): 8 positive
+    and 7 negative quantiles of N(0, 1) at evenly spaced probabilities from
+    0.9677083 to 1/2, an exact zero, normalized to [-1, 1]."""
+    from scipy.stats import norm
+    top = 0.9677083
+    positive = norm.ppf(np.linspace(top, 0.5, 9)[:-1])
+    negative = -norm.ppf(np.linspace(top, 0.5, 8)[:-1])
+    want = np.sort(np.concatenate([positive, [0.0], negative]))
+    want /= np.abs(want).max()
+    table = oracle.nf4_table()
+    assert np.all(np.diff(table) > 0)
+    assert table[0] == -1.0 and table[7] == 0.0 and table[15] == 1.0
+    assert np.abs(table.astype(np.float64) - want).max() < 2e-7
+
+
+def test_nf4_fit_round_trips_codebook_and_zero(oracle):
+    """quantization.rs:358-369, and the fit never reconstructs worse than its
+    start at scale 1 (the codebook spread to the largest magnitude)."""
+    table = oracle.nf4_table()
+    codes, s = oracle.fit_nf4(table)
+    assert np.all(np.abs(table[codes.astype(np.int64) + 8] * s - table) < 1e-6)
+    codes, s = oracle.fit_nf4(np.zeros(16, np.float32))
+    assert np.isfinite(s) and (table[codes.astype(np.int64) + 8] == 0).all()
+    rng = np.random.default_rng(5)
+    for n in (1, 7, 64):
+        x = rng.standard_normal(n).astype(np.float32)
+        codes, s = oracle.fit_nf4(x)
+        m = np.abs(x).max()
+        mids = (table[:-1] + table[1:]) / 2
+        first = table[np.searchsorted(mids, x / m, side="left")] * m
+        err = lambda y: float(((x.astype(np.float64) - y) ** 2).sum())
+        assert err(table[codes.astype(np.int64) + 8].astype(np.float64) * s) <= err(first) * (1 + 1e-5) + 1e-12
+
+
+def test_affine_embedding_rows_reconstruct(oracle):
+    """quantized_rows.rs:121-137: rows of i / 64 through the affine fit decode
+    within 0.04, each group's offset added after the scale."""
+    values = (np.arange(256) / 64.0).astype(np.float32)
+    bf16 = half_bf16(values, oracle)
+    codes, scales, offsets = oracle.weight_quantize_fitted(bf16, 2, 128, "affine", avx2=False)
+    rows = oracle.rows_decode(codes, scales, offsets, False, 2, 128)
+    assert np.all(np.abs(rows - values.reshape(2, 128)) < 0.04)
+    # the offset term is what centres the rows: without it they are far off
+    assert np.abs(oracle.rows_decode(codes, scales, None, False, 2, 128) - values.reshape(2, 128)).max() > 0.5
+
+
+def test_fitted_embedding_rows_decode_group_by_group(oracle):
+    """quantized_rows.rs:139-175: NF4 and MSE rows decode per group as the
+    group fit's value_code * scale, and reconstruct the inputs closely."""
+    i = np.arange(256)
+    bf16 = half_bf16((((i * 37) % 101) - 50.0) / 37.0, oracle)
+    x = oracle.bf16_to_f32(bf16).reshape(2, 128)
+    table = oracle.nf4_table()
+    for mode in ("nf4", "mse"):
+        codes, scales, offsets = oracle.weight_quantize_fitted(bf16, 2, 128, mode, avx2=False)
+        rows = oracle.rows_decode(codes, scales, None, mode == "nf4", 2, 128)
+        for r in range(2):
+            for g in range(2):
+                v = x[r, g * 64:(g + 1) * 64]
+                c, s = oracle.fit_nf4(v) if mode == "nf4" else oracle.fit_mse(v, avx2=False)
+                vc = table[c.astype(np.int64) + 8] if mode == "nf4" else c.astype(np.float32)
+                assert np.array_equal(rows[r, g * 64:(g + 1) * 64], vc * s)
+        assert np.abs(rows - x).max() < 0.2 * np.abs(x).max()
