@@ -116,9 +116,14 @@ void launch_fill_f32(float *p, size_t n, float v, hipStream_t s);
 // Compute units of the current device (cached per device).
 int device_cus();
 
-// The decider's token-by-token gated delta scan (pplx.hip), for the tuner.
+// The decider's gated delta scan (pplx.hip): token by token (rolled: the
+// 16-token stages as a loop) and by 64-token chunks (column_tiles 1 or 2:
+// 16 or 32 state columns per block; ws holds delta_chunk_ws_bytes).
 void launch_delta_scan_tokens(const float *qhat, const float *khat, const float *conv, const float *gb, int n,
-                              int lh, int lk, float *out, int variant, hipStream_t s);
+                              int lh, int lk, float *out, bool rolled, hipStream_t s);
+size_t delta_chunk_ws_bytes(int n, int lh);
+void launch_delta_scan_chunked(const float *qhat, const float *khat, const float *conv, const float *gb, int n,
+                               int lh, int lk, float *ws, float *out, int column_tiles, hipStream_t s);
 
 // ---- variants (tuner) --------------------------------------------------------------
 struct VariantFamily {

@@ -408,20 +408,26 @@ __global__ __launch_bounds__(256) void delta_chunk_prep_kernel(const float *__re
     }
 }
 
-// One block (4 waves) per (head, 16 state columns); the chunks in order. The
-// state S (128 x 16) lives in LDS transposed (S_T[col][dk]); wave w computes
-// rows 16w..16w+15 of the chunk's U and O and the state rows 32w..32w+31.
-__global__ __launch_bounds__(256) void delta_chunk_scan_kernel(const float *__restrict__ qhat,
-                                                               const float *__restrict__ ws, int n, int lh, int lk,
-                                                               float *__restrict__ out) {
-    __shared__ __align__(16) float st[16 * kChunkRow];       // S_T [16][128 + 4]
-    __shared__ __align__(16) float ut[16 * (kChunk + 4)];    // U_T [16][64 + 4]
+// One block per (head, CT x 16 state columns), 4 waves per 16 columns; the
+// chunks in order. The state S (128 x 16 per column tile) lives in LDS
+// transposed (S_T[col][dk]); wave w of a column tile computes rows
+// 16w..16w+15 of the chunk's U and O and the state rows 32w..32w+31. Each
+// state column's arithmetic is the same for every CT, so CT = 1 and CT = 2
+// give the same bits (CT = 2: half the blocks, eight waves each).
+template <int CT>
+__global__ __launch_bounds__(256 * CT) void delta_chunk_scan_kernel(const float *__restrict__ qhat,
+                                                                    const float *__restrict__ ws, int n, int lh,
+                                                                    int lk, float *__restrict__ out) {
     constexpr int UROW = kChunk + 4;
-    const int h = blockIdx.x, cb = blockIdx.y, tid = threadIdx.x;
-    const int wave = tid / 64, lane = tid % 64, col = lane % 16, g = lane / 16;
+    __shared__ __align__(16) float st_all[CT * 16 * kChunkRow];  // S_T [16][128 + 4] per column tile
+    __shared__ __align__(16) float ut_all[CT * 16 * UROW];       // U_T [16][64 + 4] per column tile
+    const int h = blockIdx.x, tid = threadIdx.x;
+    const int ct = tid / 256, wave = (tid / 64) % 4, lane = tid % 64, col = lane % 16, g = lane / 16;
+    const int col0 = (blockIdx.y * CT + ct) * 16;  // this column tile's first state column
+    float *st = st_all + ct * 16 * kChunkRow, *ut = ut_all + ct * 16 * UROW;
     const int kh = h / (lh / lk);
     const int chunks = (n + kChunk - 1) / kChunk;
-    for (int e = tid; e < 16 * kChunkRow; e += 256) st[e] = 0.0f;
+    for (int e = tid; e < CT * 16 * kChunkRow; e += 256 * CT) st_all[e] = 0.0f;
     __syncthreads();
     // the global operands of one chunk for this lane; the next chunk's are in
     // flight while the current one computes
@@ -447,16 +453,19 @@ __global__ __launch_bounds__(256) void delta_chunk_scan_kernel(const float *__re
 #pragma unroll
             for (int d = 0; d < 2; d++) o.r[d][i] = *(const float4_t *)(rkt + (32 * wave + 16 * d + col) * kChunk + 16 * g + 4 * i);
             const int t = 16 * wave + 4 * g + i;
-            o.u[i] = uv[t * kLd + 16 * cb + col];
+            o.u[i] = uv[t * kLd + col0 + col];
             o.gm[i] = gam[t];
         }
         o.last = gam[kChunk - 1];
         return o;
     };
+    // CT = 1 holds the next chunk's operands in registers while this chunk
+    // computes; CT = 2 (two waves per SIMD, half the registers each) loads
+    // them after the chunk and lets the other wave run meanwhile
     Ops cur = fetch(0);
     for (int c = 0; c < chunks; c++) {
         Ops nxt = cur;
-        if (c + 1 < chunks) nxt = fetch(c + 1);
+        if (CT == 1 && c + 1 < chunks) nxt = fetch(c + 1);
         const int t0 = c * kChunk;
         // X = Wk S and Q S over the 128 state rows
         float4_t xw = {0.f, 0.f, 0.f, 0.f}, qsv = xw;
@@ -503,11 +512,14 @@ __global__ __launch_bounds__(256) void delta_chunk_scan_kernel(const float *__re
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int t = t0 + 16 * wave + 4 * g + i;
-            if (t < n) out[((size_t)h * n + t) * kLd + 16 * cb + col] = o4[i];
+            if (t < n) out[((size_t)h * n + t) * kLd + col0 + col] = o4[i];
         }
 #pragma unroll
         for (int d = 0; d < 2; d++) *(float4_t *)(st + col * kChunkRow + 32 * wave + 16 * d + 4 * g) = sn[d];
-        cur = nxt;
+        if (CT == 1)
+            cur = nxt;
+        else if (c + 1 < chunks)
+            cur = fetch(c + 1);
         __builtin_amdgcn_s_waitcnt(0xC07F);  // the new S is complete; U_T is free
         __builtin_amdgcn_s_barrier();
     }
@@ -802,13 +814,36 @@ __global__ void gather_rows_kernel(const float *__restrict__ src, const int32_t 
 // 2 lk 128 on), gb [n][lh][4] = {g, beta, k.q, -}, out [lh][n][128].
 // variant 1 is the rolled loop, any other the unrolled one; the same bits.
 void launch_delta_scan_tokens(const float *qhat, const float *khat, const float *conv, const float *gb, int n,
-                              int lh, int lk, float *out, int variant, hipStream_t s) {
-    if (variant == 1)
+                              int lh, int lk, float *out, bool rolled, hipStream_t s) {
+    if (rolled)
         hipLaunchKernelGGL(delta_scan_kernel<false>, dim3(lh, kLd / kScanCols), dim3(64 * kScanWaves), 0, s, qhat,
                            khat, conv, gb, n, lh, lk, out);
     else
         hipLaunchKernelGGL(delta_scan_kernel<true>, dim3(lh, kLd / kScanCols), dim3(64 * kScanWaves), 0, s, qhat,
                            khat, conv, gb, n, lh, lk, out);
+}
+
+size_t delta_chunk_ws_bytes(int n, int lh) { return (size_t)lh * ((n + kChunk - 1) / kChunk) * kChunkWs * 4; }
+
+void launch_delta_scan_chunked(const float *qhat, const float *khat, const float *conv, const float *gb, int n,
+                               int lh, int lk, float *ws, float *out, int column_tiles, hipStream_t s) {
+    if (n <= 0) return;
+    constexpr size_t lds = (size_t)(kChunk * kChunkRow + kChunk * kChunk + 3 * kChunk) * 4;
+    static bool configured[64] = {};  // the LDS limit is a per-device function attribute
+    int dev = 0;
+    hipGetDevice(&dev);
+    if (dev >= 0 && dev < 64 && !configured[dev]) {
+        if (hipFuncSetAttribute((const void *)delta_chunk_prep_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)lds) == hipSuccess)
+            configured[dev] = true;
+    }
+    const unsigned chunks = (unsigned)((n + kChunk - 1) / kChunk);
+    hipLaunchKernelGGL(delta_chunk_prep_kernel, dim3(lh, chunks), dim3(256), lds, s, qhat, khat, conv, gb, n, lh, lk,
+                       ws);
+    if (column_tiles == 2)
+        hipLaunchKernelGGL(delta_chunk_scan_kernel<2>, dim3(lh, kLd / 32), dim3(512), 0, s, qhat, ws, n, lh, lk, out);
+    else
+        hipLaunchKernelGGL(delta_chunk_scan_kernel<1>, dim3(lh, kLd / 16), dim3(256), 0, s, qhat, ws, n, lh, lk, out);
 }
 
 }  // namespace dz
@@ -946,7 +981,7 @@ int32_t ensure_capacity(dz_ctx *ctx, dz_pplx *p, size_t n) {
     get(&p->qhat, n * c.delta_key_heads * kLd * 4);
     get(&p->khat, n * c.delta_key_heads * kLd * 4);
     get(&p->gb, n * c.delta_heads * 4 * 4);
-    get(&p->chunk_ws, (size_t)c.delta_heads * ((n + kChunk - 1) / kChunk) * kChunkWs * 4);
+    get(&p->chunk_ws, delta_chunk_ws_bytes((int)n, c.delta_heads));
     get(&p->heads, n * std::max(lv, (size_t)c.attn_heads * kAd) * 4);
     get(&p->ctx, n * ctxw * 4);
     get(&p->projected, n * d * 4);
@@ -1447,33 +1482,22 @@ int32_t mlp(dz_ctx *ctx, dz_pplx *p, const dz_pplx::Layer &L, size_t n) {
     return rc;
 }
 
-// Variants 0 ("recurrent", whole stages unrolled) and 1 ("recurrent-rolled")
-// run the token-by-token scan, with the same arithmetic;
-// 2 ("chunked64") the chunked one, whose regrouped arithmetic gives other
-// bits; 3 ("auto") picks the chunked scan from six chunks of tokens on, so
-// its bits depend on the chunk's length. Only 0 and 1 are tuned.
+// Variants 0 ("chunked64": 16 state columns per block) and 1
+// ("chunked64-c32": 32 per block) run the chunked scan, with the same
+// arithmetic; 2 ("recurrent", whole stages unrolled) and 3
+// ("recurrent-rolled") the token-by-token one, whose order gives other bits;
+// 4 ("auto") the token scan below six chunks of tokens and the chunked one
+// from there, so its bits depend on the chunk's length. Only 0 and 1 are tuned.
 void launch_delta_scan(dz_ctx *ctx, dz_pplx *p, size_t n, hipStream_t s) {
     const dz_pplx_config &c = p->cfg;
     const int v = ctx_variant(ctx, "delta_scan");
-    const bool chunked = v == 2 || (v == 3 && n >= (size_t)6 * kChunk);
-    if (!chunked) {
+    const bool tokens = v == 2 || v == 3 || (v == 4 && n < (size_t)6 * kChunk);
+    if (tokens)
         launch_delta_scan_tokens(p->qhat, p->khat, p->conv_out, p->gb, (int)n, c.delta_heads, c.delta_key_heads,
-                                 p->heads, v, s);
-        return;
-    }
-    constexpr size_t lds = (size_t)(kChunk * kChunkRow + kChunk * kChunk + 3 * kChunk) * 4;
-    static bool configured[64] = {};  // the LDS limit is a per-device function attribute
-    int dev = 0;
-    hipGetDevice(&dev);
-    if (dev >= 0 && dev < 64 && !configured[dev]) {
-        if (hipFuncSetAttribute((const void *)delta_chunk_prep_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)lds) == hipSuccess) configured[dev] = true;
-    }
-    const unsigned chunks = (unsigned)((n + kChunk - 1) / kChunk);
-    hipLaunchKernelGGL(delta_chunk_prep_kernel, dim3(c.delta_heads, chunks), dim3(256), lds, s, p->qhat, p->khat,
-                       p->conv_out, p->gb, (int)n, c.delta_heads, c.delta_key_heads, p->chunk_ws);
-    hipLaunchKernelGGL(delta_chunk_scan_kernel, dim3(c.delta_heads, kLd / 16), dim3(256), 0, s, p->qhat,
-                       p->chunk_ws, (int)n, c.delta_heads, c.delta_key_heads, p->heads);
+                                 p->heads, v == 3, s);
+    else
+        launch_delta_scan_chunked(p->qhat, p->khat, p->conv_out, p->gb, (int)n, c.delta_heads, c.delta_key_heads,
+                                  p->chunk_ws, p->heads, v == 1 ? 2 : 1, s);
 }
 
 int32_t delta_layer(dz_ctx *ctx, dz_pplx *p, const dz_pplx::Layer &L, size_t n) {

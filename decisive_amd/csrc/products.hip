@@ -2239,7 +2239,7 @@ const char *const kGroupedNames[] = {"pipe-auto",    "pipe256x128w8", "wave16x16
                                      "pipe64x128w2", "pipe128x128m8", "pipe128x128n8", "pipe32x128w8",
                                      "pipe64x128w8"};
 const char *const kMlpNames[] = {"pipe-auto", "pipe256x64w8", "pipe128x64w4", "wave16x64", "pipe256x64n2", "pipe128x64n2"};
-const char *const kDeltaNames[] = {"recurrent", "recurrent-rolled", "chunked64", "auto"};
+const char *const kDeltaNames[] = {"chunked64", "chunked64-c32", "recurrent", "recurrent-rolled", "auto"};
 const char *const kNormNames[] = {"fused", "separate"};
 
 template <int W, int MPAD, bool G32, int NP>
@@ -2467,13 +2467,13 @@ int variant_count(const char *family) {
     if (f == "i8_gemm") return 10;
     if (f == "grouped") return 9;
     if (f == "mlp") return 6;
-    if (f == "delta_scan") return 4;
+    if (f == "delta_scan") return 5;
     if (f == "norm") return 2;
     return 0;
 }
 
 int tuned_count(const char *family) {
-    // the chunked and "auto" delta scans regroup the rule's arithmetic
+    // the token scans and "auto" regroup the chunked scan's arithmetic
     if (std::string(family) == "delta_scan") return 2;
     return variant_count(family);
 }

@@ -12,20 +12,23 @@
 // re-checked for equality (:498-513). Inputs are hashed packed words with
 // small positive scales (:847-852).
 //
-// Families, in the order they are tuned:
+// Families, in the order they are tuned (the reference's stages first, in its
+// order, checkpoint.rs:251-262):
+//   delta_scan  the decider's chunked gated delta scan with 16 or 32 state
+//               columns per block, the same arithmetic, over 128 tokens of
+//               32 value and 16 key heads (select_delta_scan, :328-421,
+//               admits bit-equal scans only: the token-by-token scans regroup
+//               the rule's arithmetic and stay out)
+//   norm        the decider's layer norm with its A8 codes in one kernel
+//               against the norm and the quantizer apart (select_norm,
+//               :652-684: 64 rows of 2560, its input and weight generators)
 //   grouped     the W4A8 grouped product (select_gemm, :480-563) at
 //               (M, N, K) = (256, 8192, 2560)
 //   mlp         the fused gate/up + SiLU + A8 requant (select_mlp, :568-652)
 //               at (128, 9216, 2560)
-//   norm        the decider's layer norm with its A8 codes in one kernel
-//               against the norm and the quantizer apart (select_norm,
-//               :652-684: 64 rows of 2560, its input and weight generators)
 //   gemv, gemm_w4a16, i8_gemm   this library's W4A16 GEMV / prefill GEMM and
 //               per-row int8 GEMM (no reference counterpart) at (1 or 256,
 //               8192, 2560)
-// The decider's delta scan is not tuned: its two scans regroup the rule's
-// arithmetic differently, so the reference's bitwise rule could only ever keep
-// the baseline (select_delta_scan, :328-421, admits bit-equal scans only).
 #include <string.h>
 
 #include <algorithm>
@@ -169,13 +172,15 @@ struct Bench {
     const float *sx = nullptr, *sw = nullptr;
     const int8_t *b = nullptr;
     const float *qhat = nullptr, *khat = nullptr, *conv = nullptr, *gb = nullptr;  // the delta scan's inputs
+    float *chunk_ws = nullptr;                                                      // and its chunk workspace
     std::vector<std::vector<std::pair<void *, size_t>>> outs;  // per candidate: output buffers
 
     void run(int v) {
         auto &o = outs[v];
         switch (kind) {
-            case Kind::DeltaScan:
-                launch_delta_scan_tokens(qhat, khat, conv, gb, m, n, k, (float *)o[0].first, v, s);
+            case Kind::DeltaScan:  // the chunked scan, 16 or 32 state columns per block
+                launch_delta_scan_chunked(qhat, khat, conv, gb, m, n, k, chunk_ws, (float *)o[0].first, v == 1 ? 2 : 1,
+                                          s);
                 break;
             case Kind::Grouped:
                 launch_grouped(w, (const int8_t *)x, sx, m, (float *)o[0].first, nullptr, v, s);
@@ -251,6 +256,7 @@ bool build_bench(DeviceBuffers &buf, const Family &f, int count, Bench *b) {
             b->khat = (const float *)buf.upload(hk);
             b->conv = (const float *)buf.upload(hc);
             b->gb = (const float *)buf.upload(hg);
+            b->chunk_ws = (float *)buf.alloc(delta_chunk_ws_bytes((int)M, (int)N));
             break;
         }
         case Kind::Grouped:

@@ -537,7 +537,7 @@ int32_t dz_pplx_residency_info(dz_ctx *ctx, dz_pplx *model, char *json, size_t c
  * reference variant and faster than 0.99x it. Families, in the reference's
  * stage order (checkpoint.rs:251-262): "delta_scan" (:328-421
  * select_delta_scan: 128 tokens of 32 value and 16 key heads; only the two
- * token scans, which keep the rule's summation order, are candidates),
+ * chunked scans, which keep the default's summation order, are candidates),
  * "norm" (:652-684 select_norm: 64 rows of 2560, the fused norm and codes
  * against the separate ones), "grouped" (the W4A8 product, :480-563
  * select_gemm at M,N,K = 256, 8192, 2560), "mlp" (the fused MLP, :568-652
@@ -567,16 +567,19 @@ int32_t dz_tune(dz_ctx *ctx, uint32_t budget_ms, const char *cache_in, char *cac
  *                 pipe128x128m8, pipe128x128n8, pipe32x128w8, pipe64x128w8
  *   "mlp"         pipe-auto, pipe256x64w8, pipe128x64w4, wave16x64, pipe256x64n2,
  *                 pipe128x64n2
- *   "delta_scan"  recurrent, recurrent-rolled, chunked64, auto (the
- *                 decider's gated delta rule. The two token scans give the
- *                 same bits: the default runs whole 16-token stages
- *                 unrolled. The chunked scan regroups the arithmetic, so
- *                 it agrees with them to rounding, not bit for bit; "auto"
- *                 runs the token scan below 384 tokens and the chunked one
- *                 from there, so a decider's bits then depend on its chunk
- *                 length. chunked64 and auto are explicit opt-ins that the
- *                 tuner never selects, and the only variants anywhere that
- *                 do not give their family's reference bits)
+ *   "delta_scan"  chunked64, chunked64-c32, recurrent, recurrent-rolled,
+ *                 auto (the decider's gated delta rule. The default runs the
+ *                 rule by 64-token chunks with 16 state columns per block;
+ *                 chunked64-c32 takes 32 per block, the same bits. The two
+ *                 token scans (whole 16-token stages unrolled, or rolled)
+ *                 give the same bits as each other; they regroup the
+ *                 arithmetic, so they agree with the chunked scans to
+ *                 rounding, not bit for bit. "auto" runs the token scan
+ *                 below 384 tokens and the chunked one from there, so a
+ *                 decider's bits then depend on its chunk length. The token
+ *                 scans and auto are explicit opt-ins that the tuner never
+ *                 selects, and the only variants anywhere that do not give
+ *                 their family's reference bits)
  *   "norm"        fused, separate (the decider's layer norms above 16 rows:
  *                 one kernel for the RMSNorm and the A8 codes its products
  *                 share, or the norm then one quantization per product; the

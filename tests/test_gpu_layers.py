@@ -342,8 +342,8 @@ def _tuner_checks(ctx):
         for v, a in enumerate(f["agrees"]):
             assert a in (True, False, None)
     assert fams["grouped"]["shape"] == [256, 8192, 2560] and fams["mlp"]["shape"] == [128, 9216, 2560]
-    # the delta scan's candidates are the token scans only (select_delta_scan, checkpoint.rs:328-421)
-    assert fams["delta_scan"]["candidates"] == ["recurrent", "recurrent-rolled"]
+    # the delta scan's candidates are the chunked scans only (select_delta_scan, checkpoint.rs:328-421)
+    assert fams["delta_scan"]["candidates"] == ["chunked64", "chunked64-c32"]
     assert fams["delta_scan"]["shape"] == [128, 32, 16]
     assert list(sel["selected"]) == list(TUNED)
     assert fams["norm"]["shape"][0] == 64 and fams["norm"]["shape"][2] == 2560
@@ -404,4 +404,4 @@ def test_tuned_grouped_and_mlp_variants_agree_on_real_inputs(ctx, oracle):
 
 def rocm_reference(fam):
     return {"gemv": "auto", "gemm_w4a16": "pipe-auto", "i8_gemm": "256x256p2w8", "grouped": "pipe-auto",
-            "mlp": "pipe-auto", "norm": "fused", "delta_scan": "recurrent"}[fam]
+            "mlp": "pipe-auto", "norm": "fused", "delta_scan": "chunked64"}[fam]

@@ -75,12 +75,12 @@ def test_forward_logits_match_the_reference_chunk(ctx, oracle, small, n):
     assert close(got, want, rel=1e-2), (float(cosine(got, want)), float(np.abs(got - want).max()))
 
 
-@pytest.mark.parametrize("scan", ["recurrent", "recurrent-rolled", "chunked64"])
+@pytest.mark.parametrize("scan", ["chunked64", "chunked64-c32", "recurrent", "recurrent-rolled"])
 @pytest.mark.parametrize("n", [1, 37, 64, 130, 257])
 def test_delta_layer_matches_the_reference_for_both_scans(ctx, oracle, small, scan, n):
-    """The token-by-token scan (its unrolled and rolled forms) and the
-    chunked one (64-token chunks: one partial chunk, exact chunks, a ragged
-    tail) against the oracle's sequential rule. Both regroup the rule's
+    """The chunked scan (64-token chunks: one partial chunk, exact chunks, a
+    ragged tail; 16 or 32 state columns per block) and the token-by-token one
+    (its unrolled and rolled forms) against the oracle's sequential rule. Both regroup the rule's
     arithmetic, so an ulp now and then flips one A8 code of out_proj's input;
     the bound is a cosine of 0.99999 with max-abs within 1% (a wrong scan
     lands far below 0.9999)."""
@@ -92,7 +92,7 @@ def test_delta_layer_matches_the_reference_for_both_scans(ctx, oracle, small, sc
     try:
         p.layer(1, hd, n)
     finally:
-        ctx.select_variant("delta_scan", "recurrent")
+        ctx.select_variant("delta_scan", "chunked64")
     got = host(ctx, hd)
     want = pplx_model.ref_layer(oracle, model, 1, h)
     assert cosine(got, want) >= 0.99999 and close(got, want, rel=1e-2), (float(cosine(got, want)),
@@ -100,27 +100,41 @@ def test_delta_layer_matches_the_reference_for_both_scans(ctx, oracle, small, sc
 
 
 @pytest.mark.parametrize("n", [1, 16, 17, 130, 400])
-def test_recurrent_scan_forms_are_bitwise_equal(ctx, oracle, small, n):
-    """The unrolled token scan (whole 16-token stages) and the rolled one run
-    the same arithmetic in the same order: a delta layer gives the same
-    bits with either, at lengths inside one 16-token stage, across stages and
-    past the 384 tokens where "auto" switches to the chunked scan; "auto" equals
-    the token scan below 384 tokens."""
+def test_scan_forms_are_bitwise_equal(ctx, oracle, small, n):
+    """Each scan's forms run the same arithmetic in the same order: the two
+    chunked forms (16 or 32 state columns per block) give the same bits, and
+    so do the unrolled and rolled token scans, at lengths inside one 16-token
+    stage and one chunk, across them and past the 384 tokens where "auto"
+    switches from the token scan to the chunked one, whose bits it then gives."""
     torch = pytest.importorskip("torch")
     model, p = small
     h = np.random.default_rng(300 + n).standard_normal((n, SMALL["hidden"])).astype(np.float32)
     got = {}
     try:
-        for scan in ("recurrent", "recurrent-rolled", "auto"):
+        for scan in ("chunked64", "chunked64-c32", "recurrent", "recurrent-rolled", "auto"):
             ctx.select_variant("delta_scan", scan)
             hd = dev(h)
             p.layer(1, hd, n)
             got[scan] = host(ctx, hd).copy()
     finally:
-        ctx.select_variant("delta_scan", "recurrent")
+        ctx.select_variant("delta_scan", "chunked64")
+    assert bits_equal(got["chunked64"], got["chunked64-c32"])
     assert bits_equal(got["recurrent"], got["recurrent-rolled"])
-    if n < 384:
-        assert bits_equal(got["auto"], got["recurrent"])
+    assert bits_equal(got["auto"], got["recurrent" if n < 384 else "chunked64"])
+
+
+@pytest.mark.parametrize("n", [5, 64, 200])
+def test_chunked_scan_outputs_do_not_depend_on_the_chunk_length(ctx, oracle, small, n):
+    """The default scan is causal in its arithmetic too: the first n tokens of
+    a 257-token layer are the bits of an n-token layer (masked terms add exact
+    zeros), so a decider's outputs do not depend on where its chunk ends."""
+    torch = pytest.importorskip("torch")
+    model, p = small
+    h = np.random.default_rng(900).standard_normal((257, SMALL["hidden"])).astype(np.float32)
+    long, short = dev(h), dev(h[:n])
+    p.layer(1, long, 257)
+    p.layer(1, short, n)
+    assert bits_equal(host(ctx, short), host(ctx, long)[:n])
 
 
 # four query heads per key/value head, as the reference model has
