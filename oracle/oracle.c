@@ -6,6 +6,11 @@
  * hyperlogue/decisive tree). Built with -ffp-contract=off -fno-fast-math so the
  * only fused multiply-adds are the explicit fmaf() calls that the reference's
  * AVX2 kernel performs with _mm256_fmadd_ps.
+ *
+ * Parity unpinned: the AVX2 lane order of the fitted quantizers' sums
+ * (or_fit_mse / or_fit_affine, quantization.rs:73-129, :202-258) is followed
+ * but checked only through the reference's invariants of the fits; they make
+ * test weights, and no product's parity depends on their exact bits.
  */
 #define _GNU_SOURCE
 #include "oracle.h"
