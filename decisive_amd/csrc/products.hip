@@ -2044,7 +2044,7 @@ __global__ __launch_bounds__(BM / 32 * 64) void mlp_pipe_kernel(
     constexpr int WAVES = BM / 32, MB = 2 * WN, NT = 4 / WN, WR = 32 * WN;
     constexpr int XSTAGE = BM * 128;   // activation codes, 2 groups per step
     constexpr int CSTAGE = 8 * 1024;   // gate tiles 0-3, up tiles 0-3: one tile16x128 chunk each
-    constexpr int SWSTAGE = 2 * 1024;  // scale records: [weight][8 tiles x 128 B], tiles 0-3 used
+    constexpr int SWSTAGE = 2 * 512;   // scale records: [weight][4 tiles x 128 B]
     constexpr int SXSTAGE = BM * 8;
     constexpr int XPW = BM / 8 / WAVES;
     __shared__ __align__(16) uint8_t xs[2 * XSTAGE];
@@ -2067,7 +2067,6 @@ __global__ __launch_bounds__(BM / 32 * 64) void mlp_pipe_kernel(
     const int32x4_t rcu = buffer_rsrc(ucodes + (size_t)tile0 * kbs * 1024, (uint32_t)(4 * kbs * 1024));
     const int32x4_t rwg = buffer_rsrc(gscales + (size_t)tile0 * kbs * 128, (uint32_t)(4 * kbs * 128));
     const int32x4_t rwu = buffer_rsrc(uscales + (size_t)tile0 * kbs * 128, (uint32_t)(4 * kbs * 128));
-    // (records of tiles 4-7 fall past these four tiles' range and read as zero)
     const int32x4_t rs = buffer_rsrc(sx + (size_t)row0 * groups, (uint32_t)(rvalid * groups * 4));
     const uint32_t xs_lds = lds_address(xs), cs_lds = lds_address(cs);
     const uint32_t sws_lds = lds_address(sws), sxs_lds = lds_address(sxs);
@@ -2092,9 +2091,8 @@ __global__ __launch_bounds__(BM / 32 * 64) void mlp_pipe_kernel(
             if (ch < 4) dma16(lds, off, live ? rcg : zero_len(rcg));
             else dma16(lds, off, live ? rcu : zero_len(rcu));
         }
-        if (wave < 2) {  // wave 0 the gate records, wave 1 the up records: lane l -> tile l / 8, piece l % 8
-            // (lanes of tiles 4-7 load records the block does not use, or zeros past the end)
-            const uint32_t lds = __builtin_amdgcn_readfirstlane(sws_lds + stage * SWSTAGE + wave * 1024);
+        if (wave < 2 && lane < 32) {  // wave 0 the gate records, wave 1 the up records: lane l -> tile l / 8, piece l % 8
+            const uint32_t lds = __builtin_amdgcn_readfirstlane(sws_lds + stage * SWSTAGE + wave * 512);
             const uint32_t off = (uint32_t)(((lane / 8) * kbs + st) * 128 + (lane % 8) * 16);
             if (wave == 0) dma16(lds, off, live ? rwg : zero_len(rwg));
             else dma16(lds, off, live ? rwu : zero_len(rwu));
@@ -2126,8 +2124,8 @@ __global__ __launch_bounds__(BM / 32 * 64) void mlp_pipe_kernel(
                 const uint2_t wds = *(const uint2_t *)(cst + (wgt * 4 + t) * 1024 + lane * 16 + gp * 8);
                 const uint2_t lo = nibbles_to_i8(wds[0]), hi = nibbles_to_i8(wds[1]);
                 const int4_t b = int4_t{(int)lo[0], (int)lo[1], (int)hi[0], (int)hi[1]};
-                const float4_t s01 = *(const float4_t *)(swst + wgt * 1024 + t * 128 + qd * 32);
-                const float4_t s23 = *(const float4_t *)(swst + wgt * 1024 + t * 128 + qd * 32 + 16);
+                const float4_t s01 = *(const float4_t *)(swst + wgt * 512 + t * 128 + qd * 32);
+                const float4_t s23 = *(const float4_t *)(swst + wgt * 512 + t * 128 + qd * 32 + 16);
                 const float4_t sv = gp ? float4_t{s01[1], s01[3], s23[1], s23[3]} : float4_t{s01[0], s01[2], s23[0], s23[2]};
                 if (wgt == 0) {
                     gb[nt] = b;
