@@ -2618,7 +2618,9 @@ bool launch_grouped(const Weight &w, const int8_t *q, const float *sx, int m, fl
 // Variants: 1 pipelined 256x64 blocks (8 waves), 2 128x64 blocks (4 waves),
 // 4 and 5 the same blocks with the waves paired along N (wave tile 64 x 32), 3
 // one wave per 16x64 block. 0 picks the paired 256-row blocks when their grid
-// covers half the compute units but not all of them, else the paired 128-row
+// covers half the compute units but not all of them and has fewer blocks than
+// the 128-row grid (not at m <= 128, where the 256-row blocks are half empty:
+// 54 against 40 us at M = 128, K = 2560, N = 9216), else the paired 128-row
 // blocks when theirs covers half, else the one-wave blocks (measured at K=2560,
 // N=9216: the paired layouts are 7-16% faster than the stacked ones at every M
 // from 229 to 4096, and 128-row blocks beat 256-row blocks from M=1024 up).
@@ -2632,8 +2634,10 @@ void launch_mlp_requant(const Weight &gate, const Weight &up, const int8_t *q, c
                       gate.rows % 4 == 0;
     int pick = variant;
     if (variant == 0) {
+        // 256-row blocks only where they shorten the grid (at m <= 128 both
+        // grids have the same blocks, half of each 256-row block empty)
         const unsigned b256 = cdiv(m, 256) * tn, b128 = cdiv(m, 128) * tn;
-        if (2 * b256 >= cus && b256 < cus) pick = 4;
+        if (2 * b256 >= cus && b256 < cus && b256 < b128) pick = 4;
         else if (2 * b128 >= cus) pick = 5;
         else pick = 3;
     }
