@@ -106,6 +106,20 @@ __device__ __forceinline__ int4_t mfma_i8(int4_t a, int4_t b, int4_t c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
 }
 
+// A 64-group dot d (|d| < 2^22: at most 64 * 127 * 127 for W8A8) as an exact
+// f32 without v_cvt_f32_i32, which issues at about 60% of an add's rate on
+// gfx950: the MFMA accumulates onto kDotBias, the bits of 1.5 * 2^23, where a
+// float's ulp is 1, so the int32 result is the bit pattern of 12582912 + d and
+// one exact subtraction (dot_value) leaves f32(d), the same bits as the
+// conversion.
+constexpr int32_t kDotBias = 0x4B400000;
+__device__ __forceinline__ int4_t mfma_i8_biased(int4_t a, int4_t b) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, int4_t{kDotBias, kDotBias, kDotBias, kDotBias}, 0, 0, 0);
+}
+__device__ __forceinline__ float dot_value(int32_t biased) {
+    return __fsub_rn(__builtin_bit_cast(float, biased), 12582912.0f);
+}
+
 __device__ __forceinline__ float f16_bits_to_float(uint32_t h) {
     return (float)__builtin_bit_cast(half_t, (unsigned short)h);
 }

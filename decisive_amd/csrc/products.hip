@@ -109,10 +109,10 @@ __global__ __launch_bounds__(256) void grouped_kernel(const uint8_t *__restrict_
 #pragma unroll
         for (int u = 0; u < B; u++) {
             if (g0 + u >= groups) break;
-            const int4_t d = mfma_i8(bt.a[u], bt.b[u], zero);
+            const int4_t d = mfma_i8_biased(bt.a[u], bt.b[u]);
 #pragma unroll
             for (int v = 0; v < 4; v++) {
-                acc[v] = __builtin_fmaf((float)d[v], __fmul_rn(bt.sw[u], bt.sx[u][v]), acc[v]);
+                acc[v] = __builtin_fmaf(dot_value(d[v]), __fmul_rn(bt.sw[u], bt.sx[u][v]), acc[v]);
                 if (AFF) acc[v] = __builtin_fmaf(bt.ofs[AFF ? u : 0], bt.sq[AFF ? u : 0][v], acc[v]);
             }
         }
@@ -330,7 +330,7 @@ __global__ __launch_bounds__(kGvWaves * 64) void grouped_gemv_kernel(
                 bv = __builtin_bit_cast(int4_t, bq[gg]);
                 if (i < MPAD) av = *(const int4_t *)(acode + i * S::ASTRIDE + gg * 64 + qd * 16);
             }
-            const int4_t d = mfma_i8(av, bv, int4_t{0, 0, 0, 0});
+            const int4_t d = mfma_i8_biased(av, bv);
 #pragma unroll
             for (int v = 0; v < 4; v++) {
                 const int r = qd * 4 + v;
@@ -341,7 +341,7 @@ __global__ __launch_bounds__(kGvWaves * 64) void grouped_gemv_kernel(
         if (folds) {
             const int end = min(groups - w0, kGvWindow);
             for (int gw = 0; gw < end; gw++) {
-                const float dot = (float)dots[(gw * MPAD + fr) * 16 + fc];
+                const float dot = dot_value(dots[(gw * MPAD + fr) * 16 + fc]);
                 const float sxv = asx[fr * kGvWindow + gw], swv2 = sw[gw * 16 + fc];
                 if (PROJECT)
                     acc = __fadd_rn(acc, __fmul_rn(dot, __fmul_rn(sxv, swv2)));
@@ -392,8 +392,8 @@ __global__ __launch_bounds__(256) void mlp_requant_kernel(
         uint2_t u0 = nibbles_to_i8(uw[0]), u1 = nibbles_to_i8(uw[1]);
         int4_t gb = {(int)g0[0], (int)g0[1], (int)g1[0], (int)g1[1]};
         int4_t ub = {(int)u0[0], (int)u0[1], (int)u1[0], (int)u1[1]};
-        int4_t gd = mfma_i8(a, gb, zero);
-        int4_t ud = mfma_i8(a, ub, zero);
+        int4_t gd = mfma_i8_biased(a, gb);
+        int4_t ud = mfma_i8_biased(a, ub);
         size_t rec = (((size_t)t * kbs + kb) * 16 + j) * 8;
         float gs = ((const float *)(gscales + rec))[g & 1];
         float us = ((const float *)(uscales + rec))[g & 1];
@@ -401,8 +401,8 @@ __global__ __launch_bounds__(256) void mlp_requant_kernel(
         for (int v = 0; v < 4; v++) {
             int r = mt * 16 + qd * 4 + v;
             float sxv = r < m ? sx[(size_t)r * groups + g] : 0.0f;
-            ga[v] = __builtin_fmaf((float)gd[v], __fmul_rn(gs, sxv), ga[v]);
-            ua[v] = __builtin_fmaf((float)ud[v], __fmul_rn(us, sxv), ua[v]);
+            ga[v] = __builtin_fmaf(dot_value(gd[v]), __fmul_rn(gs, sxv), ga[v]);
+            ua[v] = __builtin_fmaf(dot_value(ud[v]), __fmul_rn(us, sxv), ua[v]);
         }
     }
     float4_t val;
@@ -1918,7 +1918,6 @@ __global__ __launch_bounds__(WGM *WGN * 64) void grouped_pipe_kernel(
     for (int a = 0; a < MB; a++)
 #pragma unroll
         for (int b = 0; b < NT; b++) acc[a][b] = float4_t{0.f, 0.f, 0.f, 0.f};
-    const int4_t zero = {0, 0, 0, 0};
     const bool nan_out = bad != nullptr && *bad != 0;
     const int steps = (groups + 1) / 2;
 
@@ -1966,10 +1965,10 @@ __global__ __launch_bounds__(WGM *WGN * 64) void grouped_pipe_kernel(
             const float sqv = AFF ? *(const float *)(sqst + r * 8 + gp * 4) : 0.0f;
 #pragma unroll
             for (int nt = 0; nt < NT; nt++) {
-                const int4_t d = mfma_i8(bfr[nt], afr, zero);
+                const int4_t d = mfma_i8_biased(bfr[nt], afr);
 #pragma unroll
                 for (int v = 0; v < 4; v++) {
-                    acc[mb][nt][v] = __builtin_fmaf((float)d[v], __fmul_rn(swv[nt][v], sxv), acc[mb][nt][v]);
+                    acc[mb][nt][v] = __builtin_fmaf(dot_value(d[v]), __fmul_rn(swv[nt][v], sxv), acc[mb][nt][v]);
                     if (AFF) acc[mb][nt][v] = __builtin_fmaf(ofv[AFF ? nt : 0][v], sqv, acc[mb][nt][v]);
                 }
             }
@@ -2109,7 +2108,6 @@ __global__ __launch_bounds__(BM / 32 * 64) void mlp_pipe_kernel(
     for (int a = 0; a < MB; a++)
 #pragma unroll
         for (int b = 0; b < NT; b++) ga[a][b] = ua[a][b] = float4_t{0.f, 0.f, 0.f, 0.f};
-    const int4_t zero = {0, 0, 0, 0};
     const bool nan_out = bad != nullptr && *bad != 0;
     const int steps = (groups + 1) / 2;
 
@@ -2146,12 +2144,12 @@ __global__ __launch_bounds__(BM / 32 * 64) void mlp_pipe_kernel(
             const float sxv = *(const float *)(sxst + r * 8 + gp * 4);
 #pragma unroll
             for (int nt = 0; nt < NT; nt++) {
-                const int4_t gd = mfma_i8(gb[nt], afr, zero);
-                const int4_t ud = mfma_i8(ub[nt], afr, zero);
+                const int4_t gd = mfma_i8_biased(gb[nt], afr);
+                const int4_t ud = mfma_i8_biased(ub[nt], afr);
 #pragma unroll
                 for (int v = 0; v < 4; v++) {
-                    ga[mb][nt][v] = __builtin_fmaf((float)gd[v], __fmul_rn(gs[nt][v], sxv), ga[mb][nt][v]);
-                    ua[mb][nt][v] = __builtin_fmaf((float)ud[v], __fmul_rn(us[nt][v], sxv), ua[mb][nt][v]);
+                    ga[mb][nt][v] = __builtin_fmaf(dot_value(gd[v]), __fmul_rn(gs[nt][v], sxv), ga[mb][nt][v]);
+                    ua[mb][nt][v] = __builtin_fmaf(dot_value(ud[v]), __fmul_rn(us[nt][v], sxv), ua[mb][nt][v]);
                 }
             }
         }

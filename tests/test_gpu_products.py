@@ -200,6 +200,7 @@ def test_fused_mlp_large_m_pipeline_equals_unfused(ctx, oracle):
     for name in ("pipe256x64w8", "pipe128x64w4", "wave16x64", "pipe256x64n2", "pipe128x64n2", "pipe-auto"):
         ctx.select_variant("mlp", name)
         q.zero_()
+        torch.cuda.synchronize()  # the fill runs on torch's stream, the product on the context's
         ctx.mlp_requant(gate, up, xd, m, q, s)
         assert np.array_equal(host(ctx, q), host(ctx, q2)), name
         assert bits_equal(host(ctx, s), host(ctx, s2)), name
@@ -264,6 +265,7 @@ def test_fused_mlp_requant_equals_unfused(ctx, oracle):
     for name in ("pipe256x64w8", "pipe128x64w4", "wave16x64", "pipe256x64n2", "pipe128x64n2", "pipe-auto"):
         ctx.select_variant("mlp", name)
         q.zero_()
+        torch.cuda.synchronize()  # the fill runs on torch's stream, the product on the context's
         ctx.mlp_requant(gate, up, xd, m, q, s)
         assert np.array_equal(host(ctx, q), host(ctx, q2)), name
         assert bits_equal(host(ctx, s), host(ctx, s2)), name
@@ -369,6 +371,7 @@ def test_gemv_stream_variants_equal_the_split_kernel(ctx, oracle, k, n):
             for name in ("stream8", "stream4", "auto"):
                 ctx.select_variant("gemv", name)
                 y.fill_(7.0)
+                torch.cuda.synchronize()  # the fill runs on torch's stream, the product on the context's
                 ctx.linear(w, xd, rocm.F16, m, y, rocm.W4A16)
                 assert bits_equal(host(ctx, y), base), (name, m)
     finally:
@@ -516,9 +519,11 @@ def test_w4a16_column_split_matches_register_kernel(ctx, oracle, n):
     m, k = 8192, 1024
     g = torch.Generator(device="cuda").manual_seed(n)
     wdev = torch.randn((n, k), generator=g, device="cuda", dtype=torch.float32) * 0.02
+    torch.cuda.synchronize()  # the context's stream is not ordered after torch's
     w = ctx.quantize(wdev, rocm.F32, n, k, 4, 32)
     del wdev
     x = torch.randn((m, k), generator=torch.Generator(device="cuda").manual_seed(3), device="cuda").half()
+    torch.cuda.synchronize()
     ys = []
     for name in ("pipe-auto", "256x128w2x2"):
         ctx.select_variant("gemm_w4a16", name)
@@ -544,6 +549,7 @@ def test_config5_prefill_rows_vs_fp32(ctx, oracle):
     m, k, n = 16384, 4096, 14336
     g = torch.Generator(device="cuda").manual_seed(1)
     wdev = torch.randn((n, k), generator=g, device="cuda", dtype=torch.float32) * 0.02
+    torch.cuda.synchronize()  # the context's stream is not ordered after torch's
     w = ctx.quantize(wdev, rocm.F32, n, k, 4, 32)
     del wdev
     x = torch.randn((m, k), generator=torch.Generator(device="cuda").manual_seed(0), device="cuda").half()
@@ -655,6 +661,7 @@ def test_config4_int8_full_size(ctx, oracle):
         ctx.select_variant("i8_gemm", name)
         rv = torch.full((m, n), -7, dtype=torch.int32, device="cuda")
         yv = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()  # the fills run on torch's stream, the products on the context's
         ctx.i8_gemm(qa, sa, m, qb, sb, n, k, rv, raw=True)
         ctx.i8_gemm(qa, sa, m, qb, sb, n, k, yv, raw=False)
         ctx.sync()
