@@ -1803,9 +1803,9 @@ __global__ __launch_bounds__(WGM *WGN * 64) void w4a16_pipe_kernel(
 //    [group][row]); activation scales: BM rows x 2 f32.
 // The MFMA takes the weight operand first, so lane (q, j) holds the dots of
 // four consecutive output columns of one row: its weight scales are one
-// 16-byte LDS read and its activation scale one 4-byte read. The fold (a
-// convert, the scale product and the fma per output and group) is VALU work
-// and bounds the kernel; the MFMAs take about a third of its time.
+// 16-byte LDS read and its activation scale one 4-byte read. The fold (the
+// dot as f32, the scale product and the fma per output and group) is VALU
+// work and bounds the kernel; the MFMAs take about a third of its time.
 // Groups past `groups` (the odd tail of a k-step) are not folded.
 // AFF (fitted affine Q4, int8.rs:566-571): the offsets (the group-64 scale
 // layout) and sxq = sx * f32(sum of the row's group codes) are staged like the
