@@ -40,6 +40,8 @@ const Weight &weight_of(const dz_weight *h);
 Weight &weight_mut(dz_weight *h);
 int32_t weight_upload(dz_ctx *ctx, const void *packed, size_t bytes, int32_t layout, size_t rows, size_t cols,
                       dz_weight **out);
+int32_t weight_upload_fitted(dz_ctx *ctx, const void *packed, size_t bytes, size_t rows, size_t cols, int32_t form,
+                             dz_weight **out);
 void weight_free(dz_weight *h);
 int32_t weight_concat_rows(dz_ctx *ctx, const dz_weight *const *parts, int count, dz_weight **out);
 int32_t ctx_readout_rows(dz_ctx *ctx, const Weight &w, const float *norm, const void *hidden, int dtype,
@@ -881,6 +883,7 @@ struct dz_pplx {
     int32_t *markers = nullptr;
     uint8_t *rows_dev = nullptr;
     dz::Weight rows_weight;
+    int32_t rows_form = DZ_ROWS_PACKED;  // how forward_rows decodes the packed embedding rows
     // What the last layer call left in the activation buffers, for
     // dz_pplx_activation: the layer, its kind and row counts, which norm and
     // gate outputs were written in which form, and where z, a and b sit.
@@ -1102,11 +1105,17 @@ void join_zab(dz_ctx *ctx, dz_pplx *p, dz_pplx::Layer &L) {
     if (weight_concat_rows(ctx, parts, 3, &L.zab) != DZ_OK) L.zab = nullptr;
 }
 
+// form: -1 for a packed.rs matrix in `layout`; DZ_FIT_SCALED for a fitted Q4
+// (quantization.rs mse) matrix in the DZ_Q4_G64_F32 wire layout.
 int32_t pplx_set_weight(dz_ctx *ctx, dz_pplx *p, const char *name, const void *packed, size_t bytes, int32_t layout,
-                        size_t rows, size_t cols) {
+                        size_t rows, size_t cols, int32_t form) {
     if (!p || !name || !packed) return ctx_fail(ctx, DZ_INVALID_REQUEST, "null pointer");
     if (layout != DZ_Q4_G64_F32 && layout != DZ_Q8_G64_F32)
         return ctx_fail(ctx, DZ_INVALID_PARAMETERS, "pplx projections are group-64 packed matrices");
+    if (form >= 0 && (form != DZ_FIT_SCALED || layout != DZ_Q4_G64_F32))
+        return ctx_fail(ctx, DZ_INVALID_PARAMETERS,
+                        "the decider takes fitted Q4 weights in the scaled (MSE) form: its products have no offset "
+                        "term and its projections no codebook");
     const dz_pplx_config &c = p->cfg;
     const size_t d = c.hidden, cw = conv_width(c), lv = (size_t)c.delta_heads * kLd;
     std::string s(name), rest;
@@ -1155,7 +1164,8 @@ int32_t pplx_set_weight(dz_ctx *ctx, dz_pplx *p, const char *name, const void *p
     if (!slot) return ctx_fail(ctx, DZ_INVALID_CHECKPOINT, "unknown pplx tensor: " + s);
     if (rows != want_r || cols != want_c) return ctx_fail(ctx, DZ_INVALID_CHECKPOINT, "tensor shape mismatch: " + s);
     dz_weight *w = nullptr;
-    int32_t rc = weight_upload(ctx, packed, bytes, layout, rows, cols, &w);
+    int32_t rc = form >= 0 ? weight_upload_fitted(ctx, packed, bytes, rows, cols, form, &w)
+                           : weight_upload(ctx, packed, bytes, layout, rows, cols, &w);
     if (rc) return rc;
     if (p->st.on && layer >= 0) {  // streamed: the new bytes replace the host copy
         const Weight &a = weight_of(w), &b = weight_of(*slot);
@@ -1701,6 +1711,16 @@ int32_t pplx_run_layer(dz_ctx *ctx, dz_pplx *p, int index, size_t n, const int32
     return DZ_OK;
 }
 
+int32_t pplx_set_rows_form(dz_ctx *ctx, dz_pplx *p, int32_t form) {
+    if (!p) return ctx_fail(ctx, DZ_INVALID_REQUEST, "null pointer");
+    if (form != DZ_ROWS_PACKED && form != DZ_FIT_SCALED && form != DZ_FIT_NF4)
+        return ctx_fail(ctx, DZ_INVALID_PARAMETERS,
+                        "embedding rows are packed, scaled (MSE) or NF4 rows: affine rows carry offsets the row bytes "
+                        "do not hold");
+    p->rows_form = form;
+    return DZ_OK;
+}
+
 int32_t pplx_set_residency(dz_ctx *ctx, dz_pplx *p, int32_t residency) {
     if (!p) return ctx_fail(ctx, DZ_INVALID_REQUEST, "null pointer");
     if (residency != DZ_PPLX_RESIDENT && residency != DZ_PPLX_STREAMED)
@@ -1843,9 +1863,11 @@ int32_t pplx_forward_rows(dz_ctx *ctx, dz_pplx *p, const void *rows_host, size_t
     if (e == hipSuccess) e = hipMemcpyAsync(p->markers, markers, count * 4, hipMemcpyHostToDevice, s);
     if (e != hipSuccess) return ctx_hip_fail(ctx, e, "pplx input upload");
     p->rows_weight.rows = (int)n;
+    p->rows_weight.fitted = p->rows_form != DZ_ROWS_PACKED;
+    p->rows_weight.nf4 = p->rows_form == DZ_FIT_NF4;  // quantized_rows.rs:98-102
     int bad = 0;
     launch_fill_i32(ctx_flag(ctx), 0, 1, s);
-    launch_upload(p->rows_weight, p->rows_dev, ctx_flag(ctx), s);
+    launch_upload(p->rows_weight, p->rows_dev, ctx_flag(ctx), s, p->rows_weight.fitted);
     launch_dequant(p->rows_weight, nullptr, (int)n, p->hidden, 0, s);
     e = hipMemcpyAsync(&bad, ctx_flag(ctx), sizeof(int), hipMemcpyDeviceToHost, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);

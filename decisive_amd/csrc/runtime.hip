@@ -77,7 +77,8 @@ int32_t encoder_readout(dz_ctx *ctx, dz_encoder *e, const void *rows_host, size_
 int32_t pplx_create(dz_ctx *ctx, const dz_pplx_config *cfg, dz_pplx **out);
 void pplx_destroy(dz_ctx *ctx, dz_pplx *p);
 int32_t pplx_set_weight(dz_ctx *ctx, dz_pplx *p, const char *name, const void *packed, size_t bytes, int32_t layout,
-                        size_t rows, size_t cols);
+                        size_t rows, size_t cols, int32_t form);
+int32_t pplx_set_rows_form(dz_ctx *ctx, dz_pplx *p, int32_t form);
 int32_t pplx_set_vector(dz_ctx *ctx, dz_pplx *p, const char *name, const float *values, size_t count);
 int32_t pplx_layer(dz_ctx *ctx, dz_pplx *p, int index, float *hidden, size_t n, const int32_t *markers_host,
                    size_t count, int part);
@@ -369,7 +370,7 @@ void free_weight(dz_weight *h) {
 // The fitted forms (bit DZ_FIT_*) a product takes; weights that are not
 // fitted run everywhere.
 constexpr int kFitGrouped = 1 << DZ_FIT_SCALED | 1 << DZ_FIT_AFFINE;
-constexpr int kFitW4A16 = 1 << DZ_FIT_SCALED;
+constexpr int kFitScaled = 1 << DZ_FIT_SCALED;  // signed scales and -8 codes: any fold takes them
 constexpr int kFitNone = 0;
 const char *const kFitNames[] = {"scaled", "affine", "NF4"};
 
@@ -789,7 +790,7 @@ int32_t dz_linear(dz_ctx *ctx, const dz_weight *w, const void *x, int32_t x_dtyp
         if (w->w.bits != 4) return fail(ctx, DZ_INVALID_PARAMETERS, "W4A16 needs a Q4 weight");
         if (w->w.cols % 8 != 0) return fail(ctx, DZ_INVALID_PARAMETERS, "W4A16 needs cols % 8 == 0");
         if (((uintptr_t)x & 15) != 0) return fail(ctx, DZ_INVALID_PARAMETERS, "W4A16 activations must be 16-byte aligned");
-        if (int32_t rc = fitted_form_ok(ctx, w, kFitW4A16, "W4A16")) return rc;
+        if (int32_t rc = fitted_form_ok(ctx, w, kFitScaled, "W4A16")) return rc;
         if (m == 0) return DZ_OK;
         dz::launch_w4a16(w->w, (const dz::half_t *)x, (int)m, y, variant(ctx, "gemv"),
                          variant(ctx, "gemm_w4a16"), ctx->stream);
@@ -840,7 +841,7 @@ int32_t dz_linear_f16(dz_ctx *ctx, const dz_weight *w, const void *x, size_t m, 
         return fail(ctx, DZ_INVALID_PARAMETERS, "unknown epilogue");
     if (epilogue == DZ_EPI_RESIDUAL && m && !residual) return fail(ctx, DZ_INVALID_REQUEST, "null residual");
     if (w->w.bits != 4) return fail(ctx, DZ_INVALID_PARAMETERS, "W4A16 needs a Q4 weight");
-    if (int32_t rc = fitted_form_ok(ctx, w, kFitW4A16, "dz_linear_f16")) return rc;
+    if (int32_t rc = fitted_form_ok(ctx, w, kFitScaled, "dz_linear_f16")) return rc;
     if (w->w.cols % 8 != 0) return fail(ctx, DZ_INVALID_PARAMETERS, "W4A16 needs cols % 8 == 0");
     if (((uintptr_t)x & 15) != 0) return fail(ctx, DZ_INVALID_PARAMETERS, "W4A16 activations must be 16-byte aligned");
     if (m == 0) return DZ_OK;
@@ -876,8 +877,8 @@ int32_t dz_mlp_requant(dz_ctx *ctx, const dz_weight *gate, const dz_weight *up, 
     const dz::Weight &g = gate->w, &u = up->w;
     if (g.kind != dz::WeightKind::Q4G64 || u.kind != dz::WeightKind::Q4G64)
         return fail(ctx, DZ_INVALID_PARAMETERS, "fused MLP needs Q4 group-64 weights");
-    if (int32_t rc = fitted_form_ok(ctx, gate, kFitNone, "dz_mlp_requant")) return rc;
-    if (int32_t rc = fitted_form_ok(ctx, up, kFitNone, "dz_mlp_requant")) return rc;
+    if (int32_t rc = fitted_form_ok(ctx, gate, kFitScaled, "dz_mlp_requant")) return rc;
+    if (int32_t rc = fitted_form_ok(ctx, up, kFitScaled, "dz_mlp_requant")) return rc;
     if (g.rows != u.rows || g.cols != u.cols || g.rows % 64 != 0)
         return fail(ctx, DZ_INVALID_PARAMETERS, "fused MLP shapes must match with rows % 64 == 0");
     if (m == 0) return DZ_OK;
@@ -900,7 +901,7 @@ int32_t dz_linear_q8(dz_ctx *ctx, const dz_weight *w, const int8_t *q, const flo
     if (!w || (m && (!q || !s || !y))) return fail(ctx, DZ_INVALID_REQUEST, "null pointer");
     if (w->w.kind == dz::WeightKind::Q4G32)
         return fail(ctx, DZ_INVALID_PARAMETERS, "grouped int8 mode needs a group-64 weight");
-    if (int32_t rc = fitted_form_ok(ctx, w, kFitNone, "dz_linear_q8")) return rc;
+    if (int32_t rc = fitted_form_ok(ctx, w, kFitScaled, "dz_linear_q8")) return rc;
     if (m <= 16)
         dz::launch_grouped_codes(w->w, q, s, (int)m, y, nullptr, false, ctx->stream);
     else
@@ -914,7 +915,7 @@ int32_t dz_project(dz_ctx *ctx, const dz_weight *w, const float *x, size_t m, fl
     if (!w || (m && (!x || !y))) return fail(ctx, DZ_INVALID_REQUEST, "null pointer");
     if (w->w.kind == dz::WeightKind::Q4G32 || w->w.cols % 64 != 0)
         return fail(ctx, DZ_INVALID_PARAMETERS, "invalid packed readout shape");
-    if (int32_t rc = fitted_form_ok(ctx, w, kFitNone, "dz_project")) return rc;
+    if (int32_t rc = fitted_form_ok(ctx, w, kFitScaled, "dz_project")) return rc;
     if (m == 0) return DZ_OK;
     if (m > (1u << 24)) return fail(ctx, DZ_INPUT_TOO_LONG, "input budget exceeded");
     int32_t rc = ensure_work(ctx, project_work_bytes(w->w, m));
@@ -932,7 +933,7 @@ int32_t dz_readout(dz_ctx *ctx, const dz_weight *w, const float *norm, const flo
     if (!w || !norm || (rows && (!hidden || !logits))) return fail(ctx, DZ_INVALID_REQUEST, "null pointer");
     if (w->w.kind == dz::WeightKind::Q4G32 || w->w.cols % 64 != 0 || w->w.cols > dz::kReadoutMaxCols)
         return fail(ctx, DZ_INVALID_PARAMETERS, "invalid packed readout shape");
-    if (int32_t rc = fitted_form_ok(ctx, w, kFitNone, "dz_readout")) return rc;
+    if (int32_t rc = fitted_form_ok(ctx, w, kFitScaled, "dz_readout")) return rc;
     if (rows == 0) return DZ_OK;
     if (rows > (1u << 20)) return fail(ctx, DZ_INPUT_TOO_LONG, "input budget exceeded");
     return readout_rows(ctx, w->w, norm, hidden, 0, nullptr, rows, eps, logits);
@@ -1168,7 +1169,21 @@ int32_t dz_pplx_set_weight(dz_ctx *ctx, dz_pplx *model, const char *name, const 
                            int32_t layout, size_t rows, size_t cols) {
     DZ_BEGIN(ctx);
     DZ_NOT_CAPTURING(ctx);
-    return dz::pplx_set_weight(ctx, model, name, packed, bytes, layout, rows, cols);
+    return dz::pplx_set_weight(ctx, model, name, packed, bytes, layout, rows, cols, -1);
+}
+
+int32_t dz_pplx_set_weight_fitted(dz_ctx *ctx, dz_pplx *model, const char *name, const void *packed, size_t bytes,
+                                  size_t rows, size_t cols, int32_t form) {
+    DZ_BEGIN(ctx);
+    DZ_NOT_CAPTURING(ctx);
+    if (form < 0) return fail(ctx, DZ_INVALID_PARAMETERS, "unknown fitted form");
+    return dz::pplx_set_weight(ctx, model, name, packed, bytes, DZ_Q4_G64_F32, rows, cols, form);
+}
+
+int32_t dz_pplx_set_rows_form(dz_ctx *ctx, dz_pplx *model, int32_t form) {
+    DZ_BEGIN(ctx);
+    DZ_NOT_CAPTURING(ctx);
+    return dz::pplx_set_rows_form(ctx, model, form);
 }
 
 int32_t dz_pplx_set_vector(dz_ctx *ctx, dz_pplx *model, const char *name, const float *values, size_t count) {
@@ -1343,6 +1358,10 @@ int32_t weight_concat_rows(dz_ctx *ctx, const dz_weight *const *parts, int count
 int32_t weight_upload(dz_ctx *ctx, const void *packed, size_t bytes, int32_t layout, size_t rows, size_t cols,
                       dz_weight **out) {
     return dz_weight_upload(ctx, packed, bytes, layout, rows, cols, out);
+}
+int32_t weight_upload_fitted(dz_ctx *ctx, const void *packed, size_t bytes, size_t rows, size_t cols, int32_t form,
+                             dz_weight **out) {
+    return dz_weight_upload_fitted(ctx, packed, bytes, rows, cols, form, nullptr, out);
 }
 int32_t ctx_readout_rows(dz_ctx *ctx, const Weight &w, const float *norm, const void *hidden, int dtype,
                          const int32_t *select, size_t rows, float eps, float *logits) {

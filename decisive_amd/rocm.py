@@ -32,6 +32,7 @@ W4A8, W4A4, W4A16 = 0, 1, 2
 PPLX_RESIDENT, PPLX_STREAMED = 0, 1
 PPLX_WHOLE, PPLX_MIXER, PPLX_MLP = 0, 1, 2  # dz_pplx_layer_part's parts
 FIT_SCALED, FIT_AFFINE, FIT_NF4 = 0, 1, 2  # dz_weight_upload_fitted's forms
+ROWS_PACKED = -1  # dz_pplx_set_rows_form's default
 
 
 class DzError(RuntimeError):
@@ -145,6 +146,8 @@ _SIGNATURES = {
     "dz_pplx_create": (I32, [P, ctypes.POINTER(PplxConfig), PP]),
     "dz_pplx_destroy": (None, [P, P]),
     "dz_pplx_set_weight": (I32, [P, P, ctypes.c_char_p, P, SZ, I32, SZ, SZ]),
+    "dz_pplx_set_weight_fitted": (I32, [P, P, ctypes.c_char_p, P, SZ, SZ, SZ, I32]),
+    "dz_pplx_set_rows_form": (I32, [P, P, I32]),
     "dz_pplx_set_vector": (I32, [P, P, ctypes.c_char_p, P, SZ]),
     "dz_pplx_layer": (I32, [P, P, I32, P, SZ, P, SZ]),
     "dz_pplx_layer_part": (I32, [P, P, I32, I32, P, SZ, P, SZ]),
@@ -496,6 +499,17 @@ class Pplx:
         packed = np.ascontiguousarray(packed, dtype=np.uint8)
         self.ctx._check(load().dz_pplx_set_weight(self.ctx.handle, self.handle, name.encode(), packed.ctypes.data,
                                                   packed.size, layout, rows, cols))
+
+    def set_weight_fitted(self, name: str, packed, rows: int, cols: int, form: int = FIT_SCALED):
+        """dz_pplx_set_weight_fitted: a fitted Q4 g64/f32 wire projection (MSE form)."""
+        import numpy as np
+        packed = np.ascontiguousarray(packed, dtype=np.uint8)
+        self.ctx._check(load().dz_pplx_set_weight_fitted(self.ctx.handle, self.handle, name.encode(),
+                                                         packed.ctypes.data, packed.size, rows, cols, form))
+
+    def set_rows_form(self, form: int):
+        """dz_pplx_set_rows_form: ROWS_PACKED, FIT_SCALED or FIT_NF4 embedding rows."""
+        self.ctx._check(load().dz_pplx_set_rows_form(self.ctx.handle, self.handle, form))
 
     def set_vector(self, name: str, values):
         import numpy as np

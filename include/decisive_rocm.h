@@ -29,11 +29,13 @@
  *    for the stream, allocate, or read host memory return DZ_INVALID_REQUEST
  *    under capture before enqueueing anything: dz_sync, dz_alloc, dz_free,
  *    dz_copy_h2d, dz_copy_d2h, dz_set_stream, dz_weight_upload,
- *    dz_weight_quantize, dz_weight_free, dz_dequant_rows, dz_project,
+ *    dz_weight_upload_fitted, dz_weight_quantize, dz_weight_free,
+ *    dz_dequant_rows, dz_project,
  *    dz_q4_quantize_rows, dz_encoder_create_random, dz_encoder_read_rows,
  *    dz_encoder_forward (it reads back the token-range flag),
  *    dz_encoder_forward_rows, dz_encoder_hidden_rows, dz_encoder_set_readout,
  *    dz_encoder_readout_rows, dz_pplx_create, dz_pplx_set_weight,
+ *    dz_pplx_set_weight_fitted, dz_pplx_set_rows_form,
  *    dz_pplx_set_vector, dz_pplx_layer and dz_pplx_layer_part (they may grow
  *    the model's activation buffers), dz_pplx_activation,
  *    dz_pplx_forward_rows, dz_pplx_set_residency and dz_tune.
@@ -178,10 +180,10 @@ int32_t dz_weight_upload(dz_ctx *ctx, const void *packed_host, size_t bytes, int
  *    as int8.rs:524-571 does:
  *      acc = fma(f32(dot), sw * sx, acc);
  *      acc = fma(offset, sx * f32(sum of the row's 64 activation codes), acc)
- *  - the W4A16 products (dz_linear in W4A16 mode, dz_linear_f16) take
- *    DZ_FIT_SCALED;
- *  - the remaining products (dz_mlp_requant, dz_linear_q8, dz_project,
- *    dz_readout, dz_linear_records) take no fitted weight.
+ *  - the other products on codes and scales (dz_linear in W4A16 mode,
+ *    dz_linear_f16, dz_mlp_requant, dz_linear_q8, dz_project, dz_readout)
+ *    take DZ_FIT_SCALED: signed scales and -8 codes need no other arithmetic;
+ *  - dz_linear_records takes no fitted weight.
  * A product refuses a form it does not take with DZ_INVALID_PARAMETERS.
  * cols % 64 == 0 (the wire layout's); a zero or non-finite scale or a
  * non-finite offset is DZ_INVALID_CHECKPOINT; an unknown form
@@ -445,6 +447,24 @@ void dz_pplx_destroy(dz_ctx *ctx, dz_pplx *model);
  * dz_weight_upload. An unknown name or shape is DZ_INVALID_CHECKPOINT. */
 int32_t dz_pplx_set_weight(dz_ctx *ctx, dz_pplx *model, const char *name, const void *packed_host,
                            size_t bytes, int32_t layout, size_t rows, size_t cols);
+/* dz_pplx_set_weight for a fitted Q4 projection of the reference's
+ * `optimized` precisions (native.rs:125-128: q4-w4a8-e8-r4-g64-mse,
+ * q4-w4a8-e4-r4-g64-mse, q4-w4a8-e4-r4-g64-mse-nf4; quantization.rs:25-71
+ * mse): the DZ_Q4_G64_F32 wire layout with the full code range and signed
+ * scales, form DZ_FIT_SCALED, validated as dz_weight_upload_fitted. The
+ * decider folds it as any weight (int8.rs:524-585). DZ_FIT_AFFINE and
+ * DZ_FIT_NF4 are DZ_INVALID_PARAMETERS: its products have no offset term
+ * (q4-w4a8-e4-r4-g64-affine is not served) and its projections no codebook. */
+int32_t dz_pplx_set_weight_fitted(dz_ctx *ctx, dz_pplx *model, const char *name, const void *packed_host,
+                                  size_t bytes, size_t rows, size_t cols, int32_t form);
+/* How dz_pplx_forward_rows decodes its packed embedding rows
+ * (quantized_rows.rs:89-110): DZ_ROWS_PACKED, the default (packed.rs:59-73:
+ * f32(code) * scale, scales positive), DZ_FIT_SCALED (MSE-fitted rows: signed
+ * scales, codes -8..7) or DZ_FIT_NF4 (NF4[code + 8] * scale, the
+ * q4-w4a8-e4-r4-g64-mse-nf4 rows). DZ_FIT_AFFINE is DZ_INVALID_PARAMETERS:
+ * affine rows carry offsets the row bytes do not hold. */
+#define DZ_ROWS_PACKED (-1)
+int32_t dz_pplx_set_rows_form(dz_ctx *ctx, dz_pplx *model, int32_t form);
 /* A vector by its checkpoint name, as f32 values in the checkpoint's order:
  * the layer norms, linear_attn.conv1d.weight ([width, 1, 4]), A_log, dt_bias,
  * linear_attn.norm.weight, self_attn.q_norm / k_norm, language_model.norm.weight. */

@@ -23,17 +23,22 @@ class Model:
     embedding: np.ndarray = None                 # packed wire rows [vocab x hidden]
     panels: dict = field(default_factory=dict)   # name -> the oracle's AVX2 panel form of quant[name]
     bits: int = 4                                # weight code bits
+    fit: str = None                              # projections fitted by quantization.rs ("mse") or packed
+    rows: tuple = None                           # fitted rows (codes, scales, nf4), else the packed embedding
 
 
 def conv_width(c):
     return 2 * c["delta_key_heads"] * LD + c["delta_heads"] * LD
 
 
-def random_model(oracle, cfg, vocab=64, seed=0, bits=4, reuse=None):
+def random_model(oracle, cfg, vocab=64, seed=0, bits=4, reuse=None, fit=None, rows_fit=None):
     """`reuse` maps a layer index to an earlier layer of the same kind whose
-    tensors it shares (real-size models with one layer of each kind)."""
+    tensors it shares (real-size models with one layer of each kind). `fit`
+    "mse" fits every projection and the readout as native.rs:125-128's
+    optimized precisions do (quantization.rs:25-71); `rows_fit` "mse" or
+    "nf4" fits the embedding rows (quantized_rows.rs:56-66)."""
     rng = np.random.default_rng(seed)
-    m = Model(cfg=dict(cfg), bits=bits)
+    m = Model(cfg=dict(cfg), bits=bits, fit=fit)
     d, ff, lh, ah, akv = cfg["hidden"], cfg["ff"], cfg["delta_heads"], cfg["attn_heads"], cfg["attn_kv_heads"]
     cw, lv = conv_width(cfg), lh * LD
 
@@ -42,8 +47,12 @@ def random_model(oracle, cfg, vocab=64, seed=0, bits=4, reuse=None):
 
     def mat(name, rows, cols, std):
         raw = oracle.f32_to_bf16((rng.standard_normal((rows, cols)) * std).astype(np.float32))
-        m.packed[name] = (oracle.pack_g64(raw, rows, cols, bits), rows, cols)
-        codes, scales = oracle.weight_quantize(raw, rows, cols, bits)
+        if fit:
+            codes, scales, _ = oracle.weight_quantize_fitted(raw, rows, cols, fit)
+            m.packed[name] = (oracle.pack_wire_codes(codes, scales, rows, cols), rows, cols)
+        else:
+            m.packed[name] = (oracle.pack_g64(raw, rows, cols, bits), rows, cols)
+            codes, scales = oracle.weight_quantize(raw, rows, cols, bits)
         m.quant[name] = (codes, scales, rows, cols)
 
     def vec(name, values):
@@ -83,7 +92,12 @@ def random_model(oracle, cfg, vocab=64, seed=0, bits=4, reuse=None):
     vec("language_model.norm.weight", rng.standard_normal(d) * 0.1)
     mat("readout", 255, d, 0.05)
     emb = oracle.f32_to_bf16(rng.standard_normal((vocab, d)).astype(np.float32))
-    m.embedding = oracle.pack_g64(emb, vocab, d, bits).reshape(vocab, -1)
+    if rows_fit:
+        codes, scales, _ = oracle.weight_quantize_fitted(emb, vocab, d, rows_fit)
+        m.embedding = oracle.pack_wire_codes(codes, scales, vocab, d).reshape(vocab, -1)
+        m.rows = (codes, scales, rows_fit == "nf4")
+    else:
+        m.embedding = oracle.pack_g64(emb, vocab, d, bits).reshape(vocab, -1)
     return m
 
 
@@ -91,7 +105,12 @@ def load(ctx, rocm, model):
     p = ctx.pplx_create(rocm.PplxConfig(**model.cfg))
     layout = rocm.Q4_G64_F32
     for name, (wire, rows, cols) in model.packed.items():
-        p.set_weight(name, wire, layout, rows, cols)
+        if model.fit:
+            p.set_weight_fitted(name, wire, rows, cols, rocm.FIT_SCALED)
+        else:
+            p.set_weight(name, wire, layout, rows, cols)
+    if model.rows is not None:
+        p.set_rows_form(rocm.FIT_NF4 if model.rows[2] else rocm.FIT_SCALED)
     for name, values in model.vectors.items():
         p.set_vector(name, values)
     return p
@@ -166,8 +185,12 @@ def ref_layer(oracle, model, i, h, markers=None):
 def ref_forward(oracle, model, ids, markers):
     """native.rs:193-274 for one chunk: embedding rows, every layer (the last
     one cut to the markers when it is an attention layer), readout logits."""
-    rows = model.embedding[ids]
-    h = oracle.unpack_g64(rows.reshape(-1), 4).reshape(len(ids), -1)
+    if model.rows is not None:  # quantized_rows.rs:89-110 over the fitted rows
+        codes, scales, nf4 = model.rows
+        h = oracle.rows_decode(codes[ids], scales[ids], None, nf4, len(ids), model.cfg["hidden"])
+    else:
+        rows = model.embedding[ids]
+        h = oracle.unpack_g64(rows.reshape(-1), 4).reshape(len(ids), -1)
     layers = model.cfg["layers"]
     prune = (layers - 1) % 4 == 3
     for i in range(layers):

@@ -175,8 +175,50 @@ def test_fitted_upload_and_product_refusals(ctx, oracle):
     refused("INVALID_PARAMETERS", lambda: ctx.linear(nf4, xh, rocm.F16, 4, y, rocm.W4A16))
     q = dev(np.zeros((4, k), np.int8))
     s = dev(np.ones((4, k // 64), np.float32))
-    refused("INVALID_PARAMETERS", lambda: ctx.linear_q8(scaled, q, s, 4, y))
+    refused("INVALID_PARAMETERS", lambda: ctx.linear_q8(affine, q, s, 4, y))
+    refused("INVALID_PARAMETERS", lambda: ctx.mlp_requant(affine, affine, x, 4, dev(np.zeros((4, n), np.int8)), s))
     # the weights refused above still run where they belong
     ctx.linear(scaled, xh, rocm.F16, 4, y, rocm.W4A16)
     ctx.linear(affine, x, rocm.F32, 4, y, rocm.W4A8)
     assert np.isfinite(host(ctx, y)).all()
+
+
+@pytest.mark.parametrize("m", [5, 300])
+def test_scaled_fit_mlp_and_code_products_equal_their_compositions(ctx, oracle, m):
+    """MSE-fitted gate/up through the fused MLP (every variant) give the codes
+    and scales of the grouped pair, SiLU * up and the A8 quantizer word for
+    word (grouped_q4.rs:313-354), and dz_linear_q8 on codes gives dz_linear's
+    bits for the same rows."""
+    torch = pytest.importorskip("torch")
+    k, n = 640, 192
+    _, gc, gs, _ = fitted(oracle, n, k, "mse", 21)
+    _, uc, us, _ = fitted(oracle, n, k, "mse", 22)
+    gate = upload(ctx, oracle, gc, gs, None, n, k, rocm.FIT_SCALED)
+    up = upload(ctx, oracle, uc, us, None, n, k, rocm.FIT_SCALED)
+    x = (np.random.default_rng(m).standard_normal((m, k)) * 1.3).astype(np.float32)
+    xd = dev(x)
+    g, u = empty((m, n), torch.float32), empty((m, n), torch.float32)
+    ctx.linear_pair(gate, up, xd, m, g, u)
+    ctx.silu_mul(g, u, m * n)
+    q2, s2 = empty((m, n), torch.int8), empty((m, n // 64), torch.float32)
+    ctx.act_quantize(g, m, n, 8, q2, s2)
+    q2h, s2h = host(ctx, q2).copy(), host(ctx, s2).copy()
+    q, s = empty((m, n), torch.int8), empty((m, n // 64), torch.float32)
+    try:
+        for name in ("pipe256x64w8", "pipe128x64w4", "wave16x64", "pipe256x64n2", "pipe128x64n2", "pipe-auto"):
+            ctx.select_variant("mlp", name)
+            q.zero_()
+            torch.cuda.synchronize()  # the fill runs on torch's stream, the product on the context's
+            ctx.mlp_requant(gate, up, xd, m, q, s)
+            assert np.array_equal(host(ctx, q), q2h), name
+            assert bits_equal(host(ctx, s), s2h), name
+    finally:
+        ctx.select_variant("mlp", "pipe-auto")
+    qx, sx = empty((m, k), torch.int8), empty((m, k // 64), torch.float32)
+    ctx.act_quantize(xd, m, k, 8, qx, sx)
+    y1, y2 = empty((m, n), torch.float32), empty((m, n), torch.float32)
+    ctx.linear_q8(gate, qx, sx, m, y1)
+    ctx.linear(gate, xd, rocm.F32, m, y2, rocm.W4A8)
+    assert bits_equal(host(ctx, y1), host(ctx, y2))
+    want = oracle.grouped_gemm(host(ctx, qx), host(ctx, sx), m, gc, gs, n, k, fused=True)
+    assert bits_equal(host(ctx, y1), want)

@@ -64,7 +64,7 @@ def test_attention_layer_prunes_to_the_markers_in_order(ctx, oracle, small):
     assert e.value.code == "INVALID_REQUEST"
 
 
-@pytest.mark.parametrize("n", [6, 64, 400])  # 400: the chunked delta scan (auto from 384 tokens), ragged chunks
+@pytest.mark.parametrize("n", [6, 64, 400])  # 400: seven 64-token chunks of the delta scan, the last ragged
 def test_forward_logits_match_the_reference_chunk(ctx, oracle, small, n):
     model, p = small
     ids = np.random.default_rng(n).integers(0, 64, n)
