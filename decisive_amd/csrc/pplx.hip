@@ -302,12 +302,22 @@ __global__ __launch_bounds__(256) void delta_chunk_prep_kernel(const float *__re
     float *rec = ws + ((size_t)h * gridDim.y + c) * kChunkWs;
     float *uv = rec, *wk = uv + kChunk * kLd, *pm = wk + kChunk * kLd, *rkt = pm + kChunk * kChunk,
           *gam = rkt + kLd * kChunk;
-    // stage K rows (zero past n), beta and log g (zero past n)
-    for (int e = tid; e < kChunk * kLd / 4; e += 256) {
-        const int t = e / (kLd / 4), u = e % (kLd / 4), tok = t0 + t;
-        float4_t kv = {0.f, 0.f, 0.f, 0.f};
-        if (tok < n) kv = *(const float4_t *)(khat + ((size_t)tok * lk + kh) * kLd + 4 * u);
-        *(float4_t *)(ks + t * kChunkRow + 4 * u) = kv;
+    // stage K rows (zero past n), beta and log g (zero past n); every load of
+    // the rows is issued before the first store
+    {
+        constexpr int KV = kChunk * kLd / 4 / 256;  // float4s per thread
+        float4_t kv[KV];
+#pragma unroll
+        for (int i = 0; i < KV; i++) {
+            const int e = tid + 256 * i, t = e / (kLd / 4), u = e % (kLd / 4), tok = t0 + t;
+            kv[i] = tok < n ? *(const float4_t *)(khat + ((size_t)tok * lk + kh) * kLd + 4 * u)
+                            : float4_t{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int i = 0; i < KV; i++) {
+            const int e = tid + 256 * i, t = e / (kLd / 4), u = e % (kLd / 4);
+            *(float4_t *)(ks + t * kChunkRow + 4 * u) = kv[i];
+        }
     }
     if (tid < kChunk) {
         const int tok = t0 + tid;
@@ -324,12 +334,20 @@ __global__ __launch_bounds__(256) void delta_chunk_prep_kernel(const float *__re
                             : float4_t{0.f, 0.f, 0.f, 0.f};
     }
     __syncthreads();
-    if (tid == 0) {
+    if (tid == 0) {  // the running sum of log g in token order, in registers (16-byte LDS reads and writes)
+        float4_t c[kChunk / 4];
+#pragma unroll
+        for (int i = 0; i < kChunk / 4; i++) c[i] = *(const float4_t *)(cum + 4 * i);
         float run = 0.0f;
-        for (int t = 0; t < kChunk; t++) {
-            run += cum[t];
-            cum[t] = run;
-        }
+#pragma unroll
+        for (int i = 0; i < kChunk / 4; i++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                run += c[i][e];
+                c[i][e] = run;
+            }
+#pragma unroll
+        for (int i = 0; i < kChunk / 4; i++) *(float4_t *)(cum + 4 * i) = c[i];
     }
     __syncthreads();
     if (tid < kChunk) bk[tid] = bet[tid] * expf(cum[tid]);
