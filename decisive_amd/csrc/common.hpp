@@ -120,6 +120,31 @@ __device__ __forceinline__ float dot_value(int32_t biased) {
     return __fsub_rn(__builtin_bit_cast(float, biased), 12582912.0f);
 }
 
+// Q4 weights for the biased MFMA in five VALU operations per 8 codes instead
+// of nine: a nibble moved to the top of its byte, with the byte's top bit
+// flipped, is the int8 16 * code (offset binary n -> 16 n - 128); the mask and
+// the flip are one v_bitop3_b32. The MFMA then sums 16 * d; accumulated onto
+// the bits of 1.5 * 2^19, where a float's ulp is 1/16, the int32 result is the
+// bit pattern of 786432 + d for |d| < 2^18 (W4A8: at most 64 * 8 * 127), and
+// dot_value16 leaves f32(d) exactly, the same bits as dot_value on the plain
+// codes.
+__device__ __forceinline__ uint2_t nibbles_to_i8x16(uint32_t w) {
+    const uint32_t hi = (w & 0xF0F0F0F0u) ^ 0x80808080u;         // bytes: 16 e2, 16 e6, 16 e3, 16 e7
+    const uint32_t lo = ((w << 4) & 0xF0F0F0F0u) ^ 0x80808080u;  // bytes: 16 e0, 16 e4, 16 e1, 16 e5
+    uint2_t out;
+    out[0] = __builtin_amdgcn_perm(hi, lo, 0x06040200u);  // 16 (e0 e1 e2 e3)
+    out[1] = __builtin_amdgcn_perm(hi, lo, 0x07050301u);  // 16 (e4 e5 e6 e7)
+    return out;
+}
+constexpr int32_t kDotBias16 = 0x49400000;
+__device__ __forceinline__ int4_t mfma_i8_biased16(int4_t a, int4_t b) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, int4_t{kDotBias16, kDotBias16, kDotBias16, kDotBias16}, 0, 0,
+                                                 0);
+}
+__device__ __forceinline__ float dot_value16(int32_t biased) {
+    return __fsub_rn(__builtin_bit_cast(float, biased), 786432.0f);
+}
+
 __device__ __forceinline__ float f16_bits_to_float(uint32_t h) {
     return (float)__builtin_bit_cast(half_t, (unsigned short)h);
 }

@@ -18,6 +18,7 @@
 #include <float.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "kernels.hpp"
 
@@ -1921,6 +1922,25 @@ __global__ __launch_bounds__(WGM *WGN * 64) void grouped_pipe_kernel(
     const bool nan_out = bad != nullptr && *bad != 0;
     const int steps = (groups + 1) / 2;
 
+    // Q4 codes enter the MFMA as 16 * code (nibbles_to_i8x16 with kDotBias16),
+    // Q8 codes as they are (kDotBias); either way dotv gives f32(dot) exactly
+    auto q4_frag = [](uint32_t w0, uint32_t w1) {
+        const uint2_t lo = nibbles_to_i8x16(w0), hi = nibbles_to_i8x16(w1);
+        return int4_t{(int)lo[0], (int)lo[1], (int)hi[0], (int)hi[1]};
+    };
+    auto mfma_dot = [](int4_t b, int4_t a) { return BITS == 4 ? mfma_i8_biased16(b, a) : mfma_i8_biased(b, a); };
+    auto dotv = [](int32_t d) { return BITS == 4 ? dot_value16(d) : dot_value(d); };
+    auto x_frag = [&](const uint8_t *xst, int r, int gp) {
+        if (BITS == 4) {
+            const int c1 = 4 * gp + qd / 2, c2 = c1 + 2;
+            const uint2_t a0 = *(const uint2_t *)(xst + r * 128 + ((c1 ^ ((r >> 1) & 7)) * 16) + 8 * (qd & 1));
+            const uint2_t a1 = *(const uint2_t *)(xst + r * 128 + ((c2 ^ ((r >> 1) & 7)) * 16) + 8 * (qd & 1));
+            return int4_t{(int)a0[0], (int)a0[1], (int)a1[0], (int)a1[1]};
+        }
+        const int c = 4 * gp + qd;
+        return *(const int4_t *)(xst + r * 128 + ((c ^ ((r >> 1) & 7)) * 16));
+    };
+
     // one group of a stage: weight fragments and scales once, then per row
     // block the activation fragment, its scale, NT MFMAs and the fold
     auto fold_group = [&](const uint8_t *xst, const uint8_t *cst, const uint8_t *swst, const uint8_t *sxst,
@@ -1932,8 +1952,7 @@ __global__ __launch_bounds__(WGM *WGN * 64) void grouped_pipe_kernel(
             const int t = wn * NT + nt;
             if (BITS == 4) {
                 const uint2_t wds = *(const uint2_t *)(cst + t * 1024 + lane * 16 + gp * 8);
-                const uint2_t lo = nibbles_to_i8(wds[0]), hi = nibbles_to_i8(wds[1]);
-                bfr[nt] = int4_t{(int)lo[0], (int)lo[1], (int)hi[0], (int)hi[1]};
+                bfr[nt] = q4_frag(wds[0], wds[1]);
                 const float4_t s01 = *(const float4_t *)(swst + t * 128 + qd * 32);       // rows 4qd, 4qd+1
                 const float4_t s23 = *(const float4_t *)(swst + t * 128 + qd * 32 + 16);  // rows 4qd+2, 4qd+3
                 swv[nt] = gp ? float4_t{s01[1], s01[3], s23[1], s23[3]} : float4_t{s01[0], s01[2], s23[0], s23[2]};
@@ -1951,44 +1970,119 @@ __global__ __launch_bounds__(WGM *WGN * 64) void grouped_pipe_kernel(
 #pragma unroll
         for (int mb = 0; mb < MB; mb++) {
             const int r = wm * TM + mb * 16 + j;
-            int4_t afr;
-            if (BITS == 4) {
-                const int c1 = 4 * gp + qd / 2, c2 = c1 + 2;
-                const uint2_t a0 = *(const uint2_t *)(xst + r * 128 + ((c1 ^ ((r >> 1) & 7)) * 16) + 8 * (qd & 1));
-                const uint2_t a1 = *(const uint2_t *)(xst + r * 128 + ((c2 ^ ((r >> 1) & 7)) * 16) + 8 * (qd & 1));
-                afr = int4_t{(int)a0[0], (int)a0[1], (int)a1[0], (int)a1[1]};
-            } else {
-                const int c = 4 * gp + qd;
-                afr = *(const int4_t *)(xst + r * 128 + ((c ^ ((r >> 1) & 7)) * 16));
-            }
+            const int4_t afr = x_frag(xst, r, gp);
             const float sxv = *(const float *)(sxst + r * 8 + gp * 4);
             const float sqv = AFF ? *(const float *)(sqst + r * 8 + gp * 4) : 0.0f;
 #pragma unroll
             for (int nt = 0; nt < NT; nt++) {
-                const int4_t d = mfma_i8_biased(bfr[nt], afr);
+                const int4_t d = mfma_dot(bfr[nt], afr);
 #pragma unroll
                 for (int v = 0; v < 4; v++) {
-                    acc[mb][nt][v] = __builtin_fmaf(dot_value(d[v]), __fmul_rn(swv[nt][v], sxv), acc[mb][nt][v]);
+                    acc[mb][nt][v] = __builtin_fmaf(dotv(d[v]), __fmul_rn(swv[nt][v], sxv), acc[mb][nt][v]);
                     if (AFF) acc[mb][nt][v] = __builtin_fmaf(ofv[AFF ? nt : 0][v], sqv, acc[mb][nt][v]);
                 }
             }
         }
     };
 
+    // Small wave tiles (MB * NT <= 4) take a whole k-step at once: every LDS
+    // read of both groups, then every MFMA, then the folds in group order, so
+    // a wave waits once per step for its reads and once for its first dots.
+    constexpr bool BATCH = MB * NT <= 4;
+    auto fold_step = [&](const uint8_t *xst, const uint8_t *cst, const uint8_t *swst, const uint8_t *sxst,
+                         const uint8_t *ofst, const uint8_t *sqst, bool g1) {
+        int4_t bfr[2][NT];
+        float4_t swv[2][NT], ofv[2][AFF ? NT : 1];
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            const int t = wn * NT + nt;
+            if (BITS == 4) {
+                const uint4_t wds = *(const uint4_t *)(cst + t * 1024 + lane * 16);  // group 0: words 0, 1
+                bfr[0][nt] = q4_frag(wds[0], wds[1]);
+                bfr[1][nt] = q4_frag(wds[2], wds[3]);
+                const float4_t s01 = *(const float4_t *)(swst + t * 128 + qd * 32);
+                const float4_t s23 = *(const float4_t *)(swst + t * 128 + qd * 32 + 16);
+                swv[0][nt] = float4_t{s01[0], s01[2], s23[0], s23[2]};
+                swv[1][nt] = float4_t{s01[1], s01[3], s23[1], s23[3]};
+                if (AFF) {
+                    const float4_t o01 = *(const float4_t *)(ofst + t * 128 + qd * 32);
+                    const float4_t o23 = *(const float4_t *)(ofst + t * 128 + qd * 32 + 16);
+                    ofv[0][AFF ? nt : 0] = float4_t{o01[0], o01[2], o23[0], o23[2]};
+                    ofv[1][AFF ? nt : 0] = float4_t{o01[1], o01[3], o23[1], o23[3]};
+                }
+            } else {
+#pragma unroll
+                for (int gp = 0; gp < 2; gp++) {
+                    bfr[gp][nt] = *(const int4_t *)(cst + (t * 2 + gp) * 1024 + lane * 16);
+                    swv[gp][nt] = *(const float4_t *)(swst + t * 128 + gp * 64 + qd * 16);
+                }
+            }
+        }
+        int4_t afr[2][MB];
+        float sxv[2][MB], sqv[2][MB];
+#pragma unroll
+        for (int mb = 0; mb < MB; mb++) {
+            const int r = wm * TM + mb * 16 + j;
+            afr[0][mb] = x_frag(xst, r, 0);
+            afr[1][mb] = x_frag(xst, r, 1);
+            const uint2_t s = *(const uint2_t *)(sxst + r * 8);
+            sxv[0][mb] = word_as_float(s[0]);
+            sxv[1][mb] = word_as_float(s[1]);
+            if (AFF) {
+                const uint2_t q2 = *(const uint2_t *)(sqst + r * 8);
+                sqv[0][mb] = word_as_float(q2[0]);
+                sqv[1][mb] = word_as_float(q2[1]);
+            }
+        }
+        int4_t d[2][MB][NT];
+#pragma unroll
+        for (int gp = 0; gp < 2; gp++)
+#pragma unroll
+            for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++) d[gp][mb][nt] = mfma_dot(bfr[gp][nt], afr[gp][mb]);
+#pragma unroll
+        for (int gp = 0; gp < 2; gp++) {
+            if (gp == 1 && !g1) break;
+#pragma unroll
+            for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+                    for (int v = 0; v < 4; v++) {
+                        acc[mb][nt][v] = __builtin_fmaf(dotv(d[gp][mb][nt][v]), __fmul_rn(swv[gp][nt][v], sxv[gp][mb]),
+                                                        acc[mb][nt][v]);
+                        if (AFF)
+                            acc[mb][nt][v] = __builtin_fmaf(ofv[gp][AFF ? nt : 0][v], sqv[gp][mb], acc[mb][nt][v]);
+                    }
+        }
+    };
+
     if (!nan_out) {
-        load_stage(0, 0, true);
-        for (int st = 0; st < steps; st++) {
-            const int cur = st & 1;
+        // the step loop unrolled by its two stages, so every LDS address is a
+        // per-lane offset fixed for the kernel plus an immediate
+        auto run_step = [&](auto stage, int st) {
+            constexpr int C = decltype(stage)::value;
             // this wave's loads of step st are done; the barrier covers every wave
             // (and every wave has finished reading the stage the next loads overwrite)
             __builtin_amdgcn_s_waitcnt(0x0F70);
             __builtin_amdgcn_s_barrier();
-            load_stage(cur ^ 1, st + 1, st + 1 < steps);
-            const uint8_t *xst = xs + cur * XSTAGE, *cst = cs + cur * CSTAGE;
-            const uint8_t *swst = sws + cur * SWSTAGE, *sxst = sxs + cur * SXSTAGE;
-            const uint8_t *ofst = ofs + (AFF ? cur * SWSTAGE : 0), *sqst = sqs + (AFF ? cur * SXSTAGE : 0);
-            fold_group(xst, cst, swst, sxst, ofst, sqst, 0);
-            if (2 * st + 1 < groups) fold_group(xst, cst, swst, sxst, ofst, sqst, 1);
+            load_stage(C ^ 1, st + 1, st + 1 < steps);
+            const uint8_t *xst = xs + C * XSTAGE, *cst = cs + C * CSTAGE;
+            const uint8_t *swst = sws + C * SWSTAGE, *sxst = sxs + C * SXSTAGE;
+            const uint8_t *ofst = ofs + (AFF ? C * SWSTAGE : 0), *sqst = sqs + (AFF ? C * SXSTAGE : 0);
+            const bool g1 = 2 * st + 1 < groups;
+            if constexpr (BATCH) {
+                fold_step(xst, cst, swst, sxst, ofst, sqst, g1);
+            } else {
+                fold_group(xst, cst, swst, sxst, ofst, sqst, 0);
+                if (g1) fold_group(xst, cst, swst, sxst, ofst, sqst, 1);
+            }
+        };
+        load_stage(0, 0, true);
+        for (int st = 0; st < steps; st += 2) {
+            run_step(std::integral_constant<int, 0>{}, st);
+            if (st + 1 < steps) run_step(std::integral_constant<int, 1>{}, st + 1);
         }
         __builtin_amdgcn_s_waitcnt(0x0F70);  // no LDS write in flight once the block ends
     }
@@ -2120,8 +2214,8 @@ __global__ __launch_bounds__(BM / 32 * 64) void mlp_pipe_kernel(
             for (int wgt = 0; wgt < 2; wgt++) {
                 const int t = wn * NT + nt;
                 const uint2_t wds = *(const uint2_t *)(cst + (wgt * 4 + t) * 1024 + lane * 16 + gp * 8);
-                const uint2_t lo = nibbles_to_i8(wds[0]), hi = nibbles_to_i8(wds[1]);
-                const int4_t b = int4_t{(int)lo[0], (int)lo[1], (int)hi[0], (int)hi[1]};
+                const uint2_t lo = nibbles_to_i8x16(wds[0]), hi = nibbles_to_i8x16(wds[1]);
+                const int4_t b = int4_t{(int)lo[0], (int)lo[1], (int)hi[0], (int)hi[1]};  // 16 * code
                 const float4_t s01 = *(const float4_t *)(swst + wgt * 512 + t * 128 + qd * 32);
                 const float4_t s23 = *(const float4_t *)(swst + wgt * 512 + t * 128 + qd * 32 + 16);
                 const float4_t sv = gp ? float4_t{s01[1], s01[3], s23[1], s23[3]} : float4_t{s01[0], s01[2], s23[0], s23[2]};
@@ -2144,28 +2238,33 @@ __global__ __launch_bounds__(BM / 32 * 64) void mlp_pipe_kernel(
             const float sxv = *(const float *)(sxst + r * 8 + gp * 4);
 #pragma unroll
             for (int nt = 0; nt < NT; nt++) {
-                const int4_t gd = mfma_i8_biased(gb[nt], afr);
-                const int4_t ud = mfma_i8_biased(ub[nt], afr);
+                const int4_t gd = mfma_i8_biased16(gb[nt], afr);
+                const int4_t ud = mfma_i8_biased16(ub[nt], afr);
 #pragma unroll
                 for (int v = 0; v < 4; v++) {
-                    ga[mb][nt][v] = __builtin_fmaf(dot_value(gd[v]), __fmul_rn(gs[nt][v], sxv), ga[mb][nt][v]);
-                    ua[mb][nt][v] = __builtin_fmaf(dot_value(ud[v]), __fmul_rn(us[nt][v], sxv), ua[mb][nt][v]);
+                    ga[mb][nt][v] = __builtin_fmaf(dot_value16(gd[v]), __fmul_rn(gs[nt][v], sxv), ga[mb][nt][v]);
+                    ua[mb][nt][v] = __builtin_fmaf(dot_value16(ud[v]), __fmul_rn(us[nt][v], sxv), ua[mb][nt][v]);
                 }
             }
         }
     };
 
     if (!nan_out) {
-        load_stage(0, 0, true);
-        for (int st = 0; st < steps; st++) {
-            const int cur = st & 1;
+        // unrolled by the two stages: every LDS address is a fixed per-lane offset plus an immediate
+        auto run_step = [&](auto stage, int st) {
+            constexpr int C = decltype(stage)::value;
             __builtin_amdgcn_s_waitcnt(0x0F70);
             __builtin_amdgcn_s_barrier();
-            load_stage(cur ^ 1, st + 1, st + 1 < steps);
-            const uint8_t *xst = xs + cur * XSTAGE, *cst = cs + cur * CSTAGE;
-            const uint8_t *swst = sws + cur * SWSTAGE, *sxst = sxs + cur * SXSTAGE;
+            load_stage(C ^ 1, st + 1, st + 1 < steps);
+            const uint8_t *xst = xs + C * XSTAGE, *cst = cs + C * CSTAGE;
+            const uint8_t *swst = sws + C * SWSTAGE, *sxst = sxs + C * SXSTAGE;
             fold_group(xst, cst, swst, sxst, 0);
             if (2 * st + 1 < groups) fold_group(xst, cst, swst, sxst, 1);
+        };
+        load_stage(0, 0, true);
+        for (int st = 0; st < steps; st += 2) {
+            run_step(std::integral_constant<int, 0>{}, st);
+            if (st + 1 < steps) run_step(std::integral_constant<int, 1>{}, st + 1);
         }
         __builtin_amdgcn_s_waitcnt(0x0F70);  // no LDS write in flight once the block ends
     }
