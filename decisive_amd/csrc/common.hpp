@@ -144,6 +144,21 @@ __device__ __forceinline__ int4_t mfma_i8_biased16(int4_t a, int4_t b) {
 __device__ __forceinline__ float dot_value16(int32_t biased) {
     return __fsub_rn(__builtin_bit_cast(float, biased), 786432.0f);
 }
+// One lane's 16 Q4 codes of a group (two packed words) as the MFMA operand 16 * code.
+__device__ __forceinline__ int4_t q4_operand16(uint32_t w0, uint32_t w1) {
+    const uint2_t lo = nibbles_to_i8x16(w0), hi = nibbles_to_i8x16(w1);
+    return int4_t{(int)lo[0], (int)lo[1], (int)hi[0], (int)hi[1]};
+}
+// The group dot of weight codes of BITS bits: Q4 operands from q4_operand16,
+// Q8 operands as they are; dot_of<BITS> of each result is f32(dot), exactly.
+template <int BITS>
+__device__ __forceinline__ int4_t mfma_dot(int4_t a, int4_t b) {
+    return BITS == 4 ? mfma_i8_biased16(a, b) : mfma_i8_biased(a, b);
+}
+template <int BITS>
+__device__ __forceinline__ float dot_of(int32_t biased) {
+    return BITS == 4 ? dot_value16(biased) : dot_value(biased);
+}
 
 __device__ __forceinline__ float f16_bits_to_float(uint32_t h) {
     return (float)__builtin_bit_cast(half_t, (unsigned short)h);

@@ -75,8 +75,7 @@ __global__ __launch_bounds__(256) void grouped_kernel(const uint8_t *__restrict_
             if (BITS == 4) {
                 const int kb = g >> 1, s0 = (g & 1) * 2;
                 uint2_t wds = *(const uint2_t *)(codes + q4_lane(t, kb, kbs, qd, j) + s0 * 4);
-                uint2_t lo = nibbles_to_i8(wds[0]), hi = nibbles_to_i8(wds[1]);
-                b = int4_t{(int)lo[0], (int)lo[1], (int)hi[0], (int)hi[1]};
+                b = q4_operand16(wds[0], wds[1]);
                 if (arow_ok) {
                     uint2_t a0 = *(const uint2_t *)(qrow + g * 64 + qd * 8);
                     uint2_t a1 = *(const uint2_t *)(qrow + g * 64 + 32 + qd * 8);
@@ -110,10 +109,10 @@ __global__ __launch_bounds__(256) void grouped_kernel(const uint8_t *__restrict_
 #pragma unroll
         for (int u = 0; u < B; u++) {
             if (g0 + u >= groups) break;
-            const int4_t d = mfma_i8_biased(bt.a[u], bt.b[u]);
+            const int4_t d = mfma_dot<BITS>(bt.a[u], bt.b[u]);
 #pragma unroll
             for (int v = 0; v < 4; v++) {
-                acc[v] = __builtin_fmaf(dot_value(d[v]), __fmul_rn(bt.sw[u], bt.sx[u][v]), acc[v]);
+                acc[v] = __builtin_fmaf(dot_of<BITS>(d[v]), __fmul_rn(bt.sw[u], bt.sx[u][v]), acc[v]);
                 if (AFF) acc[v] = __builtin_fmaf(bt.ofs[AFF ? u : 0], bt.sq[AFF ? u : 0][v], acc[v]);
             }
         }
@@ -181,6 +180,11 @@ __global__ __launch_bounds__(kGvWaves * 64) void grouped_gemv_kernel(
     float *__restrict__ y, const int *__restrict__ bad_in, int *__restrict__ bad_out,
     const uint8_t *__restrict__ offsets = nullptr) {
     static_assert(!AFF || (AMODE == 0 && !PROJECT && BITS == 4), "affine offsets: Q4 weights, f32 activations");
+    // Q4 codes as the 16 * code operand (q4_operand16) where it keeps the
+    // kernel within 64 VGPRs (8 waves per SIMD); from MPAD 4 its extra
+    // register costs a wave per SIMD (M = 4: 10.4 against 13.6 us at
+    // K = 2560, N = 9216), so the plain codes go in there. Same dots either way.
+    constexpr bool X16 = BITS == 4 && MPAD <= 2;
     using S = GvShape<MPAD, AFF>;
     extern __shared__ __align__(16) uint8_t lds[];
     float *asx = (float *)(lds + S::ACODE_ALL);
@@ -320,8 +324,12 @@ __global__ __launch_bounds__(kGvWaves * 64) void grouped_gemv_kernel(
             int4_t av = {0, 0, 0, 0}, bv;
             if (BITS == 4) {
                 const uint4_t w = bq[gg / 2];
-                const uint2_t lo = nibbles_to_i8(w[(gg % 2) * 2]), hi = nibbles_to_i8(w[(gg % 2) * 2 + 1]);
-                bv = int4_t{(int)lo[0], (int)lo[1], (int)hi[0], (int)hi[1]};
+                if (X16) {
+                    bv = q4_operand16(w[(gg % 2) * 2], w[(gg % 2) * 2 + 1]);
+                } else {
+                    const uint2_t lo = nibbles_to_i8(w[(gg % 2) * 2]), hi = nibbles_to_i8(w[(gg % 2) * 2 + 1]);
+                    bv = int4_t{(int)lo[0], (int)lo[1], (int)hi[0], (int)hi[1]};
+                }
                 if (i < MPAD) {
                     const uint2_t a0 = *(const uint2_t *)(acode + i * S::ASTRIDE + gg * 64 + qd * 8);
                     const uint2_t a1 = *(const uint2_t *)(acode + i * S::ASTRIDE + gg * 64 + 32 + qd * 8);
@@ -331,7 +339,7 @@ __global__ __launch_bounds__(kGvWaves * 64) void grouped_gemv_kernel(
                 bv = __builtin_bit_cast(int4_t, bq[gg]);
                 if (i < MPAD) av = *(const int4_t *)(acode + i * S::ASTRIDE + gg * 64 + qd * 16);
             }
-            const int4_t d = mfma_i8_biased(av, bv);
+            const int4_t d = X16 ? mfma_i8_biased16(av, bv) : mfma_i8_biased(av, bv);
 #pragma unroll
             for (int v = 0; v < 4; v++) {
                 const int r = qd * 4 + v;
@@ -342,7 +350,8 @@ __global__ __launch_bounds__(kGvWaves * 64) void grouped_gemv_kernel(
         if (folds) {
             const int end = min(groups - w0, kGvWindow);
             for (int gw = 0; gw < end; gw++) {
-                const float dot = dot_value(dots[(gw * MPAD + fr) * 16 + fc]);
+                const int32_t biased = dots[(gw * MPAD + fr) * 16 + fc];
+                const float dot = X16 ? dot_value16(biased) : dot_value(biased);
                 const float sxv = asx[fr * kGvWindow + gw], swv2 = sw[gw * 16 + fc];
                 if (PROJECT)
                     acc = __fadd_rn(acc, __fmul_rn(dot, __fmul_rn(sxv, swv2)));
@@ -389,12 +398,8 @@ __global__ __launch_bounds__(256) void mlp_requant_kernel(
         }
         uint2_t gw = *(const uint2_t *)(gcodes + q4_lane(t, kb, kbs, qd, j) + s0 * 4);
         uint2_t uw = *(const uint2_t *)(ucodes + q4_lane(t, kb, kbs, qd, j) + s0 * 4);
-        uint2_t g0 = nibbles_to_i8(gw[0]), g1 = nibbles_to_i8(gw[1]);
-        uint2_t u0 = nibbles_to_i8(uw[0]), u1 = nibbles_to_i8(uw[1]);
-        int4_t gb = {(int)g0[0], (int)g0[1], (int)g1[0], (int)g1[1]};
-        int4_t ub = {(int)u0[0], (int)u0[1], (int)u1[0], (int)u1[1]};
-        int4_t gd = mfma_i8_biased(a, gb);
-        int4_t ud = mfma_i8_biased(a, ub);
+        const int4_t gb = q4_operand16(gw[0], gw[1]), ub = q4_operand16(uw[0], uw[1]);
+        const int4_t gd = mfma_i8_biased16(a, gb), ud = mfma_i8_biased16(a, ub);
         size_t rec = (((size_t)t * kbs + kb) * 16 + j) * 8;
         float gs = ((const float *)(gscales + rec))[g & 1];
         float us = ((const float *)(uscales + rec))[g & 1];
@@ -402,8 +407,8 @@ __global__ __launch_bounds__(256) void mlp_requant_kernel(
         for (int v = 0; v < 4; v++) {
             int r = mt * 16 + qd * 4 + v;
             float sxv = r < m ? sx[(size_t)r * groups + g] : 0.0f;
-            ga[v] = __builtin_fmaf(dot_value(gd[v]), __fmul_rn(gs, sxv), ga[v]);
-            ua[v] = __builtin_fmaf(dot_value(ud[v]), __fmul_rn(us, sxv), ua[v]);
+            ga[v] = __builtin_fmaf(dot_value16(gd[v]), __fmul_rn(gs, sxv), ga[v]);
+            ua[v] = __builtin_fmaf(dot_value16(ud[v]), __fmul_rn(us, sxv), ua[v]);
         }
     }
     float4_t val;
@@ -1922,14 +1927,6 @@ __global__ __launch_bounds__(WGM *WGN * 64) void grouped_pipe_kernel(
     const bool nan_out = bad != nullptr && *bad != 0;
     const int steps = (groups + 1) / 2;
 
-    // Q4 codes enter the MFMA as 16 * code (nibbles_to_i8x16 with kDotBias16),
-    // Q8 codes as they are (kDotBias); either way dotv gives f32(dot) exactly
-    auto q4_frag = [](uint32_t w0, uint32_t w1) {
-        const uint2_t lo = nibbles_to_i8x16(w0), hi = nibbles_to_i8x16(w1);
-        return int4_t{(int)lo[0], (int)lo[1], (int)hi[0], (int)hi[1]};
-    };
-    auto mfma_dot = [](int4_t b, int4_t a) { return BITS == 4 ? mfma_i8_biased16(b, a) : mfma_i8_biased(b, a); };
-    auto dotv = [](int32_t d) { return BITS == 4 ? dot_value16(d) : dot_value(d); };
     auto x_frag = [&](const uint8_t *xst, int r, int gp) {
         if (BITS == 4) {
             const int c1 = 4 * gp + qd / 2, c2 = c1 + 2;
@@ -1952,7 +1949,7 @@ __global__ __launch_bounds__(WGM *WGN * 64) void grouped_pipe_kernel(
             const int t = wn * NT + nt;
             if (BITS == 4) {
                 const uint2_t wds = *(const uint2_t *)(cst + t * 1024 + lane * 16 + gp * 8);
-                bfr[nt] = q4_frag(wds[0], wds[1]);
+                bfr[nt] = q4_operand16(wds[0], wds[1]);
                 const float4_t s01 = *(const float4_t *)(swst + t * 128 + qd * 32);       // rows 4qd, 4qd+1
                 const float4_t s23 = *(const float4_t *)(swst + t * 128 + qd * 32 + 16);  // rows 4qd+2, 4qd+3
                 swv[nt] = gp ? float4_t{s01[1], s01[3], s23[1], s23[3]} : float4_t{s01[0], s01[2], s23[0], s23[2]};
@@ -1975,10 +1972,10 @@ __global__ __launch_bounds__(WGM *WGN * 64) void grouped_pipe_kernel(
             const float sqv = AFF ? *(const float *)(sqst + r * 8 + gp * 4) : 0.0f;
 #pragma unroll
             for (int nt = 0; nt < NT; nt++) {
-                const int4_t d = mfma_dot(bfr[nt], afr);
+                const int4_t d = mfma_dot<BITS>(bfr[nt], afr);
 #pragma unroll
                 for (int v = 0; v < 4; v++) {
-                    acc[mb][nt][v] = __builtin_fmaf(dotv(d[v]), __fmul_rn(swv[nt][v], sxv), acc[mb][nt][v]);
+                    acc[mb][nt][v] = __builtin_fmaf(dot_of<BITS>(d[v]), __fmul_rn(swv[nt][v], sxv), acc[mb][nt][v]);
                     if (AFF) acc[mb][nt][v] = __builtin_fmaf(ofv[AFF ? nt : 0][v], sqv, acc[mb][nt][v]);
                 }
             }
@@ -1998,8 +1995,8 @@ __global__ __launch_bounds__(WGM *WGN * 64) void grouped_pipe_kernel(
             const int t = wn * NT + nt;
             if (BITS == 4) {
                 const uint4_t wds = *(const uint4_t *)(cst + t * 1024 + lane * 16);  // group 0: words 0, 1
-                bfr[0][nt] = q4_frag(wds[0], wds[1]);
-                bfr[1][nt] = q4_frag(wds[2], wds[3]);
+                bfr[0][nt] = q4_operand16(wds[0], wds[1]);
+                bfr[1][nt] = q4_operand16(wds[2], wds[3]);
                 const float4_t s01 = *(const float4_t *)(swst + t * 128 + qd * 32);
                 const float4_t s23 = *(const float4_t *)(swst + t * 128 + qd * 32 + 16);
                 swv[0][nt] = float4_t{s01[0], s01[2], s23[0], s23[2]};
@@ -2040,7 +2037,7 @@ __global__ __launch_bounds__(WGM *WGN * 64) void grouped_pipe_kernel(
 #pragma unroll
             for (int mb = 0; mb < MB; mb++)
 #pragma unroll
-                for (int nt = 0; nt < NT; nt++) d[gp][mb][nt] = mfma_dot(bfr[gp][nt], afr[gp][mb]);
+                for (int nt = 0; nt < NT; nt++) d[gp][mb][nt] = mfma_dot<BITS>(bfr[gp][nt], afr[gp][mb]);
 #pragma unroll
         for (int gp = 0; gp < 2; gp++) {
             if (gp == 1 && !g1) break;
@@ -2050,7 +2047,7 @@ __global__ __launch_bounds__(WGM *WGN * 64) void grouped_pipe_kernel(
                 for (int nt = 0; nt < NT; nt++)
 #pragma unroll
                     for (int v = 0; v < 4; v++) {
-                        acc[mb][nt][v] = __builtin_fmaf(dotv(d[gp][mb][nt][v]), __fmul_rn(swv[gp][nt][v], sxv[gp][mb]),
+                        acc[mb][nt][v] = __builtin_fmaf(dot_of<BITS>(d[gp][mb][nt][v]), __fmul_rn(swv[gp][nt][v], sxv[gp][mb]),
                                                         acc[mb][nt][v]);
                         if (AFF)
                             acc[mb][nt][v] = __builtin_fmaf(ofv[gp][AFF ? nt : 0][v], sqv[gp][mb], acc[mb][nt][v]);
