@@ -225,7 +225,8 @@ int32_t dz_linear(dz_ctx *ctx, const dz_weight *w, const void *x_dev, int32_t x_
 /* No counterpart in the reference: dz_linear for callers that cannot
  * allocate device memory (code recorded under graph capture, serving loops,
  * harnesses that forbid hipMalloc). Same arguments, results and bits as
- * dz_linear; it calls no allocator. The grouped modes at m > 16 keep the A8
+ * dz_linear; it calls no allocator. The grouped modes from m = 5 (m > 16 for
+ * affine fitted weights) keep the A8
  * codes, scales and non-finite flag in a static 16 MiB device array (one per
  * GPU, held until the process ends), so 256 + round256(m*G*64) + m*G*4 bytes
  * (G = ceil(cols/64)) must fit 16 MiB: up to 3,855 rows at cols 4096, 6,168 at

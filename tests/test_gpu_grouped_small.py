@@ -95,8 +95,9 @@ def test_records_need_whole_groups(ctx):
 @pytest.mark.parametrize("wb,ab", [(4, 8), (8, 8), (4, 4), (8, 4)])
 @pytest.mark.parametrize("k,n", [(100, 17), (1000, 50), (4096, 64)])
 def test_every_row_count_up_to_16_matches_the_avx2_order(ctx, oracle, wb, ab, k, n):
-    """M = 1..16 runs the few-row kernel (quantization inside, tails zero
-    padded as int8.rs:178-202 does); the codes + scales entry (dz_linear_q8)
+    """M = 1..16 runs the few-row kernel: up to 4 rows it quantizes x in
+    every block, from 5 rows over codes quantized once (tails zero padded as
+    int8.rs:178-202 does either way); the codes + scales entry (dz_linear_q8)
     gives the same bits."""
     torch = pytest.importorskip("torch")
     rng = np.random.default_rng(k + n + wb + ab)
@@ -117,11 +118,16 @@ def test_every_row_count_up_to_16_matches_the_avx2_order(ctx, oracle, wb, ab, k,
 
 
 def test_few_rows_nonfinite_activation_makes_every_output_nan(ctx, oracle):
-    """int8.rs:170-173: one non-finite activation anywhere -> every output NaN."""
+    """int8.rs:170-173: one non-finite activation anywhere -> every output NaN,
+    whether the kernel quantizes (3 rows) or takes codes quantized once (12)."""
     torch = pytest.importorskip("torch")
     _, _, w = _weight(ctx, oracle, 40, 256, 4, 9)
-    x = np.ones((3, 256), np.float32)
-    x[2, 200] = np.nan
-    y = empty((3, 40), torch.float32)
-    ctx.linear(w, dev(x), rocm.F32, 3, y, rocm.W4A8)
-    assert np.isnan(host(ctx, y)).all()
+    for m in (3, 12):
+        x = np.ones((m, 256), np.float32)
+        x[m - 1, 200] = np.nan
+        y = empty((m, 40), torch.float32)
+        ctx.linear(w, dev(x), rocm.F32, m, y, rocm.W4A8)
+        assert np.isnan(host(ctx, y)).all(), m
+        x[m - 1, 200] = 1.0  # the flag is the call's own: a clean call after it is finite
+        ctx.linear(w, dev(x), rocm.F32, m, y, rocm.W4A8)
+        assert not np.isnan(host(ctx, y)).any(), m
