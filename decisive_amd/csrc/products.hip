@@ -1799,43 +1799,49 @@ __global__ __launch_bounds__(WGM *WGN * 64) void w4a16_pipe_kernel(
 // dot taken by v_mfma_i32_16x16x64_i8:
 //     acc = fma(f32(dot_g), sw[g][c] * sx[r][g], acc)   for g = 0, 1, ... in order,
 // so the outputs equal grouped_kernel's (and the oracle's) bit for bit.
-// Block tile BM x BN on WGM x WGN waves; one k-step covers two 64-groups, in
-// two LDS stages filled by buffer_load ... lds while the other is computed:
-//  - activation codes: BM rows x 128 bytes (chunk c of row r at slot
-//    c ^ ((r >> 1) & 7), conflict-free for the 16 rows of a fragment read);
-//  - weight codes: Q4 one 1 KiB tile16x128 chunk per 16-column tile, Q8 two
+// Block tile BM x BN on WGM x WGN waves; one k-step covers GS 64-groups (2 or
+// 4), in two LDS stages filled by buffer_load ... lds while the other is
+// computed:
+//  - activation codes: BM rows x 64 GS bytes (chunk c of row r at slot
+//    c ^ swz(r), swz(r) = (r >> 1) & 7 for 128-byte rows and r & 15 for
+//    256-byte rows: conflict-free for the 16 rows of a fragment read);
+//  - weight codes: Q4 GS/2 1 KiB tile16x128 chunks per 16-column tile, Q8 GS
 //    1 KiB tile16x64 chunks;
-//  - weight scales: 128 bytes per tile (Q4: [row][group] f32 pairs, Q8:
-//    [group][row]); activation scales: BM rows x 2 f32.
+//  - weight scales: 64 GS bytes per tile, as [k-step pair][tile][128 B] (Q4:
+//    [row][group] f32 pairs, Q8: [group][row]); activation scales: BM rows x
+//    GS f32.
 // The MFMA takes the weight operand first, so lane (q, j) holds the dots of
 // four consecutive output columns of one row: its weight scales are one
 // 16-byte LDS read and its activation scale one 4-byte read. The fold (the
 // dot as f32, the scale product and the fma per output and group) is VALU
 // work and bounds the kernel; the MFMAs take about a third of its time.
-// Groups past `groups` (the odd tail of a k-step) are not folded.
+// Groups past `groups` (the tail of a k-step) are not folded.
 // AFF (fitted affine Q4, int8.rs:566-571): the offsets (the group-64 scale
 // layout) and sxq = sx * f32(sum of the row's group codes) are staged like the
 // scales, and each group's fold is followed by acc = fma(offset, sxq, acc).
-template <int BITS, int BM, int BN, int WGM, int WGN, bool AFF = false>
+template <int BITS, int BM, int BN, int WGM, int WGN, bool AFF = false, int GS = 2>
 __global__ __launch_bounds__(WGM *WGN * 64) void grouped_pipe_kernel(
     const uint8_t *__restrict__ codes, const uint8_t *__restrict__ scales, const int8_t *__restrict__ q,
     const float *__restrict__ sx, int m, int n, int groups, int kbs, float *y, const float *res,
     const int *__restrict__ bad, const uint8_t *__restrict__ offsets = nullptr,
     const float *__restrict__ sxq = nullptr) {
     static_assert(!AFF || BITS == 4, "affine offsets are a Q4 form");
+    static_assert(GS == 2 || GS == 4, "two or four groups per k-step");
     constexpr int WAVES = WGM * WGN;
     constexpr int TM = BM / WGM, TN = BN / WGN, MB = TM / 16, NT = TN / 16;
     constexpr int TILES = BN / 16;
-    constexpr int XSTAGE = BM * 128;
-    constexpr int CSTAGE = TILES * (BITS == 4 ? 1024 : 2048);
-    constexpr int SWSTAGE = TILES * 128;
-    constexpr int SXSTAGE = BM * 8;
-    // 1 KiB loads of a stage, dealt round robin to the waves: XI of 8
-    // activation rows, CI code chunks, SI of 64 activation-scale pairs
-    constexpr int XI = BM / 8, CI = CSTAGE / 1024, SI = BM / 32;
+    constexpr int ROWB = 64 * GS, CH = ROWB / 16, RPI = 1024 / ROWB;  // row bytes, chunks, rows per 1 KiB
+    constexpr int KBS = GS / 2;                                         // Q4 k-blocks (and scale pairs) per step
+    constexpr int XSTAGE = BM * ROWB;
+    constexpr int CSTAGE = TILES * 1024 * (BITS == 4 ? KBS : GS);
+    constexpr int SWSTAGE = TILES * 128 * KBS;
+    constexpr int SXSTAGE = BM * 4 * GS;
+    // 1 KiB loads of a stage, dealt round robin to the waves: XI of RPI
+    // activation rows, CI code chunks, SI of 64 activation scales
+    constexpr int XI = BM / RPI, CI = CSTAGE / 1024, SI = BM * GS / 64;
     constexpr int XPW = (XI + WAVES - 1) / WAVES, CPW = (CI + WAVES - 1) / WAVES, SPW = (SI + WAVES - 1) / WAVES;
-    static_assert(BM % 32 == 0 && XI * 8 == BM && SI * 32 == BM, "whole 1 KiB activation and 256 B scale loads");
-    static_assert(TILES == 8, "one 1 KiB weight-scale load per stage");
+    static_assert(XI * RPI == BM && SI * 64 == BM * GS, "whole 1 KiB activation and 256 B scale loads");
+    static_assert(TILES == 8, "one 1 KiB weight-scale load per k-step pair");
     __shared__ __align__(16) uint8_t xs[2 * XSTAGE];
     __shared__ __align__(16) uint8_t cs[2 * CSTAGE];
     __shared__ __align__(16) uint8_t sws[2 * SWSTAGE];
@@ -1868,13 +1874,16 @@ __global__ __launch_bounds__(WGM *WGN * 64) void grouped_pipe_kernel(
         ofs_lds = lds_address(ofs);
         sqs_lds = lds_address(sqs);
     }
+    auto swz = [](int r) { return GS == 2 ? (r >> 1) & 7 : r & 15; };
 
-    // activation loads: lane l of instruction blk fills slot l % 8 of row
-    // 8*blk + l/8; the swizzle depends on blk only through its parity
-    const int lrow = lane / 8;
-    const uint32_t xoff[2] = {
-        (uint32_t)(lrow * rowbytes + (((lane % 8) ^ ((lrow >> 1) & 7)) * 16)),
-        (uint32_t)(lrow * rowbytes + (((lane % 8) ^ (((lrow + 8) >> 1) & 7)) * 16))};
+    // activation loads: lane l of instruction blk fills slot l % CH of row
+    // RPI*blk + l/CH; the swizzle depends on blk only through blk % NX
+    constexpr int NX = GS == 2 ? 2 : 4;
+    const int lrow = lane / CH;
+    uint32_t xoff[NX];
+#pragma unroll
+    for (int u = 0; u < NX; u++)
+        xoff[u] = (uint32_t)(lrow * rowbytes + (((lane % CH) ^ swz(lrow + RPI * u)) * 16));
     auto load_stage = [&](int stage, int st, bool live) {
         const int32x4_t nq = live ? rq : int32x4_t{rq[0], rq[1], 0, rq[3]};
         const int32x4_t nc = live ? rc : int32x4_t{rc[0], rc[1], 0, rc[3]};
@@ -1887,34 +1896,41 @@ __global__ __launch_bounds__(WGM *WGN * 64) void grouped_pipe_kernel(
             const int blk = wave + p * WAVES;
             if (XI % WAVES == 0 || blk < XI)
                 dma16(__builtin_amdgcn_readfirstlane(xs_lds + stage * XSTAGE + blk * 1024),
-                      xoff[blk & 1] + (uint32_t)(blk * 8) * rowbytes + (uint32_t)st * 128, nq);
+                      xoff[blk % NX] + (uint32_t)(blk * RPI) * rowbytes + (uint32_t)st * ROWB, nq);
         }
 #pragma unroll
         for (int p = 0; p < CPW; p++) {
-            const int ci = wave + p * WAVES;  // Q4: tile; Q8: tile * 2 + group of the step
-            const int t = BITS == 4 ? ci : ci / 2;
-            const int kc = BITS == 4 ? st : 2 * st + ci % 2;
+            // Q4: chunk ci is k-block ci % KBS of the step for tile ci / KBS; Q8: group ci % GS
+            const int ci = wave + p * WAVES;
+            const int per = BITS == 4 ? KBS : GS;
+            const int t = ci / per, kc = st * per + ci % per;
             if (CI % WAVES == 0 || ci < CI)
                 dma16(__builtin_amdgcn_readfirstlane(cs_lds + stage * CSTAGE + ci * 1024),
                       (uint32_t)((t * kbs + kc) * 1024 + lane * 16), nc);
         }
         if (wave == WAVES - 1) {
-            const int t = lane / 8;
-            const uint32_t off = BITS == 4 ? (uint32_t)(t * kbs + st) * 128 : (uint32_t)(t * groups + 2 * st) * 64;
-            dma16(__builtin_amdgcn_readfirstlane(sws_lds + stage * SWSTAGE), off + (uint32_t)(lane % 8) * 16, nw);
-            if (AFF)
-                dma16(__builtin_amdgcn_readfirstlane(ofs_lds + stage * SWSTAGE), off + (uint32_t)(lane % 8) * 16, no);
+#pragma unroll
+            for (int u = 0; u < KBS; u++) {  // one 1 KiB load per pair of groups: lane -> tile l/8, piece l%8
+                const int t = lane / 8;
+                const uint32_t off = BITS == 4 ? (uint32_t)(t * kbs + st * KBS + u) * 128
+                                               : (uint32_t)(t * groups + GS * st + 2 * u) * 64;
+                const uint32_t lds = sws_lds + stage * SWSTAGE + u * TILES * 128;
+                dma16(__builtin_amdgcn_readfirstlane(lds), off + (uint32_t)(lane % 8) * 16, nw);
+                if (AFF)
+                    dma16(__builtin_amdgcn_readfirstlane(ofs_lds + stage * SWSTAGE + u * TILES * 128),
+                          off + (uint32_t)(lane % 8) * 16, no);
+            }
         }
 #pragma unroll
         for (int p = 0; p < SPW; p++) {
             const int si = wave + p * WAVES;
-            const int r = si * 32 + lane / 2;
+            const int r = si * (64 / GS) + lane / GS;
             if (SI % WAVES == 0 || si < SI) {
                 dma4(__builtin_amdgcn_readfirstlane(sxs_lds + stage * SXSTAGE + si * 256),
-                     (uint32_t)((r * groups + 2 * st + (lane & 1)) * 4), ns);
+                     (uint32_t)((r * groups + GS * st + lane % GS) * 4), ns);
                 if (AFF)
                     dma4(__builtin_amdgcn_readfirstlane(sqs_lds + stage * SXSTAGE + si * 256),
-                         (uint32_t)((r * groups + 2 * st + (lane & 1)) * 4), nsq);
+                         (uint32_t)((r * groups + GS * st + lane % GS) * 4), nsq);
             }
         }
     };
@@ -1925,17 +1941,34 @@ __global__ __launch_bounds__(WGM *WGN * 64) void grouped_pipe_kernel(
 #pragma unroll
         for (int b = 0; b < NT; b++) acc[a][b] = float4_t{0.f, 0.f, 0.f, 0.f};
     const bool nan_out = bad != nullptr && *bad != 0;
-    const int steps = (groups + 1) / 2;
+    const int steps = (groups + GS - 1) / GS;
 
     auto x_frag = [&](const uint8_t *xst, int r, int gp) {
         if (BITS == 4) {
             const int c1 = 4 * gp + qd / 2, c2 = c1 + 2;
-            const uint2_t a0 = *(const uint2_t *)(xst + r * 128 + ((c1 ^ ((r >> 1) & 7)) * 16) + 8 * (qd & 1));
-            const uint2_t a1 = *(const uint2_t *)(xst + r * 128 + ((c2 ^ ((r >> 1) & 7)) * 16) + 8 * (qd & 1));
+            const uint2_t a0 = *(const uint2_t *)(xst + r * ROWB + ((c1 ^ swz(r)) * 16) + 8 * (qd & 1));
+            const uint2_t a1 = *(const uint2_t *)(xst + r * ROWB + ((c2 ^ swz(r)) * 16) + 8 * (qd & 1));
             return int4_t{(int)a0[0], (int)a0[1], (int)a1[0], (int)a1[1]};
         }
         const int c = 4 * gp + qd;
-        return *(const int4_t *)(xst + r * 128 + ((c ^ ((r >> 1) & 7)) * 16));
+        return *(const int4_t *)(xst + r * ROWB + ((c ^ swz(r)) * 16));
+    };
+    // group gp's weight fragment, scales (and offsets) of tile t
+    auto w_frag = [&](const uint8_t *cst, int t, int gp) {
+        if (BITS == 4) {
+            const uint2_t wds = *(const uint2_t *)(cst + (t * KBS + gp / 2) * 1024 + lane * 16 + (gp % 2) * 8);
+            return q4_operand16(wds[0], wds[1]);
+        }
+        return *(const int4_t *)(cst + (t * GS + gp) * 1024 + lane * 16);
+    };
+    auto w_scales = [&](const uint8_t *swst, int t, int gp) {
+        const uint8_t *rec = swst + (gp / 2) * TILES * 128 + t * 128;
+        if (BITS == 4) {
+            const float4_t s01 = *(const float4_t *)(rec + qd * 32);       // rows 4qd, 4qd+1
+            const float4_t s23 = *(const float4_t *)(rec + qd * 32 + 16);  // rows 4qd+2, 4qd+3
+            return gp % 2 ? float4_t{s01[1], s01[3], s23[1], s23[3]} : float4_t{s01[0], s01[2], s23[0], s23[2]};
+        }
+        return *(const float4_t *)(rec + (gp % 2) * 64 + qd * 16);
     };
 
     // one group of a stage: weight fragments and scales once, then per row
@@ -1947,29 +1980,16 @@ __global__ __launch_bounds__(WGM *WGN * 64) void grouped_pipe_kernel(
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) {
             const int t = wn * NT + nt;
-            if (BITS == 4) {
-                const uint2_t wds = *(const uint2_t *)(cst + t * 1024 + lane * 16 + gp * 8);
-                bfr[nt] = q4_operand16(wds[0], wds[1]);
-                const float4_t s01 = *(const float4_t *)(swst + t * 128 + qd * 32);       // rows 4qd, 4qd+1
-                const float4_t s23 = *(const float4_t *)(swst + t * 128 + qd * 32 + 16);  // rows 4qd+2, 4qd+3
-                swv[nt] = gp ? float4_t{s01[1], s01[3], s23[1], s23[3]} : float4_t{s01[0], s01[2], s23[0], s23[2]};
-                if (AFF) {
-                    const float4_t o01 = *(const float4_t *)(ofst + t * 128 + qd * 32);
-                    const float4_t o23 = *(const float4_t *)(ofst + t * 128 + qd * 32 + 16);
-                    ofv[AFF ? nt : 0] =
-                        gp ? float4_t{o01[1], o01[3], o23[1], o23[3]} : float4_t{o01[0], o01[2], o23[0], o23[2]};
-                }
-            } else {
-                bfr[nt] = *(const int4_t *)(cst + (t * 2 + gp) * 1024 + lane * 16);
-                swv[nt] = *(const float4_t *)(swst + t * 128 + gp * 64 + qd * 16);
-            }
+            bfr[nt] = w_frag(cst, t, gp);
+            swv[nt] = w_scales(swst, t, gp);
+            if (AFF) ofv[AFF ? nt : 0] = w_scales(ofst, t, gp);
         }
 #pragma unroll
         for (int mb = 0; mb < MB; mb++) {
             const int r = wm * TM + mb * 16 + j;
             const int4_t afr = x_frag(xst, r, gp);
-            const float sxv = *(const float *)(sxst + r * 8 + gp * 4);
-            const float sqv = AFF ? *(const float *)(sqst + r * 8 + gp * 4) : 0.0f;
+            const float sxv = *(const float *)(sxst + r * 4 * GS + gp * 4);
+            const float sqv = AFF ? *(const float *)(sqst + r * 4 * GS + gp * 4) : 0.0f;
 #pragma unroll
             for (int nt = 0; nt < NT; nt++) {
                 const int4_t d = mfma_dot<BITS>(bfr[nt], afr);
@@ -1983,72 +2003,62 @@ __global__ __launch_bounds__(WGM *WGN * 64) void grouped_pipe_kernel(
     };
 
     // Small wave tiles (MB * NT <= 4) take a whole k-step at once: every LDS
-    // read of both groups, then every MFMA, then the folds in group order, so
+    // read of its groups, then every MFMA, then the folds in group order, so
     // a wave waits once per step for its reads and once for its first dots.
     constexpr bool BATCH = MB * NT <= 4;
     auto fold_step = [&](const uint8_t *xst, const uint8_t *cst, const uint8_t *swst, const uint8_t *sxst,
-                         const uint8_t *ofst, const uint8_t *sqst, bool g1) {
-        int4_t bfr[2][NT];
-        float4_t swv[2][NT], ofv[2][AFF ? NT : 1];
+                         const uint8_t *ofst, const uint8_t *sqst, int live_groups) {
+        int4_t bfr[GS][NT];
+        float4_t swv[GS][NT], ofv[GS][AFF ? NT : 1];
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) {
             const int t = wn * NT + nt;
-            if (BITS == 4) {
-                const uint4_t wds = *(const uint4_t *)(cst + t * 1024 + lane * 16);  // group 0: words 0, 1
-                bfr[0][nt] = q4_operand16(wds[0], wds[1]);
-                bfr[1][nt] = q4_operand16(wds[2], wds[3]);
-                const float4_t s01 = *(const float4_t *)(swst + t * 128 + qd * 32);
-                const float4_t s23 = *(const float4_t *)(swst + t * 128 + qd * 32 + 16);
-                swv[0][nt] = float4_t{s01[0], s01[2], s23[0], s23[2]};
-                swv[1][nt] = float4_t{s01[1], s01[3], s23[1], s23[3]};
-                if (AFF) {
-                    const float4_t o01 = *(const float4_t *)(ofst + t * 128 + qd * 32);
-                    const float4_t o23 = *(const float4_t *)(ofst + t * 128 + qd * 32 + 16);
-                    ofv[0][AFF ? nt : 0] = float4_t{o01[0], o01[2], o23[0], o23[2]};
-                    ofv[1][AFF ? nt : 0] = float4_t{o01[1], o01[3], o23[1], o23[3]};
-                }
-            } else {
 #pragma unroll
-                for (int gp = 0; gp < 2; gp++) {
-                    bfr[gp][nt] = *(const int4_t *)(cst + (t * 2 + gp) * 1024 + lane * 16);
-                    swv[gp][nt] = *(const float4_t *)(swst + t * 128 + gp * 64 + qd * 16);
-                }
+            for (int gp = 0; gp < GS; gp++) {
+                bfr[gp][nt] = w_frag(cst, t, gp);
+                swv[gp][nt] = w_scales(swst, t, gp);
+                if (AFF) ofv[gp][AFF ? nt : 0] = w_scales(ofst, t, gp);
             }
         }
-        int4_t afr[2][MB];
-        float sxv[2][MB], sqv[2][MB];
+        int4_t afr[GS][MB];
+        float sxv[GS][MB], sqv[GS][MB];
 #pragma unroll
         for (int mb = 0; mb < MB; mb++) {
             const int r = wm * TM + mb * 16 + j;
-            afr[0][mb] = x_frag(xst, r, 0);
-            afr[1][mb] = x_frag(xst, r, 1);
-            const uint2_t s = *(const uint2_t *)(sxst + r * 8);
-            sxv[0][mb] = word_as_float(s[0]);
-            sxv[1][mb] = word_as_float(s[1]);
+#pragma unroll
+            for (int gp = 0; gp < GS; gp++) afr[gp][mb] = x_frag(xst, r, gp);
+            if (GS == 2) {
+                const uint2_t s2 = *(const uint2_t *)(sxst + r * 8);
+                sxv[0][mb] = word_as_float(s2[0]);
+                sxv[1][mb] = word_as_float(s2[1]);
+            } else {
+                const uint4_t s4 = *(const uint4_t *)(sxst + r * 16);
+#pragma unroll
+                for (int gp = 0; gp < GS; gp++) sxv[gp][mb] = word_as_float(s4[gp]);
+            }
             if (AFF) {
-                const uint2_t q2 = *(const uint2_t *)(sqst + r * 8);
-                sqv[0][mb] = word_as_float(q2[0]);
-                sqv[1][mb] = word_as_float(q2[1]);
+#pragma unroll
+                for (int gp = 0; gp < GS; gp++) sqv[gp][mb] = *(const float *)(sqst + r * 4 * GS + gp * 4);
             }
         }
-        int4_t d[2][MB][NT];
+        int4_t d[GS][MB][NT];
 #pragma unroll
-        for (int gp = 0; gp < 2; gp++)
+        for (int gp = 0; gp < GS; gp++)
 #pragma unroll
             for (int mb = 0; mb < MB; mb++)
 #pragma unroll
                 for (int nt = 0; nt < NT; nt++) d[gp][mb][nt] = mfma_dot<BITS>(bfr[gp][nt], afr[gp][mb]);
 #pragma unroll
-        for (int gp = 0; gp < 2; gp++) {
-            if (gp == 1 && !g1) break;
+        for (int gp = 0; gp < GS; gp++) {
+            if (gp >= live_groups) break;
 #pragma unroll
             for (int mb = 0; mb < MB; mb++)
 #pragma unroll
                 for (int nt = 0; nt < NT; nt++)
 #pragma unroll
                     for (int v = 0; v < 4; v++) {
-                        acc[mb][nt][v] = __builtin_fmaf(dot_of<BITS>(d[gp][mb][nt][v]), __fmul_rn(swv[gp][nt][v], sxv[gp][mb]),
-                                                        acc[mb][nt][v]);
+                        acc[mb][nt][v] = __builtin_fmaf(dot_of<BITS>(d[gp][mb][nt][v]),
+                                                        __fmul_rn(swv[gp][nt][v], sxv[gp][mb]), acc[mb][nt][v]);
                         if (AFF)
                             acc[mb][nt][v] = __builtin_fmaf(ofv[gp][AFF ? nt : 0][v], sqv[gp][mb], acc[mb][nt][v]);
                     }
@@ -2068,12 +2078,13 @@ __global__ __launch_bounds__(WGM *WGN * 64) void grouped_pipe_kernel(
             const uint8_t *xst = xs + C * XSTAGE, *cst = cs + C * CSTAGE;
             const uint8_t *swst = sws + C * SWSTAGE, *sxst = sxs + C * SXSTAGE;
             const uint8_t *ofst = ofs + (AFF ? C * SWSTAGE : 0), *sqst = sqs + (AFF ? C * SXSTAGE : 0);
-            const bool g1 = 2 * st + 1 < groups;
+            const int live = min(GS, groups - GS * st);
             if constexpr (BATCH) {
-                fold_step(xst, cst, swst, sxst, ofst, sqst, g1);
+                fold_step(xst, cst, swst, sxst, ofst, sqst, live);
             } else {
-                fold_group(xst, cst, swst, sxst, ofst, sqst, 0);
-                if (g1) fold_group(xst, cst, swst, sxst, ofst, sqst, 1);
+#pragma unroll
+                for (int gp = 0; gp < GS; gp++)
+                    if (gp < live) fold_group(xst, cst, swst, sxst, ofst, sqst, gp);
             }
         };
         load_stage(0, 0, true);
@@ -2329,7 +2340,7 @@ const char *const kI8Names[] = {"256x256p2w8", "256x256p4k64w8", "256x128p3w8", 
                                  "256x256p2w8-stream-mid", "256x128k64p2-stream2"};
 const char *const kGroupedNames[] = {"pipe-auto",    "pipe256x128w8", "wave16x16",   "pipe128x128w4",
                                      "pipe64x128w2", "pipe128x128m8", "pipe128x128n8", "pipe32x128w8",
-                                     "pipe64x128w8"};
+                                     "pipe64x128w8", "pipe32x128w8g4", "pipe64x128w8g4"};
 const char *const kMlpNames[] = {"pipe-auto", "pipe256x64w8", "pipe128x64w4", "wave16x64", "pipe256x64n2", "pipe128x64n2"};
 const char *const kDeltaNames[] = {"chunked64", "chunked64-c32", "recurrent", "recurrent-rolled", "auto"};
 const char *const kNormNames[] = {"fused", "separate"};
@@ -2557,7 +2568,7 @@ int variant_count(const char *family) {
     if (f == "gemv") return 5;
     if (f == "gemm_w4a16") return 10;
     if (f == "i8_gemm") return 10;
-    if (f == "grouped") return 9;
+    if (f == "grouped") return 11;
     if (f == "mlp") return 6;
     if (f == "delta_scan") return 5;
     if (f == "norm") return 2;
@@ -2627,20 +2638,20 @@ bool grouped_pipe_fits(const Weight &w, int bm) {
            (size_t)8 * w.kblocks() * 1024 < ((size_t)1 << 31);
 }
 
-template <int BM, int WGM, int WGN>
+template <int BM, int WGM, int WGN, int GS = 2>
 bool grouped_pipe_launch(const Weight &w, const int8_t *q, const float *sx, int m, float *y, const int *bad,
                          hipStream_t s, const float *res, const float *sxq) {
     if (!grouped_pipe_fits(w, BM)) return false;
     const dim3 blocks(cdiv(m, BM) * cdiv(w.rows, 128));
     if (w.offsets)
-        hipLaunchKernelGGL((grouped_pipe_kernel<4, BM, 128, WGM, WGN, true>), blocks, dim3(WGM * WGN * 64), 0, s,
+        hipLaunchKernelGGL((grouped_pipe_kernel<4, BM, 128, WGM, WGN, true, GS>), blocks, dim3(WGM * WGN * 64), 0, s,
                            w.codes, w.scales, q, sx, m, w.rows, w.groups, w.kblocks(), y, res, bad, w.offsets, sxq);
     else if (w.bits == 4)
-        hipLaunchKernelGGL((grouped_pipe_kernel<4, BM, 128, WGM, WGN>), blocks, dim3(WGM * WGN * 64), 0, s, w.codes,
-                           w.scales, q, sx, m, w.rows, w.groups, w.kblocks(), y, res, bad);
+        hipLaunchKernelGGL((grouped_pipe_kernel<4, BM, 128, WGM, WGN, false, GS>), blocks, dim3(WGM * WGN * 64), 0, s,
+                           w.codes, w.scales, q, sx, m, w.rows, w.groups, w.kblocks(), y, res, bad);
     else
-        hipLaunchKernelGGL((grouped_pipe_kernel<8, BM, 128, WGM, WGN>), blocks, dim3(WGM * WGN * 64), 0, s, w.codes,
-                           w.scales, q, sx, m, w.rows, w.groups, w.kblocks(), y, res, bad);
+        hipLaunchKernelGGL((grouped_pipe_kernel<8, BM, 128, WGM, WGN, false, GS>), blocks, dim3(WGM * WGN * 64), 0, s,
+                           w.codes, w.scales, q, sx, m, w.rows, w.groups, w.kblocks(), y, res, bad);
     return true;
 }
 
@@ -2648,21 +2659,27 @@ bool grouped_pipe_launch(const Weight &w, const int8_t *q, const float *sx, int 
 // 5 128x128 (4 waves side by side, each 128 rows x 32 columns), 6 128x128 (4
 // waves stacked, each 32 rows x 128 columns), 4 64x128 (2 waves), 7 32x128 (8
 // waves side by side, each 32 rows x 16 columns), 8 64x128 (8 waves as 2x4), 2
-// one wave per 16x16 tile. The fold is VALU work, so what decides is how many
-// waves keep every SIMD busy: 0 picks the side-by-side 128x128 tiles when
-// their grid gives every compute unit two blocks, else 64x128 on 8 waves when
-// that grid does, else 32x128 on 8 waves. Measured (us, 1024 rows unless
-// stated, 32x128w8 / 64x128w8 / 128x128 side by side): N=1024 K=2560 22 / 28
-// / 52; N=2560 K=9216 107 / 112 / 165; N=4096 K=2560 43 / 42 / 55; N=8192
-// K=2560 76 / 72 / 71; 4096 rows, N=8192: 271 / 238 / 218; 40 rows, N=8192:
-// 18 / 24 / 47 (the one-wave tiles 27). Every variant folds in group order:
-// all are bitwise equal.
+// one wave per 16x16 tile; 9 and 10 are 7 and 8 with four groups per k-step
+// instead of two. The fold is VALU work, so what decides is how many waves
+// keep every SIMD busy: 0 picks the side-by-side 128x128 tiles when their
+// grid gives every compute unit four blocks, else 64x128 on 8 waves when its
+// grid gives two, else 32x128 on 8 waves, with four groups per step when even
+// that grid gives a compute unit fewer than two blocks (half the barriers and
+// twice the work between a load and its use; on fuller grids it is 2-5%
+// slower). Measured (us, 1024 rows unless stated, 32x128w8 / 32x128w8g4 /
+// 64x128w8 / 128x128 side by side): N=1024 K=2560 18.6 / 16.4 / 22.2 / 47.5;
+// N=2560 K=9216 80.4 / 82.7 / 84.5 / 149; N=2560 K=4096 40.0 / 41.4 / 43.2 /
+// 72.3; N=8192 K=2560 59.0 / 62.4 / 53.4 / 57.3; 40 rows, N=8192: 14.5 / 12.9
+// / 18.2 / 42.3; 300 rows, N=2560: 15.7 / 14.1 / 19.5 / 45.1; 16384 rows,
+// K=4096, N=14336: 2210 / 2354 / 2025 / 1813. Every variant folds in group
+// order: all are bitwise equal.
 int grouped_pick(const Weight &w, int m, int variant) {
     if (variant != 0) return variant;
     const unsigned cus = (unsigned)device_cus(), tn = cdiv(w.rows, 128);
-    if (cdiv(m, 128) * tn >= 2 * cus) return 5;
+    if (cdiv(m, 128) * tn >= 4 * cus) return 5;
     if (cdiv(m, 64) * tn >= 2 * cus) return 8;
-    return 7;
+    if (cdiv(m, 32) * tn >= 2 * cus) return 7;
+    return 9;
 }
 
 // Activation rows per block of a pipelined pick (0: not a pipelined kernel).
@@ -2670,8 +2687,8 @@ int grouped_pipe_rows(int pick) {
     switch (pick) {
         case 1: return 256;
         case 3: case 5: case 6: return 128;
-        case 4: case 8: return 64;
-        case 7: return 32;
+        case 4: case 8: case 10: return 64;
+        case 7: case 9: return 32;
         default: return 0;
     }
 }
@@ -2693,6 +2710,8 @@ bool launch_grouped(const Weight &w, const int8_t *q, const float *sx, int m, fl
         case 6: if (grouped_pipe_launch<128, 4, 1>(w, q, sx, m, y, bad, s, res, sxq)) return true; break;
         case 7: if (grouped_pipe_launch<32, 1, 8>(w, q, sx, m, y, bad, s, res, sxq)) return true; break;
         case 8: if (grouped_pipe_launch<64, 2, 4>(w, q, sx, m, y, bad, s, res, sxq)) return true; break;
+        case 9: if (grouped_pipe_launch<32, 1, 8, 4>(w, q, sx, m, y, bad, s, res, sxq)) return true; break;
+        case 10: if (grouped_pipe_launch<64, 2, 4, 4>(w, q, sx, m, y, bad, s, res, sxq)) return true; break;
         default: break;
     }
     if (res) return false;  // only the pipelined kernels add a residual
