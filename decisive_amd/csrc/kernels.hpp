@@ -49,7 +49,8 @@ void launch_fill_i32(int *p, int value, int count, hipStream_t s);
 // Grouped W{4,8}A{8,4}: bit-exact AVX2 order. bad (may be null): NaN outputs.
 // With `res` (which may equal y) the product is added onto it in the kernel;
 // only for the cases grouped_adds_residual accepts. Returns false when no
-// kernel was launched (a residual product that no pipelined kernel takes).
+// kernel was launched (a residual product that neither a pipelined kernel
+// nor the few-row kernel takes).
 bool grouped_adds_residual(const Weight &w, int m, int variant);
 // Fitted affine weights (w.offsets) take sxq [m x groups] (launch_act_sums).
 bool launch_grouped(const Weight &w, const int8_t *q, const float *sx, int m, float *y,

@@ -177,8 +177,8 @@ template <int BITS, int MPAD, int AMODE, bool PROJECT, bool AFF = false>
 __global__ __launch_bounds__(kGvWaves * 64) void grouped_gemv_kernel(
     const uint8_t *__restrict__ codes, const uint8_t *__restrict__ scales, const void *__restrict__ a,
     const float *__restrict__ sa, int m, int k, int n, int groups, int kbs, int abits,
-    float *__restrict__ y, const int *__restrict__ bad_in, int *__restrict__ bad_out,
-    const uint8_t *__restrict__ offsets = nullptr) {
+    float *y, const int *__restrict__ bad_in, int *__restrict__ bad_out,
+    const uint8_t *__restrict__ offsets = nullptr, const float *res = nullptr) {
     static_assert(!AFF || (AMODE == 0 && !PROJECT && BITS == 4), "affine offsets: Q4 weights, f32 activations");
     // Q4 codes as the 16 * code operand (q4_operand16) where it keeps the
     // kernel within 64 VGPRs (8 waves per SIMD); from MPAD 4 its extra
@@ -365,8 +365,10 @@ __global__ __launch_bounds__(kGvWaves * 64) void grouped_gemv_kernel(
     const bool nan_out = *flag != 0;
     if (nan_out && bad_out != nullptr && threadIdx.x == 0) atomicOr(bad_out, 1);
     if (folds) {
+        // with `res` (which may be y itself) res + Y, the same float add as a separate residual pass
         const int row = row0 + fr, col = t * 16 + fc;
-        if (row < m && col < n) y[(size_t)row * n + col] = nan_out ? __builtin_nanf("") : acc;
+        const size_t at = (size_t)row * n + col;
+        if (row < m && col < n) y[at] = nan_out ? __builtin_nanf("") : res ? __fadd_rn(res[at], acc) : acc;
     }
 }
 
@@ -2340,7 +2342,7 @@ const char *const kI8Names[] = {"256x256p2w8", "256x256p4k64w8", "256x128p3w8", 
                                  "256x256p2w8-stream-mid", "256x128k64p2-stream2"};
 const char *const kGroupedNames[] = {"pipe-auto",    "pipe256x128w8", "wave16x16",   "pipe128x128w4",
                                      "pipe64x128w2", "pipe128x128m8", "pipe128x128n8", "pipe32x128w8",
-                                     "pipe64x128w8", "pipe32x128w8g4", "pipe64x128w8g4"};
+                                     "pipe64x128w8", "pipe32x128w8g4", "pipe64x128w8g4", "fewrow16"};
 const char *const kMlpNames[] = {"pipe-auto", "pipe256x64w8", "pipe128x64w4", "wave16x64", "pipe256x64n2", "pipe128x64n2"};
 const char *const kDeltaNames[] = {"chunked64", "chunked64-c32", "recurrent", "recurrent-rolled", "auto"};
 const char *const kNormNames[] = {"fused", "separate"};
@@ -2527,7 +2529,7 @@ void gemm_dispatch(const Weight &w, const half_t *x, int m, void *y, const half_
 
 template <int BITS, int MPAD, int AMODE, bool PROJECT, bool AFF = false>
 void gv_launch_one(const Weight &w, const void *a, const float *sa, int m, int abits, float *y,
-                   const int *bad_in, int *bad_out, hipStream_t s) {
+                   const int *bad_in, int *bad_out, hipStream_t s, const float *res = nullptr) {
     using S = GvShape<MPAD, AFF>;
     static bool configured[64] = {};  // the LDS limit is a per-device function attribute
     int dev = 0;
@@ -2539,17 +2541,17 @@ void gv_launch_one(const Weight &w, const void *a, const float *sa, int m, int a
     dim3 grid(w.tiles(), cdiv(m, 16));
     hipLaunchKernelGGL((grouped_gemv_kernel<BITS, MPAD, AMODE, PROJECT, AFF>), grid, dim3(kGvWaves * 64), S::BYTES,
                        s, w.codes, w.scales, a, sa, m, w.cols, w.rows, w.groups, w.kblocks(), abits, y, bad_in,
-                       bad_out, w.offsets);
+                       bad_out, w.offsets, res);
 }
 
 template <int BITS, int AMODE, bool PROJECT, bool AFF = false>
 void gv_launch_m(const Weight &w, const void *a, const float *sa, int m, int abits, float *y,
-                 const int *bad_in, int *bad_out, hipStream_t s) {
-    if (m <= 1) gv_launch_one<BITS, 1, AMODE, PROJECT, AFF>(w, a, sa, m, abits, y, bad_in, bad_out, s);
-    else if (m <= 2) gv_launch_one<BITS, 2, AMODE, PROJECT, AFF>(w, a, sa, m, abits, y, bad_in, bad_out, s);
-    else if (m <= 4) gv_launch_one<BITS, 4, AMODE, PROJECT, AFF>(w, a, sa, m, abits, y, bad_in, bad_out, s);
-    else if (m <= 8) gv_launch_one<BITS, 8, AMODE, PROJECT, AFF>(w, a, sa, m, abits, y, bad_in, bad_out, s);
-    else gv_launch_one<BITS, 16, AMODE, PROJECT, AFF>(w, a, sa, m, abits, y, bad_in, bad_out, s);
+                 const int *bad_in, int *bad_out, hipStream_t s, const float *res = nullptr) {
+    if (m <= 1) gv_launch_one<BITS, 1, AMODE, PROJECT, AFF>(w, a, sa, m, abits, y, bad_in, bad_out, s, res);
+    else if (m <= 2) gv_launch_one<BITS, 2, AMODE, PROJECT, AFF>(w, a, sa, m, abits, y, bad_in, bad_out, s, res);
+    else if (m <= 4) gv_launch_one<BITS, 4, AMODE, PROJECT, AFF>(w, a, sa, m, abits, y, bad_in, bad_out, s, res);
+    else if (m <= 8) gv_launch_one<BITS, 8, AMODE, PROJECT, AFF>(w, a, sa, m, abits, y, bad_in, bad_out, s, res);
+    else gv_launch_one<BITS, 16, AMODE, PROJECT, AFF>(w, a, sa, m, abits, y, bad_in, bad_out, s, res);
 }
 
 template <int AMODE, bool PROJECT>
@@ -2568,7 +2570,7 @@ int variant_count(const char *family) {
     if (f == "gemv") return 5;
     if (f == "gemm_w4a16") return 10;
     if (f == "i8_gemm") return 10;
-    if (f == "grouped") return 11;
+    if (f == "grouped") return 12;
     if (f == "mlp") return 6;
     if (f == "delta_scan") return 5;
     if (f == "norm") return 2;
@@ -2660,8 +2662,14 @@ bool grouped_pipe_launch(const Weight &w, const int8_t *q, const float *sx, int 
 // waves stacked, each 32 rows x 128 columns), 4 64x128 (2 waves), 7 32x128 (8
 // waves side by side, each 32 rows x 16 columns), 8 64x128 (8 waves as 2x4), 2
 // one wave per 16x16 tile; 9 and 10 are 7 and 8 with four groups per k-step
-// instead of two. The fold is VALU work, so what decides is how many waves
-// keep every SIMD busy: 0 picks the side-by-side 128x128 tiles when their
+// instead of two; 11 the few-row kernel over the codes (16 rows per block
+// row, a block per 16 columns). Where that kernel's grid gives a compute unit
+// at most two blocks it is the fastest (us, A8 codes in: K=9216, N=2560,
+// 17-48 rows: 19.9-21.7 against 27.6 pipelined; N=1024, 17-128 rows: 4.8-8.3
+// against 10.0; N=4096, 17-32 rows: 8.1 against 9.8; one block row more
+// and it is slower), so 0 takes it there (not for affine weights, which it
+// does not take). Otherwise the fold is VALU work, so what decides is how many
+// waves keep every SIMD busy: 0 picks the side-by-side 128x128 tiles when their
 // grid gives every compute unit four blocks, else 64x128 on 8 waves when its
 // grid gives two, else 32x128 on 8 waves, with four groups per step when even
 // that grid gives a compute unit fewer than two blocks (half the barriers and
@@ -2676,6 +2684,7 @@ bool grouped_pipe_launch(const Weight &w, const int8_t *q, const float *sx, int 
 int grouped_pick(const Weight &w, int m, int variant) {
     if (variant != 0) return variant;
     const unsigned cus = (unsigned)device_cus(), tn = cdiv(w.rows, 128);
+    if (!w.offsets && cdiv(m, 16) * (unsigned)w.tiles() <= 2 * cus) return 11;
     if (cdiv(m, 128) * tn >= 4 * cus) return 5;
     if (cdiv(m, 64) * tn >= 2 * cus) return 8;
     if (cdiv(m, 32) * tn >= 2 * cus) return 7;
@@ -2696,7 +2705,9 @@ int grouped_pipe_rows(int pick) {
 // The same predicate decides here and in launch_grouped whether a pipelined
 // kernel (the only ones with the residual epilogue) takes the product.
 bool grouped_adds_residual(const Weight &w, int m, int variant) {
-    return m > 16 && w.kind != WeightKind::Q4G32 && grouped_pipe_fits(w, grouped_pipe_rows(grouped_pick(w, m, variant)));
+    if (m <= 16 || w.kind == WeightKind::Q4G32) return false;
+    const int pick = grouped_pick(w, m, variant);
+    return (pick == 11 && !w.offsets) || grouped_pipe_fits(w, grouped_pipe_rows(pick));
 }
 
 bool launch_grouped(const Weight &w, const int8_t *q, const float *sx, int m, float *y,
@@ -2712,6 +2723,11 @@ bool launch_grouped(const Weight &w, const int8_t *q, const float *sx, int m, fl
         case 8: if (grouped_pipe_launch<64, 2, 4>(w, q, sx, m, y, bad, s, res, sxq)) return true; break;
         case 9: if (grouped_pipe_launch<32, 1, 8, 4>(w, q, sx, m, y, bad, s, res, sxq)) return true; break;
         case 10: if (grouped_pipe_launch<64, 2, 4, 4>(w, q, sx, m, y, bad, s, res, sxq)) return true; break;
+        case 11:
+            if (w.offsets) break;  // the few-row kernel over codes takes no offsets
+            if (w.bits == 4) gv_launch_m<4, 1, false>(w, q, sx, m, 8, y, bad, nullptr, s, res);
+            else gv_launch_m<8, 1, false>(w, q, sx, m, 8, y, bad, nullptr, s, res);
+            return true;
         default: break;
     }
     if (res) return false;  // only the pipelined kernels add a residual

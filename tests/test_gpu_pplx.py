@@ -210,7 +210,7 @@ def test_residual_added_in_the_product_epilogue_gives_the_same_bits(ctx, oracle,
     model, p = small
     h = np.random.default_rng(500 + n).standard_normal((n, SMALL["hidden"])).astype(np.float32)
     out = {}
-    for v in ("wave16x16", "pipe128x128w4", "pipe64x128w2", "pipe32x128w8g4"):
+    for v in ("wave16x16", "pipe128x128w4", "pipe64x128w2", "pipe32x128w8g4", "fewrow16"):
         hd = dev(h)
         ctx.select_variant("grouped", v)
         try:
@@ -221,6 +221,7 @@ def test_residual_added_in_the_product_epilogue_gives_the_same_bits(ctx, oracle,
     assert np.array_equal(out["wave16x16"].view(np.uint32), out["pipe128x128w4"].view(np.uint32))
     assert np.array_equal(out["wave16x16"].view(np.uint32), out["pipe64x128w2"].view(np.uint32))
     assert np.array_equal(out["wave16x16"].view(np.uint32), out["pipe32x128w8g4"].view(np.uint32))
+    assert np.array_equal(out["wave16x16"].view(np.uint32), out["fewrow16"].view(np.uint32))
     want = pplx_model.ref_layer(oracle, model, layer, h, markers)
     assert close(out["pipe128x128w4"], want)
 
