@@ -1843,7 +1843,7 @@ __global__ __launch_bounds__(WGM *WGN * 64) void grouped_pipe_kernel(
     constexpr int XI = BM / RPI, CI = CSTAGE / 1024, SI = BM * GS / 64;
     constexpr int XPW = (XI + WAVES - 1) / WAVES, CPW = (CI + WAVES - 1) / WAVES, SPW = (SI + WAVES - 1) / WAVES;
     static_assert(XI * RPI == BM && SI * 64 == BM * GS, "whole 1 KiB activation and 256 B scale loads");
-    static_assert(TILES == 8, "one 1 KiB weight-scale load per k-step pair");
+    static_assert(TILES == 8 || TILES == 4, "one 1 KiB (or 512 B) weight-scale load per k-step pair");
     __shared__ __align__(16) uint8_t xs[2 * XSTAGE];
     __shared__ __align__(16) uint8_t cs[2 * CSTAGE];
     __shared__ __align__(16) uint8_t sws[2 * SWSTAGE];
@@ -1910,9 +1910,9 @@ __global__ __launch_bounds__(WGM *WGN * 64) void grouped_pipe_kernel(
                 dma16(__builtin_amdgcn_readfirstlane(cs_lds + stage * CSTAGE + ci * 1024),
                       (uint32_t)((t * kbs + kc) * 1024 + lane * 16), nc);
         }
-        if (wave == WAVES - 1) {
+        if (wave == WAVES - 1 && (TILES == 8 || lane < TILES * 8)) {
 #pragma unroll
-            for (int u = 0; u < KBS; u++) {  // one 1 KiB load per pair of groups: lane -> tile l/8, piece l%8
+            for (int u = 0; u < KBS; u++) {  // one load per pair of groups: lane -> tile l/8, piece l%8
                 const int t = lane / 8;
                 const uint32_t off = BITS == 4 ? (uint32_t)(t * kbs + st * KBS + u) * 128
                                                : (uint32_t)(t * groups + GS * st + 2 * u) * 64;
@@ -2342,7 +2342,8 @@ const char *const kI8Names[] = {"256x256p2w8", "256x256p4k64w8", "256x128p3w8", 
                                  "256x256p2w8-stream-mid", "256x128k64p2-stream2"};
 const char *const kGroupedNames[] = {"pipe-auto",    "pipe256x128w8", "wave16x16",   "pipe128x128w4",
                                      "pipe64x128w2", "pipe128x128m8", "pipe128x128n8", "pipe32x128w8",
-                                     "pipe64x128w8", "pipe32x128w8g4", "pipe64x128w8g4", "fewrow16"};
+                                     "pipe64x128w8", "pipe32x128w8g4", "pipe64x128w8g4", "fewrow16",
+                                     "pipe32x64w4",  "pipe64x64w8"};
 const char *const kMlpNames[] = {"pipe-auto", "pipe256x64w8", "pipe128x64w4", "wave16x64", "pipe256x64n2", "pipe128x64n2"};
 const char *const kDeltaNames[] = {"chunked64", "chunked64-c32", "recurrent", "recurrent-rolled", "auto"};
 const char *const kNormNames[] = {"fused", "separate"};
@@ -2570,7 +2571,7 @@ int variant_count(const char *family) {
     if (f == "gemv") return 5;
     if (f == "gemm_w4a16") return 10;
     if (f == "i8_gemm") return 10;
-    if (f == "grouped") return 12;
+    if (f == "grouped") return 14;
     if (f == "mlp") return 6;
     if (f == "delta_scan") return 5;
     if (f == "norm") return 2;
@@ -2640,19 +2641,19 @@ bool grouped_pipe_fits(const Weight &w, int bm) {
            (size_t)8 * w.kblocks() * 1024 < ((size_t)1 << 31);
 }
 
-template <int BM, int WGM, int WGN, int GS = 2>
+template <int BM, int WGM, int WGN, int GS = 2, int BN = 128>
 bool grouped_pipe_launch(const Weight &w, const int8_t *q, const float *sx, int m, float *y, const int *bad,
                          hipStream_t s, const float *res, const float *sxq) {
     if (!grouped_pipe_fits(w, BM)) return false;
-    const dim3 blocks(cdiv(m, BM) * cdiv(w.rows, 128));
+    const dim3 blocks(cdiv(m, BM) * cdiv(w.rows, BN));
     if (w.offsets)
-        hipLaunchKernelGGL((grouped_pipe_kernel<4, BM, 128, WGM, WGN, true, GS>), blocks, dim3(WGM * WGN * 64), 0, s,
+        hipLaunchKernelGGL((grouped_pipe_kernel<4, BM, BN, WGM, WGN, true, GS>), blocks, dim3(WGM * WGN * 64), 0, s,
                            w.codes, w.scales, q, sx, m, w.rows, w.groups, w.kblocks(), y, res, bad, w.offsets, sxq);
     else if (w.bits == 4)
-        hipLaunchKernelGGL((grouped_pipe_kernel<4, BM, 128, WGM, WGN, false, GS>), blocks, dim3(WGM * WGN * 64), 0, s,
+        hipLaunchKernelGGL((grouped_pipe_kernel<4, BM, BN, WGM, WGN, false, GS>), blocks, dim3(WGM * WGN * 64), 0, s,
                            w.codes, w.scales, q, sx, m, w.rows, w.groups, w.kblocks(), y, res, bad);
     else
-        hipLaunchKernelGGL((grouped_pipe_kernel<8, BM, 128, WGM, WGN, false, GS>), blocks, dim3(WGM * WGN * 64), 0, s,
+        hipLaunchKernelGGL((grouped_pipe_kernel<8, BM, BN, WGM, WGN, false, GS>), blocks, dim3(WGM * WGN * 64), 0, s,
                            w.codes, w.scales, q, sx, m, w.rows, w.groups, w.kblocks(), y, res, bad);
     return true;
 }
@@ -2663,31 +2664,39 @@ bool grouped_pipe_launch(const Weight &w, const int8_t *q, const float *sx, int 
 // waves side by side, each 32 rows x 16 columns), 8 64x128 (8 waves as 2x4), 2
 // one wave per 16x16 tile; 9 and 10 are 7 and 8 with four groups per k-step
 // instead of two; 11 the few-row kernel over the codes (16 rows per block
-// row, a block per 16 columns). Where that kernel's grid gives a compute unit
-// at most two blocks it is the fastest (us, A8 codes in: K=9216, N=2560,
-// 17-48 rows: 19.9-21.7 against 27.6 pipelined; N=1024, 17-128 rows: 4.8-8.3
-// against 10.0; N=4096, 17-32 rows: 8.1 against 9.8; one block row more
-// and it is slower), so 0 takes it there (not for affine weights, which it
-// does not take). Otherwise the fold is VALU work, so what decides is how many
-// waves keep every SIMD busy: 0 picks the side-by-side 128x128 tiles when their
-// grid gives every compute unit four blocks, else 64x128 on 8 waves when its
-// grid gives two, else 32x128 on 8 waves, with four groups per step when even
-// that grid gives a compute unit fewer than two blocks (half the barriers and
-// twice the work between a load and its use; on fuller grids it is 2-5%
-// slower). Measured (us, 1024 rows unless stated, 32x128w8 / 32x128w8g4 /
-// 64x128w8 / 128x128 side by side): N=1024 K=2560 18.6 / 16.4 / 22.2 / 47.5;
-// N=2560 K=9216 80.4 / 82.7 / 84.5 / 149; N=2560 K=4096 40.0 / 41.4 / 43.2 /
-// 72.3; N=8192 K=2560 59.0 / 62.4 / 53.4 / 57.3; 40 rows, N=8192: 14.5 / 12.9
-// / 18.2 / 42.3; 300 rows, N=2560: 15.7 / 14.1 / 19.5 / 45.1; 16384 rows,
-// K=4096, N=14336: 2210 / 2354 / 2025 / 1813. Every variant folds in group
-// order: all are bitwise equal.
+// row, a block per 16 columns); 12 and 13 are 32x64 tiles on 4 waves (each
+// 32 rows x 16 columns, the per-wave work of 7) and 64x64 on 8 waves. Every
+// variant folds in group order: all are bitwise equal. "Auto" (0) picks:
+//  - the few-row kernel where its grid gives a compute unit at most two
+//    blocks (us, A8 codes in: K=9216, N=2560, 17-48 rows: 19.9-21.7 against
+//    27.6 pipelined; N=1024, 17-128 rows: 4.8-8.3 against 10.0; N=4096,
+//    17-32 rows: 8.1 against 9.8; one block row more and it is slower), not
+//    for affine weights, which it does not take;
+//  - otherwise, as the fold is VALU work, the tiles whose grid keeps every
+//    SIMD busy and every compute unit equally loaded: where a grid's blocks
+//    do not divide evenly over the units, those holding one block more end
+//    last (640 32x128 blocks at N=2560 put three on half the units and two on
+//    the rest; 1280 32x64 blocks put five on each). So 128x128 side by side
+//    when their grid gives every unit four blocks, else 64x128 on 8 waves
+//    when its grid is two or more whole blocks per unit, else 32x64 on 4
+//    waves, and 32x128 with four groups per step when the 32x128 grid gives
+//    a unit fewer than two blocks (half the barriers and twice the work
+//    between a load and its use; on fuller grids it is 2-5% slower).
+// Measured (us at 1024 rows unless stated; 32x128w8 / 32x128w8g4 / 32x64w4 /
+// 64x128w8 / 128x128 side by side): N=1024, K=2560 18.0 / 16.3 / 17.1 / 22.0
+// / 47.5; N=2560, K=9216 79.0 / 82.7 / 74.6 / 83.9 / 149; N=2560, K=4096
+// 39.9 / 41.4 / 37.7 / 43.0 / 72.3; N=4160, K=2560 39.5 / - / 37.6 / 43.0 /
+// 56.6; N=8192, K=2560 58.6 / 62.4 / 58.5 / 54.1 / 57.3; 40 rows, N=8192:
+// 14.6 / 13.0 / 13.2 / 18.0 / 42.3; 300 rows, N=2560: 15.6 / 14.2 / 14.6 /
+// 19.8 / 45.1; 16384 rows, K=4096, N=14336: 2209 / 2354 / 2252 / 2060 / 1813.
 int grouped_pick(const Weight &w, int m, int variant) {
     if (variant != 0) return variant;
     const unsigned cus = (unsigned)device_cus(), tn = cdiv(w.rows, 128);
     if (!w.offsets && cdiv(m, 16) * (unsigned)w.tiles() <= 2 * cus) return 11;
     if (cdiv(m, 128) * tn >= 4 * cus) return 5;
-    if (cdiv(m, 64) * tn >= 2 * cus) return 8;
-    if (cdiv(m, 32) * tn >= 2 * cus) return 7;
+    const unsigned b64 = cdiv(m, 64) * tn;
+    if (b64 >= 2 * cus && b64 % cus == 0) return 8;
+    if (cdiv(m, 32) * tn >= 2 * cus) return 12;
     return 9;
 }
 
@@ -2696,8 +2705,8 @@ int grouped_pipe_rows(int pick) {
     switch (pick) {
         case 1: return 256;
         case 3: case 5: case 6: return 128;
-        case 4: case 8: case 10: return 64;
-        case 7: case 9: return 32;
+        case 4: case 8: case 10: case 13: return 64;
+        case 7: case 9: case 12: return 32;
         default: return 0;
     }
 }
@@ -2723,6 +2732,8 @@ bool launch_grouped(const Weight &w, const int8_t *q, const float *sx, int m, fl
         case 8: if (grouped_pipe_launch<64, 2, 4>(w, q, sx, m, y, bad, s, res, sxq)) return true; break;
         case 9: if (grouped_pipe_launch<32, 1, 8, 4>(w, q, sx, m, y, bad, s, res, sxq)) return true; break;
         case 10: if (grouped_pipe_launch<64, 2, 4, 4>(w, q, sx, m, y, bad, s, res, sxq)) return true; break;
+        case 12: if (grouped_pipe_launch<32, 1, 4, 2, 64>(w, q, sx, m, y, bad, s, res, sxq)) return true; break;
+        case 13: if (grouped_pipe_launch<64, 2, 4, 2, 64>(w, q, sx, m, y, bad, s, res, sxq)) return true; break;
         case 11:
             if (w.offsets) break;  // the few-row kernel over codes takes no offsets
             if (w.bits == 4) gv_launch_m<4, 1, false>(w, q, sx, m, 8, y, bad, nullptr, s, res);

@@ -588,7 +588,8 @@ int32_t dz_tune(dz_ctx *ctx, uint32_t budget_ms, const char *cache_in, char *cac
  *                 pipe128x128m8, pipe128x128n8, pipe32x128w8, pipe64x128w8,
  *                 pipe32x128w8g4, pipe64x128w8g4 (g4: four 64-groups per
  *                 pipeline step instead of two), fewrow16 (the few-row kernel,
- *                 16 rows per block row, over the A8 codes)
+ *                 16 rows per block row, over the A8 codes), pipe32x64w4,
+ *                 pipe64x64w8
  *   "mlp"         pipe-auto, pipe256x64w8, pipe128x64w4, wave16x64, pipe256x64n2,
  *                 pipe128x64n2
  *   "delta_scan"  chunked64, chunked64-c32, recurrent, recurrent-rolled,

@@ -17,7 +17,7 @@ pytestmark = pytest.mark.gpu
 MAX_ABS = 1e-2  # north_star tolerance for f16/f32 GEMM outputs
 MIN_COS = 0.9999
 GROUPED_VARIANTS = ("pipe256x128w8", "wave16x16", "pipe128x128w4", "pipe64x128w2", "pipe128x128m8",
-                    "pipe128x128n8", "pipe32x128w8", "pipe64x128w8", "pipe32x128w8g4", "pipe64x128w8g4", "fewrow16", "pipe-auto")
+                    "pipe128x128n8", "pipe32x128w8", "pipe64x128w8", "pipe32x128w8g4", "pipe64x128w8g4", "fewrow16", "pipe32x64w4", "pipe64x64w8", "pipe-auto")
 
 
 def fitted(oracle, n, k, mode, seed, spread=0.05, shift=0.0):

@@ -376,7 +376,7 @@ def test_tuned_grouped_and_mlp_variants_agree_on_real_inputs(ctx, oracle):
     x = dev(rng.standard_normal((m, k)).astype(np.float32))
     outs = []
     for v in ("pipe-auto", "pipe256x128w8", "wave16x16", "pipe128x128w4", "pipe64x128w2", "pipe128x128m8",
-              "pipe128x128n8", "pipe32x128w8", "pipe64x128w8", "pipe32x128w8g4", "pipe64x128w8g4", "fewrow16"):
+              "pipe128x128n8", "pipe32x128w8", "pipe64x128w8", "pipe32x128w8g4", "pipe64x128w8g4", "fewrow16", "pipe32x64w4", "pipe64x64w8"):
         ctx.select_variant("grouped", v)
         y = empty((m, n), torch.float32)
         ctx.linear(w, x, rocm.F32, m, y, rocm.W4A8)

@@ -54,7 +54,7 @@ def test_grouped_large_m_pipeline_bit_exact(ctx, oracle, wb, ab, m, k, n):
     mode = rocm.W4A4 if ab == 4 else rocm.W4A8
     outs = []
     names = ("pipe256x128w8", "wave16x16", "pipe128x128w4", "pipe64x128w2", "pipe128x128m8", "pipe128x128n8",
-             "pipe32x128w8", "pipe64x128w8", "pipe32x128w8g4", "pipe64x128w8g4", "fewrow16", "pipe-auto")
+             "pipe32x128w8", "pipe64x128w8", "pipe32x128w8g4", "pipe64x128w8g4", "fewrow16", "pipe32x64w4", "pipe64x64w8", "pipe-auto")
     for name in names:
         ctx.select_variant("grouped", name)
         y = empty((m, n), torch.float32)
