@@ -339,9 +339,9 @@ def encoder_line(torch, ctx, rocm, stream) -> dict:
             "frac_of_f16_peak": round(flops / (ms * 1e-3) / 1e12 / F16_PEAK_TFLOPS, 4)}
 
 
-def secondary(torch, ctx, rocm, stream, cpu=True) -> dict:
-    out = {}
-    # config 4: int8 GEMM M=8192 K=N=4096
+def int8_line(torch, ctx, stream) -> dict:
+    """Config 4: the per-row int8 GEMM at M=8192, K=N=4096 (f32 out), the
+    vendor library on the same codes, and the same launch on all-zero codes."""
     m, n, k = 8192, 4096, 4096
     a = torch.randn((m, k), generator=torch.Generator(device="cuda").manual_seed(0), device="cuda")
     b = torch.randn((n, k), generator=torch.Generator(device="cuda").manual_seed(1), device="cuda") * 0.02
@@ -378,12 +378,15 @@ def secondary(torch, ctx, rocm, stream, cpu=True) -> dict:
     torch.cuda.synchronize()
     warm(torch, fn)
     ms_zero = timed_ms(torch, stream, fn, 20)
-    out["int8_gemm_m8192_k4096_n4096"] = {"ms": round(ms, 4), "TOP/s": round(tops, 1),
-                                          "frac_of_i8_peak": round(tops / I8_PEAK_TOPS, 4),
-                                          "ms_on_zero_codes": round(ms_zero, 4),
-                                          "vendor_library": vendor,
-                                          "variant": ctx.info()["variants"]["i8_gemm"]}
+    line = {"ms": round(ms, 4), "TOP/s": round(tops, 1), "frac_of_i8_peak": round(tops / I8_PEAK_TOPS, 4),
+            "ms_on_zero_codes": round(ms_zero, 4), "vendor_library": vendor,
+            "variant": ctx.info()["variants"]["i8_gemm"]}
     del a, b, qa, qb, y
+    return line
+
+
+def secondary(torch, ctx, rocm, stream, cpu=True) -> dict:
+    out = {"int8_gemm_m8192_k4096_n4096": int8_line(torch, ctx, stream)}
     # config 5: Q4 prefill M=16384 K=4096 N=14336
     m, k, n = 16384, 4096, 14336
     wf = torch.randn((n, k), generator=torch.Generator(device="cuda").manual_seed(1), device="cuda") * 0.02
@@ -691,7 +694,7 @@ def main():
     ap.add_argument("--calibrate-copy", action="store_true",
                     help=f"also run a {COPY_BYTES >> 20} MiB device copy (counter calibration)")
     ap.add_argument("--tune", type=int, default=0, help="tuner budget in ms (0 keeps reference variants)")
-    ap.add_argument("--only", choices=["pplx", "tune", "floors", "encoder", "gemv"],
+    ap.add_argument("--only", choices=["pplx", "tune", "floors", "encoder", "gemv", "int8"],
                     help="run one secondary line alone and print it (for profiling)")
     ap.add_argument("--tune-cache", help="with --only tune: a selection JSON from an earlier run to reuse")
     ap.add_argument("--tune-out", help="with --only tune: write the selection JSON here")
@@ -731,6 +734,14 @@ def main():
             line = floors_line(torch, ctx, rocm, stream)
         ctx.set_stream(None)
         print(json.dumps({"launch_floors_q4_gemv_size": line}), flush=True)
+        return
+    if args.only == "int8":
+        stream = torch.cuda.Stream()
+        ctx.set_stream(stream.cuda_stream)
+        with torch.cuda.stream(stream):
+            line = int8_line(torch, ctx, stream)
+        ctx.set_stream(None)
+        print(json.dumps({"int8_gemm_m8192_k4096_n4096": line}), flush=True)
         return
     if args.only in ("pplx", "encoder"):
         stream = torch.cuda.Stream()

@@ -1187,14 +1187,22 @@ __global__ __launch_bounds__(WGM *WGN * 64) void i8_gemm_pipe_kernel(const int8_
 #pragma unroll
         for (int z = 0; z < NB; z++) acc[x][z] = int16_t_v{};
     // compute on `stage`; when `next` is set, the loads of step `next_step`
-    // into it are issued in SUBS slices, one before each substep's MFMAs
+    // into it are issued in SUBS slices, one before each substep's MFMAs.
+    // With two stages they are all issued before the first substep instead,
+    // so that the last slice too has the whole step to land (config 4:
+    // 128.2-129.9 against 130.0-131.5 us; with three stages the slices pay)
     auto compute = [&](const uint8_t *stage, uint8_t *next, int next_step) {
         int4_t af[2][MB], bf[2][NB];
         read_frags(stage, 0, af[0], bf[0]);
 #pragma unroll
         for (int sub = 0; sub < SUBS; sub++) {
             const int cur = sub & 1;
-            if (next) dma(next, next_step, sub * DPW / SUBS, (sub + 1) * DPW / SUBS);
+            if (next) {
+                if (NS > 2)
+                    dma(next, next_step, sub * DPW / SUBS, (sub + 1) * DPW / SUBS);
+                else if (sub == 0)
+                    dma(next, next_step, 0, DPW);
+            }
             if (sub + 1 < SUBS) read_frags(stage, sub + 1, af[cur ^ 1], bf[cur ^ 1]);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
