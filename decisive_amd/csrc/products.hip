@@ -651,6 +651,132 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const uint8_t *__restr
     }
 }
 
+// Persistent form of gemv_kernel<16, MPAD, G32, 1> for weights whose chunks
+// hold at most one k-block pair (K <= 4096): a grid of a few blocks per
+// compute unit, block b taking tiles b, b + gridDim.x, ... A wave issues the
+// next tile's loads (its staging unit and its two code loads) as soon as this
+// tile's MFMAs have taken their operands, so every wave keeps its loads in
+// flight through the chunk reduction and the barrier instead of ending and
+// handing the unit to a new block. The chunk partials go to an LDS area of
+// their own, double-buffered by tile parity, so one barrier per tile orders
+// them. The arithmetic is gemv_kernel's, so the outputs are bitwise equal.
+template <int MPAD, bool G32>
+__global__ __launch_bounds__(kGemvChunks * 64) void gemv_persist_kernel(const uint8_t *__restrict__ codes,
+                                                                        const uint8_t *__restrict__ scales,
+                                                                        const half_t *__restrict__ x, int m,
+                                                                        int k, int n, int kbs,
+                                                                        float *__restrict__ y) {
+    using S = GemvShape<MPAD>;
+    constexpr int C = kGemvChunks, LIVE = S::LIVE;
+    extern __shared__ __align__(16) uint8_t lds[];
+    float *const partials = (float *)(lds + C * S::SLICE);  // [2][C][LIVE][64]
+    const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const int qd = lane / 16, i = lane % 16, j = i;
+    const int chunk = wave;
+    const bool live = chunk < kbs;  // the chunk's one pair (or nothing past K)
+    uint8_t *slice = lds + wave * S::SLICE;
+    const uint8_t *arow = slice + (i % MPAD) * S::XROW + qd * 16;
+    const uint32_t magic = 0x64006400u;
+    const float4_t fz = {0.f, 0.f, 0.f, 0.f};
+    const int tiles = (n + 15) / 16;
+    // Staging units as gemv_kernel's first round (k-blocks chunk, chunk + C):
+    // the activation units are the same for every tile, so they are staged
+    // once; a tile loads only the loads that hold its scale units.
+    constexpr int L0 = MPAD * 32 / 64;
+    if (live) {
+#pragma unroll
+        for (int L = 0; L < S::LOADS; L++) {
+            const int u = L * 64 + lane;
+            if (u < MPAD * 32) {
+                const int r = u / 32, kbu = chunk + ((u % 32) / 16) * C;
+                const int kk = kbu * 128 + (u % 16) * 8;
+                const uint8_t *p = (const uint8_t *)g_zero_unit;
+                if (r < m && kbu < kbs && kk < k) p = (const uint8_t *)(x + (size_t)r * k + kk);
+                *(uint4_t *)(slice + r * S::XROW + (u % 32) * 16) = *(const uint4_t *)p;
+            }
+        }
+    }
+    // one tile of loads in flight beside the tile being computed (two or
+    // three measured slower: the tiles' barriers, not the loads, set the pace)
+    uint4_t st[S::LOADS - L0], cw[2];
+    auto issue = [&](int t) {
+#pragma unroll
+        for (int L = L0; L < S::LOADS; L++) {
+            const int u = L * 64 + lane;
+            const uint8_t *p = (const uint8_t *)g_zero_unit;
+            if (u >= MPAD * 32 && u < S::UNITS) {
+                const int v = u - MPAD * 32, kbq = chunk + (v / 8) * C;
+                if (kbq < kbs) p = scales + ((size_t)t * kbs + kbq) * 128 + (v % 8) * 16;
+            }
+            st[L - L0] = *(const uint4_t *)p;
+        }
+        const uint8_t *cbase = codes + q4_lane(t, 0, kbs, qd, j);
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int kb = chunk + h * C;
+            cw[h] = __builtin_nontemporal_load((const uint4_t *)(cbase + (size_t)(kb < kbs ? kb : chunk) * 1024));
+        }
+    };
+    auto tile = [&](int t, int it) {
+        float acc[LIVE];
+#pragma unroll
+        for (int v = 0; v < LIVE; v++) acc[v] = 0.0f;
+        if (live) {
+            // only this wave reads its slice, and its reads of the last tile are done
+#pragma unroll
+            for (int L = L0; L < S::LOADS; L++) {
+                const int u = L * 64 + lane;
+                if (u >= MPAD * 32 && u < S::UNITS)
+                    *(uint4_t *)(slice + MPAD * S::XROW + (u - MPAD * 32) * 16) = st[L - L0];
+            }
+            // one k-block's four MFMAs at a time, their scale FMAs in gemv_kernel's order
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const uint2_t sc = *(const uint2_t *)(slice + MPAD * S::XROW + h * 128 + j * 8);
+                half8_t a[4];
+#pragma unroll
+                for (int s = 0; s < 4; s++) a[s] = *(const half8_t *)(arow + (h * 128 + s * 32) * 2);
+                float4_t pr[4];
+#pragma unroll
+                for (int s = 0; s < 4; s++) pr[s] = mfma_f16(a[s], as_half8(unpack_codes(cw[h][s], magic)), fz);
+#pragma unroll
+                for (int s = 0; s < 4; s++) asm volatile("" : "+v"(pr[s]));
+#pragma unroll
+                for (int s = 0; s < 4; s++) {
+                    const float scale = G32 ? f16_bits_to_float((sc[s >> 1] >> (16 * (s & 1))) & 0xffffu)
+                                            : word_as_float(sc[s >> 1]);
+#pragma unroll
+                    for (int v = 0; v < LIVE; v++) acc[v] = __builtin_fmaf(pr[s][v], scale, acc[v]);
+                }
+            }
+            // this tile's codes and staging are used up: the next tile's loads leave now
+            if (t + (int)gridDim.x < tiles) issue(t + (int)gridDim.x);
+        }
+        float *pb = partials + (it & 1) * (C * LIVE * 64);
+#pragma unroll
+        for (int v = 0; v < LIVE; v++) pb[(chunk * LIVE + v) * 64 + lane] = acc[v];
+        __syncthreads();  // every chunk's partial of tile t; the other buffer is free
+        if (wave == 0 && qd * 4 < MPAD) {
+            float total[LIVE];
+#pragma unroll
+            for (int c = 0; c < C; c++)
+#pragma unroll
+                for (int v = 0; v < LIVE; v++) {
+                    const float pc = pb[(c * LIVE + v) * 64 + lane];
+                    total[v] = c == 0 ? pc : __fadd_rn(total[v], pc);
+                }
+            const int col = t * 16 + j;
+#pragma unroll
+            for (int v = 0; v < LIVE; v++) {
+                const int r = qd * 4 + v;
+                if (r < m && col < n) y[(size_t)r * n + col] = total[v];
+            }
+        }
+    };
+    if (live && (int)blockIdx.x < tiles) issue(blockIdx.x);
+    for (int t = blockIdx.x, it = 0; t < tiles; t += gridDim.x, it++) tile(t, it);
+}
+
 // Streaming form for wide products (several 16-row tiles per SIMD): one wave
 // owns a whole tile, so no partial sum crosses waves, and it keeps D k-blocks
 // of codes and scale records in flight while it computes. The block's
@@ -2341,7 +2467,7 @@ inline unsigned cdiv(size_t a, size_t b) { return (unsigned)((a + b - 1) / b); }
 
 // ---- variant tables -------------------------------------------------------------
 
-const char *const kGemvNames[] = {"auto", "w16", "w8", "stream8", "stream4"};
+const char *const kGemvNames[] = {"auto", "w16", "w8", "stream8", "stream4", "persist"};
 const char *const kGemmNames[] = {"pipe-auto",   "256x256p2w8", "128x128p2w4", "128x256p2w8",
                                    "256x128w2x2", "128x128w2x2", "128x64w2x2", "256x256p2w8-persist",
                                    "256x192p2w8-persist", "256x128p2w8"};
@@ -2427,6 +2553,41 @@ template <int WAVES, int D>
 bool gemv_stream(const Weight &w, const half_t *x, int m, float *y, hipStream_t s) {
     if (w.kind == WeightKind::Q4G32) return gemv_stream_m<WAVES, true, D>(w, x, m, y, s);
     return gemv_stream_m<WAVES, false, D>(w, x, m, y, s);
+}
+
+// The persistent GEMV: two blocks per compute unit where its LDS allows, at
+// most one per tile. False (nothing launched) where a chunk would hold more
+// than one k-block pair (K > 4096) or there are more than 8 rows.
+template <int MPAD, bool G32>
+bool gemv_persist_launch(const Weight &w, const half_t *x, int m, float *y, hipStream_t s) {
+    using S = GemvShape<MPAD>;
+    if (w.kblocks() > 2 * kGemvChunks) return false;
+    const size_t lds = (size_t)kGemvChunks * S::SLICE + (size_t)2 * kGemvChunks * S::LIVE * 64 * sizeof(float);
+    static bool configured[64] = {};  // the LDS limit is a per-device function attribute
+    int dev = 0;
+    hipGetDevice(&dev);
+    if (dev >= 0 && dev < 64 && !configured[dev]) {
+        if (hipFuncSetAttribute((const void *)gemv_persist_kernel<MPAD, G32>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) == hipSuccess)
+            configured[dev] = true;
+    }
+    const unsigned blocks = std::min((unsigned)w.tiles(), (unsigned)device_cus());
+    hipLaunchKernelGGL((gemv_persist_kernel<MPAD, G32>), dim3(blocks), dim3(kGemvChunks * 64), lds, s, w.codes,
+                       w.scales, x, m, w.cols, w.rows, w.kblocks(), y);
+    return true;
+}
+
+template <bool G32>
+bool gemv_persist_m(const Weight &w, const half_t *x, int m, float *y, hipStream_t s) {
+    if (m <= 1) return gemv_persist_launch<1, G32>(w, x, m, y, s);
+    if (m <= 2) return gemv_persist_launch<2, G32>(w, x, m, y, s);
+    if (m <= 4) return gemv_persist_launch<4, G32>(w, x, m, y, s);
+    if (m <= 8) return gemv_persist_launch<8, G32>(w, x, m, y, s);
+    return false;
+}
+
+bool gemv_persist(const Weight &w, const half_t *x, int m, float *y, hipStream_t s) {
+    return w.kind == WeightKind::Q4G32 ? gemv_persist_m<true>(w, x, m, y, s) : gemv_persist_m<false>(w, x, m, y, s);
 }
 
 template <int W>
@@ -2576,7 +2737,7 @@ void gv_launch(const Weight &w, const void *a, const float *sa, int m, int abits
 
 int variant_count(const char *family) {
     std::string f(family);
-    if (f == "gemv") return 5;
+    if (f == "gemv") return 6;
     if (f == "gemm_w4a16") return 10;
     if (f == "i8_gemm") return 10;
     if (f == "grouped") return 14;
@@ -2822,18 +2983,23 @@ void launch_w4a16(const Weight &w, const half_t *x, int m, float *y, int gemv_va
     if (m <= 16) {
         int v = gemv_variant;
         if (v == 0) {
-            // "auto": the split kernel, except at 2..8 rows over wide weights (eight or
-            // more 16-row tiles per compute unit), where the streaming kernel keeps more
-            // bytes in flight per compute unit (measured at K = 4096: M = 4, N = 65536
-            // 33 against 39 us; M = 8, 36 against 51 us; at N = 16384 the split kernel
-            // is faster, and at M = 1 the two are within 2-6% up to N = 131072)
+            // "auto": the persistent kernel for up to 8 rows over two or more tiles
+            // per compute unit at K <= 4096 (graph-timed at K = 4096 against the split
+            // kernel, M = 1: N = 16384 8.3 against 9.8 us, N = 131072 53.9 against
+            // 68.3 us = 0.70 of 8 TB/s; M = 8, N = 131072: 70.4 against 104.9 us, and
+            // against 76.6 us for the streaming kernel; at one tile per compute unit,
+            // N = 4096, the split kernel is 2-5% faster); otherwise the split kernel,
+            // or the streaming kernel at 2..8 rows over eight or more tiles per
+            // compute unit (K = 4096: M = 4, N = 65536 33 against 39 us)
             const int cus = device_cus();
-            if (m >= 2 && m <= 8 && w.tiles() >= 8 * cus) v = m > 4 && w.tiles() >= 16 * cus ? 3 : 4;
+            if (m <= 8 && w.kblocks() <= 2 * kGemvChunks && w.tiles() >= 2 * cus) v = 5;
+            else if (m >= 2 && m <= 8 && w.tiles() >= 8 * cus) v = m > 4 && w.tiles() >= 16 * cus ? 3 : 4;
             else v = 1;
         }
         bool done = false;
         if (v == 3) done = gemv_stream<8, 8>(w, x, m, y, s);
         else if (v == 4) done = gemv_stream<4, 8>(w, x, m, y, s);
+        else if (v == 5) done = gemv_persist(w, x, m, y, s);
         if (done) return;
         if (v == 2)
             gemv_launch<8>(w, x, m, y, s);

@@ -572,10 +572,14 @@ int32_t dz_tune(dz_ctx *ctx, uint32_t budget_ms, const char *cache_in, char *cac
 /* Forces a variant of a family by name (tests and benchmarks). Families and
  * variants (the first of each is the default; every variant of a family
  * gives the same bits, except the delta scan's two opt-ins below):
- *   "gemv"        auto, w16, w8, stream8, stream4 (w16/w8: 16 or 8 waves share
- *                 one 16-row tile, each wave a fixed chunk of K; stream8/stream4:
- *                 one wave per tile, 8 or 4 tiles per block, for K a multiple of
- *                 2048 and up to 8 rows, else w16; "auto" takes w16, or stream4 /
+ *   "gemv"        auto, w16, w8, stream8, stream4, persist (w16/w8: 16 or 8 waves
+ *                 share one 16-row tile, each wave a fixed chunk of K; stream8/
+ *                 stream4: one wave per tile, 8 or 4 tiles per block, for K a
+ *                 multiple of 2048 and up to 8 rows, else w16; persist: w16's
+ *                 blocks, one per compute unit, each walking tiles with the next
+ *                 tile's loads in flight, for K <= 4096 and up to 8 rows, else
+ *                 w16; "auto" takes persist for up to 8 rows over two or more
+ *                 tiles per compute unit at K <= 4096, else w16, or stream4 /
  *                 stream8 for 2..8 rows over eight or more tiles per compute unit)
  *   "gemm_w4a16"  pipe-auto, 256x256p2w8, 128x128p2w4, 128x256p2w8, 256x128w2x2,
  *                 128x128w2x2, 128x64w2x2, 256x256p2w8-persist, 256x192p2w8-persist,

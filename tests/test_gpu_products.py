@@ -306,7 +306,7 @@ def test_config2_gemv_vs_closed_form(ctx, oracle, m):
     assert np.abs(got - want).max() <= MAX_ABS
     assert cosine(got, want) >= MIN_COS
     # every GEMV variant keeps the reduction order: bitwise equal outputs
-    for name in ("auto", "w16", "w8", "stream8", "stream4"):
+    for name in ("auto", "w16", "w8", "stream8", "stream4", "persist"):
         ctx.select_variant("gemv", name)
         y2 = empty((m, n), torch.float32)
         ctx.linear(w, dev(xh.view(np.float16)), rocm.F16, m, y2, rocm.W4A16)
@@ -369,6 +369,46 @@ def test_gemv_stream_variants_equal_the_split_kernel(ctx, oracle, k, n):
             base = host(ctx, y).copy()
             assert np.abs(base - want[:m]).max() <= MAX_ABS
             for name in ("stream8", "stream4", "auto"):
+                ctx.select_variant("gemv", name)
+                y.fill_(7.0)
+                torch.cuda.synchronize()  # the fill runs on torch's stream, the product on the context's
+                ctx.linear(w, xd, rocm.F16, m, y, rocm.W4A16)
+                assert bits_equal(host(ctx, y), base), (name, m)
+    finally:
+        ctx.select_variant("gemv", "auto")
+    w.free()
+
+
+@pytest.mark.parametrize("group", [32, 64])
+@pytest.mark.parametrize("k,n", [(4096, 8197), (2560, 8200), (1024, 300), (96, 33), (4160, 700)])
+def test_gemv_persistent_equals_the_split_kernel(ctx, oracle, group, k, n):
+    """The persistent GEMV (K <= 4096: a block walks tiles b, b + grid, ...,
+    the next tile's loads in flight through the chunk reduction) keeps the split
+    kernel's chunk order: for every row count 1..8, ragged N, chunks past K
+    (K = 1024 and 96) and both scale layouts its outputs equal the split
+    kernel's bit for bit and the closed form within tolerance. N = 8197 and 8200
+    give most blocks several tiles; at K = 4160 it does not apply and the split
+    kernel runs."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(k + n + group)
+    x = rng.standard_normal((8, k)).astype(np.float32)
+    wf = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    w = ctx.quantize(dev(wf), rocm.F32, n, k, 4, group)
+    deq = empty((n, k), torch.float32)
+    ctx.dequant(w, deq)
+    deq = host(ctx, deq)
+    xh = oracle.f32_to_f16_bits(x)
+    xd = dev(xh.view(np.float16))
+    want = oracle.w4a16(xh, 8, k, deq, n)
+    try:
+        for m in range(1, 9):
+            ctx.select_variant("gemv", "w16")
+            y = empty((m, n), torch.float32)
+            ctx.linear(w, xd, rocm.F16, m, y, rocm.W4A16)
+            base = host(ctx, y).copy()
+            assert np.abs(base - want[:m]).max() <= MAX_ABS
+            assert cosine(base, want[:m]) >= MIN_COS
+            for name in ("persist", "auto"):
                 ctx.select_variant("gemv", name)
                 y.fill_(7.0)
                 torch.cuda.synchronize()  # the fill runs on torch's stream, the product on the context's
