@@ -2983,16 +2983,17 @@ void launch_w4a16(const Weight &w, const half_t *x, int m, float *y, int gemv_va
     if (m <= 16) {
         int v = gemv_variant;
         if (v == 0) {
-            // "auto": the persistent kernel for up to 8 rows over two or more tiles
+            // "auto": the persistent kernel for up to 8 rows over four or more tiles
             // per compute unit at K <= 4096 (graph-timed at K = 4096 against the split
             // kernel, M = 1: N = 16384 8.3 against 9.8 us, N = 131072 53.9 against
             // 68.3 us = 0.70 of 8 TB/s; M = 8, N = 131072: 70.4 against 104.9 us, and
             // against 76.6 us for the streaming kernel; at one tile per compute unit,
-            // N = 4096, the split kernel is 2-5% faster); otherwise the split kernel,
-            // or the streaming kernel at 2..8 rows over eight or more tiles per
-            // compute unit (K = 4096: M = 4, N = 65536 33 against 39 us)
+            // N = 4096, the split kernel is 2-5% faster, and at two, N = 8192 and
+            // K = 2560, 4.8-4.9 against 4.9-5.1 us); otherwise the split kernel, or the
+            // streaming kernel at 2..8 rows over eight or more tiles per compute unit
+            // (K = 4096: M = 4, N = 65536 33 against 39 us)
             const int cus = device_cus();
-            if (m <= 8 && w.kblocks() <= 2 * kGemvChunks && w.tiles() >= 2 * cus) v = 5;
+            if (m <= 8 && w.kblocks() <= 2 * kGemvChunks && w.tiles() >= 4 * cus) v = 5;
             else if (m >= 2 && m <= 8 && w.tiles() >= 8 * cus) v = m > 4 && w.tiles() >= 16 * cus ? 3 : 4;
             else v = 1;
         }

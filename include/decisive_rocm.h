@@ -578,7 +578,7 @@ int32_t dz_tune(dz_ctx *ctx, uint32_t budget_ms, const char *cache_in, char *cac
  *                 multiple of 2048 and up to 8 rows, else w16; persist: w16's
  *                 blocks, one per compute unit, each walking tiles with the next
  *                 tile's loads in flight, for K <= 4096 and up to 8 rows, else
- *                 w16; "auto" takes persist for up to 8 rows over two or more
+ *                 w16; "auto" takes persist for up to 8 rows over four or more
  *                 tiles per compute unit at K <= 4096, else w16, or stream4 /
  *                 stream8 for 2..8 rows over eight or more tiles per compute unit)
  *   "gemm_w4a16"  pipe-auto, 256x256p2w8, 128x128p2w4, 128x256p2w8, 256x128w2x2,
