@@ -652,12 +652,13 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const uint8_t *__restr
 }
 
 // Persistent form of gemv_kernel<16, MPAD, G32, 1> for weights whose chunks
-// hold at most one k-block pair (K <= 4096): a grid of a few blocks per
-// compute unit, block b taking tiles b, b + gridDim.x, ... A wave issues the
-// next tile's loads (its staging unit and its two code loads) as soon as this
-// tile's MFMAs have taken their operands, so every wave keeps its loads in
-// flight through the chunk reduction and the barrier instead of ending and
-// handing the unit to a new block. The chunk partials go to an LDS area of
+// hold at most one k-block pair (K <= 4096): one block per compute unit,
+// block b taking tiles b, b + gridDim.x, ... The activation rows are staged
+// once. A wave issues the next tile's loads (the staging load of its scale
+// records and its two code loads) as soon as this tile's MFMAs and scale FMAs
+// are done with their operands, so every wave keeps its loads in flight
+// through the chunk reduction and the barrier instead of ending and handing
+// the unit to a new block. The chunk partials go to an LDS area of
 // their own, double-buffered by tile parity, so one barrier per tile orders
 // them. The arithmetic is gemv_kernel's, so the outputs are bitwise equal.
 template <int MPAD, bool G32>
@@ -697,7 +698,7 @@ __global__ __launch_bounds__(kGemvChunks * 64) void gemv_persist_kernel(const ui
         }
     }
     // one tile of loads in flight beside the tile being computed (two or
-    // three measured slower: the tiles' barriers, not the loads, set the pace)
+    // three tiles ahead, and two blocks per compute unit, measured slower)
     uint4_t st[S::LOADS - L0], cw[2];
     auto issue = [&](int t) {
 #pragma unroll
