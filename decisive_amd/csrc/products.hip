@@ -1737,7 +1737,11 @@ __global__ __launch_bounds__(WGM *WGN * 64) void w4a16_pipe_kernel(
     // 4*blk + q, whose source chunk is j ^ (row & 15) = j ^ q ^ 4*(blk & 3).
     const uint32_t xlane = (uint32_t)(q * k * 2);
     const int cx = j ^ q;
-    constexpr int DMA_GROUPS = 4;  // the next step's loads are spread over the first groups
+    // the next step's loads are spread over the first groups: over two, each
+    // load has longer to land than over four (config 5: 1.526-1.529 against
+    // 1.540-1.543 ms with f16 output, 1.545-1.556 against 1.572-1.582 with f32;
+    // the encoder 6.78-6.83 against 6.86-6.93 ms; all at once: in between)
+    constexpr int DMA_GROUPS = 2;
     constexpr int DMA_N = XPW + WPW;
     // loads [DMA_N*part/DMA_GROUPS, DMA_N*(part+1)/DMA_GROUPS) of one stage
     // (k % 128 == 0: every chunk of a step is inside the row)
