@@ -1245,6 +1245,7 @@ __global__ __launch_bounds__(WGM *WGN * 64) void i8_gemm_pipe_kernel(const int8_
     static_assert(DPW * WAVES * RPI == BM + BN, "DMA blocks split evenly over the waves");
     constexpr int SUBS = BK / 32;                // k-substeps of one 32x32x32 MFMA
     static_assert((NS - 2) * DPW <= 63, "vmcnt range");
+    static_assert(NS > 2 || SUBS >= 2, "two stages issue their loads over the first two substeps");
     __shared__ __align__(16) uint8_t st0[STAGE];
     __shared__ __align__(16) uint8_t st1[STAGE];
     __shared__ __align__(16) uint8_t st2[NS > 2 ? STAGE : 16];
@@ -1315,9 +1316,12 @@ __global__ __launch_bounds__(WGM *WGN * 64) void i8_gemm_pipe_kernel(const int8_
         for (int z = 0; z < NB; z++) acc[x][z] = int16_t_v{};
     // compute on `stage`; when `next` is set, the loads of step `next_step`
     // into it are issued in SUBS slices, one before each substep's MFMAs.
-    // With two stages they are all issued before the first substep instead,
-    // so that the last slice too has the whole step to land (config 4:
-    // 128.2-129.9 against 130.0-131.5 us; with three stages the slices pay)
+    // With two stages they are issued in two slices, before the first two
+    // substeps, so that the last of them has most of the step to land
+    // (config 4, alternated on one box: 123.3-123.9 us against 126.9-128.1
+    // with all of them before the first substep and 130.0-131.5 with four
+    // slices; three slices 1.2% slower than two; with three stages the four
+    // slices pay)
     auto compute = [&](const uint8_t *stage, uint8_t *next, int next_step) {
         int4_t af[2][MB], bf[2][NB];
         read_frags(stage, 0, af[0], bf[0]);
@@ -1327,8 +1331,8 @@ __global__ __launch_bounds__(WGM *WGN * 64) void i8_gemm_pipe_kernel(const int8_
             if (next) {
                 if (NS > 2)
                     dma(next, next_step, sub * DPW / SUBS, (sub + 1) * DPW / SUBS);
-                else if (sub == 0)
-                    dma(next, next_step, 0, DPW);
+                else if (sub < 2)
+                    dma(next, next_step, sub * DPW / 2, (sub + 1) * DPW / 2);
             }
             if (sub + 1 < SUBS) read_frags(stage, sub + 1, af[cur ^ 1], bf[cur ^ 1]);
             __builtin_amdgcn_sched_barrier(0);
